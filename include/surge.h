@@ -1,0 +1,307 @@
+/* surge.h - the public C ABI of the MI355X decode engine.
+ *
+ * This header keeps the reference engine's C interface for the batch-1
+ * decode hot path (reference: surge.h), so a caller written against the
+ * reference links against this library unchanged. Every declaration below
+ * cites the reference declaration it replaces as `surge.h:LINE` (reference
+ * file, not this one). Types that cross the boundary (sg_err, sg_tensor,
+ * sg_cfg, sg_layer_w, sg_model) keep the reference's field order and widths
+ * exactly, so one sg_model value can be handed to this library, to the
+ * reference's CPU oracle and to this repository's CPU oracle alike.
+ *
+ * Semantic differences from the reference, all forced by discrete memory
+ * (the reference targets a unified-memory GPU):
+ *   - sg_gpu_wrap COPIES the caller's bytes into HBM (the reference wraps
+ *     them with no copy). The caller's memory need not outlive the handle.
+ *   - sg_gpu_alloc's *host_out is a HOST MIRROR of the device buffer, not the
+ *     same memory. Every synchronous one-shot entry point (sg_gpu_run_*)
+ *     uploads each argument buffer's mirror before launching and downloads
+ *     every buffer the kernel writes into its mirror after the launch has
+ *     finished, so "write host, call, read host" works as in the reference.
+ *   - Buffers made by sg_gpu_wrap_device have no mirror: they wrap memory
+ *     that is already on the device (e.g. a torch tensor) and are never
+ *     copied. This is an addition for callers that keep data in HBM.
+ *   - sg_gpu_forward's logits are copied device-to-host once per token.
+ */
+#ifndef SURGE_H
+#define SURGE_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error convention (surge.h:7-11): msg == NULL means success. Messages are
+ * static strings or a static format buffer, so they are not thread-safe. */
+typedef struct { const char *msg; } sg_err;
+#define SG_OK ((sg_err){0})
+static inline bool sg_failed(sg_err e) { return e.msg != NULL; }
+
+/* ---------------------------------------------------------------------
+ * GGUF v3 reader (surge.h:13-46)
+ * --------------------------------------------------------------------- */
+typedef enum { SG_GGUF_U8 = 0, SG_GGUF_I8, SG_GGUF_U16, SG_GGUF_I16, SG_GGUF_U32,
+  SG_GGUF_I32, SG_GGUF_F32, SG_GGUF_BOOL, SG_GGUF_STR, SG_GGUF_ARR, SG_GGUF_U64,
+  SG_GGUF_I64, SG_GGUF_F64 } sg_gguf_kv_type;
+typedef enum { SG_T_F32 = 0, SG_T_F16 = 1, SG_T_Q8_0 = 8, SG_T_BF16 = 30 } sg_tensor_type;
+typedef struct { const char *name; sg_tensor_type type; uint32_t n_dims;
+  uint64_t dims[4]; const void *data; uint64_t nbytes; } sg_tensor;
+typedef struct sg_gguf sg_gguf;
+
+sg_err sg_gguf_open(const char *path, sg_gguf **out);              /* surge.h:22 */
+void sg_gguf_close(sg_gguf *g);                                      /* surge.h:23 */
+bool sg_gguf_get_u32(const sg_gguf *g, const char *key, uint32_t *out);   /* surge.h:25 */
+bool sg_gguf_get_f32(const sg_gguf *g, const char *key, float *out);      /* surge.h:26 */
+bool sg_gguf_get_str(const sg_gguf *g, const char *key, const char **out);/* surge.h:27 */
+/* Array metadata (surge.h:28-35): element type, raw data pointer (for
+ * non-string arrays) and element count. */
+bool sg_gguf_get_arr(const sg_gguf *g, const char *key, sg_gguf_kv_type *elem_type,
+                     const void **data, uint64_t *count);
+uint32_t sg_gguf_version(const sg_gguf *g);                          /* surge.h:41 */
+uint64_t sg_gguf_kv_count(const sg_gguf *g);                         /* surge.h:42 */
+const sg_tensor *sg_gguf_tensor(const sg_gguf *g, const char *name); /* surge.h:44 */
+uint64_t sg_gguf_tensor_count(const sg_gguf *g);                     /* surge.h:45 */
+const sg_tensor *sg_gguf_tensor_at(const sg_gguf *g, uint64_t i);    /* surge.h:46 */
+
+/* ---------------------------------------------------------------------
+ * Model description (surge.h:115-347)
+ * --------------------------------------------------------------------- */
+
+/* Model config (surge.h:115-151). key_dim = n_k_heads*head_k_dim,
+ * value_dim = n_v_heads*head_v_dim and conv_dim = 2*key_dim + value_dim are
+ * derived. Layer L is full attention iff (L+1) % full_attn_interval == 0. */
+typedef struct {
+    uint32_t n_layers, n_heads, n_kv_heads, head_dim, hidden, ffn_hidden, vocab;
+    float rope_theta, rms_eps;
+    bool tied_embeddings;
+    uint32_t rope_dim;
+    uint32_t full_attn_interval;
+    uint32_t n_k_heads, n_v_heads, head_k_dim, head_v_dim, conv_kernel;
+    bool attn_output_gate;
+} sg_cfg;
+
+/* Per-layer weight pointers (surge.h:269-277). Exactly one of the two mixer
+ * groups is non-NULL on a layer. GGUF dtypes: matmuls Q8_0 (or F32), every
+ * small tensor F32. */
+typedef struct {
+    const void *q_proj, *k_proj, *v_proj, *o_proj, *q_norm, *k_norm,
+               *gate_proj, *up_proj, *down_proj, *ln1, *ln2;
+    const void *ssm_in_qkv, *ssm_in_z, *ssm_in_b, *ssm_in_a, *ssm_a,
+               *ssm_dt_bias, *ssm_conv1d, *ssm_norm, *ssm_out;
+} sg_layer_w;
+
+/* What ssm_a stores (surge.h:281-284). GGUF stores -exp(A_log). */
+typedef enum { SG_SSM_A_LOG = 0, SG_SSM_A_NEG_EXP = 1 } sg_ssm_a_form;
+
+/* The model (surge.h:286-330). lm_head == tok_emb when tied. */
+typedef struct {
+    sg_cfg cfg;
+    const void *tok_emb, *out_norm, *lm_head;
+    sg_layer_w *layers;
+    sg_tensor_type wtype;
+    sg_ssm_a_form ssm_a_form;
+    bool v_heads_tiled;
+    sg_tensor_type ssm_a_type;
+    sg_tensor_type ssm_norm_type;
+    sg_tensor_type dense_type;
+    bool norms_are_residual;
+} sg_model;
+
+/* Value-head -> key-head map (surge.h:337-343): GGUF tiles (h % n_k). */
+static inline uint32_t sg_ssm_k_head(uint32_t v_head, uint32_t n_k_heads,
+                                     uint32_t n_v_heads, bool tiled) {
+    if (n_k_heads == 0 || n_v_heads < n_k_heads) return 0;
+    return tiled ? (v_head % n_k_heads) : (v_head / (n_v_heads / n_k_heads));
+}
+
+/* Maps a qwen35/qwen3_5 GGUF onto an sg_model (surge.h:345). The model's
+ * pointers alias the GGUF mapping, which must outlive it. */
+sg_err sg_model_from_gguf(const sg_gguf *g, sg_model *m);
+void sg_model_free(sg_model *m);                                     /* surge.h:347 */
+
+/* ---------------------------------------------------------------------
+ * GPU layer (surge.h:640-1408), implemented with HIP on gfx950
+ * ---------------------------------------------------------------------
+ *
+ * Every sg_gpu_run_* entry point is synchronous: it launches on the
+ * library's stream and waits. All buffers are f32 unless stated; a buffer
+ * argument is a handle from sg_gpu_alloc / sg_gpu_wrap / sg_gpu_wrap_device.
+ *
+ * sg_gpu_run_op kernels and params (surge.h:666-707):
+ *   kernel            a                     b                    out
+ *   k_rmsnorm         x[n]                  w[n] (or NULL)       x'[n]
+ *                     p: [0]=n [1]=eps bits [2]=1 if b holds w
+ *   k_rmsnorm_heads   x[heads*stride]       w[n] or NULL         x'[heads*stride]
+ *                     p: [0]=n [1]=heads [2]=eps bits [3]=stride (0 = n) [4]=1 if w
+ *   k_rope            x[head_dim]           cos[half]|sin[half]  x'[head_dim]
+ *                     p: [0]=head_dim [1]=rope_dim
+ *   k_rope_heads      x[heads*stride]       cos|sin              x'
+ *                     p: [0]=head_dim [1]=rope_dim [2]=heads [3]=stride
+ *   k_matvec_q8       w Q8_0 rows*(cols/32) blocks   x[cols]     y[rows]
+ *   k_matvec_f32      w[rows*cols]          x[cols]              y[rows]
+ *                     p: [0]=rows [1]=cols (cols % 32 == 0 for q8)
+ *   k_softmax         x[n]                  -                    p[n]
+ *   k_swiglu          gate[n]               up[n]                silu(gate)*up
+ *   k_silu            x[n]                  -                    silu(x)
+ *   k_gate_sigmoid    x[n]                  gate[n]              x*sigmoid(gate)
+ *   k_add             x[n]                  r[n]                 x+r
+ *   k_scale           x[n]                  -                    x*scale  p: [1]=scale bits
+ *   k_kv_store_f16    x[n] f32              -                    cache f16, p: [0]=n [1]=dst offset (elements)
+ *   k_conv1d_step     x[channels]           w[channels*ksize]    y[channels] | state[(ksize-1)*channels]
+ *                     p: [0]=channels [1]=ksize
+ *   k_delta_step      S[dv*dk] in/out       q[dk]|k[dk]|v[dv]    y[dv]
+ *                     p: [0]=dk [1]=dv [2]=beta bits [3]=decay bits
+ *   k_rmsnorm_gated   y[heads*dv]           z[heads*dv] | w[dv]  silu(z)*rmsnorm(y,w)
+ *                     p: [0]=dv [1]=heads [2]=eps bits
+ *   k_matmul_q8       X[N*K] f32            W Q8_0 M*(K/32)      Y[N*M] f32
+ *                     p: [0]=N [1]=M [2]=K
+ * Aliasing: out must not overlap a or b, except k_conv1d_step's state tail
+ * and k_delta_step's in-place S (surge.h:709-712). */
+typedef struct sg_gpu sg_gpu;
+
+sg_err sg_gpu_init(sg_gpu **out);                                    /* surge.h:725 */
+void sg_gpu_free(sg_gpu *g);                                         /* surge.h:726 */
+sg_err sg_gpu_wrap(sg_gpu *g, const void *ptr, uint64_t nbytes, void **buf_out); /* surge.h:742 */
+sg_err sg_gpu_alloc(sg_gpu *g, uint64_t nbytes, void **buf_out, void **host_out); /* surge.h:746 */
+void sg_gpu_buf_free(void *buf);                                     /* surge.h:747 */
+void *sg_gpu_buf_host(void *buf);                                    /* surge.h:749 */
+uint64_t sg_gpu_current_alloc_bytes(const sg_gpu *g);                /* surge.h:756 */
+
+/* Additions for discrete memory (no reference counterpart): wrap existing
+ * device memory with no copy and no mirror; read a handle's device address;
+ * explicit mirror synchronisation. */
+sg_err sg_gpu_wrap_device(sg_gpu *g, void *dev_ptr, uint64_t nbytes, void **buf_out);
+void *sg_gpu_buf_device(void *buf);
+sg_err sg_gpu_buf_upload(void *buf);
+sg_err sg_gpu_buf_download(void *buf);
+
+sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
+                     const uint32_t params[8]);                      /* surge.h:761 */
+
+/* fp16-KV single-pass decode attention (surge.h:774). q f32 [n_heads,
+ * q_stride]; k, v f16 [seq, n_kv, hd]; out f32 [n_heads, hd].
+ * p: [0]=n_heads [1]=n_kv [2]=hd [3]=seq [4]=q_stride [5]=scale bits. */
+sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out,
+                                  const uint32_t params[8]);
+
+/* Split-K decode attention (surge.h:890-980). Split i covers
+ * [i*seq/n, (i+1)*seq/n); m, s f32 [n_heads, n_splits]; acc f32
+ * [n_heads, n_splits, hd]. p: [0]=n_heads [1]=n_kv [2]=hd [3]=seq
+ * [4]=q_stride [5]=scale bits [6]=n_splits. The per-head and GQA partials
+ * produce the same bytes here (one kernel serves both). */
+sg_err sg_gpu_run_attn_splitk_partial(sg_gpu *g, void *q, void *k, void *v,
+                                      void *m, void *s, void *acc,
+                                      const uint32_t params[8]);
+sg_err sg_gpu_run_attn_splitk_partial_gqa(sg_gpu *g, void *q, void *k, void *v,
+                                          void *m, void *s, void *acc,
+                                          const uint32_t params[8]);
+sg_err sg_gpu_run_attn_splitk_combine(sg_gpu *g, void *m, void *s, void *acc,
+                                      void *out, const uint32_t params[8]);
+
+/* Split-count policy (surge.h:1020-1106), re-derived for 256 CUs. */
+uint32_t sg_gpu_splitk_n_splits(uint32_t seq);
+uint32_t sg_gpu_splitk_gqa_n_splits(uint32_t seq);
+uint32_t sg_gpu_splitk_gqa_n_splits_at(const sg_gpu *g, uint32_t seq);
+uint32_t sg_gpu_splitk_gqa_cap(const sg_gpu *g);
+bool sg_gpu_splitk_gqa_selected(const sg_gpu *g, uint32_t n_heads,
+                                uint32_t n_kv_heads, uint32_t seq);
+void sg_gpu_splitk_dispatch_counts(const sg_gpu *g, uint64_t *per_head, uint64_t *gqa);
+
+/* DeltaNet one-shots (surge.h:1133-1142). k_delta_multi: S [n_v, dv, dk]
+ * in/out, qkv [conv_dim] (post conv+silu, pre norm), out [value_dim], gates
+ * [2*n_v] = beta[n_v] | decay[n_v]. p: [0]=dk [1]=dv [2]=n_v [3]=n_k
+ * [4]=key_dim [5]=tiled. q/k arrive already normalised and scaled, as in the
+ * reference's k_delta_multi (kernels.metal:764-805). */
+sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *gates,
+                              const uint32_t params[8]);
+
+/* Decode (surge.h:1260-1274). */
+sg_err sg_gpu_load_model(sg_gpu *g, const sg_model *m);
+sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx);
+void sg_gpu_state_reset(sg_gpu *g);
+sg_err sg_gpu_forward(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
+                      const float **logits);
+uint32_t sg_gpu_used(const sg_gpu *g);
+
+/* Chunked prefill (surge.h:1306-1309). */
+#define SG_PREFILL_CHUNK_DEFAULT 1024u
+sg_err sg_gpu_prefill(sg_gpu *g, const sg_model *m, const int32_t *tokens,
+                      uint32_t n_tokens, uint32_t chunk_size,
+                      const float **out_last_logits);
+/* Apple compositor mitigations (surge.h:1372-1408): kept for API
+ * compatibility; no-ops on MI355X (nothing to yield to). */
+void sg_gpu_set_prefill_rest(sg_gpu *g, uint32_t work_budget_ms, uint32_t rest_ms);
+uint64_t sg_gpu_prefill_rest_ms(const sg_gpu *g);
+void sg_gpu_set_prefill_max_burst(sg_gpu *g, uint32_t max_burst_ms);
+uint64_t sg_gpu_prefill_segments(const sg_gpu *g);
+
+/* Device-resident greedy argmax over the last forward's logits (no
+ * reference counterpart; the reference reads host logits). Lowest index wins
+ * an exact tie, as sg_argmax_f32. */
+sg_err sg_gpu_argmax(sg_gpu *g, uint32_t *token_out);
+/* Forward without the logits download (no reference counterpart): for
+ * callers that only need sg_gpu_argmax or time the step. */
+sg_err sg_gpu_forward_nosync(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos);
+sg_err sg_gpu_sync(sg_gpu *g);
+/* Device-resident greedy decode (no reference counterpart): feeds `token` at
+ * `pos`, then keeps choosing the next token by argmax on the device for
+ * n_steps steps with no host round trip; out_tokens[i] is the argmax after
+ * step i. Same tokens as calling sg_gpu_forward + sg_argmax_f32 in a loop. */
+sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
+                            uint32_t n_steps, int32_t *out_tokens);
+
+/* Measurement hooks (no reference counterpart): the library's HIP stream
+ * (a hipStream_t) for event timing, and one decode-step GEMV enqueued alone
+ * against the live state (which: 0 input projection, 1 output projection,
+ * 2 gate/up, 3 down, 4 lm_head). */
+void *sg_gpu_stream(const sg_gpu *g);
+sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which);
+
+/* ---------------------------------------------------------------------
+ * KV cache + DeltaNet state sizing and f16 (surge.h:1410-1501)
+ * --------------------------------------------------------------------- */
+#define SG_KV_CAP_DEFAULT 131072u
+#define SG_KV_CAP_MAX     262144u
+uint64_t sg_kv_bytes(const sg_cfg *c, uint32_t cap, sg_tensor_type dtype); /* surge.h:1456 */
+uint64_t sg_kv_state_bytes(const sg_cfg *c);                               /* surge.h:1457 */
+uint16_t sg_f32_to_f16(float f);                                           /* surge.h:1463 */
+float    sg_f16_to_f32(uint16_t h);                                        /* surge.h:1464 */
+
+/* ---------------------------------------------------------------------
+ * Greedy argmax (surge.h:1503-1512): lowest index wins an exact tie.
+ * --------------------------------------------------------------------- */
+uint32_t sg_argmax_f32(const float *v, uint32_t n);
+
+/* ---------------------------------------------------------------------
+ * Bench math (surge.h:1784-1824)
+ * --------------------------------------------------------------------- */
+double sg_bench_slope(const double *t_wall_cum, uint32_t n, uint32_t warmup);
+double sg_bench_avg_tps(const double *t_wall_cum, uint32_t n, uint32_t warmup);
+uint32_t sg_bench_default_warmup(uint32_t n_gen);
+
+/* ---------------------------------------------------------------------
+ * Synthetic random-init models (no reference counterpart: the reference
+ * writes its fixtures from Python, tools/make_fixtures.py:1242-1416).
+ * ---------------------------------------------------------------------
+ * Builds a qwen35-shaped model of the given config with seeded random
+ * weights, laid out in one host allocation exactly as a GGUF file would hold
+ * them (Q8_0 matmuls with 34-byte blocks, F32 small tensors, -exp(A_log)
+ * ssm_a, absolute norms near 1, tiled value heads). Deterministic for a
+ * seed regardless of thread count. sg_synth_write_gguf writes the same
+ * model as a GGUF v3 file that sg_gguf_open + sg_model_from_gguf read back.
+ * wtype is SG_T_Q8_0 or SG_T_F32. */
+typedef struct sg_synth sg_synth;
+sg_err sg_synth_new(const sg_cfg *c, sg_tensor_type wtype, uint64_t seed,
+                    sg_synth **out);
+const sg_model *sg_synth_model(const sg_synth *s);
+uint64_t sg_synth_bytes(const sg_synth *s);
+sg_err sg_synth_write_gguf(const sg_synth *s, const char *path);
+void sg_synth_free(sg_synth *s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SURGE_H */

@@ -1,0 +1,1088 @@
+/* hip.c - the sg_gpu_* C ABI (reference surge.h:640-1408) on one MI355X.
+ *
+ * Replaces the reference's Metal host layer (reference src/metal.m). Plain
+ * C11 over the HIP runtime C API; every kernel is launched through the
+ * extern "C" launchers of kernels.hip on one stream.
+ *
+ * Device memory: weights are uploaded once by sg_gpu_load_model and repacked
+ * on the device into the GEMV layout, with siblings that read the same input
+ * fused into one matrix (q|k|v; qkv|z|b|a; gate/up row-interleaved). State
+ * (fp16 K/V caches, DeltaNet conv ring and S) lives in HBM for the life of
+ * the state. One decode step is one captured HIP graph replayed per token;
+ * the position and token live in a device step descriptor, so the same graph
+ * serves every position.
+ *
+ * Errors follow the reference: sg_err with a static message (or one static
+ * format buffer, so not thread-safe), NULL on success. Shapes and sizes are
+ * checked on the host before any launch.
+ */
+#define _GNU_SOURCE
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__ 1
+#endif
+#include <hip/hip_runtime_api.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "kernels.h"
+#include "surge.h"
+
+/* ---------------------------------------------------------------------
+ * errors
+ * --------------------------------------------------------------------- */
+
+static char g_errbuf[512];
+static sg_err errf(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_errbuf, sizeof g_errbuf, fmt, ap);
+    va_end(ap);
+    return (sg_err){g_errbuf};
+}
+#define HIPCHK(call, what) do { hipError_t _e = (call); \
+    if (_e != hipSuccess) return errf("gpu: %s failed: %s", what, hipGetErrorString(_e)); } while (0)
+
+/* ---------------------------------------------------------------------
+ * types
+ * --------------------------------------------------------------------- */
+
+enum { BUF_ALLOC = 0, BUF_WRAP = 1, BUF_DEVICE = 2 };
+
+typedef struct {
+    sg_gpu *g;
+    void *dev;
+    void *host;          /* ALLOC: owned mirror; WRAP: caller's pointer; DEVICE: NULL */
+    uint64_t nbytes;
+    int kind;
+} gbuf;
+
+typedef struct {          /* a device matrix in the GEMV layout */
+    int8_t *qs;
+    uint16_t *d;
+    float *wf;
+    uint32_t rows, cols;
+} dmat;
+
+typedef struct {
+    bool attn;
+    dmat in, out, gu, down;
+    float *ln1, *ln2, *qn, *kn, *ssm_norm, *conv_w, *ssm_a, *dt_bias;
+    uint16_t *kc, *vc;    /* [max_ctx][n_kv][hd] f16 */
+    float *ring;          /* [4][conv_dim]: last inputs, slot = position % 4 */
+    float *S;             /* [n_v][dv][dk] */
+} glayer;
+
+typedef struct { void *p; uint64_t n; } alloc_rec;
+
+struct sg_gpu {
+    int dev;
+    hipStream_t stream;
+    alloc_rec *allocs;
+    uint32_t n_allocs, cap_allocs;
+    uint64_t alloc_bytes;
+
+    /* model */
+    const sg_model *model;
+    sg_cfg cfg;
+    bool q8;
+    glayer *ls;
+    dmat emb, lm;
+    bool lm_is_emb;
+    float *out_norm;
+    uint32_t key_dim, value_dim, conv_dim, q_width, kv_width, attn_width;
+
+    /* state */
+    bool have_state;
+    uint32_t max_ctx, used, max_splits;
+    float *cs_table;
+    float *x, *act, *ctx, *ybuf, *ffg, *logits, *am, *as, *aacc;
+    uint32_t *amax_scratch, *hist;
+    sgk_step *d_step, *h_step;
+    float *h_logits;
+    uint32_t *h_tok;
+    hipGraphExec_t g_fwd, g_greedy;
+    bool use_graph;
+
+    /* one-shot scratch */
+    void *tmp;
+    uint64_t tmp_bytes;
+    uint64_t splitk_gqa_dispatches;
+};
+
+/* ---------------------------------------------------------------------
+ * allocation bookkeeping
+ * --------------------------------------------------------------------- */
+
+static sg_err dalloc(sg_gpu *g, uint64_t n, void **out) {
+    *out = NULL;
+    if (n == 0) n = 1;
+    void *p = NULL;
+    hipError_t e = hipMalloc(&p, n);
+    if (e != hipSuccess) return errf("gpu: hipMalloc(%llu) failed: %s", (unsigned long long)n, hipGetErrorString(e));
+    if (g->n_allocs == g->cap_allocs) {
+        uint32_t nc = g->cap_allocs ? 2 * g->cap_allocs : 256;
+        alloc_rec *r = realloc(g->allocs, nc * sizeof *r);
+        if (!r) { hipFree(p); return (sg_err){"gpu: out of host memory"}; }
+        g->allocs = r;
+        g->cap_allocs = nc;
+    }
+    g->allocs[g->n_allocs++] = (alloc_rec){p, n};
+    g->alloc_bytes += n;
+    *out = p;
+    return SG_OK;
+}
+
+static sg_err dzalloc(sg_gpu *g, uint64_t n, void **out) {
+    sg_err e = dalloc(g, n, out);
+    if (sg_failed(e)) return e;
+    HIPCHK(hipMemset(*out, 0, n ? n : 1), "hipMemset");
+    return SG_OK;
+}
+
+static void dfree(sg_gpu *g, void *p) {
+    if (!g || !p) return;
+    for (uint32_t i = 0; i < g->n_allocs; i++) {
+        if (g->allocs[i].p == p) {
+            g->alloc_bytes -= g->allocs[i].n;
+            g->allocs[i] = g->allocs[--g->n_allocs];
+            hipFree(p);
+            return;
+        }
+    }
+}
+
+uint64_t sg_gpu_current_alloc_bytes(const sg_gpu *g) { return g ? g->alloc_bytes : 0; }
+
+/* ---------------------------------------------------------------------
+ * lifecycle and buffers
+ * --------------------------------------------------------------------- */
+
+sg_err sg_gpu_init(sg_gpu **out) {
+    if (!out) return (sg_err){"gpu: invalid arguments"};
+    *out = NULL;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n < 1) return (sg_err){"gpu: no HIP device available"};
+    sg_gpu *g = calloc(1, sizeof *g);
+    if (!g) return (sg_err){"gpu: out of memory"};
+    g->dev = 0;
+    if (hipSetDevice(0) != hipSuccess) { free(g); return (sg_err){"gpu: hipSetDevice failed"}; }
+    /* Default priority (never a prioritised stream). */
+    if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess) {
+        free(g);
+        return (sg_err){"gpu: hipStreamCreate failed"};
+    }
+    const char *ev = getenv("SURGE_HIP_GRAPH");
+    g->use_graph = !(ev && strcmp(ev, "0") == 0);
+    *out = g;
+    return SG_OK;
+}
+
+static void state_free(sg_gpu *g);
+static void model_free(sg_gpu *g);
+
+void sg_gpu_free(sg_gpu *g) {
+    if (!g) return;
+    hipStreamSynchronize(g->stream);
+    state_free(g);
+    model_free(g);
+    while (g->n_allocs) dfree(g, g->allocs[g->n_allocs - 1].p);
+    free(g->allocs);
+    hipStreamDestroy(g->stream);
+    free(g);
+}
+
+sg_err sg_gpu_wrap(sg_gpu *g, const void *ptr, uint64_t nbytes, void **buf_out) {
+    if (!g || !ptr || !buf_out || !nbytes) return (sg_err){"gpu: sg_gpu_wrap got an invalid argument"};
+    *buf_out = NULL;
+    if ((uintptr_t)ptr % 4) return (sg_err){"gpu: sg_gpu_wrap needs a 4-byte aligned pointer"};
+    gbuf *b = calloc(1, sizeof *b);
+    if (!b) return (sg_err){"gpu: out of memory"};
+    sg_err e = dalloc(g, nbytes, &b->dev);
+    if (sg_failed(e)) { free(b); return e; }
+    if (hipMemcpy(b->dev, ptr, nbytes, hipMemcpyHostToDevice) != hipSuccess) {
+        dfree(g, b->dev);
+        free(b);
+        return (sg_err){"gpu: sg_gpu_wrap upload failed"};
+    }
+    b->g = g;
+    b->host = (void *)ptr;
+    b->nbytes = nbytes;
+    b->kind = BUF_WRAP;
+    *buf_out = b;
+    return SG_OK;
+}
+
+sg_err sg_gpu_alloc(sg_gpu *g, uint64_t nbytes, void **buf_out, void **host_out) {
+    if (!g || !buf_out || !nbytes) return (sg_err){"gpu: sg_gpu_alloc got an invalid argument"};
+    *buf_out = NULL;
+    if (host_out) *host_out = NULL;
+    gbuf *b = calloc(1, sizeof *b);
+    if (!b) return (sg_err){"gpu: out of memory"};
+    b->host = calloc(1, nbytes);
+    if (!b->host) { free(b); return (sg_err){"gpu: out of host memory for the mirror"}; }
+    sg_err e = dzalloc(g, nbytes, &b->dev);
+    if (sg_failed(e)) { free(b->host); free(b); return e; }
+    b->g = g;
+    b->nbytes = nbytes;
+    b->kind = BUF_ALLOC;
+    *buf_out = b;
+    if (host_out) *host_out = b->host;
+    return SG_OK;
+}
+
+sg_err sg_gpu_wrap_device(sg_gpu *g, void *dev_ptr, uint64_t nbytes, void **buf_out) {
+    if (!g || !dev_ptr || !buf_out || !nbytes) return (sg_err){"gpu: sg_gpu_wrap_device got an invalid argument"};
+    gbuf *b = calloc(1, sizeof *b);
+    if (!b) return (sg_err){"gpu: out of memory"};
+    b->g = g;
+    b->dev = dev_ptr;
+    b->nbytes = nbytes;
+    b->kind = BUF_DEVICE;
+    *buf_out = b;
+    return SG_OK;
+}
+
+void sg_gpu_buf_free(void *buf) {
+    gbuf *b = buf;
+    if (!b) return;
+    if (b->kind != BUF_DEVICE) dfree(b->g, b->dev);
+    if (b->kind == BUF_ALLOC) free(b->host);
+    free(b);
+}
+
+void *sg_gpu_buf_host(void *buf) { return buf ? ((gbuf *)buf)->host : NULL; }
+void *sg_gpu_buf_device(void *buf) { return buf ? ((gbuf *)buf)->dev : NULL; }
+
+sg_err sg_gpu_buf_upload(void *buf) {
+    gbuf *b = buf;
+    if (!b) return (sg_err){"gpu: NULL buffer"};
+    if (b->kind != BUF_ALLOC) return SG_OK;
+    HIPCHK(hipMemcpy(b->dev, b->host, b->nbytes, hipMemcpyHostToDevice), "upload");
+    return SG_OK;
+}
+
+sg_err sg_gpu_buf_download(void *buf) {
+    gbuf *b = buf;
+    if (!b) return (sg_err){"gpu: NULL buffer"};
+    if (b->kind != BUF_ALLOC) return SG_OK;
+    HIPCHK(hipMemcpy(b->host, b->dev, b->nbytes, hipMemcpyDeviceToHost), "download");
+    return SG_OK;
+}
+
+/* ---------------------------------------------------------------------
+ * one-shot helpers: size checks, mirror sync, scratch
+ * --------------------------------------------------------------------- */
+
+static float fbits(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+static sg_err need(const void *buf, uint64_t bytes, const char *what) {
+    const gbuf *b = buf;
+    if (!b) return errf("gpu: %s is NULL", what);
+    if (b->nbytes < bytes) return errf("gpu: %s holds %llu bytes, needs %llu", what,
+                                       (unsigned long long)b->nbytes, (unsigned long long)bytes);
+    return SG_OK;
+}
+
+static bool overlap(const void *a, const void *b) {
+    const gbuf *x = a, *y = b;
+    if (!x || !y) return false;
+    const char *p = x->dev, *q = y->dev;
+    return p < q + y->nbytes && q < p + x->nbytes;
+}
+
+static sg_err push(void *const *bufs, int n) {
+    for (int i = 0; i < n; i++) {
+        if (!bufs[i]) continue;
+        sg_err e = sg_gpu_buf_upload(bufs[i]);
+        if (sg_failed(e)) return e;
+    }
+    return SG_OK;
+}
+
+static sg_err finish(sg_gpu *g, hipError_t launch, void *const *outs, int n) {
+    if (launch != hipSuccess) return errf("gpu: kernel launch failed: %s", hipGetErrorString(launch));
+    HIPCHK(hipStreamSynchronize(g->stream), "kernel execution");
+    for (int i = 0; i < n; i++) {
+        if (!outs[i]) continue;
+        sg_err e = sg_gpu_buf_download(outs[i]);
+        if (sg_failed(e)) return e;
+    }
+    return SG_OK;
+}
+
+static sg_err scratch(sg_gpu *g, uint64_t bytes, void **out) {
+    if (g->tmp_bytes < bytes) {
+        dfree(g, g->tmp);
+        g->tmp = NULL;
+        g->tmp_bytes = 0;
+        sg_err e = dalloc(g, bytes, &g->tmp);
+        if (sg_failed(e)) return e;
+        g->tmp_bytes = bytes;
+    }
+    *out = g->tmp;
+    return SG_OK;
+}
+
+#define DEV(b) ((b) ? ((gbuf *)(b))->dev : NULL)
+
+/* ---------------------------------------------------------------------
+ * sg_gpu_run_op: the per-op oracle hooks (surge.h:666-762)
+ * --------------------------------------------------------------------- */
+
+sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
+                     const uint32_t p[8]) {
+    if (!g || !kernel || !a || !out || !p) return (sg_err){"gpu: sg_gpu_run_op got a NULL argument"};
+    if (overlap(out, a) || overlap(out, b)) {
+        if (strcmp(kernel, "k_delta_step") != 0)
+            return errf("gpu: %s: out must not overlap an input", kernel);
+    }
+    void *ins[3] = {a, b, out};
+    void *outs[1] = {out};
+    hipStream_t s = g->stream;
+    sg_err e;
+    const uint32_t n = p[0];
+
+    if (!strcmp(kernel, "k_matvec_q8") || !strcmp(kernel, "k_matvec_f32")) {
+        bool q8 = kernel[9] == 'q';
+        uint32_t rows = p[0], cols = p[1];
+        if (!rows || !cols || (q8 && cols % 32)) return errf("gpu: %s: bad shape %ux%u", kernel, rows, cols);
+        uint64_t wbytes = q8 ? (uint64_t)rows * (cols / 32) * 34 : (uint64_t)rows * cols * 4;
+        if (sg_failed(e = need(a, wbytes, "w")) || sg_failed(e = need(b, (uint64_t)cols * 4, "x")) ||
+            sg_failed(e = need(out, (uint64_t)rows * 4, "y"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        sgk_gemv ga = {0};
+        ga.rows = rows; ga.cols = cols; ga.x = DEV(b); ga.y = DEV(out);
+        ga.pro = SGK_PRO_NONE; ga.epi = SGK_EPI_STORE;
+        if (q8) {
+            void *t;
+            if (sg_failed(e = scratch(g, (uint64_t)rows * cols + (uint64_t)rows * (cols / 32) * 2 + 256, &t))) return e;
+            ga.qs = t;
+            ga.d = (uint16_t *)((char *)t + (((uint64_t)rows * cols + 255) / 256 * 256));
+            hipError_t he = sgk_repack_q8(DEV(a), rows, cols, (int8_t *)ga.qs, (uint16_t *)ga.d, 0, 1, s);
+            if (he != hipSuccess) return finish(g, he, NULL, 0);
+        } else {
+            ga.wf = DEV(a);
+        }
+        return finish(g, sgk_gemv_launch(&ga, s), outs, 1);
+    }
+    if (!strcmp(kernel, "k_rmsnorm") || !strcmp(kernel, "k_rmsnorm_heads")) {
+        bool heads = kernel[9] == '_';
+        uint32_t nh = heads ? p[1] : 1, stride = heads ? (p[3] ? p[3] : n) : n;
+        float eps = fbits(heads ? p[2] : p[1]);
+        bool hw = heads ? p[4] != 0 : p[2] != 0;
+        if (!n || !nh || stride < n) return errf("gpu: %s: bad shape", kernel);
+        uint64_t bytes = ((uint64_t)(nh - 1) * stride + n) * 4;
+        if (sg_failed(e = need(a, bytes, "x")) || sg_failed(e = need(out, bytes, "out"))) return e;
+        if (hw && sg_failed(e = need(b, (uint64_t)n * 4, "w"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        return finish(g, sgk_rmsnorm_heads(DEV(a), hw ? DEV(b) : NULL, DEV(out), n, nh, stride, eps, s), outs, 1);
+    }
+    if (!strcmp(kernel, "k_rope") || !strcmp(kernel, "k_rope_heads")) {
+        bool heads = kernel[6] == '_';
+        uint32_t hd = p[0], rd = p[1], nh = heads ? p[2] : 1, stride = heads ? (p[3] ? p[3] : hd) : hd;
+        if (!hd || hd > 256 || rd < 2 || rd > hd || rd % 2 || !nh || stride < hd)
+            return errf("gpu: %s: bad shape", kernel);
+        uint64_t bytes = ((uint64_t)(nh - 1) * stride + hd) * 4;
+        if (sg_failed(e = need(a, bytes, "x")) || sg_failed(e = need(b, (uint64_t)rd * 4, "cs")) ||
+            sg_failed(e = need(out, bytes, "out"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        return finish(g, sgk_rope_heads(DEV(a), DEV(b), DEV(out), hd, rd, nh, stride, s), outs, 1);
+    }
+    if (!strcmp(kernel, "k_softmax")) {
+        if (!n) return (sg_err){"gpu: k_softmax: n is zero"};
+        if (sg_failed(e = need(a, (uint64_t)n * 4, "x")) || sg_failed(e = need(out, (uint64_t)n * 4, "out"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        return finish(g, sgk_softmax(DEV(a), DEV(out), n, s), outs, 1);
+    }
+    struct { const char *name; int op; bool needs_b; } ew[] = {
+        {"k_swiglu", SGK_EW_SWIGLU, true}, {"k_silu", SGK_EW_SILU, false},
+        {"k_gate_sigmoid", SGK_EW_GATE_SIGMOID, true}, {"k_add", SGK_EW_ADD, true},
+        {"k_scale", SGK_EW_SCALE, false},
+    };
+    for (size_t i = 0; i < sizeof ew / sizeof *ew; i++) {
+        if (strcmp(kernel, ew[i].name)) continue;
+        if (!n) return errf("gpu: %s: n is zero", kernel);
+        if (sg_failed(e = need(a, (uint64_t)n * 4, "a")) || sg_failed(e = need(out, (uint64_t)n * 4, "out"))) return e;
+        if (ew[i].needs_b && sg_failed(e = need(b, (uint64_t)n * 4, "b"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        return finish(g, sgk_elementwise(ew[i].op, DEV(a), DEV(b), DEV(out), n, fbits(p[1]), s), outs, 1);
+    }
+    if (!strcmp(kernel, "k_kv_store_f16")) {
+        uint64_t off = p[1];
+        if (!n) return (sg_err){"gpu: k_kv_store_f16: n is zero"};
+        if (sg_failed(e = need(a, (uint64_t)n * 4, "x")) || sg_failed(e = need(out, (off + n) * 2, "cache"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        return finish(g, sgk_elementwise(SGK_EW_TO_F16, DEV(a), NULL, (uint16_t *)DEV(out) + off, n, 0.0f, s), outs, 1);
+    }
+    if (!strcmp(kernel, "k_conv1d_step")) {
+        uint32_t ch = p[0], ks = p[1];
+        if (!ch || !ks) return (sg_err){"gpu: k_conv1d_step: bad shape"};
+        if (sg_failed(e = need(a, (uint64_t)ch * 4, "x")) || sg_failed(e = need(b, (uint64_t)ch * ks * 4, "w")) ||
+            sg_failed(e = need(out, (uint64_t)ch * ks * 4, "out"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        float *o = DEV(out);
+        return finish(g, sgk_conv1d_step(DEV(a), DEV(b), o, o + ch, ch, ks, s), outs, 1);
+    }
+    if (!strcmp(kernel, "k_delta_step")) {
+        uint32_t dk = p[0], dv = p[1];
+        if (!dk || !dv) return (sg_err){"gpu: k_delta_step: bad shape"};
+        if (sg_failed(e = need(a, (uint64_t)dk * dv * 4, "S")) || sg_failed(e = need(b, (uint64_t)(2 * dk + dv) * 4, "qkv")) ||
+            sg_failed(e = need(out, (uint64_t)dv * 4, "out"))) return e;
+        void *t;
+        if (sg_failed(e = scratch(g, 8, &t))) return e;
+        float gates[2] = {fbits(p[2]), fbits(p[3])};
+        if (sg_failed(e = push(ins, 3))) return e;
+        HIPCHK(hipMemcpy(t, gates, 8, hipMemcpyHostToDevice), "gates upload");
+        void *o2[2] = {out, a};
+        return finish(g, sgk_delta_multi(DEV(a), DEV(b), DEV(out), t, dk, dv, 1, 1, dk, 1, s), o2, 2);
+    }
+    if (!strcmp(kernel, "k_rmsnorm_gated")) {
+        uint32_t dv = p[0], nh = p[1];
+        if (!dv || !nh) return (sg_err){"gpu: k_rmsnorm_gated: bad shape"};
+        uint64_t nb = (uint64_t)dv * nh * 4;
+        if (sg_failed(e = need(a, nb, "y")) || sg_failed(e = need(b, nb + (uint64_t)dv * 4, "z|w")) ||
+            sg_failed(e = need(out, nb, "out"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        const float *zb = DEV(b);
+        return finish(g, sgk_rmsnorm_gated(DEV(a), zb, zb + (uint64_t)dv * nh, DEV(out), dv, nh, fbits(p[2]), s), outs, 1);
+    }
+    if (!strcmp(kernel, "k_matmul_q8")) {
+        uint32_t N = p[0], M = p[1], K = p[2];
+        if (!N || !M || !K || K % 32) return (sg_err){"gpu: k_matmul_q8: bad shape (K must be a nonzero multiple of 32)"};
+        if (sg_failed(e = need(a, (uint64_t)N * K * 4, "X")) || sg_failed(e = need(b, (uint64_t)M * (K / 32) * 34, "W")) ||
+            sg_failed(e = need(out, (uint64_t)N * M * 4, "Y"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        void *t;
+        if (sg_failed(e = scratch(g, (uint64_t)M * K + (uint64_t)M * (K / 32) * 2 + 256, &t))) return e;
+        int8_t *qs = t;
+        uint16_t *d = (uint16_t *)((char *)t + (((uint64_t)M * K + 255) / 256 * 256));
+        hipError_t he = sgk_repack_q8(DEV(b), M, K, qs, d, 0, 1, s);
+        if (he == hipSuccess) he = sgk_gemm_q8(DEV(a), qs, d, DEV(out), N, M, K, s);
+        return finish(g, he, outs, 1);
+    }
+    return errf("gpu: unknown kernel '%s'", kernel);
+}
+
+/* ---------------------------------------------------------------------
+ * attention one-shots (surge.h:774-980)
+ * --------------------------------------------------------------------- */
+
+static sg_err attn_check(const uint32_t p[8], bool need_splits) {
+    uint32_t nh = p[0], nkv = p[1], hd = p[2], qs = p[4];
+    if (!nh || !nkv || nh % nkv) return (sg_err){"gpu: n_heads must be a nonzero multiple of n_kv_heads"};
+    if (nh / nkv > 8) return (sg_err){"gpu: GQA group wider than 8 is not supported"};
+    if (hd != 16 && hd != 32 && hd != 64 && hd != 128 && hd != 256) return (sg_err){"gpu: head_dim must be 16, 32, 64, 128 or 256"};
+    if (qs < hd) return (sg_err){"gpu: q_stride < head_dim"};
+    if (need_splits && (!p[6] || p[6] > 1024)) return (sg_err){"gpu: n_splits must be in [1, 1024]"};
+    return SG_OK;
+}
+
+sg_err sg_gpu_run_attn_splitk_partial_gqa(sg_gpu *g, void *q, void *k, void *v, void *m,
+                                          void *s, void *acc, const uint32_t p[8]) {
+    if (!g || !q || !k || !v || !m || !s || !acc || !p) return (sg_err){"gpu: attention one-shot got a NULL argument"};
+    sg_err e = attn_check(p, true);
+    if (sg_failed(e)) return e;
+    uint32_t nh = p[0], nkv = p[1], hd = p[2], seq = p[3], qs = p[4], ns = p[6];
+    uint64_t kvb = (uint64_t)seq * nkv * hd * 2;
+    if (sg_failed(e = need(q, ((uint64_t)(nh - 1) * qs + hd) * 4, "q")) ||
+        (seq && (sg_failed(e = need(k, kvb, "k")) || sg_failed(e = need(v, kvb, "v")))) ||
+        sg_failed(e = need(m, (uint64_t)nh * ns * 4, "m")) || sg_failed(e = need(s, (uint64_t)nh * ns * 4, "s")) ||
+        sg_failed(e = need(acc, (uint64_t)nh * ns * hd * 4, "acc"))) return e;
+    void *outs[3] = {m, s, acc};
+    for (int i = 0; i < 3; i++)
+        if (overlap(outs[i], q) || overlap(outs[i], k) || overlap(outs[i], v) ||
+            overlap(outs[i], outs[(i + 1) % 3])) return (sg_err){"gpu: attention outputs must not overlap"};
+    void *ins[3] = {q, k, v};
+    if (sg_failed(e = push(ins, 3))) return e;
+    g->splitk_gqa_dispatches++;
+    return finish(g, sgk_attn_partial(DEV(q), DEV(k), DEV(v), DEV(m), DEV(s), DEV(acc), NULL, nh, nkv, hd,
+                                      seq, qs, fbits(p[5]), ns, ns, g->stream), outs, 3);
+}
+
+sg_err sg_gpu_run_attn_splitk_partial(sg_gpu *g, void *q, void *k, void *v, void *m, void *s,
+                                      void *acc, const uint32_t p[8]) {
+    /* One kernel serves every GQA group size; the per-head and GQA partials
+     * of the reference produce the same bytes, and so do these. */
+    return sg_gpu_run_attn_splitk_partial_gqa(g, q, k, v, m, s, acc, p);
+}
+
+sg_err sg_gpu_run_attn_splitk_combine(sg_gpu *g, void *m, void *s, void *acc, void *out,
+                                      const uint32_t p[8]) {
+    if (!g || !m || !s || !acc || !out || !p) return (sg_err){"gpu: combine got a NULL argument"};
+    uint32_t nh = p[0], hd = p[2], ns = p[6];
+    if (!nh || !hd || !ns || ns > 1024) return (sg_err){"gpu: combine: bad shape"};
+    sg_err e;
+    if (sg_failed(e = need(m, (uint64_t)nh * ns * 4, "m")) || sg_failed(e = need(s, (uint64_t)nh * ns * 4, "s")) ||
+        sg_failed(e = need(acc, (uint64_t)nh * ns * hd * 4, "acc")) || sg_failed(e = need(out, (uint64_t)nh * hd * 4, "out")))
+        return e;
+    if (overlap(out, m) || overlap(out, s) || overlap(out, acc)) return (sg_err){"gpu: combine output overlaps an input"};
+    void *ins[3] = {m, s, acc}, *outs[1] = {out};
+    if (sg_failed(e = push(ins, 3))) return e;
+    return finish(g, sgk_attn_combine(DEV(m), DEV(s), DEV(acc), DEV(out), NULL, 0, NULL, nh, hd, ns, ns, g->stream),
+                  outs, 1);
+}
+
+sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out,
+                                  const uint32_t p[8]) {
+    /* Single-pass decode attention: the split-K pair with one split per 32
+     * keys, combined, in one call. p: [0]=nh [1]=nkv [2]=hd [3]=seq [4]=q_stride [5]=scale. */
+    if (!g || !q || !k || !v || !out || !p) return (sg_err){"gpu: attention one-shot got a NULL argument"};
+    uint32_t pp[8];
+    memcpy(pp, p, sizeof pp);
+    pp[6] = sgk_n_splits(p[3]);
+    sg_err e = attn_check(pp, true);
+    if (sg_failed(e)) return e;
+    uint32_t nh = pp[0], nkv = pp[1], hd = pp[2], seq = pp[3], qs = pp[4], ns = pp[6];
+    uint64_t kvb = (uint64_t)seq * nkv * hd * 2;
+    if (sg_failed(e = need(q, ((uint64_t)(nh - 1) * qs + hd) * 4, "q")) ||
+        (seq && (sg_failed(e = need(k, kvb, "k")) || sg_failed(e = need(v, kvb, "v")))) ||
+        sg_failed(e = need(out, (uint64_t)nh * hd * 4, "out"))) return e;
+    void *t;
+    if (sg_failed(e = scratch(g, (uint64_t)nh * ns * (2 + hd) * 4, &t))) return e;
+    float *mm = t, *ss = mm + (uint64_t)nh * ns, *aa = ss + (uint64_t)nh * ns;
+    void *ins[3] = {q, k, v}, *outs[1] = {out};
+    if (sg_failed(e = push(ins, 3))) return e;
+    hipError_t he = sgk_attn_partial(DEV(q), DEV(k), DEV(v), mm, ss, aa, NULL, nh, nkv, hd, seq, qs, fbits(pp[5]), ns, ns, g->stream);
+    if (he == hipSuccess) he = sgk_attn_combine(mm, ss, aa, DEV(out), NULL, 0, NULL, nh, hd, ns, ns, g->stream);
+    return finish(g, he, outs, 1);
+}
+
+/* Split policy (surge.h:1020-1106), re-derived for 256 CUs: see kernels.h. */
+uint32_t sg_gpu_splitk_n_splits(uint32_t seq) { return sgk_n_splits(seq); }
+uint32_t sg_gpu_splitk_gqa_n_splits(uint32_t seq) { return sgk_n_splits(seq); }
+uint32_t sg_gpu_splitk_gqa_n_splits_at(const sg_gpu *g, uint32_t seq) { (void)g; return sgk_n_splits(seq); }
+uint32_t sg_gpu_splitk_gqa_cap(const sg_gpu *g) { (void)g; return SGK_MAX_SPLITS; }
+bool sg_gpu_splitk_gqa_selected(const sg_gpu *g, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq) {
+    (void)seq;
+    return g && n_kv_heads && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8;
+}
+void sg_gpu_splitk_dispatch_counts(const sg_gpu *g, uint64_t *per_head, uint64_t *gqa) {
+    if (per_head) *per_head = 0;
+    if (gqa) *gqa = g ? g->splitk_gqa_dispatches : 0;
+}
+
+sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *gates,
+                              const uint32_t p[8]) {
+    if (!g || !S || !qkv || !out || !gates || !p) return (sg_err){"gpu: delta_multi got a NULL argument"};
+    uint32_t dk = p[0], dv = p[1], nv = p[2], nk = p[3], kd = p[4];
+    if (!dk || !dv || !nv || !nk || nv % nk || kd < nk * dk) return (sg_err){"gpu: delta_multi: bad shape"};
+    if (dk != 32 && dk != 64 && dk != 128 && dk != 256) return (sg_err){"gpu: delta_multi: dk must be 32, 64, 128 or 256"};
+    sg_err e;
+    if (sg_failed(e = need(S, (uint64_t)nv * dv * dk * 4, "S")) ||
+        sg_failed(e = need(qkv, ((uint64_t)2 * kd + (uint64_t)nv * dv) * 4, "qkv")) ||
+        sg_failed(e = need(out, (uint64_t)nv * dv * 4, "out")) || sg_failed(e = need(gates, (uint64_t)2 * nv * 4, "gates")))
+        return e;
+    void *ins[4] = {S, qkv, gates, out}, *outs[2] = {S, out};
+    if (sg_failed(e = push(ins, 4))) return e;
+    return finish(g, sgk_delta_multi(DEV(S), DEV(qkv), DEV(out), DEV(gates), dk, dv, nv, nk, kd, p[5] != 0, g->stream),
+                  outs, 2);
+}
+
+/* ---------------------------------------------------------------------
+ * model load
+ * --------------------------------------------------------------------- */
+
+static void model_free(sg_gpu *g) {
+    if (!g->ls) return;
+    /* every device pointer is in the allocation table; sg_gpu_free releases
+     * them. Here we only drop the layer table so a reload starts clean. */
+    free(g->ls);
+    g->ls = NULL;
+    g->model = NULL;
+}
+
+static sg_err mat_alloc(sg_gpu *g, dmat *M, uint32_t rows, uint32_t cols) {
+    M->rows = rows;
+    M->cols = cols;
+    sg_err e;
+    if (g->q8) {
+        if (sg_failed(e = dalloc(g, (uint64_t)rows * cols, (void **)&M->qs))) return e;
+        return dalloc(g, (uint64_t)rows * (cols / 32) * 2, (void **)&M->d);
+    }
+    return dalloc(g, (uint64_t)rows * cols * 4, (void **)&M->wf);
+}
+
+/* Uploads one [rows, cols] weight from host memory into rows row0,
+ * row0+step, ... of a device matrix. */
+static sg_err mat_put(sg_gpu *g, dmat *M, const void *host, uint32_t rows, uint32_t row0,
+                      uint32_t step, void *stage) {
+    uint32_t cols = M->cols;
+    if (g->q8) {
+        uint64_t raw = (uint64_t)rows * (cols / 32) * 34;
+        HIPCHK(hipMemcpyAsync(stage, host, raw, hipMemcpyHostToDevice, g->stream), "weight upload");
+        HIPCHK(sgk_repack_q8(stage, rows, cols, M->qs, M->d, row0, step, g->stream), "repack");
+        HIPCHK(hipStreamSynchronize(g->stream), "repack");
+        return SG_OK;
+    }
+    for (uint32_t r = 0; r < rows; r++)
+        HIPCHK(hipMemcpy(M->wf + (uint64_t)(row0 + (uint64_t)r * step) * cols, (const float *)host + (uint64_t)r * cols,
+                         (uint64_t)cols * 4, hipMemcpyHostToDevice), "weight upload");
+    return SG_OK;
+}
+
+static float bf16f(uint16_t h) { uint32_t u = (uint32_t)h << 16; float f; memcpy(&f, &u, 4); return f; }
+
+static sg_err small_put(sg_gpu *g, float **dst, const void *src, sg_tensor_type t, uint64_t n, float shift) {
+    float *tmp = malloc(n * 4);
+    if (!tmp) return (sg_err){"gpu: out of host memory"};
+    for (uint64_t i = 0; i < n; i++)
+        tmp[i] = (t == SG_T_BF16 ? bf16f(((const uint16_t *)src)[i]) : ((const float *)src)[i]) + shift;
+    sg_err e = dalloc(g, n * 4, (void **)dst);
+    if (!sg_failed(e) && hipMemcpy(*dst, tmp, n * 4, hipMemcpyHostToDevice) != hipSuccess)
+        e = (sg_err){"gpu: small tensor upload failed"};
+    free(tmp);
+    return e;
+}
+
+static sg_err check_model(const sg_model *m) {
+    const sg_cfg *c = &m->cfg;
+    if (!m->layers || !m->tok_emb || !m->out_norm || !m->lm_head) return (sg_err){"gpu: model is missing tensors"};
+    if (!c->n_layers || !c->hidden || !c->ffn_hidden || !c->vocab || !c->head_dim || !c->n_heads || !c->n_kv_heads ||
+        !c->full_attn_interval)
+        return (sg_err){"gpu: model config has a zero dimension"};
+    if (m->wtype != SG_T_Q8_0 && m->wtype != SG_T_F32) return (sg_err){"gpu: matmul weights must be Q8_0 or F32"};
+    if (c->n_heads % c->n_kv_heads || c->n_heads / c->n_kv_heads > 8) return (sg_err){"gpu: GQA group must divide and be at most 8"};
+    if (c->head_dim != 16 && c->head_dim != 32 && c->head_dim != 64 && c->head_dim != 128 && c->head_dim != 256)
+        return (sg_err){"gpu: head_dim must be 16, 32, 64, 128 or 256"};
+    for (uint32_t i = 0; i < c->n_layers; i++) {
+        bool is_attn = m->layers[i].q_proj != NULL;
+        if (is_attn != ((i + 1) % c->full_attn_interval == 0))
+            return (sg_err){"gpu: layer kind disagrees with full_attn_interval"};
+        if (!is_attn) {
+            if (!c->n_k_heads || !c->n_v_heads || c->n_v_heads % c->n_k_heads || c->conv_kernel < 1 || c->conv_kernel > 4)
+                return (sg_err){"gpu: DeltaNet dims unsupported (conv_kernel 1..4, n_v multiple of n_k)"};
+            if (c->head_k_dim != 32 && c->head_k_dim != 64 && c->head_k_dim != 128 && c->head_k_dim != 256)
+                return (sg_err){"gpu: head_k_dim must be 32, 64, 128 or 256"};
+        } else if (c->rope_dim < 2 || c->rope_dim > c->head_dim || c->rope_dim % 2) {
+            return (sg_err){"gpu: rope_dim must be even and in [2, head_dim]"};
+        }
+    }
+    if (m->wtype == SG_T_Q8_0) {
+        uint32_t w[] = { c->hidden, c->ffn_hidden, c->n_heads * c->head_dim, c->n_v_heads * c->head_v_dim };
+        for (int i = 0; i < 4; i++) if (w[i] % 32) return (sg_err){"gpu: a Q8_0 matmul width is not a multiple of 32"};
+    }
+    return SG_OK;
+}
+
+sg_err sg_gpu_load_model(sg_gpu *g, const sg_model *m) {
+    if (!g || !m) return (sg_err){"gpu: sg_gpu_load_model got a NULL argument"};
+    sg_err e = check_model(m);
+    if (sg_failed(e)) return e;
+    if (g->have_state) state_free(g);
+    model_free(g);
+    const sg_cfg *c = &m->cfg;
+    g->cfg = *c;
+    g->q8 = m->wtype == SG_T_Q8_0;
+    g->key_dim = c->n_k_heads * c->head_k_dim;
+    g->value_dim = c->n_v_heads * c->head_v_dim;
+    g->conv_dim = 2 * g->key_dim + g->value_dim;
+    g->attn_width = c->n_heads * c->head_dim;
+    g->q_width = c->attn_output_gate ? 2 * g->attn_width : g->attn_width;
+    g->kv_width = c->n_kv_heads * c->head_dim;
+    g->ls = calloc(c->n_layers, sizeof *g->ls);
+    if (!g->ls) return (sg_err){"gpu: out of memory"};
+
+    /* staging for the largest single weight */
+    uint64_t H = c->hidden, F = c->ffn_hidden;
+    uint64_t maxrows = c->vocab;
+    if (F > maxrows) maxrows = F;
+    uint64_t maxelems = maxrows * (H > F ? H : F);
+    uint64_t big[] = { (uint64_t)g->q_width * H, (uint64_t)g->conv_dim * H, (uint64_t)g->value_dim * H, H * g->attn_width };
+    for (int i = 0; i < 4; i++) if (big[i] > maxelems) maxelems = big[i];
+    void *stage = NULL;
+    if (g->q8 && sg_failed(e = dalloc(g, maxelems / 32 * 34 + 256, &stage))) return e;
+
+    float sh = m->norms_are_residual ? 1.0f : 0.0f;
+    for (uint32_t i = 0; i < c->n_layers && !sg_failed(e); i++) {
+        const sg_layer_w *w = &m->layers[i];
+        glayer *L = &g->ls[i];
+        L->attn = w->q_proj != NULL;
+        if (sg_failed(e = small_put(g, &L->ln1, w->ln1, m->dense_type, H, sh))) break;
+        if (sg_failed(e = small_put(g, &L->ln2, w->ln2, m->dense_type, H, sh))) break;
+        if (sg_failed(e = mat_alloc(g, &L->gu, 2 * c->ffn_hidden, c->hidden))) break;
+        if (sg_failed(e = mat_put(g, &L->gu, w->gate_proj, c->ffn_hidden, 0, 2, stage))) break;
+        if (sg_failed(e = mat_put(g, &L->gu, w->up_proj, c->ffn_hidden, 1, 2, stage))) break;
+        if (sg_failed(e = mat_alloc(g, &L->down, c->hidden, c->ffn_hidden))) break;
+        if (sg_failed(e = mat_put(g, &L->down, w->down_proj, c->hidden, 0, 1, stage))) break;
+        if (L->attn) {
+            uint32_t rows = g->q_width + 2 * g->kv_width;
+            if (sg_failed(e = mat_alloc(g, &L->in, rows, c->hidden))) break;
+            if (sg_failed(e = mat_put(g, &L->in, w->q_proj, g->q_width, 0, 1, stage))) break;
+            if (sg_failed(e = mat_put(g, &L->in, w->k_proj, g->kv_width, g->q_width, 1, stage))) break;
+            if (sg_failed(e = mat_put(g, &L->in, w->v_proj, g->kv_width, g->q_width + g->kv_width, 1, stage))) break;
+            if (sg_failed(e = mat_alloc(g, &L->out, c->hidden, g->attn_width))) break;
+            if (sg_failed(e = mat_put(g, &L->out, w->o_proj, c->hidden, 0, 1, stage))) break;
+            if (sg_failed(e = small_put(g, &L->qn, w->q_norm, m->dense_type, c->head_dim, sh))) break;
+            if (sg_failed(e = small_put(g, &L->kn, w->k_norm, m->dense_type, c->head_dim, sh))) break;
+        } else {
+            uint32_t nv = c->n_v_heads, rows = g->conv_dim + g->value_dim + 2 * nv;
+            if (sg_failed(e = mat_alloc(g, &L->in, rows, c->hidden))) break;
+            if (sg_failed(e = mat_put(g, &L->in, w->ssm_in_qkv, g->conv_dim, 0, 1, stage))) break;
+            if (sg_failed(e = mat_put(g, &L->in, w->ssm_in_z, g->value_dim, g->conv_dim, 1, stage))) break;
+            if (sg_failed(e = mat_put(g, &L->in, w->ssm_in_b, nv, g->conv_dim + g->value_dim, 1, stage))) break;
+            if (sg_failed(e = mat_put(g, &L->in, w->ssm_in_a, nv, g->conv_dim + g->value_dim + nv, 1, stage))) break;
+            if (sg_failed(e = mat_alloc(g, &L->out, c->hidden, g->value_dim))) break;
+            if (sg_failed(e = mat_put(g, &L->out, w->ssm_out, c->hidden, 0, 1, stage))) break;
+            if (sg_failed(e = small_put(g, &L->ssm_norm, w->ssm_norm, m->ssm_norm_type, c->head_v_dim, 0.0f))) break;
+            if (sg_failed(e = small_put(g, &L->ssm_a, w->ssm_a, m->ssm_a_type, nv, 0.0f))) break;
+            if (sg_failed(e = small_put(g, &L->dt_bias, w->ssm_dt_bias, m->dense_type, nv, 0.0f))) break;
+            if (sg_failed(e = small_put(g, &L->conv_w, w->ssm_conv1d, m->dense_type, (uint64_t)g->conv_dim * c->conv_kernel, 0.0f))) break;
+        }
+    }
+    if (!sg_failed(e)) e = mat_alloc(g, &g->emb, c->vocab, c->hidden);
+    if (!sg_failed(e)) e = mat_put(g, &g->emb, m->tok_emb, c->vocab, 0, 1, stage);
+    g->lm_is_emb = m->lm_head == m->tok_emb;
+    if (!sg_failed(e)) {
+        if (g->lm_is_emb) {
+            g->lm = g->emb;
+        } else {
+            e = mat_alloc(g, &g->lm, c->vocab, c->hidden);
+            if (!sg_failed(e)) e = mat_put(g, &g->lm, m->lm_head, c->vocab, 0, 1, stage);
+        }
+    }
+    if (!sg_failed(e)) e = small_put(g, &g->out_norm, m->out_norm, m->dense_type, H, sh);
+    dfree(g, stage);
+    if (sg_failed(e)) { model_free(g); return e; }
+    g->model = m;
+    return SG_OK;
+}
+
+/* ---------------------------------------------------------------------
+ * decode state and the per-token graph
+ * --------------------------------------------------------------------- */
+
+static void state_free(sg_gpu *g) {
+    if (!g->have_state) return;
+    if (g->g_fwd) hipGraphExecDestroy(g->g_fwd);
+    if (g->g_greedy) hipGraphExecDestroy(g->g_greedy);
+    g->g_fwd = g->g_greedy = NULL;
+    if (g->h_step) hipHostFree(g->h_step);
+    if (g->h_logits) hipHostFree(g->h_logits);
+    if (g->h_tok) hipHostFree(g->h_tok);
+    g->h_step = NULL;
+    g->h_logits = NULL;
+    g->h_tok = NULL;
+    for (uint32_t i = 0; g->ls && i < g->cfg.n_layers; i++) {
+        glayer *L = &g->ls[i];
+        dfree(g, L->kc); dfree(g, L->vc); dfree(g, L->ring); dfree(g, L->S);
+        L->kc = L->vc = NULL; L->ring = L->S = NULL;
+    }
+    void *bufs[] = { g->cs_table, g->x, g->act, g->ctx, g->ybuf, g->ffg, g->logits, g->am, g->as,
+                     g->aacc, g->amax_scratch, g->hist, g->d_step };
+    for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) dfree(g, bufs[i]);
+    g->cs_table = g->x = g->act = g->ctx = g->ybuf = g->ffg = g->logits = g->am = g->as = g->aacc = NULL;
+    g->amax_scratch = g->hist = NULL;
+    g->d_step = NULL;
+    g->have_state = false;
+}
+
+/* Enqueues one decode step (everything after the step descriptor is set). */
+static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
+    const sg_cfg *c = &g->cfg;
+    hipStream_t s = g->stream;
+    hipError_t e;
+    const int8_t *eq = g->emb.qs;
+    if ((e = sgk_embed(eq, g->emb.d, g->emb.wf, c->hidden, g->d_step, 0, g->x, s)) != hipSuccess) return e;
+    const uint32_t hd = c->head_dim, qs = c->attn_output_gate ? 2 * hd : hd;
+    for (uint32_t i = 0; i < c->n_layers; i++) {
+        glayer *L = &g->ls[i];
+        sgk_gemv a = {0};
+        a.qs = L->in.qs; a.d = L->in.d; a.wf = L->in.wf; a.rows = L->in.rows; a.cols = L->in.cols;
+        a.x = g->x; a.nw = L->ln1; a.eps = c->rms_eps; a.y = g->act;
+        a.pro = SGK_PRO_RMS; a.epi = SGK_EPI_STORE;
+        if ((e = sgk_gemv_launch(&a, s)) != hipSuccess) return e;
+        sgk_gemv o = {0};
+        o.qs = L->out.qs; o.d = L->out.d; o.wf = L->out.wf; o.rows = L->out.rows; o.cols = L->out.cols;
+        o.y = g->x; o.epi = SGK_EPI_ADD; o.eps = c->rms_eps;
+        if (L->attn) {
+            if ((e = sgk_attn_prep(g->act, L->qn, L->kn, g->cs_table, L->kc, L->vc, g->d_step, c->n_heads,
+                                   c->n_kv_heads, hd, c->rope_dim, qs, c->rms_eps, s)) != hipSuccess) return e;
+            if ((e = sgk_attn_partial(g->act, L->kc, L->vc, g->am, g->as, g->aacc, g->d_step, c->n_heads,
+                                      c->n_kv_heads, hd, 0, qs, (float)(1.0 / sqrt((double)hd)), 0,
+                                      g->max_splits, s)) != hipSuccess) return e;
+            if ((e = sgk_attn_combine(g->am, g->as, g->aacc, g->ctx, c->attn_output_gate ? g->act + hd : NULL, qs,
+                                      g->d_step, c->n_heads, hd, 0, g->max_splits, s)) != hipSuccess) return e;
+            o.x = g->ctx; o.pro = SGK_PRO_NONE;
+        } else {
+            sgk_gdn d = {0};
+            d.in = g->act; d.conv_w = L->conv_w; d.ring = L->ring; d.ssm_a = L->ssm_a; d.dt_bias = L->dt_bias;
+            d.S = L->S; d.y = g->ybuf; d.step = g->d_step; d.n_k = c->n_k_heads; d.n_v = c->n_v_heads;
+            d.dk = c->head_k_dim; d.dv = c->head_v_dim; d.conv_dim = g->conv_dim; d.ksize = c->conv_kernel;
+            d.tiled = g->model->v_heads_tiled; d.neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
+            if ((e = sgk_gdn_step(&d, s)) != hipSuccess) return e;
+            o.x = g->ybuf; o.pro = SGK_PRO_RMS_GATED; o.z = g->act + g->conv_dim; o.nw = L->ssm_norm;
+            o.head = c->head_v_dim;
+        }
+        if ((e = sgk_gemv_launch(&o, s)) != hipSuccess) return e;
+        sgk_gemv f = {0};
+        f.qs = L->gu.qs; f.d = L->gu.d; f.wf = L->gu.wf; f.rows = L->gu.rows; f.cols = L->gu.cols;
+        f.x = g->x; f.nw = L->ln2; f.eps = c->rms_eps; f.y = g->ffg; f.pro = SGK_PRO_RMS; f.epi = SGK_EPI_SWIGLU;
+        if ((e = sgk_gemv_launch(&f, s)) != hipSuccess) return e;
+        sgk_gemv dn = {0};
+        dn.qs = L->down.qs; dn.d = L->down.d; dn.wf = L->down.wf; dn.rows = L->down.rows; dn.cols = L->down.cols;
+        dn.x = g->ffg; dn.y = g->x; dn.pro = SGK_PRO_NONE; dn.epi = SGK_EPI_ADD;
+        if ((e = sgk_gemv_launch(&dn, s)) != hipSuccess) return e;
+    }
+    sgk_gemv lm = {0};
+    lm.qs = g->lm.qs; lm.d = g->lm.d; lm.wf = g->lm.wf; lm.rows = g->lm.rows; lm.cols = g->lm.cols;
+    lm.x = g->x; lm.nw = g->out_norm; lm.eps = c->rms_eps; lm.y = g->logits; lm.pro = SGK_PRO_RMS; lm.epi = SGK_EPI_STORE;
+    if ((e = sgk_gemv_launch(&lm, s)) != hipSuccess) return e;
+    if (greedy) {
+        /* next token = argmax, written straight into the descriptor, then
+         * recorded and the position advanced (sgk_step_advance). */
+        if ((e = sgk_argmax(g->logits, c->vocab, (uint32_t *)&g->d_step->token, g->amax_scratch, s)) != hipSuccess)
+            return e;
+        if ((e = sgk_step_advance(g->d_step, g->hist, s)) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+static sg_err capture(sg_gpu *g, bool greedy, hipGraphExec_t *out) {
+    hipGraph_t graph = NULL;
+    HIPCHK(hipStreamBeginCapture(g->stream, hipStreamCaptureModeRelaxed), "graph capture begin");
+    hipError_t le = enqueue_step(g, greedy);
+    hipError_t ce = hipStreamEndCapture(g->stream, &graph);
+    if (le != hipSuccess) { if (graph) hipGraphDestroy(graph); return errf("gpu: capture launch failed: %s", hipGetErrorString(le)); }
+    if (ce != hipSuccess) return errf("gpu: graph capture failed: %s", hipGetErrorString(ce));
+    hipError_t ie = hipGraphInstantiate(out, graph, NULL, NULL, 0);
+    hipGraphDestroy(graph);
+    if (ie != hipSuccess) return errf("gpu: graph instantiate failed: %s", hipGetErrorString(ie));
+    return SG_OK;
+}
+
+sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
+    if (!g || !m) return (sg_err){"gpu: sg_gpu_state_new got a NULL argument"};
+    if (m != g->model) return (sg_err){"gpu: this gpu was loaded with a different sg_model"};
+    if (!max_ctx || max_ctx > SG_KV_CAP_MAX) return (sg_err){"gpu: max_ctx must be in [1, 262144]"};
+    state_free(g);
+    const sg_cfg *c = &g->cfg;
+    g->max_ctx = max_ctx;
+    g->max_splits = sgk_n_splits(max_ctx);
+    sg_err e = SG_OK;
+    uint32_t act_rows = 0;
+    for (uint32_t i = 0; i < c->n_layers; i++) if (g->ls[i].in.rows > act_rows) act_rows = g->ls[i].in.rows;
+    for (uint32_t i = 0; i < c->n_layers && !sg_failed(e); i++) {
+        glayer *L = &g->ls[i];
+        if (L->attn) {
+            uint64_t kvb = (uint64_t)max_ctx * g->kv_width * 2;
+            if (!sg_failed(e = dzalloc(g, kvb, (void **)&L->kc))) e = dzalloc(g, kvb, (void **)&L->vc);
+        } else {
+            if (!sg_failed(e = dzalloc(g, (uint64_t)4 * g->conv_dim * 4, (void **)&L->ring)))
+                e = dzalloc(g, (uint64_t)c->n_v_heads * c->head_v_dim * c->head_k_dim * 4, (void **)&L->S);
+        }
+    }
+    uint64_t ah = (uint64_t)c->n_heads * g->max_splits;
+    struct { void **p; uint64_t n; } al[] = {
+        {(void **)&g->x, (uint64_t)c->hidden * 4}, {(void **)&g->act, (uint64_t)act_rows * 4},
+        {(void **)&g->ctx, (uint64_t)g->attn_width * 4 + 4}, {(void **)&g->ybuf, (uint64_t)g->value_dim * 4 + 4},
+        {(void **)&g->ffg, (uint64_t)c->ffn_hidden * 4}, {(void **)&g->logits, (uint64_t)c->vocab * 4},
+        {(void **)&g->am, ah * 4}, {(void **)&g->as, ah * 4}, {(void **)&g->aacc, ah * c->head_dim * 4},
+        {(void **)&g->amax_scratch, 4096}, {(void **)&g->hist, ((uint64_t)max_ctx + 2) * 4},
+        {(void **)&g->d_step, sizeof(sgk_step)},
+    };
+    for (size_t i = 0; i < sizeof al / sizeof *al && !sg_failed(e); i++) e = dzalloc(g, al[i].n, al[i].p);
+    /* RoPE cos|sin per position, angle and trig in double, stored f32
+     * (reference metal.m:4027-4037, ref.c:561-602). */
+    uint32_t rd = c->rope_dim ? c->rope_dim : 2;
+    if (!sg_failed(e)) e = dalloc(g, (uint64_t)max_ctx * rd * 4, (void **)&g->cs_table);
+    if (!sg_failed(e)) {
+        float *t = malloc((uint64_t)max_ctx * rd * 4);
+        if (!t) e = (sg_err){"gpu: out of host memory"};
+        else {
+            uint32_t half = rd / 2;
+            for (uint32_t p = 0; p < max_ctx; p++)
+                for (uint32_t i = 0; i < half; i++) {
+                    double ang = (double)p * pow((double)c->rope_theta, -2.0 * (double)i / (double)rd);
+                    t[(uint64_t)p * rd + i] = (float)cos(ang);
+                    t[(uint64_t)p * rd + half + i] = (float)sin(ang);
+                }
+            if (hipMemcpy(g->cs_table, t, (uint64_t)max_ctx * rd * 4, hipMemcpyHostToDevice) != hipSuccess)
+                e = (sg_err){"gpu: RoPE table upload failed"};
+            free(t);
+        }
+    }
+    if (!sg_failed(e) && hipHostMalloc((void **)&g->h_step, sizeof(sgk_step), 0) != hipSuccess) e = (sg_err){"gpu: hipHostMalloc failed"};
+    if (!sg_failed(e) && hipHostMalloc((void **)&g->h_logits, (uint64_t)c->vocab * 4, 0) != hipSuccess) e = (sg_err){"gpu: hipHostMalloc failed"};
+    if (!sg_failed(e) && hipHostMalloc((void **)&g->h_tok, ((uint64_t)max_ctx + 2) * 4, 0) != hipSuccess) e = (sg_err){"gpu: hipHostMalloc failed"};
+    g->have_state = true;
+    if (!sg_failed(e) && g->use_graph) {
+        e = capture(g, false, &g->g_fwd);
+        if (!sg_failed(e)) e = capture(g, true, &g->g_greedy);
+    }
+    if (sg_failed(e)) { state_free(g); return e; }
+    g->used = 0;
+    return SG_OK;
+}
+
+void sg_gpu_state_reset(sg_gpu *g) {
+    if (!g || !g->have_state) return;
+    hipStreamSynchronize(g->stream);
+    const sg_cfg *c = &g->cfg;
+    for (uint32_t i = 0; i < c->n_layers; i++) {
+        glayer *L = &g->ls[i];
+        if (L->ring) sgk_fill_f32(L->ring, 0.0f, (uint64_t)4 * g->conv_dim, g->stream);
+        if (L->S) sgk_fill_f32(L->S, 0.0f, (uint64_t)c->n_v_heads * c->head_v_dim * c->head_k_dim, g->stream);
+    }
+    hipStreamSynchronize(g->stream);
+    g->used = 0;
+}
+
+uint32_t sg_gpu_used(const sg_gpu *g) { return (g && g->have_state) ? g->used : 0; }
+
+static sg_err step_checks(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos) {
+    if (!g || !m) return (sg_err){"gpu: sg_gpu_forward got a NULL argument"};
+    if (!g->have_state) return (sg_err){"gpu: call sg_gpu_state_new first"};
+    if (m != g->model) return (sg_err){"gpu: this gpu was loaded with a different sg_model"};
+    if (token < 0 || (uint32_t)token >= g->cfg.vocab) return (sg_err){"gpu: token id out of range"};
+    if (pos >= g->max_ctx) return (sg_err){"gpu: position exceeds max_ctx"};
+    if (pos != g->used) return (sg_err){"gpu: positions must be presented in order"};
+    return SG_OK;
+}
+
+static sg_err launch_step(sg_gpu *g, int32_t token, uint32_t pos, bool greedy) {
+    g->h_step->token = token;
+    g->h_step->pos = pos;
+    HIPCHK(hipMemcpyAsync(g->d_step, g->h_step, sizeof(sgk_step), hipMemcpyHostToDevice, g->stream), "step upload");
+    if (g->use_graph) {
+        HIPCHK(hipGraphLaunch(greedy ? g->g_greedy : g->g_fwd, g->stream), "graph launch");
+    } else {
+        hipError_t e = enqueue_step(g, greedy);
+        if (e != hipSuccess) return errf("gpu: decode step launch failed: %s", hipGetErrorString(e));
+    }
+    return SG_OK;
+}
+
+sg_err sg_gpu_forward(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos, const float **logits) {
+    sg_err e = step_checks(g, m, token, pos);
+    if (sg_failed(e)) return e;
+    if (sg_failed(e = launch_step(g, token, pos, false))) return e;
+    HIPCHK(hipMemcpyAsync(g->h_logits, g->logits, (uint64_t)g->cfg.vocab * 4, hipMemcpyDeviceToHost, g->stream), "logits download");
+    HIPCHK(hipStreamSynchronize(g->stream), "decode step");
+    g->used = pos + 1;
+    if (logits) *logits = g->h_logits;
+    return SG_OK;
+}
+
+sg_err sg_gpu_forward_nosync(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos) {
+    sg_err e = step_checks(g, m, token, pos);
+    if (sg_failed(e)) return e;
+    /* The step buffer is reused: wait for the previous upload to drain. */
+    HIPCHK(hipStreamSynchronize(g->stream), "previous step");
+    if (sg_failed(e = launch_step(g, token, pos, false))) return e;
+    g->used = pos + 1;
+    return SG_OK;
+}
+
+sg_err sg_gpu_sync(sg_gpu *g) {
+    if (!g) return (sg_err){"gpu: NULL gpu"};
+    HIPCHK(hipStreamSynchronize(g->stream), "stream synchronize");
+    return SG_OK;
+}
+
+sg_err sg_gpu_argmax(sg_gpu *g, uint32_t *token_out) {
+    if (!g || !token_out || !g->have_state) return (sg_err){"gpu: sg_gpu_argmax needs a live state"};
+    HIPCHK(sgk_argmax(g->logits, g->cfg.vocab, g->hist + g->max_ctx + 1, g->amax_scratch, g->stream), "argmax");
+    HIPCHK(hipMemcpyAsync(g->h_tok, g->hist + g->max_ctx + 1, 4, hipMemcpyDeviceToHost, g->stream), "argmax download");
+    HIPCHK(hipStreamSynchronize(g->stream), "argmax");
+    *token_out = g->h_tok[0];
+    return SG_OK;
+}
+
+/* Device-resident greedy decode (no reference counterpart): feeds `token` at
+ * position `pos`, then n_steps-1 more tokens each chosen on the device by
+ * argmax, with no host round trip in between. out_tokens receives the n
+ * argmax tokens (the token after each step). */
+sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
+                            uint32_t n_steps, int32_t *out_tokens) {
+    sg_err e = step_checks(g, m, token, pos);
+    if (sg_failed(e)) return e;
+    if (!n_steps || (uint64_t)pos + n_steps > g->max_ctx) return (sg_err){"gpu: greedy decode runs past max_ctx"};
+    g->h_step->token = token;
+    g->h_step->pos = pos;
+    HIPCHK(hipMemcpyAsync(g->d_step, g->h_step, sizeof(sgk_step), hipMemcpyHostToDevice, g->stream), "step upload");
+    for (uint32_t i = 0; i < n_steps; i++) {
+        if (g->use_graph) {
+            HIPCHK(hipGraphLaunch(g->g_greedy, g->stream), "graph launch");
+        } else {
+            hipError_t he = enqueue_step(g, true);
+            if (he != hipSuccess) return errf("gpu: decode step launch failed: %s", hipGetErrorString(he));
+        }
+    }
+    HIPCHK(hipMemcpyAsync(g->h_tok, g->hist + pos + 1, (uint64_t)n_steps * 4, hipMemcpyDeviceToHost, g->stream), "tokens download");
+    HIPCHK(hipStreamSynchronize(g->stream), "greedy decode");
+    if (out_tokens) memcpy(out_tokens, g->h_tok, (uint64_t)n_steps * 4);
+    g->used = pos + n_steps;
+    return SG_OK;
+}
+
+/* ---------------------------------------------------------------------
+ * prefill (surge.h:1276-1309)
+ * --------------------------------------------------------------------- */
+
+sg_err sg_gpu_prefill(sg_gpu *g, const sg_model *m, const int32_t *tokens, uint32_t n_tokens,
+                      uint32_t chunk_size, const float **out_last_logits) {
+    (void)chunk_size;
+    if (!g || !m || !tokens) return (sg_err){"gpu: sg_gpu_prefill got a NULL argument"};
+    if (!g->have_state) return (sg_err){"gpu: call sg_gpu_state_new first"};
+    if (m != g->model) return (sg_err){"gpu: this gpu was loaded with a different sg_model"};
+    if (!n_tokens || n_tokens > g->max_ctx) return (sg_err){"gpu: n_tokens must be in [1, max_ctx]"};
+    for (uint32_t i = 0; i < n_tokens; i++)
+        if (tokens[i] < 0 || (uint32_t)tokens[i] >= g->cfg.vocab) return (sg_err){"gpu: token id out of range"};
+    sg_gpu_state_reset(g);
+    sg_err e = SG_OK;
+    for (uint32_t i = 0; i + 1 < n_tokens && !sg_failed(e); i++) e = sg_gpu_forward_nosync(g, m, tokens[i], i);
+    if (sg_failed(e)) return e;
+    return sg_gpu_forward(g, m, tokens[n_tokens - 1], n_tokens - 1, out_last_logits);
+}
+
+void sg_gpu_set_prefill_rest(sg_gpu *g, uint32_t work_budget_ms, uint32_t rest_ms) {
+    (void)g; (void)work_budget_ms; (void)rest_ms;
+}
+uint64_t sg_gpu_prefill_rest_ms(const sg_gpu *g) { (void)g; return 0; }
+void sg_gpu_set_prefill_max_burst(sg_gpu *g, uint32_t max_burst_ms) { (void)g; (void)max_burst_ms; }
+uint64_t sg_gpu_prefill_segments(const sg_gpu *g) { (void)g; return 0; }
+
+/* ---------------------------------------------------------------------
+ * measurement hooks (no reference counterpart)
+ * --------------------------------------------------------------------- */
+
+void *sg_gpu_stream(const sg_gpu *g) { return g ? (void *)g->stream : NULL; }
+
+/* Enqueues (asynchronously, on the library stream) exactly one of the decode
+ * step's GEMV launches for `layer`, against the live state's activation
+ * buffers: which = 0 input projection, 1 output projection, 2 gate/up,
+ * 3 down, 4 lm_head (layer ignored). Used to time one kernel in isolation
+ * with events on sg_gpu_stream; it mutates the activation buffers. */
+sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which) {
+    if (!g || !g->have_state) return (sg_err){"gpu: sg_gpu_enqueue_gemv needs a live state"};
+    if (which != 4 && layer >= g->cfg.n_layers) return (sg_err){"gpu: layer out of range"};
+    const sg_cfg *c = &g->cfg;
+    sgk_gemv a = {0};
+    const dmat *M;
+    a.eps = c->rms_eps;
+    if (which == 4) {
+        M = &g->lm;
+        a.x = g->x; a.nw = g->out_norm; a.y = g->logits; a.pro = SGK_PRO_RMS; a.epi = SGK_EPI_STORE;
+    } else {
+        glayer *L = &g->ls[layer];
+        switch (which) {
+        case 0: M = &L->in; a.x = g->x; a.nw = L->ln1; a.y = g->act; a.pro = SGK_PRO_RMS; a.epi = SGK_EPI_STORE; break;
+        case 1:
+            M = &L->out; a.y = g->x; a.epi = SGK_EPI_ADD;
+            if (L->attn) { a.x = g->ctx; a.pro = SGK_PRO_NONE; }
+            else { a.x = g->ybuf; a.pro = SGK_PRO_RMS_GATED; a.z = g->act + g->conv_dim; a.nw = L->ssm_norm; a.head = c->head_v_dim; }
+            break;
+        case 2: M = &L->gu; a.x = g->x; a.nw = L->ln2; a.y = g->ffg; a.pro = SGK_PRO_RMS; a.epi = SGK_EPI_SWIGLU; break;
+        case 3: M = &L->down; a.x = g->ffg; a.y = g->x; a.pro = SGK_PRO_NONE; a.epi = SGK_EPI_ADD; break;
+        default: return (sg_err){"gpu: which must be 0..4"};
+        }
+    }
+    a.qs = M->qs; a.d = M->d; a.wf = M->wf; a.rows = M->rows; a.cols = M->cols;
+    HIPCHK(sgk_gemv_launch(&a, g->stream), "gemv launch");
+    return SG_OK;
+}

@@ -1,0 +1,164 @@
+/* kernels.h - launchers exported by kernels.hip to the C host layer (hip.c).
+ *
+ * Every launcher is asynchronous on the given stream and takes device
+ * pointers only. Shapes are validated by the caller (hip.c) before any launch:
+ * the kernels trust them. Q8_0 matrices live on the device in a split layout
+ * built at load time by sgk_repack_q8: an int8 plane qs[rows][cols] (each row
+ * 32-byte aligned, so a lane can stream 16 bytes per load) and an f16 scale
+ * plane d[rows][cols/32]. The bytes per weight are the same as the file's
+ * 34-byte blocks.
+ */
+#ifndef SURGE_KERNELS_H
+#define SURGE_KERNELS_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Per-token step descriptor, read by every position-dependent kernel so one
+ * captured HIP graph serves every decode step. */
+typedef struct {
+    int32_t token;
+    uint32_t pos;       /* position being written; attention sees pos+1 keys */
+    uint32_t pad[2];
+} sgk_step;
+
+/* The split-K decode-attention split count (also evaluated on the device).
+ * MI355X policy: about 32 keys per split so that n_splits * n_kv_heads
+ * reaches several hundred workgroups at 4k context on 256 CUs, capped at
+ * SGK_MAX_SPLITS; never more splits than keys. */
+#define SGK_MAX_SPLITS 256u
+#define SGK_KEYS_PER_SPLIT 32u
+static inline uint32_t sgk_n_splits(uint32_t seq) {
+    uint32_t n = (seq + SGK_KEYS_PER_SPLIT - 1) / SGK_KEYS_PER_SPLIT;
+    if (n < 1) n = 1;
+    if (n > SGK_MAX_SPLITS) n = SGK_MAX_SPLITS;
+    return n;
+}
+
+/* GEMV prologues (what is staged into LDS as the input vector) and epilogues
+ * (what is done with each output row). */
+enum { SGK_PRO_NONE = 0, SGK_PRO_RMS = 1, SGK_PRO_RMS_GATED = 2 };
+enum { SGK_EPI_STORE = 0, SGK_EPI_ADD = 1, SGK_EPI_SWIGLU = 2 };
+
+typedef struct {
+    const int8_t *qs;       /* Q8: int8 plane [rows][cols] */
+    const uint16_t *d;      /* Q8: f16 scales [rows][cols/32] */
+    const float *wf;        /* F32 weights [rows][cols] (when qs == NULL) */
+    uint32_t rows, cols;
+    const float *x;         /* input vector [cols] */
+    const float *nw;        /* prologue norm weight ([cols], or [head] for gated) */
+    const float *z;         /* gated prologue: z [cols] */
+    float eps;
+    uint32_t head;          /* gated prologue: head width */
+    float *y;               /* output [rows] (or [rows/2] for SWIGLU) */
+    int pro, epi;
+} sgk_gemv;
+
+hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s);
+
+/* Split Q8_0 blocks (34-byte) of a [rows, cols] matrix into the device layout.
+ * Destination row of source row r is row0 + r * row_step. */
+hipError_t sgk_repack_q8(const uint8_t *src, uint32_t rows, uint32_t cols,
+                         int8_t *qs, uint16_t *d, uint32_t row0, uint32_t row_step,
+                         hipStream_t s);
+
+/* Embedding row gather: x[hidden] = row `token` of the table (token from the
+ * step descriptor when `step` is non-NULL, else `token`). */
+hipError_t sgk_embed(const int8_t *qs, const uint16_t *d, const float *wf, uint32_t hidden,
+                     const sgk_step *step, int32_t token, float *x, hipStream_t s);
+
+/* Elementwise ops: out[i] = op(a[i], b[i]). */
+enum { SGK_EW_SWIGLU = 0, SGK_EW_SILU, SGK_EW_GATE_SIGMOID, SGK_EW_ADD, SGK_EW_SCALE,
+       SGK_EW_TO_F16 };
+hipError_t sgk_elementwise(int op, const float *a, const float *b, void *out, uint32_t n,
+                           float scale, hipStream_t s);
+
+/* RMSNorm over `heads` slices of n elements at stride `stride` (out may
+ * equal x). w may be NULL. */
+hipError_t sgk_rmsnorm_heads(const float *x, const float *w, float *out, uint32_t n,
+                             uint32_t heads, uint32_t stride, float eps, hipStream_t s);
+/* Half-split partial RoPE over `heads` slices, cos|sin table cs[rope_dim]. */
+hipError_t sgk_rope_heads(const float *x, const float *cs, float *out, uint32_t head_dim,
+                          uint32_t rope_dim, uint32_t heads, uint32_t stride, hipStream_t s);
+hipError_t sgk_softmax(const float *x, float *out, uint32_t n, hipStream_t s);
+
+/* Decode attention pre-step, fused: q_norm + RoPE on the q half of each
+ * head (stride 2*hd when gated), k_norm + RoPE on each kv head, then K and V
+ * stored as f16 into the caches at the descriptor's position. cs_table is
+ * [max_ctx][rope_dim] (cos | sin per position). */
+hipError_t sgk_attn_prep(float *qkv, const float *qn, const float *kn, const float *cs_table,
+                         uint16_t *kc, uint16_t *vc, const sgk_step *step,
+                         uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t rope_dim,
+                         uint32_t q_stride, float eps, hipStream_t s);
+
+/* Split-K GQA decode attention partials. One workgroup per (split, kv head)
+ * serves all n_heads/n_kv query heads. seq/n_splits come from the arguments
+ * when step == NULL, else seq = step->pos + 1 and n_splits = sgk_n_splits(seq)
+ * (grid sized for max_splits). */
+hipError_t sgk_attn_partial(const float *q, const uint16_t *kc, const uint16_t *vc,
+                            float *m, float *sacc, float *acc, const sgk_step *step,
+                            uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t seq,
+                            uint32_t q_stride, float scale, uint32_t n_splits,
+                            uint32_t max_splits, hipStream_t s);
+/* LSE combine; optional fused sigmoid output gate read from gate (stride
+ * gstride per head, NULL for none). */
+hipError_t sgk_attn_combine(const float *m, const float *sacc, const float *acc, float *out,
+                            const float *gate, uint32_t gstride, const sgk_step *step,
+                            uint32_t n_heads, uint32_t hd, uint32_t n_splits,
+                            uint32_t max_splits, hipStream_t s);
+
+/* Gated DeltaNet decode step for one layer, fused: causal conv (ring state
+ * of 4 slots indexed by position) + SiLU, q/k RMS (eps 1e-6) and scaling,
+ * the beta/decay gates and the rank-1 state update with readout. Writes the
+ * pre-norm readout y[value_dim]. The out-projection's gated-RMS prologue
+ * finishes the layer. */
+typedef struct {
+    const float *in;        /* GEMV output: qkv[conv_dim] | z[value_dim] | b[n_v] | a[n_v] */
+    const float *conv_w;    /* [conv_dim][ksize] */
+    float *ring;            /* [4][conv_dim] last inputs, slot = position % 4 */
+    const float *ssm_a, *dt_bias;  /* [n_v] */
+    float *S;               /* [n_v][dv][dk] */
+    float *y;               /* [value_dim] */
+    const sgk_step *step;
+    uint32_t n_k, n_v, dk, dv, conv_dim, ksize;
+    int tiled, neg_exp;
+} sgk_gdn;
+hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s);
+
+/* The bare delta rule over every value head (the per-op oracle hook):
+ * qkv holds normalised q|k|v, gates = beta[n_v] | decay[n_v]. */
+hipError_t sgk_delta_multi(float *S, const float *qkv, float *out, const float *gates,
+                           uint32_t dk, uint32_t dv, uint32_t n_v, uint32_t n_k,
+                           uint32_t key_dim, int tiled, hipStream_t s);
+/* Single-token causal conv step (state oldest-first [ksize-1][channels]). */
+hipError_t sgk_conv1d_step(const float *x, const float *w, float *y, float *state,
+                           uint32_t channels, uint32_t ksize, hipStream_t s);
+/* silu(z) * rmsnorm(y, w) per head of dv. */
+hipError_t sgk_rmsnorm_gated(const float *y, const float *z, const float *w, float *out,
+                             uint32_t dv, uint32_t heads, float eps, hipStream_t s);
+
+/* Argmax over n floats, lowest index wins ties; result written to *out. */
+hipError_t sgk_argmax(const float *v, uint32_t n, uint32_t *out, uint32_t *scratch,
+                      hipStream_t s);
+
+/* Greedy bookkeeping inside the decode graph: hist[pos + 1] = token (the
+ * argmax just written into the descriptor), then pos += 1. */
+hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream_t s);
+
+/* Fills n f32 with a value (a kernel, so it may sit inside a captured graph). */
+hipError_t sgk_fill_f32(float *p, float v, uint64_t n, hipStream_t s);
+
+/* Prefill GEMM Y[N][M] = X[N][K] * W[M][K]^T with W in the Q8 device layout,
+ * on MFMA (bf16 inputs, x split hi+lo, fp32 accumulate, per-block scale in
+ * the accumulator). */
+hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, float *Y,
+                       uint32_t N, uint32_t M, uint32_t K, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,1070 @@
+// kernels.hip - hand-written CDNA4 (gfx950) kernels for the batch-1 decode
+// hot path, with extern "C" launchers for the C host layer (hip.c).
+//
+// Reference behaviour each kernel reproduces (reference files):
+//   Q8_0 GEMV            src/ref.c:638-663, src/kernels.metal:227-250
+//   RMSNorm / per-head   src/ref.c:113-125, src/kernels.metal:82-104, :611-635
+//   RoPE (half split)    src/ref.c:561-606, src/kernels.metal:641-663
+//   fp16 KV store        src/kv.c:152-190, src/kernels.metal:432-441
+//   split-K attention    src/ref.c:416-555, src/kernels_splitk.metal:473-683
+//   LSE combine          src/ref.c:256-373, src/kernels_splitk.metal:308-364
+//   output gate          src/ref.c:185-188, src/kernels.metal:668-679
+//   conv1d step          src/ref.c:669-706, src/kernels.metal:520-548
+//   DeltaNet gates/step  src/ref.c:127-170,708-739, src/kernels.metal:742-805
+//   RMSNormGated         src/ref.c:1322-1330, src/kernels.metal:109-134
+//   argmax               src/greedy.c:17-27
+//
+// Design rules (MI355X, 64-wide waves):
+//   - every reduction is a fixed tree (xor butterflies inside a wave, then a
+//     fixed-order fold across waves), no atomics: reruns are bit-identical;
+//   - fp32 arithmetic with IEEE division/sqrt and libm-accurate exp/log (no
+//     fast-math); f16 denormal scales decode exactly;
+//   - the GEMV streams 16-byte loads of int8 weights, coalesced along a row,
+//     with the input vector staged once per workgroup in LDS.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+#define TPB 256
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+// Sum over all 256 threads of a workgroup; every thread gets the same value.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+// Streaming (non-temporal) 16-byte load: weights are read once per token.
+__device__ __forceinline__ uint4 ldnt(const uint4 *p) {
+    const v4u v = __builtin_nontemporal_load((const v4u *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// sigmoid split on the sign so exp never overflows (ref.c:127-134).
+__device__ __forceinline__ float sigm(float x) {
+    if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+    float e = expf(x);
+    return e / (1.0f + e);
+}
+__device__ __forceinline__ float silu(float x) { return x * sigm(x); }
+// max(x,0) + log1p(e^-|x|) (ref.c:136-142).
+__device__ __forceinline__ float softplus(float x) { return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x))); }
+
+__device__ __forceinline__ uint32_t dev_n_splits(uint32_t seq) {
+    uint32_t n = (seq + SGK_KEYS_PER_SPLIT - 1) / SGK_KEYS_PER_SPLIT;
+    n = n < 1 ? 1 : n;
+    return n > SGK_MAX_SPLITS ? SGK_MAX_SPLITS : n;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV: input staging prologues
+// ---------------------------------------------------------------------------
+
+template <int PRO>
+__device__ __forceinline__ void stage_x(const sgk_gemv &a, float *xs) {
+    __shared__ float red[4];
+    const uint32_t n = a.cols, t = threadIdx.x;
+    if (PRO == SGK_PRO_NONE) {
+        for (uint32_t i = t; i < n; i += TPB) xs[i] = a.x[i];
+    } else if (PRO == SGK_PRO_RMS) {
+        // x * (1/sqrt(mean(x^2) + eps)) * w  (ref.c:113-125)
+        float ss = 0.0f;
+        for (uint32_t i = t; i < n; i += TPB) { float v = a.x[i]; xs[i] = v; ss = fmaf(v, v, ss); }
+        ss = block_sum(ss, red);
+        const float r = 1.0f / sqrtf(ss / (float)n + a.eps);
+        for (uint32_t i = t; i < n; i += TPB) xs[i] = (xs[i] * r) * a.nw[i];
+    } else {
+        // silu(z) * rmsnorm(y, w) per head (ref.c:1322-1330)
+        float *rh = xs + n;
+        const uint32_t head = a.head, heads = n / head, lane = t & 63, w = t >> 6;
+        for (uint32_t i = t; i < n; i += TPB) xs[i] = a.x[i];
+        __syncthreads();
+        for (uint32_t h = w; h < heads; h += TPB / 64) {
+            float ss = 0.0f;
+            for (uint32_t j = lane; j < head; j += 64) { float v = xs[h * head + j]; ss = fmaf(v, v, ss); }
+            ss = wave_sum(ss);
+            if (lane == 0) rh[h] = 1.0f / sqrtf(ss / (float)head + a.eps);
+        }
+        __syncthreads();
+        for (uint32_t i = t; i < n; i += TPB) {
+            const uint32_t h = i / head;
+            const float yn = (xs[i] * rh[h]) * a.nw[i - h * head];
+            xs[i] = silu(a.z[i]) * yn;
+        }
+    }
+    __syncthreads();
+}
+
+template <int EPI>
+__device__ __forceinline__ void gemv_store(const sgk_gemv &a, uint32_t row, float v) {
+    if (EPI == SGK_EPI_ADD) a.y[row] += v;
+    else a.y[row] = v;
+}
+
+// Dot product of 16 int8 weights with 16 staged floats.
+__device__ __forceinline__ float dot16(const uint4 q, const float4 x0, const float4 x1,
+                                       const float4 x2, const float4 x3) {
+    float s0, s1;
+    s0 = (float)(int8_t)(q.x) * x0.x;
+    s1 = (float)(int8_t)(q.x >> 8) * x0.y;
+    s0 = fmaf((float)(int8_t)(q.x >> 16), x0.z, s0);
+    s1 = fmaf((float)((int32_t)q.x >> 24), x0.w, s1);
+    s0 = fmaf((float)(int8_t)(q.y), x1.x, s0);
+    s1 = fmaf((float)(int8_t)(q.y >> 8), x1.y, s1);
+    s0 = fmaf((float)(int8_t)(q.y >> 16), x1.z, s0);
+    s1 = fmaf((float)((int32_t)q.y >> 24), x1.w, s1);
+    s0 = fmaf((float)(int8_t)(q.z), x2.x, s0);
+    s1 = fmaf((float)(int8_t)(q.z >> 8), x2.y, s1);
+    s0 = fmaf((float)(int8_t)(q.z >> 16), x2.z, s0);
+    s1 = fmaf((float)((int32_t)q.z >> 24), x2.w, s1);
+    s0 = fmaf((float)(int8_t)(q.w), x3.x, s0);
+    s1 = fmaf((float)(int8_t)(q.w >> 8), x3.y, s1);
+    s0 = fmaf((float)(int8_t)(q.w >> 16), x3.z, s0);
+    s1 = fmaf((float)((int32_t)q.w >> 24), x3.w, s1);
+    return s0 + s1;
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 GEMV. One wave owns R consecutive output rows at a time (grid-stride
+// over row groups); lane l streams 16-byte chunks l, l+64, ... of each row.
+// A chunk is half a Q8_0 block: 16 int8 and the block's f16 scale.
+// ---------------------------------------------------------------------------
+
+template <int R, int PRO, int EPI>
+__global__ void __launch_bounds__(TPB) k_gemv_q8(sgk_gemv a) {
+    extern __shared__ float xs[];
+    stage_x<PRO>(a, xs);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t cols = a.cols, nch = cols >> 4, nbl = cols >> 5;
+    const uint32_t ngroups = (a.rows + R - 1) / R;
+    for (uint32_t g = blockIdx.x * (TPB / 64) + wave; g < ngroups; g += gridDim.x * (TPB / 64)) {
+        const uint32_t r0 = g * R;
+        const uint4 *qrow[R];
+        const uint16_t *drow[R];
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t rr = min(r0 + r, a.rows - 1);
+            qrow[r] = (const uint4 *)(a.qs + (size_t)rr * cols);
+            drow[r] = a.d + (size_t)rr * nbl;
+            acc[r] = 0.0f;
+        }
+        uint32_t c = lane;
+        for (; c + 64 < nch; c += 128) {
+            uint4 qa[R], qb[R];
+            uint16_t da[R], db[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                qa[r] = ldnt(qrow[r] + c);
+                qb[r] = ldnt(qrow[r] + c + 64);
+                da[r] = drow[r][c >> 1];
+                db[r] = drow[r][(c + 64) >> 1];
+            }
+            const float4 *xa = (const float4 *)(xs + c * 16);
+            const float4 *xb = (const float4 *)(xs + (c + 64) * 16);
+            const float4 a0 = xa[0], a1 = xa[1], a2 = xa[2], a3 = xa[3];
+            const float4 b0 = xb[0], b1 = xb[1], b2 = xb[2], b3 = xb[3];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                acc[r] = fmaf(h2f(da[r]), dot16(qa[r], a0, a1, a2, a3), acc[r]);
+                acc[r] = fmaf(h2f(db[r]), dot16(qb[r], b0, b1, b2, b3), acc[r]);
+            }
+        }
+        if (c < nch) {
+            const float4 *xa = (const float4 *)(xs + c * 16);
+            const float4 a0 = xa[0], a1 = xa[1], a2 = xa[2], a3 = xa[3];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint4 q = ldnt(qrow[r] + c);
+                acc[r] = fmaf(h2f(drow[r][c >> 1]), dot16(q, a0, a1, a2, a3), acc[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+        if (EPI == SGK_EPI_SWIGLU) {
+            // rows come in (gate, up) pairs: y[i] = silu(gate_i) * up_i
+#pragma unroll
+            for (int p = 0; p < R / 2; p++)
+                if (lane == (uint32_t)p && r0 + 2 * p + 1 < a.rows)
+                    a.y[(r0 >> 1) + p] = silu(acc[2 * p]) * acc[2 * p + 1];
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (lane == (uint32_t)r && r0 + r < a.rows) gemv_store<EPI>(a, r0 + r, acc[r]);
+        }
+    }
+}
+
+// f32-weight GEMV (small test models only): one wave per row pair.
+template <int PRO, int EPI>
+__global__ void __launch_bounds__(TPB) k_gemv_f32(sgk_gemv a) {
+    extern __shared__ float xs[];
+    stage_x<PRO>(a, xs);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t ngroups = (a.rows + 1) / 2;
+    for (uint32_t g = blockIdx.x * (TPB / 64) + wave; g < ngroups; g += gridDim.x * (TPB / 64)) {
+        const uint32_t r0 = 2 * g, r1 = min(r0 + 1, a.rows - 1);
+        const float *w0 = a.wf + (size_t)r0 * a.cols, *w1 = a.wf + (size_t)r1 * a.cols;
+        float s0 = 0.0f, s1 = 0.0f;
+        for (uint32_t c = lane; c < a.cols; c += 64) {
+            s0 = fmaf(w0[c], xs[c], s0);
+            s1 = fmaf(w1[c], xs[c], s1);
+        }
+        s0 = wave_sum(s0);
+        s1 = wave_sum(s1);
+        if (lane == 0) {
+            if (EPI == SGK_EPI_SWIGLU) {
+                if (r0 + 1 < a.rows) a.y[g] = silu(s0) * s1;
+            } else {
+                gemv_store<EPI>(a, r0, s0);
+                if (r0 + 1 < a.rows) gemv_store<EPI>(a, r0 + 1, s1);
+            }
+        }
+    }
+}
+
+template <typename K>
+static hipError_t launch_lds(K kern, dim3 grid, size_t lds, hipStream_t s, const sgk_gemv &a) {
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(TPB), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int PRO, int EPI>
+static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
+    size_t lds = (size_t)a->cols * 4 + (PRO == SGK_PRO_RMS_GATED ? (a->cols / a->head) * 4 + 16 : 16);
+    if (!a->qs) {
+        uint32_t groups = (a->rows + 1) / 2;
+        uint32_t blocks = min((groups + 3) / 4, 4096u);
+        return launch_lds(k_gemv_f32<PRO, EPI>, dim3(blocks), lds, s, *a);
+    }
+    // Pick rows-per-wave so the grid still covers every CU several times.
+    int R = 4;
+    if (a->rows < 4 * 4 * 1024) R = 2;
+    if (a->rows < 2 * 4 * 1024) R = (EPI == SGK_EPI_SWIGLU) ? 2 : 1;
+    uint32_t groups = (a->rows + R - 1) / R;
+    uint32_t blocks = min((groups + 3) / 4, 8192u);
+    if (R == 4) return launch_lds(k_gemv_q8<4, PRO, EPI>, dim3(blocks), lds, s, *a);
+    if (R == 2) return launch_lds(k_gemv_q8<2, PRO, EPI>, dim3(blocks), lds, s, *a);
+    return launch_lds(k_gemv_q8<1, PRO, (EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI)>, dim3(blocks), lds, s, *a);
+}
+
+extern "C" hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s) {
+#define CASE(P, E) if (a->pro == P && a->epi == E) return gemv_dispatch<P, E>(a, s)
+    CASE(SGK_PRO_NONE, SGK_EPI_STORE);
+    CASE(SGK_PRO_NONE, SGK_EPI_ADD);
+    CASE(SGK_PRO_NONE, SGK_EPI_SWIGLU);
+    CASE(SGK_PRO_RMS, SGK_EPI_STORE);
+    CASE(SGK_PRO_RMS, SGK_EPI_ADD);
+    CASE(SGK_PRO_RMS, SGK_EPI_SWIGLU);
+    CASE(SGK_PRO_RMS_GATED, SGK_EPI_STORE);
+    CASE(SGK_PRO_RMS_GATED, SGK_EPI_ADD);
+#undef CASE
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 repack: 34-byte blocks -> int8 plane + f16 scale plane
+// ---------------------------------------------------------------------------
+
+__global__ void k_repack_q8(const uint8_t *src, uint32_t rows, uint32_t cols, int8_t *qs,
+                            uint16_t *d, uint32_t row0, uint32_t step) {
+    const uint32_t nbl = cols >> 5;
+    const uint64_t b = (uint64_t)blockIdx.x * TPB + threadIdx.x;
+    if (b >= (uint64_t)rows * nbl) return;
+    const uint32_t r = (uint32_t)(b / nbl), j = (uint32_t)(b % nbl);
+    const uint8_t *p = src + b * 34;
+    const uint64_t dr = (uint64_t)row0 + (uint64_t)r * step;
+    d[dr * nbl + j] = (uint16_t)(p[0] | (p[1] << 8));
+    uint32_t *o = (uint32_t *)(qs + dr * cols + (uint64_t)j * 32);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        o[k] = (uint32_t)p[2 + 4 * k] | ((uint32_t)p[3 + 4 * k] << 8) |
+               ((uint32_t)p[4 + 4 * k] << 16) | ((uint32_t)p[5 + 4 * k] << 24);
+}
+
+extern "C" hipError_t sgk_repack_q8(const uint8_t *src, uint32_t rows, uint32_t cols,
+                                    int8_t *qs, uint16_t *d, uint32_t row0, uint32_t row_step,
+                                    hipStream_t s) {
+    const uint64_t n = (uint64_t)rows * (cols >> 5);
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_repack_q8, dim3((unsigned)((n + TPB - 1) / TPB)), dim3(TPB), 0, s, src,
+                       rows, cols, qs, d, row0, row_step);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Embedding gather (ref.c:826-854): d * q in f32, one multiply.
+// ---------------------------------------------------------------------------
+
+__global__ void k_embed(const int8_t *qs, const uint16_t *d, const float *wf, uint32_t hidden,
+                        const sgk_step *step, int32_t token, float *x) {
+    const uint32_t i = blockIdx.x * TPB + threadIdx.x;
+    if (i >= hidden) return;
+    const uint64_t t = (uint64_t)(uint32_t)(step ? step->token : token);
+    if (qs) x[i] = h2f(d[t * (hidden >> 5) + (i >> 5)]) * (float)qs[t * hidden + i];
+    else x[i] = wf[t * hidden + i];
+}
+
+extern "C" hipError_t sgk_embed(const int8_t *qs, const uint16_t *d, const float *wf,
+                                uint32_t hidden, const sgk_step *step, int32_t token, float *x,
+                                hipStream_t s) {
+    hipLaunchKernelGGL(k_embed, dim3((hidden + TPB - 1) / TPB), dim3(TPB), 0, s, qs, d, wf,
+                       hidden, step, token, x);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise ops (ref.c:172-188; kernels.metal:316-335, 694-714)
+// ---------------------------------------------------------------------------
+
+__global__ void k_elementwise(int op, const float *a, const float *b, void *out, uint32_t n,
+                              float scale) {
+    const uint32_t i = blockIdx.x * TPB + threadIdx.x;
+    if (i >= n) return;
+    float *o = (float *)out;
+    switch (op) {
+    case SGK_EW_SWIGLU: o[i] = silu(a[i]) * b[i]; break;
+    case SGK_EW_SILU: o[i] = silu(a[i]); break;
+    case SGK_EW_GATE_SIGMOID: o[i] = a[i] * sigm(b[i]); break;
+    case SGK_EW_ADD: o[i] = a[i] + b[i]; break;
+    case SGK_EW_SCALE: o[i] = a[i] * scale; break;
+    case SGK_EW_TO_F16: ((uint16_t *)out)[i] = f2h(a[i]); break;
+    }
+}
+
+extern "C" hipError_t sgk_elementwise(int op, const float *a, const float *b, void *out,
+                                      uint32_t n, float scale, hipStream_t s) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_elementwise, dim3((n + TPB - 1) / TPB), dim3(TPB), 0, s, op, a, b, out,
+                       n, scale);
+    return hipGetLastError();
+}
+
+__global__ void k_fill(float *p, float v, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * TPB + threadIdx.x; i < n; i += (uint64_t)gridDim.x * TPB)
+        p[i] = v;
+}
+
+extern "C" hipError_t sgk_fill_f32(float *p, float v, uint64_t n, hipStream_t s) {
+    if (!n) return hipSuccess;
+    uint64_t blocks = (n + TPB - 1) / TPB;
+    hipLaunchKernelGGL(k_fill, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(TPB), 0, s, p,
+                       v, n);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm over strided slices; RoPE over strided slices; softmax.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(TPB) k_rmsnorm_heads(const float *x, const float *w, float *out,
+                                                       uint32_t n, uint32_t stride, float eps) {
+    __shared__ float red[4];
+    const float *xh = x + (size_t)blockIdx.x * stride;
+    float *oh = out + (size_t)blockIdx.x * stride;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += TPB) { float v = xh[i]; ss = fmaf(v, v, ss); }
+    ss = block_sum(ss, red);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += TPB) {
+        float v = xh[i] * r;
+        oh[i] = w ? v * w[i] : v;
+    }
+}
+
+extern "C" hipError_t sgk_rmsnorm_heads(const float *x, const float *w, float *out, uint32_t n,
+                                        uint32_t heads, uint32_t stride, float eps,
+                                        hipStream_t s) {
+    if (!heads || !n) return hipSuccess;
+    hipLaunchKernelGGL(k_rmsnorm_heads, dim3(heads), dim3(TPB), 0, s, x, w, out, n,
+                       stride ? stride : n, eps);
+    return hipGetLastError();
+}
+
+__global__ void k_rope_heads(const float *x, const float *cs, float *out, uint32_t head_dim,
+                             uint32_t rope_dim, uint32_t stride) {
+    // head_dim <= TPB (checked by the launcher): one element per thread.
+    const float *xh = x + (size_t)blockIdx.x * stride;
+    float *oh = out + (size_t)blockIdx.x * stride;
+    const uint32_t half = rope_dim >> 1, i = threadIdx.x;
+    float v = 0.0f;
+    if (i < half) v = xh[i] * cs[i] - xh[i + half] * cs[half + i];
+    else if (i < rope_dim) v = xh[i - half] * cs[i] + xh[i] * cs[i - half];
+    else if (i < head_dim) v = xh[i];
+    __syncthreads();   // every read of the slice precedes any in-place write
+    if (i < head_dim) oh[i] = v;
+}
+
+extern "C" hipError_t sgk_rope_heads(const float *x, const float *cs, float *out,
+                                     uint32_t head_dim, uint32_t rope_dim, uint32_t heads,
+                                     uint32_t stride, hipStream_t s) {
+    if (!heads || head_dim > TPB) return heads ? hipErrorInvalidValue : hipSuccess;
+    hipLaunchKernelGGL(k_rope_heads, dim3(heads), dim3(TPB), 0, s, x, cs, out, head_dim, rope_dim,
+                       stride ? stride : head_dim);
+    return hipGetLastError();
+}
+
+// softmax over n with the reference's NaN / +-inf conventions (ref.c:190-235)
+__global__ void __launch_bounds__(TPB) k_softmax(const float *x, float *out, uint32_t n) {
+    __shared__ float red[4];
+    __shared__ float bc[2];
+    float mx = -INFINITY;
+    for (uint32_t i = threadIdx.x; i < n; i += TPB) mx = fmaxf(mx, x[i]);
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) bc[0] = isnan(x[0]) ? x[0] : fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    mx = bc[0];
+    if (isnan(mx)) { for (uint32_t i = threadIdx.x; i < n; i += TPB) out[i] = mx; return; }
+    if (isinf(mx)) {
+        float hits = 0.0f;
+        for (uint32_t i = threadIdx.x; i < n; i += TPB) hits += (x[i] == mx) ? 1.0f : 0.0f;
+        hits = block_sum(hits, red);
+        const float u = 1.0f / (mx < 0.0f ? (float)n : hits);
+        for (uint32_t i = threadIdx.x; i < n; i += TPB) out[i] = (mx < 0.0f || x[i] == mx) ? u : 0.0f;
+        return;
+    }
+    float sum = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += TPB) sum += expf(x[i] - mx);
+    sum = block_sum(sum, red);
+    for (uint32_t i = threadIdx.x; i < n; i += TPB) out[i] = expf(x[i] - mx) / sum;
+}
+
+extern "C" hipError_t sgk_softmax(const float *x, float *out, uint32_t n, hipStream_t s) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_softmax, dim3(1), dim3(TPB), 0, s, x, out, n);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Attention pre-step (decode): q_norm/k_norm + RoPE + f16 KV store.
+// One workgroup per query head, then one per kv head.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(TPB) k_attn_prep(float *qkv, const float *qn, const float *kn,
+                                                   const float *cs_table, uint16_t *kc, uint16_t *vc,
+                                                   const sgk_step *step, uint32_t n_heads,
+                                                   uint32_t n_kv, uint32_t hd, uint32_t rope_dim,
+                                                   uint32_t q_stride, float eps) {
+    __shared__ float red[4];
+    __shared__ float buf[TPB];
+    const uint32_t pos = step->pos, t = threadIdx.x, b = blockIdx.x;
+    const float *cs = cs_table + (size_t)pos * rope_dim;
+    const bool isq = b < n_heads;
+    const uint32_t kh = b - n_heads;
+    float *x = isq ? qkv + (size_t)b * q_stride : qkv + (size_t)n_heads * q_stride + (size_t)kh * hd;
+    const float *w = isq ? qn : kn;
+    const float v = t < hd ? x[t] : 0.0f;
+    const float ss = block_sum(v * v, red);
+    const float r = 1.0f / sqrtf(ss / (float)hd + eps);
+    const float xn = t < hd ? (v * r) * w[t] : 0.0f;
+    buf[t] = xn;
+    __syncthreads();
+    const uint32_t half = rope_dim >> 1;
+    float o = xn;
+    if (t < half) o = buf[t] * cs[t] - buf[t + half] * cs[half + t];
+    else if (t < rope_dim) o = buf[t - half] * cs[t] + buf[t] * cs[t - half];
+    if (t >= hd) return;
+    if (isq) {
+        x[t] = o;
+    } else {
+        const size_t at = ((size_t)pos * n_kv + kh) * hd + t;
+        const float *vraw = qkv + (size_t)n_heads * q_stride + (size_t)n_kv * hd + (size_t)kh * hd;
+        kc[at] = f2h(o);
+        vc[at] = f2h(vraw[t]);
+    }
+}
+
+extern "C" hipError_t sgk_attn_prep(float *qkv, const float *qn, const float *kn,
+                                    const float *cs_table, uint16_t *kc, uint16_t *vc,
+                                    const sgk_step *step, uint32_t n_heads, uint32_t n_kv,
+                                    uint32_t hd, uint32_t rope_dim, uint32_t q_stride, float eps,
+                                    hipStream_t s) {
+    if (hd > TPB) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attn_prep, dim3(n_heads + n_kv), dim3(TPB), 0, s, qkv, qn, kn, cs_table,
+                       kc, vc, step, n_heads, n_kv, hd, rope_dim, q_stride, eps);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Split-K GQA decode attention partial.
+//
+// Workgroup (split i, kv head hk) owns keys [i*seq/n, (i+1)*seq/n) and all
+// G = n_heads/n_kv query heads of the group, so every K/V byte is read once.
+// Keys are processed in tiles of 32: scores (8 lanes per key, HD/8 dims per
+// lane, q from LDS), tile max and exp per head, then P*V with one output dim
+// per lane. Across tiles the running max/sum/acc are rescaled (online
+// softmax); a split of at most 32 keys is exactly the reference's two-pass
+// form. Output: m, s and the UNNORMALISED acc, as ref.c's attn_partial.
+// ---------------------------------------------------------------------------
+
+#define GMAX 8
+#define KT 32
+
+template <int HD>
+__global__ void __launch_bounds__(TPB) k_attn_partial(const float *q, const uint16_t *kc,
+                                                      const uint16_t *vc, float *mo, float *so,
+                                                      float *acco, const sgk_step *step,
+                                                      uint32_t n_heads, uint32_t n_kv,
+                                                      uint32_t seq_arg, uint32_t q_stride,
+                                                      float scale, uint32_t ns_arg) {
+    constexpr int KG = TPB / HD;          // key groups for P*V (HD <= 256)
+    constexpr int DPL = HD / 8;           // dims per lane in the score phase
+    __shared__ float qsh[GMAX][HD];
+    __shared__ float sc[GMAX][KT];
+    __shared__ float mrun[GMAX], srun[GMAX], alpha[GMAX];
+    __shared__ float accx[KG > 1 ? GMAX * TPB : 1];
+
+    const uint32_t G = n_heads / n_kv;
+    const uint32_t seq = step ? step->pos + 1 : seq_arg;
+    const uint32_t ns = step ? dev_n_splits(seq) : ns_arg;
+    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x;
+    if (i >= ns) return;
+    const uint32_t t0 = (uint32_t)((uint64_t)i * seq / ns);
+    const uint32_t t1 = (uint32_t)((uint64_t)(i + 1) * seq / ns);
+    const uint32_t h0 = hk * G;
+
+    for (uint32_t e = t; e < G * HD; e += TPB) {
+        const uint32_t h = e / HD, dd = e % HD;
+        qsh[h][dd] = q[(size_t)(h0 + h) * q_stride + dd];
+    }
+    if (t < GMAX) { mrun[t] = -INFINITY; srun[t] = 0.0f; }
+    __syncthreads();
+
+    const uint32_t d = t % HD, kg = t / HD;      // P*V mapping
+    const uint32_t kj = t >> 3, kp = t & 7;      // score mapping
+    float acc[GMAX];
+#pragma unroll
+    for (int h = 0; h < GMAX; h++) acc[h] = 0.0f;
+
+    for (uint32_t ts = t0; ts < t1; ts += KT) {
+        const uint32_t nk = min((uint32_t)KT, t1 - ts);
+        // V for this tile, issued before the score math so the loads overlap it.
+        float vr[KT / KG];
+#pragma unroll
+        for (int u = 0; u < KT / KG; u++) {
+            const uint32_t j = kg + u * KG;
+            vr[u] = (j < nk) ? h2f(vc[((size_t)(ts + j) * n_kv + hk) * HD + d]) : 0.0f;
+        }
+        // Scores: a group of 8 lanes per key, HD/8 dims per lane.
+        float part[GMAX];
+#pragma unroll
+        for (int h = 0; h < GMAX; h++) part[h] = 0.0f;
+        if (kj < nk) {
+            const uint16_t *kr = kc + ((size_t)(ts + kj) * n_kv + hk) * HD + kp * DPL;
+            float kf[DPL];
+            if constexpr (DPL % 8 == 0) {
+#pragma unroll
+                for (int c8 = 0; c8 < DPL / 8; c8++) {
+                    const uint4 raw = ((const uint4 *)kr)[c8];
+                    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        kf[c8 * 8 + 2 * e] = h2f((uint16_t)(w4[e] & 0xFFFF));
+                        kf[c8 * 8 + 2 * e + 1] = h2f((uint16_t)(w4[e] >> 16));
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < DPL; e++) kf[e] = h2f(kr[e]);
+            }
+#pragma unroll
+            for (int h = 0; h < GMAX; h++) {
+                if (h < (int)G) {
+                    float sacc = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < DPL; e++) sacc = fmaf(qsh[h][kp * DPL + e], kf[e], sacc);
+                    part[h] = sacc;
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < GMAX; h++) {
+            part[h] += __shfl_xor(part[h], 1, 64);
+            part[h] += __shfl_xor(part[h], 2, 64);
+            part[h] += __shfl_xor(part[h], 4, 64);
+        }
+        if (kp == 0) {
+#pragma unroll
+            for (int h = 0; h < GMAX; h++)
+                if (h < (int)G) sc[h][kj] = (kj < nk) ? part[h] * scale : -INFINITY;
+        }
+        __syncthreads();
+        // Per head (32 lanes each): tile max, new running max, p = exp(s - m),
+        // tile sum; lane 0 of the head updates the running max and sum.
+        {
+            const uint32_t h = t >> 5, j = t & 31;
+            if (h < G) {
+                const float v = sc[h][j];
+                float tm = v;
+#pragma unroll
+                for (int o = 16; o >= 1; o >>= 1) tm = fmaxf(tm, __shfl_xor(tm, o, 64));
+                const float mold = mrun[h];
+                const float mnew = fmaxf(mold, tm);
+                const float p = (j < nk) ? expf(v - mnew) : 0.0f;
+                sc[h][j] = p;
+                float ps = p;
+#pragma unroll
+                for (int o = 16; o >= 1; o >>= 1) ps += __shfl_xor(ps, o, 64);
+                if (j == 0) {
+                    const float al = (mold == -INFINITY) ? 0.0f : expf(mold - mnew);
+                    alpha[h] = al;
+                    mrun[h] = mnew;
+                    srun[h] = srun[h] * al + ps;
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < GMAX; h++) {
+            if (h < (int)G) {
+                float a = acc[h] * alpha[h];
+#pragma unroll
+                for (int u = 0; u < KT / KG; u++) a = fmaf(sc[h][kg + u * KG], vr[u], a);
+                acc[h] = a;
+            }
+        }
+        __syncthreads();
+    }
+
+    // Fold the key groups in a fixed order and write the triple.
+    if constexpr (KG > 1) {
+#pragma unroll
+        for (int h = 0; h < GMAX; h++)
+            if (h < (int)G) accx[(kg * GMAX + h) * HD + d] = acc[h];
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int h = 0; h < GMAX; h++) {
+                if (h < (int)G) {
+                    float a = accx[h * HD + d];
+                    for (int g2 = 1; g2 < KG; g2++) a += accx[(g2 * GMAX + h) * HD + d];
+                    acc[h] = a;
+                }
+            }
+        }
+    }
+    if (kg == 0) {
+#pragma unroll
+        for (int h = 0; h < GMAX; h++) {
+            if (h < (int)G) {
+                const size_t o = (size_t)(h0 + h) * ns + i;
+                acco[o * HD + d] = acc[h];
+                if (d == 0) {
+                    mo[o] = mrun[h];
+                    so[o] = srun[h];
+                }
+            }
+        }
+    }
+}
+
+extern "C" hipError_t sgk_attn_partial(const float *q, const uint16_t *kc, const uint16_t *vc,
+                                       float *m, float *sacc, float *acc, const sgk_step *step,
+                                       uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t seq,
+                                       uint32_t q_stride, float scale, uint32_t n_splits,
+                                       uint32_t max_splits, hipStream_t s) {
+    if (!n_kv || n_heads % n_kv || n_heads / n_kv > GMAX) return hipErrorInvalidValue;
+    const uint32_t gx = step ? max_splits : n_splits;
+    if (!gx) return hipSuccess;
+    dim3 grid(gx, n_kv);
+#define HDCASE(H) case H: hipLaunchKernelGGL(k_attn_partial<H>, grid, dim3(TPB), 0, s, q, kc, vc, m, sacc, acc, step, n_heads, n_kv, seq, q_stride, scale, n_splits); break
+    switch (hd) {
+        HDCASE(16); HDCASE(32); HDCASE(64); HDCASE(128); HDCASE(256);
+    default: return hipErrorInvalidValue;
+    }
+#undef HDCASE
+    return hipGetLastError();
+}
+
+// LSE combine (+ optional sigmoid gate). One workgroup per query head,
+// one output dim per thread. NaN/inf conventions of ref.c:265-373.
+__global__ void __launch_bounds__(TPB) k_attn_combine(const float *m, const float *sarr,
+                                                      const float *acc, float *out,
+                                                      const float *gate, uint32_t gstride,
+                                                      const sgk_step *step, uint32_t hd,
+                                                      uint32_t ns_arg) {
+    __shared__ float wts[SGK_MAX_SPLITS > 1024 ? SGK_MAX_SPLITS : 1024];
+    __shared__ float red[4];
+    __shared__ float bc;
+    const uint32_t ns = step ? dev_n_splits(step->pos + 1) : ns_arg;
+    const uint32_t h = blockIdx.x, t = threadIdx.x;
+    const float *mh = m + (size_t)h * ns, *sh = sarr + (size_t)h * ns;
+    float *oh = out + (size_t)h * hd;
+    // M: max over splits; a NaN first entry poisons the result (ref.c:288-300).
+    float mx = -INFINITY;
+    for (uint32_t k = t; k < ns; k += TPB) mx = fmaxf(mx, mh[k]);
+    mx = wave_max(mx);
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    if (t == 0) bc = (ns && isnan(mh[0])) ? mh[0] : fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    const float M = bc;
+    if (ns == 0 || M == -INFINITY || isnan(M)) {
+        const float fill = isnan(M) ? M : 0.0f;
+        for (uint32_t dd = t; dd < hd; dd += TPB) oh[dd] = fill;
+        return;
+    }
+    float sp = 0.0f;
+    for (uint32_t k = t; k < ns; k += TPB) {
+        const float mk = mh[k];
+        const float w = (mk == M) ? 1.0f : expf(mk - M);
+        wts[k] = w;
+        sp += sh[k] * w;
+    }
+    const float S = block_sum(sp, red);   // includes the barrier that publishes wts
+    for (uint32_t dd = t; dd < hd; dd += TPB) {
+        float o;
+        if (isnan(S)) {
+            o = S;
+        } else {
+            float num = 0.0f;
+            for (uint32_t k = 0; k < ns; k++) num = fmaf(acc[((size_t)h * ns + k) * hd + dd], wts[k], num);
+            o = S > 0.0f ? num / S : 0.0f;
+        }
+        if (gate) o *= sigm(gate[(size_t)h * gstride + dd]);
+        oh[dd] = o;
+    }
+}
+
+extern "C" hipError_t sgk_attn_combine(const float *m, const float *sacc, const float *acc,
+                                       float *out, const float *gate, uint32_t gstride,
+                                       const sgk_step *step, uint32_t n_heads, uint32_t hd,
+                                       uint32_t n_splits, uint32_t max_splits, hipStream_t s) {
+    (void)max_splits;
+    if (!n_heads) return hipSuccess;
+    if (!step && n_splits > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attn_combine, dim3(n_heads), dim3(TPB), 0, s, m, sacc, acc, out, gate,
+                       gstride, step, hd, n_splits);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Gated DeltaNet.
+// ---------------------------------------------------------------------------
+
+#define GDN_ROWS 16   // value rows per workgroup (4 per wave)
+
+// One delta-rule row update held across a wave: element i of the row lives
+// in lane i / EPL, slot i % EPL (EPL = DK / 64, or 1 lane per element when
+// DK < 64). Returns y_j (the readout after the write); S row updated in place.
+template <int DK>
+__device__ __forceinline__ float delta_row(float *row, const float *kk, const float *qq,
+                                           float vj, float beta, float decay, uint32_t lane) {
+    constexpr int EPL = DK >= 64 ? DK / 64 : 1;
+    float s[EPL], k[EPL], q[EPL];
+    const bool on = DK >= 64 || lane < (uint32_t)DK;
+#pragma unroll
+    for (int e = 0; e < EPL; e++) {
+        const uint32_t i = lane * EPL + e;
+        s[e] = on ? row[i] : 0.0f;
+        k[e] = on ? kk[i] : 0.0f;
+        q[e] = on ? qq[i] : 0.0f;
+    }
+    float kv = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; e++) { s[e] *= decay; kv = fmaf(s[e], k[e], kv); }
+    kv = wave_sum(kv);
+    const float delta = (vj - kv) * beta;
+    float y = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; e++) { s[e] = fmaf(k[e], delta, s[e]); y = fmaf(s[e], q[e], y); }
+    y = wave_sum(y);
+    if (on) {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) row[lane * EPL + e] = s[e];
+    }
+    return y;
+}
+
+template <int DK>
+__global__ void __launch_bounds__(TPB) k_gdn_step(sgk_gdn a) {
+    __shared__ float qk[2 * DK];
+    __shared__ float vv[GDN_ROWS];
+    __shared__ float red[4];
+    const uint32_t h = blockIdx.x, j0 = blockIdx.y * GDN_ROWS, t = threadIdx.x;
+    const uint32_t lane = t & 63, wave = t >> 6;
+    const uint32_t dk = DK, dv = a.dv, key_dim = a.n_k * dk, cd = a.conv_dim;
+    const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k);
+    const uint32_t pos = a.step->pos, keep = a.ksize - 1;
+    // This workgroup writes the ring slot of the q/k channels only when it is
+    // the first value head mapped to hk, row block 0 (one writer per channel).
+    const bool qk_writer = blockIdx.y == 0 && (a.tiled ? h < a.n_k : (h % (a.n_v / a.n_k)) == 0);
+    const uint32_t nrows = min((uint32_t)GDN_ROWS, dv - j0);
+
+    // 1. causal conv + SiLU on the channels this workgroup needs.
+    for (uint32_t e = t; e < 2 * dk + nrows; e += TPB) {
+        uint32_t ch;
+        if (e < dk) ch = hk * dk + e;
+        else if (e < 2 * dk) ch = key_dim + hk * dk + (e - dk);
+        else ch = 2 * key_dim + h * dv + j0 + (e - 2 * dk);
+        const float x = a.in[ch];
+        const float *w = a.conv_w + (size_t)ch * a.ksize;
+        float acc = 0.0f;
+        for (uint32_t jj = 0; jj < keep; jj++)
+            acc = fmaf(w[jj], a.ring[(size_t)((pos + 4 - keep + jj) & 3) * cd + ch], acc);
+        acc = fmaf(w[keep], x, acc);
+        const float o = silu(acc);
+        if (e < 2 * dk) qk[e] = o; else vv[e - 2 * dk] = o;
+        if (e >= 2 * dk || qk_writer) a.ring[(size_t)(pos & 3) * cd + ch] = x;
+    }
+    __syncthreads();
+    // 2. q, k: RMS (eps 1e-6, no weight), then q / dk and k / sqrt(dk).
+    float vq = 0.0f, vk = 0.0f;
+    for (uint32_t i = t; i < dk; i += TPB) { vq = fmaf(qk[i], qk[i], vq); vk = fmaf(qk[dk + i], qk[dk + i], vk); }
+    const float ssq = block_sum(vq, red);
+    const float ssk = block_sum(vk, red);
+    const float rq = 1.0f / sqrtf(ssq / (float)dk + 1e-6f), rk = 1.0f / sqrtf(ssk / (float)dk + 1e-6f);
+    const float qsc = 1.0f / (float)dk, ksc = 1.0f / sqrtf((float)dk);
+    __syncthreads();
+    for (uint32_t i = t; i < dk; i += TPB) {
+        qk[i] = (qk[i] * rq) * qsc;
+        qk[dk + i] = (qk[dk + i] * rk) * ksc;
+    }
+    __syncthreads();
+    // 3. gates (ref.c:127-170): beta = sigmoid(b); decay by the stored form.
+    const float *bb = a.in + cd + a.n_v * dv, *aa = bb + a.n_v;
+    const float beta = sigm(bb[h]);
+    const float sp = softplus(aa[h] + a.dt_bias[h]);
+    const float decay = a.neg_exp ? expf(a.ssm_a[h] * sp) : expf(-(expf(a.ssm_a[h]) * sp));
+    // 4. rank-1 update and readout, 4 rows per wave.
+    float *Sh = a.S + (size_t)h * dv * dk;
+    for (uint32_t r = wave; r < nrows; r += TPB / 64) {
+        const uint32_t j = j0 + r;
+        const float y = delta_row<DK>(Sh + (size_t)j * dk, qk + dk, qk, vv[r], beta, decay, lane);
+        if (lane == 0) a.y[(size_t)h * dv + j] = y;
+    }
+}
+
+extern "C" hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s) {
+    if (a->ksize < 1 || a->ksize > 4 || !a->n_k || a->n_v % a->n_k) return hipErrorInvalidValue;
+    dim3 grid(a->n_v, (a->dv + GDN_ROWS - 1) / GDN_ROWS);
+    switch (a->dk) {
+    case 32: hipLaunchKernelGGL(k_gdn_step<32>, grid, dim3(TPB), 0, s, *a); break;
+    case 64: hipLaunchKernelGGL(k_gdn_step<64>, grid, dim3(TPB), 0, s, *a); break;
+    case 128: hipLaunchKernelGGL(k_gdn_step<128>, grid, dim3(TPB), 0, s, *a); break;
+    case 256: hipLaunchKernelGGL(k_gdn_step<256>, grid, dim3(TPB), 0, s, *a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int DK>
+__global__ void __launch_bounds__(TPB) k_delta_multi(float *S, const float *qkv, float *out,
+                                                     const float *gates, uint32_t dv, uint32_t n_v,
+                                                     uint32_t n_k, uint32_t key_dim, int tiled) {
+    const uint32_t h = blockIdx.x, j0 = blockIdx.y * GDN_ROWS;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t hk = (n_k && n_v >= n_k) ? (tiled ? h % n_k : h / (n_v / n_k)) : 0;
+    const float *qq = qkv + (size_t)hk * DK, *kk = qkv + key_dim + (size_t)hk * DK;
+    const float *v = qkv + 2 * (size_t)key_dim + (size_t)h * dv;
+    const float beta = gates[h], decay = gates[n_v + h];
+    float *Sh = S + (size_t)h * dv * DK;
+    for (uint32_t r = wave; r < GDN_ROWS && j0 + r < dv; r += TPB / 64) {
+        const uint32_t j = j0 + r;
+        const float y = delta_row<DK>(Sh + (size_t)j * DK, kk, qq, v[j], beta, decay, lane);
+        if (lane == 0) out[(size_t)h * dv + j] = y;
+    }
+}
+
+extern "C" hipError_t sgk_delta_multi(float *S, const float *qkv, float *out, const float *gates,
+                                      uint32_t dk, uint32_t dv, uint32_t n_v, uint32_t n_k,
+                                      uint32_t key_dim, int tiled, hipStream_t s) {
+    dim3 grid(n_v, (dv + GDN_ROWS - 1) / GDN_ROWS);
+    if (!n_v || !dv) return hipSuccess;
+    switch (dk) {
+    case 32: hipLaunchKernelGGL(k_delta_multi<32>, grid, dim3(TPB), 0, s, S, qkv, out, gates, dv, n_v, n_k, key_dim, tiled); break;
+    case 64: hipLaunchKernelGGL(k_delta_multi<64>, grid, dim3(TPB), 0, s, S, qkv, out, gates, dv, n_v, n_k, key_dim, tiled); break;
+    case 128: hipLaunchKernelGGL(k_delta_multi<128>, grid, dim3(TPB), 0, s, S, qkv, out, gates, dv, n_v, n_k, key_dim, tiled); break;
+    case 256: hipLaunchKernelGGL(k_delta_multi<256>, grid, dim3(TPB), 0, s, S, qkv, out, gates, dv, n_v, n_k, key_dim, tiled); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Single-token causal conv: state oldest-first [ksize-1][channels] (ref.c:669-706).
+__global__ void k_conv1d_step(const float *x, const float *w, float *y, float *state,
+                              uint32_t channels, uint32_t ksize) {
+    const uint32_t c = blockIdx.x * TPB + threadIdx.x;
+    if (c >= channels) return;
+    const uint32_t keep = ksize - 1;
+    const float *wc = w + (size_t)c * ksize;
+    const float cur = x[c];
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < keep; j++) acc = fmaf(wc[j], state[(size_t)j * channels + c], acc);
+    acc = fmaf(wc[keep], cur, acc);
+    for (uint32_t j = 0; j + 1 < keep; j++) state[(size_t)j * channels + c] = state[(size_t)(j + 1) * channels + c];
+    if (keep) state[(size_t)(keep - 1) * channels + c] = cur;
+    y[c] = acc;
+}
+
+extern "C" hipError_t sgk_conv1d_step(const float *x, const float *w, float *y, float *state,
+                                      uint32_t channels, uint32_t ksize, hipStream_t s) {
+    if (!channels || !ksize) return hipSuccess;
+    hipLaunchKernelGGL(k_conv1d_step, dim3((channels + TPB - 1) / TPB), dim3(TPB), 0, s, x, w, y,
+                       state, channels, ksize);
+    return hipGetLastError();
+}
+
+__global__ void __launch_bounds__(TPB) k_rmsnorm_gated(const float *y, const float *z,
+                                                       const float *w, float *out, uint32_t dv,
+                                                       float eps) {
+    __shared__ float red[4];
+    const size_t o = (size_t)blockIdx.x * dv;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < dv; i += TPB) { float v = y[o + i]; ss = fmaf(v, v, ss); }
+    ss = block_sum(ss, red);
+    const float r = 1.0f / sqrtf(ss / (float)dv + eps);
+    for (uint32_t i = threadIdx.x; i < dv; i += TPB) out[o + i] = silu(z[o + i]) * ((y[o + i] * r) * w[i]);
+}
+
+extern "C" hipError_t sgk_rmsnorm_gated(const float *y, const float *z, const float *w,
+                                        float *out, uint32_t dv, uint32_t heads, float eps,
+                                        hipStream_t s) {
+    if (!heads || !dv) return hipSuccess;
+    hipLaunchKernelGGL(k_rmsnorm_gated, dim3(heads), dim3(TPB), 0, s, y, z, w, out, dv, eps);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Argmax (greedy.c:17-27): lowest index wins an exact tie. Two passes:
+// per-workgroup winners into scratch, then one workgroup folds them.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void better(float &bv, uint32_t &bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+__global__ void __launch_bounds__(TPB) k_argmax(const float *v, uint32_t n, uint32_t *scratch,
+                                                uint32_t *out, int final_pass) {
+    __shared__ float sv[TPB];
+    __shared__ uint32_t si[TPB];
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    if (!final_pass) {
+        for (uint32_t i = blockIdx.x * TPB + threadIdx.x; i < n; i += gridDim.x * TPB) better(bv, bi, v[i], i);
+    } else {
+        for (uint32_t k = threadIdx.x; k < n; k += TPB) {
+            const uint32_t i = scratch[k];
+            if (i != 0xFFFFFFFFu) better(bv, bi, v[i], i);
+        }
+    }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (uint32_t o = TPB / 2; o >= 1; o >>= 1) {
+        if (threadIdx.x < o) {
+            float b2 = sv[threadIdx.x];
+            uint32_t i2 = si[threadIdx.x];
+            better(b2, i2, sv[threadIdx.x + o], si[threadIdx.x + o]);
+            sv[threadIdx.x] = b2;
+            si[threadIdx.x] = i2;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        if (final_pass) *out = si[0] == 0xFFFFFFFFu ? 0u : si[0];
+        else scratch[blockIdx.x] = si[0];
+    }
+}
+
+extern "C" hipError_t sgk_argmax(const float *v, uint32_t n, uint32_t *out, uint32_t *scratch,
+                                 hipStream_t s) {
+    const uint32_t blocks = 256;
+    hipLaunchKernelGGL(k_argmax, dim3(blocks), dim3(TPB), 0, s, v, n, scratch, out, 0);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(TPB), 0, s, v, blocks, scratch, out, 1);
+    return hipGetLastError();
+}
+
+__global__ void k_step_advance(sgk_step *step, uint32_t *hist) {
+    const uint32_t pos = step->pos;
+    hist[pos + 1] = (uint32_t)step->token;
+    step->pos = pos + 1;
+}
+
+extern "C" hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream_t s) {
+    hipLaunchKernelGGL(k_step_advance, dim3(1), dim3(1), 0, s, step, hist);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Prefill GEMM Y[N][M] = X[N][K] * W[M][K]^T, W in the Q8 device layout.
+// Straightforward LDS-tiled version: 64x64 output tile, one Q8_0 block
+// (32 columns of K) per step, per-block scale applied to the block partial.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(TPB) k_gemm_q8_tiled(const float *X, const int8_t *qs,
+                                                       const uint16_t *d, float *Y, uint32_t N,
+                                                       uint32_t M, uint32_t K) {
+    __shared__ float xt[64][33];
+    __shared__ float wt[64][33];
+    const uint32_t n0 = blockIdx.y * 64, m0 = blockIdx.x * 64, t = threadIdx.x;
+    const uint32_t tn = t / 16, tm = t % 16;      // each thread: 4x4 outputs
+    float acc[4][4] = {};
+    const uint32_t nbl = K / 32;
+    for (uint32_t b = 0; b < nbl; b++) {
+        for (uint32_t e = t; e < 64 * 32; e += TPB) {
+            const uint32_t r = e / 32, c = e % 32;
+            xt[r][c] = (n0 + r < N) ? X[(size_t)(n0 + r) * K + b * 32 + c] : 0.0f;
+            wt[r][c] = (m0 + r < M) ? (float)qs[(size_t)(m0 + r) * K + b * 32 + c] : 0.0f;
+        }
+        __syncthreads();
+        float part[4][4] = {};
+        for (uint32_t c = 0; c < 32; c++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) part[i][j] = fmaf(xt[tn * 4 + i][c], wt[tm * 4 + j][c], part[i][j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t m = m0 + tm * 4 + j;
+            const float dd = (m < M) ? h2f(d[(size_t)m * nbl + b]) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i][j] = fmaf(dd, part[i][j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t n = n0 + tn * 4 + i, m = m0 + tm * 4 + j;
+            if (n < N && m < M) Y[(size_t)n * M + m] = acc[i][j];
+        }
+}
+
+extern "C" hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, float *Y,
+                                  uint32_t N, uint32_t M, uint32_t K, hipStream_t s) {
+    if (!N || !M || K % 32) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gemm_q8_tiled, dim3((M + 63) / 64, (N + 63) / 64), dim3(TPB), 0, s, X, qs, d, Y,
+                       N, M, K);
+    return hipGetLastError();
+}

@@ -1,0 +1,72 @@
+"""Writes the greedy-decode golden token sequences the GPU end-to-end tests
+compare against (run here, where the reference sources exist).
+
+Model: the seeded random-init qwen35 hybrid of the given shape from
+sg_synth_new (deterministic for a seed on any thread count). Prompt: n_prompt
+ids from numpy default_rng(seed).integers(0, vocab). The CPU reference then
+ingests the prompt one position at a time and greedily generates n_gen tokens
+(argmax, lowest index wins ties).
+
+  --lib ref     the reference's own src/ref.c (oracle/_ref, f32 K/V cache):
+                the sequence the GPU must reproduce;
+  --lib oracle  this repository's restatement, optionally with --kv-f16 (K/V
+                rounded through f16 as the GPU stores them), a diagnostic.
+
+Usage: python tests/golden/make_greedy.py --shape 2b --lib ref --out tests/golden/greedy_2b_ref.json
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+import oracle_lib as O  # noqa: E402
+import surge_amd as S   # noqa: E402
+
+SHAPES = {"2b": S.CFG_2B, "27b": S.CFG_27B}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--shape", default="2b")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--n-prompt", type=int, default=128)
+    ap.add_argument("--n-gen", type=int, default=64)
+    ap.add_argument("--lib", choices=["ref", "oracle"], default="ref")
+    ap.add_argument("--kv-f16", action="store_true")
+    ap.add_argument("--threads", type=int, default=8)
+    ap.add_argument("--out", required=True)
+    a = ap.parse_args()
+    cfg = SHAPES[a.shape]
+    syn = S.Synth(cfg, S.SG_T_Q8_0, seed=a.seed)
+    prompt = np.random.default_rng(a.seed).integers(0, cfg["vocab"], a.n_prompt).astype(int).tolist()
+    L = O.ref() if a.lib == "ref" else O.oracle()
+    if a.lib == "oracle":
+        L.sg_ref_set_threads(a.threads)
+    rm = O.RefModel(L, syn.model, a.n_prompt + a.n_gen + 1, kv_f16=a.kv_f16)
+    t0 = time.time()
+    for p, t in enumerate(prompt):
+        lg = rm.forward(t, p)
+    gen, margins = [], []
+    for i in range(a.n_gen):
+        nxt = int(np.argmax(lg))          # numpy argmax: first (lowest) index of the max
+        top2 = np.partition(lg, -2)[-2:]
+        margins.append(float(top2[1] - top2[0]))
+        gen.append(nxt)
+        lg = rm.forward(nxt, a.n_prompt + i)
+    out = dict(shape=a.shape, cfg=cfg, seed=a.seed, wtype="q8_0", prompt_ids=prompt, gen_ids=gen,
+               lib=("reference src/ref.c" if a.lib == "ref" else "oracle/ref.c"), kv_f16=a.kv_f16,
+               min_top2_margin=min(margins), seconds=round(time.time() - t0, 1))
+    with open(a.out, "w") as f:
+        json.dump(out, f, indent=1)
+    print(a.out, "gen:", gen[:16], "... min margin", min(margins), "in", out["seconds"], "s")
+
+
+if __name__ == "__main__":
+    main()

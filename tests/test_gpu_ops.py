@@ -1,0 +1,406 @@
+"""GPU per-op parity: each HIP kernel, called through the C ABI, against the
+CPU oracle on the same seeded inputs (the reference's own per-op strategy,
+reference tests/test_metal_ops.c:1-63).
+
+Bars (stated per test): integer/byte work bit-exact; fp32 outputs within
+1e-3 relative, measured both as the reference's scale-relative
+max|err|/max|want| and per element with an absolute floor of 1e-3*max|want|.
+The GPU accumulates in fp32 where the oracle uses double, so ~1e-6 is the
+expected error; 1e-3 is the acceptance bar.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import surge_amd as S
+from oracle_lib import fp
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = max(np.abs(want).max(), 1e-30)
+    return float(np.abs(got - want).max() / scale)
+
+
+def assert_close(got, want, tol=TOL):
+    e = rel_err(got, want)
+    assert e < tol, f"scale-relative error {e:.3e} >= {tol}"
+    floor = tol * max(np.abs(want).max(), 1e-30)
+    bad = np.abs(np.asarray(got, np.float64) - want) > tol * np.abs(want) + floor
+    assert not bad.any(), f"{bad.sum()} elements outside rel {tol} + floor"
+
+
+def q8_matrix(rng, rows, cols, sigma=0.02):
+    """BASELINE GEMV config: 32 int8 uniform in [-127,127] per block and
+    scale f16(|N(0, sigma)|/127) (about 30% subnormal at sigma 0.02)."""
+    nb = cols // 32
+    q = rng.integers(-127, 128, size=(rows, nb, 32), dtype=np.int8)
+    d = (np.abs(rng.standard_normal((rows, nb))) * sigma / 127).astype(np.float16)
+    raw = np.zeros((rows, nb, 34), np.uint8)
+    raw[:, :, :2] = d.view(np.uint8).reshape(rows, nb, 2)
+    raw[:, :, 2:] = q.view(np.uint8)
+    return raw.reshape(-1)
+
+
+def oracle_matvec_q8(raw, x, rows, cols):
+    y = np.zeros(rows, np.float32)
+    O.oracle().sg_ref_matvec_q8(raw.ctypes.data, fp(x), fp(y), rows, cols)
+    return y
+
+
+def gpu_matvec_q8(gpu, raw, x, rows, cols):
+    w, xb, y = gpu.buf(raw), gpu.buf(x), gpu.buf(np.zeros(rows, np.float32))
+    gpu.run_op("k_matvec_q8", w, xb, y, [rows, cols])
+    out = y.array.copy()
+    for b in (w, xb, y):
+        b.free()
+    return out
+
+
+# ---------------------------------------------------------------- GEMV
+
+def test_gemv_q8_scale_decode_exact_all_f16_patterns(gpu):
+    """Row r has one block with scale bits r, q = (1, 0, ...), x = e_0: y[r]
+    must be exactly the f16 value, subnormals included."""
+    rows, cols = 65536, 32
+    raw = np.zeros((rows, 34), np.uint8)
+    raw[:, :2] = np.arange(rows, dtype=np.uint16).view(np.uint8).reshape(rows, 2)
+    raw[:, 2] = 1
+    x = np.zeros(cols, np.float32)
+    x[0] = 1
+    got = gpu_matvec_q8(gpu, raw.reshape(-1), x, rows, cols)
+    want = np.arange(rows, dtype=np.uint16).view(np.float16).astype(np.float32)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin], want[fin])
+    assert np.isnan(got[np.isnan(want)]).all()
+
+
+def test_gemv_q8_baseline_config_4096(gpu):
+    rng = np.random.default_rng(0)
+    rows = cols = 4096
+    raw = q8_matrix(rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = gpu_matvec_q8(gpu, raw, x, rows, cols)
+    want = oracle_matvec_q8(raw, x, rows, cols)
+    assert_close(got, want)
+    assert rel_err(got, want) < 1e-5          # fp32 accumulation, expect ~1e-7
+    again = gpu_matvec_q8(gpu, raw, x, rows, cols)
+    assert np.array_equal(got, again)          # bit-identical reruns
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (37, 64), (3, 17408), (5120, 6144),
+                                       (16480, 5120), (40000, 2048), (7, 96)])
+def test_gemv_q8_shapes(gpu, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    raw = q8_matrix(rng, rows, cols, sigma=1.0)
+    x = rng.standard_normal(cols).astype(np.float32)
+    assert_close(gpu_matvec_q8(gpu, raw, x, rows, cols), oracle_matvec_q8(raw, x, rows, cols))
+
+
+def test_gemv_f32(gpu):
+    rng = np.random.default_rng(3)
+    rows, cols = 50, 24
+    w = rng.standard_normal(rows * cols).astype(np.float32)
+    x = rng.standard_normal(cols).astype(np.float32)
+    want = np.zeros(rows, np.float32)
+    O.oracle().sg_ref_matvec_f32(fp(w), fp(x), fp(want), rows, cols)
+    wb, xb, yb = gpu.buf(w), gpu.buf(x), gpu.buf(np.zeros(rows, np.float32))
+    gpu.run_op("k_matvec_f32", wb, xb, yb, [rows, cols])
+    assert_close(yb.array, want)
+
+
+def test_gemv_rejects_bad_shapes(gpu):
+    w, x, y = gpu.buf(np.zeros(34, np.uint8)), gpu.buf(np.zeros(48, np.float32)), gpu.buf(np.zeros(1, np.float32))
+    with pytest.raises(S.SurgeError):
+        gpu.run_op("k_matvec_q8", w, x, y, [1, 48])     # cols % 32
+    with pytest.raises(S.SurgeError):
+        gpu.run_op("k_matvec_q8", w, x, y, [2, 32])     # w too small
+    with pytest.raises(S.SurgeError):
+        gpu.run_op("k_matvec_q8", w, x, w, [1, 32])     # out aliases input
+
+
+# ---------------------------------------------------------------- attention
+
+def f16(rng, n):
+    return rng.standard_normal(n).astype(np.float16)
+
+
+def run_partial_combine(gpu, q, k16, v16, nh, nkv, hd, seq, qs, ns):
+    sc = 1.0 / np.sqrt(hd)
+    p = [nh, nkv, hd, seq, qs, S.fbits(sc), ns]
+    qb, kb, vb = gpu.buf(q), gpu.buf(k16.view(np.uint16) if seq else np.zeros(1, np.uint16)), \
+        gpu.buf(v16.view(np.uint16) if seq else np.zeros(1, np.uint16))
+    mb, sb = gpu.buf(np.zeros(nh * ns, np.float32)), gpu.buf(np.zeros(nh * ns, np.float32))
+    ab, ob = gpu.buf(np.zeros(nh * ns * hd, np.float32)), gpu.buf(np.zeros(nh * hd, np.float32))
+    gpu.attn_partial(qb, kb, vb, mb, sb, ab, p)
+    gpu.attn_combine(mb, sb, ab, ob, p)
+    res = (mb.array.copy(), sb.array.copy(), ab.array.copy(), ob.array.copy())
+    for b in (qb, kb, vb, mb, sb, ab, ob):
+        b.free()
+    return res
+
+
+def oracle_attn(q, k16, v16, nh, nkv, hd, seq, qs, ns):
+    kc = k16.astype(np.float32) if seq else np.zeros(1, np.float32)
+    vc = v16.astype(np.float32) if seq else np.zeros(1, np.float32)
+    sc = np.float32(1.0 / np.sqrt(hd))
+    m, s = np.zeros(nh * ns, np.float32), np.zeros(nh * ns, np.float32)
+    acc = np.zeros(nh * ns * hd, np.float32)
+    O.oracle().sg_ref_attn_partials(fp(q), fp(kc), fp(vc), nh, nkv, hd, seq, qs, sc, ns, fp(m), fp(s), fp(acc))
+    out = np.zeros(nh * hd, np.float32)
+    O.oracle().sg_ref_attn_decode_splitk(fp(q), fp(kc), fp(vc), nh, nkv, hd, seq, qs, sc, ns, fp(out))
+    return m, s, acc, out
+
+
+@pytest.mark.parametrize("seq,ns", [(512, 8), (512, 16), (4096, 32), (4096, 64), (32768, 64)])
+def test_splitk_gqa_baseline_config(gpu, seq, ns):
+    """BASELINE attention config: 16 q / 4 kv heads, head_dim 256, f16 KV
+    N(0,1), q N(0,1), scale 1/16, then the LSE combine."""
+    rng = np.random.default_rng(seq + ns)
+    nh, nkv, hd = 16, 4, 256
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k16, v16 = f16(rng, seq * nkv * hd), f16(rng, seq * nkv * hd)
+    gm, gs, gacc, gout = run_partial_combine(gpu, q, k16, v16, nh, nkv, hd, seq, hd, ns)
+    om, os_, oacc, oout = oracle_attn(q, k16, v16, nh, nkv, hd, seq, hd, ns)
+    assert np.abs(gm - om).max() <= 1e-5 * np.abs(om).max()
+    assert_close(gs, os_)
+    assert_close(gacc, oacc)
+    assert_close(gout, oout)
+    assert rel_err(gout, oout) < 1e-5
+
+
+@pytest.mark.parametrize("nh,nkv,hd,seq,ns", [(4, 4, 64, 100, 3), (8, 1, 128, 77, 5), (6, 2, 32, 40, 64),
+                                              (2, 2, 16, 1, 1), (24, 4, 256, 1000, 31), (4, 2, 128, 0, 4)])
+def test_splitk_shapes_and_edges(gpu, nh, nkv, hd, seq, ns):
+    """Per-head (G=1), wide groups, tiny head dims, more splits than keys
+    (empty splits), seq 0, and a gated q_stride whose gate half is NaN."""
+    rng = np.random.default_rng(nh * 1000 + seq)
+    qs = 2 * hd
+    q = rng.standard_normal(nh * qs).astype(np.float32).reshape(nh, qs)
+    q[:, hd:] = np.nan                      # the gate half must never be read
+    q = np.ascontiguousarray(q.reshape(-1))
+    k16, v16 = f16(rng, seq * nkv * hd), f16(rng, seq * nkv * hd)
+    gm, gs, gacc, gout = run_partial_combine(gpu, q, k16, v16, nh, nkv, hd, seq, qs, ns)
+    om, os_, oacc, oout = oracle_attn(q, k16, v16, nh, nkv, hd, seq, qs, ns)
+    assert np.isfinite(gout).all()
+    assert np.array_equal(np.isneginf(gm), np.isneginf(om))   # same empty splits
+    fin = np.isfinite(om)
+    if fin.any():
+        assert np.abs(gm[fin] - om[fin]).max() <= 1e-5 * max(np.abs(om[fin]).max(), 1)
+    if seq:
+        assert_close(gout, oout)
+    else:
+        assert (gout == 0).all()
+
+
+def test_attn_decode_f16_single_call(gpu):
+    rng = np.random.default_rng(11)
+    nh, nkv, hd, seq = 16, 4, 256, 700
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k16, v16 = f16(rng, seq * nkv * hd), f16(rng, seq * nkv * hd)
+    qb, kb, vb = gpu.buf(q), gpu.buf(k16.view(np.uint16)), gpu.buf(v16.view(np.uint16))
+    ob = gpu.buf(np.zeros(nh * hd, np.float32))
+    gpu.attn_decode_f16(qb, kb, vb, ob, [nh, nkv, hd, seq, hd, S.fbits(1 / 16)])
+    want = np.zeros(nh * hd, np.float32)
+    kc, vc = k16.astype(np.float32), v16.astype(np.float32)
+    O.oracle().sg_ref_attn_decode(fp(q), fp(kc), fp(vc), nh, nkv, hd, seq, hd, np.float32(1 / 16), fp(want))
+    assert_close(ob.array, want)
+
+
+def test_combine_degenerate_cases(gpu):
+    hd, ns, nh = 32, 3, 4
+    rng = np.random.default_rng(1)
+    acc = rng.standard_normal(nh * ns * hd).astype(np.float32)
+    m = np.float32([[1.5, -np.inf, 0.5], [-np.inf] * 3, [np.nan, 1, 2], [np.inf, 3, np.inf]]).reshape(-1)
+    s = np.float32([[2, 0, 3], [0, 0, 0], [1, 1, 1], [2, 1, 4]]).reshape(-1)
+    mb, sb, ab = gpu.buf(m), gpu.buf(s), gpu.buf(acc)
+    ob = gpu.buf(np.full(nh * hd, 7, np.float32))
+    gpu.attn_combine(mb, sb, ab, ob, [nh, 1, hd, 0, hd, 0, ns])
+    want = np.zeros(nh * hd, np.float32)
+    for h in range(nh):
+        O.oracle().sg_ref_attn_combine(fp(m[h * ns:(h + 1) * ns].copy()), fp(s[h * ns:(h + 1) * ns].copy()),
+                                       fp(acc[h * ns * hd:(h + 1) * ns * hd].copy()), ns, hd,
+                                       fp(want[h * hd:(h + 1) * hd]))
+    got = ob.array.reshape(nh, hd)
+    want = want.reshape(nh, hd)
+    assert_close(got[0], want[0])
+    assert (got[1] == 0).all()                       # all splits empty
+    assert np.isnan(got[2]).all()                    # NaN first max propagates
+    assert_close(got[3], want[3])                    # +inf ties combine among themselves
+
+
+# ---------------------------------------------------------------- DeltaNet
+
+def test_delta_multi_baseline_config(gpu):
+    """BASELINE DeltaNet config: 16 heads, dk = dv = 128, S N(0, 0.1), q, k
+    L2-normalised, v N(0,1), beta = sigmoid(N), decay = exp(-softplus(N)).
+    Two consecutive steps thread S."""
+    rng = np.random.default_rng(4)
+    nv = nk = 16
+    dk = dv = 128
+    kd = nk * dk
+    S0 = (rng.standard_normal(nv * dv * dk) * 0.1).astype(np.float32)
+    Sg = gpu.buf(S0.copy())
+    So = S0.copy()
+    for step in range(2):
+        q = rng.standard_normal((nk, dk))
+        k = rng.standard_normal((nk, dk))
+        q = (q / np.linalg.norm(q, axis=1, keepdims=True)).astype(np.float32)
+        k = (k / np.linalg.norm(k, axis=1, keepdims=True)).astype(np.float32)
+        v = rng.standard_normal(nv * dv).astype(np.float32)
+        qkv = np.concatenate([q.reshape(-1), k.reshape(-1), v]).astype(np.float32)
+        beta = np.array([O.oracle().sg_ref_sigmoid(float(b)) for b in rng.standard_normal(nv)], np.float32)
+        decay = np.array([O.oracle().sg_ref_delta_decay_neg_a(-1.0, float(a), 0.0) for a in rng.standard_normal(nv)],
+                         np.float32)
+        qb, ob, gb = gpu.buf(qkv), gpu.buf(np.zeros(nv * dv, np.float32)), gpu.buf(np.concatenate([beta, decay]))
+        gpu.delta_multi(Sg, qb, ob, gb, [dk, dv, nv, nk, kd, 1])
+        want = np.zeros(nv * dv, np.float32)
+        for h in range(nv):
+            hk = h % nk
+            O.oracle().sg_ref_delta_step(fp(So[h * dv * dk:]), fp(np.ascontiguousarray(q[hk])),
+                                         fp(np.ascontiguousarray(k[hk])), fp(np.ascontiguousarray(v[h * dv:(h + 1) * dv])),
+                                         float(beta[h]), float(decay[h]), fp(want[h * dv:]), dk, dv)
+        assert_close(ob.array, want)
+        assert_close(Sg.array, So)
+        for b in (qb, ob, gb):
+            b.free()
+
+
+def test_delta_multi_tiled_group_map(gpu):
+    """48 value heads over 16 key heads (the 27B shape): tiled h % n_k."""
+    rng = np.random.default_rng(9)
+    nv, nk, dk, dv = 48, 16, 128, 128
+    kd = nk * dk
+    S0 = (rng.standard_normal(nv * dv * dk) * 0.1).astype(np.float32)
+    qkv = rng.standard_normal(2 * kd + nv * dv).astype(np.float32) * 0.1
+    gates = np.concatenate([rng.uniform(0, 1, nv), rng.uniform(0.5, 1, nv)]).astype(np.float32)
+    Sg, qb, ob, gb = gpu.buf(S0.copy()), gpu.buf(qkv), gpu.buf(np.zeros(nv * dv, np.float32)), gpu.buf(gates)
+    gpu.delta_multi(Sg, qb, ob, gb, [dk, dv, nv, nk, kd, 1])
+    So, want = S0.copy(), np.zeros(nv * dv, np.float32)
+    for h in range(nv):
+        hk = h % nk
+        O.oracle().sg_ref_delta_step(fp(So[h * dv * dk:]), fp(qkv[hk * dk:]), fp(qkv[kd + hk * dk:]),
+                                     fp(qkv[2 * kd + h * dv:]), float(gates[h]), float(gates[nv + h]),
+                                     fp(want[h * dv:]), dk, dv)
+    assert_close(ob.array, want)
+    assert_close(Sg.array, So)
+
+
+def test_conv1d_step_baseline_config(gpu):
+    """Causal conv width 4 over 2048 channels with rolling state, 3 steps."""
+    rng = np.random.default_rng(6)
+    ch, ks = 2048, 4
+    w = rng.standard_normal(ch * ks).astype(np.float32)
+    st_o = np.zeros((ks - 1) * ch, np.float32)
+    ob = gpu.buf(np.zeros(ch * ks, np.float32))    # y[ch] | state[(ks-1)*ch]
+    wb = gpu.buf(w)
+    for _ in range(3):
+        x = rng.standard_normal(ch).astype(np.float32)
+        xb = gpu.buf(x)
+        gpu.run_op("k_conv1d_step", xb, wb, ob, [ch, ks])
+        xo = x.copy()
+        O.oracle().sg_ref_conv1d_causal(fp(xo), fp(w), fp(st_o), fp(st_o), ch, ks)
+        assert_close(ob.array[:ch], xo)
+        assert np.array_equal(ob.array[ch:], st_o)   # the state shift is exact
+        xb.free()
+
+
+# ---------------------------------------------------------------- small ops
+
+def test_small_ops(gpu):
+    rng = np.random.default_rng(8)
+    n = 5000
+    x = (rng.standard_normal(n) * 4).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    o = O.oracle()
+
+    def run(kernel, a, b, p):
+        ab, bb, ob = gpu.buf(a), gpu.buf(b) if b is not None else None, gpu.buf(np.zeros(len(a), np.float32))
+        gpu.run_op(kernel, ab, bb, ob, p)
+        return ob.array.copy()
+
+    want = x.copy(); o.sg_ref_rmsnorm(fp(want), fp(w), n, 1e-6)
+    assert_close(run("k_rmsnorm", x, w, [n, S.fbits(1e-6), 1]), want)
+    want = x.copy(); o.sg_ref_swiglu(fp(want), fp(w), n)
+    assert_close(run("k_swiglu", x, w, [n]), want)
+    want = x.copy(); o.sg_ref_silu(fp(want), n)
+    assert_close(run("k_silu", x, None, [n]), want)
+    want = x.copy(); o.sg_ref_gate_sigmoid(fp(want), fp(w), n)
+    assert_close(run("k_gate_sigmoid", x, w, [n]), want)
+    assert np.array_equal(run("k_add", x, w, [n]), x + w)
+    assert np.array_equal(run("k_scale", x, None, [n, S.fbits(0.25)]), x * np.float32(0.25))
+    xs = np.concatenate([x[:100], np.float32([-1e30] * 5)])
+    want = xs.copy(); o.sg_ref_softmax(fp(want), len(xs))
+    assert_close(run("k_softmax", xs, None, [len(xs)]), want)
+
+
+def test_rope_heads_and_rmsnorm_heads(gpu):
+    rng = np.random.default_rng(12)
+    hd, rd, nh, stride, pos, theta = 256, 64, 6, 512, 4095, 1e7
+    x = rng.standard_normal(nh * stride).astype(np.float32)
+    half = rd // 2
+    inv = theta ** (-2.0 * np.arange(half) / rd)
+    cs = np.concatenate([np.cos(pos * inv), np.sin(pos * inv)]).astype(np.float32)
+    xb, cb, ob = gpu.buf(x), gpu.buf(cs), gpu.buf(np.zeros(nh * stride, np.float32))
+    gpu.run_op("k_rope_heads", xb, cb, ob, [hd, rd, nh, stride])
+    want = x.copy()
+    for h in range(nh):
+        seg = np.ascontiguousarray(want[h * stride:h * stride + hd])
+        O.oracle().sg_ref_rope_partial(fp(seg), hd, rd, pos, theta)
+        want[h * stride:h * stride + hd] = seg
+    got = ob.array.reshape(nh, stride)[:, :hd]
+    assert_close(got, want.reshape(nh, stride)[:, :hd], 1e-5)
+    assert np.array_equal(got[:, rd:], x.reshape(nh, stride)[:, rd:hd])
+    wn = rng.standard_normal(hd).astype(np.float32)
+    ob2 = gpu.buf(np.zeros(nh * stride, np.float32))
+    gpu.run_op("k_rmsnorm_heads", xb, gpu.buf(wn), ob2, [hd, nh, S.fbits(1e-6), stride, 1])
+    want = x.copy()
+    for h in range(nh):
+        seg = np.ascontiguousarray(want[h * stride:h * stride + hd])
+        O.oracle().sg_ref_rmsnorm(fp(seg), fp(wn), hd, 1e-6)
+        assert_close(ob2.array[h * stride:h * stride + hd], seg)
+
+
+def test_rmsnorm_gated(gpu):
+    rng = np.random.default_rng(13)
+    dv, nh = 128, 48
+    y = rng.standard_normal(dv * nh).astype(np.float32)
+    z = rng.standard_normal(dv * nh).astype(np.float32)
+    w = rng.standard_normal(dv).astype(np.float32)
+    yb, zb, ob = gpu.buf(y), gpu.buf(np.concatenate([z, w])), gpu.buf(np.zeros(dv * nh, np.float32))
+    gpu.run_op("k_rmsnorm_gated", yb, zb, ob, [dv, nh, S.fbits(1e-6)])
+    want = np.zeros(dv * nh, np.float32)
+    for h in range(nh):
+        yy = y[h * dv:(h + 1) * dv].copy()
+        zz = z[h * dv:(h + 1) * dv].copy()
+        O.oracle().sg_ref_rmsnorm(fp(yy), fp(w), dv, 1e-6)
+        O.oracle().sg_ref_swiglu(fp(zz), fp(yy), dv)
+        want[h * dv:(h + 1) * dv] = zz
+    assert_close(ob.array, want)
+
+
+def test_kv_store_f16_bit_exact(gpu):
+    rng = np.random.default_rng(14)
+    x = np.concatenate([rng.standard_normal(10000).astype(np.float32) * 10.0 ** rng.integers(-8, 5, 10000),
+                        np.float32([65504, 65519, 65520, 1e9, -1e9, 2 ** -25, 2 ** -24, 3e-5, 0, -0.0])])
+    x = x.astype(np.float32)
+    xb, ob = gpu.buf(x), gpu.buf(np.zeros(len(x) + 8, np.uint16))
+    gpu.run_op("k_kv_store_f16", xb, None, ob, [len(x), 8])
+    want = np.array([O.oracle().sg_ref_f32_to_f16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(ob.array[8:], want)
+    assert (ob.array[:8] == 0).all()
+
+
+def test_matmul_q8_prefill_gemm(gpu):
+    rng = np.random.default_rng(15)
+    N, M, K = 70, 130, 256
+    X = rng.standard_normal(N * K).astype(np.float32)
+    raw = q8_matrix(rng, M, K, sigma=1.0)
+    xb, wb, yb = gpu.buf(X), gpu.buf(raw), gpu.buf(np.zeros(N * M, np.float32))
+    gpu.run_op("k_matmul_q8", xb, wb, yb, [N, M, K])
+    want = np.stack([oracle_matvec_q8(raw, np.ascontiguousarray(X[n * K:(n + 1) * K]), M, K) for n in range(N)])
+    assert_close(yb.array.reshape(N, M), want)
