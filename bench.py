@@ -4,7 +4,7 @@ Workload (BASELINE.json metric and configs[4]): random-init 27B-shaped qwen35
 hybrid, Q8_0 weights (hidden 5120, 64 layers, 3 DeltaNet : 1 attention,
 attention 24q/4kv x 256, DeltaNet 48 v-heads / 16 k-heads x 128, FFN 17408,
 vocab 151936). The context is filled with 4096 random token ids through
-sg_gpu_prefill; then W untimed and K timed greedy decode steps run
+sg_gpu_prefill (512-token chunks, MFMA GEMMs); then W untimed and K timed greedy decode steps run
 device-resident (sg_gpu_decode_greedy: one captured HIP graph per token, the
 argmax feeds the next step on the device). One step = one token at batch 1.
 
@@ -176,6 +176,7 @@ def main():
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--shape", default="27b", choices=["27b", "2b"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--chunk", type=int, default=512, help="prefill chunk (tokens)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {a.gpus}); this build has no "
@@ -193,8 +194,10 @@ def main():
     gpu.state_new(a.ctx + a.warmup + a.steps + 8)
     prompt = np.random.default_rng(0).integers(0, cfg["vocab"], a.ctx).astype(np.int32)
     t = time.time()
-    lg = gpu.prefill(prompt)
-    log(f"prefilled {a.ctx} tokens in {time.time() - t:.1f} s")
+    lg = gpu.prefill(prompt, chunk=a.chunk)
+    gpu.sync()
+    pf_s = time.time() - t
+    log(f"prefilled {a.ctx} context tokens in {pf_s:.2f} s ({a.ctx / pf_s:.0f} tok/s, chunk {a.chunk})")
     tok = int(np.argmax(lg))
     pos = a.ctx
     if a.warmup:
@@ -226,6 +229,8 @@ def main():
                    "ctx": a.ctx, "batch": 1, "model_bytes": syn_bytes_hint(cfg)},
         "decode_hbm": {"bytes_per_token": int(bytes_tok), "parts": parts,
                        "achieved_GBs": round(decode_gbs, 1), "frac": round(decode_gbs / HBM_PEAK_GBS, 4)},
+        "prefill": {"tokens": a.ctx, "chunk": a.chunk, "seconds": round(pf_s, 3),
+                    "tok_per_s": round(a.ctx / pf_s, 1)},
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -99,13 +99,19 @@ struct sg_gpu {
     bool have_state;
     uint32_t max_ctx, used, max_splits;
     float *cs_table;
-    float *x, *act, *ctx, *ybuf, *ffg, *logits, *am, *as, *aacc;
+    float *x, *act, *ctx, *ybuf, *gbuf, *ffg, *logits, *am, *as, *aacc;
     uint32_t *amax_scratch, *hist;
     sgk_step *d_step, *h_step;
     float *h_logits;
     uint32_t *h_tok;
     hipGraphExec_t g_fwd, g_greedy;
     bool use_graph;
+
+    /* prefill chunk scratch */
+    uint32_t pf_chunk;
+    uint64_t pf_segments;
+    sgk_step *pf_steps, *pf_hsteps;
+    float *pf_X, *pf_Xn, *pf_IN, *pf_CONV, *pf_Y, *pf_G, *pf_CTX, *pf_FF, *pf_m, *pf_s, *pf_acc;
 
     /* one-shot scratch */
     void *tmp;
@@ -500,8 +506,11 @@ sg_err sg_gpu_run_attn_splitk_partial_gqa(sg_gpu *g, void *q, void *k, void *v, 
     void *ins[3] = {q, k, v};
     if (sg_failed(e = push(ins, 3))) return e;
     g->splitk_gqa_dispatches++;
-    return finish(g, sgk_attn_partial(DEV(q), DEV(k), DEV(v), DEV(m), DEV(s), DEV(acc), NULL, nh, nkv, hd,
-                                      seq, qs, fbits(p[5]), ns, ns, g->stream), outs, 3);
+    sgk_attn A = {0};
+    A.q = DEV(q); A.kc = DEV(k); A.vc = DEV(v); A.m = DEV(m); A.s = DEV(s); A.acc = DEV(acc);
+    A.n_heads = nh; A.n_kv = nkv; A.hd = hd; A.q_stride = qs; A.seq = seq; A.n_splits = ns; A.max_splits = ns;
+    A.ntok = 1; A.scale = fbits(p[5]);
+    return finish(g, sgk_attn_partial(&A, g->stream), outs, 3);
 }
 
 sg_err sg_gpu_run_attn_splitk_partial(sg_gpu *g, void *q, void *k, void *v, void *m, void *s,
@@ -523,8 +532,10 @@ sg_err sg_gpu_run_attn_splitk_combine(sg_gpu *g, void *m, void *s, void *acc, vo
     if (overlap(out, m) || overlap(out, s) || overlap(out, acc)) return (sg_err){"gpu: combine output overlaps an input"};
     void *ins[3] = {m, s, acc}, *outs[1] = {out};
     if (sg_failed(e = push(ins, 3))) return e;
-    return finish(g, sgk_attn_combine(DEV(m), DEV(s), DEV(acc), DEV(out), NULL, 0, NULL, nh, hd, ns, ns, g->stream),
-                  outs, 1);
+    sgk_attn A = {0};
+    A.m = DEV(m); A.s = DEV(s); A.acc = DEV(acc); A.out = DEV(out);
+    A.n_heads = nh; A.hd = hd; A.n_splits = ns; A.max_splits = ns; A.ntok = 1;
+    return finish(g, sgk_attn_combine(&A, g->stream), outs, 1);
 }
 
 sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out,
@@ -547,8 +558,12 @@ sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *ou
     float *mm = t, *ss = mm + (uint64_t)nh * ns, *aa = ss + (uint64_t)nh * ns;
     void *ins[3] = {q, k, v}, *outs[1] = {out};
     if (sg_failed(e = push(ins, 3))) return e;
-    hipError_t he = sgk_attn_partial(DEV(q), DEV(k), DEV(v), mm, ss, aa, NULL, nh, nkv, hd, seq, qs, fbits(pp[5]), ns, ns, g->stream);
-    if (he == hipSuccess) he = sgk_attn_combine(mm, ss, aa, DEV(out), NULL, 0, NULL, nh, hd, ns, ns, g->stream);
+    sgk_attn A = {0};
+    A.q = DEV(q); A.kc = DEV(k); A.vc = DEV(v); A.m = mm; A.s = ss; A.acc = aa; A.out = DEV(out);
+    A.n_heads = nh; A.n_kv = nkv; A.hd = hd; A.q_stride = qs; A.seq = seq; A.n_splits = ns; A.max_splits = ns;
+    A.ntok = 1; A.scale = fbits(pp[5]);
+    hipError_t he = sgk_attn_partial(&A, g->stream);
+    if (he == hipSuccess) he = sgk_attn_combine(&A, g->stream);
     return finish(g, he, outs, 1);
 }
 
@@ -764,6 +779,15 @@ static void state_free(sg_gpu *g) {
     if (g->h_step) hipHostFree(g->h_step);
     if (g->h_logits) hipHostFree(g->h_logits);
     if (g->h_tok) hipHostFree(g->h_tok);
+    if (g->pf_hsteps) hipHostFree(g->pf_hsteps);
+    g->pf_hsteps = NULL;
+    {
+        void **pb[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
+                        (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
+                        (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc };
+        for (size_t i = 0; i < sizeof pb / sizeof *pb; i++) { dfree(g, *pb[i]); *pb[i] = NULL; }
+        g->pf_chunk = 0;
+    }
     g->h_step = NULL;
     g->h_logits = NULL;
     g->h_tok = NULL;
@@ -772,10 +796,10 @@ static void state_free(sg_gpu *g) {
         dfree(g, L->kc); dfree(g, L->vc); dfree(g, L->ring); dfree(g, L->S);
         L->kc = L->vc = NULL; L->ring = L->S = NULL;
     }
-    void *bufs[] = { g->cs_table, g->x, g->act, g->ctx, g->ybuf, g->ffg, g->logits, g->am, g->as,
+    void *bufs[] = { g->cs_table, g->x, g->act, g->ctx, g->ybuf, g->gbuf, g->ffg, g->logits, g->am, g->as,
                      g->aacc, g->amax_scratch, g->hist, g->d_step };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) dfree(g, bufs[i]);
-    g->cs_table = g->x = g->act = g->ctx = g->ybuf = g->ffg = g->logits = g->am = g->as = g->aacc = NULL;
+    g->cs_table = g->x = g->act = g->ctx = g->ybuf = g->gbuf = g->ffg = g->logits = g->am = g->as = g->aacc = NULL;
     g->amax_scratch = g->hist = NULL;
     g->d_step = NULL;
     g->have_state = false;
@@ -800,13 +824,14 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
         o.qs = L->out.qs; o.d = L->out.d; o.wf = L->out.wf; o.rows = L->out.rows; o.cols = L->out.cols;
         o.y = g->x; o.epi = SGK_EPI_ADD; o.eps = c->rms_eps;
         if (L->attn) {
-            if ((e = sgk_attn_prep(g->act, L->qn, L->kn, g->cs_table, L->kc, L->vc, g->d_step, c->n_heads,
-                                   c->n_kv_heads, hd, c->rope_dim, qs, c->rms_eps, s)) != hipSuccess) return e;
-            if ((e = sgk_attn_partial(g->act, L->kc, L->vc, g->am, g->as, g->aacc, g->d_step, c->n_heads,
-                                      c->n_kv_heads, hd, 0, qs, (float)(1.0 / sqrt((double)hd)), 0,
-                                      g->max_splits, s)) != hipSuccess) return e;
-            if ((e = sgk_attn_combine(g->am, g->as, g->aacc, g->ctx, c->attn_output_gate ? g->act + hd : NULL, qs,
-                                      g->d_step, c->n_heads, hd, 0, g->max_splits, s)) != hipSuccess) return e;
+            sgk_attn A = {0};
+            A.q = g->act; A.kc = L->kc; A.vc = L->vc; A.m = g->am; A.s = g->as; A.acc = g->aacc; A.out = g->ctx;
+            A.gate = c->attn_output_gate ? g->act + hd : NULL; A.steps = g->d_step;
+            A.n_heads = c->n_heads; A.n_kv = c->n_kv_heads; A.hd = hd; A.rope_dim = c->rope_dim; A.q_stride = qs;
+            A.max_splits = g->max_splits; A.ntok = 1; A.scale = (float)(1.0 / sqrt((double)hd));
+            if ((e = sgk_attn_prep(&A, L->qn, L->kn, g->cs_table, c->rms_eps, s)) != hipSuccess) return e;
+            if ((e = sgk_attn_partial(&A, s)) != hipSuccess) return e;
+            if ((e = sgk_attn_combine(&A, s)) != hipSuccess) return e;
             o.x = g->ctx; o.pro = SGK_PRO_NONE;
         } else {
             sgk_gdn d = {0};
@@ -815,8 +840,10 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             d.dk = c->head_k_dim; d.dv = c->head_v_dim; d.conv_dim = g->conv_dim; d.ksize = c->conv_kernel;
             d.tiled = g->model->v_heads_tiled; d.neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
             if ((e = sgk_gdn_step(&d, s)) != hipSuccess) return e;
-            o.x = g->ybuf; o.pro = SGK_PRO_RMS_GATED; o.z = g->act + g->conv_dim; o.nw = L->ssm_norm;
-            o.head = c->head_v_dim;
+            /* RMSNormGated once (not in every GEMV workgroup), then the out projection */
+            if ((e = sgk_rmsnorm_gated(g->ybuf, g->act + g->conv_dim, L->ssm_norm, g->gbuf, c->head_v_dim,
+                                       c->n_v_heads, c->rms_eps, s)) != hipSuccess) return e;
+            o.x = g->gbuf; o.pro = SGK_PRO_NONE;
         }
         if ((e = sgk_gemv_launch(&o, s)) != hipSuccess) return e;
         sgk_gemv f = {0};
@@ -880,6 +907,7 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     struct { void **p; uint64_t n; } al[] = {
         {(void **)&g->x, (uint64_t)c->hidden * 4}, {(void **)&g->act, (uint64_t)act_rows * 4},
         {(void **)&g->ctx, (uint64_t)g->attn_width * 4 + 4}, {(void **)&g->ybuf, (uint64_t)g->value_dim * 4 + 4},
+        {(void **)&g->gbuf, (uint64_t)g->value_dim * 4 + 4},
         {(void **)&g->ffg, (uint64_t)c->ffn_hidden * 4}, {(void **)&g->logits, (uint64_t)c->vocab * 4},
         {(void **)&g->am, ah * 4}, {(void **)&g->as, ah * 4}, {(void **)&g->aacc, ah * c->head_dim * 4},
         {(void **)&g->amax_scratch, 4096}, {(void **)&g->hist, ((uint64_t)max_ctx + 2) * 4},
@@ -1024,20 +1052,123 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
  * prefill (surge.h:1276-1309)
  * --------------------------------------------------------------------- */
 
+/* Chunk scratch, sized for `chunk` tokens on first use (and regrown). */
+static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
+    if (g->pf_chunk >= chunk) return SG_OK;
+    void **bufs[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
+                      (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
+                      (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc };
+    for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) { dfree(g, *bufs[i]); *bufs[i] = NULL; }
+    if (g->pf_hsteps) { hipHostFree(g->pf_hsteps); g->pf_hsteps = NULL; }
+    g->pf_chunk = 0;
+    const sg_cfg *c = &g->cfg;
+    uint32_t in_rows = 0;
+    for (uint32_t i = 0; i < c->n_layers; i++) if (g->ls[i].in.rows > in_rows) in_rows = g->ls[i].in.rows;
+    uint64_t n = chunk, ah = n * c->n_heads * SGK_PREFILL_SPLITS;
+    uint64_t sizes[] = { n * sizeof(sgk_step), n * c->hidden * 4, n * c->hidden * 4, n * in_rows * 4,
+                         n * g->conv_dim * 4 + 4, n * g->value_dim * 4 + 4, n * g->value_dim * 4 + 4,
+                         n * g->attn_width * 4 + 4, n * c->ffn_hidden * 4, ah * 4, ah * 4, ah * c->head_dim * 4 };
+    sg_err e = SG_OK;
+    for (size_t i = 0; i < sizeof bufs / sizeof *bufs && !sg_failed(e); i++) e = dzalloc(g, sizes[i], bufs[i]);
+    if (!sg_failed(e) && hipHostMalloc((void **)&g->pf_hsteps, n * sizeof(sgk_step), 0) != hipSuccess)
+        e = (sg_err){"gpu: hipHostMalloc failed"};
+    if (sg_failed(e)) return e;
+    g->pf_chunk = chunk;
+    return SG_OK;
+}
+
+static hipError_t gemm_rows(sg_gpu *g, const dmat *M, const float *X, uint32_t ldx, float *Y, uint32_t ldy,
+                            uint32_t n, int epi) {
+    sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi };
+    return sgk_gemm(&a, g->stream);
+}
+
+/* One chunk of n tokens at positions base..base+n-1 through every layer. */
+static hipError_t prefill_chunk(sg_gpu *g, uint32_t n) {
+    const sg_cfg *c = &g->cfg;
+    hipStream_t s = g->stream;
+    hipError_t e;
+    const uint32_t H = c->hidden, hd = c->head_dim, qs = c->attn_output_gate ? 2 * hd : hd;
+    if ((e = sgk_embed_rows(g->emb.qs, g->emb.d, g->emb.wf, H, g->pf_steps, n, g->pf_X, s)) != hipSuccess) return e;
+    for (uint32_t i = 0; i < c->n_layers; i++) {
+        glayer *L = &g->ls[i];
+        const uint32_t in_rows = L->in.rows;
+        if ((e = sgk_rmsnorm_heads(g->pf_X, L->ln1, g->pf_Xn, H, n, H, c->rms_eps, s)) != hipSuccess) return e;
+        if ((e = gemm_rows(g, &L->in, g->pf_Xn, H, g->pf_IN, in_rows, n, SGK_EPI_STORE)) != hipSuccess) return e;
+        if (L->attn) {
+            sgk_attn A = {0};
+            A.q = g->pf_IN; A.kc = L->kc; A.vc = L->vc; A.m = g->pf_m; A.s = g->pf_s; A.acc = g->pf_acc;
+            A.out = g->pf_CTX; A.gate = c->attn_output_gate ? g->pf_IN + hd : NULL; A.steps = g->pf_steps;
+            A.n_heads = c->n_heads; A.n_kv = c->n_kv_heads; A.hd = hd; A.rope_dim = c->rope_dim; A.q_stride = qs;
+            A.q_tok = in_rows; A.out_tok = g->attn_width; A.max_splits = SGK_PREFILL_SPLITS; A.ntok = n;
+            A.scale = (float)(1.0 / sqrt((double)hd)); A.prefill = 1;
+            if ((e = sgk_attn_prep(&A, L->qn, L->kn, g->cs_table, c->rms_eps, s)) != hipSuccess) return e;
+            if ((e = sgk_attn_partial(&A, s)) != hipSuccess) return e;
+            if ((e = sgk_attn_combine(&A, s)) != hipSuccess) return e;
+            if ((e = gemm_rows(g, &L->out, g->pf_CTX, g->attn_width, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;
+        } else {
+            sgk_gdn d = {0};
+            d.in = g->pf_IN; d.conv_w = L->conv_w; d.ring = L->ring; d.ssm_a = L->ssm_a; d.dt_bias = L->dt_bias;
+            d.S = L->S; d.y = g->pf_Y; d.step = g->pf_steps; d.n_k = c->n_k_heads; d.n_v = c->n_v_heads;
+            d.dk = c->head_k_dim; d.dv = c->head_v_dim; d.conv_dim = g->conv_dim; d.ksize = c->conv_kernel;
+            d.tiled = g->model->v_heads_tiled; d.neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
+            if ((e = sgk_gdn_chunk(&d, g->pf_CONV, in_rows, n, s)) != hipSuccess) return e;
+            if ((e = sgk_rmsnorm_gated_rows(g->pf_Y, g->pf_IN + g->conv_dim, in_rows, L->ssm_norm, g->pf_G,
+                                            c->head_v_dim, c->n_v_heads, n, c->rms_eps, s)) != hipSuccess) return e;
+            if ((e = gemm_rows(g, &L->out, g->pf_G, g->value_dim, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;
+        }
+        if ((e = sgk_rmsnorm_heads(g->pf_X, L->ln2, g->pf_Xn, H, n, H, c->rms_eps, s)) != hipSuccess) return e;
+        if ((e = gemm_rows(g, &L->gu, g->pf_Xn, H, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU)) != hipSuccess) return e;
+        if ((e = gemm_rows(g, &L->down, g->pf_FF, c->ffn_hidden, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+/* Chunked prompt ingest (surge.h:1276-1309): every projection of a chunk is
+ * one MFMA GEMM; attention runs the decode split-K kernels over the chunk's
+ * tokens (each against its own causal prefix); the DeltaNet conv and delta
+ * rule scan the chunk in order with the state threaded through, exactly as
+ * decode would. Only the last row gets out_norm + lm_head. */
 sg_err sg_gpu_prefill(sg_gpu *g, const sg_model *m, const int32_t *tokens, uint32_t n_tokens,
                       uint32_t chunk_size, const float **out_last_logits) {
-    (void)chunk_size;
     if (!g || !m || !tokens) return (sg_err){"gpu: sg_gpu_prefill got a NULL argument"};
     if (!g->have_state) return (sg_err){"gpu: call sg_gpu_state_new first"};
     if (m != g->model) return (sg_err){"gpu: this gpu was loaded with a different sg_model"};
     if (!n_tokens || n_tokens > g->max_ctx) return (sg_err){"gpu: n_tokens must be in [1, max_ctx]"};
     for (uint32_t i = 0; i < n_tokens; i++)
         if (tokens[i] < 0 || (uint32_t)tokens[i] >= g->cfg.vocab) return (sg_err){"gpu: token id out of range"};
-    sg_gpu_state_reset(g);
-    sg_err e = SG_OK;
-    for (uint32_t i = 0; i + 1 < n_tokens && !sg_failed(e); i++) e = sg_gpu_forward_nosync(g, m, tokens[i], i);
+    uint32_t chunk = chunk_size ? chunk_size : SG_PREFILL_CHUNK_DEFAULT;
+    if (chunk > n_tokens) chunk = n_tokens;
+    sg_err e = prefill_alloc(g, chunk);
     if (sg_failed(e)) return e;
-    return sg_gpu_forward(g, m, tokens[n_tokens - 1], n_tokens - 1, out_last_logits);
+    sg_gpu_state_reset(g);
+    g->pf_segments = 0;
+    for (uint32_t base = 0; base < n_tokens; base += chunk) {
+        uint32_t n = n_tokens - base < chunk ? n_tokens - base : chunk;
+        for (uint32_t z = 0; z < n; z++) {
+            g->pf_hsteps[z].token = tokens[base + z];
+            g->pf_hsteps[z].pos = base + z;
+        }
+        HIPCHK(hipMemcpyAsync(g->pf_steps, g->pf_hsteps, (uint64_t)n * sizeof(sgk_step), hipMemcpyHostToDevice,
+                              g->stream), "chunk descriptors");
+        hipError_t he = prefill_chunk(g, n);
+        if (he != hipSuccess) return errf("gpu: prefill launch failed: %s", hipGetErrorString(he));
+        if (base + n >= n_tokens) {
+            sgk_gemv lm = {0};
+            lm.qs = g->lm.qs; lm.d = g->lm.d; lm.wf = g->lm.wf; lm.rows = g->lm.rows; lm.cols = g->lm.cols;
+            lm.x = g->pf_X + (uint64_t)(n - 1) * g->cfg.hidden; lm.nw = g->out_norm; lm.eps = g->cfg.rms_eps;
+            lm.y = g->logits; lm.pro = SGK_PRO_RMS; lm.epi = SGK_EPI_STORE;
+            HIPCHK(sgk_gemv_launch(&lm, g->stream), "lm_head");
+            HIPCHK(hipMemcpyAsync(g->h_logits, g->logits, (uint64_t)g->cfg.vocab * 4, hipMemcpyDeviceToHost,
+                                  g->stream), "logits download");
+        }
+        /* the pinned descriptor buffer is reused by the next chunk */
+        HIPCHK(hipStreamSynchronize(g->stream), "prefill chunk");
+        g->pf_segments++;
+    }
+    g->used = n_tokens;
+    if (out_last_logits) *out_last_logits = g->h_logits;
+    return SG_OK;
 }
 
 void sg_gpu_set_prefill_rest(sg_gpu *g, uint32_t work_budget_ms, uint32_t rest_ms) {
@@ -1045,7 +1176,7 @@ void sg_gpu_set_prefill_rest(sg_gpu *g, uint32_t work_budget_ms, uint32_t rest_m
 }
 uint64_t sg_gpu_prefill_rest_ms(const sg_gpu *g) { (void)g; return 0; }
 void sg_gpu_set_prefill_max_burst(sg_gpu *g, uint32_t max_burst_ms) { (void)g; (void)max_burst_ms; }
-uint64_t sg_gpu_prefill_segments(const sg_gpu *g) { (void)g; return 0; }
+uint64_t sg_gpu_prefill_segments(const sg_gpu *g) { return g ? g->pf_segments : 0; }
 
 /* ---------------------------------------------------------------------
  * measurement hooks (no reference counterpart)
@@ -1075,7 +1206,7 @@ sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which) {
         case 1:
             M = &L->out; a.y = g->x; a.epi = SGK_EPI_ADD;
             if (L->attn) { a.x = g->ctx; a.pro = SGK_PRO_NONE; }
-            else { a.x = g->ybuf; a.pro = SGK_PRO_RMS_GATED; a.z = g->act + g->conv_dim; a.nw = L->ssm_norm; a.head = c->head_v_dim; }
+            else { a.x = g->gbuf; a.pro = SGK_PRO_NONE; }
             break;
         case 2: M = &L->gu; a.x = g->x; a.nw = L->ln2; a.y = g->ffg; a.pro = SGK_PRO_RMS; a.epi = SGK_EPI_SWIGLU; break;
         case 3: M = &L->down; a.x = g->ffg; a.y = g->x; a.pro = SGK_PRO_NONE; a.epi = SGK_EPI_ADD; break;

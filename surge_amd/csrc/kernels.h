@@ -56,6 +56,7 @@ typedef struct {
     uint32_t head;          /* gated prologue: head width */
     float *y;               /* output [rows] (or [rows/2] for SWIGLU) */
     int pro, epi;
+    uint32_t tune_r, tune_blocks;   /* 0 = measured default; rows per wave, workgroups */
 } sgk_gemv;
 
 hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s);
@@ -86,30 +87,35 @@ hipError_t sgk_rope_heads(const float *x, const float *cs, float *out, uint32_t 
                           uint32_t rope_dim, uint32_t heads, uint32_t stride, hipStream_t s);
 hipError_t sgk_softmax(const float *x, float *out, uint32_t n, hipStream_t s);
 
-/* Decode attention pre-step, fused: q_norm + RoPE on the q half of each
- * head (stride 2*hd when gated), k_norm + RoPE on each kv head, then K and V
- * stored as f16 into the caches at the descriptor's position. cs_table is
- * [max_ctx][rope_dim] (cos | sin per position). */
-hipError_t sgk_attn_prep(float *qkv, const float *qn, const float *kn, const float *cs_table,
-                         uint16_t *kc, uint16_t *vc, const sgk_step *step,
-                         uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t rope_dim,
-                         uint32_t q_stride, float eps, hipStream_t s);
+/* Decode attention over one token (a decode step) or many (a prefill chunk:
+ * gridDim.z = ntok). Token z uses steps[z] (it writes K/V at steps[z].pos and
+ * attends over pos+1 keys); q/gate of token z start at q + z*q_tok (head h at
+ * + h*q_stride, its gate half at + hd); its m/s/acc slice starts at
+ * z*n_heads*max_splits (x hd for acc); its output at out + z*out_tok.
+ * Without steps (one-shot per-op calls) seq/n_splits are taken from here. */
+#define SGK_PREFILL_SPLITS 8u
+typedef struct {
+    float *q;                   /* prep: the fused q|k|v GEMM rows (q normed+roped in place) */
+    uint16_t *kc, *vc;          /* f16 caches [cap][n_kv][hd] */
+    float *m, *s, *acc;         /* partials */
+    float *out;                 /* combine output [ntok][n_heads*hd] */
+    const float *gate;          /* combine: q rows again (gate half), or NULL */
+    const sgk_step *steps;
+    uint32_t n_heads, n_kv, hd, rope_dim, q_stride, q_tok, out_tok;
+    uint32_t seq, n_splits, max_splits, ntok;
+    float scale;
+    int prefill;                /* split policy: 0 decode (kernels.h), 1 prefill */
+} sgk_attn;
 
-/* Split-K GQA decode attention partials. One workgroup per (split, kv head)
- * serves all n_heads/n_kv query heads. seq/n_splits come from the arguments
- * when step == NULL, else seq = step->pos + 1 and n_splits = sgk_n_splits(seq)
- * (grid sized for max_splits). */
-hipError_t sgk_attn_partial(const float *q, const uint16_t *kc, const uint16_t *vc,
-                            float *m, float *sacc, float *acc, const sgk_step *step,
-                            uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t seq,
-                            uint32_t q_stride, float scale, uint32_t n_splits,
-                            uint32_t max_splits, hipStream_t s);
-/* LSE combine; optional fused sigmoid output gate read from gate (stride
- * gstride per head, NULL for none). */
-hipError_t sgk_attn_combine(const float *m, const float *sacc, const float *acc, float *out,
-                            const float *gate, uint32_t gstride, const sgk_step *step,
-                            uint32_t n_heads, uint32_t hd, uint32_t n_splits,
-                            uint32_t max_splits, hipStream_t s);
+/* q_norm/k_norm + RoPE on each head, K and V stored f16 at each token's
+ * position. cs_table is [max_ctx][rope_dim] (cos | sin per position). */
+hipError_t sgk_attn_prep(const sgk_attn *a, const float *qn, const float *kn,
+                         const float *cs_table, float eps, hipStream_t s);
+/* Split-K GQA partials: workgroup (split, kv head, token) serves all
+ * n_heads/n_kv query heads of the group (grid x = max_splits with steps). */
+hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s);
+/* LSE combine with the optional fused sigmoid output gate. */
+hipError_t sgk_attn_combine(const sgk_attn *a, hipStream_t s);
 
 /* Gated DeltaNet decode step for one layer, fused: causal conv (ring state
  * of 4 slots indexed by position) + SiLU, q/k RMS (eps 1e-6) and scaling,
@@ -128,6 +134,21 @@ typedef struct {
     int tiled, neg_exp;
 } sgk_gdn;
 hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s);
+
+/* The DeltaNet layer over a prefill chunk of ntok tokens (a->step holds the
+ * chunk's descriptors, a->in the chunk's GEMM rows at in_stride, a->y the
+ * readouts [ntok][value_dim]): conv scan into conv_out [ntok][conv_dim], q/k
+ * norms, then the delta-rule scan with S in registers. Same arithmetic as
+ * sgk_gdn_step, token by token. */
+hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t in_stride, uint32_t ntok,
+                         hipStream_t s);
+/* silu(z) * rmsnorm(y, w) per (value head, token); z rows at z_stride. */
+hipError_t sgk_rmsnorm_gated_rows(const float *y, const float *z, uint32_t z_stride, const float *w,
+                                  float *out, uint32_t dv, uint32_t n_v, uint32_t ntok, float eps,
+                                  hipStream_t s);
+/* Embedding rows for a chunk: X[z] = row steps[z].token. */
+hipError_t sgk_embed_rows(const int8_t *qs, const uint16_t *d, const float *wf, uint32_t hidden,
+                          const sgk_step *steps, uint32_t ntok, float *X, hipStream_t s);
 
 /* The bare delta rule over every value head (the per-op oracle hook):
  * qkv holds normalised q|k|v, gates = beta[n_v] | decay[n_v]. */
@@ -155,6 +176,16 @@ hipError_t sgk_fill_f32(float *p, float v, uint64_t n, hipStream_t s);
 /* Prefill GEMM Y[N][M] = X[N][K] * W[M][K]^T with W in the Q8 device layout,
  * on MFMA (bf16 inputs, x split hi+lo, fp32 accumulate, per-block scale in
  * the accumulator). */
+typedef struct {
+    const float *X;          /* [N][ldx] */
+    const int8_t *qs;        /* Q8 layout W [M][K] (or NULL with wf) */
+    const uint16_t *d;
+    const float *wf;         /* f32 W [M][K] */
+    float *Y;                /* [N][ldy] */
+    uint32_t N, M, K, ldx, ldy;
+    int epi;                 /* SGK_EPI_*: store, += (residual), SwiGLU on (gate, up) column pairs */
+} sgk_gemm_args;
+hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s);
 hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, float *Y,
                        uint32_t N, uint32_t M, uint32_t K, hipStream_t s);
 

@@ -146,74 +146,105 @@ __device__ __forceinline__ float dot16(const uint4 q, const float4 x0, const flo
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 GEMV. One wave owns R consecutive output rows at a time (grid-stride
-// over row groups); lane l streams 16-byte chunks l, l+64, ... of each row.
-// A chunk is half a Q8_0 block: 16 int8 and the block's f16 scale.
+// Q8_0 GEMV. Persistent workgroups (a few per CU) walk row groups with a grid
+// stride, so the per-workgroup prologue (input staging, norm) is paid a few
+// times per CU rather than once per handful of rows. One wave owns R
+// consecutive output rows at a time; lane l streams 16-byte chunks l, l+64,
+// ... of each row (a chunk is half a Q8_0 block: 16 int8 and the block's f16
+// scale). The first row group's first chunks are requested before the
+// prologue runs, so HBM is busy while the input vector is staged.
 // ---------------------------------------------------------------------------
 
-template <int R, int PRO, int EPI>
+template <int R>
+struct gemv_chunk {
+    uint4 q[R];
+    uint16_t d[R];
+};
+
+template <int R>
+__device__ __forceinline__ void gemv_load(gemv_chunk<R> &ch, const int8_t *qs, const uint16_t *d,
+                                          uint32_t r0, uint32_t rows, uint32_t cols, uint32_t c) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint32_t rr = min(r0 + r, rows - 1);
+        ch.q[r] = ldnt((const uint4 *)(qs + (size_t)rr * cols) + c);
+        ch.d[r] = d[(size_t)rr * (cols >> 5) + (c >> 1)];
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void gemv_fma(float *acc, const gemv_chunk<R> &ch, const float *xs, uint32_t c) {
+    const float4 *xa = (const float4 *)(xs + c * 16);
+    const float4 a0 = xa[0], a1 = xa[1], a2 = xa[2], a3 = xa[3];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = fmaf(h2f(ch.d[r]), dot16(ch.q[r], a0, a1, a2, a3), acc[r]);
+}
+
+// x from LDS (staged) or, for long rows (XG), straight from global memory
+// through L1/L2 so the kernel needs no LDS and keeps full occupancy.
+template <int R, bool XG>
+__device__ __forceinline__ void gemv_fma_x(float *acc, const gemv_chunk<R> &ch, const float *xs,
+                                           const float *xg, uint32_t c) {
+    gemv_fma<R>(acc, ch, XG ? xg : xs, c);
+}
+
+// One row group of R rows: every chunk of the rows, two chunks per step, the
+// first chunk optionally already loaded (pre).
+template <int R, int EPI, bool PRE, bool XG>
+__device__ __forceinline__ void gemv_group(const sgk_gemv &a, const float *xs, uint32_t g, uint32_t lane,
+                                           const gemv_chunk<R> *pre) {
+    const uint32_t cols = a.cols, nch = cols >> 4, r0 = g * R;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    uint32_t c = lane;
+    if (PRE) {
+        if (c < nch) gemv_fma_x<R, XG>(acc, *pre, xs, a.x, c);
+        c += 64;
+    }
+    for (; c + 64 < nch; c += 128) {
+        gemv_chunk<R> ca, cb;
+        gemv_load<R>(ca, a.qs, a.d, r0, a.rows, cols, c);
+        gemv_load<R>(cb, a.qs, a.d, r0, a.rows, cols, c + 64);
+        gemv_fma_x<R, XG>(acc, ca, xs, a.x, c);
+        gemv_fma_x<R, XG>(acc, cb, xs, a.x, c + 64);
+    }
+    if (c < nch) {
+        gemv_chunk<R> ca;
+        gemv_load<R>(ca, a.qs, a.d, r0, a.rows, cols, c);
+        gemv_fma_x<R, XG>(acc, ca, xs, a.x, c);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    if (EPI == SGK_EPI_SWIGLU) {
+        // rows come in (gate, up) pairs: y[i] = silu(gate_i) * up_i
+#pragma unroll
+        for (int p = 0; p < R / 2; p++)
+            if (lane == (uint32_t)p && r0 + 2 * p + 1 < a.rows)
+                a.y[(r0 >> 1) + p] = silu(acc[2 * p]) * acc[2 * p + 1];
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (lane == (uint32_t)r && r0 + r < a.rows) gemv_store<EPI>(a, r0 + r, acc[r]);
+    }
+}
+
+template <int R, int PRO, int EPI, bool XG>
 __global__ void __launch_bounds__(TPB) k_gemv_q8(sgk_gemv a) {
     extern __shared__ float xs[];
-    stage_x<PRO>(a, xs);
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t cols = a.cols, nch = cols >> 4, nbl = cols >> 5;
-    const uint32_t ngroups = (a.rows + R - 1) / R;
-    for (uint32_t g = blockIdx.x * (TPB / 64) + wave; g < ngroups; g += gridDim.x * (TPB / 64)) {
-        const uint32_t r0 = g * R;
-        const uint4 *qrow[R];
-        const uint16_t *drow[R];
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint32_t rr = min(r0 + r, a.rows - 1);
-            qrow[r] = (const uint4 *)(a.qs + (size_t)rr * cols);
-            drow[r] = a.d + (size_t)rr * nbl;
-            acc[r] = 0.0f;
-        }
-        uint32_t c = lane;
-        for (; c + 64 < nch; c += 128) {
-            uint4 qa[R], qb[R];
-            uint16_t da[R], db[R];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                qa[r] = ldnt(qrow[r] + c);
-                qb[r] = ldnt(qrow[r] + c + 64);
-                da[r] = drow[r][c >> 1];
-                db[r] = drow[r][(c + 64) >> 1];
-            }
-            const float4 *xa = (const float4 *)(xs + c * 16);
-            const float4 *xb = (const float4 *)(xs + (c + 64) * 16);
-            const float4 a0 = xa[0], a1 = xa[1], a2 = xa[2], a3 = xa[3];
-            const float4 b0 = xb[0], b1 = xb[1], b2 = xb[2], b3 = xb[3];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                acc[r] = fmaf(h2f(da[r]), dot16(qa[r], a0, a1, a2, a3), acc[r]);
-                acc[r] = fmaf(h2f(db[r]), dot16(qb[r], b0, b1, b2, b3), acc[r]);
-            }
-        }
-        if (c < nch) {
-            const float4 *xa = (const float4 *)(xs + c * 16);
-            const float4 a0 = xa[0], a1 = xa[1], a2 = xa[2], a3 = xa[3];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 q = ldnt(qrow[r] + c);
-                acc[r] = fmaf(h2f(drow[r][c >> 1]), dot16(q, a0, a1, a2, a3), acc[r]);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
-        if (EPI == SGK_EPI_SWIGLU) {
-            // rows come in (gate, up) pairs: y[i] = silu(gate_i) * up_i
-#pragma unroll
-            for (int p = 0; p < R / 2; p++)
-                if (lane == (uint32_t)p && r0 + 2 * p + 1 < a.rows)
-                    a.y[(r0 >> 1) + p] = silu(acc[2 * p]) * acc[2 * p + 1];
-        } else {
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                if (lane == (uint32_t)r && r0 + r < a.rows) gemv_store<EPI>(a, r0 + r, acc[r]);
-        }
-    }
+    const uint32_t nch = a.cols >> 4;
+    const uint32_t ngroups = (a.rows + R - 1) / R, gstride = gridDim.x * (TPB / 64);
+    uint32_t g = blockIdx.x * (TPB / 64) + wave;
+    const bool have = g < ngroups;
+    // The first chunk of this wave's first row group is requested before the
+    // prologue, so HBM is already busy while the input vector is staged.
+    gemv_chunk<R> pre;
+    if (have && lane < nch) gemv_load<R>(pre, a.qs, a.d, g * R, a.rows, a.cols, lane);
+    if (!XG) stage_x<PRO>(a, xs);
+    if (!have) return;
+    gemv_group<R, EPI, true, XG>(a, xs, g, lane, &pre);
+    for (g += gstride; g < ngroups; g += gstride) gemv_group<R, EPI, false, XG>(a, xs, g, lane, nullptr);
 }
 
 // f32-weight GEMV (small test models only): one wave per row pair.
@@ -245,33 +276,48 @@ __global__ void __launch_bounds__(TPB) k_gemv_f32(sgk_gemv a) {
 }
 
 template <typename K>
-static hipError_t launch_lds(K kern, dim3 grid, size_t lds, hipStream_t s, const sgk_gemv &a) {
+static hipError_t launch_lds(K kern, uint32_t want_blocks, size_t lds, hipStream_t s, const sgk_gemv &a,
+                             uint32_t tune_blocks) {
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)kern,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kern, grid, dim3(TPB), lds, s, a);
+    // One co-resident round of workgroups (the whole grid in flight at once,
+    // each walking its row groups), unless the caller fixes the count.
+    uint32_t blocks = tune_blocks;
+    if (!blocks) {
+        static int cus = 0;
+        if (!cus && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) cus = 256;
+        int per = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)kern, TPB, lds) != hipSuccess || per < 1)
+            per = 1;
+        blocks = (uint32_t)(cus * per);
+    }
+    blocks = min(blocks, want_blocks);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(TPB), lds, s, a);
     return hipGetLastError();
 }
 
 template <int PRO, int EPI>
 static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
-    size_t lds = (size_t)a->cols * 4 + (PRO == SGK_PRO_RMS_GATED ? (a->cols / a->head) * 4 + 16 : 16);
+    const bool xg = PRO == SGK_PRO_NONE && a->cols > 8192;     // long rows: x from L1/L2, no LDS
+    size_t lds = xg ? 0 : (size_t)a->cols * 4 + (PRO == SGK_PRO_RMS_GATED ? (a->cols / a->head) * 4 + 16 : 16);
     if (!a->qs) {
         uint32_t groups = (a->rows + 1) / 2;
-        uint32_t blocks = min((groups + 3) / 4, 4096u);
-        return launch_lds(k_gemv_f32<PRO, EPI>, dim3(blocks), lds, s, *a);
+        hipLaunchKernelGGL((k_gemv_f32<PRO, EPI>), dim3(min((groups + 3) / 4, 4096u)), dim3(TPB), lds, s, *a);
+        return hipGetLastError();
     }
-    // Pick rows-per-wave so the grid still covers every CU several times.
-    int R = 4;
-    if (a->rows < 4 * 4 * 1024) R = 2;
-    if (a->rows < 2 * 4 * 1024) R = (EPI == SGK_EPI_SWIGLU) ? 2 : 1;
-    uint32_t groups = (a->rows + R - 1) / R;
-    uint32_t blocks = min((groups + 3) / 4, 8192u);
-    if (R == 4) return launch_lds(k_gemv_q8<4, PRO, EPI>, dim3(blocks), lds, s, *a);
-    if (R == 2) return launch_lds(k_gemv_q8<2, PRO, EPI>, dim3(blocks), lds, s, *a);
-    return launch_lds(k_gemv_q8<1, PRO, (EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI)>, dim3(blocks), lds, s, *a);
+    int R = a->tune_r ? (int)a->tune_r : (a->rows >= 65536 ? 4 : 2);
+    if (EPI == SGK_EPI_SWIGLU && R < 2) R = 2;
+    const uint32_t want = (((a->rows + R - 1) / R) + 3) / 4;
+    const uint32_t tb = a->tune_blocks;
+#define GV(RR, X) return launch_lds(k_gemv_q8<RR, PRO, (RR == 1 && EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI), X>, want, lds, s, *a, tb)
+    if (xg) { if (R == 4) GV(4, true); if (R == 2) GV(2, true); GV(1, true); }
+    if (R == 4) GV(4, false);
+    if (R == 2) GV(2, false);
+    GV(1, false);
+#undef GV
 }
 
 extern "C" hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s) {
@@ -464,22 +510,34 @@ extern "C" hipError_t sgk_softmax(const float *x, float *out, uint32_t n, hipStr
 }
 
 // ---------------------------------------------------------------------------
-// Attention pre-step (decode): q_norm/k_norm + RoPE + f16 KV store.
-// One workgroup per query head, then one per kv head.
+// Decode attention for one or many tokens. Token z of a launch (gridDim.z)
+// reads its descriptor steps[z] (position; it attends over pos+1 keys), its
+// query/gate row at q + z*q_tok, and owns its own m/s/acc slice. A decode step
+// is the one-token case; a prefill chunk runs the same kernels over its tokens.
 // ---------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(TPB) k_attn_prep(float *qkv, const float *qn, const float *kn,
-                                                   const float *cs_table, uint16_t *kc, uint16_t *vc,
-                                                   const sgk_step *step, uint32_t n_heads,
-                                                   uint32_t n_kv, uint32_t hd, uint32_t rope_dim,
-                                                   uint32_t q_stride, float eps) {
+// Split count as the kernels see it: the decode policy (kernels.h), or the
+// prefill policy (at most SGK_PREFILL_SPLITS splits of >= 1024 keys, so a
+// chunk's partial scratch stays bounded).
+__device__ __forceinline__ uint32_t dev_splits(uint32_t seq, int prefill) {
+    if (!prefill) return dev_n_splits(seq);
+    uint32_t n = seq / 1024u;
+    n = n < 1 ? 1 : n;
+    return n > SGK_PREFILL_SPLITS ? SGK_PREFILL_SPLITS : n;
+}
+
+// q_norm/k_norm + RoPE + f16 KV store. Workgroup (head, token): query heads
+// first, then kv heads.
+__global__ void __launch_bounds__(TPB) k_attn_prep(sgk_attn a, const float *qn, const float *kn,
+                                                   const float *cs_table, float eps) {
     __shared__ float red[4];
     __shared__ float buf[TPB];
-    const uint32_t pos = step->pos, t = threadIdx.x, b = blockIdx.x;
-    const float *cs = cs_table + (size_t)pos * rope_dim;
-    const bool isq = b < n_heads;
-    const uint32_t kh = b - n_heads;
-    float *x = isq ? qkv + (size_t)b * q_stride : qkv + (size_t)n_heads * q_stride + (size_t)kh * hd;
+    const uint32_t z = blockIdx.y, pos = a.steps[z].pos, t = threadIdx.x, b = blockIdx.x, hd = a.hd;
+    const float *cs = cs_table + (size_t)pos * a.rope_dim;
+    const bool isq = b < a.n_heads;
+    const uint32_t kh = b - a.n_heads;
+    float *row = (float *)a.q + (size_t)z * a.q_tok;
+    float *x = isq ? row + (size_t)b * a.q_stride : row + (size_t)a.n_heads * a.q_stride + (size_t)kh * hd;
     const float *w = isq ? qn : kn;
     const float v = t < hd ? x[t] : 0.0f;
     const float ss = block_sum(v * v, red);
@@ -487,54 +545,47 @@ __global__ void __launch_bounds__(TPB) k_attn_prep(float *qkv, const float *qn, 
     const float xn = t < hd ? (v * r) * w[t] : 0.0f;
     buf[t] = xn;
     __syncthreads();
-    const uint32_t half = rope_dim >> 1;
+    const uint32_t half = a.rope_dim >> 1;
     float o = xn;
     if (t < half) o = buf[t] * cs[t] - buf[t + half] * cs[half + t];
-    else if (t < rope_dim) o = buf[t - half] * cs[t] + buf[t] * cs[t - half];
+    else if (t < a.rope_dim) o = buf[t - half] * cs[t] + buf[t] * cs[t - half];
     if (t >= hd) return;
     if (isq) {
         x[t] = o;
     } else {
-        const size_t at = ((size_t)pos * n_kv + kh) * hd + t;
-        const float *vraw = qkv + (size_t)n_heads * q_stride + (size_t)n_kv * hd + (size_t)kh * hd;
-        kc[at] = f2h(o);
-        vc[at] = f2h(vraw[t]);
+        const size_t at = ((size_t)pos * a.n_kv + kh) * hd + t;
+        const float *vraw = row + (size_t)a.n_heads * a.q_stride + (size_t)a.n_kv * hd + (size_t)kh * hd;
+        ((uint16_t *)a.kc)[at] = f2h(o);
+        ((uint16_t *)a.vc)[at] = f2h(vraw[t]);
     }
 }
 
-extern "C" hipError_t sgk_attn_prep(float *qkv, const float *qn, const float *kn,
-                                    const float *cs_table, uint16_t *kc, uint16_t *vc,
-                                    const sgk_step *step, uint32_t n_heads, uint32_t n_kv,
-                                    uint32_t hd, uint32_t rope_dim, uint32_t q_stride, float eps,
-                                    hipStream_t s) {
-    if (hd > TPB) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attn_prep, dim3(n_heads + n_kv), dim3(TPB), 0, s, qkv, qn, kn, cs_table,
-                       kc, vc, step, n_heads, n_kv, hd, rope_dim, q_stride, eps);
+extern "C" hipError_t sgk_attn_prep(const sgk_attn *a, const float *qn, const float *kn,
+                                    const float *cs_table, float eps, hipStream_t s) {
+    if (a->hd > TPB || !a->ntok) return a->ntok ? hipErrorInvalidValue : hipSuccess;
+    hipLaunchKernelGGL(k_attn_prep, dim3(a->n_heads + a->n_kv, a->ntok), dim3(TPB), 0, s, *a, qn, kn,
+                       cs_table, eps);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // Split-K GQA decode attention partial.
 //
-// Workgroup (split i, kv head hk) owns keys [i*seq/n, (i+1)*seq/n) and all
-// G = n_heads/n_kv query heads of the group, so every K/V byte is read once.
-// Keys are processed in tiles of 32: scores (8 lanes per key, HD/8 dims per
-// lane, q from LDS), tile max and exp per head, then P*V with one output dim
-// per lane. Across tiles the running max/sum/acc are rescaled (online
-// softmax); a split of at most 32 keys is exactly the reference's two-pass
-// form. Output: m, s and the UNNORMALISED acc, as ref.c's attn_partial.
+// Workgroup (split i, kv head hk, token z) owns keys [i*seq/n, (i+1)*seq/n) and
+// all G = n_heads/n_kv query heads of the group, so every K/V byte is read
+// once per token. Keys are processed in tiles of 32: scores (8 lanes per key,
+// HD/8 dims per lane, q from LDS), tile max and exp per head, then P*V with
+// one output dim per lane. Across tiles the running max/sum/acc are rescaled
+// (online softmax); a split of at most 32 keys is exactly the reference's
+// two-pass form. Output: m, s and the UNNORMALISED acc, as ref.c's
+// attn_partial.
 // ---------------------------------------------------------------------------
 
 #define GMAX 8
 #define KT 32
 
 template <int HD>
-__global__ void __launch_bounds__(TPB) k_attn_partial(const float *q, const uint16_t *kc,
-                                                      const uint16_t *vc, float *mo, float *so,
-                                                      float *acco, const sgk_step *step,
-                                                      uint32_t n_heads, uint32_t n_kv,
-                                                      uint32_t seq_arg, uint32_t q_stride,
-                                                      float scale, uint32_t ns_arg) {
+__global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
     constexpr int KG = TPB / HD;          // key groups for P*V (HD <= 256)
     constexpr int DPL = HD / 8;           // dims per lane in the score phase
     __shared__ float qsh[GMAX][HD];
@@ -542,18 +593,21 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(const float *q, const uint
     __shared__ float mrun[GMAX], srun[GMAX], alpha[GMAX];
     __shared__ float accx[KG > 1 ? GMAX * TPB : 1];
 
-    const uint32_t G = n_heads / n_kv;
-    const uint32_t seq = step ? step->pos + 1 : seq_arg;
-    const uint32_t ns = step ? dev_n_splits(seq) : ns_arg;
+    const uint32_t G = a.n_heads / a.n_kv, n_kv = a.n_kv, z = blockIdx.z;
+    const uint32_t seq = a.steps ? a.steps[z].pos + 1 : a.seq;
+    const uint32_t ns = a.steps ? dev_splits(seq, a.prefill) : a.n_splits;
     const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x;
     if (i >= ns) return;
     const uint32_t t0 = (uint32_t)((uint64_t)i * seq / ns);
     const uint32_t t1 = (uint32_t)((uint64_t)(i + 1) * seq / ns);
     const uint32_t h0 = hk * G;
+    const float *q = a.q + (size_t)z * a.q_tok;
+    const uint16_t *kc = a.kc, *vc = a.vc;
+    const size_t zoff = (size_t)z * a.n_heads * a.max_splits;
 
     for (uint32_t e = t; e < G * HD; e += TPB) {
         const uint32_t h = e / HD, dd = e % HD;
-        qsh[h][dd] = q[(size_t)(h0 + h) * q_stride + dd];
+        qsh[h][dd] = q[(size_t)(h0 + h) * a.q_stride + dd];
     }
     if (t < GMAX) { mrun[t] = -INFINITY; srun[t] = 0.0f; }
     __syncthreads();
@@ -614,7 +668,7 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(const float *q, const uint
         if (kp == 0) {
 #pragma unroll
             for (int h = 0; h < GMAX; h++)
-                if (h < (int)G) sc[h][kj] = (kj < nk) ? part[h] * scale : -INFINITY;
+                if (h < (int)G) sc[h][kj] = (kj < nk) ? part[h] * a.scale : -INFINITY;
         }
         __syncthreads();
         // Per head (32 lanes each): tile max, new running max, p = exp(s - m),
@@ -645,10 +699,10 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(const float *q, const uint
 #pragma unroll
         for (int h = 0; h < GMAX; h++) {
             if (h < (int)G) {
-                float a = acc[h] * alpha[h];
+                float v = acc[h] * alpha[h];
 #pragma unroll
-                for (int u = 0; u < KT / KG; u++) a = fmaf(sc[h][kg + u * KG], vr[u], a);
-                acc[h] = a;
+                for (int u = 0; u < KT / KG; u++) v = fmaf(sc[h][kg + u * KG], vr[u], v);
+                acc[h] = v;
             }
         }
         __syncthreads();
@@ -664,9 +718,9 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(const float *q, const uint
 #pragma unroll
             for (int h = 0; h < GMAX; h++) {
                 if (h < (int)G) {
-                    float a = accx[h * HD + d];
-                    for (int g2 = 1; g2 < KG; g2++) a += accx[(g2 * GMAX + h) * HD + d];
-                    acc[h] = a;
+                    float v = accx[h * HD + d];
+                    for (int g2 = 1; g2 < KG; g2++) v += accx[(g2 * GMAX + h) * HD + d];
+                    acc[h] = v;
                 }
             }
         }
@@ -675,28 +729,24 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(const float *q, const uint
 #pragma unroll
         for (int h = 0; h < GMAX; h++) {
             if (h < (int)G) {
-                const size_t o = (size_t)(h0 + h) * ns + i;
-                acco[o * HD + d] = acc[h];
+                const size_t o = zoff + (size_t)(h0 + h) * ns + i;
+                a.acc[o * HD + d] = acc[h];
                 if (d == 0) {
-                    mo[o] = mrun[h];
-                    so[o] = srun[h];
+                    a.m[o] = mrun[h];
+                    a.s[o] = srun[h];
                 }
             }
         }
     }
 }
 
-extern "C" hipError_t sgk_attn_partial(const float *q, const uint16_t *kc, const uint16_t *vc,
-                                       float *m, float *sacc, float *acc, const sgk_step *step,
-                                       uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t seq,
-                                       uint32_t q_stride, float scale, uint32_t n_splits,
-                                       uint32_t max_splits, hipStream_t s) {
-    if (!n_kv || n_heads % n_kv || n_heads / n_kv > GMAX) return hipErrorInvalidValue;
-    const uint32_t gx = step ? max_splits : n_splits;
-    if (!gx) return hipSuccess;
-    dim3 grid(gx, n_kv);
-#define HDCASE(H) case H: hipLaunchKernelGGL(k_attn_partial<H>, grid, dim3(TPB), 0, s, q, kc, vc, m, sacc, acc, step, n_heads, n_kv, seq, q_stride, scale, n_splits); break
-    switch (hd) {
+extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
+    if (!a->n_kv || a->n_heads % a->n_kv || a->n_heads / a->n_kv > GMAX) return hipErrorInvalidValue;
+    const uint32_t gx = a->steps ? a->max_splits : a->n_splits;
+    if (!gx || !a->ntok) return hipSuccess;
+    dim3 grid(gx, a->n_kv, a->ntok);
+#define HDCASE(H) case H: hipLaunchKernelGGL(k_attn_partial<H>, grid, dim3(TPB), 0, s, *a); break
+    switch (a->hd) {
         HDCASE(16); HDCASE(32); HDCASE(64); HDCASE(128); HDCASE(256);
     default: return hipErrorInvalidValue;
     }
@@ -704,20 +754,19 @@ extern "C" hipError_t sgk_attn_partial(const float *q, const uint16_t *kc, const
     return hipGetLastError();
 }
 
-// LSE combine (+ optional sigmoid gate). One workgroup per query head,
-// one output dim per thread. NaN/inf conventions of ref.c:265-373.
-__global__ void __launch_bounds__(TPB) k_attn_combine(const float *m, const float *sarr,
-                                                      const float *acc, float *out,
-                                                      const float *gate, uint32_t gstride,
-                                                      const sgk_step *step, uint32_t hd,
-                                                      uint32_t ns_arg) {
-    __shared__ float wts[SGK_MAX_SPLITS > 1024 ? SGK_MAX_SPLITS : 1024];
+// LSE combine (+ optional sigmoid gate). Workgroup (head, token), one output
+// dim per thread. NaN/inf conventions of ref.c:265-373.
+__global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
+    __shared__ float wts[1024];
     __shared__ float red[4];
     __shared__ float bc;
-    const uint32_t ns = step ? dev_n_splits(step->pos + 1) : ns_arg;
-    const uint32_t h = blockIdx.x, t = threadIdx.x;
-    const float *mh = m + (size_t)h * ns, *sh = sarr + (size_t)h * ns;
-    float *oh = out + (size_t)h * hd;
+    const uint32_t z = blockIdx.y, h = blockIdx.x, t = threadIdx.x, hd = a.hd;
+    const uint32_t ns = a.steps ? dev_splits(a.steps[z].pos + 1, a.prefill) : a.n_splits;
+    const size_t zoff = (size_t)z * a.n_heads * a.max_splits;
+    const float *mh = a.m + zoff + (size_t)h * ns, *sh = a.s + zoff + (size_t)h * ns;
+    const float *acc = a.acc + (zoff + (size_t)h * ns) * hd;
+    float *oh = a.out + (size_t)z * a.out_tok + (size_t)h * hd;
+    const float *gate = a.gate ? a.gate + (size_t)z * a.q_tok + (size_t)h * a.q_stride : NULL;
     // M: max over splits; a NaN first entry poisons the result (ref.c:288-300).
     float mx = -INFINITY;
     for (uint32_t k = t; k < ns; k += TPB) mx = fmaxf(mx, mh[k]);
@@ -746,23 +795,18 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(const float *m, const floa
             o = S;
         } else {
             float num = 0.0f;
-            for (uint32_t k = 0; k < ns; k++) num = fmaf(acc[((size_t)h * ns + k) * hd + dd], wts[k], num);
+            for (uint32_t k = 0; k < ns; k++) num = fmaf(acc[(size_t)k * hd + dd], wts[k], num);
             o = S > 0.0f ? num / S : 0.0f;
         }
-        if (gate) o *= sigm(gate[(size_t)h * gstride + dd]);
+        if (gate) o *= sigm(gate[dd]);
         oh[dd] = o;
     }
 }
 
-extern "C" hipError_t sgk_attn_combine(const float *m, const float *sacc, const float *acc,
-                                       float *out, const float *gate, uint32_t gstride,
-                                       const sgk_step *step, uint32_t n_heads, uint32_t hd,
-                                       uint32_t n_splits, uint32_t max_splits, hipStream_t s) {
-    (void)max_splits;
-    if (!n_heads) return hipSuccess;
-    if (!step && n_splits > 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attn_combine, dim3(n_heads), dim3(TPB), 0, s, m, sacc, acc, out, gate,
-                       gstride, step, hd, n_splits);
+extern "C" hipError_t sgk_attn_combine(const sgk_attn *a, hipStream_t s) {
+    if (!a->n_heads || !a->ntok) return hipSuccess;
+    if (!a->steps && a->n_splits > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attn_combine, dim3(a->n_heads, a->ntok), dim3(TPB), 0, s, *a);
     return hipGetLastError();
 }
 
@@ -772,21 +816,23 @@ extern "C" hipError_t sgk_attn_combine(const float *m, const float *sacc, const 
 
 #define GDN_ROWS 16   // value rows per workgroup (4 per wave)
 
-// One delta-rule row update held across a wave: element i of the row lives
-// in lane i / EPL, slot i % EPL (EPL = DK / 64, or 1 lane per element when
-// DK < 64). Returns y_j (the readout after the write); S row updated in place.
+// One delta-rule row update held across a wave (ref.c:708-739): element i of
+// the row lives in lane i / EPL, slot i % EPL (EPL = DK / 64, or one lane per
+// element when DK < 64). s[] holds the row; returns y_j, the readout AFTER
+// the write. Decode and the prefill scan share this arithmetic exactly.
 template <int DK>
-__device__ __forceinline__ float delta_row(float *row, const float *kk, const float *qq,
-                                           float vj, float beta, float decay, uint32_t lane) {
-    constexpr int EPL = DK >= 64 ? DK / 64 : 1;
-    float s[EPL], k[EPL], q[EPL];
+struct drow { static constexpr int EPL = DK >= 64 ? DK / 64 : 1; };
+
+template <int DK>
+__device__ __forceinline__ float delta_update(float *s, const float *kk, const float *qq, float vj,
+                                              float beta, float decay, uint32_t lane) {
+    constexpr int EPL = drow<DK>::EPL;
     const bool on = DK >= 64 || lane < (uint32_t)DK;
+    float k[EPL], q[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; e++) {
-        const uint32_t i = lane * EPL + e;
-        s[e] = on ? row[i] : 0.0f;
-        k[e] = on ? kk[i] : 0.0f;
-        q[e] = on ? qq[i] : 0.0f;
+        k[e] = on ? kk[lane * EPL + e] : 0.0f;
+        q[e] = on ? qq[lane * EPL + e] : 0.0f;
     }
     float kv = 0.0f;
 #pragma unroll
@@ -796,12 +842,39 @@ __device__ __forceinline__ float delta_row(float *row, const float *kk, const fl
     float y = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPL; e++) { s[e] = fmaf(k[e], delta, s[e]); y = fmaf(s[e], q[e], y); }
-    y = wave_sum(y);
-    if (on) {
+    return wave_sum(y);
+}
+
+template <int DK>
+__device__ __forceinline__ void row_load(float *s, const float *row, uint32_t lane) {
 #pragma unroll
-        for (int e = 0; e < EPL; e++) row[lane * EPL + e] = s[e];
+    for (int e = 0; e < drow<DK>::EPL; e++)
+        s[e] = (DK >= 64 || lane < (uint32_t)DK) ? row[lane * drow<DK>::EPL + e] : 0.0f;
+}
+template <int DK>
+__device__ __forceinline__ void row_store(const float *s, float *row, uint32_t lane) {
+    if (DK >= 64 || lane < (uint32_t)DK) {
+#pragma unroll
+        for (int e = 0; e < drow<DK>::EPL; e++) row[lane * drow<DK>::EPL + e] = s[e];
     }
+}
+
+template <int DK>
+__device__ __forceinline__ float delta_row(float *row, const float *kk, const float *qq, float vj,
+                                           float beta, float decay, uint32_t lane) {
+    float sr[drow<DK>::EPL];
+    row_load<DK>(sr, row, lane);
+    const float y = delta_update<DK>(sr, kk, qq, vj, beta, decay, lane);
+    row_store<DK>(sr, row, lane);
     return y;
+}
+
+// The per-head gates (ref.c:127-170): beta = sigmoid(b); decay by the stored form.
+__device__ __forceinline__ void gdn_gates(float b, float a, float ssm_a, float dt, int neg_exp,
+                                          float *beta, float *decay) {
+    *beta = sigm(b);
+    const float sp = softplus(a + dt);
+    *decay = neg_exp ? expf(ssm_a * sp) : expf(-(expf(ssm_a) * sp));
 }
 
 template <int DK>
@@ -849,11 +922,10 @@ __global__ void __launch_bounds__(TPB) k_gdn_step(sgk_gdn a) {
         qk[dk + i] = (qk[dk + i] * rk) * ksc;
     }
     __syncthreads();
-    // 3. gates (ref.c:127-170): beta = sigmoid(b); decay by the stored form.
+    // 3. gates
     const float *bb = a.in + cd + a.n_v * dv, *aa = bb + a.n_v;
-    const float beta = sigm(bb[h]);
-    const float sp = softplus(aa[h] + a.dt_bias[h]);
-    const float decay = a.neg_exp ? expf(a.ssm_a[h] * sp) : expf(-(expf(a.ssm_a[h]) * sp));
+    float beta, decay;
+    gdn_gates(bb[h], aa[h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
     // 4. rank-1 update and readout, 4 rows per wave.
     float *Sh = a.S + (size_t)h * dv * dk;
     for (uint32_t r = wave; r < nrows; r += TPB / 64) {
@@ -954,6 +1026,146 @@ extern "C" hipError_t sgk_rmsnorm_gated(const float *y, const float *z, const fl
 }
 
 // ---------------------------------------------------------------------------
+// Gated DeltaNet over a prefill chunk: the same arithmetic as the decode step,
+// scanned over the chunk's tokens in order (state threaded through).
+// ---------------------------------------------------------------------------
+
+// Causal conv + SiLU, one thread per channel walking the tokens; the ring
+// holds the last inputs by position, as in decode.
+__global__ void k_conv_chunk(const float *in, uint32_t in_stride, const float *conv_w, float *ring,
+                             float *out, const sgk_step *steps, uint32_t ntok, uint32_t cd, uint32_t ksize) {
+    const uint32_t ch = blockIdx.x * TPB + threadIdx.x;
+    if (ch >= cd) return;
+    const uint32_t keep = ksize - 1;
+    const float *w = conv_w + (size_t)ch * ksize;
+    for (uint32_t z = 0; z < ntok; z++) {
+        const uint32_t pos = steps[z].pos;
+        const float x = in[(size_t)z * in_stride + ch];
+        float acc = 0.0f;
+        for (uint32_t jj = 0; jj < keep; jj++)
+            acc = fmaf(w[jj], ring[(size_t)((pos + 4 - keep + jj) & 3) * cd + ch], acc);
+        acc = fmaf(w[keep], x, acc);
+        ring[(size_t)(pos & 3) * cd + ch] = x;
+        out[(size_t)z * cd + ch] = silu(acc);
+    }
+}
+
+// q and k of every key head of every token: RMS (eps 1e-6, no weight), then
+// q / dk and k / sqrt(dk), in place. Workgroup (head slice, token).
+__global__ void __launch_bounds__(TPB) k_qk_norm_chunk(float *conv_out, uint32_t cd, uint32_t n_k, uint32_t dk) {
+    __shared__ float red[4];
+    const uint32_t b = blockIdx.x, z = blockIdx.y, t = threadIdx.x;
+    const bool isq = b < n_k;
+    float *x = conv_out + (size_t)z * cd + (isq ? (size_t)b * dk : (size_t)n_k * dk + (size_t)(b - n_k) * dk);
+    float v = 0.0f;
+    for (uint32_t i = t; i < dk; i += TPB) v = fmaf(x[i], x[i], v);
+    const float ss = block_sum(v, red);
+    const float r = 1.0f / sqrtf(ss / (float)dk + 1e-6f);
+    const float sc = isq ? 1.0f / (float)dk : 1.0f / sqrtf((float)dk);
+    for (uint32_t i = t; i < dk; i += TPB) x[i] = (x[i] * r) * sc;
+}
+
+// Delta-rule scan: workgroup (value head, 16-row block) keeps its rows of S in
+// registers for the whole chunk, reads each token's q, k, v and gates, and
+// writes each token's readout y.
+template <int DK>
+__global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *conv_out, uint32_t in_stride,
+                                                     uint32_t ntok) {
+    constexpr int EPL = drow<DK>::EPL, RPW = GDN_ROWS / (TPB / 64);
+    const uint32_t h = blockIdx.x, j0 = blockIdx.y * GDN_ROWS, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t dv = a.dv, key_dim = a.n_k * DK, cd = a.conv_dim, vd = a.n_v * dv;
+    const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k);
+    float *Sh = a.S + (size_t)h * dv * DK;
+    float sr[RPW][EPL];
+#pragma unroll
+    for (int u = 0; u < RPW; u++) {
+        const uint32_t j = j0 + wave + u * (TPB / 64);
+        if (j < dv) row_load<DK>(sr[u], Sh + (size_t)j * DK, lane);
+    }
+    for (uint32_t z = 0; z < ntok; z++) {
+        const float *cz = conv_out + (size_t)z * cd;
+        const float *iz = a.in + (size_t)z * in_stride;
+        float beta, decay;
+        gdn_gates(iz[cd + vd + h], iz[cd + vd + a.n_v + h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
+#pragma unroll
+        for (int u = 0; u < RPW; u++) {
+            const uint32_t j = j0 + wave + u * (TPB / 64);
+            if (j < dv) {
+                const float y = delta_update<DK>(sr[u], cz + key_dim + (size_t)hk * DK, cz + (size_t)hk * DK,
+                                                 cz[2 * key_dim + (size_t)h * dv + j], beta, decay, lane);
+                if (lane == 0) a.y[(size_t)z * vd + (size_t)h * dv + j] = y;
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < RPW; u++) {
+        const uint32_t j = j0 + wave + u * (TPB / 64);
+        if (j < dv) row_store<DK>(sr[u], Sh + (size_t)j * DK, lane);
+    }
+}
+
+// silu(z) * rmsnorm(y, w) per (value head, token), one wave each, with the
+// GEMV gated prologue's arithmetic.
+__global__ void k_rmsnorm_gated_rows(const float *y, const float *zsrc, uint32_t z_stride, const float *w,
+                                     float *out, uint32_t dv, uint32_t n_v, float eps) {
+    const uint32_t lane = threadIdx.x & 63, h = blockIdx.x * (TPB / 64) + (threadIdx.x >> 6), z = blockIdx.y;
+    if (h >= n_v) return;
+    const float *yh = y + (size_t)z * n_v * dv + (size_t)h * dv;
+    const float *zh = zsrc + (size_t)z * z_stride + (size_t)h * dv;
+    float *oh = out + (size_t)z * n_v * dv + (size_t)h * dv;
+    float ss = 0.0f;
+    for (uint32_t j = lane; j < dv; j += 64) ss = fmaf(yh[j], yh[j], ss);
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)dv + eps);
+    for (uint32_t j = lane; j < dv; j += 64) oh[j] = silu(zh[j]) * ((yh[j] * r) * w[j]);
+}
+
+__global__ void k_embed_rows(const int8_t *qs, const uint16_t *d, const float *wf, uint32_t hidden,
+                             const sgk_step *steps, float *X) {
+    const uint32_t i = blockIdx.x * TPB + threadIdx.x, z = blockIdx.y;
+    if (i >= hidden) return;
+    const uint64_t t = (uint64_t)(uint32_t)steps[z].token;
+    float *x = X + (size_t)z * hidden;
+    if (qs) x[i] = h2f(d[t * (hidden >> 5) + (i >> 5)]) * (float)qs[t * hidden + i];
+    else x[i] = wf[t * hidden + i];
+}
+
+extern "C" hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t in_stride, uint32_t ntok,
+                                    hipStream_t s) {
+    if (!ntok) return hipSuccess;
+    if (a->ksize < 1 || a->ksize > 4 || !a->n_k || a->n_v % a->n_k) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_conv_chunk, dim3((a->conv_dim + TPB - 1) / TPB), dim3(TPB), 0, s, a->in, in_stride,
+                       a->conv_w, a->ring, conv_out, a->step, ntok, a->conv_dim, a->ksize);
+    hipLaunchKernelGGL(k_qk_norm_chunk, dim3(2 * a->n_k, ntok), dim3(TPB), 0, s, conv_out, a->conv_dim, a->n_k, a->dk);
+    dim3 grid(a->n_v, (a->dv + GDN_ROWS - 1) / GDN_ROWS);
+    switch (a->dk) {
+    case 32: hipLaunchKernelGGL(k_delta_chunk<32>, grid, dim3(TPB), 0, s, *a, conv_out, in_stride, ntok); break;
+    case 64: hipLaunchKernelGGL(k_delta_chunk<64>, grid, dim3(TPB), 0, s, *a, conv_out, in_stride, ntok); break;
+    case 128: hipLaunchKernelGGL(k_delta_chunk<128>, grid, dim3(TPB), 0, s, *a, conv_out, in_stride, ntok); break;
+    case 256: hipLaunchKernelGGL(k_delta_chunk<256>, grid, dim3(TPB), 0, s, *a, conv_out, in_stride, ntok); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t sgk_rmsnorm_gated_rows(const float *y, const float *z, uint32_t z_stride, const float *w,
+                                             float *out, uint32_t dv, uint32_t n_v, uint32_t ntok, float eps,
+                                             hipStream_t s) {
+    if (!ntok || !n_v) return hipSuccess;
+    hipLaunchKernelGGL(k_rmsnorm_gated_rows, dim3((n_v + 3) / 4, ntok), dim3(TPB), 0, s, y, z, z_stride, w, out,
+                       dv, n_v, eps);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t sgk_embed_rows(const int8_t *qs, const uint16_t *d, const float *wf, uint32_t hidden,
+                                     const sgk_step *steps, uint32_t ntok, float *X, hipStream_t s) {
+    if (!ntok) return hipSuccess;
+    hipLaunchKernelGGL(k_embed_rows, dim3((hidden + TPB - 1) / TPB, ntok), dim3(TPB), 0, s, qs, d, wf, hidden,
+                       steps, X);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Argmax (greedy.c:17-27): lowest index wins an exact tie. Two passes:
 // per-workgroup winners into scratch, then one workgroup folds them.
 // ---------------------------------------------------------------------------
@@ -1015,56 +1227,183 @@ extern "C" hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream
 }
 
 // ---------------------------------------------------------------------------
-// Prefill GEMM Y[N][M] = X[N][K] * W[M][K]^T, W in the Q8 device layout.
-// Straightforward LDS-tiled version: 64x64 output tile, one Q8_0 block
-// (32 columns of K) per step, per-block scale applied to the block partial.
+// Prefill GEMM Y[N][M] = X[N][K] * W[M][K]^T (chunk of N tokens through one
+// weight), W in the Q8 device layout, on MFMA.
+//
+// Precision: int8 weights are exact in bf16 (|q| <= 127); x is split into
+// bf16 hi + lo (x = hi + lo to ~16 bits), so each Q8_0 block's partial dot is
+// two v_mfma_f32_16x16x32_bf16 into a zeroed fp32 tile, then scaled by the
+// block's f16 scale into the fp32 accumulator. The weights are never
+// dequantised into bf16 (d*q has ~18 significant bits).
+//
+// Tiling: workgroup 256 threads = 4 waves over a 64-token x 128-row tile
+// (waves 2 x 2, each 32 x 64 = 2 x 4 MFMA tiles of 16x16), K in steps of 64
+// (two Q8_0 blocks). X is staged in LDS as bf16 hi/lo per step; each lane
+// loads its weight fragments straight from HBM (8 int8 per 16-row tile per
+// block). XCD-aware order: the token tiles that share a weight tile are
+// dispatched to the same XCD, so the weight tile is fetched into one L2.
+// MFMA 16x16x32 operand layout: A[i][k] in lane i + 16*(k/8), element k%8;
+// B[k][j] in lane j + 16*(k/8); D[i][j] in lane j + 16*(i/4), element i%4.
 // ---------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(TPB) k_gemm_q8_tiled(const float *X, const int8_t *qs,
-                                                       const uint16_t *d, float *Y, uint32_t N,
-                                                       uint32_t M, uint32_t K) {
-    __shared__ float xt[64][33];
-    __shared__ float wt[64][33];
-    const uint32_t n0 = blockIdx.y * 64, m0 = blockIdx.x * 64, t = threadIdx.x;
-    const uint32_t tn = t / 16, tm = t % 16;      // each thread: 4x4 outputs
-    float acc[4][4] = {};
-    const uint32_t nbl = K / 32;
-    for (uint32_t b = 0; b < nbl; b++) {
-        for (uint32_t e = t; e < 64 * 32; e += TPB) {
-            const uint32_t r = e / 32, c = e % 32;
-            xt[r][c] = (n0 + r < N) ? X[(size_t)(n0 + r) * K + b * 32 + c] : 0.0f;
-            wt[r][c] = (m0 + r < M) ? (float)qs[(size_t)(m0 + r) * K + b * 32 + c] : 0.0f;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint16_t bf16_bits_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);     // round to nearest even (finite inputs)
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16_to_f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+#define GM_TN 64    // tokens per workgroup tile
+#define GM_TM 128   // weight rows per workgroup tile
+#define GM_KS 64    // K per step
+#define GM_LD (GM_KS + 8)   // padded LDS row (bf16 elements)
+
+template <int EPI>
+__global__ void __launch_bounds__(TPB) k_gemm_q8_mfma(const float *X, const int8_t *qs, const uint16_t *d,
+                                                      float *Y, uint32_t N, uint32_t M, uint32_t K,
+                                                      uint32_t ldx, uint32_t ldy) {
+    __shared__ uint16_t xhi[GM_TN * GM_LD];
+    __shared__ uint16_t xlo[GM_TN * GM_LD];
+    const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
+    // XCD-aware tile order: workgroup b runs on XCD b % 8; keep all token
+    // tiles of one weight tile on one XCD.
+    const uint32_t b = blockIdx.x, xcd = b & 7, qq = b >> 3;
+    const uint32_t mt_id = xcd + 8 * (qq / nb), nt_id = qq % nb;
+    if (mt_id >= mb) return;
+    const uint32_t n0 = nt_id * GM_TN, m0 = mt_id * GM_TM;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t wn = wave & 1, wm = wave >> 1;
+    const uint32_t li = lane & 15, lg = lane >> 4;
+    const uint32_t nbl = K >> 5;
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    // weight rows this lane feeds (B operand column j = li of each 16-row tile)
+    const int8_t *wrow[4];
+    const uint16_t *drow[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t m = min(m0 + wm * 64 + c * 16 + li, M - 1);
+        wrow[c] = qs + (size_t)m * K;
+        drow[c] = d + (size_t)m * nbl;
+    }
+    for (uint32_t k0 = 0; k0 < K; k0 += GM_KS) {
+        const uint32_t nblk = min(2u, (K - k0) >> 5);
+        // stage X[n0 .. n0+64][k0 .. k0+64] as bf16 hi/lo: 16 floats per thread
+        {
+            const uint32_t r = t >> 2, c0 = (t & 3) * 16;
+            const uint32_t n = n0 + r;
+#pragma unroll
+            for (int e = 0; e < 16; e += 4) {
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (n < N && k0 + c0 + e < K) v = *(const float4 *)(X + (size_t)n * ldx + k0 + c0 + e);
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const uint16_t h = bf16_bits_rne(vv[u]);
+                    xhi[r * GM_LD + c0 + e + u] = h;
+                    xlo[r * GM_LD + c0 + e + u] = bf16_bits_rne(vv[u] - bf16_to_f(h));
+                }
+            }
         }
         __syncthreads();
-        float part[4][4] = {};
-        for (uint32_t c = 0; c < 32; c++) {
+        for (uint32_t blk = 0; blk < nblk; blk++) {
+            const uint32_t kb = k0 + blk * 32;
+            bf16x8 wf[4];
+            float ds[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int c = 0; c < 4; c++) {
+                const uint2 raw = *(const uint2 *)(wrow[c] + kb + lg * 8);
+                u16x8 w;
 #pragma unroll
-                for (int j = 0; j < 4; j++) part[i][j] = fmaf(xt[tn * 4 + i][c], wt[tm * 4 + j][c], part[i][j]);
-        }
+                for (int e = 0; e < 4; e++) {
+                    w[e] = bf16_bits_rne((float)(int8_t)(raw.x >> (8 * e)));
+                    w[4 + e] = bf16_bits_rne((float)(int8_t)(raw.y >> (8 * e)));
+                }
+                wf[c] = __builtin_bit_cast(bf16x8, w);
+                ds[c] = h2f(drow[c][kb >> 5]);
+            }
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t m = m0 + tm * 4 + j;
-            const float dd = (m < M) ? h2f(d[(size_t)m * nbl + b]) : 0.0f;
+            for (int a = 0; a < 2; a++) {
+                const uint32_t row = wn * 32 + a * 16 + li;
+                const bf16x8 ah = __builtin_bit_cast(bf16x8, *(const u16x8 *)(xhi + row * GM_LD + blk * 32 + lg * 8));
+                const bf16x8 al = __builtin_bit_cast(bf16x8, *(const u16x8 *)(xlo + row * GM_LD + blk * 32 + lg * 8));
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[i][j] = fmaf(dd, part[i][j], acc[i][j]);
+                for (int c = 0; c < 4; c++) {
+                    f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[c], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[c], p, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[a][c][e] = fmaf(ds[c], p[e], acc[a][c][e]);
+                }
+            }
         }
         __syncthreads();
     }
+    // epilogue: lane holds D[i = 4*lg + e][j = li] of each tile
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int a = 0; a < 2; a++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t n = n0 + tn * 4 + i, m = m0 + tm * 4 + j;
-            if (n < N && m < M) Y[(size_t)n * M + m] = acc[i][j];
-        }
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t n = n0 + wn * 32 + a * 16 + lg * 4 + e;
+                const uint32_t m = m0 + wm * 64 + c * 16 + li;
+                const float v = acc[a][c][e];
+                if (EPI == SGK_EPI_SWIGLU) {
+                    const float up = __shfl_xor(v, 1, 64);    // column m+1 lives in lane li^1
+                    if (!(li & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(v) * up;
+                } else if (n < N && m < M) {
+                    if (EPI == SGK_EPI_ADD) Y[(size_t)n * ldy + m] += v;
+                    else Y[(size_t)n * ldy + m] = v;
+                }
+            }
+}
+
+// f32-weight GEMM for small test models (VALU, 16x16 outputs per workgroup).
+template <int EPI>
+__global__ void __launch_bounds__(TPB) k_gemm_f32(const float *X, const float *W, float *Y, uint32_t N,
+                                                  uint32_t M, uint32_t K, uint32_t ldx, uint32_t ldy) {
+    const uint32_t n = blockIdx.y * 16 + (threadIdx.x >> 4), m = blockIdx.x * 16 + (threadIdx.x & 15);
+    float s = 0.f;
+    if (n < N && m < M)
+        for (uint32_t k = 0; k < K; k++) s = fmaf(X[(size_t)n * ldx + k], W[(size_t)m * K + k], s);
+    if (EPI == SGK_EPI_SWIGLU) {
+        const float up = __shfl_xor(s, 1, 64);
+        if (!(m & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(s) * up;
+    } else if (n < N && m < M) {
+        if (EPI == SGK_EPI_ADD) Y[(size_t)n * ldy + m] += s;
+        else Y[(size_t)n * ldy + m] = s;
+    }
+}
+
+extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
+    if (!a->N || !a->M || !a->K) return hipSuccess;
+    if (a->epi == SGK_EPI_SWIGLU && (a->M & 1)) return hipErrorInvalidValue;
+    if (a->qs) {
+        if (a->K % 32) return hipErrorInvalidValue;
+        const uint32_t nb = (a->N + GM_TN - 1) / GM_TN, mb = (a->M + GM_TM - 1) / GM_TM;
+        const uint32_t grid = 8 * nb * ((mb + 7) / 8);
+#define GQ(E) hipLaunchKernelGGL(k_gemm_q8_mfma<E>, dim3(grid), dim3(TPB), 0, s, a->X, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldx, a->ldy)
+        if (a->epi == SGK_EPI_ADD) GQ(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GQ(SGK_EPI_SWIGLU); else GQ(SGK_EPI_STORE);
+#undef GQ
+    } else {
+        dim3 grid((a->M + 15) / 16, (a->N + 15) / 16);
+#define GF(E) hipLaunchKernelGGL(k_gemm_f32<E>, grid, dim3(TPB), 0, s, a->X, a->wf, a->Y, a->N, a->M, a->K, a->ldx, a->ldy)
+        if (a->epi == SGK_EPI_ADD) GF(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GF(SGK_EPI_SWIGLU); else GF(SGK_EPI_STORE);
+#undef GF
+    }
+    return hipGetLastError();
 }
 
 extern "C" hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, float *Y,
                                   uint32_t N, uint32_t M, uint32_t K, hipStream_t s) {
-    if (!N || !M || K % 32) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gemm_q8_tiled, dim3((M + 63) / 64, (N + 63) / 64), dim3(TPB), 0, s, X, qs, d, Y,
-                       N, M, K);
-    return hipGetLastError();
+    sgk_gemm_args a = {X, qs, d, NULL, Y, N, M, K, K, M, SGK_EPI_STORE};
+    return sgk_gemm(&a, s);
 }

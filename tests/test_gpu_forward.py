@@ -36,12 +36,15 @@ def test_mini_fwd_gguf_f32_vs_mlx_and_oracle(gpu):
     gpu.load_model(gm.model)
     gpu.state_new(len(ids))
     got = np.stack([gpu.forward(t, p) for p, t in enumerate(ids)])
-    assert np.abs(got - want).max() < 1e-4
-    assert (got.argmax(1) == want.argmax(1)).all()
-    rm = O.RefModel(O.oracle(), gm.model, len(ids))
-    orc = np.stack([rm.forward(t, p) for p, t in enumerate(ids)])
+    # The GPU keeps K/V in f16 (the reference GPU path's default, surge.h:1179-1191);
+    # against the oracle with the same f16 K/V rounding everything else is fp32 vs double.
+    rm = O.RefModel(O.oracle(), gm.model, len(ids), kv_f16=True)
+    orc16 = np.stack([rm.forward(t, p) for p, t in enumerate(ids)])
     rm.close()
-    assert rel(got, orc) < 1e-5
+    assert rel(got, orc16) < 1e-5
+    # against mlx (f32 K/V) the f16 storage costs ~1e-4: the 1e-3 kernel bar applies
+    assert np.abs(got - want).max() < 1e-3 * np.abs(want).max()
+    assert (got.argmax(1) == want.argmax(1)).all()
     gm.close()
 
 
@@ -62,7 +65,7 @@ def test_small_q8_hybrid_per_position_vs_oracle(gpu, small):
     rng = np.random.default_rng(0)
     ids = rng.integers(0, SMALL["vocab"], 520).tolist()
     gpu.state_reset()
-    rm = O.RefModel(O.oracle(), small.model, 600)
+    rm = O.RefModel(O.oracle(), small.model, 600, kv_f16=True)
     worst = 0.0
     for p, t in enumerate(ids):
         g = gpu.forward(t, p)
