@@ -105,7 +105,7 @@ def gemv_roofline(gpu, cfg, reps=3):
     gbs = algo / avg_s / 1e9
     return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
-                kernel="k_gemv_q8<4,PRO_RMS,EPI_SWIGLU> (gate|up %dx%d)" % (rows, cols),
+                kernel="k_gemv_q8 gate|up %dx%d (RMSNorm prologue, SwiGLU epilogue)" % (rows, cols),
                 avg_us=round(avg_s * 1e6, 2), algo_bytes=int(algo), launches=reps * L)
 
 
