@@ -109,6 +109,32 @@ def gemv_roofline(gpu, cfg, reps=3):
                 avg_us=round(avg_s * 1e6, 2), algo_bytes=int(algo), launches=reps * L)
 
 
+def calib_copy(nbytes):
+    """One plain device-to-device copy of known size: rocprofv3 counter runs
+    scale the GEMV's FETCH_SIZE/WRITE_SIZE by what the copy kernel reads."""
+    h = C.CDLL("libamdhip64.so")
+    a, b = C.c_void_p(), C.c_void_p()
+    assert h.hipMalloc(C.byref(a), C.c_size_t(nbytes)) == 0 and h.hipMalloc(C.byref(b), C.c_size_t(nbytes)) == 0
+    assert h.hipMemcpy(b, a, C.c_size_t(nbytes), 3) == 0          # hipMemcpyDeviceToDevice
+    assert h.hipDeviceSynchronize() == 0
+    h.hipFree(a)
+    h.hipFree(b)
+
+
+def measured_traffic(algo_bytes):
+    """HBM bytes per gate/up GEMV launch from the committed rocprofv3 counter
+    summary (profiles/gemv_gate_up_traffic.json: FETCH_SIZE + WRITE_SIZE per
+    dispatch, calibrated against a plain copy kernel), or None if absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_gate_up_traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        d = json.load(open(path))
+        return int(d["bytes_per_dispatch"])
+    except (ValueError, KeyError):
+        return None
+
+
 def cpu_baseline(syn, cfg, ctx, budget_s=15.0):
     """Reference CPU path on this host: per-op timings at the real shapes,
     composed to one decode token (a full scalar token takes tens of seconds)."""
@@ -177,6 +203,8 @@ def main():
     ap.add_argument("--shape", default="27b", choices=["27b", "2b"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--chunk", type=int, default=512, help="prefill chunk (tokens)")
+    ap.add_argument("--calib-mb", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB (counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {a.gpus}); this build has no "
@@ -212,6 +240,9 @@ def main():
     bytes_tok, parts = step_bytes(cfg, a.ctx + a.warmup + a.steps // 2)
     decode_gbs = bytes_tok * tps / 1e9
     roof = gemv_roofline(gpu, cfg)
+    if a.calib_mb:
+        calib_copy(a.calib_mb << 20)
+    roof["traffic"] = measured_traffic(roof["algo_bytes"])
     log(f"gate/up GEMV: {roof['avg_us']} us/launch, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
     gpu.close()
     cpu = None

@@ -201,6 +201,22 @@ sg_err sg_gpu_run_attn_splitk_partial_gqa(sg_gpu *g, void *q, void *k, void *v,
 sg_err sg_gpu_run_attn_splitk_combine(sg_gpu *g, void *m, void *s, void *acc,
                                       void *out, const uint32_t params[8]);
 
+/* The online-softmax arm (surge.h:974-1050): the partial kernel here is the
+ * online form already, so these are the same kernel and the same counts. */
+sg_err sg_gpu_run_attn_splitk_partial_gqa_online(sg_gpu *g, void *q, void *k, void *v,
+                                                 void *m, void *s, void *acc,
+                                                 const uint32_t params[8]);
+bool sg_gpu_splitk_online_selected(const sg_gpu *g, uint32_t n_heads,
+                                   uint32_t n_kv_heads, uint32_t seq);
+uint64_t sg_gpu_splitk_online_dispatches(const sg_gpu *g);
+
+/* Causal chunk attention (surge.h:787-788): q f32 [n, n_heads, q_stride];
+ * k, v f16 [base+n, n_kv, hd] already holding base+n positions; out f32
+ * [n, n_heads, hd]; token t (position base+t) attends over 0..base+t.
+ * p: [0]=n_heads [1]=n_kv [2]=hd [3]=base [4]=n [5]=q_stride [6]=scale bits. */
+sg_err sg_gpu_run_attn_prefill(sg_gpu *g, void *q, void *k, void *v, void *out,
+                               const uint32_t params[8]);
+
 /* Split-count policy (surge.h:1020-1106), re-derived for 256 CUs. */
 uint32_t sg_gpu_splitk_n_splits(uint32_t seq);
 uint32_t sg_gpu_splitk_gqa_n_splits(uint32_t seq);
@@ -217,6 +233,24 @@ void sg_gpu_splitk_dispatch_counts(const sg_gpu *g, uint64_t *per_head, uint64_t
  * reference's k_delta_multi (kernels.metal:764-805). */
 sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *gates,
                               const uint32_t params[8]);
+/* Prefill chunk hooks (surge.h:1111-1142), reference layouts:
+ *   conv1d_chunk: x [n_tok, ch], w [ch, ksize], out [n_tok, ch], state
+ *     [ksize-1, ch] oldest-first in/out; no activation. p: [0]=ch [1]=ksize [2]=n_tok
+ *   delta_gates_chunk: a, b [n_tok, n], gates [n_tok, 2n] (beta | decay),
+ *     adt [ssm_a(n) | dt_bias(n)]. p: [0]=n [1]=neg_exp [2]=n_tok
+ *   delta_chunk: S [n_v, dv, dk] in/out, qkv [n_tok, conv_dim] (normalised
+ *     q, k), out [n_tok, value_dim], gates [n_tok, 2*n_v].
+ *     p: [0]=dk [1]=dv [2]=n_v [3]=n_k [4]=key_dim [5]=tiled [6]=n_tok [7]=conv_dim
+ *   rmsnorm_gated_chunk: y, z, out [n_tok, heads*dv], w [dv].
+ *     p: [0]=dv [1]=heads [2]=eps bits [3]=n_tok */
+sg_err sg_gpu_run_conv1d_chunk(sg_gpu *g, void *x, void *w, void *out, void *state,
+                               const uint32_t params[8]);
+sg_err sg_gpu_run_delta_gates_chunk(sg_gpu *g, void *a, void *b, void *gates, void *adt,
+                                    const uint32_t params[8]);
+sg_err sg_gpu_run_delta_chunk(sg_gpu *g, void *S, void *qkv, void *out, void *gates,
+                              const uint32_t params[8]);
+sg_err sg_gpu_run_rmsnorm_gated_chunk(sg_gpu *g, void *y, void *z, void *out, void *w,
+                                      const uint32_t params[8]);
 
 /* Decode (surge.h:1260-1274). */
 sg_err sg_gpu_load_model(sg_gpu *g, const sg_model *m);

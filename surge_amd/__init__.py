@@ -103,6 +103,14 @@ _SIGS = {
     "sg_gpu_run_attn_splitk_partial_gqa": (SgErr, [C.c_void_p] * 7 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_run_attn_splitk_combine": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_run_delta_multi": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_run_conv1d_chunk": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_run_delta_gates_chunk": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_run_delta_chunk": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_run_rmsnorm_gated_chunk": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_run_attn_prefill": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_run_attn_splitk_partial_gqa_online": (SgErr, [C.c_void_p] * 7 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_splitk_online_dispatches": (C.c_uint64, [C.c_void_p]),
+    "sg_gpu_prefill_segments": (C.c_uint64, [C.c_void_p]),
     "sg_gpu_splitk_n_splits": (C.c_uint32, [C.c_uint32]),
     "sg_gpu_splitk_gqa_n_splits": (C.c_uint32, [C.c_uint32]),
     "sg_gpu_load_model": (SgErr, [C.c_void_p, C.POINTER(SgModel)]),
@@ -246,6 +254,11 @@ class Gpu:
     def delta_multi(self, S, qkv, out, gates, p):
         check(lib().sg_gpu_run_delta_multi(self.handle, S.handle, qkv.handle, out.handle,
                                            gates.handle, params(p)))
+
+    def run4(self, entry: str, a, b, c, d, p):
+        """Any four-buffer one-shot: sg_gpu_run_<entry>(g, a, b, c, d, params)."""
+        check(getattr(lib(), "sg_gpu_run_" + entry)(self.handle, a.handle, b.handle, c.handle, d.handle,
+                                                       params(p)))
 
     # ---- decode
     def load_model(self, model_ptr):

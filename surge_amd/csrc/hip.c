@@ -599,6 +599,119 @@ sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *ga
 }
 
 /* ---------------------------------------------------------------------
+ * prefill per-op hooks (surge.h:787-800, 1133-1142): the chunk kernels the
+ * prefill path runs, one synchronous call each, with the reference's
+ * argument layouts and params.
+ * --------------------------------------------------------------------- */
+
+sg_err sg_gpu_run_conv1d_chunk(sg_gpu *g, void *x, void *w, void *out, void *state, const uint32_t p[8]) {
+    if (!g || !x || !w || !out || !state || !p) return (sg_err){"gpu: conv1d_chunk got a NULL argument"};
+    uint32_t ch = p[0], ks = p[1], n = p[2];
+    if (!ch || ks < 1 || ks > 4 || !n) return (sg_err){"gpu: conv1d_chunk: bad shape (ksize 1..4)"};
+    sg_err e;
+    uint64_t xb = (uint64_t)n * ch * 4;
+    if (sg_failed(e = need(x, xb, "x")) || sg_failed(e = need(w, (uint64_t)ch * ks * 4, "w")) ||
+        sg_failed(e = need(out, xb, "out")) || sg_failed(e = need(state, (uint64_t)(ks - 1) * ch * 4 + (ks == 1 ? 4 : 0), "state")))
+        return e;
+    if (overlap(out, x) || overlap(out, w) || overlap(out, state)) return (sg_err){"gpu: conv1d_chunk: out overlaps an input"};
+    void *ins[4] = {x, w, out, state}, *outs[2] = {out, state};
+    if (sg_failed(e = push(ins, 4))) return e;
+    return finish(g, sgk_conv1d_chunk(DEV(x), DEV(w), DEV(out), DEV(state), ch, ks, n, g->stream), outs, 2);
+}
+
+sg_err sg_gpu_run_delta_gates_chunk(sg_gpu *g, void *a, void *b, void *gates, void *adt, const uint32_t p[8]) {
+    if (!g || !a || !b || !gates || !adt || !p) return (sg_err){"gpu: delta_gates_chunk got a NULL argument"};
+    uint32_t n = p[0], n_tok = p[2];
+    if (!n || !n_tok) return (sg_err){"gpu: delta_gates_chunk: bad shape"};
+    sg_err e;
+    uint64_t ab = (uint64_t)n * n_tok * 4;
+    if (sg_failed(e = need(a, ab, "a")) || sg_failed(e = need(b, ab, "b")) ||
+        sg_failed(e = need(gates, 2 * ab, "gates")) || sg_failed(e = need(adt, (uint64_t)2 * n * 4, "adt"))) return e;
+    void *ins[3] = {a, b, adt}, *outs[1] = {gates};
+    if (sg_failed(e = push(ins, 3))) return e;
+    return finish(g, sgk_delta_gates_chunk(DEV(a), DEV(b), DEV(gates), DEV(adt), n, p[1] != 0, n_tok, g->stream),
+                  outs, 1);
+}
+
+sg_err sg_gpu_run_delta_chunk(sg_gpu *g, void *S, void *qkv, void *out, void *gates, const uint32_t p[8]) {
+    if (!g || !S || !qkv || !out || !gates || !p) return (sg_err){"gpu: delta_chunk got a NULL argument"};
+    uint32_t dk = p[0], dv = p[1], nv = p[2], nk = p[3], kd = p[4], n_tok = p[6], cd = p[7];
+    if (!dk || !dv || !nv || !nk || nv % nk || kd != nk * dk || cd < 2 * kd + nv * dv || !n_tok)
+        return (sg_err){"gpu: delta_chunk: bad shape"};
+    if (dk != 32 && dk != 64 && dk != 128 && dk != 256) return (sg_err){"gpu: delta_chunk: dk must be 32, 64, 128 or 256"};
+    sg_err e;
+    if (sg_failed(e = need(S, (uint64_t)nv * dv * dk * 4, "S")) || sg_failed(e = need(qkv, (uint64_t)n_tok * cd * 4, "qkv")) ||
+        sg_failed(e = need(out, (uint64_t)n_tok * nv * dv * 4, "out")) ||
+        sg_failed(e = need(gates, (uint64_t)n_tok * 2 * nv * 4, "gates"))) return e;
+    void *ins[4] = {S, qkv, gates, out}, *outs[2] = {S, out};
+    if (sg_failed(e = push(ins, 4))) return e;
+    sgk_gdn d = {0};
+    d.S = DEV(S); d.y = DEV(out); d.n_k = nk; d.n_v = nv; d.dk = dk; d.dv = dv; d.conv_dim = cd; d.tiled = p[5] != 0;
+    return finish(g, sgk_delta_scan(&d, DEV(qkv), cd, n_tok, DEV(gates), g->stream), outs, 2);
+}
+
+sg_err sg_gpu_run_rmsnorm_gated_chunk(sg_gpu *g, void *y, void *z, void *out, void *w, const uint32_t p[8]) {
+    if (!g || !y || !z || !out || !w || !p) return (sg_err){"gpu: rmsnorm_gated_chunk got a NULL argument"};
+    uint32_t dv = p[0], nh = p[1], n_tok = p[3];
+    if (!dv || !nh || !n_tok) return (sg_err){"gpu: rmsnorm_gated_chunk: bad shape"};
+    sg_err e;
+    uint64_t nb = (uint64_t)n_tok * nh * dv * 4;
+    if (sg_failed(e = need(y, nb, "y")) || sg_failed(e = need(z, nb, "z")) || sg_failed(e = need(out, nb, "out")) ||
+        sg_failed(e = need(w, (uint64_t)dv * 4, "w"))) return e;
+    void *ins[3] = {y, z, w}, *outs[1] = {out};
+    if (sg_failed(e = push(ins, 3))) return e;
+    return finish(g, sgk_rmsnorm_gated_rows(DEV(y), DEV(z), nh * dv, DEV(w), DEV(out), dv, nh, n_tok, fbits(p[2]),
+                                            g->stream), outs, 1);
+}
+
+/* Causal chunk attention (surge.h:787-788): query token t (position base+t)
+ * over cache positions 0..base+t, through the split-K kernels with the
+ * prefill split policy. */
+sg_err sg_gpu_run_attn_prefill(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8]) {
+    if (!g || !q || !k || !v || !out || !p) return (sg_err){"gpu: attn_prefill got a NULL argument"};
+    uint32_t pp[8] = {p[0], p[1], p[2], 0, p[5], 0, 1, 0};
+    sg_err e = attn_check(pp, false);
+    if (sg_failed(e)) return e;
+    uint32_t nh = p[0], nkv = p[1], hd = p[2], base = p[3], n = p[4], qs = p[5];
+    if (!n) return (sg_err){"gpu: attn_prefill: n is zero"};
+    uint64_t kvb = (uint64_t)(base + n) * nkv * hd * 2;
+    if (sg_failed(e = need(q, (uint64_t)n * nh * qs * 4, "q")) || sg_failed(e = need(k, kvb, "k")) ||
+        sg_failed(e = need(v, kvb, "v")) || sg_failed(e = need(out, (uint64_t)n * nh * hd * 4, "out"))) return e;
+    uint64_t ah = (uint64_t)n * nh * SGK_PREFILL_SPLITS;
+    uint64_t steps_b = ((uint64_t)n * sizeof(sgk_step) + 255) / 256 * 256;
+    void *t;
+    if (sg_failed(e = scratch(g, steps_b + ah * (2 + hd) * 4, &t))) return e;
+    sgk_step *hs = malloc((uint64_t)n * sizeof *hs);
+    if (!hs) return (sg_err){"gpu: out of host memory"};
+    for (uint32_t z = 0; z < n; z++) { hs[z].token = 0; hs[z].pos = base + z; }
+    hipError_t he = hipMemcpy(t, hs, (uint64_t)n * sizeof *hs, hipMemcpyHostToDevice);
+    free(hs);
+    if (he != hipSuccess) return (sg_err){"gpu: attn_prefill: descriptor upload failed"};
+    void *ins[3] = {q, k, v}, *outs[1] = {out};
+    if (sg_failed(e = push(ins, 3))) return e;
+    float *mm = (float *)((char *)t + steps_b), *ss = mm + ah, *aa = ss + ah;
+    sgk_attn A = {0};
+    A.q = DEV(q); A.kc = DEV(k); A.vc = DEV(v); A.m = mm; A.s = ss; A.acc = aa; A.out = DEV(out); A.steps = t;
+    A.n_heads = nh; A.n_kv = nkv; A.hd = hd; A.q_stride = qs; A.q_tok = nh * qs; A.out_tok = nh * hd;
+    A.max_splits = SGK_PREFILL_SPLITS; A.ntok = n; A.scale = fbits(p[6]); A.prefill = 1;
+    he = sgk_attn_partial(&A, g->stream);
+    if (he == hipSuccess) he = sgk_attn_combine(&A, g->stream);
+    return finish(g, he, outs, 1);
+}
+
+/* The online-softmax arm (surge.h:974-1050). The partial kernel here IS the
+ * online form (running max/sum/acc rescaled across 32-key tiles), so the
+ * online entry points are the same kernel. */
+sg_err sg_gpu_run_attn_splitk_partial_gqa_online(sg_gpu *g, void *q, void *k, void *v, void *m, void *s,
+                                                 void *acc, const uint32_t p[8]) {
+    return sg_gpu_run_attn_splitk_partial_gqa(g, q, k, v, m, s, acc, p);
+}
+bool sg_gpu_splitk_online_selected(const sg_gpu *g, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq) {
+    return sg_gpu_splitk_gqa_selected(g, n_heads, n_kv_heads, seq);
+}
+uint64_t sg_gpu_splitk_online_dispatches(const sg_gpu *g) { return g ? g->splitk_gqa_dispatches : 0; }
+
+/* ---------------------------------------------------------------------
  * model load
  * --------------------------------------------------------------------- */
 
@@ -972,7 +1085,14 @@ static sg_err step_checks(sg_gpu *g, const sg_model *m, int32_t token, uint32_t 
     return SG_OK;
 }
 
+static uint32_t n_attn_layers(const sg_gpu *g) {
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < g->cfg.n_layers; i++) n += g->ls[i].attn;
+    return n;
+}
+
 static sg_err launch_step(sg_gpu *g, int32_t token, uint32_t pos, bool greedy) {
+    g->splitk_gqa_dispatches += n_attn_layers(g);
     g->h_step->token = token;
     g->h_step->pos = pos;
     HIPCHK(hipMemcpyAsync(g->d_step, g->h_step, sizeof(sgk_step), hipMemcpyHostToDevice, g->stream), "step upload");
@@ -1033,6 +1153,7 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
     g->h_step->token = token;
     g->h_step->pos = pos;
     HIPCHK(hipMemcpyAsync(g->d_step, g->h_step, sizeof(sgk_step), hipMemcpyHostToDevice, g->stream), "step upload");
+    g->splitk_gqa_dispatches += (uint64_t)n_steps * n_attn_layers(g);
     for (uint32_t i = 0; i < n_steps; i++) {
         if (g->use_graph) {
             HIPCHK(hipGraphLaunch(g->g_greedy, g->stream), "graph launch");

@@ -142,6 +142,18 @@ hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s);
  * sgk_gdn_step, token by token. */
 hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t in_stride, uint32_t ntok,
                          hipStream_t s);
+/* The delta-rule scan alone: qkv rows [ntok][in_stride] hold normalised
+ * q | k | v; gates [ntok][2*n_v] = beta | decay (or NULL: computed from the
+ * b/a columns of a->in as in sgk_gdn_chunk). */
+hipError_t sgk_delta_scan(const sgk_gdn *a, const float *qkv, uint32_t in_stride, uint32_t ntok,
+                          const float *gates, hipStream_t s);
+/* Conv over a chunk with an oldest-first state [ksize-1][ch] in/out, no
+ * activation (the reference's k_conv1d_chunk contract). */
+hipError_t sgk_conv1d_chunk(const float *x, const float *w, float *out, float *state, uint32_t ch,
+                            uint32_t ksize, uint32_t ntok, hipStream_t s);
+/* beta/decay for every (token, head). */
+hipError_t sgk_delta_gates_chunk(const float *a, const float *b, float *gates, const float *adt,
+                                 uint32_t n, int neg_exp, uint32_t ntok, hipStream_t s);
 /* silu(z) * rmsnorm(y, w) per (value head, token); z rows at z_stride. */
 hipError_t sgk_rmsnorm_gated_rows(const float *y, const float *z, uint32_t z_stride, const float *w,
                                   float *out, uint32_t dv, uint32_t n_v, uint32_t ntok, float eps,

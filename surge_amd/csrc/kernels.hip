@@ -891,6 +891,16 @@ __global__ void __launch_bounds__(TPB) k_gdn_step(sgk_gdn a) {
     // the first value head mapped to hk, row block 0 (one writer per channel).
     const bool qk_writer = blockIdx.y == 0 && (a.tiled ? h < a.n_k : (h % (a.n_v / a.n_k)) == 0);
     const uint32_t nrows = min((uint32_t)GDN_ROWS, dv - j0);
+    // The state rows depend on nothing computed here: request them first so
+    // their latency overlaps the conv / norm prologue.
+    constexpr int RPW = GDN_ROWS / (TPB / 64);
+    float *Sh = a.S + (size_t)h * dv * dk;
+    float sr[RPW][drow<DK>::EPL];
+#pragma unroll
+    for (int u = 0; u < RPW; u++) {
+        const uint32_t r = wave + u * (TPB / 64);
+        if (r < nrows) row_load<DK>(sr[u], Sh + (size_t)(j0 + r) * dk, lane);
+    }
 
     // 1. causal conv + SiLU on the channels this workgroup needs.
     for (uint32_t e = t; e < 2 * dk + nrows; e += TPB) {
@@ -927,11 +937,14 @@ __global__ void __launch_bounds__(TPB) k_gdn_step(sgk_gdn a) {
     float beta, decay;
     gdn_gates(bb[h], aa[h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
     // 4. rank-1 update and readout, 4 rows per wave.
-    float *Sh = a.S + (size_t)h * dv * dk;
-    for (uint32_t r = wave; r < nrows; r += TPB / 64) {
-        const uint32_t j = j0 + r;
-        const float y = delta_row<DK>(Sh + (size_t)j * dk, qk + dk, qk, vv[r], beta, decay, lane);
-        if (lane == 0) a.y[(size_t)h * dv + j] = y;
+#pragma unroll
+    for (int u = 0; u < RPW; u++) {
+        const uint32_t r = wave + u * (TPB / 64);
+        if (r < nrows) {
+            const float y = delta_update<DK>(sr[u], qk + dk, qk, vv[r], beta, decay, lane);
+            row_store<DK>(sr[u], Sh + (size_t)(j0 + r) * dk, lane);
+            if (lane == 0) a.y[(size_t)h * dv + j0 + r] = y;
+        }
     }
 }
 
@@ -1070,7 +1083,7 @@ __global__ void __launch_bounds__(TPB) k_qk_norm_chunk(float *conv_out, uint32_t
 // writes each token's readout y.
 template <int DK>
 __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *conv_out, uint32_t in_stride,
-                                                     uint32_t ntok) {
+                                                     uint32_t ntok, const float *gates) {
     constexpr int EPL = drow<DK>::EPL, RPW = GDN_ROWS / (TPB / 64);
     const uint32_t h = blockIdx.x, j0 = blockIdx.y * GDN_ROWS, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t dv = a.dv, key_dim = a.n_k * DK, cd = a.conv_dim, vd = a.n_v * dv;
@@ -1086,7 +1099,12 @@ __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *con
         const float *cz = conv_out + (size_t)z * cd;
         const float *iz = a.in + (size_t)z * in_stride;
         float beta, decay;
-        gdn_gates(iz[cd + vd + h], iz[cd + vd + a.n_v + h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
+        if (gates) {
+            beta = gates[(size_t)z * 2 * a.n_v + h];
+            decay = gates[(size_t)z * 2 * a.n_v + a.n_v + h];
+        } else {
+            gdn_gates(iz[cd + vd + h], iz[cd + vd + a.n_v + h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
+        }
 #pragma unroll
         for (int u = 0; u < RPW; u++) {
             const uint32_t j = j0 + wave + u * (TPB / 64);
@@ -1137,14 +1155,72 @@ extern "C" hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t 
     hipLaunchKernelGGL(k_conv_chunk, dim3((a->conv_dim + TPB - 1) / TPB), dim3(TPB), 0, s, a->in, in_stride,
                        a->conv_w, a->ring, conv_out, a->step, ntok, a->conv_dim, a->ksize);
     hipLaunchKernelGGL(k_qk_norm_chunk, dim3(2 * a->n_k, ntok), dim3(TPB), 0, s, conv_out, a->conv_dim, a->n_k, a->dk);
+    return sgk_delta_scan(a, conv_out, in_stride, ntok, NULL, s);
+}
+
+extern "C" hipError_t sgk_delta_scan(const sgk_gdn *a, const float *qkv, uint32_t in_stride, uint32_t ntok,
+                                     const float *gates, hipStream_t s) {
+    if (!ntok || !a->n_v || !a->dv) return hipSuccess;
     dim3 grid(a->n_v, (a->dv + GDN_ROWS - 1) / GDN_ROWS);
     switch (a->dk) {
-    case 32: hipLaunchKernelGGL(k_delta_chunk<32>, grid, dim3(TPB), 0, s, *a, conv_out, in_stride, ntok); break;
-    case 64: hipLaunchKernelGGL(k_delta_chunk<64>, grid, dim3(TPB), 0, s, *a, conv_out, in_stride, ntok); break;
-    case 128: hipLaunchKernelGGL(k_delta_chunk<128>, grid, dim3(TPB), 0, s, *a, conv_out, in_stride, ntok); break;
-    case 256: hipLaunchKernelGGL(k_delta_chunk<256>, grid, dim3(TPB), 0, s, *a, conv_out, in_stride, ntok); break;
+    case 32: hipLaunchKernelGGL(k_delta_chunk<32>, grid, dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates); break;
+    case 64: hipLaunchKernelGGL(k_delta_chunk<64>, grid, dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates); break;
+    case 128: hipLaunchKernelGGL(k_delta_chunk<128>, grid, dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates); break;
+    case 256: hipLaunchKernelGGL(k_delta_chunk<256>, grid, dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates); break;
     default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+// Conv over a chunk with the reference's oldest-first state [ksize-1][ch]
+// (in and out), no activation: the per-op hook (kernels.metal:1111-1141).
+__global__ void k_conv1d_chunk_state(const float *x, const float *w, float *out, float *state, uint32_t ch,
+                                     uint32_t ksize, uint32_t ntok) {
+    const uint32_t c = blockIdx.x * TPB + threadIdx.x;
+    if (c >= ch) return;
+    const uint32_t keep = ksize - 1;
+    float st[3] = {0.f, 0.f, 0.f};
+    for (uint32_t j = 0; j < keep; j++) st[j] = state[(size_t)j * ch + c];
+    const float *wc = w + (size_t)c * ksize;
+    for (uint32_t z = 0; z < ntok; z++) {
+        const float cur = x[(size_t)z * ch + c];
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < keep; j++) acc = fmaf(wc[j], st[j], acc);
+        acc = fmaf(wc[keep], cur, acc);
+        for (uint32_t j = 0; j + 1 < keep; j++) st[j] = st[j + 1];
+        if (keep) st[keep - 1] = cur;
+        out[(size_t)z * ch + c] = acc;
+    }
+    for (uint32_t j = 0; j < keep; j++) state[(size_t)j * ch + c] = st[j];
+}
+
+extern "C" hipError_t sgk_conv1d_chunk(const float *x, const float *w, float *out, float *state, uint32_t ch,
+                                       uint32_t ksize, uint32_t ntok, hipStream_t s) {
+    if (!ch || !ntok) return hipSuccess;
+    if (ksize < 1 || ksize > 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_conv1d_chunk_state, dim3((ch + TPB - 1) / TPB), dim3(TPB), 0, s, x, w, out, state, ch,
+                       ksize, ntok);
+    return hipGetLastError();
+}
+
+// beta/decay for every (token, head): gates[z] = beta[n] | decay[n]
+// (kernels.metal:1154-1172); adt = ssm_a[n] | dt_bias[n].
+__global__ void k_delta_gates_chunk(const float *av, const float *bv, float *gates, const float *adt, uint32_t n,
+                                    int neg_exp, uint32_t ntok) {
+    const uint32_t i = blockIdx.x * TPB + threadIdx.x;
+    if (i >= n * ntok) return;
+    const uint32_t z = i / n, h = i % n;
+    float beta, decay;
+    gdn_gates(bv[i], av[i], adt[h], adt[n + h], neg_exp, &beta, &decay);
+    gates[(size_t)z * 2 * n + h] = beta;
+    gates[(size_t)z * 2 * n + n + h] = decay;
+}
+
+extern "C" hipError_t sgk_delta_gates_chunk(const float *a, const float *b, float *gates, const float *adt,
+                                            uint32_t n, int neg_exp, uint32_t ntok, hipStream_t s) {
+    if (!n || !ntok) return hipSuccess;
+    hipLaunchKernelGGL(k_delta_gates_chunk, dim3((n * ntok + TPB - 1) / TPB), dim3(TPB), 0, s, a, b, gates, adt,
+                       n, neg_exp, ntok);
     return hipGetLastError();
 }
 

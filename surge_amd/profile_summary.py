@@ -1,0 +1,104 @@
+"""Turns rocprofv3 output into the short text summaries kept under profiles/.
+
+  python -m surge_amd.profile_summary stats KERNEL_STATS_CSV --tokens N > summary.md
+      per-kernel calls, total/avg time and time per decode token from a
+      `rocprofv3 --kernel-trace --stats` run;
+  python -m surge_amd.profile_summary pmc COUNTER_CSV --counter FETCH_SIZE --calib-bytes B
+      per-kernel average of one counter (KiB per dispatch) from a
+      `rocprofv3 --pmc <counter>` run, and the same figure scaled into bytes by
+      the counter's reading for the largest plain copy kernel
+      (__amd_rocclr_copyBuffer) of known size B bytes in the same run;
+  python -m surge_amd.profile_summary trace KERNEL_TRACE_CSV --kernel NAME --last N
+      average duration of the last N dispatches of kernel NAME (prefix match)
+      from a `rocprofv3 --kernel-trace` run, next to the average over all of
+      its dispatches: bench.py times its GEMV roofline leg last, so the last
+      N dispatches are exactly the launches it timed with HIP events.
+"""
+import argparse
+import csv
+import json
+import sys
+from collections import defaultdict
+
+
+def short(name: str) -> str:
+    return name.split("(")[0].replace("void ", "")[:70]
+
+
+def stats(path, tokens):
+    rows = list(csv.DictReader(open(path)))
+    tot = sum(float(r["TotalDurationNs"]) for r in rows)
+    print("| kernel | calls | calls/token | avg us | total ms | ms/token | % |")
+    print("|---|---|---|---|---|---|---|")
+    for r in rows:
+        t = float(r["TotalDurationNs"])
+        print(f"| `{short(r['Name'])}` | {r['Calls']} | {int(r['Calls']) / tokens:.2f} | "
+              f"{float(r['AverageNs']) / 1e3:.2f} | {t / 1e6:.1f} | {t / tokens / 1e6:.4f} | {100 * t / tot:.1f} |")
+    print(f"\nTotal kernel time {tot / 1e6:.1f} ms over {tokens} tokens = {tot / tokens / 1e6:.3f} ms/token.")
+
+
+def pmc(path, counter, calib_bytes):
+    vals = defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        if r.get("Counter_Name", counter) != counter:
+            continue
+        vals[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    copies = vals.get("__amd_rocclr_copyBuffer", [])
+    ref = max(copies) if copies else 0.0
+    scale = calib_bytes / (ref * 1024.0) if ref else None
+    out = {}
+    print(f"| kernel | dispatches | avg {counter} (KiB) | bytes/dispatch (calibrated) |")
+    print("|---|---|---|---|")
+    for k, v in sorted(vals.items(), key=lambda kv: -sum(kv[1])):
+        avg = sum(v) / len(v)
+        b = avg * 1024.0 * scale if scale else None
+        out[short(k)] = {"dispatches": len(v), "avg_kib": avg, "bytes": b}
+        print(f"| `{short(k)}` | {len(v)} | {avg:.1f} | {b / 1e6:.2f} MB |" if b else
+              f"| `{short(k)}` | {len(v)} | {avg:.1f} | - |")
+    print(f"\nCalibration: largest __amd_rocclr_copyBuffer read {ref:.1f} KiB for a {calib_bytes} B copy "
+          f"(scale {scale:.4f})." if scale else "\nNo calibration copy found.")
+    return out, scale
+
+
+def trace(path, kernel, last):
+    durs = []
+    for r in csv.DictReader(open(path)):
+        if short(r["Kernel_Name"]).startswith(kernel):
+            durs.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    durs.sort()
+    if not durs:
+        print(f"no dispatches of {kernel}")
+        return None
+    tail = [d for _, d in durs[-last:]] if last else [d for _, d in durs]
+    all_avg = sum(d for _, d in durs) / len(durs) / 1e3
+    avg = sum(tail) / len(tail) / 1e3
+    print(f"`{kernel}`: {len(durs)} dispatches, average {all_avg:.2f} us; "
+          f"last {len(tail)} dispatches average {avg:.2f} us (min {min(tail) / 1e3:.2f}, max {max(tail) / 1e3:.2f}).")
+    return {"kernel": kernel, "dispatches": len(durs), "avg_us": all_avg, "last": len(tail), "last_avg_us": avg}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("mode", choices=["stats", "pmc", "trace"])
+    ap.add_argument("csv")
+    ap.add_argument("--tokens", type=int, default=1)
+    ap.add_argument("--counter", default="FETCH_SIZE")
+    ap.add_argument("--calib-bytes", type=float, default=0)
+    ap.add_argument("--json", default=None)
+    ap.add_argument("--kernel", default="k_gemv_q8<2, 1, 2, false>")
+    ap.add_argument("--last", type=int, default=0)
+    a = ap.parse_args()
+    if a.mode == "stats":
+        stats(a.csv, a.tokens)
+    elif a.mode == "trace":
+        out = trace(a.csv, a.kernel, a.last)
+        if a.json and out:
+            json.dump(out, open(a.json, "w"), indent=1)
+    else:
+        out, scale = pmc(a.csv, a.counter, a.calib_bytes)
+        if a.json:
+            json.dump({"counter": a.counter, "scale": scale, "kernels": out}, open(a.json, "w"), indent=1)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -404,3 +404,100 @@ def test_matmul_q8_prefill_gemm(gpu):
     gpu.run_op("k_matmul_q8", xb, wb, yb, [N, M, K])
     want = np.stack([oracle_matvec_q8(raw, np.ascontiguousarray(X[n * K:(n + 1) * K]), M, K) for n in range(N)])
     assert_close(yb.array.reshape(N, M), want)
+
+
+# ---------------------------------------------------------------- prefill chunk hooks
+
+def test_conv1d_chunk_threads_state(gpu):
+    rng = np.random.default_rng(21)
+    ch, ks, n = 2048, 4, 9
+    x = rng.standard_normal(n * ch).astype(np.float32)
+    w = rng.standard_normal(ch * ks).astype(np.float32)
+    st0 = rng.standard_normal((ks - 1) * ch).astype(np.float32)
+    xb, wb, ob, sb = gpu.buf(x), gpu.buf(w), gpu.buf(np.zeros(n * ch, np.float32)), gpu.buf(st0.copy())
+    gpu.run4("conv1d_chunk", xb, wb, ob, sb, [ch, ks, n])
+    st = st0.copy()
+    want = np.zeros(n * ch, np.float32)
+    for t in range(n):
+        xt = x[t * ch:(t + 1) * ch].copy()
+        O.oracle().sg_ref_conv1d_causal(fp(xt), fp(w), fp(st), fp(st), ch, ks)
+        want[t * ch:(t + 1) * ch] = xt
+    assert_close(ob.array, want)
+    assert np.array_equal(sb.array, st)
+
+
+def test_delta_gates_chunk(gpu):
+    rng = np.random.default_rng(22)
+    n, nt = 48, 5
+    a = rng.standard_normal(n * nt).astype(np.float32)
+    b = rng.standard_normal(n * nt).astype(np.float32)
+    adt = np.concatenate([-np.exp(rng.uniform(-1, 1, n)), rng.uniform(-0.5, 0.5, n)]).astype(np.float32)
+    ab, bb, gb, db = gpu.buf(a), gpu.buf(b), gpu.buf(np.zeros(2 * n * nt, np.float32)), gpu.buf(adt)
+    gpu.run4("delta_gates_chunk", ab, bb, gb, db, [n, 1, nt])
+    got = gb.array.reshape(nt, 2, n)
+    for z in range(nt):
+        for h in range(n):
+            i = z * n + h
+            beta = O.oracle().sg_ref_sigmoid(float(b[i]))
+            decay = O.oracle().sg_ref_delta_decay_neg_a(float(adt[h]), float(a[i]), float(adt[n + h]))
+            assert abs(got[z, 0, h] - beta) <= 1e-6 and abs(got[z, 1, h] - decay) <= 1e-5 * max(decay, 1e-30) + 1e-7
+
+
+def test_delta_chunk_scan_matches_token_loop(gpu):
+    rng = np.random.default_rng(23)
+    nv, nk, dk, dv, nt = 6, 2, 128, 64, 7
+    kd = nk * dk
+    cd = 2 * kd + nv * dv
+    S0 = (rng.standard_normal(nv * dv * dk) * 0.1).astype(np.float32)
+    qkv = (rng.standard_normal(nt * cd) * 0.1).astype(np.float32)
+    gates = np.concatenate([rng.uniform(0, 1, (nt, nv)), rng.uniform(0.5, 1, (nt, nv))], axis=1).astype(np.float32)
+    Sg, qb, ob, gb = gpu.buf(S0.copy()), gpu.buf(qkv), gpu.buf(np.zeros(nt * nv * dv, np.float32)), gpu.buf(gates)
+    gpu.run4("delta_chunk", Sg, qb, ob, gb, [dk, dv, nv, nk, kd, 1, nt, cd])
+    So, want = S0.copy(), np.zeros(nt * nv * dv, np.float32)
+    for z in range(nt):
+        row = qkv[z * cd:(z + 1) * cd]
+        for h in range(nv):
+            hk = h % nk
+            O.oracle().sg_ref_delta_step(fp(So[h * dv * dk:]), fp(np.ascontiguousarray(row[hk * dk:])),
+                                         fp(np.ascontiguousarray(row[kd + hk * dk:])),
+                                         fp(np.ascontiguousarray(row[2 * kd + h * dv:])), float(gates[z, h]),
+                                         float(gates[z, nv + h]), fp(want[(z * nv + h) * dv:]), dk, dv)
+    assert_close(ob.array, want)
+    assert_close(Sg.array, So)
+
+
+def test_rmsnorm_gated_chunk(gpu):
+    rng = np.random.default_rng(24)
+    dv, nh, nt = 128, 6, 3
+    y = rng.standard_normal(nt * nh * dv).astype(np.float32)
+    z = rng.standard_normal(nt * nh * dv).astype(np.float32)
+    w = rng.standard_normal(dv).astype(np.float32)
+    yb, zb, ob, wb = gpu.buf(y), gpu.buf(z), gpu.buf(np.zeros(nt * nh * dv, np.float32)), gpu.buf(w)
+    gpu.run4("rmsnorm_gated_chunk", yb, zb, ob, wb, [dv, nh, S.fbits(1e-6), nt])
+    want = np.zeros_like(y)
+    for i in range(nt * nh):
+        yy, zz = y[i * dv:(i + 1) * dv].copy(), z[i * dv:(i + 1) * dv].copy()
+        O.oracle().sg_ref_rmsnorm(fp(yy), fp(w), dv, 1e-6)
+        O.oracle().sg_ref_swiglu(fp(zz), fp(yy), dv)
+        want[i * dv:(i + 1) * dv] = zz
+    assert_close(ob.array, want)
+
+
+@pytest.mark.parametrize("base,n", [(0, 5), (37, 16), (2000, 9)])
+def test_attn_prefill_causal(gpu, base, n):
+    """Token t of the chunk (position base+t) attends over keys 0..base+t only."""
+    rng = np.random.default_rng(base + n)
+    nh, nkv, hd = 24, 4, 256
+    qs = 2 * hd
+    tot = base + n
+    q = rng.standard_normal(n * nh * qs).astype(np.float32)
+    k16, v16 = f16(rng, tot * nkv * hd), f16(rng, tot * nkv * hd)
+    qb, kb, vb = gpu.buf(q), gpu.buf(k16.view(np.uint16)), gpu.buf(v16.view(np.uint16))
+    ob = gpu.buf(np.zeros(n * nh * hd, np.float32))
+    gpu.run4("attn_prefill", qb, kb, vb, ob, [nh, nkv, hd, base, n, qs, S.fbits(1 / 16)])
+    kc, vc = k16.astype(np.float32), v16.astype(np.float32)
+    for t in range(n):
+        want = np.zeros(nh * hd, np.float32)
+        O.oracle().sg_ref_attn_decode(fp(np.ascontiguousarray(q[t * nh * qs:(t + 1) * nh * qs])), fp(kc), fp(vc),
+                                      nh, nkv, hd, base + t + 1, qs, np.float32(1 / 16), fp(want))
+        assert_close(ob.array[t * nh * hd:(t + 1) * nh * hd], want)
