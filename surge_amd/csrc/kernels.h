@@ -39,9 +39,10 @@ static inline uint32_t sgk_n_splits(uint32_t seq) {
     return n;
 }
 
-/* GEMV prologues (what is staged into LDS as the input vector) and epilogues
- * (what is done with each output row). */
-enum { SGK_PRO_NONE = 0, SGK_PRO_RMS = 1, SGK_PRO_RMS_GATED = 2 };
+/* GEMV prologues (what is staged into LDS as the input vector: x, or x*w with
+ * the RMS factor applied to each row sum) and epilogues (what is done with
+ * each output row). */
+enum { SGK_PRO_NONE = 0, SGK_PRO_RMS = 1 };
 enum { SGK_EPI_STORE = 0, SGK_EPI_ADD = 1, SGK_EPI_SWIGLU = 2 };
 
 typedef struct {
@@ -49,14 +50,12 @@ typedef struct {
     const uint16_t *d;      /* Q8: f16 scales [rows][cols/32] */
     const float *wf;        /* F32 weights [rows][cols] (when qs == NULL) */
     uint32_t rows, cols;
-    const float *x;         /* input vector [cols] */
-    const float *nw;        /* prologue norm weight ([cols], or [head] for gated) */
-    const float *z;         /* gated prologue: z [cols] */
+    const float *x;         /* input vector [cols], 16-byte aligned */
+    const float *nw;        /* PRO_RMS norm weight [cols], 16-byte aligned */
     float eps;
-    uint32_t head;          /* gated prologue: head width */
     float *y;               /* output [rows] (or [rows/2] for SWIGLU) */
     int pro, epi;
-    uint32_t tune_r, tune_blocks;   /* 0 = measured default; rows per wave, workgroups */
+    uint32_t tune_r, tune_blocks;   /* 0 = default; rows per wave (1/2/4), workgroups */
 } sgk_gemv;
 
 hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s);

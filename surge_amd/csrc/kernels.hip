@@ -78,42 +78,65 @@ __device__ __forceinline__ uint32_t dev_n_splits(uint32_t seq) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMV: input staging prologues
+// GEMV: input staging prologue
 // ---------------------------------------------------------------------------
 
+// Stage the input vector in LDS with 16-byte loads, all of a thread's loads in
+// flight before its first LDS store. PRO_RMS stages x*w and returns the RMS
+// factor 1/sqrt(mean(x^2) + eps) (ref.c:113-125) for the epilogue to apply to
+// each row sum: W(x*r*w) = r * W(x*w). Other prologues return 1. Needs x and w
+// 16-byte aligned (every buffer of this library is).
 template <int PRO>
-__device__ __forceinline__ void stage_x(const sgk_gemv &a, float *xs) {
-    __shared__ float red[4];
-    const uint32_t n = a.cols, t = threadIdx.x;
-    if (PRO == SGK_PRO_NONE) {
-        for (uint32_t i = t; i < n; i += TPB) xs[i] = a.x[i];
-    } else if (PRO == SGK_PRO_RMS) {
-        // x * (1/sqrt(mean(x^2) + eps)) * w  (ref.c:113-125)
-        float ss = 0.0f;
-        for (uint32_t i = t; i < n; i += TPB) { float v = a.x[i]; xs[i] = v; ss = fmaf(v, v, ss); }
-        ss = block_sum(ss, red);
-        const float r = 1.0f / sqrtf(ss / (float)n + a.eps);
-        for (uint32_t i = t; i < n; i += TPB) xs[i] = (xs[i] * r) * a.nw[i];
-    } else {
-        // silu(z) * rmsnorm(y, w) per head (ref.c:1322-1330)
-        float *rh = xs + n;
-        const uint32_t head = a.head, heads = n / head, lane = t & 63, w = t >> 6;
-        for (uint32_t i = t; i < n; i += TPB) xs[i] = a.x[i];
-        __syncthreads();
-        for (uint32_t h = w; h < heads; h += TPB / 64) {
-            float ss = 0.0f;
-            for (uint32_t j = lane; j < head; j += 64) { float v = xs[h * head + j]; ss = fmaf(v, v, ss); }
-            ss = wave_sum(ss);
-            if (lane == 0) rh[h] = 1.0f / sqrtf(ss / (float)head + a.eps);
+__device__ __forceinline__ float stage_x(const sgk_gemv &a, float *xs) {
+    __shared__ float red[TPB / 64];
+    const uint32_t n = a.cols, t = threadIdx.x, n4 = n >> 2;
+    const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.nw;
+    float4 *s4 = (float4 *)xs;
+    float ss = 0.0f;
+    // Loads in flight per thread: 4 of x, or 2 of x and 2 of w (keeps the
+    // prologue's registers below the main loop's).
+    constexpr uint32_t NS = PRO == SGK_PRO_RMS ? 2 : 4;
+#pragma unroll 1
+    for (uint32_t i0 = t; i0 < n4; i0 += NS * TPB) {
+        const uint32_t i1 = i0 + TPB, i2 = i0 + 2 * TPB, i3 = i0 + 3 * TPB;
+        float4 v0, v1, v2, v3, g0, g1;
+        v0 = x4[i0];
+        if (i1 < n4) v1 = x4[i1];
+        if (NS == 4 && i2 < n4) v2 = x4[i2];
+        if (NS == 4 && i3 < n4) v3 = x4[i3];
+        if (PRO == SGK_PRO_RMS) {
+            g0 = w4[i0];
+            if (i1 < n4) g1 = w4[i1];
         }
-        __syncthreads();
-        for (uint32_t i = t; i < n; i += TPB) {
-            const uint32_t h = i / head;
-            const float yn = (xs[i] * rh[h]) * a.nw[i - h * head];
-            xs[i] = silu(a.z[i]) * yn;
+#define SG_STAGE(V, G, I)                                                                \
+        if (I < n4) {                                                                    \
+            if (PRO == SGK_PRO_RMS) {                                                    \
+                ss = fmaf(V.x, V.x, ss); ss = fmaf(V.y, V.y, ss);                        \
+                ss = fmaf(V.z, V.z, ss); ss = fmaf(V.w, V.w, ss);                        \
+                V.x *= G.x; V.y *= G.y; V.z *= G.z; V.w *= G.w;                          \
+            }                                                                            \
+            s4[I] = V;                                                                   \
+        }
+        SG_STAGE(v0, g0, i0) SG_STAGE(v1, g1, i1)
+#undef SG_STAGE
+        if (NS == 4) {
+            if (i2 < n4) s4[i2] = v2;
+            if (i3 < n4) s4[i3] = v3;
         }
     }
+    for (uint32_t i = 4 * n4 + t; i < n; i += TPB) {       // cols % 4 tail (f32 test models)
+        float v = a.x[i];
+        if (PRO == SGK_PRO_RMS) { ss = fmaf(v, v, ss); v *= a.nw[i]; }
+        xs[i] = v;
+    }
+    if (PRO == SGK_PRO_RMS) {
+        ss = wave_sum(ss);
+        if ((t & 63) == 0) red[t >> 6] = ss;
+    }
     __syncthreads();
+    if (PRO != SGK_PRO_RMS) return 1.0f;
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    return 1.0f / sqrtf(tot / (float)n + a.eps);
 }
 
 template <int EPI>
@@ -146,13 +169,14 @@ __device__ __forceinline__ float dot16(const uint4 q, const float4 x0, const flo
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 GEMV. Persistent workgroups (a few per CU) walk row groups with a grid
-// stride, so the per-workgroup prologue (input staging, norm) is paid a few
-// times per CU rather than once per handful of rows. One wave owns R
-// consecutive output rows at a time; lane l streams 16-byte chunks l, l+64,
-// ... of each row (a chunk is half a Q8_0 block: 16 int8 and the block's f16
-// scale). The first row group's first chunks are requested before the
-// prologue runs, so HBM is busy while the input vector is staged.
+// Q8_0 GEMV, rows up to 8192 columns. Persistent 256-thread workgroups, as
+// many as are resident at once (never more, so none waits for a slot), walk
+// row groups with a grid stride; the grid is sized so every wave gets the same
+// number of row groups. One wave owns R consecutive output rows at a time;
+// lane l streams 16-byte chunks l, l+64, ... of each row (a chunk is half a
+// Q8_0 block: 16 int8 and the block's f16 scale). The first row group's first
+// chunks are requested before the prologue runs, so HBM is already busy while
+// the input vector is staged.
 // ---------------------------------------------------------------------------
 
 template <int R>
@@ -180,42 +204,34 @@ __device__ __forceinline__ void gemv_fma(float *acc, const gemv_chunk<R> &ch, co
     for (int r = 0; r < R; r++) acc[r] = fmaf(h2f(ch.d[r]), dot16(ch.q[r], a0, a1, a2, a3), acc[r]);
 }
 
-// x from LDS (staged) or, for long rows (XG), straight from global memory
-// through L1/L2 so the kernel needs no LDS and keeps full occupancy.
-template <int R, bool XG>
-__device__ __forceinline__ void gemv_fma_x(float *acc, const gemv_chunk<R> &ch, const float *xs,
-                                           const float *xg, uint32_t c) {
-    gemv_fma<R>(acc, ch, XG ? xg : xs, c);
-}
-
 // One row group of R rows: every chunk of the rows, two chunks per step, the
-// first chunk optionally already loaded (pre).
-template <int R, int EPI, bool PRE, bool XG>
+// first chunk optionally already loaded (pre). post scales each row sum.
+template <int R, int EPI, bool PRE>
 __device__ __forceinline__ void gemv_group(const sgk_gemv &a, const float *xs, uint32_t g, uint32_t lane,
-                                           const gemv_chunk<R> *pre) {
+                                           const gemv_chunk<R> *pre, float post) {
     const uint32_t cols = a.cols, nch = cols >> 4, r0 = g * R;
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
     uint32_t c = lane;
     if (PRE) {
-        if (c < nch) gemv_fma_x<R, XG>(acc, *pre, xs, a.x, c);
+        if (c < nch) gemv_fma<R>(acc, *pre, xs, c);
         c += 64;
     }
     for (; c + 64 < nch; c += 128) {
         gemv_chunk<R> ca, cb;
         gemv_load<R>(ca, a.qs, a.d, r0, a.rows, cols, c);
         gemv_load<R>(cb, a.qs, a.d, r0, a.rows, cols, c + 64);
-        gemv_fma_x<R, XG>(acc, ca, xs, a.x, c);
-        gemv_fma_x<R, XG>(acc, cb, xs, a.x, c + 64);
+        gemv_fma<R>(acc, ca, xs, c);
+        gemv_fma<R>(acc, cb, xs, c + 64);
     }
     if (c < nch) {
         gemv_chunk<R> ca;
         gemv_load<R>(ca, a.qs, a.d, r0, a.rows, cols, c);
-        gemv_fma_x<R, XG>(acc, ca, xs, a.x, c);
+        gemv_fma<R>(acc, ca, xs, c);
     }
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]) * post;
     if (EPI == SGK_EPI_SWIGLU) {
         // rows come in (gate, up) pairs: y[i] = silu(gate_i) * up_i
 #pragma unroll
@@ -229,7 +245,7 @@ __device__ __forceinline__ void gemv_group(const sgk_gemv &a, const float *xs, u
     }
 }
 
-template <int R, int PRO, int EPI, bool XG>
+template <int R, int PRO, int EPI>
 __global__ void __launch_bounds__(TPB) k_gemv_q8(sgk_gemv a) {
     extern __shared__ float xs[];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -237,21 +253,19 @@ __global__ void __launch_bounds__(TPB) k_gemv_q8(sgk_gemv a) {
     const uint32_t ngroups = (a.rows + R - 1) / R, gstride = gridDim.x * (TPB / 64);
     uint32_t g = blockIdx.x * (TPB / 64) + wave;
     const bool have = g < ngroups;
-    // The first chunk of this wave's first row group is requested before the
-    // prologue, so HBM is already busy while the input vector is staged.
     gemv_chunk<R> pre;
     if (have && lane < nch) gemv_load<R>(pre, a.qs, a.d, g * R, a.rows, a.cols, lane);
-    if (!XG) stage_x<PRO>(a, xs);
+    const float post = stage_x<PRO>(a, xs);
     if (!have) return;
-    gemv_group<R, EPI, true, XG>(a, xs, g, lane, &pre);
-    for (g += gstride; g < ngroups; g += gstride) gemv_group<R, EPI, false, XG>(a, xs, g, lane, nullptr);
+    gemv_group<R, EPI, true>(a, xs, g, lane, &pre, post);
+    for (g += gstride; g < ngroups; g += gstride) gemv_group<R, EPI, false>(a, xs, g, lane, nullptr, post);
 }
 
 // f32-weight GEMV (small test models only): one wave per row pair.
 template <int PRO, int EPI>
 __global__ void __launch_bounds__(TPB) k_gemv_f32(sgk_gemv a) {
     extern __shared__ float xs[];
-    stage_x<PRO>(a, xs);
+    const float post = stage_x<PRO>(a, xs);
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t ngroups = (a.rows + 1) / 2;
     for (uint32_t g = blockIdx.x * (TPB / 64) + wave; g < ngroups; g += gridDim.x * (TPB / 64)) {
@@ -262,8 +276,8 @@ __global__ void __launch_bounds__(TPB) k_gemv_f32(sgk_gemv a) {
             s0 = fmaf(w0[c], xs[c], s0);
             s1 = fmaf(w1[c], xs[c], s1);
         }
-        s0 = wave_sum(s0);
-        s1 = wave_sum(s1);
+        s0 = wave_sum(s0) * post;
+        s1 = wave_sum(s1) * post;
         if (lane == 0) {
             if (EPI == SGK_EPI_SWIGLU) {
                 if (r0 + 1 < a.rows) a.y[g] = silu(s0) * s1;
@@ -275,49 +289,231 @@ __global__ void __launch_bounds__(TPB) k_gemv_f32(sgk_gemv a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q8_0 GEMV for long rows (more than 8192 columns: the 27B down-projection,
+// 17408). One 1024-thread workgroup per CU stages x once in LDS (68 KB for
+// 17408 columns). Rows are dealt as a chip-wide contiguous front: in round t,
+// wave w of workgroup b takes row (t*16 + w)*G + b, so at any moment the chip
+// reads neighbouring rows. The rows left after the full rounds (fewer than
+// 16*G) go to workgroup b as base + i*G + b and each is split by chunk range
+// over S = 16/n of its waves; the S partial sums meet in LDS and are added in
+// part order, so results do not depend on timing. Each wave requests its next
+// batch of chunks before multiplying the current one.
+// ---------------------------------------------------------------------------
+
+#define LTPB 1024
+#define LW (LTPB / 64)
+#define LU 3                      // chunks per lane per batch
+
+struct long_task { uint32_t row, c0, c1, slot; };
+struct long_plan { uint32_t nch, F, nb, S, nbr, G, b, base; };
+
+// The k-th batch of wave w; false past the end. slot: LW*LW+ for a whole row,
+// else the LDS partial slot (i*LW + part).
+__device__ __forceinline__ bool long_task_at(const long_plan &p, uint32_t w, uint32_t k, long_task &t) {
+    const uint32_t nfull = p.F * p.nbr;
+    if (k < nfull) {
+        const uint32_t i = k / p.nbr, bb = k - i * p.nbr;
+        t.row = (i * LW + w) * p.G + p.b;
+        t.c0 = bb * 64 * LU;
+        t.c1 = min(t.c0 + 64 * LU, p.nch);
+        t.slot = 0xffffffffu;
+        return true;
+    }
+    k -= nfull;
+    if (p.nb == 0 || w >= p.nb * p.S) return false;
+    const uint32_t i = w / p.S, part = w - i * p.S;
+    const uint32_t pc0 = (uint32_t)((uint64_t)part * p.nch / p.S);
+    const uint32_t pc1 = (uint32_t)((uint64_t)(part + 1) * p.nch / p.S);
+    const uint32_t c0 = pc0 + k * 64 * LU;
+    if (c0 >= pc1) return false;
+    t.row = p.base + i * p.G + p.b;
+    t.c0 = c0;
+    t.c1 = min(c0 + 64 * LU, pc1);
+    t.slot = i * LW + part;
+    return true;
+}
+
+struct long_batch { uint4 q[LU]; uint16_t d[LU]; };
+
+__device__ __forceinline__ void long_load(long_batch &bt, const sgk_gemv &a, const long_task &t, uint32_t lane) {
+    const uint4 *q = (const uint4 *)(a.qs + (size_t)t.row * a.cols);
+    const uint16_t *dr = a.d + (size_t)t.row * (a.cols >> 5);
+#pragma unroll
+    for (int u = 0; u < LU; u++) {
+        const uint32_t c = t.c0 + lane + 64 * u;
+        if (c < t.c1) { bt.q[u] = ldnt(q + c); bt.d[u] = dr[c >> 1]; }
+    }
+}
+
+__device__ __forceinline__ float long_fma(const long_batch &bt, const float *xs, const long_task &t, uint32_t lane,
+                                          float acc) {
+#pragma unroll
+    for (int u = 0; u < LU; u++) {
+        const uint32_t c = t.c0 + lane + 64 * u;
+        if (c < t.c1) {
+            const float4 *xa = (const float4 *)(xs + c * 16);
+            acc = fmaf(h2f(bt.d[u]), dot16(bt.q[u], xa[0], xa[1], xa[2], xa[3]), acc);
+        }
+    }
+    return acc;
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(LTPB) k_gemv_q8_long(sgk_gemv a) {
+    extern __shared__ float lds[];
+    float *xs = lds, *part = lds + a.cols;          // part[LW * LW]
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    long_plan p;
+    p.G = gridDim.x;
+    p.b = blockIdx.x;
+    p.nch = a.cols >> 4;
+    p.F = a.rows / (LW * p.G);
+    p.base = p.F * LW * p.G;
+    const uint32_t urem = a.rows - p.base;
+    p.nb = urem > p.b ? (urem - p.b + p.G - 1) / p.G : 0;
+    p.S = p.nb ? LW / p.nb : 1;
+    p.nbr = (p.nch + 64 * LU - 1) / (64 * LU);
+    long_task t;
+    bool have = long_task_at(p, w, 0, t);
+    long_batch cur;
+    if (have) long_load(cur, a, t, lane);
+    {   // stage x: 16-byte loads, up to four in flight per thread
+        const uint32_t n4 = a.cols >> 2;
+        const float4 *x4 = (const float4 *)a.x;
+        float4 *s4 = (float4 *)xs;
+        for (uint32_t i0 = threadIdx.x; i0 < n4; i0 += 4 * LTPB) {
+            const uint32_t i1 = i0 + LTPB, i2 = i0 + 2 * LTPB, i3 = i0 + 3 * LTPB;
+            float4 v0, v1, v2, v3;
+            v0 = x4[i0];
+            if (i1 < n4) v1 = x4[i1];
+            if (i2 < n4) v2 = x4[i2];
+            if (i3 < n4) v3 = x4[i3];
+            s4[i0] = v0;
+            if (i1 < n4) s4[i1] = v1;
+            if (i2 < n4) s4[i2] = v2;
+            if (i3 < n4) s4[i3] = v3;
+        }
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    for (uint32_t k = 0; have; k++) {
+        long_task tn;
+        const bool hn = long_task_at(p, w, k + 1, tn);
+        long_batch nxt;
+        if (hn) long_load(nxt, a, tn, lane);
+        acc = long_fma(cur, xs, t, lane, acc);
+        if (!hn || tn.row != t.row) {
+            acc = wave_sum(acc);
+            if (t.slot == 0xffffffffu) {
+                if (lane == 0) gemv_store<EPI>(a, t.row, acc);
+            } else if (lane == 0) {
+                part[t.slot] = acc;
+            }
+            acc = 0.0f;
+        }
+        if (!hn) break;
+        t = tn;
+        cur = nxt;
+    }
+    if (p.nb == 0) return;
+    __syncthreads();
+    if (threadIdx.x < p.nb) {
+        float s = 0.0f;
+        for (uint32_t q = 0; q < p.S; q++) s += part[threadIdx.x * LW + q];
+        gemv_store<EPI>(a, p.base + threadIdx.x * p.G + p.b, s);
+    }
+}
+
+// Workgroups of `kern` (tpb threads, lds bytes of dynamic LDS) that fit on one
+// CU at once: the wave slots its VGPR count leaves per SIMD, and the LDS.
 template <typename K>
-static hipError_t launch_lds(K kern, uint32_t want_blocks, size_t lds, hipStream_t s, const sgk_gemv &a,
-                             uint32_t tune_blocks) {
-    if (lds > 65536) {
-        hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
+static uint32_t resident_per_cu(K kern, uint32_t tpb, size_t lds) {
+    hipFuncAttributes at;
+    int vg = 128, shm = 0;
+    if (hipFuncGetAttributes(&at, (const void *)kern) == hipSuccess) {
+        vg = at.numRegs > 0 ? at.numRegs : 128;
+        shm = (int)at.sharedSizeBytes;
     }
-    // One co-resident round of workgroups (the whole grid in flight at once,
-    // each walking its row groups), unless the caller fixes the count.
-    uint32_t blocks = tune_blocks;
+    int waves_simd = 512 / ((vg + 7) & ~7);
+    waves_simd = waves_simd > 8 ? 8 : waves_simd;
+    const int by_waves = 4 * waves_simd / (int)(tpb / 64);
+    const size_t per_wg = ((lds + (size_t)shm + 511) & ~(size_t)511);
+    const int by_lds = per_wg ? (int)(163840 / per_wg) : 64;
+    int api = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&api, (const void *)kern, (int)tpb, lds) != hipSuccess) api = 64;
+    int n = by_waves < by_lds ? by_waves : by_lds;
+    n = api < n ? api : n;
+    return n < 1 ? 1u : (uint32_t)n;
+}
+
+static int device_cus() {
+    static int cus = 0;
+    if (!cus && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) cus = 256;
+    return cus;
+}
+
+static hipError_t allow_lds(const void *kern, size_t lds) {
+    if (lds <= 65536) return hipSuccess;
+    if (lds > 163840) return hipErrorInvalidValue;
+    return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+}
+
+// Launch k_gemv_q8<R,...>: resident workgroups only, sized so every wave gets
+// ceil(groups / waves) row groups and no wave gets one fewer than another by
+// more than one (the caller may fix the count with tune_blocks).
+template <int R, int PRO, int EPI>
+static hipError_t launch_q8(const sgk_gemv &a, size_t lds, hipStream_t s) {
+    auto kern = k_gemv_q8<R, PRO, EPI>;
+    hipError_t e = allow_lds((const void *)kern, lds);
+    if (e != hipSuccess) return e;
+    static size_t seen_lds[8];                      // residency per LDS size, per instantiation
+    static uint32_t seen_per[8];
+    static int nseen = 0;
+    uint32_t per = 0;
+    for (int i = 0; i < nseen; i++)
+        if (seen_lds[i] == lds) per = seen_per[i];
+    if (!per) {
+        per = resident_per_cu(kern, TPB, lds);
+        if (nseen < 8) { seen_lds[nseen] = lds; seen_per[nseen] = per; nseen++; }
+    }
+    const uint32_t groups = (a.rows + R - 1) / R;
+    uint32_t blocks = a.tune_blocks;
     if (!blocks) {
-        static int cus = 0;
-        if (!cus && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) cus = 256;
-        int per = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)kern, TPB, lds) != hipSuccess || per < 1)
-            per = 1;
-        blocks = (uint32_t)(cus * per);
+        const uint32_t max_waves = (uint32_t)device_cus() * per * (TPB / 64);
+        const uint32_t k = (groups + max_waves - 1) / max_waves;
+        const uint32_t waves = (groups + k - 1) / k;
+        blocks = (waves + TPB / 64 - 1) / (TPB / 64);
     }
-    blocks = min(blocks, want_blocks);
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(TPB), lds, s, a);
     return hipGetLastError();
 }
 
 template <int PRO, int EPI>
 static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
-    const bool xg = PRO == SGK_PRO_NONE && a->cols > 8192;     // long rows: x from L1/L2, no LDS
-    size_t lds = xg ? 0 : (size_t)a->cols * 4 + (PRO == SGK_PRO_RMS_GATED ? (a->cols / a->head) * 4 + 16 : 16);
+    if (((uintptr_t)a->x & 15) || (PRO == SGK_PRO_RMS && ((uintptr_t)a->nw & 15))) return hipErrorInvalidValue;
     if (!a->qs) {
-        uint32_t groups = (a->rows + 1) / 2;
+        const size_t lds = (size_t)a->cols * 4;
+        hipError_t e = allow_lds((const void *)k_gemv_f32<PRO, EPI>, lds);
+        if (e != hipSuccess) return e;
+        const uint32_t groups = (a->rows + 1) / 2;
         hipLaunchKernelGGL((k_gemv_f32<PRO, EPI>), dim3(min((groups + 3) / 4, 4096u)), dim3(TPB), lds, s, *a);
         return hipGetLastError();
     }
-    int R = a->tune_r ? (int)a->tune_r : (a->rows >= 65536 ? 4 : 2);
-    if (EPI == SGK_EPI_SWIGLU && R < 2) R = 2;
-    const uint32_t want = (((a->rows + R - 1) / R) + 3) / 4;
-    const uint32_t tb = a->tune_blocks;
-#define GV(RR, X) return launch_lds(k_gemv_q8<RR, PRO, (RR == 1 && EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI), X>, want, lds, s, *a, tb)
-    if (xg) { if (R == 4) GV(4, true); if (R == 2) GV(2, true); GV(1, true); }
-    if (R == 4) GV(4, false);
-    if (R == 2) GV(2, false);
-    GV(1, false);
-#undef GV
+    if (PRO == SGK_PRO_NONE && EPI != SGK_EPI_SWIGLU && a->cols > 8192) {
+        const size_t lds = ((size_t)a->cols + LW * LW) * 4;
+        auto kern = k_gemv_q8_long<EPI == SGK_EPI_ADD ? SGK_EPI_ADD : SGK_EPI_STORE>;
+        hipError_t e = allow_lds((const void *)kern, lds);
+        if (e != hipSuccess) return e;
+        const uint32_t blocks = a->tune_blocks ? a->tune_blocks : (uint32_t)device_cus();
+        hipLaunchKernelGGL(kern, dim3(blocks), dim3(LTPB), lds, s, *a);
+        return hipGetLastError();
+    }
+    const size_t lds = (size_t)a->cols * 4;
+    const int R = EPI == SGK_EPI_SWIGLU ? 2 : (a->tune_r == 1 ? 1 : a->tune_r == 4 ? 4 : 2);
+    if (R == 4) return launch_q8<4, PRO, EPI>(*a, lds, s);
+    if (R == 1) return launch_q8<1, PRO, (EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI)>(*a, lds, s);
+    return launch_q8<2, PRO, EPI>(*a, lds, s);
 }
 
 extern "C" hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s) {
@@ -328,8 +524,6 @@ extern "C" hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s) {
     CASE(SGK_PRO_RMS, SGK_EPI_STORE);
     CASE(SGK_PRO_RMS, SGK_EPI_ADD);
     CASE(SGK_PRO_RMS, SGK_EPI_SWIGLU);
-    CASE(SGK_PRO_RMS_GATED, SGK_EPI_STORE);
-    CASE(SGK_PRO_RMS_GATED, SGK_EPI_ADD);
 #undef CASE
     return hipErrorInvalidValue;
 }
