@@ -113,6 +113,8 @@ _SIGS = {
     "sg_gpu_prefill_segments": (C.c_uint64, [C.c_void_p]),
     "sg_gpu_splitk_n_splits": (C.c_uint32, [C.c_uint32]),
     "sg_gpu_splitk_gqa_n_splits": (C.c_uint32, [C.c_uint32]),
+    "sg_gpu_splitk_gqa_n_splits_at": (C.c_uint32, [C.c_void_p, C.c_uint32]),
+    "sg_gpu_splitk_gqa_cap": (C.c_uint32, [C.c_void_p]),
     "sg_gpu_load_model": (SgErr, [C.c_void_p, C.POINTER(SgModel)]),
     "sg_gpu_state_new": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_uint32]),
     "sg_gpu_state_reset": (None, [C.c_void_p]),
@@ -270,6 +272,12 @@ class Gpu:
 
     def state_reset(self):
         lib().sg_gpu_state_reset(self.handle)
+
+    def split_cap(self) -> int:
+        return int(lib().sg_gpu_splitk_gqa_cap(self.handle))
+
+    def n_splits_at(self, seq: int) -> int:
+        return int(lib().sg_gpu_splitk_gqa_n_splits_at(self.handle, seq))
 
     def forward(self, token: int, pos: int) -> np.ndarray:
         lg = C.POINTER(C.c_float)()

@@ -98,9 +98,11 @@ struct sg_gpu {
     /* state */
     bool have_state;
     uint32_t max_ctx, used, max_splits;
+    uint32_t split_cap;     /* resolved decode split cap (SURGE_SPLITK_GQA_CAP or SGK_MAX_SPLITS) */
     float *cs_table;
     float *x, *act, *ctx, *ybuf, *gbuf, *ffg, *logits, *am, *as, *aacc;
     uint32_t *amax_scratch, *hist;
+    float *gss;             /* DeltaNet step: per-head row-block sums of squares */
     sgk_step *d_step, *h_step;
     float *h_logits;
     uint32_t *h_tok;
@@ -540,7 +542,7 @@ sg_err sg_gpu_run_attn_splitk_combine(sg_gpu *g, void *m, void *s, void *acc, vo
 
 sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out,
                                   const uint32_t p[8]) {
-    /* Single-pass decode attention: the split-K pair with one split per 32
+    /* Single-pass decode attention: the split-K pair with one split per 64
      * keys, combined, in one call. p: [0]=nh [1]=nkv [2]=hd [3]=seq [4]=q_stride [5]=scale. */
     if (!g || !q || !k || !v || !out || !p) return (sg_err){"gpu: attention one-shot got a NULL argument"};
     uint32_t pp[8];
@@ -570,8 +572,14 @@ sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *ou
 /* Split policy (surge.h:1020-1106), re-derived for 256 CUs: see kernels.h. */
 uint32_t sg_gpu_splitk_n_splits(uint32_t seq) { return sgk_n_splits(seq); }
 uint32_t sg_gpu_splitk_gqa_n_splits(uint32_t seq) { return sgk_n_splits(seq); }
-uint32_t sg_gpu_splitk_gqa_n_splits_at(const sg_gpu *g, uint32_t seq) { (void)g; return sgk_n_splits(seq); }
-uint32_t sg_gpu_splitk_gqa_cap(const sg_gpu *g) { (void)g; return SGK_MAX_SPLITS; }
+/* The cap a live state dispatches with: its accepted SURGE_SPLITK_GQA_CAP, or
+ * the default (also for NULL or a gpu with no live state). */
+uint32_t sg_gpu_splitk_gqa_cap(const sg_gpu *g) {
+    return (g && g->have_state && g->split_cap) ? g->split_cap : SGK_MAX_SPLITS;
+}
+uint32_t sg_gpu_splitk_gqa_n_splits_at(const sg_gpu *g, uint32_t seq) {
+    return sgk_n_splits_cap(seq, sg_gpu_splitk_gqa_cap(g));
+}
 bool sg_gpu_splitk_gqa_selected(const sg_gpu *g, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq) {
     (void)seq;
     return g && n_kv_heads && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8;
@@ -786,6 +794,9 @@ static sg_err check_model(const sg_model *m) {
                 return (sg_err){"gpu: DeltaNet dims unsupported (conv_kernel 1..4, n_v multiple of n_k)"};
             if (c->head_k_dim != 32 && c->head_k_dim != 64 && c->head_k_dim != 128 && c->head_k_dim != 256)
                 return (sg_err){"gpu: head_k_dim must be 32, 64, 128 or 256"};
+            if (!c->head_v_dim || c->head_v_dim > SGK_GDN_MAX_DV || c->head_v_dim % 4)
+                return (sg_err){"gpu: head_v_dim must be a multiple of 4 in [4, 256]"};
+            if (c->n_v_heads > SGK_GATED_MAX_HEADS) return (sg_err){"gpu: at most 256 DeltaNet value heads"};
         } else if (c->rope_dim < 2 || c->rope_dim > c->head_dim || c->rope_dim % 2) {
             return (sg_err){"gpu: rope_dim must be even and in [2, head_dim]"};
         }
@@ -910,10 +921,11 @@ static void state_free(sg_gpu *g) {
         L->kc = L->vc = NULL; L->ring = L->S = NULL;
     }
     void *bufs[] = { g->cs_table, g->x, g->act, g->ctx, g->ybuf, g->gbuf, g->ffg, g->logits, g->am, g->as,
-                     g->aacc, g->amax_scratch, g->hist, g->d_step };
+                     g->aacc, g->amax_scratch, g->hist, g->d_step, g->gss };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) dfree(g, bufs[i]);
     g->cs_table = g->x = g->act = g->ctx = g->ybuf = g->gbuf = g->ffg = g->logits = g->am = g->as = g->aacc = NULL;
     g->amax_scratch = g->hist = NULL;
+    g->gss = NULL;
     g->d_step = NULL;
     g->have_state = false;
 }
@@ -942,7 +954,8 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             A.gate = c->attn_output_gate ? g->act + hd : NULL; A.steps = g->d_step;
             A.n_heads = c->n_heads; A.n_kv = c->n_kv_heads; A.hd = hd; A.rope_dim = c->rope_dim; A.q_stride = qs;
             A.max_splits = g->max_splits; A.ntok = 1; A.scale = (float)(1.0 / sqrt((double)hd));
-            if ((e = sgk_attn_prep(&A, L->qn, L->kn, g->cs_table, c->rms_eps, s)) != hipSuccess) return e;
+            A.fuse_prep = 1; A.qn = L->qn; A.kn = L->kn; A.cs = g->cs_table; A.eps = c->rms_eps;
+            A.split_cap = g->split_cap;
             if ((e = sgk_attn_partial(&A, s)) != hipSuccess) return e;
             if ((e = sgk_attn_combine(&A, s)) != hipSuccess) return e;
             o.x = g->ctx; o.pro = SGK_PRO_NONE;
@@ -952,11 +965,12 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             d.S = L->S; d.y = g->ybuf; d.step = g->d_step; d.n_k = c->n_k_heads; d.n_v = c->n_v_heads;
             d.dk = c->head_k_dim; d.dv = c->head_v_dim; d.conv_dim = g->conv_dim; d.ksize = c->conv_kernel;
             d.tiled = g->model->v_heads_tiled; d.neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
+            d.z = g->act + g->conv_dim; d.norm_w = L->ssm_norm; d.out = g->gbuf; d.eps = c->rms_eps;
+            d.ss = g->gss;
             if ((e = sgk_gdn_step(&d, s)) != hipSuccess) return e;
-            /* RMSNormGated once (not in every GEMV workgroup), then the out projection */
-            if ((e = sgk_rmsnorm_gated(g->ybuf, g->act + g->conv_dim, L->ssm_norm, g->gbuf, c->head_v_dim,
-                                       c->n_v_heads, c->rms_eps, s)) != hipSuccess) return e;
-            o.x = g->gbuf; o.pro = SGK_PRO_NONE;
+            /* RMSNormGated in the out projection's prologue */
+            o.x = g->ybuf; o.x2 = g->gbuf; o.gss = g->gss; o.nw = L->ssm_norm; o.gdv = c->head_v_dim;
+            o.pro = SGK_PRO_GATED;
         }
         if ((e = sgk_gemv_launch(&o, s)) != hipSuccess) return e;
         sgk_gemv f = {0};
@@ -1000,9 +1014,23 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     if (m != g->model) return (sg_err){"gpu: this gpu was loaded with a different sg_model"};
     if (!max_ctx || max_ctx > SG_KV_CAP_MAX) return (sg_err){"gpu: max_ctx must be in [1, 262144]"};
     state_free(g);
+    /* SURGE_SPLITK_GQA_CAP (reference surge.h:1239-1256): plain decimal digits
+     * in [4, 1024], else the state is refused. */
+    uint32_t cap = SGK_MAX_SPLITS;
+    const char *cap_env = getenv("SURGE_SPLITK_GQA_CAP");
+    if (cap_env && cap_env[0] != '\0') {
+        uint64_t v = 0;
+        const char *ch = cap_env;
+        for (; *ch >= '0' && *ch <= '9' && v <= SGK_SPLIT_CAP_MAX; ch++) v = v * 10 + (uint64_t)(*ch - '0');
+        if (*ch != '\0' || v < SGK_SPLIT_CAP_MIN || v > SGK_SPLIT_CAP_MAX)
+            return errf("gpu: SURGE_SPLITK_GQA_CAP='%s' is not an integer in [%u, %u]", cap_env,
+                        SGK_SPLIT_CAP_MIN, SGK_SPLIT_CAP_MAX);
+        cap = (uint32_t)v;
+    }
     const sg_cfg *c = &g->cfg;
     g->max_ctx = max_ctx;
-    g->max_splits = sgk_n_splits(max_ctx);
+    g->split_cap = cap;
+    g->max_splits = sgk_n_splits_cap(max_ctx, cap);
     sg_err e = SG_OK;
     uint32_t act_rows = 0;
     for (uint32_t i = 0; i < c->n_layers; i++) if (g->ls[i].in.rows > act_rows) act_rows = g->ls[i].in.rows;
@@ -1024,6 +1052,7 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
         {(void **)&g->ffg, (uint64_t)c->ffn_hidden * 4}, {(void **)&g->logits, (uint64_t)c->vocab * 4},
         {(void **)&g->am, ah * 4}, {(void **)&g->as, ah * 4}, {(void **)&g->aacc, ah * c->head_dim * 4},
         {(void **)&g->amax_scratch, 4096}, {(void **)&g->hist, ((uint64_t)max_ctx + 2) * 4},
+        {(void **)&g->gss, (uint64_t)c->n_v_heads * SGK_GDN_BLOCKS * 4 + 4},
         {(void **)&g->d_step, sizeof(sgk_step)},
     };
     for (size_t i = 0; i < sizeof al / sizeof *al && !sg_failed(e); i++) e = dzalloc(g, al[i].n, al[i].p);
@@ -1327,7 +1356,10 @@ sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which) {
         case 1:
             M = &L->out; a.y = g->x; a.epi = SGK_EPI_ADD;
             if (L->attn) { a.x = g->ctx; a.pro = SGK_PRO_NONE; }
-            else { a.x = g->gbuf; a.pro = SGK_PRO_NONE; }
+            else {
+                a.x = g->ybuf; a.x2 = g->gbuf; a.gss = g->gss; a.nw = L->ssm_norm; a.gdv = c->head_v_dim;
+                a.pro = SGK_PRO_GATED;
+            }
             break;
         case 2: M = &L->gu; a.x = g->x; a.nw = L->ln2; a.y = g->ffg; a.pro = SGK_PRO_RMS; a.epi = SGK_EPI_SWIGLU; break;
         case 3: M = &L->down; a.x = g->ffg; a.y = g->x; a.pro = SGK_PRO_NONE; a.epi = SGK_EPI_ADD; break;

@@ -27,22 +27,28 @@ typedef struct {
 } sgk_step;
 
 /* The split-K decode-attention split count (also evaluated on the device).
- * MI355X policy: about 32 keys per split so that n_splits * n_kv_heads
- * reaches several hundred workgroups at 4k context on 256 CUs, capped at
- * SGK_MAX_SPLITS; never more splits than keys. */
+ * MI355X policy: about 64 keys per split (one key tile of the partial kernel
+ * at head_dim 256) so that n_splits * n_kv_heads reaches a workgroup per CU
+ * at 4k context with 4 kv heads, capped at SGK_MAX_SPLITS; never more
+ * splits than keys. */
 #define SGK_MAX_SPLITS 256u
-#define SGK_KEYS_PER_SPLIT 32u
-static inline uint32_t sgk_n_splits(uint32_t seq) {
+#define SGK_KEYS_PER_SPLIT 64u
+/* A state may lower or raise the cap (SURGE_SPLITK_GQA_CAP) within [4, 1024]. */
+#define SGK_SPLIT_CAP_MIN 4u
+#define SGK_SPLIT_CAP_MAX 1024u
+static inline uint32_t sgk_n_splits_cap(uint32_t seq, uint32_t cap) {
     uint32_t n = (seq + SGK_KEYS_PER_SPLIT - 1) / SGK_KEYS_PER_SPLIT;
     if (n < 1) n = 1;
-    if (n > SGK_MAX_SPLITS) n = SGK_MAX_SPLITS;
+    if (n > cap) n = cap;
     return n;
 }
+static inline uint32_t sgk_n_splits(uint32_t seq) { return sgk_n_splits_cap(seq, SGK_MAX_SPLITS); }
 
 /* GEMV prologues (what is staged into LDS as the input vector: x, or x*w with
  * the RMS factor applied to each row sum) and epilogues (what is done with
  * each output row). */
-enum { SGK_PRO_NONE = 0, SGK_PRO_RMS = 1 };
+enum { SGK_PRO_NONE = 0, SGK_PRO_RMS = 1, SGK_PRO_GATED = 2 };
+#define SGK_GATED_MAX_HEADS 256u
 enum { SGK_EPI_STORE = 0, SGK_EPI_ADD = 1, SGK_EPI_SWIGLU = 2 };
 
 typedef struct {
@@ -56,6 +62,10 @@ typedef struct {
     float *y;               /* output [rows] (or [rows/2] for SWIGLU) */
     int pro, epi;
     uint32_t tune_r, tune_blocks;   /* 0 = default; rows per wave (1/2/4), workgroups */
+    /* PRO_GATED (the DeltaNet out projection): x = readout y, x2 = silu(z),
+     * nw = ssm_norm [gdv], gss = row-block sums of squares [heads][SGK_GDN_BLOCKS] */
+    const float *x2, *gss;
+    uint32_t gdv;
 } sgk_gemv;
 
 hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s);
@@ -102,8 +112,14 @@ typedef struct {
     const sgk_step *steps;
     uint32_t n_heads, n_kv, hd, rope_dim, q_stride, q_tok, out_tok;
     uint32_t seq, n_splits, max_splits, ntok;
+    uint32_t split_cap;         /* decode split cap (0 = SGK_MAX_SPLITS) */
     float scale;
     int prefill;                /* split policy: 0 decode (kernels.h), 1 prefill */
+    /* fused prep (decode, ntok == 1): q_norm/k_norm weights, the cos|sin
+     * table [max_ctx][rope_dim], the norm eps */
+    int fuse_prep;
+    const float *qn, *kn, *cs;
+    float eps;
 } sgk_attn;
 
 /* q_norm/k_norm + RoPE on each head, K and V stored f16 at each token's
@@ -111,7 +127,9 @@ typedef struct {
 hipError_t sgk_attn_prep(const sgk_attn *a, const float *qn, const float *kn,
                          const float *cs_table, float eps, hipStream_t s);
 /* Split-K GQA partials: workgroup (split, kv head, token) serves all
- * n_heads/n_kv query heads of the group (grid x = max_splits with steps). */
+ * n_heads/n_kv query heads of the group (grid x = max_splits with steps).
+ * With fuse_prep the prep above is done inside (q in LDS; the split holding
+ * the position stores the new K/V), so a decode step needs no prep launch. */
 hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s);
 /* LSE combine with the optional fused sigmoid output gate. */
 hipError_t sgk_attn_combine(const sgk_attn *a, hipStream_t s);
@@ -131,7 +149,19 @@ typedef struct {
     const sgk_step *step;
     uint32_t n_k, n_v, dk, dv, conv_dim, ksize;
     int tiled, neg_exp;
+    /* decode step only: z [value_dim] (the projection's z rows); out receives
+     * silu(z), y the pre-norm readouts and ss [n_v][SGK_GDN_BLOCKS] each row
+     * block's sum of squared readouts, for the gated GEMV prologue */
+    const float *z, *norm_w;
+    float *out;
+    float eps;
+    float *ss;
 } sgk_gdn;
+#define SGK_GDN_MAX_DV 256u
+#define SGK_GDN_BLOCKS 4u
+/* The decode step (SGK_GDN_BLOCKS workgroups per value head; needs dv <=
+ * SGK_GDN_MAX_DV); RMSNormGated is finished by the out projection's
+ * SGK_PRO_GATED prologue. */
 hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s);
 
 /* The DeltaNet layer over a prefill chunk of ntok tokens (a->step holds the

@@ -33,14 +33,59 @@
 // helpers
 // ---------------------------------------------------------------------------
 
+// Cross-lane moves without the LDS crossbar (gfx950): DPP lane selects inside
+// a row of 16 lanes and the permlane swaps across rows / half-waves.
+//   xor1: quad_perm [1,0,3,2]      xor2: quad_perm [2,3,0,1]
+//   mir8: row_half_mirror (i <-> 7-i in each 8 lanes; flips bits 0..2)
+//   xor8: row_ror:8 (i <-> i^8 in each row)
+//   xor16 / xor32: v_permlane16_swap / v_permlane32_swap of v with itself
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_xor1(float v) { return dppf<0xB1>(v); }
+__device__ __forceinline__ float lane_xor2(float v) { return dppf<0x4E>(v); }
+__device__ __forceinline__ float lane_mir8(float v) { return dppf<0x141>(v); }
+__device__ __forceinline__ float lane_xor8(float v) { return dppf<0x128>(v); }
+__device__ __forceinline__ float lane_xor16(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return __int_as_float((threadIdx.x & 16) ? p[0] : p[1]);
+}
+__device__ __forceinline__ float lane_xor32(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return __int_as_float((threadIdx.x & 32) ? p[0] : p[1]);
+}
+// Exact partner l ^ O for any power-of-two O.
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+    if (O == 1) return lane_xor1(v);
+    if (O == 2) return lane_xor2(v);
+    if (O == 8) return lane_xor8(v);
+    if (O == 16) return lane_xor16(v);
+    if (O == 32) return lane_xor32(v);
+    return __shfl_xor(v, O, 64);
+}
+__device__ __forceinline__ float lane_read(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+// Butterfly sum / max over the 64 lanes; every lane ends with the same bits
+// (each step adds a pair in both orders, and + / max commute).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += lane_xor1(v);
+    v += lane_xor2(v);
+    v += lane_mir8(v);
+    v += lane_xor8(v);
+    v += lane_xor16(v);
+    v += lane_xor32(v);
     return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = fmaxf(v, lane_xor1(v));
+    v = fmaxf(v, lane_xor2(v));
+    v = fmaxf(v, lane_mir8(v));
+    v = fmaxf(v, lane_xor8(v));
+    v = fmaxf(v, lane_xor16(v));
+    v = fmaxf(v, lane_xor32(v));
     return v;
 }
 // Sum over all 256 threads of a workgroup; every thread gets the same value.
@@ -71,10 +116,11 @@ __device__ __forceinline__ float silu(float x) { return x * sigm(x); }
 // max(x,0) + log1p(e^-|x|) (ref.c:136-142).
 __device__ __forceinline__ float softplus(float x) { return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x))); }
 
-__device__ __forceinline__ uint32_t dev_n_splits(uint32_t seq) {
+__device__ __forceinline__ uint32_t dev_n_splits(uint32_t seq, uint32_t cap) {
     uint32_t n = (seq + SGK_KEYS_PER_SPLIT - 1) / SGK_KEYS_PER_SPLIT;
     n = n < 1 ? 1 : n;
-    return n > SGK_MAX_SPLITS ? SGK_MAX_SPLITS : n;
+    cap = cap ? cap : SGK_MAX_SPLITS;
+    return n > cap ? cap : n;
 }
 
 // ---------------------------------------------------------------------------
@@ -86,10 +132,35 @@ __device__ __forceinline__ uint32_t dev_n_splits(uint32_t seq) {
 // factor 1/sqrt(mean(x^2) + eps) (ref.c:113-125) for the epilogue to apply to
 // each row sum: W(x*r*w) = r * W(x*w). Other prologues return 1. Needs x and w
 // 16-byte aligned (every buffer of this library is).
-template <int PRO>
-__device__ __forceinline__ float stage_x(const sgk_gemv &a, float *xs) {
-    __shared__ float red[TPB / 64];
+template <int PRO, int NT>
+__device__ __forceinline__ float stage_x_n(const sgk_gemv &a, float *xs) {
+    __shared__ float red[NT / 64];
     const uint32_t n = a.cols, t = threadIdx.x, n4 = n >> 2;
+    if (PRO == SGK_PRO_GATED) {
+        // RMSNormGated of the DeltaNet readout (ref.c:1322-1330): head hh's
+        // factor from its row blocks' sums of squares (added in block order),
+        // then x = silu(z) * ((y * r) * w) with silu(z) precomputed.
+        __shared__ float rh[SGK_GATED_MAX_HEADS];
+        const uint32_t dv = a.gdv, nh = n / dv;
+        for (uint32_t hh = t; hh < nh; hh += NT) {
+            float tot = 0.0f;
+            for (uint32_t b = 0; b < SGK_GDN_BLOCKS; b++) tot += a.gss[hh * SGK_GDN_BLOCKS + b];
+            rh[hh] = 1.0f / sqrtf(tot / (float)dv + a.eps);
+        }
+        __syncthreads();
+        const float4 *y4 = (const float4 *)a.x, *z4 = (const float4 *)a.x2;
+        float4 *s4 = (float4 *)xs;
+        for (uint32_t i = t; i < n4; i += NT) {
+            const float4 yv = y4[i], zv = z4[i];
+            const uint32_t j = 4 * i, hh = j / dv, jj = j - hh * dv;
+            const float r = rh[hh];
+            const float4 wv = *(const float4 *)(a.nw + jj);
+            s4[i] = make_float4(zv.x * ((yv.x * r) * wv.x), zv.y * ((yv.y * r) * wv.y),
+                                zv.z * ((yv.z * r) * wv.z), zv.w * ((yv.w * r) * wv.w));
+        }
+        __syncthreads();
+        return 1.0f;
+    }
     const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.nw;
     float4 *s4 = (float4 *)xs;
     float ss = 0.0f;
@@ -97,8 +168,8 @@ __device__ __forceinline__ float stage_x(const sgk_gemv &a, float *xs) {
     // prologue's registers below the main loop's).
     constexpr uint32_t NS = PRO == SGK_PRO_RMS ? 2 : 4;
 #pragma unroll 1
-    for (uint32_t i0 = t; i0 < n4; i0 += NS * TPB) {
-        const uint32_t i1 = i0 + TPB, i2 = i0 + 2 * TPB, i3 = i0 + 3 * TPB;
+    for (uint32_t i0 = t; i0 < n4; i0 += NS * NT) {
+        const uint32_t i1 = i0 + NT, i2 = i0 + 2 * NT, i3 = i0 + 3 * NT;
         float4 v0, v1, v2, v3, g0, g1;
         v0 = x4[i0];
         if (i1 < n4) v1 = x4[i1];
@@ -124,7 +195,7 @@ __device__ __forceinline__ float stage_x(const sgk_gemv &a, float *xs) {
             if (i3 < n4) s4[i3] = v3;
         }
     }
-    for (uint32_t i = 4 * n4 + t; i < n; i += TPB) {       // cols % 4 tail (f32 test models)
+    for (uint32_t i = 4 * n4 + t; i < n; i += NT) {       // cols % 4 tail (f32 test models)
         float v = a.x[i];
         if (PRO == SGK_PRO_RMS) { ss = fmaf(v, v, ss); v *= a.nw[i]; }
         xs[i] = v;
@@ -135,9 +206,13 @@ __device__ __forceinline__ float stage_x(const sgk_gemv &a, float *xs) {
     }
     __syncthreads();
     if (PRO != SGK_PRO_RMS) return 1.0f;
-    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NT / 64; i += 2) tot += red[i] + red[i + 1];
     return 1.0f / sqrtf(tot / (float)n + a.eps);
 }
+template <int PRO>
+__device__ __forceinline__ float stage_x(const sgk_gemv &a, float *xs) { return stage_x_n<PRO, TPB>(a, xs); }
 
 template <int EPI>
 __device__ __forceinline__ void gemv_store(const sgk_gemv &a, uint32_t row, float v) {
@@ -260,6 +335,9 @@ __global__ void __launch_bounds__(TPB) k_gemv_q8(sgk_gemv a) {
     gemv_group<R, EPI, true>(a, xs, g, lane, &pre, post);
     for (g += gstride; g < ngroups; g += gstride) gemv_group<R, EPI, false>(a, xs, g, lane, nullptr, post);
 }
+
+
+
 
 // f32-weight GEMV (small test models only): one wave per row pair.
 template <int PRO, int EPI>
@@ -459,6 +537,8 @@ static hipError_t allow_lds(const void *kern, size_t lds) {
     return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
 
+
+
 // Launch k_gemv_q8<R,...>: resident workgroups only, sized so every wave gets
 // ceil(groups / waves) row groups and no wave gets one fewer than another by
 // more than one (the caller may fix the count with tune_blocks).
@@ -492,6 +572,10 @@ static hipError_t launch_q8(const sgk_gemv &a, size_t lds, hipStream_t s) {
 template <int PRO, int EPI>
 static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
     if (((uintptr_t)a->x & 15) || (PRO == SGK_PRO_RMS && ((uintptr_t)a->nw & 15))) return hipErrorInvalidValue;
+    if (PRO == SGK_PRO_GATED && (!a->x2 || !a->gss || !a->nw || !a->gdv || a->gdv % 4 || a->cols % a->gdv ||
+                                 a->cols / a->gdv > SGK_GATED_MAX_HEADS || ((uintptr_t)a->x2 & 15) ||
+                                 ((uintptr_t)a->nw & 15)))
+        return hipErrorInvalidValue;
     if (!a->qs) {
         const size_t lds = (size_t)a->cols * 4;
         hipError_t e = allow_lds((const void *)k_gemv_f32<PRO, EPI>, lds);
@@ -524,6 +608,8 @@ extern "C" hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s) {
     CASE(SGK_PRO_RMS, SGK_EPI_STORE);
     CASE(SGK_PRO_RMS, SGK_EPI_ADD);
     CASE(SGK_PRO_RMS, SGK_EPI_SWIGLU);
+    CASE(SGK_PRO_GATED, SGK_EPI_ADD);
+    CASE(SGK_PRO_GATED, SGK_EPI_STORE);
 #undef CASE
     return hipErrorInvalidValue;
 }
@@ -713,8 +799,8 @@ extern "C" hipError_t sgk_softmax(const float *x, float *out, uint32_t n, hipStr
 // Split count as the kernels see it: the decode policy (kernels.h), or the
 // prefill policy (at most SGK_PREFILL_SPLITS splits of >= 1024 keys, so a
 // chunk's partial scratch stays bounded).
-__device__ __forceinline__ uint32_t dev_splits(uint32_t seq, int prefill) {
-    if (!prefill) return dev_n_splits(seq);
+__device__ __forceinline__ uint32_t dev_splits(uint32_t seq, int prefill, uint32_t cap) {
+    if (!prefill) return dev_n_splits(seq, cap);
     uint32_t n = seq / 1024u;
     n = n < 1 ? 1 : n;
     return n > SGK_PREFILL_SPLITS ? SGK_PREFILL_SPLITS : n;
@@ -776,21 +862,81 @@ extern "C" hipError_t sgk_attn_prep(const sgk_attn *a, const float *qn, const fl
 // ---------------------------------------------------------------------------
 
 #define GMAX 8
-#define KT 32
+
+// Query / key prep shared by k_attn_prep and the fused decode partial:
+// RMSNorm (w) then half-split RoPE over the first rope_dim dims, element d
+// of a row x whose raw values and 1/rms factor are given (ref.c:1207-1235,
+// 561-606). cs is the position's cos|sin row.
+__device__ __forceinline__ float prep_elem(const float *x, float r, const float *w, const float *cs,
+                                           uint32_t d, uint32_t rope_dim) {
+    const uint32_t half = rope_dim >> 1;
+    if (d < half) return ((x[d] * r) * w[d]) * cs[d] - ((x[d + half] * r) * w[d + half]) * cs[half + d];
+    if (d < rope_dim) return ((x[d - half] * r) * w[d - half]) * cs[d] + ((x[d] * r) * w[d]) * cs[d - half];
+    return (x[d] * r) * w[d];
+}
+
+// ---------------------------------------------------------------------------
+// Split-K GQA attention partial (tiled).
+//
+// Workgroup (split i, kv head hk, token z) owns keys [i*seq/n, (i+1)*seq/n)
+// and all G = n_heads/n_kv query heads of its group, so every K/V byte is
+// read once per token. Keys go in tiles of TK = 256*DPT/HD (64 at head_dim
+// 256). Every K and V load of a tile is issued unconditionally, indices
+// clamped into the split (keys past its end score -inf and their V is
+// zeroed), so a tile costs one memory round trip; the next tile's K is
+// requested once the scores are formed and its V once P*V is done.
+//   scores: TPK = HD/DPT lanes per key, DPT dims per lane, q from LDS;
+//   softmax: one wave per head over the tile, running max/sum rescaled
+//            across tiles (online form);
+//   P*V:    lane = (key group kg, 8-dim chunk vc), KGV key groups folded at
+//           the end in a fixed order (xor shuffles, then waves in order).
+// Output: m, s and the UNNORMALISED acc of each (head, split), as ref.c's
+// attn_partial (ref.c:416-455). Empty splits give m=-inf, s=0, acc=0.
+//
+// With a.fuse_prep (decode, one token): the workgroup first forms the
+// q_norm+RoPE'd queries of its heads in LDS from the raw projection rows,
+// and the split holding the new position also stores that token's
+// k_norm+RoPE'd K and raw V as f16 at the position before reading any key
+// (one writer per (position, kv head)).
+// ---------------------------------------------------------------------------
+
+template <int HD>
+struct attn_geom {
+    static constexpr int DPT = HD < 64 ? HD : 64;   // score dims per lane
+    static constexpr int TPK = HD / DPT;            // lanes per key
+    static constexpr int TK = TPB / TPK;            // keys per tile
+    static constexpr int KU = DPT / 8;              // K uint4 per lane
+    static constexpr int VC = HD / 8;               // 8-dim chunks of a V row
+    static constexpr int KGV = TPB / VC;            // key groups in P*V
+    static constexpr int VU = TK / KGV;             // V uint4 per lane
+    static constexpr int QP = DPT + 4;              // padded q chunk (LDS banks)
+    static constexpr int QROW = TPK * QP;
+};
+
+__device__ __forceinline__ void h8(const uint4 r, float *f) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        f[2 * e] = h2f((uint16_t)(w[e] & 0xFFFF));
+        f[2 * e + 1] = h2f((uint16_t)(w[e] >> 16));
+    }
+}
 
 template <int HD>
 __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
-    constexpr int KG = TPB / HD;          // key groups for P*V (HD <= 256)
-    constexpr int DPL = HD / 8;           // dims per lane in the score phase
-    __shared__ float qsh[GMAX][HD];
-    __shared__ float sc[GMAX][KT];
-    __shared__ float mrun[GMAX], srun[GMAX], alpha[GMAX];
-    __shared__ float accx[KG > 1 ? GMAX * TPB : 1];
+    using Gm = attn_geom<HD>;
+    constexpr int DPT = Gm::DPT, TPK = Gm::TPK, TK = Gm::TK, KU = Gm::KU, VC = Gm::VC, KGV = Gm::KGV,
+                  VU = Gm::VU, QP = Gm::QP, QROW = Gm::QROW;
+    __shared__ float qsh[GMAX * QROW];
+    __shared__ float sc[GMAX][TK];
+    __shared__ float mrun[GMAX], srun[GMAX], alpha[GMAX], rn[GMAX + 1];
+    __shared__ __align__(16) float red[TPB / 64][GMAX * HD];   // end fold; raw rows during prep
 
     const uint32_t G = a.n_heads / a.n_kv, n_kv = a.n_kv, z = blockIdx.z;
-    const uint32_t seq = a.steps ? a.steps[z].pos + 1 : a.seq;
-    const uint32_t ns = a.steps ? dev_splits(seq, a.prefill) : a.n_splits;
-    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x;
+    const uint32_t pos = a.steps ? a.steps[z].pos : 0;
+    const uint32_t seq = a.steps ? pos + 1 : a.seq;
+    const uint32_t ns = a.steps ? dev_splits(seq, a.prefill, a.split_cap) : a.n_splits;
+    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     if (i >= ns) return;
     const uint32_t t0 = (uint32_t)((uint64_t)i * seq / ns);
     const uint32_t t1 = (uint32_t)((uint64_t)(i + 1) * seq / ns);
@@ -798,66 +944,128 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
     const float *q = a.q + (size_t)z * a.q_tok;
     const uint16_t *kc = a.kc, *vc = a.vc;
     const size_t zoff = (size_t)z * a.n_heads * a.max_splits;
+    const uint32_t kj = t / TPK, kp = t % TPK;      // score mapping
+    const uint32_t vcc = t % VC, kg = t / VC;       // P*V mapping
 
-    for (uint32_t e = t; e < G * HD; e += TPB) {
-        const uint32_t h = e / HD, dd = e % HD;
-        qsh[h][dd] = q[(size_t)(h0 + h) * a.q_stride + dd];
+    uint4 kr[KU], vr[VU];
+    auto load_k = [&](uint32_t ts) {
+        const uint32_t key = min(ts + kj, t1 - 1);
+        const uint4 *p = (const uint4 *)(kc + ((size_t)key * n_kv + hk) * HD + kp * DPT);
+#pragma unroll
+        for (int u = 0; u < KU; u++) kr[u] = p[u];
+    };
+    auto load_v = [&](uint32_t ts) {
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const uint32_t key = min(ts + kg + u * KGV, t1 - 1);
+            vr[u] = ((const uint4 *)(vc + ((size_t)key * n_kv + hk) * HD))[vcc];
+        }
+    };
+    // The first tile's K and V depend only on the split: request them before
+    // anything else so their latency overlaps the query staging.
+    if (t0 < t1) { load_k(t0); load_v(t0); }
+
+    if (a.fuse_prep) {
+        // One round trip for everything the prep reads: raw q rows of the
+        // group, and for the split holding the position its raw k and v rows,
+        // the position's cos|sin row and both norm weights.
+        __shared__ float cs_s[HD], qn_s[HD], kn_s[HD];
+        __shared__ __align__(16) uint16_t knew[HD], vnew[HD];
+        float *raw = &red[0][0];                 // [G][HD] q, then k at [GMAX*HD]
+        const bool kv_writer = i == ns - 1;
+        const float *krow = q + (size_t)a.n_heads * a.q_stride + (size_t)hk * HD;
+        const float *vrow = krow + (size_t)n_kv * HD;
+        const float *csrow = a.cs + (size_t)pos * a.rope_dim;
+        float vraw[(HD + TPB - 1) / TPB];
+        for (uint32_t e = t; e < G * HD; e += TPB) raw[e] = q[(size_t)(h0 + e / HD) * a.q_stride + e % HD];
+        for (uint32_t d = t; d < HD; d += TPB) {
+            qn_s[d] = a.qn[d];
+            cs_s[d] = d < a.rope_dim ? csrow[d] : 0.0f;
+            if (kv_writer) { raw[GMAX * HD + d] = krow[d]; kn_s[d] = a.kn[d]; vraw[d / TPB] = vrow[d]; }
+        }
+        __syncthreads();
+        for (uint32_t h = wave; h <= (uint32_t)G; h += TPB / 64) {
+            if (h == (uint32_t)G && !kv_writer) break;
+            const float *x = h < (uint32_t)G ? raw + h * HD : raw + GMAX * HD;
+            float ss = 0.0f;
+            for (uint32_t d = lane; d < HD; d += 64) ss = fmaf(x[d], x[d], ss);
+            ss = wave_sum(ss);
+            if (lane == 0) rn[h] = 1.0f / sqrtf(ss / (float)HD + a.eps);
+        }
+        __syncthreads();
+        for (uint32_t e = t; e < G * HD; e += TPB) {
+            const uint32_t h = e / HD, d = e % HD;
+            qsh[h * QROW + (d / DPT) * QP + d % DPT] = prep_elem(raw + h * HD, rn[h], qn_s, cs_s, d, a.rope_dim);
+        }
+        if (kv_writer) {
+            const size_t at = ((size_t)pos * n_kv + hk) * HD;
+            for (uint32_t d = t; d < HD; d += TPB) {
+                const uint16_t kh = f2h(prep_elem(raw + GMAX * HD, rn[G], kn_s, cs_s, d, a.rope_dim));
+                const uint16_t vh = f2h(vraw[d / TPB]);
+                ((uint16_t *)a.kc)[at + d] = kh;
+                ((uint16_t *)a.vc)[at + d] = vh;
+                knew[d] = kh;
+                vnew[d] = vh;
+            }
+        }
+        __syncthreads();
+        // The first tile was requested before the new row was stored: if it
+        // holds the position, take that key's K and V from LDS. Later tiles
+        // are loaded after the store and the barrier above, which makes the
+        // stored row visible to the whole workgroup.
+        if (kv_writer && t0 < t1 && pos - t0 < (uint32_t)TK) {
+            if (t0 + kj == pos) {
+#pragma unroll
+                for (int u = 0; u < KU; u++) kr[u] = ((const uint4 *)(knew + kp * DPT))[u];
+            }
+#pragma unroll
+            for (int u = 0; u < VU; u++)
+                if (t0 + kg + u * KGV == pos) vr[u] = ((const uint4 *)vnew)[vcc];
+        }
+    } else {
+        for (uint32_t e = t; e < G * HD; e += TPB) {
+            const uint32_t h = e / HD, d = e % HD;
+            qsh[h * QROW + (d / DPT) * QP + d % DPT] = q[(size_t)(h0 + h) * a.q_stride + d];
+        }
     }
-    if (t < GMAX) { mrun[t] = -INFINITY; srun[t] = 0.0f; }
+    if (t < (uint32_t)G) { mrun[t] = -INFINITY; srun[t] = 0.0f; }
     __syncthreads();
 
-    const uint32_t d = t % HD, kg = t / HD;      // P*V mapping
-    const uint32_t kj = t >> 3, kp = t & 7;      // score mapping
-    float acc[GMAX];
+    float acc[GMAX][8];
 #pragma unroll
-    for (int h = 0; h < GMAX; h++) acc[h] = 0.0f;
+    for (int h = 0; h < GMAX; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
 
-    for (uint32_t ts = t0; ts < t1; ts += KT) {
-        const uint32_t nk = min((uint32_t)KT, t1 - ts);
-        // V for this tile, issued before the score math so the loads overlap it.
-        float vr[KT / KG];
-#pragma unroll
-        for (int u = 0; u < KT / KG; u++) {
-            const uint32_t j = kg + u * KG;
-            vr[u] = (j < nk) ? h2f(vc[((size_t)(ts + j) * n_kv + hk) * HD + d]) : 0.0f;
-        }
-        // Scores: a group of 8 lanes per key, HD/8 dims per lane.
+    for (uint32_t ts = t0; ts < t1; ts += TK) {
+        const uint32_t nk = min((uint32_t)TK, t1 - ts);
+        const bool more = ts + TK < t1;
+        // scores
         float part[GMAX];
 #pragma unroll
         for (int h = 0; h < GMAX; h++) part[h] = 0.0f;
-        if (kj < nk) {
-            const uint16_t *kr = kc + ((size_t)(ts + kj) * n_kv + hk) * HD + kp * DPL;
-            float kf[DPL];
-            if constexpr (DPL % 8 == 0) {
 #pragma unroll
-                for (int c8 = 0; c8 < DPL / 8; c8++) {
-                    const uint4 raw = ((const uint4 *)kr)[c8];
-                    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        kf[c8 * 8 + 2 * e] = h2f((uint16_t)(w4[e] & 0xFFFF));
-                        kf[c8 * 8 + 2 * e + 1] = h2f((uint16_t)(w4[e] >> 16));
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < DPL; e++) kf[e] = h2f(kr[e]);
-            }
+        for (int u = 0; u < KU; u++) {
+            float kf[8];
+            h8(kr[u], kf);
 #pragma unroll
             for (int h = 0; h < GMAX; h++) {
                 if (h < (int)G) {
-                    float sacc = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < DPL; e++) sacc = fmaf(qsh[h][kp * DPL + e], kf[e], sacc);
-                    part[h] = sacc;
+                    const float4 *qa = (const float4 *)(qsh + h * QROW + kp * QP + u * 8);
+                    const float4 x0 = qa[0], x1 = qa[1];
+                    float s = part[h];
+                    s = fmaf(x0.x, kf[0], s); s = fmaf(x0.y, kf[1], s); s = fmaf(x0.z, kf[2], s);
+                    s = fmaf(x0.w, kf[3], s); s = fmaf(x1.x, kf[4], s); s = fmaf(x1.y, kf[5], s);
+                    s = fmaf(x1.z, kf[6], s); s = fmaf(x1.w, kf[7], s);
+                    part[h] = s;
                 }
             }
         }
+        if (more) load_k(ts + TK);
 #pragma unroll
         for (int h = 0; h < GMAX; h++) {
-            part[h] += __shfl_xor(part[h], 1, 64);
-            part[h] += __shfl_xor(part[h], 2, 64);
-            part[h] += __shfl_xor(part[h], 4, 64);
+            if (TPK >= 2) part[h] += lane_xor1(part[h]);
+            if (TPK >= 4) part[h] += lane_xor2(part[h]);
         }
         if (kp == 0) {
 #pragma unroll
@@ -865,77 +1073,101 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
                 if (h < (int)G) sc[h][kj] = (kj < nk) ? part[h] * a.scale : -INFINITY;
         }
         __syncthreads();
-        // Per head (32 lanes each): tile max, new running max, p = exp(s - m),
-        // tile sum; lane 0 of the head updates the running max and sum.
-        {
-            const uint32_t h = t >> 5, j = t & 31;
-            if (h < G) {
-                const float v = sc[h][j];
-                float tm = v;
+        // softmax: one wave per head over the tile
+        for (uint32_t h = wave; h < (uint32_t)G; h += TPB / 64) {
+            float v[TK / 64];
+            float tm = -INFINITY;
 #pragma unroll
-                for (int o = 16; o >= 1; o >>= 1) tm = fmaxf(tm, __shfl_xor(tm, o, 64));
-                const float mold = mrun[h];
-                const float mnew = fmaxf(mold, tm);
-                const float p = (j < nk) ? expf(v - mnew) : 0.0f;
+            for (int r = 0; r < TK / 64; r++) { v[r] = sc[h][lane + 64 * r]; tm = fmaxf(tm, v[r]); }
+            tm = wave_max(tm);
+            const float mold = mrun[h];
+            const float mnew = fmaxf(mold, tm);
+            float ps = 0.0f;
+#pragma unroll
+            for (int r = 0; r < TK / 64; r++) {
+                const uint32_t j = lane + 64 * r;
+                const float p = (j < nk) ? expf(v[r] - mnew) : 0.0f;
                 sc[h][j] = p;
-                float ps = p;
-#pragma unroll
-                for (int o = 16; o >= 1; o >>= 1) ps += __shfl_xor(ps, o, 64);
-                if (j == 0) {
-                    const float al = (mold == -INFINITY) ? 0.0f : expf(mold - mnew);
-                    alpha[h] = al;
-                    mrun[h] = mnew;
-                    srun[h] = srun[h] * al + ps;
-                }
+                ps += p;
+            }
+            ps = wave_sum(ps);
+            if (lane == 0) {
+                const float al = (mold == -INFINITY) ? 0.0f : expf(mold - mnew);
+                alpha[h] = al;
+                mrun[h] = mnew;
+                srun[h] = srun[h] * al + ps;
             }
         }
         __syncthreads();
+        // P*V
 #pragma unroll
         for (int h = 0; h < GMAX; h++) {
             if (h < (int)G) {
-                float v = acc[h] * alpha[h];
+                const float al = alpha[h];
 #pragma unroll
-                for (int u = 0; u < KT / KG; u++) v = fmaf(sc[h][kg + u * KG], vr[u], v);
-                acc[h] = v;
+                for (int e = 0; e < 8; e++) acc[h][e] *= al;
             }
         }
-        __syncthreads();
-    }
-
-    // Fold the key groups in a fixed order and write the triple.
-    if constexpr (KG > 1) {
 #pragma unroll
-        for (int h = 0; h < GMAX; h++)
-            if (h < (int)G) accx[(kg * GMAX + h) * HD + d] = acc[h];
-        __syncthreads();
-        if (kg == 0) {
+        for (int u = 0; u < VU; u++) {
+            const uint32_t key = kg + u * KGV;
+            float vf[8];
+            h8(vr[u], vf);
+            if (key >= nk) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) vf[e] = 0.0f;
+            }
 #pragma unroll
             for (int h = 0; h < GMAX; h++) {
                 if (h < (int)G) {
-                    float v = accx[h * HD + d];
-                    for (int g2 = 1; g2 < KG; g2++) v += accx[(g2 * GMAX + h) * HD + d];
-                    acc[h] = v;
+                    const float p = sc[h][key];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
                 }
             }
         }
+        if (more) load_v(ts + TK);
+        __syncthreads();
     }
-    if (kg == 0) {
+
+    // Fold the key groups: inside the wave, then the four waves in order.
+#pragma unroll
+    for (int h = 0; h < GMAX; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+        {
+            if (VC <= 2) acc[h][e] += lane_xor<2>(acc[h][e]);
+            if (VC <= 4) acc[h][e] += lane_xor<4>(acc[h][e]);
+            if (VC <= 8) acc[h][e] += lane_xor<8>(acc[h][e]);
+            if (VC <= 16) acc[h][e] += lane_xor<16>(acc[h][e]);
+            acc[h][e] += lane_xor<32>(acc[h][e]);
+        }
+    if (lane < (uint32_t)VC) {
 #pragma unroll
         for (int h = 0; h < GMAX; h++) {
-            if (h < (int)G) {
-                const size_t o = zoff + (size_t)(h0 + h) * ns + i;
-                a.acc[o * HD + d] = acc[h];
-                if (d == 0) {
-                    a.m[o] = mrun[h];
-                    a.s[o] = srun[h];
-                }
-            }
+            if (h >= (int)G) break;
+            float4 *dst = (float4 *)&red[wave][h * HD + vcc * 8];
+            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
         }
+    }
+    __syncthreads();
+    for (uint32_t e = t; e < G * HD; e += TPB) {
+        const uint32_t h = e / HD, d = e % HD;
+        const float v = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
+        a.acc[(zoff + (size_t)(h0 + h) * ns + i) * HD + d] = v;
+    }
+    if (t < (uint32_t)G) {
+        const size_t o = zoff + (size_t)(h0 + t) * ns + i;
+        a.m[o] = mrun[t];
+        a.s[o] = srun[t];
     }
 }
 
 extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
     if (!a->n_kv || a->n_heads % a->n_kv || a->n_heads / a->n_kv > GMAX) return hipErrorInvalidValue;
+    if (a->fuse_prep && (!a->steps || a->ntok != 1 || !a->qn || !a->kn || !a->cs || a->rope_dim > a->hd))
+        return hipErrorInvalidValue;
     const uint32_t gx = a->steps ? a->max_splits : a->n_splits;
     if (!gx || !a->ntok) return hipSuccess;
     dim3 grid(gx, a->n_kv, a->ntok);
@@ -948,20 +1180,26 @@ extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// LSE combine (+ optional sigmoid gate). Workgroup (head, token), one output
-// dim per thread. NaN/inf conventions of ref.c:265-373.
+// LSE combine (+ optional sigmoid gate). Workgroup (head, token). NaN/inf
+// conventions of ref.c:265-373: a NaN first max poisons, all-empty gives 0,
+// +inf maxima combine among themselves. The weighted sum over splits runs
+// with every load of a lane in flight: lane = (split group kg, 4-dim chunk),
+// each group summing its splits in increasing order, the groups then added in
+// order.
+template <int HD>
 __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
+    constexpr int C4 = HD / 4, KG = TPB / C4;
     __shared__ float wts[1024];
     __shared__ float red[4];
     __shared__ float bc;
-    const uint32_t z = blockIdx.y, h = blockIdx.x, t = threadIdx.x, hd = a.hd;
-    const uint32_t ns = a.steps ? dev_splits(a.steps[z].pos + 1, a.prefill) : a.n_splits;
+    __shared__ float4 part[KG][C4];
+    const uint32_t z = blockIdx.y, h = blockIdx.x, t = threadIdx.x;
+    const uint32_t ns = a.steps ? dev_splits(a.steps[z].pos + 1, a.prefill, a.split_cap) : a.n_splits;
     const size_t zoff = (size_t)z * a.n_heads * a.max_splits;
     const float *mh = a.m + zoff + (size_t)h * ns, *sh = a.s + zoff + (size_t)h * ns;
-    const float *acc = a.acc + (zoff + (size_t)h * ns) * hd;
-    float *oh = a.out + (size_t)z * a.out_tok + (size_t)h * hd;
+    const float4 *acc = (const float4 *)(a.acc + (zoff + (size_t)h * ns) * HD);
+    float *oh = a.out + (size_t)z * a.out_tok + (size_t)h * HD;
     const float *gate = a.gate ? a.gate + (size_t)z * a.q_tok + (size_t)h * a.q_stride : NULL;
-    // M: max over splits; a NaN first entry poisons the result (ref.c:288-300).
     float mx = -INFINITY;
     for (uint32_t k = t; k < ns; k += TPB) mx = fmaxf(mx, mh[k]);
     mx = wave_max(mx);
@@ -972,7 +1210,7 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
     const float M = bc;
     if (ns == 0 || M == -INFINITY || isnan(M)) {
         const float fill = isnan(M) ? M : 0.0f;
-        for (uint32_t dd = t; dd < hd; dd += TPB) oh[dd] = fill;
+        for (uint32_t dd = t; dd < HD; dd += TPB) oh[dd] = fill;
         return;
     }
     float sp = 0.0f;
@@ -983,15 +1221,41 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
         sp += sh[k] * w;
     }
     const float S = block_sum(sp, red);   // includes the barrier that publishes wts
-    for (uint32_t dd = t; dd < hd; dd += TPB) {
-        float o;
-        if (isnan(S)) {
-            o = S;
-        } else {
-            float num = 0.0f;
-            for (uint32_t k = 0; k < ns; k++) num = fmaf(acc[(size_t)k * hd + dd], wts[k], num);
-            o = S > 0.0f ? num / S : 0.0f;
+    const uint32_t c = t % C4, kg = t / C4;
+    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    uint32_t k = kg;
+    for (; k + 7 * KG < ns; k += 8 * KG) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = acc[(size_t)(k + u * KG) * C4 + c];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float w = wts[k + u * KG];
+            num.x = fmaf(v[u].x, w, num.x); num.y = fmaf(v[u].y, w, num.y);
+            num.z = fmaf(v[u].z, w, num.z); num.w = fmaf(v[u].w, w, num.w);
         }
+    }
+    for (; k < ns; k += KG) {
+        const float4 v = acc[(size_t)k * C4 + c];
+        const float w = wts[k];
+        num.x = fmaf(v.x, w, num.x); num.y = fmaf(v.y, w, num.y);
+        num.z = fmaf(v.z, w, num.z); num.w = fmaf(v.w, w, num.w);
+    }
+    part[kg][c] = num;
+    __syncthreads();
+    if (t >= (uint32_t)C4) return;
+    float4 tot = part[0][t];
+    for (int g2 = 1; g2 < KG; g2++) {
+        const float4 v = part[g2][t];
+        tot.x += v.x; tot.y += v.y; tot.z += v.z; tot.w += v.w;
+    }
+    const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t dd = 4 * t + e;
+        float o;
+        if (isnan(S)) o = S;
+        else o = S > 0.0f ? tv[e] / S : 0.0f;
         if (gate) o *= sigm(gate[dd]);
         oh[dd] = o;
     }
@@ -1000,7 +1264,13 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
 extern "C" hipError_t sgk_attn_combine(const sgk_attn *a, hipStream_t s) {
     if (!a->n_heads || !a->ntok) return hipSuccess;
     if (!a->steps && a->n_splits > 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attn_combine, dim3(a->n_heads, a->ntok), dim3(TPB), 0, s, *a);
+    dim3 grid(a->n_heads, a->ntok);
+#define HDCASE(H) case H: hipLaunchKernelGGL(k_attn_combine<H>, grid, dim3(TPB), 0, s, *a); break
+    switch (a->hd) {
+        HDCASE(16); HDCASE(32); HDCASE(64); HDCASE(128); HDCASE(256);
+    default: return hipErrorInvalidValue;
+    }
+#undef HDCASE
     return hipGetLastError();
 }
 
@@ -1071,87 +1341,234 @@ __device__ __forceinline__ void gdn_gates(float b, float a, float ssm_a, float d
     *decay = neg_exp ? expf(ssm_a * sp) : expf(-(expf(ssm_a) * sp));
 }
 
-template <int DK>
-__global__ void __launch_bounds__(TPB) k_gdn_step(sgk_gdn a) {
+// Sum over the 64 lanes of a wave of RW per-lane partials at once (one per
+// state row, RW <= 16): a transposed butterfly that halves the rows a lane
+// carries at each of the first log2(RW) steps (lane bits 5, 4, 3, 2 in that
+// order; the bit-2 step pairs lane l with l^7, which flips bit 2 and leaves
+// the pair in the same 8 lanes), then sums over the remaining lane bits.
+// Returns the full sum of row rows_row<RW>(lane); lanes that agree in the top
+// log2(RW) bits agree in the result. A fixed tree: reruns are bit-identical.
+template <int LVL>
+__device__ __forceinline__ float rows_partner(float v) {
+    if (LVL == 0) return lane_xor32(v);
+    if (LVL == 1) return lane_xor16(v);
+    if (LVL == 2) return lane_xor8(v);
+    return lane_mir8(v);
+}
+template <int RW, int LVL = 0>
+__device__ __forceinline__ void rows_fold(float *v, uint32_t lane) {
+    if constexpr (RW > 1) {
+        const bool hi = lane & (32u >> LVL);
+#pragma unroll
+        for (int r = 0; r < RW / 2; r++) {
+            const float mine = hi ? v[r + RW / 2] : v[r], other = hi ? v[r] : v[r + RW / 2];
+            v[r] = mine + rows_partner<LVL>(other);
+        }
+        rows_fold<RW / 2, LVL + 1>(v, lane);
+    } else {
+        // sum over the lane bits below the ones used for rows
+        float s = v[0];
+        s += lane_xor1(s);
+        s += lane_xor2(s);
+        if (LVL <= 3) s += lane_mir8(s);
+        if (LVL <= 2) s += lane_xor8(s);
+        if (LVL <= 1) s += lane_xor16(s);
+        if (LVL == 0) s += lane_xor32(s);
+        v[0] = s;
+    }
+}
+template <int RW>
+__device__ __forceinline__ float rows_sum(float *v, uint32_t lane) {
+    static_assert(RW >= 1 && RW <= 16, "rows_sum: 1..16 rows");
+    rows_fold<RW>(v, lane);
+    return v[0];
+}
+template <int RW>
+__device__ __forceinline__ uint32_t rows_row(uint32_t lane) {
+    constexpr int LB = RW >= 32 ? 5 : RW >= 16 ? 4 : RW >= 8 ? 3 : RW >= 4 ? 2 : RW >= 2 ? 1 : 0;
+    return LB ? (lane >> (6 - LB)) & (RW - 1) : 0;
+}
+template <int RW>
+__device__ __forceinline__ uint32_t rows_lane(uint32_t r) {   // a lane holding row r
+    constexpr int LB = RW >= 32 ? 5 : RW >= 16 ? 4 : RW >= 8 ? 3 : RW >= 4 ? 2 : RW >= 2 ? 1 : 0;
+    return LB ? r << (6 - LB) : 0;
+}
+
+// Gated DeltaNet decode step for one layer (reference ref.c:669-739 +
+// 1273-1330, kernels.metal:520-548, 742-805, 109-134). Workgroup (value head
+// h, row block jb) of GDN_NB per head: causal conv of the head's q/k channels
+// and of its rows' v channels over the position-indexed ring + SiLU, q/k RMS
+// (eps 1e-6, no weight) then q/dk and k/sqrt(dk), beta/decay, the rank-1
+// delta update of its dv/GDN_NB state rows with their readout, all requested
+// before any arithmetic. Wave w updates RW rows; each row's two dot products
+// are reduced for all of them at once (rows_sum). RMSNormGated needs the whole
+// head, so it is left to the output projection's gated prologue: each block
+// writes its readouts y, silu(z) of its rows and its rows' sum of squares,
+// with no synchronisation between blocks.
+#define GDN_TPB 256
+#define GDN_NB 4
+
+template <int DK, int RW>
+__global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
+    constexpr int EPL = DK >= 64 ? DK / 64 : 1;
+    constexpr int NW = GDN_TPB / 64;
     __shared__ float qk[2 * DK];
-    __shared__ float vv[GDN_ROWS];
-    __shared__ float red[4];
-    const uint32_t h = blockIdx.x, j0 = blockIdx.y * GDN_ROWS, t = threadIdx.x;
-    const uint32_t lane = t & 63, wave = t >> 6;
+    __shared__ float vv[NW * RW];
+    __shared__ float red[NW];
+    __shared__ float gts[2];
+    const uint32_t h = blockIdx.x, jb = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t dk = DK, dv = a.dv, key_dim = a.n_k * dk, cd = a.conv_dim;
+    const uint32_t rpb = (dv + GDN_NB - 1) / GDN_NB, jlo = jb * rpb, jhi = min(dv, jlo + rpb);
     const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k);
     const uint32_t pos = a.step->pos, keep = a.ksize - 1;
-    // This workgroup writes the ring slot of the q/k channels only when it is
-    // the first value head mapped to hk, row block 0 (one writer per channel).
-    const bool qk_writer = blockIdx.y == 0 && (a.tiled ? h < a.n_k : (h % (a.n_v / a.n_k)) == 0);
-    const uint32_t nrows = min((uint32_t)GDN_ROWS, dv - j0);
-    // The state rows depend on nothing computed here: request them first so
-    // their latency overlaps the conv / norm prologue.
-    constexpr int RPW = GDN_ROWS / (TPB / 64);
+    // The ring slot of the q/k channels is written by block 0 of the first
+    // value head mapped to hk only (one writer per channel).
+    const bool qk_writer = jb == 0 && (a.tiled ? h < a.n_k : (h % (a.n_v / a.n_k)) == 0);
+    const bool on = DK >= 64 || lane < (uint32_t)DK;
     float *Sh = a.S + (size_t)h * dv * dk;
-    float sr[RPW][drow<DK>::EPL];
-#pragma unroll
-    for (int u = 0; u < RPW; u++) {
-        const uint32_t r = wave + u * (TPB / 64);
-        if (r < nrows) row_load<DK>(sr[u], Sh + (size_t)(j0 + r) * dk, lane);
-    }
 
-    // 1. causal conv + SiLU on the channels this workgroup needs.
-    for (uint32_t e = t; e < 2 * dk + nrows; e += TPB) {
-        uint32_t ch;
-        if (e < dk) ch = hk * dk + e;
-        else if (e < 2 * dk) ch = key_dim + hk * dk + (e - dk);
-        else ch = 2 * key_dim + h * dv + j0 + (e - 2 * dk);
-        const float x = a.in[ch];
-        const float *w = a.conv_w + (size_t)ch * a.ksize;
+    // 1. requests: this wave's state rows, the conv inputs, the gate inputs,
+    //    and z / the norm weight for whichever block finishes the head.
+    const uint32_t j0 = jlo + wave * RW;
+    float sr[RW][EPL];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const uint32_t j = j0 + r;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) sr[r][e] = (j < jhi && on) ? Sh[(size_t)j * dk + lane * EPL + e] : 0.0f;
+    }
+    const uint32_t nch = 2 * dk + (jhi - jlo);
+    float cx = 0.0f, cw[4] = {0.0f, 0.0f, 0.0f, 0.0f}, cr[3] = {0.0f, 0.0f, 0.0f};
+    uint32_t ch = 0;
+    auto chan = [&](uint32_t e) -> uint32_t {
+        if (e < dk) return hk * dk + e;
+        if (e < 2 * dk) return key_dim + hk * dk + (e - dk);
+        return 2 * key_dim + h * dv + jlo + (e - 2 * dk);
+    };
+    if (t < nch) {
+        ch = chan(t);
+        cx = a.in[ch];
+        for (uint32_t jj = 0; jj <= keep; jj++) cw[jj] = a.conv_w[(size_t)ch * a.ksize + jj];
+        for (uint32_t jj = 0; jj < keep; jj++) cr[jj] = a.ring[(size_t)((pos + 4 - keep + jj) & 3) * cd + ch];
+    }
+    float zj = 0.0f;
+    if (t >= jlo && t < jhi) zj = a.z[(size_t)h * dv + t];
+    if (t == 0) {
+        const float *bb = a.in + cd + a.n_v * dv, *aa = bb + a.n_v;
+        float beta, decay;
+        gdn_gates(bb[h], aa[h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
+        gts[0] = beta;
+        gts[1] = decay;
+    }
+    // 2. conv + SiLU; this step's input into the ring slot pos % 4.
+    for (uint32_t e = t; e < nch; e += GDN_TPB) {
+        if (e != t) {
+            ch = chan(e);
+            cx = a.in[ch];
+            for (uint32_t jj = 0; jj <= keep; jj++) cw[jj] = a.conv_w[(size_t)ch * a.ksize + jj];
+            for (uint32_t jj = 0; jj < keep; jj++) cr[jj] = a.ring[(size_t)((pos + 4 - keep + jj) & 3) * cd + ch];
+        }
         float acc = 0.0f;
-        for (uint32_t jj = 0; jj < keep; jj++)
-            acc = fmaf(w[jj], a.ring[(size_t)((pos + 4 - keep + jj) & 3) * cd + ch], acc);
-        acc = fmaf(w[keep], x, acc);
+        for (uint32_t jj = 0; jj < keep; jj++) acc = fmaf(cw[jj], cr[jj], acc);
+        acc = fmaf(cw[keep], cx, acc);
         const float o = silu(acc);
         if (e < 2 * dk) qk[e] = o; else vv[e - 2 * dk] = o;
-        if (e >= 2 * dk || qk_writer) a.ring[(size_t)(pos & 3) * cd + ch] = x;
+        if (e >= 2 * dk || qk_writer) a.ring[(size_t)(pos & 3) * cd + ch] = cx;
     }
     __syncthreads();
-    // 2. q, k: RMS (eps 1e-6, no weight), then q / dk and k / sqrt(dk).
-    float vq = 0.0f, vk = 0.0f;
-    for (uint32_t i = t; i < dk; i += TPB) { vq = fmaf(qk[i], qk[i], vq); vk = fmaf(qk[dk + i], qk[dk + i], vk); }
-    const float ssq = block_sum(vq, red);
-    const float ssk = block_sum(vk, red);
-    const float rq = 1.0f / sqrtf(ssq / (float)dk + 1e-6f), rk = 1.0f / sqrtf(ssk / (float)dk + 1e-6f);
+    // 3. q, k: RMS (eps 1e-6, no weight), then q / dk and k / sqrt(dk).
+    if (wave < 2) {
+        const float *src = qk + wave * dk;
+        float ss = 0.0f;
+        for (uint32_t i = lane; i < dk; i += 64) ss = fmaf(src[i], src[i], ss);
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+    }
+    __syncthreads();
+    const float rq = 1.0f / sqrtf(red[0] / (float)dk + 1e-6f), rk = 1.0f / sqrtf(red[1] / (float)dk + 1e-6f);
     const float qsc = 1.0f / (float)dk, ksc = 1.0f / sqrtf((float)dk);
-    __syncthreads();
-    for (uint32_t i = t; i < dk; i += TPB) {
-        qk[i] = (qk[i] * rq) * qsc;
-        qk[dk + i] = (qk[dk + i] * rk) * ksc;
-    }
-    __syncthreads();
-    // 3. gates
-    const float *bb = a.in + cd + a.n_v * dv, *aa = bb + a.n_v;
-    float beta, decay;
-    gdn_gates(bb[h], aa[h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
-    // 4. rank-1 update and readout, 4 rows per wave.
+    float kq[EPL], qq[EPL];
 #pragma unroll
-    for (int u = 0; u < RPW; u++) {
-        const uint32_t r = wave + u * (TPB / 64);
-        if (r < nrows) {
-            const float y = delta_update<DK>(sr[u], qk + dk, qk, vv[r], beta, decay, lane);
-            row_store<DK>(sr[u], Sh + (size_t)(j0 + r) * dk, lane);
-            if (lane == 0) a.y[(size_t)h * dv + j0 + r] = y;
+    for (int e = 0; e < EPL; e++) {
+        const uint32_t i = on ? lane * EPL + e : 0;
+        qq[e] = on ? (qk[i] * rq) * qsc : 0.0f;
+        kq[e] = on ? (qk[dk + i] * rk) * ksc : 0.0f;
+    }
+    const float beta = gts[0], decay = gts[1];
+    // 4. rank-1 update and readout of this wave's rows.
+    float ss_part = 0.0f;
+    if (j0 < jhi) {
+        float part[RW];
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            float kv = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) { sr[r][e] *= decay; kv = fmaf(sr[r][e], kq[e], kv); }
+            part[r] = kv;
+        }
+        const uint32_t myrow = rows_row<RW>(lane);
+        const float kvr = rows_sum<RW>(part, lane);
+        const float vj = j0 + myrow < jhi ? vv[wave * RW + myrow] : 0.0f;
+        const float dmine = (vj - kvr) * beta;
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const float dr = lane_read(dmine, rows_lane<RW>(r));
+            float y = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) { sr[r][e] = fmaf(kq[e], dr, sr[r][e]); y = fmaf(sr[r][e], qq[e], y); }
+            part[r] = y;
+        }
+        const float yr = rows_sum<RW>(part, lane);
+        const bool owner = (lane & (64 / RW - 1)) == 0 && j0 + myrow < jhi;
+        if (owner) a.y[(size_t)h * dv + j0 + myrow] = yr;
+        // sum of squares of this wave's readouts, in row order
+        float yy[RW];
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const float yv = lane_read(yr, rows_lane<RW>(r));
+            yy[r] = (j0 + r < jhi) ? yv * yv : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < RW; r++) ss_part += yy[r];
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const uint32_t j = j0 + r;
+            if (j < jhi && on) {
+#pragma unroll
+                for (int e = 0; e < EPL; e++) Sh[(size_t)j * dk + lane * EPL + e] = sr[r][e];
+            }
         }
     }
+    if (lane == 0) red[wave] = ss_part;
+    __syncthreads();
+    // 5. this block's sum of squares and silu(z) of its rows: the output
+    //    projection's gated prologue finishes RMSNormGated from them.
+    if (t == 0) {
+        float sb = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) sb += red[w];
+        a.ss[(size_t)h * GDN_NB + jb] = sb;
+    }
+    if (t >= jlo && t < jhi) a.out[(size_t)h * dv + t] = silu(zj);
 }
 
 extern "C" hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s) {
     if (a->ksize < 1 || a->ksize > 4 || !a->n_k || a->n_v % a->n_k) return hipErrorInvalidValue;
-    dim3 grid(a->n_v, (a->dv + GDN_ROWS - 1) / GDN_ROWS);
+    if (!a->dv || a->dv > GDN_TPB || !a->z || !a->out || !a->y || !a->ss) return hipErrorInvalidValue;
+    const uint32_t rpb = (a->dv + GDN_NB - 1) / GDN_NB;    // rows per block, at most 64
+    dim3 grid(a->n_v, GDN_NB);
+#define DKCASE(D) case D:                                                                          \
+        if (rpb <= 4) hipLaunchKernelGGL((k_gdn_step<D, 1>), grid, dim3(GDN_TPB), 0, s, *a);        \
+        else if (rpb <= 8) hipLaunchKernelGGL((k_gdn_step<D, 2>), grid, dim3(GDN_TPB), 0, s, *a);   \
+        else if (rpb <= 16) hipLaunchKernelGGL((k_gdn_step<D, 4>), grid, dim3(GDN_TPB), 0, s, *a);  \
+        else if (rpb <= 32) hipLaunchKernelGGL((k_gdn_step<D, 8>), grid, dim3(GDN_TPB), 0, s, *a);  \
+        else hipLaunchKernelGGL((k_gdn_step<D, 16>), grid, dim3(GDN_TPB), 0, s, *a);                \
+        break
     switch (a->dk) {
-    case 32: hipLaunchKernelGGL(k_gdn_step<32>, grid, dim3(TPB), 0, s, *a); break;
-    case 64: hipLaunchKernelGGL(k_gdn_step<64>, grid, dim3(TPB), 0, s, *a); break;
-    case 128: hipLaunchKernelGGL(k_gdn_step<128>, grid, dim3(TPB), 0, s, *a); break;
-    case 256: hipLaunchKernelGGL(k_gdn_step<256>, grid, dim3(TPB), 0, s, *a); break;
+        DKCASE(32); DKCASE(64); DKCASE(128); DKCASE(256);
     default: return hipErrorInvalidValue;
     }
+#undef DKCASE
     return hipGetLastError();
 }
 

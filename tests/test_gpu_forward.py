@@ -162,3 +162,44 @@ def test_2b_greedy_64_tokens_identical_to_reference(gpu):
     gen = gpu.decode_greedy(prompt[-1], len(prompt) - 1, len(gold["gen_ids"]))
     syn.close()
     assert gen.tolist() == gold["gen_ids"]
+
+
+HD256 = dict(n_layers=4, n_heads=8, n_kv_heads=2, head_dim=256, hidden=256, ffn_hidden=512,
+             vocab=800, rope_theta=1e7, rms_eps=1e-6, tied_embeddings=False, rope_dim=64,
+             full_attn_interval=4, n_k_heads=2, n_v_heads=4, head_k_dim=64, head_v_dim=64,
+             conv_kernel=4, attn_output_gate=True)
+
+
+def test_split_cap_override_multi_tile_decode_vs_oracle(gpu, monkeypatch):
+    """SURGE_SPLITK_GQA_CAP=4 (the reference's gate knob, surge.h:1239-1256)
+    puts up to 75 keys in each split at 300 positions: with head_dim 256 the
+    fused decode partial then walks two key tiles, the second loaded after its
+    own store of the new K/V row. Logits within 1e-3 of the oracle and
+    argmax identical at sampled positions; the override is parsed, reported
+    and used."""
+    syn = S.Synth(HD256, S.SG_T_Q8_0, seed=9)
+    gpu.load_model(syn.model)
+    monkeypatch.setenv("SURGE_SPLITK_GQA_CAP", "4")
+    gpu.state_new(320)
+    assert gpu.split_cap() == 4
+    assert gpu.n_splits_at(300) == 4 and gpu.n_splits_at(100) == 2
+    rng = np.random.default_rng(4)
+    ids = rng.integers(0, HD256["vocab"], 300).tolist()
+    rm = O.RefModel(O.oracle(), syn.model, 320, kv_f16=True)
+    worst = 0.0
+    for p, t in enumerate(ids):
+        g = gpu.forward(t, p)
+        o = rm.forward(t, p)
+        if p % 23 == 0 or p >= 290:
+            worst = max(worst, rel(g, o))
+            assert np.argmax(g) == np.argmax(o), f"argmax differs at position {p}"
+    rm.close()
+    assert worst < 1e-3, worst
+    for bad in (" 4", "+4", "3", "1025", "12x", "-8"):
+        monkeypatch.setenv("SURGE_SPLITK_GQA_CAP", bad)
+        with pytest.raises(S.SurgeError):
+            gpu.state_new(64)
+    monkeypatch.delenv("SURGE_SPLITK_GQA_CAP")
+    gpu.state_new(64)
+    assert gpu.split_cap() == 256
+    syn.close()
