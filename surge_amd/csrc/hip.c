@@ -99,6 +99,7 @@ struct sg_gpu {
     bool have_state;
     uint32_t max_ctx, used, max_splits;
     uint32_t split_cap;     /* resolved decode split cap (SURGE_SPLITK_GQA_CAP or SGK_MAX_SPLITS) */
+    uint32_t gdn_blocks;    /* DeltaNet step workgroups per value head (1 or SGK_GDN_BLOCKS) */
     float *cs_table;
     float *x, *act, *ctx, *ybuf, *gbuf, *ffg, *logits, *am, *as, *aacc;
     uint32_t *amax_scratch, *hist;
@@ -966,11 +967,14 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             d.dk = c->head_k_dim; d.dv = c->head_v_dim; d.conv_dim = g->conv_dim; d.ksize = c->conv_kernel;
             d.tiled = g->model->v_heads_tiled; d.neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
             d.z = g->act + g->conv_dim; d.norm_w = L->ssm_norm; d.out = g->gbuf; d.eps = c->rms_eps;
-            d.ss = g->gss;
+            d.ss = g->gss; d.blocks = g->gdn_blocks;
             if ((e = sgk_gdn_step(&d, s)) != hipSuccess) return e;
-            /* RMSNormGated in the out projection's prologue */
-            o.x = g->ybuf; o.x2 = g->gbuf; o.gss = g->gss; o.nw = L->ssm_norm; o.gdv = c->head_v_dim;
-            o.pro = SGK_PRO_GATED;
+            if (g->gdn_blocks == 1) {
+                o.x = g->gbuf; o.pro = SGK_PRO_NONE;          /* the step finished RMSNormGated */
+            } else {                                          /* RMSNormGated in the out projection's prologue */
+                o.x = g->ybuf; o.x2 = g->gbuf; o.gss = g->gss; o.nw = L->ssm_norm; o.gdv = c->head_v_dim;
+                o.pro = SGK_PRO_GATED;
+            }
         }
         if ((e = sgk_gemv_launch(&o, s)) != hipSuccess) return e;
         sgk_gemv f = {0};
@@ -1030,6 +1034,18 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     const sg_cfg *c = &g->cfg;
     g->max_ctx = max_ctx;
     g->split_cap = cap;
+    /* One workgroup per DeltaNet value head finishes RMSNormGated itself
+     * (head_v_dim <= 128); wider heads use SGK_GDN_BLOCKS row blocks and the
+     * out projection's gated prologue. SURGE_GDN_BLOCKS=1|4 overrides. */
+    g->gdn_blocks = c->head_v_dim <= 128 ? 1 : SGK_GDN_BLOCKS;
+    {
+        const char *gb = getenv("SURGE_GDN_BLOCKS");
+        if (gb && gb[0]) {
+            if (!strcmp(gb, "4")) g->gdn_blocks = SGK_GDN_BLOCKS;
+            else if (!strcmp(gb, "1") && c->head_v_dim <= 128) g->gdn_blocks = 1;
+            else return errf("gpu: SURGE_GDN_BLOCKS='%s' must be 1 (head_v_dim <= 128) or 4", gb);
+        }
+    }
     g->max_splits = sgk_n_splits_cap(max_ctx, cap);
     sg_err e = SG_OK;
     uint32_t act_rows = 0;
@@ -1356,6 +1372,7 @@ sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which) {
         case 1:
             M = &L->out; a.y = g->x; a.epi = SGK_EPI_ADD;
             if (L->attn) { a.x = g->ctx; a.pro = SGK_PRO_NONE; }
+            else if (g->gdn_blocks == 1) { a.x = g->gbuf; a.pro = SGK_PRO_NONE; }
             else {
                 a.x = g->ybuf; a.x2 = g->gbuf; a.gss = g->gss; a.nw = L->ssm_norm; a.gdv = c->head_v_dim;
                 a.pro = SGK_PRO_GATED;

@@ -156,6 +156,8 @@ typedef struct {
     float *out;
     float eps;
     float *ss;
+    uint32_t blocks;        /* workgroups per head: 1 (the step finishes RMSNormGated into out)
+                             * or SGK_GDN_BLOCKS (out = silu(z), y and ss for the gated prologue) */
 } sgk_gdn;
 #define SGK_GDN_MAX_DV 256u
 #define SGK_GDN_BLOCKS 4u

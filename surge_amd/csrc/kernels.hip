@@ -381,13 +381,13 @@ __global__ void __launch_bounds__(TPB) k_gemv_f32(sgk_gemv a) {
 
 #define LTPB 1024
 #define LW (LTPB / 64)
-#define LU 3                      // chunks per lane per batch
 
 struct long_task { uint32_t row, c0, c1, slot; };
 struct long_plan { uint32_t nch, F, nb, S, nbr, G, b, base; };
 
 // The k-th batch of wave w; false past the end. slot: LW*LW+ for a whole row,
 // else the LDS partial slot (i*LW + part).
+template <int LU>
 __device__ __forceinline__ bool long_task_at(const long_plan &p, uint32_t w, uint32_t k, long_task &t) {
     const uint32_t nfull = p.F * p.nbr;
     if (k < nfull) {
@@ -412,9 +412,11 @@ __device__ __forceinline__ bool long_task_at(const long_plan &p, uint32_t w, uin
     return true;
 }
 
+template <int LU>
 struct long_batch { uint4 q[LU]; uint16_t d[LU]; };
 
-__device__ __forceinline__ void long_load(long_batch &bt, const sgk_gemv &a, const long_task &t, uint32_t lane) {
+template <int LU>
+__device__ __forceinline__ void long_load(long_batch<LU> &bt, const sgk_gemv &a, const long_task &t, uint32_t lane) {
     const uint4 *q = (const uint4 *)(a.qs + (size_t)t.row * a.cols);
     const uint16_t *dr = a.d + (size_t)t.row * (a.cols >> 5);
 #pragma unroll
@@ -424,7 +426,8 @@ __device__ __forceinline__ void long_load(long_batch &bt, const sgk_gemv &a, con
     }
 }
 
-__device__ __forceinline__ float long_fma(const long_batch &bt, const float *xs, const long_task &t, uint32_t lane,
+template <int LU>
+__device__ __forceinline__ float long_fma(const long_batch<LU> &bt, const float *xs, const long_task &t, uint32_t lane,
                                           float acc) {
 #pragma unroll
     for (int u = 0; u < LU; u++) {
@@ -437,7 +440,7 @@ __device__ __forceinline__ float long_fma(const long_batch &bt, const float *xs,
     return acc;
 }
 
-template <int EPI>
+template <int EPI, int LU>
 __global__ void __launch_bounds__(LTPB) k_gemv_q8_long(sgk_gemv a) {
     extern __shared__ float lds[];
     float *xs = lds, *part = lds + a.cols;          // part[LW * LW]
@@ -453,9 +456,9 @@ __global__ void __launch_bounds__(LTPB) k_gemv_q8_long(sgk_gemv a) {
     p.S = p.nb ? LW / p.nb : 1;
     p.nbr = (p.nch + 64 * LU - 1) / (64 * LU);
     long_task t;
-    bool have = long_task_at(p, w, 0, t);
-    long_batch cur;
-    if (have) long_load(cur, a, t, lane);
+    bool have = long_task_at<LU>(p, w, 0, t);
+    long_batch<LU> cur;
+    if (have) long_load<LU>(cur, a, t, lane);
     {   // stage x: 16-byte loads, up to four in flight per thread
         const uint32_t n4 = a.cols >> 2;
         const float4 *x4 = (const float4 *)a.x;
@@ -477,10 +480,10 @@ __global__ void __launch_bounds__(LTPB) k_gemv_q8_long(sgk_gemv a) {
     float acc = 0.0f;
     for (uint32_t k = 0; have; k++) {
         long_task tn;
-        const bool hn = long_task_at(p, w, k + 1, tn);
-        long_batch nxt;
-        if (hn) long_load(nxt, a, tn, lane);
-        acc = long_fma(cur, xs, t, lane, acc);
+        const bool hn = long_task_at<LU>(p, w, k + 1, tn);
+        long_batch<LU> nxt;
+        if (hn) long_load<LU>(nxt, a, tn, lane);
+        acc = long_fma<LU>(cur, xs, t, lane, acc);
         if (!hn || tn.row != t.row) {
             acc = wave_sum(acc);
             if (t.slot == 0xffffffffu) {
@@ -539,6 +542,42 @@ static hipError_t allow_lds(const void *kern, size_t lds) {
 
 
 
+// Row groups the busiest CU carries when `blocks` workgroups of TPB/64 waves
+// split `groups` row groups (wave i of the grid-stride order takes
+// ceil or floor of groups/waves) and workgroup b runs on CU b mod cus.
+static uint32_t gemv_cu_load(uint32_t groups, uint32_t blocks, uint32_t cus) {
+    const uint32_t wpb = TPB / 64, waves = blocks * wpb, q = groups / waves, r = groups % waves;
+    uint32_t worst = 0;
+    for (uint32_t c = 0; c < cus && c < blocks; c++) {
+        uint32_t load = 0;
+        for (uint32_t b = c; b < blocks; b += cus)
+            for (uint32_t w = 0; w < wpb; w++) load += q + (b * wpb + w < r ? 1u : 0u);
+        worst = load > worst ? load : worst;
+    }
+    return worst;
+}
+
+// Grid for the row-group GEMV: resident workgroups only. Candidates are the
+// wave-balanced count (every wave gets ceil(groups / waves) groups, as few
+// waves as that allows) and every whole number of workgroups per CU up to
+// residency; the one whose busiest CU carries the fewest row groups wins, ties
+// going to the count nearest three workgroups per CU (measured best on
+// MI355X for these kernels: enough waves to hide latency, few prologues).
+static uint32_t gemv_grid(uint32_t groups, uint32_t per) {
+    const uint32_t cus = (uint32_t)device_cus(), wpb = TPB / 64;
+    const uint32_t max_waves = cus * per * wpb;
+    const uint32_t k = (groups + max_waves - 1) / max_waves;
+    const uint32_t waves = (groups + k - 1) / k;
+    uint32_t best = (waves + wpb - 1) / wpb, best_load = gemv_cu_load(groups, best, cus);
+    for (uint32_t m = 1; m <= per; m++) {
+        const uint32_t b = cus * m, load = gemv_cu_load(groups, b, cus);
+        const uint32_t d_new = b > 3 * cus ? b - 3 * cus : 3 * cus - b;
+        const uint32_t d_old = best > 3 * cus ? best - 3 * cus : 3 * cus - best;
+        if (load < best_load || (load == best_load && d_new < d_old)) { best = b; best_load = load; }
+    }
+    return best;
+}
+
 // Launch k_gemv_q8<R,...>: resident workgroups only, sized so every wave gets
 // ceil(groups / waves) row groups and no wave gets one fewer than another by
 // more than one (the caller may fix the count with tune_blocks).
@@ -559,11 +598,15 @@ static hipError_t launch_q8(const sgk_gemv &a, size_t lds, hipStream_t s) {
     }
     const uint32_t groups = (a.rows + R - 1) / R;
     uint32_t blocks = a.tune_blocks;
-    if (!blocks) {
-        const uint32_t max_waves = (uint32_t)device_cus() * per * (TPB / 64);
-        const uint32_t k = (groups + max_waves - 1) / max_waves;
-        const uint32_t waves = (groups + k - 1) / k;
-        blocks = (waves + TPB / 64 - 1) / (TPB / 64);
+    if (!blocks) {                                  // per (groups) of this instantiation
+        static uint32_t seen_g[16], seen_b[16];
+        static int ng = 0;
+        for (int i = 0; i < ng && !blocks; i++)
+            if (seen_g[i] == groups) blocks = seen_b[i];
+        if (!blocks) {
+            blocks = gemv_grid(groups, per);
+            if (ng < 16) { seen_g[ng] = groups; seen_b[ng] = blocks; ng++; }
+        }
     }
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(TPB), lds, s, a);
     return hipGetLastError();
@@ -584,9 +627,11 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         hipLaunchKernelGGL((k_gemv_f32<PRO, EPI>), dim3(min((groups + 3) / 4, 4096u)), dim3(TPB), lds, s, *a);
         return hipGetLastError();
     }
-    if (PRO == SGK_PRO_NONE && EPI != SGK_EPI_SWIGLU && a->cols > 8192) {
+    if (PRO == SGK_PRO_NONE && EPI != SGK_EPI_SWIGLU && a->cols > 8192 && a->tune_r != 7 && a->tune_r != 8) {
         const size_t lds = ((size_t)a->cols + LW * LW) * 4;
-        auto kern = k_gemv_q8_long<EPI == SGK_EPI_ADD ? SGK_EPI_ADD : SGK_EPI_STORE>;
+        constexpr int LE = EPI == SGK_EPI_ADD ? SGK_EPI_ADD : SGK_EPI_STORE;
+        auto kern = a->tune_r == 3 ? k_gemv_q8_long<LE, 4> : a->tune_r == 5 ? k_gemv_q8_long<LE, 6>
+                  : a->tune_r == 6 ? k_gemv_q8_long<LE, 8> : k_gemv_q8_long<LE, 3>;
         hipError_t e = allow_lds((const void *)kern, lds);
         if (e != hipSuccess) return e;
         const uint32_t blocks = a->tune_blocks ? a->tune_blocks : (uint32_t)device_cus();
@@ -594,7 +639,7 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         return hipGetLastError();
     }
     const size_t lds = (size_t)a->cols * 4;
-    const int R = EPI == SGK_EPI_SWIGLU ? 2 : (a->tune_r == 1 ? 1 : a->tune_r == 4 ? 4 : 2);
+    const int R = EPI == SGK_EPI_SWIGLU ? 2 : (a->tune_r == 1 ? 1 : (a->tune_r == 4 || a->tune_r == 8) ? 4 : 2);
     if (R == 4) return launch_q8<4, PRO, EPI>(*a, lds, s);
     if (R == 1) return launch_q8<1, PRO, (EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI)>(*a, lds, s);
     return launch_q8<2, PRO, EPI>(*a, lds, s);
@@ -900,9 +945,9 @@ __device__ __forceinline__ float prep_elem(const float *x, float r, const float 
 // (one writer per (position, kv head)).
 // ---------------------------------------------------------------------------
 
-template <int HD>
+template <int HD, int DPTMAX = 64>
 struct attn_geom {
-    static constexpr int DPT = HD < 64 ? HD : 64;   // score dims per lane
+    static constexpr int DPT = HD < DPTMAX ? HD : DPTMAX;   // score dims per lane
     static constexpr int TPK = HD / DPT;            // lanes per key
     static constexpr int TK = TPB / TPK;            // keys per tile
     static constexpr int KU = DPT / 8;              // K uint4 per lane
@@ -922,9 +967,9 @@ __device__ __forceinline__ void h8(const uint4 r, float *f) {
     }
 }
 
-template <int HD>
+template <int HD, int DPTMAX>
 __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
-    using Gm = attn_geom<HD>;
+    using Gm = attn_geom<HD, DPTMAX>;
     constexpr int DPT = Gm::DPT, TPK = Gm::TPK, TK = Gm::TK, KU = Gm::KU, VC = Gm::VC, KGV = Gm::KGV,
                   VU = Gm::VU, QP = Gm::QP, QROW = Gm::QROW;
     __shared__ float qsh[GMAX * QROW];
@@ -961,10 +1006,6 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
             vr[u] = ((const uint4 *)(vc + ((size_t)key * n_kv + hk) * HD))[vcc];
         }
     };
-    // The first tile's K and V depend only on the split: request them before
-    // anything else so their latency overlaps the query staging.
-    if (t0 < t1) { load_k(t0); load_v(t0); }
-
     if (a.fuse_prep) {
         // One round trip for everything the prep reads: raw q rows of the
         // group, and for the split holding the position its raw k and v rows,
@@ -976,12 +1017,31 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
         const float *krow = q + (size_t)a.n_heads * a.q_stride + (size_t)hk * HD;
         const float *vrow = krow + (size_t)n_kv * HD;
         const float *csrow = a.cs + (size_t)pos * a.rope_dim;
-        float vraw[(HD + TPB - 1) / TPB];
-        for (uint32_t e = t; e < G * HD; e += TPB) raw[e] = q[(size_t)(h0 + e / HD) * a.q_stride + e % HD];
-        for (uint32_t d = t; d < HD; d += TPB) {
-            qn_s[d] = a.qn[d];
-            cs_s[d] = d < a.rope_dim ? csrow[d] : 0.0f;
-            if (kv_writer) { raw[GMAX * HD + d] = krow[d]; kn_s[d] = a.kn[d]; vraw[d / TPB] = vrow[d]; }
+        // Loads retire in order: the prep's few loads go first, into
+        // registers; then the first tile's K and V (their addresses depend
+        // only on the split), whose latency overlaps the prep's arithmetic.
+        constexpr int QPT = (GMAX * HD + TPB - 1) / TPB;  // q values per thread
+        float qv[QPT], kr0 = 0.0f, vr0 = 0.0f, qn0 = 0.0f, kn0 = 0.0f, cs0 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < QPT; k++) {
+            const uint32_t e = t + k * TPB;
+            qv[k] = e < G * HD ? q[(size_t)(h0 + e / HD) * a.q_stride + e % HD] : 0.0f;
+        }
+        if (t < HD) {
+            qn0 = a.qn[t];
+            cs0 = t < a.rope_dim ? csrow[t] : 0.0f;
+            if (kv_writer) { kr0 = krow[t]; kn0 = a.kn[t]; vr0 = vrow[t]; }
+        }
+        if (t0 < t1) { load_k(t0); load_v(t0); }
+#pragma unroll
+        for (int k = 0; k < QPT; k++) {
+            const uint32_t e = t + k * TPB;
+            if (e < G * HD) raw[e] = qv[k];
+        }
+        if (t < HD) {
+            qn_s[t] = qn0;
+            cs_s[t] = cs0;
+            if (kv_writer) { raw[GMAX * HD + t] = kr0; kn_s[t] = kn0; }
         }
         __syncthreads();
         for (uint32_t h = wave; h <= (uint32_t)G; h += TPB / 64) {
@@ -1001,7 +1061,7 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
             const size_t at = ((size_t)pos * n_kv + hk) * HD;
             for (uint32_t d = t; d < HD; d += TPB) {
                 const uint16_t kh = f2h(prep_elem(raw + GMAX * HD, rn[G], kn_s, cs_s, d, a.rope_dim));
-                const uint16_t vh = f2h(vraw[d / TPB]);
+                const uint16_t vh = f2h(vr0);
                 ((uint16_t *)a.kc)[at + d] = kh;
                 ((uint16_t *)a.vc)[at + d] = vh;
                 knew[d] = kh;
@@ -1023,9 +1083,18 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
                 if (t0 + kg + u * KGV == pos) vr[u] = ((const uint4 *)vnew)[vcc];
         }
     } else {
-        for (uint32_t e = t; e < G * HD; e += TPB) {
-            const uint32_t h = e / HD, d = e % HD;
-            qsh[h * QROW + (d / DPT) * QP + d % DPT] = q[(size_t)(h0 + h) * a.q_stride + d];
+        constexpr int QPT = (GMAX * HD + TPB - 1) / TPB;
+        float qv[QPT];
+#pragma unroll
+        for (int k = 0; k < QPT; k++) {
+            const uint32_t e = t + k * TPB;
+            qv[k] = e < G * HD ? q[(size_t)(h0 + e / HD) * a.q_stride + e % HD] : 0.0f;
+        }
+        if (t0 < t1) { load_k(t0); load_v(t0); }
+#pragma unroll
+        for (int k = 0; k < QPT; k++) {
+            const uint32_t e = t + k * TPB, h = e / HD, d = e % HD;
+            if (e < G * HD) qsh[h * QROW + (d / DPT) * QP + d % DPT] = qv[k];
         }
     }
     if (t < (uint32_t)G) { mrun[t] = -INFINITY; srun[t] = 0.0f; }
@@ -1066,6 +1135,8 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
         for (int h = 0; h < GMAX; h++) {
             if (TPK >= 2) part[h] += lane_xor1(part[h]);
             if (TPK >= 4) part[h] += lane_xor2(part[h]);
+            if (TPK >= 8) part[h] += lane_xor<4>(part[h]);
+            if (TPK >= 16) part[h] += lane_xor8(part[h]);
         }
         if (kp == 0) {
 #pragma unroll
@@ -1075,19 +1146,24 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
         __syncthreads();
         // softmax: one wave per head over the tile
         for (uint32_t h = wave; h < (uint32_t)G; h += TPB / 64) {
-            float v[TK / 64];
+            constexpr int NV = TK >= 64 ? TK / 64 : 1;   // keys per lane
+            float v[NV];
             float tm = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < TK / 64; r++) { v[r] = sc[h][lane + 64 * r]; tm = fmaxf(tm, v[r]); }
+            for (int r = 0; r < NV; r++) {
+                const uint32_t j = lane + 64 * r;
+                v[r] = j < (uint32_t)TK ? sc[h][j] : -INFINITY;
+                tm = fmaxf(tm, v[r]);
+            }
             tm = wave_max(tm);
             const float mold = mrun[h];
             const float mnew = fmaxf(mold, tm);
             float ps = 0.0f;
 #pragma unroll
-            for (int r = 0; r < TK / 64; r++) {
+            for (int r = 0; r < NV; r++) {
                 const uint32_t j = lane + 64 * r;
                 const float p = (j < nk) ? expf(v[r] - mnew) : 0.0f;
-                sc[h][j] = p;
+                if (j < (uint32_t)TK) sc[h][j] = p;
                 ps += p;
             }
             ps = wave_sum(ps);
@@ -1171,7 +1247,7 @@ extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
     const uint32_t gx = a->steps ? a->max_splits : a->n_splits;
     if (!gx || !a->ntok) return hipSuccess;
     dim3 grid(gx, a->n_kv, a->ntok);
-#define HDCASE(H) case H: hipLaunchKernelGGL(k_attn_partial<H>, grid, dim3(TPB), 0, s, *a); break
+#define HDCASE(H) case H: hipLaunchKernelGGL((k_attn_partial<H, 64>), grid, dim3(TPB), 0, s, *a); break
     switch (a->hd) {
         HDCASE(16); HDCASE(32); HDCASE(64); HDCASE(128); HDCASE(256);
     default: return hipErrorInvalidValue;
@@ -1405,17 +1481,16 @@ __device__ __forceinline__ uint32_t rows_lane(uint32_t r) {   // a lane holding 
 // head, so it is left to the output projection's gated prologue: each block
 // writes its readouts y, silu(z) of its rows and its rows' sum of squares,
 // with no synchronisation between blocks.
-#define GDN_TPB 256
-#define GDN_NB 4
-
-template <int DK, int RW>
+template <int DK, int RW, int NB, int GDN_TPB>
 __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
+    constexpr int GDN_NB = NB;
     constexpr int EPL = DK >= 64 ? DK / 64 : 1;
     constexpr int NW = GDN_TPB / 64;
     __shared__ float qk[2 * DK];
     __shared__ float vv[NW * RW];
     __shared__ float red[NW];
     __shared__ float gts[2];
+    __shared__ float ysh[NB == 1 ? SGK_GDN_MAX_DV : 1];
     const uint32_t h = blockIdx.x, jb = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t dk = DK, dv = a.dv, key_dim = a.n_k * dk, cd = a.conv_dim;
     const uint32_t rpb = (dv + GDN_NB - 1) / GDN_NB, jlo = jb * rpb, jhi = min(dv, jlo + rpb);
@@ -1427,16 +1502,9 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
     const bool on = DK >= 64 || lane < (uint32_t)DK;
     float *Sh = a.S + (size_t)h * dv * dk;
 
-    // 1. requests: this wave's state rows, the conv inputs, the gate inputs,
-    //    and z / the norm weight for whichever block finishes the head.
-    const uint32_t j0 = jlo + wave * RW;
-    float sr[RW][EPL];
-#pragma unroll
-    for (int r = 0; r < RW; r++) {
-        const uint32_t j = j0 + r;
-#pragma unroll
-        for (int e = 0; e < EPL; e++) sr[r][e] = (j < jhi && on) ? Sh[(size_t)j * dk + lane * EPL + e] : 0.0f;
-    }
+    // 1. requests, smallest first (loads retire in order, so the conv inputs
+    //    must not queue behind the state rows): the conv inputs, z and the
+    //    gate inputs, then this wave's state rows.
     const uint32_t nch = 2 * dk + (jhi - jlo);
     float cx = 0.0f, cw[4] = {0.0f, 0.0f, 0.0f, 0.0f}, cr[3] = {0.0f, 0.0f, 0.0f};
     uint32_t ch = 0;
@@ -1460,6 +1528,15 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
         gts[0] = beta;
         gts[1] = decay;
     }
+    const uint32_t j0 = jlo + wave * RW;
+    float sr[RW][EPL];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const uint32_t j = j0 + r;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) sr[r][e] = (j < jhi && on) ? Sh[(size_t)j * dk + lane * EPL + e] : 0.0f;
+    }
+
     // 2. conv + SiLU; this step's input into the ring slot pos % 4.
     for (uint32_t e = t; e < nch; e += GDN_TPB) {
         if (e != t) {
@@ -1520,7 +1597,10 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
         }
         const float yr = rows_sum<RW>(part, lane);
         const bool owner = (lane & (64 / RW - 1)) == 0 && j0 + myrow < jhi;
-        if (owner) a.y[(size_t)h * dv + j0 + myrow] = yr;
+        if (owner) {
+            if (NB == 1) ysh[j0 + myrow] = yr;
+            else a.y[(size_t)h * dv + j0 + myrow] = yr;
+        }
         // sum of squares of this wave's readouts, in row order
         float yy[RW];
 #pragma unroll
@@ -1541,6 +1621,19 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
     }
     if (lane == 0) red[wave] = ss_part;
     __syncthreads();
+    if (NB == 1) {
+        // 5. the whole head is here: RMSNormGated in place (ref.c:1322-1330),
+        //    silu(z) * (y * rsqrt(mean y^2 + eps) * w).
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) tot += red[w];
+        const float r = 1.0f / sqrtf(tot / (float)dv + a.eps);
+        if (t < dv) {
+            const float yv = ysh[t];
+            a.out[(size_t)h * dv + t] = silu(zj) * ((yv * r) * a.norm_w[t]);
+        }
+        return;
+    }
     // 5. this block's sum of squares and silu(z) of its rows: the output
     //    projection's gated prologue finishes RMSNormGated from them.
     if (t == 0) {
@@ -1554,15 +1647,36 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
 
 extern "C" hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s) {
     if (a->ksize < 1 || a->ksize > 4 || !a->n_k || a->n_v % a->n_k) return hipErrorInvalidValue;
-    if (!a->dv || a->dv > GDN_TPB || !a->z || !a->out || !a->y || !a->ss) return hipErrorInvalidValue;
-    const uint32_t rpb = (a->dv + GDN_NB - 1) / GDN_NB;    // rows per block, at most 64
-    dim3 grid(a->n_v, GDN_NB);
-#define DKCASE(D) case D:                                                                          \
-        if (rpb <= 4) hipLaunchKernelGGL((k_gdn_step<D, 1>), grid, dim3(GDN_TPB), 0, s, *a);        \
-        else if (rpb <= 8) hipLaunchKernelGGL((k_gdn_step<D, 2>), grid, dim3(GDN_TPB), 0, s, *a);   \
-        else if (rpb <= 16) hipLaunchKernelGGL((k_gdn_step<D, 4>), grid, dim3(GDN_TPB), 0, s, *a);  \
-        else if (rpb <= 32) hipLaunchKernelGGL((k_gdn_step<D, 8>), grid, dim3(GDN_TPB), 0, s, *a);  \
-        else hipLaunchKernelGGL((k_gdn_step<D, 16>), grid, dim3(GDN_TPB), 0, s, *a);                \
+    if (!a->dv || a->dv > SGK_GDN_MAX_DV || !a->z || !a->out) return hipErrorInvalidValue;
+    if (a->blocks == 1) {
+        // one 512-thread workgroup per head, 16 rows per wave (dv <= 128) or
+        // 32 (dv <= 256, two passes of 16 are not needed: RW = 16 covers 128)
+        if (!a->norm_w || a->dv > 128) return hipErrorInvalidValue;
+        const uint32_t rw = (a->dv + 7) / 8;
+        dim3 grid(a->n_v, 1);
+#define DKCASE1(D) case D:                                                                               \
+        if (rw <= 1) hipLaunchKernelGGL((k_gdn_step<D, 1, 1, 512>), grid, dim3(512), 0, s, *a);          \
+        else if (rw <= 2) hipLaunchKernelGGL((k_gdn_step<D, 2, 1, 512>), grid, dim3(512), 0, s, *a);     \
+        else if (rw <= 4) hipLaunchKernelGGL((k_gdn_step<D, 4, 1, 512>), grid, dim3(512), 0, s, *a);     \
+        else if (rw <= 8) hipLaunchKernelGGL((k_gdn_step<D, 8, 1, 512>), grid, dim3(512), 0, s, *a);     \
+        else hipLaunchKernelGGL((k_gdn_step<D, 16, 1, 512>), grid, dim3(512), 0, s, *a);                 \
+        break
+        switch (a->dk) {
+            DKCASE1(32); DKCASE1(64); DKCASE1(128); DKCASE1(256);
+        default: return hipErrorInvalidValue;
+        }
+#undef DKCASE1
+        return hipGetLastError();
+    }
+    if (!a->y || !a->ss || a->dv > 256) return hipErrorInvalidValue;
+    const uint32_t rpb = (a->dv + SGK_GDN_BLOCKS - 1) / SGK_GDN_BLOCKS;    // rows per block, at most 64
+    dim3 grid(a->n_v, SGK_GDN_BLOCKS);
+#define DKCASE(D) case D:                                                                                  \
+        if (rpb <= 4) hipLaunchKernelGGL((k_gdn_step<D, 1, SGK_GDN_BLOCKS, 256>), grid, dim3(256), 0, s, *a);        \
+        else if (rpb <= 8) hipLaunchKernelGGL((k_gdn_step<D, 2, SGK_GDN_BLOCKS, 256>), grid, dim3(256), 0, s, *a);   \
+        else if (rpb <= 16) hipLaunchKernelGGL((k_gdn_step<D, 4, SGK_GDN_BLOCKS, 256>), grid, dim3(256), 0, s, *a);  \
+        else if (rpb <= 32) hipLaunchKernelGGL((k_gdn_step<D, 8, SGK_GDN_BLOCKS, 256>), grid, dim3(256), 0, s, *a);  \
+        else hipLaunchKernelGGL((k_gdn_step<D, 16, SGK_GDN_BLOCKS, 256>), grid, dim3(256), 0, s, *a);                \
         break
     switch (a->dk) {
         DKCASE(32); DKCASE(64); DKCASE(128); DKCASE(256);
