@@ -798,6 +798,8 @@ static sg_err check_model(const sg_model *m) {
             if (!c->head_v_dim || c->head_v_dim > SGK_GDN_MAX_DV || c->head_v_dim % 4)
                 return (sg_err){"gpu: head_v_dim must be a multiple of 4 in [4, 256]"};
             if (c->n_v_heads > SGK_GATED_MAX_HEADS) return (sg_err){"gpu: at most 256 DeltaNet value heads"};
+            if (c->head_v_dim > 128 && c->n_v_heads * c->head_v_dim > 8192)
+                return (sg_err){"gpu: DeltaNet value_dim above 8192 needs head_v_dim <= 128"};
         } else if (c->rope_dim < 2 || c->rope_dim > c->head_dim || c->rope_dim % 2) {
             return (sg_err){"gpu: rope_dim must be even and in [2, head_dim]"};
         }

@@ -127,36 +127,81 @@ __device__ __forceinline__ uint32_t dev_n_splits(uint32_t seq, uint32_t cap) {
 // GEMV: input staging prologue
 // ---------------------------------------------------------------------------
 
-// Stage the input vector in LDS with 16-byte loads, all of a thread's loads in
-// flight before its first LDS store. PRO_RMS stages x*w and returns the RMS
-// factor 1/sqrt(mean(x^2) + eps) (ref.c:113-125) for the epilogue to apply to
-// each row sum: W(x*r*w) = r * W(x*w). Other prologues return 1. Needs x and w
-// 16-byte aligned (every buffer of this library is).
-template <int PRO, int NT>
-__device__ __forceinline__ float stage_x_n(const sgk_gemv &a, float *xs) {
+// Stage the input vector in LDS with 16-byte loads, in two phases so a
+// kernel can put its first weight loads between them: stage_issue requests
+// every float4 of x (and of the norm weight w for PRO_RMS) this thread stages,
+// all in flight at once (K per thread cover rows up to K*NT*4 columns; wider
+// rows finish with a strided loop); stage_finish stores them to LDS. The
+// loads are unconditional with the index clamped to the last float4, so no
+// branch separates them and each waits only for its own data. PRO_RMS stages
+// x*w and returns the RMS factor 1/sqrt(mean(x^2) + eps) (ref.c:113-125) for
+// the epilogue to apply to each row sum: W(x*r*w) = r * W(x*w). Other
+// prologues return 1. Needs x and w 16-byte aligned (every buffer of this
+// library is).
+// PRO_GATED keeps y in v, silu(z) in g, the norm weight in w and this
+// thread's head's per-block sums of squares in gs.
+template <int PRO, int NT, int K>
+struct xstage {
+    float4 v[K], g[PRO != SGK_PRO_NONE ? K : 1], w[PRO == SGK_PRO_GATED ? K : 1];
+    float gs[PRO == SGK_PRO_GATED ? SGK_GDN_BLOCKS : 1];
+};
+
+template <int PRO, int NT, int K>
+__device__ __forceinline__ void stage_issue(const sgk_gemv &a, xstage<PRO, NT, K> &st) {
+    const uint32_t n4 = a.cols >> 2, t = threadIdx.x;
+    if (!n4) return;
+    const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.nw;
+    if (PRO == SGK_PRO_GATED) {
+        const float4 *z4 = (const float4 *)a.x2;
+        const uint32_t nh = a.cols / a.gdv, hh = min(t, nh - 1);
+#pragma unroll
+        for (uint32_t b = 0; b < SGK_GDN_BLOCKS; b++) st.gs[b] = a.gss[hh * SGK_GDN_BLOCKS + b];
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const uint32_t i = min(t + (uint32_t)k * NT, n4 - 1), j = 4 * i;
+            st.v[k] = x4[i];
+            st.g[k] = z4[i];
+            st.w[k] = *(const float4 *)(a.nw + (j - (j / a.gdv) * a.gdv));
+        }
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const uint32_t i = min(t + (uint32_t)k * NT, n4 - 1);
+        st.v[k] = x4[i];
+        if (PRO == SGK_PRO_RMS) st.g[k] = w4[i];
+    }
+}
+
+template <int PRO, int NT, int K>
+__device__ __forceinline__ float stage_finish(const sgk_gemv &a, xstage<PRO, NT, K> &st, float *xs) {
     __shared__ float red[NT / 64];
     const uint32_t n = a.cols, t = threadIdx.x, n4 = n >> 2;
     if (PRO == SGK_PRO_GATED) {
         // RMSNormGated of the DeltaNet readout (ref.c:1322-1330): head hh's
         // factor from its row blocks' sums of squares (added in block order),
         // then x = silu(z) * ((y * r) * w) with silu(z) precomputed.
+        // The loads were issued by stage_issue (K float4s per thread cover
+        // every column: the launcher holds cols <= K*NT*4 and heads <= NT).
         __shared__ float rh[SGK_GATED_MAX_HEADS];
         const uint32_t dv = a.gdv, nh = n / dv;
-        for (uint32_t hh = t; hh < nh; hh += NT) {
+        if (t < nh) {
             float tot = 0.0f;
-            for (uint32_t b = 0; b < SGK_GDN_BLOCKS; b++) tot += a.gss[hh * SGK_GDN_BLOCKS + b];
-            rh[hh] = 1.0f / sqrtf(tot / (float)dv + a.eps);
+#pragma unroll
+            for (uint32_t b = 0; b < SGK_GDN_BLOCKS; b++) tot += st.gs[b];
+            rh[t] = 1.0f / sqrtf(tot / (float)dv + a.eps);
         }
         __syncthreads();
-        const float4 *y4 = (const float4 *)a.x, *z4 = (const float4 *)a.x2;
         float4 *s4 = (float4 *)xs;
-        for (uint32_t i = t; i < n4; i += NT) {
-            const float4 yv = y4[i], zv = z4[i];
-            const uint32_t j = 4 * i, hh = j / dv, jj = j - hh * dv;
-            const float r = rh[hh];
-            const float4 wv = *(const float4 *)(a.nw + jj);
-            s4[i] = make_float4(zv.x * ((yv.x * r) * wv.x), zv.y * ((yv.y * r) * wv.y),
-                                zv.z * ((yv.z * r) * wv.z), zv.w * ((yv.w * r) * wv.w));
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const uint32_t i = t + (uint32_t)k * NT;
+            if (i < n4) {
+                const float4 yv = st.v[k], zv = st.g[k], wv = st.w[k];
+                const float r = rh[(4 * i) / dv];
+                s4[i] = make_float4(zv.x * ((yv.x * r) * wv.x), zv.y * ((yv.y * r) * wv.y),
+                                    zv.z * ((yv.z * r) * wv.z), zv.w * ((yv.w * r) * wv.w));
+            }
         }
         __syncthreads();
         return 1.0f;
@@ -164,36 +209,29 @@ __device__ __forceinline__ float stage_x_n(const sgk_gemv &a, float *xs) {
     const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.nw;
     float4 *s4 = (float4 *)xs;
     float ss = 0.0f;
-    // Loads in flight per thread: 4 of x, or 2 of x and 2 of w (keeps the
-    // prologue's registers below the main loop's).
-    constexpr uint32_t NS = PRO == SGK_PRO_RMS ? 2 : 4;
-#pragma unroll 1
-    for (uint32_t i0 = t; i0 < n4; i0 += NS * NT) {
-        const uint32_t i1 = i0 + NT, i2 = i0 + 2 * NT, i3 = i0 + 3 * NT;
-        float4 v0, v1, v2, v3, g0, g1;
-        v0 = x4[i0];
-        if (i1 < n4) v1 = x4[i1];
-        if (NS == 4 && i2 < n4) v2 = x4[i2];
-        if (NS == 4 && i3 < n4) v3 = x4[i3];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const uint32_t i = t + (uint32_t)k * NT;
+        if (i < n4) {
+            float4 v = st.v[k];
+            if (PRO == SGK_PRO_RMS) {
+                const float4 g = st.g[k];
+                ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+                v.x *= g.x; v.y *= g.y; v.z *= g.z; v.w *= g.w;
+            }
+            s4[i] = v;
+        }
+    }
+    for (uint32_t i = t + (uint32_t)K * NT; i < n4; i += NT) {   // rows wider than K*NT*4
+        float4 v = x4[i];
         if (PRO == SGK_PRO_RMS) {
-            g0 = w4[i0];
-            if (i1 < n4) g1 = w4[i1];
+            const float4 g = w4[i];
+            ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+            v.x *= g.x; v.y *= g.y; v.z *= g.z; v.w *= g.w;
         }
-#define SG_STAGE(V, G, I)                                                                \
-        if (I < n4) {                                                                    \
-            if (PRO == SGK_PRO_RMS) {                                                    \
-                ss = fmaf(V.x, V.x, ss); ss = fmaf(V.y, V.y, ss);                        \
-                ss = fmaf(V.z, V.z, ss); ss = fmaf(V.w, V.w, ss);                        \
-                V.x *= G.x; V.y *= G.y; V.z *= G.z; V.w *= G.w;                          \
-            }                                                                            \
-            s4[I] = V;                                                                   \
-        }
-        SG_STAGE(v0, g0, i0) SG_STAGE(v1, g1, i1)
-#undef SG_STAGE
-        if (NS == 4) {
-            if (i2 < n4) s4[i2] = v2;
-            if (i3 < n4) s4[i3] = v3;
-        }
+        s4[i] = v;
     }
     for (uint32_t i = 4 * n4 + t; i < n; i += NT) {       // cols % 4 tail (f32 test models)
         float v = a.x[i];
@@ -211,8 +249,17 @@ __device__ __forceinline__ float stage_x_n(const sgk_gemv &a, float *xs) {
     for (int i = 0; i < NT / 64; i += 2) tot += red[i] + red[i + 1];
     return 1.0f / sqrtf(tot / (float)n + a.eps);
 }
+
+// float4s per thread a TPB-thread workgroup's stage_issue keeps in flight:
+// enough for rows of 8192 columns, the widest the row-group GEMV takes.
+constexpr int XK = 8192 / 4 / TPB;
+
 template <int PRO>
-__device__ __forceinline__ float stage_x(const sgk_gemv &a, float *xs) { return stage_x_n<PRO, TPB>(a, xs); }
+__device__ __forceinline__ float stage_x(const sgk_gemv &a, float *xs) {
+    xstage<PRO, TPB, XK> st;
+    stage_issue<PRO, TPB, XK>(a, st);
+    return stage_finish<PRO, TPB, XK>(a, st, xs);
+}
 
 template <int EPI>
 __device__ __forceinline__ void gemv_store(const sgk_gemv &a, uint32_t row, float v) {
@@ -328,9 +375,11 @@ __global__ void __launch_bounds__(TPB) k_gemv_q8(sgk_gemv a) {
     const uint32_t ngroups = (a.rows + R - 1) / R, gstride = gridDim.x * (TPB / 64);
     uint32_t g = blockIdx.x * (TPB / 64) + wave;
     const bool have = g < ngroups;
+    xstage<PRO, TPB, XK> st;
+    stage_issue<PRO, TPB, XK>(a, st);
     gemv_chunk<R> pre;
     if (have && lane < nch) gemv_load<R>(pre, a.qs, a.d, g * R, a.rows, a.cols, lane);
-    const float post = stage_x<PRO>(a, xs);
+    const float post = stage_finish<PRO, TPB, XK>(a, st, xs);
     if (!have) return;
     gemv_group<R, EPI, true>(a, xs, g, lane, &pre, post);
     for (g += gstride; g < ngroups; g += gstride) gemv_group<R, EPI, false>(a, xs, g, lane, nullptr, post);
@@ -381,6 +430,8 @@ __global__ void __launch_bounds__(TPB) k_gemv_f32(sgk_gemv a) {
 
 #define LTPB 1024
 #define LW (LTPB / 64)
+// float4s of x per thread in flight when the long kernel stages rows of up to 20480 columns.
+constexpr int LXK = 5;
 
 struct long_task { uint32_t row, c0, c1, slot; };
 struct long_plan { uint32_t nch, F, nb, S, nbr, G, b, base; };
@@ -457,26 +508,11 @@ __global__ void __launch_bounds__(LTPB) k_gemv_q8_long(sgk_gemv a) {
     p.nbr = (p.nch + 64 * LU - 1) / (64 * LU);
     long_task t;
     bool have = long_task_at<LU>(p, w, 0, t);
+    xstage<SGK_PRO_NONE, LTPB, LXK> st;                 // x first, then the first weights
+    stage_issue<SGK_PRO_NONE, LTPB, LXK>(a, st);
     long_batch<LU> cur;
     if (have) long_load<LU>(cur, a, t, lane);
-    {   // stage x: 16-byte loads, up to four in flight per thread
-        const uint32_t n4 = a.cols >> 2;
-        const float4 *x4 = (const float4 *)a.x;
-        float4 *s4 = (float4 *)xs;
-        for (uint32_t i0 = threadIdx.x; i0 < n4; i0 += 4 * LTPB) {
-            const uint32_t i1 = i0 + LTPB, i2 = i0 + 2 * LTPB, i3 = i0 + 3 * LTPB;
-            float4 v0, v1, v2, v3;
-            v0 = x4[i0];
-            if (i1 < n4) v1 = x4[i1];
-            if (i2 < n4) v2 = x4[i2];
-            if (i3 < n4) v3 = x4[i3];
-            s4[i0] = v0;
-            if (i1 < n4) s4[i1] = v1;
-            if (i2 < n4) s4[i2] = v2;
-            if (i3 < n4) s4[i3] = v3;
-        }
-    }
-    __syncthreads();
+    stage_finish<SGK_PRO_NONE, LTPB, LXK>(a, st, xs);
     float acc = 0.0f;
     for (uint32_t k = 0; have; k++) {
         long_task tn;
@@ -616,7 +652,8 @@ template <int PRO, int EPI>
 static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
     if (((uintptr_t)a->x & 15) || (PRO == SGK_PRO_RMS && ((uintptr_t)a->nw & 15))) return hipErrorInvalidValue;
     if (PRO == SGK_PRO_GATED && (!a->x2 || !a->gss || !a->nw || !a->gdv || a->gdv % 4 || a->cols % a->gdv ||
-                                 a->cols / a->gdv > SGK_GATED_MAX_HEADS || ((uintptr_t)a->x2 & 15) ||
+                                 a->cols / a->gdv > SGK_GATED_MAX_HEADS || a->cols > (uint32_t)XK * TPB * 4 ||
+                                 ((uintptr_t)a->x2 & 15) ||
                                  ((uintptr_t)a->nw & 15)))
         return hipErrorInvalidValue;
     if (!a->qs) {
@@ -1489,7 +1526,6 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
     __shared__ float qk[2 * DK];
     __shared__ float vv[NW * RW];
     __shared__ float red[NW];
-    __shared__ float gts[2];
     __shared__ float ysh[NB == 1 ? SGK_GDN_MAX_DV : 1];
     const uint32_t h = blockIdx.x, jb = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t dk = DK, dv = a.dv, key_dim = a.n_k * dk, cd = a.conv_dim;
@@ -1503,51 +1539,62 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
     float *Sh = a.S + (size_t)h * dv * dk;
 
     // 1. requests, smallest first (loads retire in order, so the conv inputs
-    //    must not queue behind the state rows): the conv inputs, z and the
-    //    gate inputs, then this wave's state rows.
+    //    must not queue behind the state rows): the conv input and taps, z and
+    //    the gate inputs, the ring (its slots need the position), then this
+    //    wave's state rows. Every load is unconditional at a clamped index and
+    //    the tap loops have a fixed trip count, so nothing waits until all of
+    //    them are in flight.
     const uint32_t nch = 2 * dk + (jhi - jlo);
-    float cx = 0.0f, cw[4] = {0.0f, 0.0f, 0.0f, 0.0f}, cr[3] = {0.0f, 0.0f, 0.0f};
-    uint32_t ch = 0;
     auto chan = [&](uint32_t e) -> uint32_t {
         if (e < dk) return hk * dk + e;
         if (e < 2 * dk) return key_dim + hk * dk + (e - dk);
         return 2 * key_dim + h * dv + jlo + (e - 2 * dk);
     };
-    if (t < nch) {
-        ch = chan(t);
-        cx = a.in[ch];
-        for (uint32_t jj = 0; jj <= keep; jj++) cw[jj] = a.conv_w[(size_t)ch * a.ksize + jj];
-        for (uint32_t jj = 0; jj < keep; jj++) cr[jj] = a.ring[(size_t)((pos + 4 - keep + jj) & 3) * cd + ch];
-    }
-    float zj = 0.0f;
-    if (t >= jlo && t < jhi) zj = a.z[(size_t)h * dv + t];
-    if (t == 0) {
-        const float *bb = a.in + cd + a.n_v * dv, *aa = bb + a.n_v;
-        float beta, decay;
-        gdn_gates(bb[h], aa[h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
-        gts[0] = beta;
-        gts[1] = decay;
-    }
+    // All four ring slots are loaded (their addresses need no position), the
+    // taps' slots picked once the position is in.
+    float cx, cw[4], rs[4];
+    auto conv_loads = [&](uint32_t c) {
+        cx = a.in[c];
+#pragma unroll
+        for (uint32_t jj = 0; jj < 4; jj++) cw[jj] = a.conv_w[(size_t)c * a.ksize + min(jj, keep)];
+#pragma unroll
+        for (uint32_t sl = 0; sl < 4; sl++) rs[sl] = a.ring[(size_t)sl * cd + c];
+    };
+    uint32_t ch = chan(min(t, nch - 1));
+    conv_loads(ch);
+    const float zraw = a.z[(size_t)h * dv + min(max(t, jlo), jhi - 1)];
+    const float *bb = a.in + cd + a.n_v * dv, *aa = bb + a.n_v;
+    const float gb = bb[h], ga = aa[h], gA = a.ssm_a[h], gdt = a.dt_bias[h];
     const uint32_t j0 = jlo + wave * RW;
     float sr[RW][EPL];
 #pragma unroll
     for (int r = 0; r < RW; r++) {
-        const uint32_t j = j0 + r;
+        const uint32_t j = min(j0 + r, jhi - 1);
 #pragma unroll
-        for (int e = 0; e < EPL; e++) sr[r][e] = (j < jhi && on) ? Sh[(size_t)j * dk + lane * EPL + e] : 0.0f;
+        for (int e = 0; e < EPL; e++) sr[r][e] = Sh[(size_t)j * dk + (on ? lane * EPL + e : 0)];
     }
+    const float zj = (t >= jlo && t < jhi) ? zraw : 0.0f;
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) sr[r][e] = (j0 + r < jhi && on) ? sr[r][e] : 0.0f;
 
-    // 2. conv + SiLU; this step's input into the ring slot pos % 4.
+    // 2. conv + SiLU (the taps in order, then the current input; ref.c
+    //    conv1d step); this step's input into the ring slot pos % 4.
     for (uint32_t e = t; e < nch; e += GDN_TPB) {
         if (e != t) {
             ch = chan(e);
-            cx = a.in[ch];
-            for (uint32_t jj = 0; jj <= keep; jj++) cw[jj] = a.conv_w[(size_t)ch * a.ksize + jj];
-            for (uint32_t jj = 0; jj < keep; jj++) cr[jj] = a.ring[(size_t)((pos + 4 - keep + jj) & 3) * cd + ch];
+            conv_loads(ch);
         }
         float acc = 0.0f;
-        for (uint32_t jj = 0; jj < keep; jj++) acc = fmaf(cw[jj], cr[jj], acc);
-        acc = fmaf(cw[keep], cx, acc);
+#pragma unroll
+        for (uint32_t jj = 0; jj < 3; jj++) {
+            const uint32_t sl = (pos + 4 - keep + jj) & 3;
+            const float cr = sl == 0 ? rs[0] : sl == 1 ? rs[1] : sl == 2 ? rs[2] : rs[3];
+            if (jj < keep) acc = fmaf(cw[jj], cr, acc);
+        }
+        const float wcur = keep == 0 ? cw[0] : keep == 1 ? cw[1] : keep == 2 ? cw[2] : cw[3];
+        acc = fmaf(wcur, cx, acc);
         const float o = silu(acc);
         if (e < 2 * dk) qk[e] = o; else vv[e - 2 * dk] = o;
         if (e >= 2 * dk || qk_writer) a.ring[(size_t)(pos & 3) * cd + ch] = cx;
@@ -1571,7 +1618,8 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
         qq[e] = on ? (qk[i] * rq) * qsc : 0.0f;
         kq[e] = on ? (qk[dk + i] * rk) * ksc : 0.0f;
     }
-    const float beta = gts[0], decay = gts[1];
+    float beta, decay;                                  // every thread, from scalar loads
+    gdn_gates(gb, ga, gA, gdt, a.neg_exp, &beta, &decay);
     // 4. rank-1 update and readout of this wave's rows.
     float ss_part = 0.0f;
     if (j0 < jhi) {
