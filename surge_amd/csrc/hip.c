@@ -115,6 +115,7 @@ struct sg_gpu {
     uint64_t pf_segments;
     sgk_step *pf_steps, *pf_hsteps;
     float *pf_X, *pf_Xn, *pf_IN, *pf_CONV, *pf_Y, *pf_G, *pf_CTX, *pf_FF, *pf_m, *pf_s, *pf_acc;
+    uint16_t *pf_XS;        /* the prefill GEMMs' X split into bf16 hi | lo */
 
     /* one-shot scratch */
     void *tmp;
@@ -467,11 +468,13 @@ sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
             sg_failed(e = need(out, (uint64_t)N * M * 4, "Y"))) return e;
         if (sg_failed(e = push(ins, 3))) return e;
         void *t;
-        if (sg_failed(e = scratch(g, (uint64_t)M * K + (uint64_t)M * (K / 32) * 2 + 256, &t))) return e;
+        const uint64_t qb = ((uint64_t)M * K + 255) / 256 * 256, db = ((uint64_t)M * (K / 32) * 2 + 255) / 256 * 256;
+        if (sg_failed(e = scratch(g, qb + db + (uint64_t)N * K * 4, &t))) return e;
         int8_t *qs = t;
-        uint16_t *d = (uint16_t *)((char *)t + (((uint64_t)M * K + 255) / 256 * 256));
+        uint16_t *d = (uint16_t *)((char *)t + qb);
+        uint16_t *xs = (uint16_t *)((char *)t + qb + db);
         hipError_t he = sgk_repack_q8(DEV(b), M, K, qs, d, 0, 1, s);
-        if (he == hipSuccess) he = sgk_gemm_q8(DEV(a), qs, d, DEV(out), N, M, K, s);
+        if (he == hipSuccess) he = sgk_gemm_q8(DEV(a), qs, d, DEV(out), N, M, K, xs, s);
         return finish(g, he, outs, 1);
     }
     return errf("gpu: unknown kernel '%s'", kernel);
@@ -911,7 +914,8 @@ static void state_free(sg_gpu *g) {
     {
         void **pb[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
                         (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
-                        (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc };
+                        (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc,
+                        (void **)&g->pf_XS };
         for (size_t i = 0; i < sizeof pb / sizeof *pb; i++) { dfree(g, *pb[i]); *pb[i] = NULL; }
         g->pf_chunk = 0;
     }
@@ -1225,7 +1229,8 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     if (g->pf_chunk >= chunk) return SG_OK;
     void **bufs[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
                       (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
-                      (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc };
+                      (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc,
+                      (void **)&g->pf_XS };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) { dfree(g, *bufs[i]); *bufs[i] = NULL; }
     if (g->pf_hsteps) { hipHostFree(g->pf_hsteps); g->pf_hsteps = NULL; }
     g->pf_chunk = 0;
@@ -1233,9 +1238,14 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     uint32_t in_rows = 0;
     for (uint32_t i = 0; i < c->n_layers; i++) if (g->ls[i].in.rows > in_rows) in_rows = g->ls[i].in.rows;
     uint64_t n = chunk, ah = n * c->n_heads * SGK_PREFILL_SPLITS;
+    uint64_t kmax = c->hidden;                      /* widest GEMM input row */
+    if (c->ffn_hidden > kmax) kmax = c->ffn_hidden;
+    if (g->attn_width > kmax) kmax = g->attn_width;
+    if (g->value_dim > kmax) kmax = g->value_dim;
     uint64_t sizes[] = { n * sizeof(sgk_step), n * c->hidden * 4, n * c->hidden * 4, n * in_rows * 4,
                          n * g->conv_dim * 4 + 4, n * g->value_dim * 4 + 4, n * g->value_dim * 4 + 4,
-                         n * g->attn_width * 4 + 4, n * c->ffn_hidden * 4, ah * 4, ah * 4, ah * c->head_dim * 4 };
+                         n * g->attn_width * 4 + 4, n * c->ffn_hidden * 4, ah * 4, ah * 4, ah * c->head_dim * 4,
+                         n * kmax * 4 };
     sg_err e = SG_OK;
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs && !sg_failed(e); i++) e = dzalloc(g, sizes[i], bufs[i]);
     if (!sg_failed(e) && hipHostMalloc((void **)&g->pf_hsteps, n * sizeof(sgk_step), 0) != hipSuccess)
@@ -1247,7 +1257,7 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
 
 static hipError_t gemm_rows(sg_gpu *g, const dmat *M, const float *X, uint32_t ldx, float *Y, uint32_t ldy,
                             uint32_t n, int epi) {
-    sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi };
+    sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi, g->pf_XS };
     return sgk_gemm(&a, g->stream);
 }
 

@@ -1015,23 +1015,49 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
     __shared__ __align__(16) float red[TPB / 64][GMAX * HD];   // end fold; raw rows during prep
 
     const uint32_t G = a.n_heads / a.n_kv, n_kv = a.n_kv, z = blockIdx.z;
+    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t h0 = hk * G;
+    const float *q = a.q + (size_t)z * a.q_tok;
+    const bool fp = a.fuse_prep != 0;
+
+    // 1. Loads that need no position go first, so their round trip overlaps
+    //    the position's: the group's q rows and, for the fused prep, both
+    //    norm weights and the raw k and v rows (unused outside the split that
+    //    holds the position). Every load is unconditional at a clamped index
+    //    (pointers the call does not use are swapped for q), so no branch
+    //    makes a load wait early.
+    constexpr int QPT = (GMAX * HD + TPB - 1) / TPB;   // q values per thread
+    float qv[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const uint32_t e = min(t + k * TPB, G * HD - 1);
+        qv[k] = q[(size_t)(h0 + e / HD) * a.q_stride + e % HD];
+    }
+    const uint32_t td = min(t, (uint32_t)HD - 1);
+    const float *krow = fp ? q + (size_t)a.n_heads * a.q_stride + (size_t)hk * HD : q;
+    const float *vrow = fp ? krow + (size_t)n_kv * HD : q;
+    const float qn0 = (fp ? a.qn : q)[td], kn0 = (fp ? a.kn : q)[td];
+    const float kr0 = krow[td], vr0 = vrow[td];
+
     const uint32_t pos = a.steps ? a.steps[z].pos : 0;
     const uint32_t seq = a.steps ? pos + 1 : a.seq;
     const uint32_t ns = a.steps ? dev_splits(seq, a.prefill, a.split_cap) : a.n_splits;
-    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     if (i >= ns) return;
     const uint32_t t0 = (uint32_t)((uint64_t)i * seq / ns);
     const uint32_t t1 = (uint32_t)((uint64_t)(i + 1) * seq / ns);
-    const uint32_t h0 = hk * G;
-    const float *q = a.q + (size_t)z * a.q_tok;
     const uint16_t *kc = a.kc, *vc = a.vc;
     const size_t zoff = (size_t)z * a.n_heads * a.max_splits;
     const uint32_t kj = t / TPK, kp = t % TPK;      // score mapping
     const uint32_t vcc = t % VC, kg = t / VC;       // P*V mapping
 
+    // K/V tile loads are unconditional: keys past the split clamp to its last
+    // key (a whole tile past the end re-reads one row), so no branch joins
+    // paths with and without loads in flight, which would make the waits
+    // before later uses count as if nothing were queued behind them.
     uint4 kr[KU], vr[VU];
+    const uint32_t klast = t1 ? t1 - 1 : 0;
     auto load_k = [&](uint32_t ts) {
-        const uint32_t key = min(ts + kj, t1 - 1);
+        const uint32_t key = min(ts + kj, klast);
         const uint4 *p = (const uint4 *)(kc + ((size_t)key * n_kv + hk) * HD + kp * DPT);
 #pragma unroll
         for (int u = 0; u < KU; u++) kr[u] = p[u];
@@ -1039,51 +1065,36 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
     auto load_v = [&](uint32_t ts) {
 #pragma unroll
         for (int u = 0; u < VU; u++) {
-            const uint32_t key = min(ts + kg + u * KGV, t1 - 1);
+            const uint32_t key = min(ts + kg + u * KGV, klast);
             vr[u] = ((const uint4 *)(vc + ((size_t)key * n_kv + hk) * HD))[vcc];
         }
     };
-    if (a.fuse_prep) {
-        // One round trip for everything the prep reads: raw q rows of the
-        // group, and for the split holding the position its raw k and v rows,
-        // the position's cos|sin row and both norm weights.
+    // 2. The position's cos|sin entry, then the first tile's K and V; all of
+    //    it overlaps the prep's first steps.
+    const float cs0 = (fp ? a.cs + (size_t)pos * a.rope_dim : q)[min(td, a.rope_dim ? a.rope_dim - 1 : 0u)];
+    __builtin_amdgcn_sched_barrier(0);              // keep it ahead of the tile in the load queue
+    load_k(t0);
+    load_v(t0);
+    if (fp) {
         __shared__ float cs_s[HD], qn_s[HD], kn_s[HD];
         __shared__ __align__(16) uint16_t knew[HD], vnew[HD];
-        float *raw = &red[0][0];                 // [G][HD] q, then k at [GMAX*HD]
+        float *raw = &red[0][0];                 // [G][HD] q, then k past the q slots
         const bool kv_writer = i == ns - 1;
-        const float *krow = q + (size_t)a.n_heads * a.q_stride + (size_t)hk * HD;
-        const float *vrow = krow + (size_t)n_kv * HD;
-        const float *csrow = a.cs + (size_t)pos * a.rope_dim;
-        // Loads retire in order: the prep's few loads go first, into
-        // registers; then the first tile's K and V (their addresses depend
-        // only on the split), whose latency overlaps the prep's arithmetic.
-        constexpr int QPT = (GMAX * HD + TPB - 1) / TPB;  // q values per thread
-        float qv[QPT], kr0 = 0.0f, vr0 = 0.0f, qn0 = 0.0f, kn0 = 0.0f, cs0 = 0.0f;
+        // LDS stores are unconditional (duplicates store equal values; q
+        // slots past the group are never read); each waits only for its own
+        // data, not the tile behind it.
+        constexpr int KOFF = QPT * TPB;                   // raw k row, past every q slot
+        static_assert(KOFF + HD <= (TPB / 64) * GMAX * HD, "raw q|k rows exceed the fold buffer");
 #pragma unroll
-        for (int k = 0; k < QPT; k++) {
-            const uint32_t e = t + k * TPB;
-            qv[k] = e < G * HD ? q[(size_t)(h0 + e / HD) * a.q_stride + e % HD] : 0.0f;
-        }
-        if (t < HD) {
-            qn0 = a.qn[t];
-            cs0 = t < a.rope_dim ? csrow[t] : 0.0f;
-            if (kv_writer) { kr0 = krow[t]; kn0 = a.kn[t]; vr0 = vrow[t]; }
-        }
-        if (t0 < t1) { load_k(t0); load_v(t0); }
-#pragma unroll
-        for (int k = 0; k < QPT; k++) {
-            const uint32_t e = t + k * TPB;
-            if (e < G * HD) raw[e] = qv[k];
-        }
-        if (t < HD) {
-            qn_s[t] = qn0;
-            cs_s[t] = cs0;
-            if (kv_writer) { raw[GMAX * HD + t] = kr0; kn_s[t] = kn0; }
-        }
+        for (int k = 0; k < QPT; k++) raw[t + k * TPB] = qv[k];
+        qn_s[td] = qn0;
+        raw[KOFF + td] = kr0;
+        kn_s[td] = kn0;
         __syncthreads();
+        cs_s[td] = td < a.rope_dim ? cs0 : 0.0f;        // read after the next barrier
         for (uint32_t h = wave; h <= (uint32_t)G; h += TPB / 64) {
             if (h == (uint32_t)G && !kv_writer) break;
-            const float *x = h < (uint32_t)G ? raw + h * HD : raw + GMAX * HD;
+            const float *x = h < (uint32_t)G ? raw + h * HD : raw + KOFF;
             float ss = 0.0f;
             for (uint32_t d = lane; d < HD; d += 64) ss = fmaf(x[d], x[d], ss);
             ss = wave_sum(ss);
@@ -1097,7 +1108,7 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
         if (kv_writer) {
             const size_t at = ((size_t)pos * n_kv + hk) * HD;
             for (uint32_t d = t; d < HD; d += TPB) {
-                const uint16_t kh = f2h(prep_elem(raw + GMAX * HD, rn[G], kn_s, cs_s, d, a.rope_dim));
+                const uint16_t kh = f2h(prep_elem(raw + KOFF, rn[G], kn_s, cs_s, d, a.rope_dim));
                 const uint16_t vh = f2h(vr0);
                 ((uint16_t *)a.kc)[at + d] = kh;
                 ((uint16_t *)a.vc)[at + d] = vh;
@@ -1120,14 +1131,6 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
                 if (t0 + kg + u * KGV == pos) vr[u] = ((const uint4 *)vnew)[vcc];
         }
     } else {
-        constexpr int QPT = (GMAX * HD + TPB - 1) / TPB;
-        float qv[QPT];
-#pragma unroll
-        for (int k = 0; k < QPT; k++) {
-            const uint32_t e = t + k * TPB;
-            qv[k] = e < G * HD ? q[(size_t)(h0 + e / HD) * a.q_stride + e % HD] : 0.0f;
-        }
-        if (t0 < t1) { load_k(t0); load_v(t0); }
 #pragma unroll
         for (int k = 0; k < QPT; k++) {
             const uint32_t e = t + k * TPB, h = e / HD, d = e % HD;
@@ -1145,7 +1148,6 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
 
     for (uint32_t ts = t0; ts < t1; ts += TK) {
         const uint32_t nk = min((uint32_t)TK, t1 - ts);
-        const bool more = ts + TK < t1;
         // scores
         float part[GMAX];
 #pragma unroll
@@ -1167,7 +1169,7 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
                 }
             }
         }
-        if (more) load_k(ts + TK);
+        load_k(ts + TK);                             // past the split: one row, unused
 #pragma unroll
         for (int h = 0; h < GMAX; h++) {
             if (TPK >= 2) part[h] += lane_xor1(part[h]);
@@ -1239,7 +1241,7 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
                 }
             }
         }
-        if (more) load_v(ts + TK);
+        load_v(ts + TK);
         __syncthreads();
     }
 
@@ -1816,24 +1818,55 @@ extern "C" hipError_t sgk_rmsnorm_gated(const float *y, const float *z, const fl
 // scanned over the chunk's tokens in order (state threaded through).
 // ---------------------------------------------------------------------------
 
-// Causal conv + SiLU, one thread per channel walking the tokens; the ring
-// holds the last inputs by position, as in decode.
-__global__ void k_conv_chunk(const float *in, uint32_t in_stride, const float *conv_w, float *ring,
-                             float *out, const sgk_step *steps, uint32_t ntok, uint32_t cd, uint32_t ksize) {
-    const uint32_t ch = blockIdx.x * TPB + threadIdx.x;
+// Causal conv + SiLU over a chunk at consecutive positions pos0 .. pos0+ntok-1
+// (the ring holds the inputs of the positions before pos0 by slot p % 4, as
+// in decode). Thread (channel, block of CC_TOK tokens): the taps of token z
+// are the chunk's own inputs for positions inside the chunk, else the ring
+// slots; each output is the taps in order, then the current input (the
+// decode step's arithmetic). The ring is only read here: k_conv_ring writes
+// the chunk's last inputs into it afterwards.
+#define CC_TOK 16
+__global__ void __launch_bounds__(TPB) k_conv_chunk(const float *in, uint32_t in_stride, const float *conv_w,
+                                                    const float *ring, float *out, const sgk_step *steps,
+                                                    uint32_t ntok, uint32_t cd, uint32_t ksize) {
+    const uint32_t ch = blockIdx.x * TPB + threadIdx.x, z0 = blockIdx.y * CC_TOK;
     if (ch >= cd) return;
-    const uint32_t keep = ksize - 1;
-    const float *w = conv_w + (size_t)ch * ksize;
-    for (uint32_t z = 0; z < ntok; z++) {
-        const uint32_t pos = steps[z].pos;
-        const float x = in[(size_t)z * in_stride + ch];
+    const uint32_t keep = ksize - 1, pos0 = steps[0].pos;
+    float w[4], x[CC_TOK + 3];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; j++) w[j] = conv_w[(size_t)ch * ksize + min(j, keep)];
+    // x[3 + i] = input of token z0 + i; x[0..2] = the three before z0
+#pragma unroll
+    for (int i = 0; i < CC_TOK + 3; i++) {
+        const int z = (int)z0 + i - 3;
+        const uint32_t zc = (uint32_t)min(max(z, 0), (int)ntok - 1);
+        const float vi = in[(size_t)zc * in_stride + ch];
+        const float vr = ring[(size_t)((pos0 + 4 + (uint32_t)min(z, 0)) & 3) * cd + ch];
+        x[i] = z < 0 ? vr : vi;
+    }
+#pragma unroll
+    for (int i = 0; i < CC_TOK; i++) {
+        const uint32_t z = z0 + i;
+        if (z >= ntok) break;
         float acc = 0.0f;
-        for (uint32_t jj = 0; jj < keep; jj++)
-            acc = fmaf(w[jj], ring[(size_t)((pos + 4 - keep + jj) & 3) * cd + ch], acc);
-        acc = fmaf(w[keep], x, acc);
-        ring[(size_t)(pos & 3) * cd + ch] = x;
+#pragma unroll
+        for (uint32_t jj = 0; jj < 3; jj++)
+            if (jj < keep) acc = fmaf(w[jj], x[3 + i - keep + jj], acc);
+        const float wcur = keep == 0 ? w[0] : keep == 1 ? w[1] : keep == 2 ? w[2] : w[3];
+        acc = fmaf(wcur, x[3 + i], acc);
         out[(size_t)z * cd + ch] = silu(acc);
     }
+}
+
+// The ring after a chunk: slot p % 4 = input of position p for the chunk's
+// last min(ntok, 4) positions (older slots keep their values).
+__global__ void k_conv_ring(const float *in, uint32_t in_stride, float *ring, const sgk_step *steps,
+                            uint32_t ntok, uint32_t cd) {
+    const uint32_t ch = blockIdx.x * TPB + threadIdx.x;
+    if (ch >= cd) return;
+    const uint32_t pos0 = steps[0].pos;
+    for (uint32_t z = ntok > 4 ? ntok - 4 : 0; z < ntok; z++)
+        ring[(size_t)((pos0 + z) & 3) * cd + ch] = in[(size_t)z * in_stride + ch];
 }
 
 // q and k of every key head of every token: RMS (eps 1e-6, no weight), then
@@ -1925,8 +1958,10 @@ extern "C" hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t 
                                     hipStream_t s) {
     if (!ntok) return hipSuccess;
     if (a->ksize < 1 || a->ksize > 4 || !a->n_k || a->n_v % a->n_k) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_conv_chunk, dim3((a->conv_dim + TPB - 1) / TPB), dim3(TPB), 0, s, a->in, in_stride,
-                       a->conv_w, a->ring, conv_out, a->step, ntok, a->conv_dim, a->ksize);
+    hipLaunchKernelGGL(k_conv_chunk, dim3((a->conv_dim + TPB - 1) / TPB, (ntok + CC_TOK - 1) / CC_TOK), dim3(TPB), 0, s,
+                       a->in, in_stride, a->conv_w, a->ring, conv_out, a->step, ntok, a->conv_dim, a->ksize);
+    hipLaunchKernelGGL(k_conv_ring, dim3((a->conv_dim + TPB - 1) / TPB), dim3(TPB), 0, s, a->in, in_stride, a->ring,
+                       a->step, ntok, a->conv_dim);
     hipLaunchKernelGGL(k_qk_norm_chunk, dim3(2 * a->n_k, ntok), dim3(TPB), 0, s, conv_out, a->conv_dim, a->n_k, a->dk);
     return sgk_delta_scan(a, conv_out, in_stride, ntok, NULL, s);
 }
@@ -2079,44 +2114,98 @@ extern "C" hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream
 // Prefill GEMM Y[N][M] = X[N][K] * W[M][K]^T (chunk of N tokens through one
 // weight), W in the Q8 device layout, on MFMA.
 //
-// Precision: int8 weights are exact in bf16 (|q| <= 127); x is split into
-// bf16 hi + lo (x = hi + lo to ~16 bits), so each Q8_0 block's partial dot is
-// two v_mfma_f32_16x16x32_bf16 into a zeroed fp32 tile, then scaled by the
-// block's f16 scale into the fp32 accumulator. The weights are never
-// dequantised into bf16 (d*q has ~18 significant bits).
+// Precision: int8 weights are exact in bf16 (|q| <= 127); x is split once per
+// GEMM into bf16 hi + lo (x = hi + lo to ~16 bits; k_split_bf16), so each
+// Q8_0 block's partial dot is two v_mfma_f32_16x16x32_bf16 into a zeroed fp32
+// tile, then scaled by the block's f16 scale into the fp32 accumulator. The
+// weights are never dequantised into bf16 (d*q has ~18 significant bits).
 //
-// Tiling: workgroup 256 threads = 4 waves over a 64-token x 128-row tile
-// (waves 2 x 2, each 32 x 64 = 2 x 4 MFMA tiles of 16x16), K in steps of 64
-// (two Q8_0 blocks). X is staged in LDS as bf16 hi/lo per step; each lane
-// loads its weight fragments straight from HBM (8 int8 per 16-row tile per
-// block). XCD-aware order: the token tiles that share a weight tile are
-// dispatched to the same XCD, so the weight tile is fetched into one L2.
+// Tiling: workgroup 256 threads = 4 waves over a 128-token x 128-row tile
+// (waves 2 x 2, each 64 x 64 = 4 x 4 MFMA tiles of 16x16), K in steps of 64
+// (two Q8_0 blocks). The X hi/lo tile of a step (32 KB) is double-buffered in
+// LDS: the next step's tile and weights are requested before the current
+// step's MFMAs and stored after them, one barrier per step. Each lane loads
+// its weight fragments (8 int8 of 4 rows per block) straight from memory one
+// step ahead and converts them to bf16. XCD-aware order: the token tiles that
+// share a weight tile run on one XCD, so the weight tile is fetched into one
+// L2. Every load is unconditional at a clamped index (rows past N or M are
+// computed and dropped at the store).
 // MFMA 16x16x32 operand layout: A[i][k] in lane i + 16*(k/8), element k%8;
 // B[k][j] in lane j + 16*(k/8); D[i][j] in lane j + 16*(i/4), element i%4.
 // ---------------------------------------------------------------------------
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ uint16_t bf16_bits_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    u += 0x7FFFu + ((u >> 16) & 1u);     // round to nearest even (finite inputs)
-    return (uint16_t)(u >> 16);
+// X [N][ldx] f32 -> xs[0 .. N*K) bf16 hi, xs[N*K .. 2*N*K) bf16 lo = x - hi,
+// both round-to-nearest-even, rows of K (K % 4 == 0, ldx % 4 == 0, X 16-byte
+// aligned).
+__global__ void __launch_bounds__(TPB) k_split_bf16(const float *X, uint32_t ldx, uint32_t N, uint32_t K,
+                                                    uint16_t *xs) {
+    const uint32_t k4 = K >> 2;
+    const size_t total = (size_t)N * k4;
+    uint16_t *xl = xs + (size_t)N * K;
+    for (size_t i = (size_t)blockIdx.x * TPB + threadIdx.x; i < total; i += (size_t)gridDim.x * TPB) {
+        const uint32_t n = (uint32_t)(i / k4), c = (uint32_t)(i - (size_t)n * k4) * 4;
+        const float4 v = *(const float4 *)(X + (size_t)n * ldx + c);
+        const bf16x2 h01 = {(__bf16)v.x, (__bf16)v.y}, h23 = {(__bf16)v.z, (__bf16)v.w};
+        const bf16x2 l01 = {(__bf16)(v.x - (float)h01[0]), (__bf16)(v.y - (float)h01[1])};
+        const bf16x2 l23 = {(__bf16)(v.z - (float)h23[0]), (__bf16)(v.w - (float)h23[1])};
+        *(uint2 *)(xs + (size_t)n * K + c) = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+        *(uint2 *)(xl + (size_t)n * K + c) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+    }
 }
-__device__ __forceinline__ float bf16_to_f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-#define GM_TN 64    // tokens per workgroup tile
+// 8 int8 weights -> 8 bf16, exact.
+__device__ __forceinline__ bf16x8 q8x8_bf16(uint2 r) {
+    uint32_t o[4];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const uint32_t w = p ? r.y : r.x;
+        const bf16x2 a = {(__bf16)(float)(int8_t)w, (__bf16)(float)(int8_t)(w >> 8)};
+        const bf16x2 b = {(__bf16)(float)(int8_t)(w >> 16), (__bf16)(float)((int32_t)w >> 24)};
+        o[2 * p] = __builtin_bit_cast(uint32_t, a);
+        o[2 * p + 1] = __builtin_bit_cast(uint32_t, b);
+    }
+    return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+// Prefill GEMM step pieces: this thread's 64 bytes of a token row's X hi and
+// lo from k offset kc; its copy into the LDS tile; the weight fragments and
+// scales of step st (blocks clamped into the row).
+__device__ __forceinline__ void gm_x_load(uint4 (&xr)[8], const uint4 *xhr, const uint4 *xlr, uint32_t kc) {
+    const uint4 *ph = xhr + kc / 8, *pl = xlr + kc / 8;
+#pragma unroll
+    for (int u = 0; u < 4; u++) { xr[u] = ph[u]; xr[4 + u] = pl[u]; }
+}
+__device__ __forceinline__ void gm_x_store(const uint4 (&xr)[8], uint16_t *dh, uint16_t *dl) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) { ((uint4 *)dh)[u] = xr[u]; ((uint4 *)dl)[u] = xr[4 + u]; }
+}
+__device__ __forceinline__ void gm_w_load(uint2 (&wq)[2][4], uint32_t (&wd)[2][4], const int8_t *const (&wr)[4],
+                                          const uint16_t *const (&dr)[4], uint32_t st, uint32_t nblk) {
+#pragma unroll
+    for (int bb = 0; bb < 2; bb++) {
+        const uint32_t kb = min(st * 2 + bb, nblk - 1);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            wq[bb][c] = *(const uint2 *)(wr[c] + (size_t)kb * 32);
+            wd[bb][c] = dr[c][kb];
+        }
+    }
+}
+
+#define GM_TN 128   // tokens per workgroup tile
 #define GM_TM 128   // weight rows per workgroup tile
-#define GM_KS 64    // K per step
-#define GM_LD (GM_KS + 8)   // padded LDS row (bf16 elements)
+#define GM_KS 64    // K per step (two Q8_0 blocks)
+#define GM_LD (GM_KS + 8)   // padded LDS row (bf16 elements, 144 bytes)
 
 template <int EPI>
-__global__ void __launch_bounds__(TPB) k_gemm_q8_mfma(const float *X, const int8_t *qs, const uint16_t *d,
-                                                      float *Y, uint32_t N, uint32_t M, uint32_t K,
-                                                      uint32_t ldx, uint32_t ldy) {
-    __shared__ uint16_t xhi[GM_TN * GM_LD];
-    __shared__ uint16_t xlo[GM_TN * GM_LD];
+__global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d,
+                                                      float *Y, uint32_t N, uint32_t M, uint32_t K, uint32_t ldy) {
+    __shared__ __align__(16) uint16_t xt[2][2][GM_TN * GM_LD];     // [buffer][hi | lo][token][k]
     const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
     // XCD-aware tile order: workgroup b runs on XCD b % 8; keep all token
     // tiles of one weight tile on one XCD.
@@ -2127,62 +2216,63 @@ __global__ void __launch_bounds__(TPB) k_gemm_q8_mfma(const float *X, const int8
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t wn = wave & 1, wm = wave >> 1;
     const uint32_t li = lane & 15, lg = lane >> 4;
-    const uint32_t nbl = K >> 5;
-    f32x4 acc[2][4];
-#pragma unroll
-    for (int a = 0; a < 2; a++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    // weight rows this lane feeds (B operand column j = li of each 16-row tile)
-    const int8_t *wrow[4];
-    const uint16_t *drow[4];
+    const uint32_t nblk = K >> 5, nstep = (K + GM_KS - 1) / GM_KS;
+    const uint16_t *xh = xs, *xl = xs + (size_t)N * K;
+
+    // X tile copy: thread t moves 32 k (64 bytes) of hi and of lo of one token
+    // row per step.
+    const uint32_t sr = t >> 1, sc = (t & 1) * 32;
+    const uint4 *xhr = (const uint4 *)(xh + (size_t)min(n0 + sr, N - 1) * K);
+    const uint4 *xlr = (const uint4 *)(xl + (size_t)min(n0 + sr, N - 1) * K);
+    const uint32_t xso = sr * GM_LD + sc;
+    uint4 xr[8];
+    // weight fragments: rows m0 + wm*64 + c*16 + li, bytes 8*lg .. +7 of each block
+    const int8_t *wr[4];
+    const uint16_t *dr[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const uint32_t m = min(m0 + wm * 64 + c * 16 + li, M - 1);
-        wrow[c] = qs + (size_t)m * K;
-        drow[c] = d + (size_t)m * nbl;
+        wr[c] = qs + (size_t)m * K + lg * 8;
+        dr[c] = d + (size_t)m * nblk;
     }
-    for (uint32_t k0 = 0; k0 < K; k0 += GM_KS) {
-        const uint32_t nblk = min(2u, (K - k0) >> 5);
-        // stage X[n0 .. n0+64][k0 .. k0+64] as bf16 hi/lo: 16 floats per thread
-        {
-            const uint32_t r = t >> 2, c0 = (t & 3) * 16;
-            const uint32_t n = n0 + r;
+    uint2 wq[2][4];
+    uint32_t wd[2][4];
+    f32x4 acc[4][4];
 #pragma unroll
-            for (int e = 0; e < 16; e += 4) {
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (n < N && k0 + c0 + e < K) v = *(const float4 *)(X + (size_t)n * ldx + k0 + c0 + e);
-                const float vv[4] = {v.x, v.y, v.z, v.w};
+    for (int a = 0; a < 4; a++)
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const uint16_t h = bf16_bits_rne(vv[u]);
-                    xhi[r * GM_LD + c0 + e + u] = h;
-                    xlo[r * GM_LD + c0 + e + u] = bf16_bits_rne(vv[u] - bf16_to_f(h));
-                }
-            }
-        }
-        __syncthreads();
-        for (uint32_t blk = 0; blk < nblk; blk++) {
-            const uint32_t kb = k0 + blk * 32;
+        for (int c = 0; c < 4; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    gm_x_load(xr, xhr, xlr, min(sc, K - 32));
+    gm_w_load(wq, wd, wr, dr, 0, nblk);
+    gm_x_store(xr, &xt[0][0][xso], &xt[0][1][xso]);
+    __syncthreads();
+    for (uint32_t st = 0; st < nstep; st++) {
+        const uint32_t buf = st & 1;
+        uint2 cq[2][4];
+        uint32_t cd[2][4];
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) { cq[bb][c] = wq[bb][c]; cd[bb][c] = wd[bb][c]; }
+        const uint32_t nx = min(st + 1, nstep - 1);     // the last step re-requests itself, unused
+        gm_x_load(xr, xhr, xlr, min(nx * GM_KS + sc, K - 32));
+        gm_w_load(wq, wd, wr, dr, nx, nblk);
+        const bool two = st * 2 + 1 < nblk;                  // K tail: one block in the last step
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            if (bb == 1 && !two) continue;
             bf16x8 wf[4];
             float ds[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const uint2 raw = *(const uint2 *)(wrow[c] + kb + lg * 8);
-                u16x8 w;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    w[e] = bf16_bits_rne((float)(int8_t)(raw.x >> (8 * e)));
-                    w[4 + e] = bf16_bits_rne((float)(int8_t)(raw.y >> (8 * e)));
-                }
-                wf[c] = __builtin_bit_cast(bf16x8, w);
-                ds[c] = h2f(drow[c][kb >> 5]);
+                wf[c] = q8x8_bf16(cq[bb][c]);
+                ds[c] = h2f((uint16_t)cd[bb][c]);
             }
 #pragma unroll
-            for (int a = 0; a < 2; a++) {
-                const uint32_t row = wn * 32 + a * 16 + li;
-                const bf16x8 ah = __builtin_bit_cast(bf16x8, *(const u16x8 *)(xhi + row * GM_LD + blk * 32 + lg * 8));
-                const bf16x8 al = __builtin_bit_cast(bf16x8, *(const u16x8 *)(xlo + row * GM_LD + blk * 32 + lg * 8));
+            for (int a = 0; a < 4; a++) {
+                const uint32_t row = wn * 64 + a * 16 + li;
+                const bf16x8 ah = *(const bf16x8 *)&xt[buf][0][row * GM_LD + bb * 32 + lg * 8];
+                const bf16x8 al = *(const bf16x8 *)&xt[buf][1][row * GM_LD + bb * 32 + lg * 8];
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -2193,20 +2283,21 @@ __global__ void __launch_bounds__(TPB) k_gemm_q8_mfma(const float *X, const int8
                 }
             }
         }
+        gm_x_store(xr, &xt[buf ^ 1][0][xso], &xt[buf ^ 1][1][xso]);
         __syncthreads();
     }
     // epilogue: lane holds D[i = 4*lg + e][j = li] of each tile
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < 4; a++)
 #pragma unroll
         for (int c = 0; c < 4; c++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const uint32_t n = n0 + wn * 32 + a * 16 + lg * 4 + e;
+                const uint32_t n = n0 + wn * 64 + a * 16 + lg * 4 + e;
                 const uint32_t m = m0 + wm * 64 + c * 16 + li;
                 const float v = acc[a][c][e];
                 if (EPI == SGK_EPI_SWIGLU) {
-                    const float up = __shfl_xor(v, 1, 64);    // column m+1 lives in lane li^1
+                    const float up = lane_xor1(v);            // column m+1 lives in lane li^1
                     if (!(li & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(v) * up;
                 } else if (n < N && m < M) {
                     if (EPI == SGK_EPI_ADD) Y[(size_t)n * ldy + m] += v;
@@ -2236,10 +2327,15 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
     if (!a->N || !a->M || !a->K) return hipSuccess;
     if (a->epi == SGK_EPI_SWIGLU && (a->M & 1)) return hipErrorInvalidValue;
     if (a->qs) {
-        if (a->K % 32) return hipErrorInvalidValue;
+        if (a->K % 32 || !a->xs || a->ldx % 4 || ((uintptr_t)a->X & 15) || ((uintptr_t)a->xs & 15))
+            return hipErrorInvalidValue;
+        const uint32_t k4 = a->K / 4;
+        const uint64_t total = (uint64_t)a->N * k4;
+        const uint32_t sg = (uint32_t)min((total + TPB - 1) / TPB, (uint64_t)4096);
+        hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
         const uint32_t nb = (a->N + GM_TN - 1) / GM_TN, mb = (a->M + GM_TM - 1) / GM_TM;
         const uint32_t grid = 8 * nb * ((mb + 7) / 8);
-#define GQ(E) hipLaunchKernelGGL(k_gemm_q8_mfma<E>, dim3(grid), dim3(TPB), 0, s, a->X, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldx, a->ldy)
+#define GQ(E) hipLaunchKernelGGL(k_gemm_q8_mfma<E>, dim3(grid), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy)
         if (a->epi == SGK_EPI_ADD) GQ(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GQ(SGK_EPI_SWIGLU); else GQ(SGK_EPI_STORE);
 #undef GQ
     } else {
@@ -2252,7 +2348,7 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
 }
 
 extern "C" hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, float *Y,
-                                  uint32_t N, uint32_t M, uint32_t K, hipStream_t s) {
-    sgk_gemm_args a = {X, qs, d, NULL, Y, N, M, K, K, M, SGK_EPI_STORE};
+                                  uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, hipStream_t s) {
+    sgk_gemm_args a = {X, qs, d, NULL, Y, N, M, K, K, M, SGK_EPI_STORE, xs};
     return sgk_gemm(&a, s);
 }

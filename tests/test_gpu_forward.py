@@ -106,7 +106,10 @@ def test_small_greedy_device_loop_matches_host_loop_and_oracle(gpu, small):
     assert host == ref
 
 
-def test_small_prefill_then_decode_matches_serial(gpu, small):
+@pytest.mark.parametrize("chunk", [16, 1, 5, 64])
+def test_small_prefill_then_decode_matches_serial(gpu, small, chunk):
+    """Chunks below the 4-slot conv ring (1, 5 tokens), a partial last chunk,
+    and a chunk of several conv token blocks."""
     rng = np.random.default_rng(2)
     prompt = rng.integers(0, SMALL["vocab"], 77).tolist()
     gpu.state_reset()
@@ -114,7 +117,7 @@ def test_small_prefill_then_decode_matches_serial(gpu, small):
     for p, t in enumerate(prompt):
         serial = gpu.forward(t, p)
     nxt_serial = gpu.forward(int(np.argmax(serial)), len(prompt))
-    last = gpu.prefill(prompt, chunk=16)
+    last = gpu.prefill(prompt, chunk=chunk)
     assert rel(last, serial) < 2e-4
     assert int(np.argmax(last)) == int(np.argmax(serial))
     nxt = gpu.forward(int(np.argmax(last)), len(prompt))
