@@ -2121,15 +2121,14 @@ extern "C" hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream
 // weights are never dequantised into bf16 (d*q has ~18 significant bits).
 //
 // Tiling: workgroup 256 threads = 4 waves over a 128-token x 128-row tile
-// (waves 2 x 2, each 64 x 64 = 4 x 4 MFMA tiles of 16x16), K in steps of 64
-// (two Q8_0 blocks). The X hi/lo tile of a step (32 KB) is double-buffered in
+// (waves 2 x 2, each 64 x 64 = 4 x 4 MFMA tiles of 16x16; the kernel also
+// takes 32 x 64 wave tiles, which measured slower), K in steps of 64 (two
+// Q8_0 blocks). The X hi/lo tile of a step (32 KB) is double-buffered in
 // LDS: the next step's tile and weights are requested before the current
 // step's MFMAs and stored after them, one barrier per step. Each lane loads
 // its weight fragments (8 int8 of 4 rows per block) straight from memory one
-// step ahead and converts them to bf16. XCD-aware order: the token tiles that
-// share a weight tile run on one XCD, so the weight tile is fetched into one
-// L2. Every load is unconditional at a clamped index (rows past N or M are
-// computed and dropped at the store).
+// step ahead and converts them to bf16. Every load is unconditional at a
+// clamped index (rows past N or M are computed and dropped at the store).
 // MFMA 16x16x32 operand layout: A[i][k] in lane i + 16*(k/8), element k%8;
 // B[k][j] in lane j + 16*(k/8); D[i][j] in lane j + 16*(i/4), element i%4.
 // ---------------------------------------------------------------------------
@@ -2171,17 +2170,21 @@ __device__ __forceinline__ bf16x8 q8x8_bf16(uint2 r) {
     return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-// Prefill GEMM step pieces: this thread's 64 bytes of a token row's X hi and
-// lo from k offset kc; its copy into the LDS tile; the weight fragments and
+// Prefill GEMM step pieces: this thread's 16*XU bytes of a token row's X hi
+// and lo from k offset kc; its copy into the LDS tile; the weight fragments and
 // scales of step st (blocks clamped into the row).
-__device__ __forceinline__ void gm_x_load(uint4 (&xr)[8], const uint4 *xhr, const uint4 *xlr, uint32_t kc) {
-    const uint4 *ph = xhr + kc / 8, *pl = xlr + kc / 8;
+// (v4u, a native vector, so copies are plain loads and stores the register
+// allocator keeps in VGPRs; HIP's uint4 struct copies as memcpy.)
+template <int XU>
+__device__ __forceinline__ void gm_x_load(v4u (&xr)[2 * XU], const v4u *xhr, const v4u *xlr, uint32_t kc) {
+    const v4u *ph = xhr + kc / 8, *pl = xlr + kc / 8;
 #pragma unroll
-    for (int u = 0; u < 4; u++) { xr[u] = ph[u]; xr[4 + u] = pl[u]; }
+    for (int u = 0; u < XU; u++) { xr[u] = ph[u]; xr[XU + u] = pl[u]; }
 }
-__device__ __forceinline__ void gm_x_store(const uint4 (&xr)[8], uint16_t *dh, uint16_t *dl) {
+template <int XU>
+__device__ __forceinline__ void gm_x_store(const v4u (&xr)[2 * XU], uint16_t *dh, uint16_t *dl) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) { ((uint4 *)dh)[u] = xr[u]; ((uint4 *)dl)[u] = xr[4 + u]; }
+    for (int u = 0; u < XU; u++) { ((v4u *)dh)[u] = xr[u]; ((v4u *)dl)[u] = xr[XU + u]; }
 }
 __device__ __forceinline__ void gm_w_load(uint2 (&wq)[2][4], uint32_t (&wd)[2][4], const int8_t *const (&wr)[4],
                                           const uint16_t *const (&dr)[4], uint32_t st, uint32_t nblk) {
@@ -2196,22 +2199,76 @@ __device__ __forceinline__ void gm_w_load(uint2 (&wq)[2][4], uint32_t (&wd)[2][4
     }
 }
 
-#define GM_TN 128   // tokens per workgroup tile
 #define GM_TM 128   // weight rows per workgroup tile
 #define GM_KS 64    // K per step (two Q8_0 blocks)
 #define GM_LD (GM_KS + 8)   // padded LDS row (bf16 elements, 144 bytes)
+// WT tokens x 64 rows per wave (WT = 64 or 32), workgroup tile 2*WT tokens x GM_TM rows
 
-template <int EPI>
-__global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// One 64-wide K step st of the prefill GEMM: convert this step's weight set
+// (loaded two steps ago) to bf16, request the next step's X and, into the
+// same set, the weights of step st+2, run the MFMAs on the X tile in LDS
+// buffer cb, then store the next X tile into buffer cb^1. Steps past the end
+// only request (clamped) and store; their MFMAs are skipped.
+template <int NA, int WT, int XU>
+__device__ __forceinline__ void gm_step(f32x4 (&acc)[NA][4], uint2 (&wq)[2][4], uint32_t (&wd)[2][4],
+                                        v4u (&xr)[2 * XU], uint16_t (&xt)[2][2][2 * WT * GM_LD], uint32_t cb,
+                                        const v4u *xhr, const v4u *xlr,
+                                        const int8_t *const (&wr)[4], const uint16_t *const (&dr)[4],
+                                        uint32_t st, uint32_t nstep, uint32_t nblk, uint32_t K, uint32_t sc,
+                                        uint32_t xso, uint32_t wn, uint32_t li, uint32_t lg) {
+    constexpr uint32_t XK = 8 * XU;
+    bf16x8 wf[2][4];
+    float ds[2][4];
+#pragma unroll
+    for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            wf[bb][c] = q8x8_bf16(wq[bb][c]);
+            ds[bb][c] = h2f((uint16_t)wd[bb][c]);
+        }
+    gm_x_load<XU>(xr, xhr, xlr, min(min(st + 1, nstep - 1) * GM_KS + sc, K - XK));
+    __builtin_amdgcn_sched_barrier(0);
+    gm_w_load(wq, wd, wr, dr, min(st + 2, nstep - 1), nblk);
+    if (st < nstep) {
+        const bool two = st * 2 + 1 < nblk;                  // K tail: one block in the last step
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            if (bb == 1 && !two) continue;
+#pragma unroll
+            for (int a = 0; a < NA; a++) {
+                const uint32_t row = wn * WT + a * 16 + li;
+                const bf16x8 ah = *(const bf16x8 *)&xt[cb][0][row * GM_LD + bb * 32 + lg * 8];
+                const bf16x8 al = *(const bf16x8 *)&xt[cb][1][row * GM_LD + bb * 32 + lg * 8];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[bb][c], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[bb][c], p, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[a][c][e] = fmaf(ds[bb][c], p[e], acc[a][c][e]);
+                }
+            }
+        }
+    }
+    gm_x_store<XU>(xr, &xt[cb ^ 1][0][xso], &xt[cb ^ 1][1][xso]);
+    __syncthreads();
+}
+
+
+template <int EPI, int WT>
+__global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, WT == 64 ? 2 : 3)))
 k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d,
                                                       float *Y, uint32_t N, uint32_t M, uint32_t K, uint32_t ldy) {
+    constexpr uint32_t GM_TN = 2 * WT, NA = WT / 16;               // tokens per tile, token MFMA tiles per wave
     __shared__ __align__(16) uint16_t xt[2][2][GM_TN * GM_LD];     // [buffer][hi | lo][token][k]
     const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
-    // XCD-aware tile order: workgroup b runs on XCD b % 8; keep all token
-    // tiles of one weight tile on one XCD.
-    const uint32_t b = blockIdx.x, xcd = b & 7, qq = b >> 3;
-    const uint32_t mt_id = xcd + 8 * (qq / nb), nt_id = qq % nb;
-    if (mt_id >= mb) return;
+    // XCD-aware tile order: workgroup b runs on XCD b % 8, which owns weight
+    // tiles xcd, xcd+8, ...; on each XCD the token tile is the slow index, so
+    // the workgroups resident together share one X tile (2.6 MB at K 5120,
+    // held in that XCD's L2) and stream their weight tiles.
+    const uint32_t b = blockIdx.x, xcd = b & 7, qq = b >> 3, mper = (mb + 7) / 8;
+    const uint32_t mt_id = xcd + 8 * (qq % mper), nt_id = qq / mper;
+    if (mt_id >= mb || nt_id >= nb) return;
     const uint32_t n0 = nt_id * GM_TN, m0 = mt_id * GM_TM;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t wn = wave & 1, wm = wave >> 1;
@@ -2219,13 +2276,14 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d,
     const uint32_t nblk = K >> 5, nstep = (K + GM_KS - 1) / GM_KS;
     const uint16_t *xh = xs, *xl = xs + (size_t)N * K;
 
-    // X tile copy: thread t moves 32 k (64 bytes) of hi and of lo of one token
-    // row per step.
-    const uint32_t sr = t >> 1, sc = (t & 1) * 32;
-    const uint4 *xhr = (const uint4 *)(xh + (size_t)min(n0 + sr, N - 1) * K);
-    const uint4 *xlr = (const uint4 *)(xl + (size_t)min(n0 + sr, N - 1) * K);
+    // X tile copy: thread t moves 64*GM_TN/256 k of hi and of lo of one token
+    // row per step (32 k at 128 tokens, 16 at 64).
+    constexpr uint32_t XK = GM_KS * GM_TN / TPB, XU = XK / 8;     // k and uint4s per thread
+    const uint32_t sr = t / (GM_KS / XK), sc = (t % (GM_KS / XK)) * XK;
+    const v4u *xhr = (const v4u *)(xh + (size_t)min(n0 + sr, N - 1) * K);
+    const v4u *xlr = (const v4u *)(xl + (size_t)min(n0 + sr, N - 1) * K);
     const uint32_t xso = sr * GM_LD + sc;
-    uint4 xr[8];
+    v4u xr[2 * XU];
     // weight fragments: rows m0 + wm*64 + c*16 + li, bytes 8*lg .. +7 of each block
     const int8_t *wr[4];
     const uint16_t *dr[4];
@@ -2235,65 +2293,37 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d,
         wr[c] = qs + (size_t)m * K + lg * 8;
         dr[c] = d + (size_t)m * nblk;
     }
-    uint2 wq[2][4];
-    uint32_t wd[2][4];
-    f32x4 acc[4][4];
+    // Weights run two steps ahead in two register sets (A for even steps, B
+    // for odd): a step converts its set to bf16, then reloads it for the
+    // step after next; X runs one step ahead through the LDS double buffer
+    // and is requested before the weights, so the wait for it at the end of
+    // the step leaves the weight loads in flight.
+    uint2 wqA[2][4], wqB[2][4];
+    uint32_t wdA[2][4], wdB[2][4];
+    f32x4 acc[NA][4];
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int a = 0; a < NA; a++)
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    gm_x_load(xr, xhr, xlr, min(sc, K - 32));
-    gm_w_load(wq, wd, wr, dr, 0, nblk);
-    gm_x_store(xr, &xt[0][0][xso], &xt[0][1][xso]);
+    gm_x_load<XU>(xr, xhr, xlr, min(sc, K - XK));
+    __builtin_amdgcn_sched_barrier(0);
+    gm_w_load(wqA, wdA, wr, dr, 0, nblk);
+    gm_w_load(wqB, wdB, wr, dr, min(1u, nstep - 1), nblk);
+    gm_x_store<XU>(xr, &xt[0][0][xso], &xt[0][1][xso]);
     __syncthreads();
-    for (uint32_t st = 0; st < nstep; st++) {
-        const uint32_t buf = st & 1;
-        uint2 cq[2][4];
-        uint32_t cd[2][4];
-#pragma unroll
-        for (int bb = 0; bb < 2; bb++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) { cq[bb][c] = wq[bb][c]; cd[bb][c] = wd[bb][c]; }
-        const uint32_t nx = min(st + 1, nstep - 1);     // the last step re-requests itself, unused
-        gm_x_load(xr, xhr, xlr, min(nx * GM_KS + sc, K - 32));
-        gm_w_load(wq, wd, wr, dr, nx, nblk);
-        const bool two = st * 2 + 1 < nblk;                  // K tail: one block in the last step
-#pragma unroll
-        for (int bb = 0; bb < 2; bb++) {
-            if (bb == 1 && !two) continue;
-            bf16x8 wf[4];
-            float ds[4];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                wf[c] = q8x8_bf16(cq[bb][c]);
-                ds[c] = h2f((uint16_t)cd[bb][c]);
-            }
-#pragma unroll
-            for (int a = 0; a < 4; a++) {
-                const uint32_t row = wn * 64 + a * 16 + li;
-                const bf16x8 ah = *(const bf16x8 *)&xt[buf][0][row * GM_LD + bb * 32 + lg * 8];
-                const bf16x8 al = *(const bf16x8 *)&xt[buf][1][row * GM_LD + bb * 32 + lg * 8];
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
-                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[c], p, 0, 0, 0);
-                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[c], p, 0, 0, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) acc[a][c][e] = fmaf(ds[c], p[e], acc[a][c][e]);
-                }
-            }
-        }
-        gm_x_store(xr, &xt[buf ^ 1][0][xso], &xt[buf ^ 1][1][xso]);
-        __syncthreads();
+    const uint32_t npair = (nstep + 1) / 2;
+    for (uint32_t pr = 0; pr < npair; pr++) {
+        gm_step<NA, WT, XU>(acc, wqA, wdA, xr, xt, 0, xhr, xlr, wr, dr, 2 * pr, nstep, nblk, K, sc, xso, wn, li, lg);
+        gm_step<NA, WT, XU>(acc, wqB, wdB, xr, xt, 1, xhr, xlr, wr, dr, 2 * pr + 1, nstep, nblk, K, sc, xso, wn, li, lg);
     }
     // epilogue: lane holds D[i = 4*lg + e][j = li] of each tile
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int a = 0; a < NA; a++)
 #pragma unroll
         for (int c = 0; c < 4; c++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const uint32_t n = n0 + wn * 64 + a * 16 + lg * 4 + e;
+                const uint32_t n = n0 + wn * WT + a * 16 + lg * 4 + e;
                 const uint32_t m = m0 + wm * 64 + c * 16 + li;
                 const float v = acc[a][c][e];
                 if (EPI == SGK_EPI_SWIGLU) {
@@ -2333,9 +2363,9 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
         const uint64_t total = (uint64_t)a->N * k4;
         const uint32_t sg = (uint32_t)min((total + TPB - 1) / TPB, (uint64_t)4096);
         hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
-        const uint32_t nb = (a->N + GM_TN - 1) / GM_TN, mb = (a->M + GM_TM - 1) / GM_TM;
+        const uint32_t mb = (a->M + GM_TM - 1) / GM_TM, nb = (a->N + 127) / 128;
         const uint32_t grid = 8 * nb * ((mb + 7) / 8);
-#define GQ(E) hipLaunchKernelGGL(k_gemm_q8_mfma<E>, dim3(grid), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy)
+#define GQ(E) hipLaunchKernelGGL((k_gemm_q8_mfma<E, 64>), dim3(grid), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy)
         if (a->epi == SGK_EPI_ADD) GQ(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GQ(SGK_EPI_SWIGLU); else GQ(SGK_EPI_STORE);
 #undef GQ
     } else {

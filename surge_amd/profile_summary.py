@@ -14,6 +14,16 @@
       bench.py (from the third k_embed launch to the last k_step_advance: the
       prefill and the first warm-up steps are left out), the span per token
       and the time between kernels;
+  python -m surge_amd.profile_summary prefill KERNEL_TRACE_CSV
+      per kernel: calls, average and total time over the prefill of a
+      `rocprofv3 --kernel-trace` run of bench.py (from the first k_embed_rows
+      launch to the last launch before the first decode k_embed);
+  python -m surge_amd.profile_summary counters COUNTER_CSV --kernel NAME
+      every counter of a `rocprofv3 --pmc` run averaged over the dispatches of
+      kernel NAME (prefix match), with derived fractions: wave cycles spent
+      waiting for instruction issue (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES) or on
+      memory (SQ_WAIT_ANY / SQ_WAVE_CYCLES), and MFMA busy per SIMD
+      (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs * 4 SIMDs * CUs));
   python -m surge_amd.profile_summary traffic FETCH_CSV WRITE_CSV --kernel NAME --calib-bytes B
          --algo-bytes A --json OUT
       HBM bytes per dispatch of kernel NAME (prefix match): FETCH_SIZE from the
@@ -74,6 +84,63 @@ def decode(path):
     print("|---|---|---|---|---|")
     for k, (n, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
         print(f"| `{k}` | {n / ntok:.2f} | {t / n / 1e3:.2f} | {t / ntok / 1e3:.1f} | {100 * t / busy:.1f} |")
+
+
+def prefill(path):
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    names = [short(r["Kernel_Name"]) for r in rows]
+    st = next((i for i, n in enumerate(names) if n == "k_embed_rows"), None)
+    en = next((i for i, n in enumerate(names) if n == "k_embed"), None)
+    if st is None or en is None or en <= st:
+        print("no prefill in this trace")
+        return
+    seg = rows[st:en]
+    span = int(seg[-1]["End_Timestamp"]) - int(seg[0]["Start_Timestamp"])
+    agg = defaultdict(lambda: [0, 0])
+    busy = 0
+    for r in seg:
+        d = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        key = f"{short(r['Kernel_Name'])} (grid {int(r['Grid_Size_X']) // max(1, int(r['Workgroup_Size_X']))}" \
+              f"x{r['Grid_Size_Y']}x{r.get('Grid_Size_Z', '1')})"
+        agg[key][0] += 1
+        agg[key][1] += d
+        busy += d
+    print(f"prefill: span {span / 1e6:.1f} ms, kernels busy {busy / 1e6:.1f} ms\n")
+    print("| kernel (workgroups) | calls | avg us | total ms | % of busy |")
+    print("|---|---|---|---|---|")
+    for k, (n, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        if t < 0.001 * busy:
+            continue
+        print(f"| `{k}` | {n} | {t / n / 1e3:.1f} | {t / 1e6:.1f} | {100 * t / busy:.1f} |")
+
+
+def counters(path, kernel, cus=256):
+    vals = defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        if short(r["Kernel_Name"]).startswith(kernel):
+            vals[r["Counter_Name"]].append(float(r["Counter_Value"]))
+    if not vals:
+        print(f"no dispatches of {kernel}")
+        return None
+    avg = {c: sum(v) / len(v) for c, v in vals.items()}
+    print(f"`{kernel}`: {len(next(iter(vals.values())))} dispatches\n")
+    print("| counter | average per dispatch |")
+    print("|---|---|")
+    for c in sorted(avg):
+        print(f"| {c} | {avg[c]:.0f} |")
+    out = {"kernel": kernel, "counters": avg}
+    wc = avg.get("SQ_WAVE_CYCLES")
+    if wc:
+        for c in ("SQ_WAIT_INST_ANY", "SQ_WAIT_ANY", "SQ_ACTIVE_INST_ANY"):
+            if c in avg:
+                out[c + "/SQ_WAVE_CYCLES"] = avg[c] / wc
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in avg and avg.get("GRBM_GUI_ACTIVE"):
+        out["mfma_busy_per_simd"] = avg["SQ_VALU_MFMA_BUSY_CYCLES"] / (avg["GRBM_GUI_ACTIVE"] / 8 * 4 * cus)
+    print()
+    for k, v in out.items():
+        if k not in ("kernel", "counters"):
+            print(f"- {k}: {v:.3f}")
+    return out
 
 
 def pmc(path, counter, calib_bytes):
@@ -139,7 +206,7 @@ def trace(path, kernel, last):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("mode", choices=["stats", "pmc", "trace", "decode", "traffic"])
+    ap.add_argument("mode", choices=["stats", "pmc", "trace", "decode", "traffic", "prefill", "counters"])
     ap.add_argument("csv")
     ap.add_argument("csv2", nargs="?", default=None)
     ap.add_argument("--algo-bytes", type=float, default=0)
@@ -154,6 +221,12 @@ def main():
         stats(a.csv, a.tokens)
     elif a.mode == "decode":
         decode(a.csv)
+    elif a.mode == "prefill":
+        prefill(a.csv)
+    elif a.mode == "counters":
+        out = counters(a.csv, a.kernel)
+        if a.json and out:
+            json.dump(out, open(a.json, "w"), indent=1)
     elif a.mode == "traffic":
         out = traffic(a.csv, a.csv2, a.kernel, a.calib_bytes, a.algo_bytes)
         print(json.dumps(out, indent=1))
