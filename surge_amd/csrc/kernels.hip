@@ -2114,21 +2114,23 @@ extern "C" hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream
 // Prefill GEMM Y[N][M] = X[N][K] * W[M][K]^T (chunk of N tokens through one
 // weight), W in the Q8 device layout, on MFMA.
 //
-// Precision: int8 weights are exact in bf16 (|q| <= 127); x is split once per
-// GEMM into bf16 hi + lo (x = hi + lo to ~16 bits; k_split_bf16), so each
-// Q8_0 block's partial dot is two v_mfma_f32_16x16x32_bf16 into a zeroed fp32
-// tile, then scaled by the block's f16 scale into the fp32 accumulator. The
-// weights are never dequantised into bf16 (d*q has ~18 significant bits).
+// Precision: x is split once per GEMM into bf16 hi + lo (k_split_bf16; x =
+// hi + lo to ~2^-18); each weight w = d*q is exact in fp32 (an f16 scale times
+// an int8 has at most 18 significant bits) and is split the same way when its
+// tile is staged. A product is xh*wh + xh*wl + xl*wh (xl*wl, ~2^-18 of it, is
+// dropped): three v_mfma_f32_16x16x32_bf16 accumulating straight into the
+// fp32 output tile, so no per-block arithmetic sits between MFMAs.
 //
 // Tiling: workgroup 256 threads = 4 waves over a 128-token x 128-row tile
-// (waves 2 x 2, each 64 x 64 = 4 x 4 MFMA tiles of 16x16; the kernel also
-// takes 32 x 64 wave tiles, which measured slower), K in steps of 64 (two
-// Q8_0 blocks). The X hi/lo tile of a step (32 KB) is double-buffered in
-// LDS: the next step's tile and weights are requested before the current
-// step's MFMAs and stored after them, one barrier per step. Each lane loads
-// its weight fragments (8 int8 of 4 rows per block) straight from memory one
-// step ahead and converts them to bf16. Every load is unconditional at a
-// clamped index (rows past N or M are computed and dropped at the store).
+// (waves 2 x 2, each 64 x 64 = 4 x 4 MFMA tiles of 16x16), K in steps of one
+// Q8_0 block (32). Per step the X hi|lo tile and the dequantised W hi|lo tile
+// (2 x 10 KB each) are double-buffered in LDS: X is requested one step ahead,
+// the raw weights two steps ahead (two register sets), and the next step's
+// tiles are stored after the current step's MFMAs, one barrier per step.
+// XCD-aware order: workgroup b runs on XCD b % 8, which owns weight tiles
+// xcd, xcd+8, ...; on each XCD the token tile is the slow index. Every load
+// is unconditional at a clamped index (rows past N or M are computed and
+// dropped at the store).
 // MFMA 16x16x32 operand layout: A[i][k] in lane i + 16*(k/8), element k%8;
 // B[k][j] in lane j + 16*(k/8); D[i][j] in lane j + 16*(i/4), element i%4.
 // ---------------------------------------------------------------------------
@@ -2156,116 +2158,83 @@ __global__ void __launch_bounds__(TPB) k_split_bf16(const float *X, uint32_t ldx
     }
 }
 
-// 8 int8 weights -> 8 bf16, exact.
-__device__ __forceinline__ bf16x8 q8x8_bf16(uint2 r) {
-    uint32_t o[4];
-#pragma unroll
-    for (int p = 0; p < 2; p++) {
-        const uint32_t w = p ? r.y : r.x;
-        const bf16x2 a = {(__bf16)(float)(int8_t)w, (__bf16)(float)(int8_t)(w >> 8)};
-        const bf16x2 b = {(__bf16)(float)(int8_t)(w >> 16), (__bf16)(float)((int32_t)w >> 24)};
-        o[2 * p] = __builtin_bit_cast(uint32_t, a);
-        o[2 * p + 1] = __builtin_bit_cast(uint32_t, b);
-    }
-    return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
-}
-
-// Prefill GEMM step pieces: this thread's 16*XU bytes of a token row's X hi
-// and lo from k offset kc; its copy into the LDS tile; the weight fragments and
-// scales of step st (blocks clamped into the row).
-// (v4u, a native vector, so copies are plain loads and stores the register
-// allocator keeps in VGPRs; HIP's uint4 struct copies as memcpy.)
-template <int XU>
-__device__ __forceinline__ void gm_x_load(v4u (&xr)[2 * XU], const v4u *xhr, const v4u *xlr, uint32_t kc) {
-    const v4u *ph = xhr + kc / 8, *pl = xlr + kc / 8;
-#pragma unroll
-    for (int u = 0; u < XU; u++) { xr[u] = ph[u]; xr[XU + u] = pl[u]; }
-}
-template <int XU>
-__device__ __forceinline__ void gm_x_store(const v4u (&xr)[2 * XU], uint16_t *dh, uint16_t *dl) {
-#pragma unroll
-    for (int u = 0; u < XU; u++) { ((v4u *)dh)[u] = xr[u]; ((v4u *)dl)[u] = xr[XU + u]; }
-}
-__device__ __forceinline__ void gm_w_load(uint2 (&wq)[2][4], uint32_t (&wd)[2][4], const int8_t *const (&wr)[4],
-                                          const uint16_t *const (&dr)[4], uint32_t st, uint32_t nblk) {
-#pragma unroll
-    for (int bb = 0; bb < 2; bb++) {
-        const uint32_t kb = min(st * 2 + bb, nblk - 1);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            wq[bb][c] = *(const uint2 *)(wr[c] + (size_t)kb * 32);
-            wd[bb][c] = dr[c][kb];
-        }
-    }
-}
-
+#define GM_TN 128   // tokens per workgroup tile
 #define GM_TM 128   // weight rows per workgroup tile
-#define GM_KS 64    // K per step (two Q8_0 blocks)
-#define GM_LD (GM_KS + 8)   // padded LDS row (bf16 elements, 144 bytes)
-// WT tokens x 64 rows per wave (WT = 64 or 32), workgroup tile 2*WT tokens x GM_TM rows
+#define GM_LD 40    // LDS row of one 32-wide step, padded (bf16 elements, 80 bytes)
 
-// One 64-wide K step st of the prefill GEMM: convert this step's weight set
-// (loaded two steps ago) to bf16, request the next step's X and, into the
-// same set, the weights of step st+2, run the MFMAs on the X tile in LDS
-// buffer cb, then store the next X tile into buffer cb^1. Steps past the end
-// only request (clamped) and store; their MFMAs are skipped.
-template <int NA, int WT, int XU>
-__device__ __forceinline__ void gm_step(f32x4 (&acc)[NA][4], uint2 (&wq)[2][4], uint32_t (&wd)[2][4],
-                                        v4u (&xr)[2 * XU], uint16_t (&xt)[2][2][2 * WT * GM_LD], uint32_t cb,
-                                        const v4u *xhr, const v4u *xlr,
-                                        const int8_t *const (&wr)[4], const uint16_t *const (&dr)[4],
-                                        uint32_t st, uint32_t nstep, uint32_t nblk, uint32_t K, uint32_t sc,
-                                        uint32_t xso, uint32_t wn, uint32_t li, uint32_t lg) {
-    constexpr uint32_t XK = 8 * XU;
-    bf16x8 wf[2][4];
-    float ds[2][4];
+// 16 int8 weights of one row and its block scale -> 16 bf16 hi and 16 bf16 lo
+// of w = d*q, stored at h[0..15] and l[0..15].
+__device__ __forceinline__ void gm_dequant16(v4u q, uint32_t dbits, uint16_t *h, uint16_t *l) {
+    const float dd = h2f((uint16_t)dbits);
+    uint32_t oh[8], ol[8];
 #pragma unroll
-    for (int bb = 0; bb < 2; bb++)
+    for (int p = 0; p < 8; p++) {
+        const uint32_t w = q[p >> 1] >> (16 * (p & 1));
+        const float w0 = dd * (float)(int8_t)w, w1 = dd * (float)(int8_t)(w >> 8);
+        const bf16x2 hh = {(__bf16)w0, (__bf16)w1};
+        const bf16x2 ll = {(__bf16)(w0 - (float)hh[0]), (__bf16)(w1 - (float)hh[1])};
+        oh[p] = __builtin_bit_cast(uint32_t, hh);
+        ol[p] = __builtin_bit_cast(uint32_t, ll);
+    }
+    ((v4u *)h)[0] = (v4u){oh[0], oh[1], oh[2], oh[3]};
+    ((v4u *)h)[1] = (v4u){oh[4], oh[5], oh[6], oh[7]};
+    ((v4u *)l)[0] = (v4u){ol[0], ol[1], ol[2], ol[3]};
+    ((v4u *)l)[1] = (v4u){ol[4], ol[5], ol[6], ol[7]};
+}
+
+// One K step (Q8_0 block s) of the prefill GEMM on LDS buffer cb: request the
+// next block's X and, into the register set this step frees, the raw weights
+// of block s+2; the MFMAs; then stage block s+1 (X from xr, W dequantised from
+// the other register set wn) into buffer cb^1. Blocks past the end only
+// request (clamped) and stage; their MFMAs are skipped.
+__device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &wself, uint32_t &dself,
+                                        const v4u &wnext, const uint32_t &dnext,
+                                        uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wt)[2][2][GM_TM * GM_LD],
+                                        uint32_t cb, const v4u *xhr, const v4u *xlr, const v4u *wrow,
+                                        const uint16_t *drow, uint32_t s, uint32_t nblk, uint32_t so,
+                                        uint32_t wn, uint32_t wm, uint32_t li, uint32_t lg) {
+    const uint32_t s1 = min(s + 1, nblk - 1), s2 = min(s + 2, nblk - 1);
+#pragma unroll
+    for (int u = 0; u < 2; u++) { xr[u] = xhr[s1 * 4 + u]; xr[2 + u] = xlr[s1 * 4 + u]; }
+    __builtin_amdgcn_sched_barrier(0);
+    wself = wrow[s2 * 2];
+    dself = drow[s2];
+    if (s < nblk) {
+        bf16x8 bh[4], bl[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            wf[bb][c] = q8x8_bf16(wq[bb][c]);
-            ds[bb][c] = h2f((uint16_t)wd[bb][c]);
+            const uint32_t row = wm * 64 + c * 16 + li;
+            bh[c] = *(const bf16x8 *)&wt[cb][0][row * GM_LD + lg * 8];
+            bl[c] = *(const bf16x8 *)&wt[cb][1][row * GM_LD + lg * 8];
         }
-    gm_x_load<XU>(xr, xhr, xlr, min(min(st + 1, nstep - 1) * GM_KS + sc, K - XK));
-    __builtin_amdgcn_sched_barrier(0);
-    gm_w_load(wq, wd, wr, dr, min(st + 2, nstep - 1), nblk);
-    if (st < nstep) {
-        const bool two = st * 2 + 1 < nblk;                  // K tail: one block in the last step
 #pragma unroll
-        for (int bb = 0; bb < 2; bb++) {
-            if (bb == 1 && !two) continue;
+        for (int a = 0; a < 4; a++) {
+            const uint32_t row = wn * 64 + a * 16 + li;
+            const bf16x8 ah = *(const bf16x8 *)&xt[cb][0][row * GM_LD + lg * 8];
+            const bf16x8 al = *(const bf16x8 *)&xt[cb][1][row * GM_LD + lg * 8];
 #pragma unroll
-            for (int a = 0; a < NA; a++) {
-                const uint32_t row = wn * WT + a * 16 + li;
-                const bf16x8 ah = *(const bf16x8 *)&xt[cb][0][row * GM_LD + bb * 32 + lg * 8];
-                const bf16x8 al = *(const bf16x8 *)&xt[cb][1][row * GM_LD + bb * 32 + lg * 8];
+            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh[c], acc[a][c], 0, 0, 0);
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    f32x4 p = (f32x4){0.f, 0.f, 0.f, 0.f};
-                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[bb][c], p, 0, 0, 0);
-                    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[bb][c], p, 0, 0, 0);
+            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl[c], acc[a][c], 0, 0, 0);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) acc[a][c][e] = fmaf(ds[bb][c], p[e], acc[a][c][e]);
-                }
-            }
+            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh[c], acc[a][c], 0, 0, 0);
         }
     }
-    gm_x_store<XU>(xr, &xt[cb ^ 1][0][xso], &xt[cb ^ 1][1][xso]);
+    gm_dequant16(wnext, dnext, &wt[cb ^ 1][0][so], &wt[cb ^ 1][1][so]);
+    ((v4u *)&xt[cb ^ 1][0][so])[0] = xr[0];
+    ((v4u *)&xt[cb ^ 1][0][so])[1] = xr[1];
+    ((v4u *)&xt[cb ^ 1][1][so])[0] = xr[2];
+    ((v4u *)&xt[cb ^ 1][1][so])[1] = xr[3];
     __syncthreads();
 }
 
-
-template <int EPI, int WT>
-__global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, WT == 64 ? 2 : 3)))
-k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d,
-                                                      float *Y, uint32_t N, uint32_t M, uint32_t K, uint32_t ldy) {
-    constexpr uint32_t GM_TN = 2 * WT, NA = WT / 16;               // tokens per tile, token MFMA tiles per wave
+template <int EPI>
+__global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, uint32_t N, uint32_t M,
+               uint32_t K, uint32_t ldy) {
     __shared__ __align__(16) uint16_t xt[2][2][GM_TN * GM_LD];     // [buffer][hi | lo][token][k]
+    __shared__ __align__(16) uint16_t wt[2][2][GM_TM * GM_LD];     // [buffer][hi | lo][row][k]
     const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
-    // XCD-aware tile order: workgroup b runs on XCD b % 8, which owns weight
-    // tiles xcd, xcd+8, ...; on each XCD the token tile is the slow index, so
-    // the workgroups resident together share one X tile (2.6 MB at K 5120,
-    // held in that XCD's L2) and stream their weight tiles.
     const uint32_t b = blockIdx.x, xcd = b & 7, qq = b >> 3, mper = (mb + 7) / 8;
     const uint32_t mt_id = xcd + 8 * (qq % mper), nt_id = qq / mper;
     if (mt_id >= mb || nt_id >= nb) return;
@@ -2273,57 +2242,50 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d,
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t wn = wave & 1, wm = wave >> 1;
     const uint32_t li = lane & 15, lg = lane >> 4;
-    const uint32_t nblk = K >> 5, nstep = (K + GM_KS - 1) / GM_KS;
-    const uint16_t *xh = xs, *xl = xs + (size_t)N * K;
+    const uint32_t nblk = K >> 5;
+    // staging role: row t/2 of both tiles, k 16*(t%2) .. +15 of each block
+    const uint32_t sr = t >> 1, sk = (t & 1) * 16, so = sr * GM_LD + sk;
+    const size_t xrow = (size_t)min(n0 + sr, N - 1) * K + sk;
+    const v4u *xhr = (const v4u *)(xs + xrow), *xlr = (const v4u *)(xs + (size_t)N * K + xrow);
+    const uint32_t wrow_i = min(m0 + sr, M - 1);
+    const v4u *wrow = (const v4u *)(qs + (size_t)wrow_i * K + sk);     // block s: wrow[2 s] (16 int8)
+    const uint16_t *drow = d + (size_t)wrow_i * nblk;
 
-    // X tile copy: thread t moves 64*GM_TN/256 k of hi and of lo of one token
-    // row per step (32 k at 128 tokens, 16 at 64).
-    constexpr uint32_t XK = GM_KS * GM_TN / TPB, XU = XK / 8;     // k and uint4s per thread
-    const uint32_t sr = t / (GM_KS / XK), sc = (t % (GM_KS / XK)) * XK;
-    const v4u *xhr = (const v4u *)(xh + (size_t)min(n0 + sr, N - 1) * K);
-    const v4u *xlr = (const v4u *)(xl + (size_t)min(n0 + sr, N - 1) * K);
-    const uint32_t xso = sr * GM_LD + sc;
-    v4u xr[2 * XU];
-    // weight fragments: rows m0 + wm*64 + c*16 + li, bytes 8*lg .. +7 of each block
-    const int8_t *wr[4];
-    const uint16_t *dr[4];
+    f32x4 acc[4][4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint32_t m = min(m0 + wm * 64 + c * 16 + li, M - 1);
-        wr[c] = qs + (size_t)m * K + lg * 8;
-        dr[c] = d + (size_t)m * nblk;
-    }
-    // Weights run two steps ahead in two register sets (A for even steps, B
-    // for odd): a step converts its set to bf16, then reloads it for the
-    // step after next; X runs one step ahead through the LDS double buffer
-    // and is requested before the weights, so the wait for it at the end of
-    // the step leaves the weight loads in flight.
-    uint2 wqA[2][4], wqB[2][4];
-    uint32_t wdA[2][4], wdB[2][4];
-    f32x4 acc[NA][4];
-#pragma unroll
-    for (int a = 0; a < NA; a++)
+    for (int a = 0; a < 4; a++)
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    gm_x_load<XU>(xr, xhr, xlr, min(sc, K - XK));
+    v4u xr[4], wA, wB;
+    uint32_t dA, dB;
+    // prologue: block 0 staged into buffer 0, block 1's raw weights in B
+#pragma unroll
+    for (int u = 0; u < 2; u++) { xr[u] = xhr[u]; xr[2 + u] = xlr[u]; }
     __builtin_amdgcn_sched_barrier(0);
-    gm_w_load(wqA, wdA, wr, dr, 0, nblk);
-    gm_w_load(wqB, wdB, wr, dr, min(1u, nstep - 1), nblk);
-    gm_x_store<XU>(xr, &xt[0][0][xso], &xt[0][1][xso]);
+    wA = wrow[0];
+    dA = drow[0];
+    wB = wrow[min(1u, nblk - 1) * 2];
+    dB = drow[min(1u, nblk - 1)];
+    gm_dequant16(wA, dA, &wt[0][0][so], &wt[0][1][so]);
+    ((v4u *)&xt[0][0][so])[0] = xr[0];
+    ((v4u *)&xt[0][0][so])[1] = xr[1];
+    ((v4u *)&xt[0][1][so])[0] = xr[2];
+    ((v4u *)&xt[0][1][so])[1] = xr[3];
     __syncthreads();
-    const uint32_t npair = (nstep + 1) / 2;
-    for (uint32_t pr = 0; pr < npair; pr++) {
-        gm_step<NA, WT, XU>(acc, wqA, wdA, xr, xt, 0, xhr, xlr, wr, dr, 2 * pr, nstep, nblk, K, sc, xso, wn, li, lg);
-        gm_step<NA, WT, XU>(acc, wqB, wdB, xr, xt, 1, xhr, xlr, wr, dr, 2 * pr + 1, nstep, nblk, K, sc, xso, wn, li, lg);
+    // step s uses buffer s%2; its register set (A for even s) is reloaded with
+    // block s+2 while the other set (holding block s+1) is staged
+    for (uint32_t s = 0; s < nblk; s += 2) {
+        gm_step(acc, xr, wA, dA, wB, dB, xt, wt, 0, xhr, xlr, wrow, drow, s, nblk, so, wn, wm, li, lg);
+        gm_step(acc, xr, wB, dB, wA, dA, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, nblk, so, wn, wm, li, lg);
     }
     // epilogue: lane holds D[i = 4*lg + e][j = li] of each tile
 #pragma unroll
-    for (int a = 0; a < NA; a++)
+    for (int a = 0; a < 4; a++)
 #pragma unroll
         for (int c = 0; c < 4; c++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const uint32_t n = n0 + wn * WT + a * 16 + lg * 4 + e;
+                const uint32_t n = n0 + wn * 64 + a * 16 + lg * 4 + e;
                 const uint32_t m = m0 + wm * 64 + c * 16 + li;
                 const float v = acc[a][c][e];
                 if (EPI == SGK_EPI_SWIGLU) {
@@ -2365,7 +2327,7 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
         hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
         const uint32_t mb = (a->M + GM_TM - 1) / GM_TM, nb = (a->N + 127) / 128;
         const uint32_t grid = 8 * nb * ((mb + 7) / 8);
-#define GQ(E) hipLaunchKernelGGL((k_gemm_q8_mfma<E, 64>), dim3(grid), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy)
+#define GQ(E) hipLaunchKernelGGL((k_gemm_q8_mfma<E>), dim3(grid), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy)
         if (a->epi == SGK_EPI_ADD) GQ(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GQ(SGK_EPI_SWIGLU); else GQ(SGK_EPI_STORE);
 #undef GQ
     } else {
