@@ -1281,8 +1281,12 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t n) {
             A.q_tok = in_rows; A.out_tok = g->attn_width; A.max_splits = SGK_PREFILL_SPLITS; A.ntok = n;
             A.scale = (float)(1.0 / sqrt((double)hd)); A.prefill = 1;
             if ((e = sgk_attn_prep(&A, L->qn, L->kn, g->cs_table, c->rms_eps, s)) != hipSuccess) return e;
-            if ((e = sgk_attn_partial(&A, s)) != hipSuccess) return e;
-            if ((e = sgk_attn_combine(&A, s)) != hipSuccess) return e;
+            if (hd == 64 || hd == 128 || hd == 256) {
+                if ((e = sgk_attn_flash(&A, s)) != hipSuccess) return e;
+            } else {
+                if ((e = sgk_attn_partial(&A, s)) != hipSuccess) return e;
+                if ((e = sgk_attn_combine(&A, s)) != hipSuccess) return e;
+            }
             if ((e = gemm_rows(g, &L->out, g->pf_CTX, g->attn_width, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;
         } else {
             sgk_gdn d = {0};
@@ -1303,8 +1307,9 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t n) {
 }
 
 /* Chunked prompt ingest (surge.h:1276-1309): every projection of a chunk is
- * one MFMA GEMM; attention runs the decode split-K kernels over the chunk's
- * tokens (each against its own causal prefix); the DeltaNet conv and delta
+ * one MFMA GEMM; attention is one MFMA pass per (64-token block, head) over
+ * the causal prefix (head_dim 64/128/256; other sizes run the decode split-K
+ * kernels per token); the DeltaNet conv and delta
  * rule scan the chunk in order with the state threaded through, exactly as
  * decode would. Only the last row gets out_norm + lm_head. */
 sg_err sg_gpu_prefill(sg_gpu *g, const sg_model *m, const int32_t *tokens, uint32_t n_tokens,

@@ -133,6 +133,10 @@ hipError_t sgk_attn_prep(const sgk_attn *a, const float *qn, const float *kn,
 hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s);
 /* LSE combine with the optional fused sigmoid output gate. */
 hipError_t sgk_attn_combine(const sgk_attn *a, hipStream_t s);
+/* Prefill: causal attention of a chunk (ntok tokens at consecutive positions
+ * from steps[0].pos, prepped by sgk_attn_prep) in one MFMA pass per (64-token
+ * block, head), gate applied, written to out. head_dim 64, 128 or 256. */
+hipError_t sgk_attn_flash(const sgk_attn *a, hipStream_t s);
 
 /* Gated DeltaNet decode step for one layer, fused: causal conv (ring state
  * of 4 slots indexed by position) + SiLU, q/k RMS (eps 1e-6) and scaling,

@@ -98,6 +98,7 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 // Streaming (non-temporal) 16-byte load: weights are read once per token.
 __device__ __forceinline__ uint4 ldnt(const uint4 *p) {
     const v4u v = __builtin_nontemporal_load((const v4u *)p);
@@ -1376,6 +1377,229 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill attention on MFMA: causal attention of a chunk of tokens (at
+// consecutive positions, after k_attn_prep stored their K/V and prepped q)
+// against every key up to each token's position, in one pass per (64-token
+// block, query head) with an online softmax, finished in place (divide by the
+// row sum, sigmoid output gate), so no partials or combine pass.
+//
+// Scores S = Q K^T on v_mfma_f32_16x16x32_f16: K is the f16 cache itself, q is
+// split into f16 hi + lo (q = hi + lo to ~2^-22), two MFMAs per tile. P V on
+// the same MFMA with p split into f16 hi + lo against V, which is staged
+// transposed in LDS (an 8 x 8 transpose in registers per thread) so its
+// B fragments are contiguous. Per 64-key tile: K and V^T staged, one wave per
+// 16-token row tile: scores (scaled, masked above the row's position), tile
+// maximum and sum by 16-lane butterflies, the running max/sum/accumulator
+// rescaled as the decode partial does per tile (ref.c:416-555 semantics; a
+// fully masked tile leaves a row unchanged), P through LDS into the A layout.
+// MFMA 16x16x32 layout as in the prefill GEMM.
+// ---------------------------------------------------------------------------
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+#define FA_TQ 64    // tokens per workgroup (4 waves x 16)
+#define FA_TK 64    // keys per tile
+#define FA_PLD (FA_TK + 8)
+
+// x[0..7] -> f16 hi and lo fragments
+__device__ __forceinline__ void fa_split8(const float *x, f16x8 &hi, f16x8 &lo) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const _Float16 h = (_Float16)x[e];
+        hi[e] = h;
+        lo[e] = (_Float16)(x[e] - (float)h);
+    }
+}
+
+// max / sum over the 16 lanes of a row group (lanes sharing lane / 16)
+__device__ __forceinline__ float fa_max16(float v) {
+    v = fmaxf(v, lane_xor1(v));
+    v = fmaxf(v, lane_xor2(v));
+    v = fmaxf(v, lane_xor<4>(v));
+    return fmaxf(v, lane_xor8(v));
+}
+__device__ __forceinline__ float fa_sum16(float v) {
+    v += lane_xor1(v);
+    v += lane_xor2(v);
+    v += lane_xor<4>(v);
+    return v + lane_xor8(v);
+}
+
+template <int HD>
+__global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
+    static_assert(HD % 64 == 0 && HD <= 256, "flash prefill takes head_dim 64, 128, 192 or 256");
+    constexpr int KLD = HD + 8, NKB = HD / 32, NNT = HD / 16;
+    constexpr int KDT = HD / 4;                 // K staging: dims per thread (4 threads per key)
+    constexpr int VDC = HD / 8, VKG = TPB / VDC; // V staging: dim chunks of 8, key groups of 8
+    __shared__ __align__(16) uint16_t ks[FA_TK * KLD];
+    __shared__ __align__(16) uint16_t vt[HD * FA_PLD];
+    __shared__ __align__(16) uint16_t ps[2][FA_TQ * FA_PLD];
+    const uint32_t h = blockIdx.x, tb = blockIdx.y, G = a.n_heads / a.n_kv, hk = h / G, n_kv = a.n_kv;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 15, lg = lane >> 4;
+    const uint32_t ntok = a.ntok, z0 = tb * FA_TQ;
+    const uint32_t base = a.steps[0].pos;
+    const uint32_t zlast = min(z0 + FA_TQ, ntok) - 1;
+    const uint32_t kend = base + zlast + 1;     // keys 0 .. kend-1 (positions are consecutive)
+    const uint16_t *kc = a.kc, *vc = a.vc;
+
+    // q fragments of this wave's 16 tokens (A operand: row li, dims 8*lg.. of each 32)
+    f16x8 qh[NKB], ql[NKB];
+    {
+        const uint32_t z = min(z0 + wave * 16 + li, ntok - 1);
+        const float *qr = a.q + (size_t)z * a.q_tok + (size_t)h * a.q_stride;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const float4 x0 = *(const float4 *)(qr + kb * 32 + lg * 8);
+            const float4 x1 = *(const float4 *)(qr + kb * 32 + lg * 8 + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            fa_split8(xv, qh[kb], ql[kb]);
+        }
+    }
+    // this lane's rows in the D layout: 4*lg + e of the wave's tile
+    uint32_t rpos[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) rpos[e] = base + z0 + wave * 16 + lg * 4 + e;
+    float mrun[4], srun[4];
+    f32x4 o[NNT];
+#pragma unroll
+    for (int e = 0; e < 4; e++) { mrun[e] = -INFINITY; srun[e] = 0.0f; }
+#pragma unroll
+    for (int n = 0; n < NNT; n++) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t kk = t >> 2, kd = (t & 3) * KDT;        // K staging role
+    const uint32_t vkg = t / VDC, vdc = t % VDC;            // V staging role
+    for (uint32_t k0 = 0; k0 < kend; k0 += FA_TK) {
+        // stage K [key][dim] and V^T [dim][key] (keys clamped into the range)
+        {
+            const uint32_t key = min(k0 + kk, kend - 1);
+            const v4u *src = (const v4u *)(kc + ((size_t)key * n_kv + hk) * HD + kd);
+            v4u r[KDT / 8];
+#pragma unroll
+            for (int u = 0; u < KDT / 8; u++) r[u] = src[u];
+#pragma unroll
+            for (int u = 0; u < KDT / 8; u++) ((v4u *)&ks[kk * KLD + kd])[u] = r[u];
+        }
+        if (vkg < FA_TK / 8) {
+            v4u r[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const uint32_t key = min(k0 + vkg * 8 + j, kend - 1);
+                r[j] = *(const v4u *)(vc + ((size_t)key * n_kv + hk) * HD + vdc * 8);
+            }
+#pragma unroll
+            for (int dd = 0; dd < 8; dd++) {
+                // half dd of keys 0..7, packed in key order
+                const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
+                v4u out;
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+                    out[w] = __builtin_amdgcn_perm(r[2 * w + 1][dd >> 1], r[2 * w][dd >> 1], sel);
+                *(v4u *)&vt[(vdc * 8 + dd) * FA_PLD + vkg * 8] = out;
+            }
+        }
+        __syncthreads();
+        // scores of this wave's 16 tokens x 64 keys
+        f32x4 sc[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) sc[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+#pragma unroll
+            for (int n = 0; n < 4; n++) {
+                const f16x8 bk = *(const f16x8 *)&ks[(n * 16 + li) * KLD + kb * 32 + lg * 8];
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kb], bk, sc[n], 0, 0, 0);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[kb], bk, sc[n], 0, 0, 0);
+            }
+        }
+        // online softmax per row (lane holds rows 4*lg+e, key n*16+li)
+        float al[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float v[4], tm = -INFINITY;
+#pragma unroll
+            for (int n = 0; n < 4; n++) {
+                const uint32_t key = k0 + n * 16 + li;
+                v[n] = key <= rpos[e] ? sc[n][e] * a.scale : -INFINITY;
+                tm = fmaxf(tm, v[n]);
+            }
+            tm = fa_max16(tm);
+            const float mnew = fmaxf(mrun[e], tm);
+            float ps_sum = 0.0f;
+#pragma unroll
+            for (int n = 0; n < 4; n++) {
+                const uint32_t key = k0 + n * 16 + li;
+                const float pv = key <= rpos[e] ? expf(v[n] - mnew) : 0.0f;
+                sc[n][e] = pv;
+                ps_sum += pv;
+            }
+            ps_sum = fa_sum16(ps_sum);
+            al[e] = (mrun[e] == -INFINITY) ? 0.0f : expf(mrun[e] - mnew);
+            mrun[e] = mnew;
+            srun[e] = srun[e] * al[e] + ps_sum;
+        }
+        // P (hi, lo) into LDS rows of this wave
+#pragma unroll
+        for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t row = wave * 16 + lg * 4 + e, col = n * 16 + li;
+                const _Float16 hp = (_Float16)sc[n][e];
+                ps[0][row * FA_PLD + col] = __builtin_bit_cast(uint16_t, hp);
+                ps[1][row * FA_PLD + col] = __builtin_bit_cast(uint16_t, (_Float16)(sc[n][e] - (float)hp));
+            }
+#pragma unroll
+        for (int n = 0; n < NNT; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[n][e] *= al[e];
+        __syncthreads();
+        // O += P V
+#pragma unroll
+        for (int kb = 0; kb < FA_TK / 32; kb++) {
+            const f16x8 ph = *(const f16x8 *)&ps[0][(wave * 16 + li) * FA_PLD + kb * 32 + lg * 8];
+            const f16x8 pl = *(const f16x8 *)&ps[1][(wave * 16 + li) * FA_PLD + kb * 32 + lg * 8];
+#pragma unroll
+            for (int n = 0; n < NNT; n++) {
+                const f16x8 bv = *(const f16x8 *)&vt[(n * 16 + li) * FA_PLD + kb * 32 + lg * 8];
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bv, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, bv, o[n], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    // finish: o / s, sigmoid gate, store (lane: rows 4*lg+e, dims n*16+li)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t z = z0 + wave * 16 + lg * 4 + e;
+        if (z >= ntok) continue;
+        const float S = srun[e];
+        float *out = a.out + (size_t)z * a.out_tok + (size_t)h * HD;
+        const float *gate = a.gate ? a.gate + (size_t)z * a.q_tok + (size_t)h * a.q_stride : NULL;
+#pragma unroll
+        for (int n = 0; n < NNT; n++) {
+            const uint32_t dd = n * 16 + li;
+            float v = isnan(S) ? S : (S > 0.0f ? o[n][e] / S : 0.0f);
+            if (gate) v *= sigm(gate[dd]);
+            out[dd] = v;
+        }
+    }
+}
+
+extern "C" hipError_t sgk_attn_flash(const sgk_attn *a, hipStream_t s) {
+    if (!a->ntok || !a->n_heads) return hipSuccess;
+    if (!a->steps || !a->n_kv || a->n_heads % a->n_kv || ((uintptr_t)a->q & 15) || a->q_stride % 4 || a->q_tok % 4)
+        return hipErrorInvalidValue;
+    dim3 grid(a->n_heads, (a->ntok + FA_TQ - 1) / FA_TQ);
+    switch (a->hd) {
+    case 64: hipLaunchKernelGGL(k_attn_flash<64>, grid, dim3(TPB), 0, s, *a); break;
+    case 128: hipLaunchKernelGGL(k_attn_flash<128>, grid, dim3(TPB), 0, s, *a); break;
+    case 256: hipLaunchKernelGGL(k_attn_flash<256>, grid, dim3(TPB), 0, s, *a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 extern "C" hipError_t sgk_attn_combine(const sgk_attn *a, hipStream_t s) {
     if (!a->n_heads || !a->ntok) return hipSuccess;
     if (!a->steps && a->n_splits > 1024) return hipErrorInvalidValue;
@@ -2137,7 +2361,6 @@ extern "C" hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // X [N][ldx] f32 -> xs[0 .. N*K) bf16 hi, xs[N*K .. 2*N*K) bf16 lo = x - hi,
 // both round-to-nearest-even, rows of K (K % 4 == 0, ldx % 4 == 0, X 16-byte

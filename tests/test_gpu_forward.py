@@ -207,3 +207,28 @@ def test_split_cap_override_multi_tile_decode_vs_oracle(gpu, monkeypatch):
     gpu.state_new(64)
     assert gpu.split_cap() == 256
     syn.close()
+
+
+@pytest.mark.parametrize("chunk", [128, 100])
+def test_hd256_prefill_matches_serial(gpu, chunk):
+    """head_dim 256 (the 27B shape's attention) through the MFMA prefill
+    attention: 300 tokens in chunks of 128 (several 64-key tiles per token
+    block, a partial last block) and of 100 (token blocks that start inside a
+    key tile). Last logits and the next greedy step against the serial GPU
+    forward, within 2e-4 and with the same argmax (the reference's prefill
+    bar, tests/test_gpu_prefill.c)."""
+    syn = S.Synth(HD256, S.SG_T_Q8_0, seed=11)
+    gpu.load_model(syn.model)
+    gpu.state_new(320)
+    rng = np.random.default_rng(6)
+    prompt = rng.integers(0, HD256["vocab"], 300).tolist()
+    serial = None
+    for p, t in enumerate(prompt):
+        serial = gpu.forward(t, p)
+    nxt_serial = gpu.forward(int(np.argmax(serial)), len(prompt))
+    last = gpu.prefill(prompt, chunk=chunk)
+    assert rel(last, serial) < 2e-4
+    assert int(np.argmax(last)) == int(np.argmax(serial))
+    nxt = gpu.forward(int(np.argmax(last)), len(prompt))
+    assert rel(nxt, nxt_serial) < 2e-4
+    syn.close()
