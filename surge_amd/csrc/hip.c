@@ -71,7 +71,7 @@ typedef struct {
     bool attn;
     dmat in, out, gu, down;
     float *ln1, *ln2, *qn, *kn, *ssm_norm, *conv_w, *ssm_a, *dt_bias;
-    uint16_t *kc, *vc;    /* [max_ctx][n_kv][hd] f16 */
+    uint16_t *kc, *vc;    /* [n_kv][max_ctx][hd] f16 (head-major: a split's keys are contiguous) */
     float *ring;          /* [4][conv_dim]: last inputs, slot = position % 4 */
     float *S;             /* [n_v][dv][dk] */
 } glayer;
@@ -961,6 +961,7 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             A.gate = c->attn_output_gate ? g->act + hd : NULL; A.steps = g->d_step;
             A.n_heads = c->n_heads; A.n_kv = c->n_kv_heads; A.hd = hd; A.rope_dim = c->rope_dim; A.q_stride = qs;
             A.max_splits = g->max_splits; A.ntok = 1; A.scale = (float)(1.0 / sqrt((double)hd));
+            A.kv_ps = hd; A.kv_hs = (uint64_t)g->max_ctx * hd;
             A.fuse_prep = 1; A.qn = L->qn; A.kn = L->kn; A.cs = g->cs_table; A.eps = c->rms_eps;
             A.split_cap = g->split_cap;
             if ((e = sgk_attn_partial(&A, s)) != hipSuccess) return e;
@@ -1280,6 +1281,7 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t n) {
             A.n_heads = c->n_heads; A.n_kv = c->n_kv_heads; A.hd = hd; A.rope_dim = c->rope_dim; A.q_stride = qs;
             A.q_tok = in_rows; A.out_tok = g->attn_width; A.max_splits = SGK_PREFILL_SPLITS; A.ntok = n;
             A.scale = (float)(1.0 / sqrt((double)hd)); A.prefill = 1;
+            A.kv_ps = hd; A.kv_hs = (uint64_t)g->max_ctx * hd;
             if ((e = sgk_attn_prep(&A, L->qn, L->kn, g->cs_table, c->rms_eps, s)) != hipSuccess) return e;
             if (hd == 64 || hd == 128 || hd == 256) {
                 if ((e = sgk_attn_flash(&A, s)) != hipSuccess) return e;

@@ -105,7 +105,7 @@ hipError_t sgk_softmax(const float *x, float *out, uint32_t n, hipStream_t s);
 #define SGK_PREFILL_SPLITS 8u
 typedef struct {
     float *q;                   /* prep: the fused q|k|v GEMM rows (q normed+roped in place) */
-    uint16_t *kc, *vc;          /* f16 caches [cap][n_kv][hd] */
+    uint16_t *kc, *vc;          /* f16 caches (layout: kv_ps, kv_hs below) */
     float *m, *s, *acc;         /* partials */
     float *out;                 /* combine output [ntok][n_heads*hd] */
     const float *gate;          /* combine: q rows again (gate half), or NULL */
@@ -120,6 +120,13 @@ typedef struct {
     int fuse_prep;
     const float *qn, *kn, *cs;
     float eps;
+    /* K/V cache strides in elements: position p of kv head h starts at
+     * p*kv_ps + h*kv_hs. 0 = the reference layout [pos][n_kv][hd]
+     * (kv_ps = n_kv*hd, kv_hs = hd); the decode state is head-major
+     * [n_kv][cap][hd] (kv_ps = hd, kv_hs = cap*hd), so a split's keys are
+     * one contiguous run. */
+    uint32_t kv_ps;
+    uint64_t kv_hs;
 } sgk_attn;
 
 /* q_norm/k_norm + RoPE on each head, K and V stored f16 at each token's

@@ -889,6 +889,17 @@ __device__ __forceinline__ uint32_t dev_splits(uint32_t seq, int prefill, uint32
     return n > SGK_PREFILL_SPLITS ? SGK_PREFILL_SPLITS : n;
 }
 
+// Element offset of position pos of kv head kh in a K/V cache (the launchers
+// resolve 0 strides to the reference layout).
+__device__ __forceinline__ size_t kv_at(const sgk_attn &a, uint32_t pos, uint32_t kh) {
+    return (size_t)pos * a.kv_ps + (size_t)kh * a.kv_hs;
+}
+static inline sgk_attn kv_resolved(const sgk_attn *a) {
+    sgk_attn b = *a;
+    if (!b.kv_ps) { b.kv_ps = b.n_kv * b.hd; b.kv_hs = b.hd; }
+    return b;
+}
+
 // q_norm/k_norm + RoPE + f16 KV store. Workgroup (head, token): query heads
 // first, then kv heads.
 __global__ void __launch_bounds__(TPB) k_attn_prep(sgk_attn a, const float *qn, const float *kn,
@@ -916,7 +927,7 @@ __global__ void __launch_bounds__(TPB) k_attn_prep(sgk_attn a, const float *qn, 
     if (isq) {
         x[t] = o;
     } else {
-        const size_t at = ((size_t)pos * a.n_kv + kh) * hd + t;
+        const size_t at = kv_at(a, pos, kh) + t;
         const float *vraw = row + (size_t)a.n_heads * a.q_stride + (size_t)a.n_kv * hd + (size_t)kh * hd;
         ((uint16_t *)a.kc)[at] = f2h(o);
         ((uint16_t *)a.vc)[at] = f2h(vraw[t]);
@@ -926,7 +937,7 @@ __global__ void __launch_bounds__(TPB) k_attn_prep(sgk_attn a, const float *qn, 
 extern "C" hipError_t sgk_attn_prep(const sgk_attn *a, const float *qn, const float *kn,
                                     const float *cs_table, float eps, hipStream_t s) {
     if (a->hd > TPB || !a->ntok) return a->ntok ? hipErrorInvalidValue : hipSuccess;
-    hipLaunchKernelGGL(k_attn_prep, dim3(a->n_heads + a->n_kv, a->ntok), dim3(TPB), 0, s, *a, qn, kn,
+    hipLaunchKernelGGL(k_attn_prep, dim3(a->n_heads + a->n_kv, a->ntok), dim3(TPB), 0, s, kv_resolved(a), qn, kn,
                        cs_table, eps);
     return hipGetLastError();
 }
@@ -1059,7 +1070,7 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
     const uint32_t klast = t1 ? t1 - 1 : 0;
     auto load_k = [&](uint32_t ts) {
         const uint32_t key = min(ts + kj, klast);
-        const uint4 *p = (const uint4 *)(kc + ((size_t)key * n_kv + hk) * HD + kp * DPT);
+        const uint4 *p = (const uint4 *)(kc + kv_at(a, key, hk) + kp * DPT);
 #pragma unroll
         for (int u = 0; u < KU; u++) kr[u] = p[u];
     };
@@ -1067,7 +1078,7 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
 #pragma unroll
         for (int u = 0; u < VU; u++) {
             const uint32_t key = min(ts + kg + u * KGV, klast);
-            vr[u] = ((const uint4 *)(vc + ((size_t)key * n_kv + hk) * HD))[vcc];
+            vr[u] = ((const uint4 *)(vc + kv_at(a, key, hk)))[vcc];
         }
     };
     // 2. The position's cos|sin entry, then the first tile's K and V; all of
@@ -1107,7 +1118,7 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
             qsh[h * QROW + (d / DPT) * QP + d % DPT] = prep_elem(raw + h * HD, rn[h], qn_s, cs_s, d, a.rope_dim);
         }
         if (kv_writer) {
-            const size_t at = ((size_t)pos * n_kv + hk) * HD;
+            const size_t at = kv_at(a, pos, hk);
             for (uint32_t d = t; d < HD; d += TPB) {
                 const uint16_t kh = f2h(prep_elem(raw + KOFF, rn[G], kn_s, cs_s, d, a.rope_dim));
                 const uint16_t vh = f2h(vr0);
@@ -1280,6 +1291,281 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
     }
 }
 
+// Shared by the MFMA attention kernels (decode partial and prefill pass).
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+#define FA_TQ 64    // tokens per workgroup (4 waves x 16)
+#define FA_TK 64    // keys per tile
+#define FA_PLD (FA_TK + 8)
+
+// x[0..7] -> f16 hi and lo fragments
+__device__ __forceinline__ void fa_split8(const float *x, f16x8 &hi, f16x8 &lo) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const _Float16 h = (_Float16)x[e];
+        hi[e] = h;
+        lo[e] = (_Float16)(x[e] - (float)h);
+    }
+}
+
+// max / sum over the 16 lanes of a row group (lanes sharing lane / 16)
+__device__ __forceinline__ float fa_max16(float v) {
+    v = fmaxf(v, lane_xor1(v));
+    v = fmaxf(v, lane_xor2(v));
+    v = fmaxf(v, lane_xor<4>(v));
+    return fmaxf(v, lane_xor8(v));
+}
+__device__ __forceinline__ float fa_sum16(float v) {
+    v += lane_xor1(v);
+    v += lane_xor2(v);
+    v += lane_xor<4>(v);
+    return v + lane_xor8(v);
+}
+
+// ---------------------------------------------------------------------------
+// Decode split-K partial on MFMA (head_dim 128 or 256, fused prep): the same
+// workgroup (split, kv head), prep, position store and output partials as
+// k_attn_partial, with each 64-key tile on v_mfma_f32_16x16x32_f16:
+//  - scores: A = the group's q rows (heads in rows 0..G-1 of a 16-row tile,
+//    split into f16 hi + lo), B = the tile's K straight from the f16 cache
+//    (wave w takes keys 16w..16w+15: lane holds 8 dims of one key per 32);
+//  - softmax per head over the tile as in k_attn_partial (scores and p in LDS);
+//  - P V: A = p (f16 hi + lo), B = V^T staged in LDS (each thread transposes 8
+//    keys x 8 dims in registers); wave w owns a quarter of the head dims, so
+//    each wave writes its own slice of the partial and no fold is needed.
+// ---------------------------------------------------------------------------
+
+#define MK 64       // keys per tile
+
+template <int HD>
+__device__ __forceinline__ void mf_load_k(v4u (&kr)[HD / 32], const uint16_t *kh, uint32_t key, uint32_t ps,
+                                          uint32_t lg) {
+    const v4u *p = (const v4u *)(kh + (size_t)key * ps + lg * 8);
+#pragma unroll
+    for (int kb = 0; kb < HD / 32; kb++) kr[kb] = p[kb * 4];
+}
+template <int HD>
+__device__ __forceinline__ void mf_load_v(v4u (&vr)[8], const uint16_t *vh, uint32_t key0, uint32_t klast,
+                                          uint32_t ps, uint32_t vdc) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t key = min(key0 + j, klast);
+        vr[j] = *(const v4u *)(vh + (size_t)key * ps + vdc * 8);
+    }
+}
+// 8 keys x 8 dims (vr[j] = key j's dims) -> rows dims 0..7 of V^T, keys in order
+__device__ __forceinline__ void mf_store_vt(const v4u (&vr)[8], uint16_t *vt, uint32_t vdc, uint32_t vkg) {
+#pragma unroll
+    for (int dd = 0; dd < 8; dd++) {
+        const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
+        v4u out;
+#pragma unroll
+        for (int w = 0; w < 4; w++) out[w] = __builtin_amdgcn_perm(vr[2 * w + 1][dd >> 1], vr[2 * w][dd >> 1], sel);
+        *(v4u *)&vt[(vdc * 8 + dd) * FA_PLD + vkg * 8] = out;
+    }
+}
+
+template <int HD>
+__global__ void __launch_bounds__(TPB) k_attn_partial_mf(sgk_attn a) {
+    static_assert(HD == 128 || HD == 256, "MFMA decode partial takes head_dim 128 or 256");
+    constexpr int NKB = HD / 32, NTW = HD / 64;       // score k-blocks; output 16-dim tiles per wave
+    constexpr int VDC = HD / 8;                       // V staging: 8-dim chunks (threads t < 8*VDC)
+    constexpr int QPT = (GMAX * HD + TPB - 1) / TPB, KOFF = QPT * TPB;
+    __shared__ __align__(16) float qsh[GMAX * HD];
+    __shared__ __align__(16) float raw[KOFF + HD];    // raw q rows, then the raw k row
+    __shared__ __align__(16) float sc[GMAX][MK];
+    __shared__ float mrun[GMAX], srun[GMAX], alpha[GMAX], rn[GMAX + 1];
+    __shared__ __align__(16) uint16_t vt[HD * FA_PLD];
+    __shared__ float cs_s[HD], qn_s[HD], kn_s[HD];
+    __shared__ __align__(16) uint16_t knew[HD], vnew[HD];
+
+    const uint32_t G = a.n_heads / a.n_kv, n_kv = a.n_kv, z = blockIdx.z;
+    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t li = lane & 15, lg = lane >> 4, h0 = hk * G;
+    const float *q = a.q + (size_t)z * a.q_tok;
+
+    // 1. position-independent loads first (as in k_attn_partial)
+    float qv[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const uint32_t e = min(t + k * TPB, G * HD - 1);
+        qv[k] = q[(size_t)(h0 + e / HD) * a.q_stride + e % HD];
+    }
+    const uint32_t td = min(t, (uint32_t)HD - 1);
+    const float *krow = q + (size_t)a.n_heads * a.q_stride + (size_t)hk * HD;
+    const float *vrow = krow + (size_t)n_kv * HD;
+    const float qn0 = a.qn[td], kn0 = a.kn[td], kr0 = krow[td], vr0 = vrow[td];
+
+    const uint32_t pos = a.steps[z].pos, seq = pos + 1;
+    const uint32_t ns = dev_splits(seq, a.prefill, a.split_cap);
+    if (i >= ns) return;
+    const uint32_t t0 = (uint32_t)((uint64_t)i * seq / ns), t1 = (uint32_t)((uint64_t)(i + 1) * seq / ns);
+    const uint32_t klast = t1 ? t1 - 1 : 0;
+    const size_t zoff = (size_t)z * a.n_heads * a.max_splits;
+    const uint32_t vkg = t / VDC, vdc = t % VDC;      // V staging role: keys 8*vkg.., dims 8*vdc..
+    const bool vst = vkg < MK / 8;
+
+    // 2. the position's cos|sin entry, then the first tile's K and V
+    const float cs0 = (a.cs + (size_t)pos * a.rope_dim)[min(td, a.rope_dim - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    v4u kr[NKB], vr[8];
+    const uint16_t *kch = a.kc + (size_t)hk * a.kv_hs, *vch = a.vc + (size_t)hk * a.kv_hs;
+    mf_load_k<HD>(kr, kch, min(t0 + wave * 16 + li, klast), a.kv_ps, lg);
+    mf_load_v<HD>(vr, vch, t0 + (vst ? vkg : 0) * 8, klast, a.kv_ps, vdc);
+
+    // 3. prep: q_norm + RoPE of the group's heads into qsh; the split holding
+    //    the position stores that token's K (k_norm + RoPE) and raw V as f16
+    const bool kv_writer = i == ns - 1;
+#pragma unroll
+    for (int k = 0; k < QPT; k++) raw[t + k * TPB] = qv[k];
+    qn_s[td] = qn0;
+    raw[KOFF + td] = kr0;
+    kn_s[td] = kn0;
+    __syncthreads();
+    cs_s[td] = td < a.rope_dim ? cs0 : 0.0f;
+    for (uint32_t h = wave; h <= G; h += TPB / 64) {
+        if (h == G && !kv_writer) break;
+        const float *x = h < G ? raw + h * HD : raw + KOFF;
+        float ss = 0.0f;
+        for (uint32_t d = lane; d < HD; d += 64) ss = fmaf(x[d], x[d], ss);
+        ss = wave_sum(ss);
+        if (lane == 0) rn[h] = 1.0f / sqrtf(ss / (float)HD + a.eps);
+    }
+    __syncthreads();
+    for (uint32_t e = t; e < G * HD; e += TPB) {
+        const uint32_t h = e / HD, d = e % HD;
+        qsh[e] = prep_elem(raw + h * HD, rn[h], qn_s, cs_s, d, a.rope_dim);
+    }
+    if (kv_writer) {
+        const size_t at = kv_at(a, pos, hk);
+        for (uint32_t d = t; d < HD; d += TPB) {
+            const uint16_t kh = f2h(prep_elem(raw + KOFF, rn[G], kn_s, cs_s, d, a.rope_dim));
+            const uint16_t vh = f2h(vr0);
+            ((uint16_t *)a.kc)[at + d] = kh;
+            ((uint16_t *)a.vc)[at + d] = vh;
+            knew[d] = kh;
+            vnew[d] = vh;
+        }
+    }
+    if (t < G) { mrun[t] = -INFINITY; srun[t] = 0.0f; }
+    __syncthreads();
+    // the first tile was requested before the store: take the position's row from LDS
+    if (kv_writer && pos - t0 < (uint32_t)MK) {
+        if (t0 + wave * 16 + li == pos) {
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++) kr[kb] = ((const v4u *)(knew + lg * 8))[kb * 4];
+        }
+        if (vst) {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (t0 + vkg * 8 + j == pos) vr[j] = *(const v4u *)(vnew + vdc * 8);
+        }
+    }
+    // q fragments: row li = head li (zero past the group), dims 8*lg.. of each 32
+    f16x8 qh[NKB], ql[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+        float xv[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) xv[e] = li < G ? qsh[li * HD + kb * 32 + lg * 8 + e] : 0.0f;
+        fa_split8(xv, qh[kb], ql[kb]);
+    }
+    f32x4 o[NTW];
+#pragma unroll
+    for (int n = 0; n < NTW; n++) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    for (uint32_t ts = t0; ts < t1; ts += MK) {
+        const uint32_t nk = min((uint32_t)MK, t1 - ts);
+        if (vst) mf_store_vt(vr, vt, vdc, vkg);
+        // scores of keys 16*wave + li for the 16 rows (heads)
+        f32x4 s4 = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const f16x8 bk = __builtin_bit_cast(f16x8, kr[kb]);
+            s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kb], bk, s4, 0, 0, 0);
+            s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[kb], bk, s4, 0, 0, 0);
+        }
+        // the next tile (past the split: clamped, unused); vr was staged above
+        mf_load_k<HD>(kr, kch, min(ts + MK + wave * 16 + li, klast), a.kv_ps, lg);
+        mf_load_v<HD>(vr, vch, ts + MK + (vst ? vkg : 0) * 8, klast, a.kv_ps, vdc);
+        {
+            const uint32_t key = wave * 16 + li;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t h = lg * 4 + e;
+                if (h < G) sc[h][key] = key < nk ? s4[e] * a.scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // softmax: one wave per head over the tile (k_attn_partial's rules)
+        for (uint32_t h = wave; h < G; h += TPB / 64) {
+            const float v = sc[h][lane];
+            const float tm = wave_max(v);
+            const float mold = mrun[h];
+            const float mnew = fmaxf(mold, tm);
+            const float p = lane < nk ? expf(v - mnew) : 0.0f;
+            sc[h][lane] = p;
+            const float ps = wave_sum(p);
+            if (lane == 0) {
+                const float al = (mold == -INFINITY) ? 0.0f : expf(mold - mnew);
+                alpha[h] = al;
+                mrun[h] = mnew;
+                srun[h] = srun[h] * al + ps;
+            }
+        }
+        __syncthreads();
+        // p fragments: row li = head, keys 8*lg.. of each 32
+        f16x8 ph[2], pl[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+            float xv[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) xv[e] = li < G ? sc[li][kb * 32 + lg * 8 + e] : 0.0f;
+            fa_split8(xv, ph[kb], pl[kb]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t h = lg * 4 + e;
+            const float al = h < G ? alpha[h] : 0.0f;
+#pragma unroll
+            for (int n = 0; n < NTW; n++) o[n][e] *= al;
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int n = 0; n < NTW; n++) {
+                const uint32_t dim = (wave * NTW + n) * 16 + li;
+                const f16x8 bv = *(const f16x8 *)&vt[dim * FA_PLD + kb * 32 + lg * 8];
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[kb], bv, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[kb], bv, o[n], 0, 0, 0);
+            }
+        __syncthreads();
+    }
+    // partials: lane holds heads 4*lg+e, dims (wave*NTW + n)*16 + li
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t h = lg * 4 + e;
+        if (h >= G) continue;
+        float *dst = a.acc + (zoff + (size_t)(h0 + h) * ns + i) * HD;
+#pragma unroll
+        for (int n = 0; n < NTW; n++) dst[(wave * NTW + n) * 16 + li] = o[n][e];
+    }
+    if (t < G) {
+        const size_t oi = zoff + (size_t)(h0 + t) * ns + i;
+        a.m[oi] = mrun[t];
+        a.s[oi] = srun[t];
+    }
+}
+
+// SURGE_ATTN_VALU=1 keeps the decode partial on the VALU kernel (for A/B
+// measurement); the MFMA partial is the default for head_dim 128 and 256.
+static bool getenv_mf() {
+    static int v = -1;
+    if (v < 0) { const char *e = getenv("SURGE_ATTN_VALU"); v = (e && e[0] == '1') ? 0 : 1; }
+    return v == 1;
+}
+
 extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
     if (!a->n_kv || a->n_heads % a->n_kv || a->n_heads / a->n_kv > GMAX) return hipErrorInvalidValue;
     if (a->fuse_prep && (!a->steps || a->ntok != 1 || !a->qn || !a->kn || !a->cs || a->rope_dim > a->hd))
@@ -1287,7 +1573,12 @@ extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
     const uint32_t gx = a->steps ? a->max_splits : a->n_splits;
     if (!gx || !a->ntok) return hipSuccess;
     dim3 grid(gx, a->n_kv, a->ntok);
-#define HDCASE(H) case H: hipLaunchKernelGGL((k_attn_partial<H, 64>), grid, dim3(TPB), 0, s, *a); break
+    if (a->fuse_prep && (a->hd == 128 || a->hd == 256) && getenv_mf()) {
+        if (a->hd == 256) hipLaunchKernelGGL(k_attn_partial_mf<256>, grid, dim3(TPB), 0, s, kv_resolved(a));
+        else hipLaunchKernelGGL(k_attn_partial_mf<128>, grid, dim3(TPB), 0, s, kv_resolved(a));
+        return hipGetLastError();
+    }
+#define HDCASE(H) case H: hipLaunchKernelGGL((k_attn_partial<H, 64>), grid, dim3(TPB), 0, s, kv_resolved(a)); break
     switch (a->hd) {
         HDCASE(16); HDCASE(32); HDCASE(64); HDCASE(128); HDCASE(256);
     default: return hipErrorInvalidValue;
@@ -1396,37 +1687,6 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
 // MFMA 16x16x32 layout as in the prefill GEMM.
 // ---------------------------------------------------------------------------
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-#define FA_TQ 64    // tokens per workgroup (4 waves x 16)
-#define FA_TK 64    // keys per tile
-#define FA_PLD (FA_TK + 8)
-
-// x[0..7] -> f16 hi and lo fragments
-__device__ __forceinline__ void fa_split8(const float *x, f16x8 &hi, f16x8 &lo) {
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const _Float16 h = (_Float16)x[e];
-        hi[e] = h;
-        lo[e] = (_Float16)(x[e] - (float)h);
-    }
-}
-
-// max / sum over the 16 lanes of a row group (lanes sharing lane / 16)
-__device__ __forceinline__ float fa_max16(float v) {
-    v = fmaxf(v, lane_xor1(v));
-    v = fmaxf(v, lane_xor2(v));
-    v = fmaxf(v, lane_xor<4>(v));
-    return fmaxf(v, lane_xor8(v));
-}
-__device__ __forceinline__ float fa_sum16(float v) {
-    v += lane_xor1(v);
-    v += lane_xor2(v);
-    v += lane_xor<4>(v);
-    return v + lane_xor8(v);
-}
-
 template <int HD>
 __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
     static_assert(HD % 64 == 0 && HD <= 256, "flash prefill takes head_dim 64, 128, 192 or 256");
@@ -1474,7 +1734,7 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
         // stage K [key][dim] and V^T [dim][key] (keys clamped into the range)
         {
             const uint32_t key = min(k0 + kk, kend - 1);
-            const v4u *src = (const v4u *)(kc + ((size_t)key * n_kv + hk) * HD + kd);
+            const v4u *src = (const v4u *)(kc + kv_at(a, key, hk) + kd);
             v4u r[KDT / 8];
 #pragma unroll
             for (int u = 0; u < KDT / 8; u++) r[u] = src[u];
@@ -1486,7 +1746,7 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const uint32_t key = min(k0 + vkg * 8 + j, kend - 1);
-                r[j] = *(const v4u *)(vc + ((size_t)key * n_kv + hk) * HD + vdc * 8);
+                r[j] = *(const v4u *)(vc + kv_at(a, key, hk) + vdc * 8);
             }
 #pragma unroll
             for (int dd = 0; dd < 8; dd++) {
@@ -1592,9 +1852,9 @@ extern "C" hipError_t sgk_attn_flash(const sgk_attn *a, hipStream_t s) {
         return hipErrorInvalidValue;
     dim3 grid(a->n_heads, (a->ntok + FA_TQ - 1) / FA_TQ);
     switch (a->hd) {
-    case 64: hipLaunchKernelGGL(k_attn_flash<64>, grid, dim3(TPB), 0, s, *a); break;
-    case 128: hipLaunchKernelGGL(k_attn_flash<128>, grid, dim3(TPB), 0, s, *a); break;
-    case 256: hipLaunchKernelGGL(k_attn_flash<256>, grid, dim3(TPB), 0, s, *a); break;
+    case 64: hipLaunchKernelGGL(k_attn_flash<64>, grid, dim3(TPB), 0, s, kv_resolved(a)); break;
+    case 128: hipLaunchKernelGGL(k_attn_flash<128>, grid, dim3(TPB), 0, s, kv_resolved(a)); break;
+    case 256: hipLaunchKernelGGL(k_attn_flash<256>, grid, dim3(TPB), 0, s, kv_resolved(a)); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
