@@ -2369,14 +2369,72 @@ __global__ void __launch_bounds__(TPB) k_qk_norm_chunk(float *conv_out, uint32_t
 }
 
 // Delta-rule scan: workgroup (value head, 16-row block) keeps its rows of S in
-// registers for the whole chunk, reads each token's q, k, v and gates, and
-// writes each token's readout y.
+// registers for the whole chunk and walks the tokens in order, writing each
+// token's readout y (the decode step's arithmetic, delta_update, per row).
+// The tokens' inputs are staged in LDS in blocks of DCT tokens (k | q of the
+// key head, the block's 16 v values, beta and decay), double-buffered: the
+// next block's global loads are in flight while the current block is walked,
+// so a token step reads only LDS.
+template <int DK>
+struct dcg {
+    static constexpr int DCT = DK > 128 ? 16 : 32;        // tokens per staged block
+    static constexpr int TPT = TPB / DCT;                 // threads per token (k|q)
+    static constexpr int NV4 = 2 * DK / TPT / 4;          // k|q float4s per thread
+};
+
+template <int DK>
+__device__ __forceinline__ void dc_load(f32x4 (&r)[dcg<DK>::NV4 + 1], const sgk_gdn &a, const float *conv_out,
+                                        uint32_t z0, uint32_t ntok, uint32_t hk, uint32_t h, uint32_t j0) {
+    using C = dcg<DK>;
+    const uint32_t t = threadIdx.x, zt = t / C::TPT, part = t % C::TPT, key_dim = a.n_k * DK;
+    const float *cz = conv_out + (size_t)min(z0 + zt, ntok - 1) * a.conv_dim;
+#pragma unroll
+    for (int u = 0; u < C::NV4; u++) {
+        const uint32_t e = (part * C::NV4 + u) * 4;          // 0 .. 2*DK-1: k, then q
+        const float *src = e < DK ? cz + key_dim + (size_t)hk * DK + e : cz + (size_t)hk * DK + (e - DK);
+        r[u] = *(const f32x4 *)src;
+    }
+    // v: token t/4, rows j0 + 4*(t%4) .. +3
+    const uint32_t vz = t >> 2, vr = j0 + (t & 3) * 4;
+    const float *vp = conv_out + (size_t)min(z0 + vz, ntok - 1) * a.conv_dim + 2 * key_dim + (size_t)h * a.dv + vr;
+    r[C::NV4] = (vz < (uint32_t)C::DCT && vr < a.dv) ? *(const f32x4 *)vp : (f32x4){0.f, 0.f, 0.f, 0.f};
+}
+
+template <int DK>
+__device__ __forceinline__ void dc_store(const f32x4 (&r)[dcg<DK>::NV4 + 1], float *kq, float *vs, float *gs,
+                                         const sgk_gdn &a, const float *gates, uint32_t in_stride, uint32_t z0,
+                                         uint32_t ntok, uint32_t h) {
+    using C = dcg<DK>;
+    const uint32_t t = threadIdx.x, zt = t / C::TPT, part = t % C::TPT;
+#pragma unroll
+    for (int u = 0; u < C::NV4; u++) *(f32x4 *)&kq[zt * 2 * DK + (part * C::NV4 + u) * 4] = r[u];
+    const uint32_t vz = t >> 2;
+    if (vz < (uint32_t)C::DCT) *(f32x4 *)&vs[vz * GDN_ROWS + (t & 3) * 4] = r[C::NV4];
+    if (t < (uint32_t)C::DCT) {
+        const uint32_t z = min(z0 + t, ntok - 1), cd = a.conv_dim, vd = a.n_v * a.dv;
+        float beta, decay;
+        if (gates) {
+            beta = gates[(size_t)z * 2 * a.n_v + h];
+            decay = gates[(size_t)z * 2 * a.n_v + a.n_v + h];
+        } else {
+            const float *iz = a.in + (size_t)z * in_stride;
+            gdn_gates(iz[cd + vd + h], iz[cd + vd + a.n_v + h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
+        }
+        gs[2 * t] = beta;
+        gs[2 * t + 1] = decay;
+    }
+}
+
 template <int DK>
 __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *conv_out, uint32_t in_stride,
                                                      uint32_t ntok, const float *gates) {
+    using C = dcg<DK>;
     constexpr int EPL = drow<DK>::EPL, RPW = GDN_ROWS / (TPB / 64);
+    __shared__ __align__(16) float kq[2][C::DCT * 2 * DK];
+    __shared__ __align__(16) float vs[2][C::DCT * GDN_ROWS];
+    __shared__ float gs[2][2 * C::DCT];
     const uint32_t h = blockIdx.x, j0 = blockIdx.y * GDN_ROWS, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t dv = a.dv, key_dim = a.n_k * DK, cd = a.conv_dim, vd = a.n_v * dv;
+    const uint32_t dv = a.dv, vd = a.n_v * dv;
     const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k);
     float *Sh = a.S + (size_t)h * dv * DK;
     float sr[RPW][EPL];
@@ -2385,25 +2443,28 @@ __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *con
         const uint32_t j = j0 + wave + u * (TPB / 64);
         if (j < dv) row_load<DK>(sr[u], Sh + (size_t)j * DK, lane);
     }
-    for (uint32_t z = 0; z < ntok; z++) {
-        const float *cz = conv_out + (size_t)z * cd;
-        const float *iz = a.in + (size_t)z * in_stride;
-        float beta, decay;
-        if (gates) {
-            beta = gates[(size_t)z * 2 * a.n_v + h];
-            decay = gates[(size_t)z * 2 * a.n_v + a.n_v + h];
-        } else {
-            gdn_gates(iz[cd + vd + h], iz[cd + vd + a.n_v + h], a.ssm_a[h], a.dt_bias[h], a.neg_exp, &beta, &decay);
-        }
+    f32x4 r[C::NV4 + 1];
+    dc_load<DK>(r, a, conv_out, 0, ntok, hk, h, j0);
+    dc_store<DK>(r, kq[0], vs[0], gs[0], a, gates, in_stride, 0, ntok, h);
+    __syncthreads();
+    for (uint32_t z0 = 0; z0 < ntok; z0 += C::DCT) {
+        const uint32_t buf = (z0 / C::DCT) & 1;
+        dc_load<DK>(r, a, conv_out, z0 + C::DCT, ntok, hk, h, j0);    // past the end: clamped, unused
+        const uint32_t zn = min((uint32_t)C::DCT, ntok - z0);
+        for (uint32_t zz = 0; zz < zn; zz++) {
+            const float beta = gs[buf][2 * zz], decay = gs[buf][2 * zz + 1];
+            const float *kz = &kq[buf][zz * 2 * DK];
 #pragma unroll
-        for (int u = 0; u < RPW; u++) {
-            const uint32_t j = j0 + wave + u * (TPB / 64);
-            if (j < dv) {
-                const float y = delta_update<DK>(sr[u], cz + key_dim + (size_t)hk * DK, cz + (size_t)hk * DK,
-                                                 cz[2 * key_dim + (size_t)h * dv + j], beta, decay, lane);
-                if (lane == 0) a.y[(size_t)z * vd + (size_t)h * dv + j] = y;
+            for (int u = 0; u < RPW; u++) {
+                const uint32_t jr = wave + u * (TPB / 64), j = j0 + jr;
+                if (j < dv) {
+                    const float y = delta_update<DK>(sr[u], kz, kz + DK, vs[buf][zz * GDN_ROWS + jr], beta, decay, lane);
+                    if (lane == 0) a.y[(size_t)(z0 + zz) * vd + (size_t)h * dv + j] = y;
+                }
             }
         }
+        dc_store<DK>(r, kq[buf ^ 1], vs[buf ^ 1], gs[buf ^ 1], a, gates, in_stride, z0 + C::DCT, ntok, h);
+        __syncthreads();
     }
 #pragma unroll
     for (int u = 0; u < RPW; u++) {
