@@ -2370,7 +2370,8 @@ __global__ void __launch_bounds__(TPB) k_qk_norm_chunk(float *conv_out, uint32_t
 
 // Delta-rule scan: workgroup (value head, 16-row block) keeps its rows of S in
 // registers for the whole chunk and walks the tokens in order, writing each
-// token's readout y (the decode step's arithmetic, delta_update, per row).
+// token's readout y (the decode step's arithmetic; a wave's rows are reduced
+// together as in k_gdn_step).
 // The tokens' inputs are staged in LDS in blocks of DCT tokens (k | q of the
 // key head, the block's 16 v values, beta and decay), double-buffered: the
 // next block's global loads are in flight while the current block is walked,
@@ -2437,10 +2438,13 @@ __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *con
     const uint32_t dv = a.dv, vd = a.n_v * dv;
     const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k);
     float *Sh = a.S + (size_t)h * dv * DK;
+    const bool on = DK >= 64 || lane < (uint32_t)DK;
     float sr[RPW][EPL];
 #pragma unroll
     for (int u = 0; u < RPW; u++) {
         const uint32_t j = j0 + wave + u * (TPB / 64);
+#pragma unroll
+        for (int e = 0; e < EPL; e++) sr[u][e] = 0.0f;
         if (j < dv) row_load<DK>(sr[u], Sh + (size_t)j * DK, lane);
     }
     f32x4 r[C::NV4 + 1];
@@ -2452,16 +2456,36 @@ __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *con
         dc_load<DK>(r, a, conv_out, z0 + C::DCT, ntok, hk, h, j0);    // past the end: clamped, unused
         const uint32_t zn = min((uint32_t)C::DCT, ntok - z0);
         for (uint32_t zz = 0; zz < zn; zz++) {
+            // delta_update for the wave's RPW rows at once: both dot products
+            // of all rows reduced together (rows_sum), the deltas broadcast
             const float beta = gs[buf][2 * zz], decay = gs[buf][2 * zz + 1];
             const float *kz = &kq[buf][zz * 2 * DK];
+            float k[EPL], q[EPL], part[RPW];
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                k[e] = on ? kz[lane * EPL + e] : 0.0f;
+                q[e] = on ? kz[DK + lane * EPL + e] : 0.0f;
+            }
 #pragma unroll
             for (int u = 0; u < RPW; u++) {
-                const uint32_t jr = wave + u * (TPB / 64), j = j0 + jr;
-                if (j < dv) {
-                    const float y = delta_update<DK>(sr[u], kz, kz + DK, vs[buf][zz * GDN_ROWS + jr], beta, decay, lane);
-                    if (lane == 0) a.y[(size_t)(z0 + zz) * vd + (size_t)h * dv + j] = y;
-                }
+                float kv = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) { sr[u][e] *= decay; kv = fmaf(sr[u][e], k[e], kv); }
+                part[u] = kv;
             }
+            const uint32_t myrow = rows_row<RPW>(lane), jr = wave + myrow * (TPB / 64);
+            const float kvr = rows_sum<RPW>(part, lane);
+            const float dmine = (vs[buf][zz * GDN_ROWS + jr] - kvr) * beta;
+#pragma unroll
+            for (int u = 0; u < RPW; u++) {
+                const float dr = lane_read(dmine, rows_lane<RPW>(u));
+                float y = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) { sr[u][e] = fmaf(k[e], dr, sr[u][e]); y = fmaf(sr[u][e], q[e], y); }
+                part[u] = y;
+            }
+            const float yr = rows_sum<RPW>(part, lane);
+            if ((lane & (64 / RPW - 1)) == 0 && j0 + jr < dv) a.y[(size_t)(z0 + zz) * vd + (size_t)h * dv + j0 + jr] = yr;
         }
         dc_store<DK>(r, kq[buf ^ 1], vs[buf ^ 1], gs[buf ^ 1], a, gates, in_stride, z0 + C::DCT, ntok, h);
         __syncthreads();
