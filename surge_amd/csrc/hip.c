@@ -116,6 +116,7 @@ struct sg_gpu {
     sgk_step *pf_steps, *pf_hsteps;
     float *pf_X, *pf_Xn, *pf_IN, *pf_CONV, *pf_Y, *pf_G, *pf_CTX, *pf_FF, *pf_m, *pf_s, *pf_acc;
     uint16_t *pf_XS;        /* the prefill GEMMs' X split into bf16 hi | lo */
+    float *pf_PART;         /* split-K partials of the narrow prefill GEMMs: 4 x chunk x hidden */
 
     /* one-shot scratch */
     void *tmp;
@@ -469,12 +470,14 @@ sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
         if (sg_failed(e = push(ins, 3))) return e;
         void *t;
         const uint64_t qb = ((uint64_t)M * K + 255) / 256 * 256, db = ((uint64_t)M * (K / 32) * 2 + 255) / 256 * 256;
-        if (sg_failed(e = scratch(g, qb + db + (uint64_t)N * K * 4, &t))) return e;
+        const uint64_t xb = ((uint64_t)N * K * 4 + 255) / 256 * 256, pc = (uint64_t)4 * N * M;   /* split-K partials */
+        if (sg_failed(e = scratch(g, qb + db + xb + pc * 4, &t))) return e;
         int8_t *qs = t;
         uint16_t *d = (uint16_t *)((char *)t + qb);
         uint16_t *xs = (uint16_t *)((char *)t + qb + db);
+        float *part = (float *)((char *)t + qb + db + xb);
         hipError_t he = sgk_repack_q8(DEV(b), M, K, qs, d, 0, 1, s);
-        if (he == hipSuccess) he = sgk_gemm_q8(DEV(a), qs, d, DEV(out), N, M, K, xs, s);
+        if (he == hipSuccess) he = sgk_gemm_q8(DEV(a), qs, d, DEV(out), N, M, K, xs, part, pc, s);
         return finish(g, he, outs, 1);
     }
     return errf("gpu: unknown kernel '%s'", kernel);
@@ -915,7 +918,7 @@ static void state_free(sg_gpu *g) {
         void **pb[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
                         (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
                         (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc,
-                        (void **)&g->pf_XS };
+                        (void **)&g->pf_XS, (void **)&g->pf_PART };
         for (size_t i = 0; i < sizeof pb / sizeof *pb; i++) { dfree(g, *pb[i]); *pb[i] = NULL; }
         g->pf_chunk = 0;
     }
@@ -1231,7 +1234,7 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     void **bufs[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
                       (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
                       (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc,
-                      (void **)&g->pf_XS };
+                      (void **)&g->pf_XS, (void **)&g->pf_PART };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) { dfree(g, *bufs[i]); *bufs[i] = NULL; }
     if (g->pf_hsteps) { hipHostFree(g->pf_hsteps); g->pf_hsteps = NULL; }
     g->pf_chunk = 0;
@@ -1246,7 +1249,7 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     uint64_t sizes[] = { n * sizeof(sgk_step), n * c->hidden * 4, n * c->hidden * 4, n * in_rows * 4,
                          n * g->conv_dim * 4 + 4, n * g->value_dim * 4 + 4, n * g->value_dim * 4 + 4,
                          n * g->attn_width * 4 + 4, n * c->ffn_hidden * 4, ah * 4, ah * 4, ah * c->head_dim * 4,
-                         n * kmax * 4 };
+                         n * kmax * 4, 4 * n * c->hidden * 4 };
     sg_err e = SG_OK;
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs && !sg_failed(e); i++) e = dzalloc(g, sizes[i], bufs[i]);
     if (!sg_failed(e) && hipHostMalloc((void **)&g->pf_hsteps, n * sizeof(sgk_step), 0) != hipSuccess)
@@ -1258,7 +1261,8 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
 
 static hipError_t gemm_rows(sg_gpu *g, const dmat *M, const float *X, uint32_t ldx, float *Y, uint32_t ldy,
                             uint32_t n, int epi) {
-    sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi, g->pf_XS };
+    sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi, g->pf_XS, g->pf_PART,
+                        (uint64_t)4 * g->pf_chunk * g->cfg.hidden };
     return sgk_gemm(&a, g->stream);
 }
 

@@ -239,11 +239,14 @@ typedef struct {
     uint32_t N, M, K, ldx, ldy;
     int epi;                 /* SGK_EPI_*: store, += (residual), SwiGLU on (gate, up) column pairs */
     uint16_t *xs;            /* Q8 W: scratch of 2*N*K bf16 (X split into hi | lo), 16-byte aligned */
+    float *part;             /* optional split-K partials (NULL: never split) */
+    uint64_t part_cap;       /* floats in part */
 } sgk_gemm_args;
 /* Q8 W needs K % 32 == 0, ldx % 4 == 0 and X 16-byte aligned. */
 hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s);
 hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, float *Y,
-                       uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, hipStream_t s);
+                       uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, float *part,
+                       uint64_t part_cap, hipStream_t s);
 
 #ifdef __cplusplus
 }

@@ -2753,21 +2753,22 @@ __device__ __forceinline__ void gm_dequant16(v4u q, uint32_t dbits, uint16_t *h,
 // One K step (Q8_0 block s) of the prefill GEMM on LDS buffer cb: request the
 // next block's X and, into the register set this step frees, the raw weights
 // of block s+2; the MFMAs; then stage block s+1 (X from xr, W dequantised from
-// the other register set wn) into buffer cb^1. Blocks past the end only
-// request (clamped) and stage; their MFMAs are skipped.
+// the other register set wn) into buffer cb^1. Blocks at or past kend (the
+// end of this workgroup's K range) only request (clamped) and stage; their
+// MFMAs are skipped.
 __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &wself, uint32_t &dself,
                                         const v4u &wnext, const uint32_t &dnext,
                                         uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wt)[2][2][GM_TM * GM_LD],
                                         uint32_t cb, const v4u *xhr, const v4u *xlr, const v4u *wrow,
-                                        const uint16_t *drow, uint32_t s, uint32_t nblk, uint32_t so,
+                                        const uint16_t *drow, uint32_t s, uint32_t kend, uint32_t so,
                                         uint32_t wn, uint32_t wm, uint32_t li, uint32_t lg) {
-    const uint32_t s1 = min(s + 1, nblk - 1), s2 = min(s + 2, nblk - 1);
+    const uint32_t s1 = min(s + 1, kend - 1), s2 = min(s + 2, kend - 1);
 #pragma unroll
     for (int u = 0; u < 2; u++) { xr[u] = xhr[s1 * 4 + u]; xr[2 + u] = xlr[s1 * 4 + u]; }
     __builtin_amdgcn_sched_barrier(0);
     wself = wrow[s2 * 2];
     dself = drow[s2];
-    if (s < nblk) {
+    if (s < kend) {
         bf16x8 bh[4], bl[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -2796,10 +2797,13 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
     __syncthreads();
 }
 
+// Split-K: workgroup row blockIdx.y of gridDim.y takes the Q8_0 blocks
+// [nblk*y/Y, nblk*(y+1)/Y) and writes at Y + y*ysplit (k_splitk_reduce sums
+// the partials in order); one split is the whole K.
 template <int EPI>
 __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, uint32_t N, uint32_t M,
-               uint32_t K, uint32_t ldy) {
+               uint32_t K, uint32_t ldy, uint64_t ysplit) {
     __shared__ __align__(16) uint16_t xt[2][2][GM_TN * GM_LD];     // [buffer][hi | lo][token][k]
     __shared__ __align__(16) uint16_t wt[2][2][GM_TM * GM_LD];     // [buffer][hi | lo][row][k]
     const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
@@ -2811,6 +2815,9 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     const uint32_t wn = wave & 1, wm = wave >> 1;
     const uint32_t li = lane & 15, lg = lane >> 4;
     const uint32_t nblk = K >> 5;
+    const uint32_t kb0 = (uint32_t)((uint64_t)nblk * blockIdx.y / gridDim.y);
+    const uint32_t kb1 = (uint32_t)((uint64_t)nblk * (blockIdx.y + 1) / gridDim.y);
+    Y += (size_t)blockIdx.y * ysplit;
     // staging role: row t/2 of both tiles, k 16*(t%2) .. +15 of each block
     const uint32_t sr = t >> 1, sk = (t & 1) * 16, so = sr * GM_LD + sk;
     const size_t xrow = (size_t)min(n0 + sr, N - 1) * K + sk;
@@ -2826,14 +2833,14 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
         for (int c = 0; c < 4; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
     v4u xr[4], wA, wB;
     uint32_t dA, dB;
-    // prologue: block 0 staged into buffer 0, block 1's raw weights in B
+    // prologue: block kb0 staged into buffer 0, block kb0+1's raw weights in B
 #pragma unroll
-    for (int u = 0; u < 2; u++) { xr[u] = xhr[u]; xr[2 + u] = xlr[u]; }
+    for (int u = 0; u < 2; u++) { xr[u] = xhr[kb0 * 4 + u]; xr[2 + u] = xlr[kb0 * 4 + u]; }
     __builtin_amdgcn_sched_barrier(0);
-    wA = wrow[0];
-    dA = drow[0];
-    wB = wrow[min(1u, nblk - 1) * 2];
-    dB = drow[min(1u, nblk - 1)];
+    wA = wrow[kb0 * 2];
+    dA = drow[kb0];
+    wB = wrow[min(kb0 + 1, kb1 - 1) * 2];
+    dB = drow[min(kb0 + 1, kb1 - 1)];
     gm_dequant16(wA, dA, &wt[0][0][so], &wt[0][1][so]);
     ((v4u *)&xt[0][0][so])[0] = xr[0];
     ((v4u *)&xt[0][0][so])[1] = xr[1];
@@ -2842,9 +2849,9 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     __syncthreads();
     // step s uses buffer s%2; its register set (A for even s) is reloaded with
     // block s+2 while the other set (holding block s+1) is staged
-    for (uint32_t s = 0; s < nblk; s += 2) {
-        gm_step(acc, xr, wA, dA, wB, dB, xt, wt, 0, xhr, xlr, wrow, drow, s, nblk, so, wn, wm, li, lg);
-        gm_step(acc, xr, wB, dB, wA, dA, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, nblk, so, wn, wm, li, lg);
+    for (uint32_t s = kb0; s < kb1; s += 2) {
+        gm_step(acc, xr, wA, dA, wB, dB, xt, wt, 0, xhr, xlr, wrow, drow, s, kb1, so, wn, wm, li, lg);
+        gm_step(acc, xr, wB, dB, wA, dA, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, kb1, so, wn, wm, li, lg);
     }
     // epilogue: lane holds D[i = 4*lg + e][j = li] of each tile
 #pragma unroll
@@ -2864,6 +2871,28 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
                     else Y[(size_t)n * ldy + m] = v;
                 }
             }
+}
+
+// Split-K epilogue: the S partials P[s][N][M] summed in order, then the GEMM
+// epilogue (store, += residual, SwiGLU on (gate, up) column pairs).
+template <int EPI>
+__global__ void __launch_bounds__(TPB) k_splitk_reduce(const float *P, uint32_t S, uint32_t N, uint32_t M,
+                                                       float *Y, uint32_t ldy) {
+    const size_t nm = (size_t)N * M, step = EPI == SGK_EPI_SWIGLU ? 2 : 1;
+    for (size_t i = ((size_t)blockIdx.x * TPB + threadIdx.x) * step; i < nm; i += (size_t)gridDim.x * TPB * step) {
+        const uint32_t n = (uint32_t)(i / M), m = (uint32_t)(i - (size_t)n * M);
+        float v = P[i];
+        for (uint32_t k = 1; k < S; k++) v += P[(size_t)k * nm + i];
+        if (EPI == SGK_EPI_SWIGLU) {
+            float u = P[i + 1];
+            for (uint32_t k = 1; k < S; k++) u += P[(size_t)k * nm + i + 1];
+            Y[(size_t)n * ldy + (m >> 1)] = silu(v) * u;
+        } else if (EPI == SGK_EPI_ADD) {
+            Y[(size_t)n * ldy + m] += v;
+        } else {
+            Y[(size_t)n * ldy + m] = v;
+        }
+    }
 }
 
 // f32-weight GEMM for small test models (VALU, 16x16 outputs per workgroup).
@@ -2894,8 +2923,25 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
         const uint32_t sg = (uint32_t)min((total + TPB - 1) / TPB, (uint64_t)4096);
         hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
         const uint32_t mb = (a->M + GM_TM - 1) / GM_TM, nb = (a->N + 127) / 128;
-        const uint32_t grid = 8 * nb * ((mb + 7) / 8);
-#define GQ(E) hipLaunchKernelGGL((k_gemm_q8_mfma<E>), dim3(grid), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy)
+        const uint32_t grid = 8 * nb * ((mb + 7) / 8), nblk = a->K / 32;
+        // Split K when the tiles alone leave CUs idle (narrow weights): up to 4
+        // splits of at least 8 blocks, partials in a->part, summed in order.
+        const uint32_t cus = (uint32_t)device_cus();
+        uint32_t S = 1;
+        if (a->part && grid < cus) {
+            S = min(4u, (2 * cus + grid - 1) / grid);
+            while (S > 1 && (nblk / S < 8 || (uint64_t)S * a->N * a->M > a->part_cap)) S--;
+        }
+        if (S > 1) {
+            hipLaunchKernelGGL((k_gemm_q8_mfma<SGK_EPI_STORE>), dim3(grid, S), dim3(TPB), 0, s, a->xs, a->qs, a->d,
+                               a->part, a->N, a->M, a->K, a->M, (uint64_t)a->N * a->M);
+            const uint32_t rg = (uint32_t)min(((uint64_t)a->N * a->M + TPB - 1) / TPB, (uint64_t)4096);
+#define GR(E) hipLaunchKernelGGL((k_splitk_reduce<E>), dim3(rg), dim3(TPB), 0, s, a->part, S, a->N, a->M, a->Y, a->ldy)
+            if (a->epi == SGK_EPI_ADD) GR(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GR(SGK_EPI_SWIGLU); else GR(SGK_EPI_STORE);
+#undef GR
+            return hipGetLastError();
+        }
+#define GQ(E) hipLaunchKernelGGL((k_gemm_q8_mfma<E>), dim3(grid), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy, (uint64_t)0)
         if (a->epi == SGK_EPI_ADD) GQ(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GQ(SGK_EPI_SWIGLU); else GQ(SGK_EPI_STORE);
 #undef GQ
     } else {
@@ -2908,7 +2954,8 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
 }
 
 extern "C" hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, float *Y,
-                                  uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, hipStream_t s) {
-    sgk_gemm_args a = {X, qs, d, NULL, Y, N, M, K, K, M, SGK_EPI_STORE, xs};
+                                  uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, float *part,
+                                  uint64_t part_cap, hipStream_t s) {
+    sgk_gemm_args a = {X, qs, d, NULL, Y, N, M, K, K, M, SGK_EPI_STORE, xs, part, part_cap};
     return sgk_gemm(&a, s);
 }

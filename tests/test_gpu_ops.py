@@ -397,8 +397,9 @@ def test_kv_store_f16_bit_exact(gpu):
 
 @pytest.mark.parametrize("N,M,K", [(70, 130, 256), (300, 260, 96), (1, 32, 32), (129, 384, 1056)])
 def test_matmul_q8_prefill_gemm(gpu, N, M, K):
-    """Token and row tails (N, M past a 128 tile), K with an odd block count
-    (the last 64-wide step holds one Q8_0 block), a single token."""
+    """Token and row tails (N, M past a 128 tile), an odd block count, a
+    single token; (129, 384, 1056) is narrow enough to split K four ways
+    (8, 8, 8 and 9 blocks, partials summed in order)."""
     rng = np.random.default_rng(15 + N)
     X = rng.standard_normal(N * K).astype(np.float32)
     raw = q8_matrix(rng, M, K, sigma=1.0)
