@@ -2769,7 +2769,9 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
     wself = wrow[s2 * 2];
     dself = drow[s2];
     if (s < kend) {
-        bf16x8 bh[4], bl[4];
+        // all fragments first, then the three products over all 16 tiles in
+        // turn, so an accumulator's next MFMA comes 16 MFMAs after its last
+        bf16x8 bh[4], bl[4], ah[4], al[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t row = wm * 64 + c * 16 + li;
@@ -2779,15 +2781,21 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
 #pragma unroll
         for (int a = 0; a < 4; a++) {
             const uint32_t row = wn * 64 + a * 16 + li;
-            const bf16x8 ah = *(const bf16x8 *)&xt[cb][0][row * GM_LD + lg * 8];
-            const bf16x8 al = *(const bf16x8 *)&xt[cb][1][row * GM_LD + lg * 8];
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh[c], acc[a][c], 0, 0, 0);
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl[c], acc[a][c], 0, 0, 0);
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh[c], acc[a][c], 0, 0, 0);
+            ah[a] = *(const bf16x8 *)&xt[cb][0][row * GM_LD + lg * 8];
+            al[a] = *(const bf16x8 *)&xt[cb][1][row * GM_LD + lg * 8];
         }
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[a], bh[c], acc[a][c], 0, 0, 0);
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[a], bl[c], acc[a][c], 0, 0, 0);
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[a], bh[c], acc[a][c], 0, 0, 0);
     }
     gm_dequant16(wnext, dnext, &wt[cb ^ 1][0][so], &wt[cb ^ 1][1][so]);
     ((v4u *)&xt[cb ^ 1][0][so])[0] = xr[0];
