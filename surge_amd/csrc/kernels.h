@@ -30,8 +30,10 @@ typedef struct {
  * MI355X policy: about 64 keys per split (one key tile of the partial kernel
  * at head_dim 256) so that n_splits * n_kv_heads reaches a workgroup per CU
  * at 4k context with 4 kv heads, capped at SGK_MAX_SPLITS; never more
- * splits than keys. */
-#define SGK_MAX_SPLITS 256u
+ * splits than keys. Past 8k keys a split walks several tiles: 512
+ * workgroups (two per CU, which is what the partial's registers allow)
+ * with a 128-way combine beat 1024 workgroups with a 256-way one. */
+#define SGK_MAX_SPLITS 128u
 #define SGK_KEYS_PER_SPLIT 64u
 /* A state may lower or raise the cap (SURGE_SPLITK_GQA_CAP) within [4, 1024]. */
 #define SGK_SPLIT_CAP_MIN 4u

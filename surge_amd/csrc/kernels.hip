@@ -1373,10 +1373,13 @@ __global__ void __launch_bounds__(TPB) k_attn_partial_mf(sgk_attn a) {
     constexpr int VDC = HD / 8;                       // V staging: 8-dim chunks (threads t < 8*VDC)
     constexpr int QPT = (GMAX * HD + TPB - 1) / TPB, KOFF = QPT * TPB;
     __shared__ __align__(16) float qsh[GMAX * HD];
-    __shared__ __align__(16) float raw[KOFF + HD];    // raw q rows, then the raw k row
     __shared__ __align__(16) float sc[GMAX][MK];
     __shared__ float mrun[GMAX], srun[GMAX], alpha[GMAX], rn[GMAX + 1];
     __shared__ __align__(16) uint16_t vt[HD * FA_PLD];
+    // the raw q rows and k row of the prep live in the V^T tile's space: the
+    // prep is done (and a barrier passed) before the first tile is staged
+    static_assert((KOFF + HD) * sizeof(float) <= sizeof(vt), "raw rows exceed the V^T tile");
+    float *raw = (float *)vt;
     __shared__ float cs_s[HD], qn_s[HD], kn_s[HD];
     __shared__ __align__(16) uint16_t knew[HD], vnew[HD];
 

@@ -205,7 +205,8 @@ def test_split_cap_override_multi_tile_decode_vs_oracle(gpu, monkeypatch):
             gpu.state_new(64)
     monkeypatch.delenv("SURGE_SPLITK_GQA_CAP")
     gpu.state_new(64)
-    assert gpu.split_cap() == 256
+    assert gpu.split_cap() == 128
+    assert gpu.n_splits_at(32768) == 128 and gpu.n_splits_at(8192) == 128 and gpu.n_splits_at(4096) == 64
     syn.close()
 
 
