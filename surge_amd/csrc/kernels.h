@@ -51,7 +51,7 @@ static inline uint32_t sgk_n_splits(uint32_t seq) { return sgk_n_splits_cap(seq,
  * each output row). */
 enum { SGK_PRO_NONE = 0, SGK_PRO_RMS = 1, SGK_PRO_GATED = 2 };
 #define SGK_GATED_MAX_HEADS 256u
-enum { SGK_EPI_STORE = 0, SGK_EPI_ADD = 1, SGK_EPI_SWIGLU = 2 };
+enum { SGK_EPI_STORE = 0, SGK_EPI_ADD = 1, SGK_EPI_SWIGLU = 2, SGK_EPI_TILE = 3 /* prefill GEMM internal */ };
 
 typedef struct {
     const int8_t *qs;       /* Q8: int8 plane [rows][cols] */

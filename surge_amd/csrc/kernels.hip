@@ -571,6 +571,19 @@ static int device_cus() {
     return cus;
 }
 
+// Workgroups of the prefill GEMM resident at once: two per CU (its LDS).
+// SURGE_GEMM_SLOTS (decimal, >= 1) overrides it, for tests that exercise the
+// round split on small shapes.
+static uint32_t gemm_slots() {
+    const char *e = getenv("SURGE_GEMM_SLOTS");
+    if (e && *e) {
+        char *end = NULL;
+        const unsigned long v = strtoul(e, &end, 10);
+        if (end && !*end && v >= 1 && v <= 65536) return (uint32_t)v;
+    }
+    return 2 * (uint32_t)device_cus();
+}
+
 static hipError_t allow_lds(const void *kern, size_t lds) {
     if (lds <= 65536) return hipSuccess;
     if (lds > 163840) return hipErrorInvalidValue;
@@ -2808,19 +2821,32 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
     __syncthreads();
 }
 
+// Tile of linear workgroup index b: consecutive indices go to the 8 XCDs in
+// turn, and each XCD walks its weight-row tiles (mt = xcd, xcd+8, ...) for one
+// token tile before the next, so its L2 holds a row tile's weights while the
+// token tiles reuse them. Indices past the last row tile of an XCD are holes.
+__device__ __forceinline__ bool gm_tile(uint32_t b, uint32_t mb, uint32_t nb, uint32_t &mt, uint32_t &nt) {
+    const uint32_t xcd = b & 7, qq = b >> 3, mper = (mb + 7) / 8;
+    mt = xcd + 8 * (qq % mper);
+    nt = qq / mper;
+    return mt < mb && nt < nb;
+}
+
 // Split-K: workgroup row blockIdx.y of gridDim.y takes the Q8_0 blocks
 // [nblk*y/Y, nblk*(y+1)/Y) and writes at Y + y*ysplit (k_splitk_reduce sums
-// the partials in order); one split is the whole K.
+// the partials in order); one split is the whole K. The tile is that of
+// index blockIdx.x + boff. EPI == SGK_EPI_TILE writes the raw sums as one
+// 128x128 tile per workgroup at Y + (blockIdx.y*gridDim.x + blockIdx.x)*16384
+// (k_tile_reduce finishes them).
 template <int EPI>
 __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, uint32_t N, uint32_t M,
-               uint32_t K, uint32_t ldy, uint64_t ysplit) {
+               uint32_t K, uint32_t ldy, uint64_t ysplit, uint32_t boff) {
     __shared__ __align__(16) uint16_t xt[2][2][GM_TN * GM_LD];     // [buffer][hi | lo][token][k]
     __shared__ __align__(16) uint16_t wt[2][2][GM_TM * GM_LD];     // [buffer][hi | lo][row][k]
     const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
-    const uint32_t b = blockIdx.x, xcd = b & 7, qq = b >> 3, mper = (mb + 7) / 8;
-    const uint32_t mt_id = xcd + 8 * (qq % mper), nt_id = qq / mper;
-    if (mt_id >= mb || nt_id >= nb) return;
+    uint32_t mt_id, nt_id;
+    if (!gm_tile(blockIdx.x + boff, mb, nb, mt_id, nt_id)) return;
     const uint32_t n0 = nt_id * GM_TN, m0 = mt_id * GM_TM;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t wn = wave & 1, wm = wave >> 1;
@@ -2865,6 +2891,7 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
         gm_step(acc, xr, wB, dB, wA, dA, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, kb1, so, wn, wm, li, lg);
     }
     // epilogue: lane holds D[i = 4*lg + e][j = li] of each tile
+    float *Yt = Y + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (GM_TN * GM_TM);
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
@@ -2874,7 +2901,9 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
                 const uint32_t n = n0 + wn * 64 + a * 16 + lg * 4 + e;
                 const uint32_t m = m0 + wm * 64 + c * 16 + li;
                 const float v = acc[a][c][e];
-                if (EPI == SGK_EPI_SWIGLU) {
+                if (EPI == SGK_EPI_TILE) {
+                    Yt[(n - n0) * GM_TM + (m - m0)] = v;
+                } else if (EPI == SGK_EPI_SWIGLU) {
                     const float up = lane_xor1(v);            // column m+1 lives in lane li^1
                     if (!(li & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(v) * up;
                 } else if (n < N && m < M) {
@@ -2906,6 +2935,47 @@ __global__ void __launch_bounds__(TPB) k_splitk_reduce(const float *P, uint32_t 
     }
 }
 
+// Split-K epilogue of the tiles a SGK_EPI_TILE launch computed: workgroup
+// (t, part) takes 1/GM_TR_PARTS of the tile of index t + boff; each thread
+// requests its 4 columns of all S partial tiles (P + (s*ntile + t)*16384) at
+// once, sums them in order, then applies the GEMM epilogue.
+#define GM_TR_PARTS 16
+#define GM_TR_SMAX 16
+static_assert(GM_TR_PARTS * TPB * 4 == GM_TN * GM_TM, "k_tile_reduce covers a tile exactly");
+template <int EPI>
+__global__ void __launch_bounds__(TPB) k_tile_reduce(const float *P, uint32_t S, uint32_t ntile, uint32_t boff,
+                                                     uint32_t N, uint32_t M, float *Y, uint32_t ldy) {
+    const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
+    uint32_t mt, nt;
+    if (!gm_tile(blockIdx.x + boff, mb, nb, mt, nt)) return;
+    const uint32_t idx = (blockIdx.y * TPB + threadIdx.x) * 4;       // 4 columns of one token row
+    const uint32_t n = nt * GM_TN + idx / GM_TM, m = mt * GM_TM + idx % GM_TM;
+    if (n >= N || m >= M) return;
+    const float4 *Pt = (const float4 *)(P + (size_t)blockIdx.x * (GM_TN * GM_TM) + idx);
+    const size_t sstride = (size_t)ntile * (GM_TN * GM_TM) / 4;
+    float4 part[GM_TR_SMAX];
+#pragma unroll
+    for (uint32_t k = 0; k < GM_TR_SMAX; k++) part[k] = k < S ? Pt[k * sstride] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 v = part[0];
+#pragma unroll
+    for (uint32_t k = 1; k < GM_TR_SMAX; k++)
+        if (k < S) { v.x += part[k].x; v.y += part[k].y; v.z += part[k].z; v.w += part[k].w; }
+    float *y = Y + (size_t)n * ldy;
+    if (EPI == SGK_EPI_SWIGLU) {
+        // (gate, up) column pairs: m is even, so m+1 and m+3 sit in this float4
+        if (m + 1 < M) y[m >> 1] = silu(v.x) * v.y;
+        if (m + 3 < M) y[(m >> 1) + 1] = silu(v.z) * v.w;
+        return;
+    }
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        if (m + e >= M) break;
+        if (EPI == SGK_EPI_ADD) y[m + e] += vv[e];
+        else y[m + e] = vv[e];
+    }
+}
+
 // f32-weight GEMM for small test models (VALU, 16x16 outputs per workgroup).
 template <int EPI>
 __global__ void __launch_bounds__(TPB) k_gemm_f32(const float *X, const float *W, float *Y, uint32_t N,
@@ -2933,28 +3003,51 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
         const uint64_t total = (uint64_t)a->N * k4;
         const uint32_t sg = (uint32_t)min((total + TPB - 1) / TPB, (uint64_t)4096);
         hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
-        const uint32_t mb = (a->M + GM_TM - 1) / GM_TM, nb = (a->N + 127) / 128;
-        const uint32_t grid = 8 * nb * ((mb + 7) / 8), nblk = a->K / 32;
-        // Split K when the tiles alone leave CUs idle (narrow weights): up to 4
-        // splits of at least 8 blocks, partials in a->part, summed in order.
-        const uint32_t cus = (uint32_t)device_cus();
+        const uint32_t mb = (a->M + GM_TM - 1) / GM_TM, nb = (a->N + GM_TN - 1) / GM_TN;
+        const uint32_t grid = 8 * nb * ((mb + 7) / 8), nblk = a->K / 32, tiles = mb * nb;
+        // Workgroups run in rounds of `slots` (two resident per CU) and every
+        // tile takes the same time, so a launch costs ceil(tiles / slots)
+        // rounds. Narrow weights (one partial round) split K up to 4 ways to
+        // fill the round; wide ones whose last round is under half full run
+        // the full rounds as they are and split the leftover tiles' K over a
+        // whole round, partial tiles summed in order by k_tile_reduce. Splits
+        // keep at least 8 Q8_0 blocks and fit the partials in a->part.
+        const uint32_t slots = gemm_slots();
         uint32_t S = 1;
-        if (a->part && grid < cus) {
-            S = min(4u, (2 * cus + grid - 1) / grid);
+        if (a->part && tiles < slots) {
+            S = min(4u, slots / tiles);
             while (S > 1 && (nblk / S < 8 || (uint64_t)S * a->N * a->M > a->part_cap)) S--;
         }
         if (S > 1) {
             hipLaunchKernelGGL((k_gemm_q8_mfma<SGK_EPI_STORE>), dim3(grid, S), dim3(TPB), 0, s, a->xs, a->qs, a->d,
-                               a->part, a->N, a->M, a->K, a->M, (uint64_t)a->N * a->M);
+                               a->part, a->N, a->M, a->K, a->M, (uint64_t)a->N * a->M, 0u);
             const uint32_t rg = (uint32_t)min(((uint64_t)a->N * a->M + TPB - 1) / TPB, (uint64_t)4096);
 #define GR(E) hipLaunchKernelGGL((k_splitk_reduce<E>), dim3(rg), dim3(TPB), 0, s, a->part, S, a->N, a->M, a->Y, a->ldy)
             if (a->epi == SGK_EPI_ADD) GR(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GR(SGK_EPI_SWIGLU); else GR(SGK_EPI_STORE);
 #undef GR
             return hipGetLastError();
         }
-#define GQ(E) hipLaunchKernelGGL((k_gemm_q8_mfma<E>), dim3(grid), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy, (uint64_t)0)
+        uint32_t full = grid, S2 = 1;
+        if (a->part && grid > slots) {
+            full = grid / slots * slots;               // indices of the full rounds
+            const uint32_t left = grid - full;
+            if (left && left <= slots / 2) {
+                S2 = min((uint32_t)GM_TR_SMAX, slots / left);
+                while (S2 > 1 && (nblk / S2 < 8 || (uint64_t)S2 * left * (GM_TN * GM_TM) > a->part_cap)) S2--;
+            }
+            if (S2 < 2) full = grid;
+        }
+#define GQ(E) hipLaunchKernelGGL((k_gemm_q8_mfma<E>), dim3(full), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy, (uint64_t)0, 0u)
         if (a->epi == SGK_EPI_ADD) GQ(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GQ(SGK_EPI_SWIGLU); else GQ(SGK_EPI_STORE);
 #undef GQ
+        if (full < grid) {
+            const uint32_t left = grid - full;
+            hipLaunchKernelGGL((k_gemm_q8_mfma<SGK_EPI_TILE>), dim3(left, S2), dim3(TPB), 0, s, a->xs, a->qs, a->d,
+                               a->part, a->N, a->M, a->K, 0u, (uint64_t)0, full);
+#define GT(E) hipLaunchKernelGGL((k_tile_reduce<E>), dim3(left, GM_TR_PARTS), dim3(TPB), 0, s, a->part, S2, left, full, a->N, a->M, a->Y, a->ldy)
+            if (a->epi == SGK_EPI_ADD) GT(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GT(SGK_EPI_SWIGLU); else GT(SGK_EPI_STORE);
+#undef GT
+        }
     } else {
         dim3 grid((a->M + 15) / 16, (a->N + 15) / 16);
 #define GF(E) hipLaunchKernelGGL(k_gemm_f32<E>, grid, dim3(TPB), 0, s, a->X, a->wf, a->Y, a->N, a->M, a->K, a->ldx, a->ldy)

@@ -409,6 +409,31 @@ def test_matmul_q8_prefill_gemm(gpu, N, M, K):
     assert_close(yb.array.reshape(N, M), want)
 
 
+def test_matmul_q8_prefill_gemm_round_split(gpu, monkeypatch):
+    """The prefill GEMM's round split: with 28 workgroup slots, the 32 tiles
+    of a 256 x 2048 x 1792 product run as one full round plus 4 leftover
+    tiles whose K is split 7 ways (8 Q8_0 blocks each), partial tiles summed
+    in order by k_tile_reduce. Against the oracle, and against the unsplit
+    launch (default slots) within fp32 reassociation."""
+    N, M, K = 256, 2048, 1792
+    rng = np.random.default_rng(31)
+    X = rng.standard_normal(N * K).astype(np.float32)
+    raw = q8_matrix(rng, M, K, sigma=1.0)
+    xb, wb = gpu.buf(X), gpu.buf(raw)
+    ys = gpu.buf(np.zeros(N * M, np.float32))
+    monkeypatch.setenv("SURGE_GEMM_SLOTS", "28")
+    gpu.run_op("k_matmul_q8", xb, wb, ys, [N, M, K])
+    monkeypatch.delenv("SURGE_GEMM_SLOTS")
+    yu = gpu.buf(np.zeros(N * M, np.float32))
+    gpu.run_op("k_matmul_q8", xb, wb, yu, [N, M, K])
+    rows = [0, 1, 127, 128, 255]
+    want = np.stack([oracle_matvec_q8(raw, np.ascontiguousarray(X[n * K:(n + 1) * K]), M, K) for n in rows])
+    got = ys.array.reshape(N, M)
+    assert_close(got[rows], want)
+    unsplit = yu.array.reshape(N, M)
+    assert np.abs(got - unsplit).max() <= 1e-5 * np.abs(unsplit).max()
+
+
 # ---------------------------------------------------------------- prefill chunk hooks
 
 def test_conv1d_chunk_threads_state(gpu):
