@@ -715,7 +715,7 @@ sg_err sg_gpu_run_attn_prefill(sg_gpu *g, void *q, void *k, void *v, void *out, 
 }
 
 /* The online-softmax arm (surge.h:974-1050). The partial kernel here IS the
- * online form (running max/sum/acc rescaled across 32-key tiles), so the
+ * online form (running max/sum/acc rescaled across key tiles), so the
  * online entry points are the same kernel. */
 sg_err sg_gpu_run_attn_splitk_partial_gqa_online(sg_gpu *g, void *q, void *k, void *v, void *m, void *s,
                                                  void *acc, const uint32_t p[8]) {

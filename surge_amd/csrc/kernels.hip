@@ -1605,13 +1605,14 @@ extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
 
 // LSE combine (+ optional sigmoid gate). Workgroup (head, token). NaN/inf
 // conventions of ref.c:265-373: a NaN first max poisons, all-empty gives 0,
-// +inf maxima combine among themselves. The weighted sum over splits runs
-// with every load of a lane in flight: lane = (split group kg, 4-dim chunk),
+// +inf maxima combine among themselves. Loads do not wait for the merge
+// weights: a lane requests its split's max and sum and its first 16 rows of
+// acc before the maximum is reduced. Lane = (split group kg, 4-dim chunk),
 // each group summing its splits in increasing order, the groups then added in
 // order.
 template <int HD>
 __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
-    constexpr int C4 = HD / 4, KG = TPB / C4;
+    constexpr int C4 = HD / 4, KG = TPB / C4, PFX = 16;
     __shared__ float wts[1024];
     __shared__ float red[4];
     __shared__ float bc;
@@ -1623,8 +1624,18 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
     const float4 *acc = (const float4 *)(a.acc + (zoff + (size_t)h * ns) * HD);
     float *oh = a.out + (size_t)z * a.out_tok + (size_t)h * HD;
     const float *gate = a.gate ? a.gate + (size_t)z * a.q_tok + (size_t)h * a.q_stride : NULL;
-    float mx = -INFINITY;
-    for (uint32_t k = t; k < ns; k += TPB) mx = fmaxf(mx, mh[k]);
+    // every load that does not depend on the merge weights goes out first:
+    // this thread's first split's max and sum, and its first PFX rows of acc
+    const uint32_t c = t % C4, kg = t / C4;
+    const float m0 = t < ns ? mh[t] : -INFINITY, s0 = t < ns ? sh[t] : 0.0f;
+    float4 v[PFX];
+#pragma unroll
+    for (int u = 0; u < PFX; u++) {
+        const uint32_t k = kg + (uint32_t)u * KG;
+        v[u] = k < ns ? acc[(size_t)k * C4 + c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float mx = m0;
+    for (uint32_t k = t + TPB; k < ns; k += TPB) mx = fmaxf(mx, mh[k]);
     mx = wave_max(mx);
     if ((t & 63) == 0) red[t >> 6] = mx;
     __syncthreads();
@@ -1638,39 +1649,47 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
     }
     float sp = 0.0f;
     for (uint32_t k = t; k < ns; k += TPB) {
-        const float mk = mh[k];
+        const float mk = k == t ? m0 : mh[k];
         const float w = (mk == M) ? 1.0f : expf(mk - M);
         wts[k] = w;
-        sp += sh[k] * w;
+        sp += (k == t ? s0 : sh[k]) * w;
     }
     const float S = block_sum(sp, red);   // includes the barrier that publishes wts
-    const uint32_t c = t % C4, kg = t / C4;
     float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    uint32_t k = kg;
-    for (; k + 7 * KG < ns; k += 8 * KG) {
-        float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = acc[(size_t)(k + u * KG) * C4 + c];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const float w = wts[k + u * KG];
+    for (int u = 0; u < PFX; u++) {
+        const uint32_t k = kg + (uint32_t)u * KG;
+        if (k < ns) {
+            const float w = wts[k];
             num.x = fmaf(v[u].x, w, num.x); num.y = fmaf(v[u].y, w, num.y);
             num.z = fmaf(v[u].z, w, num.z); num.w = fmaf(v[u].w, w, num.w);
         }
     }
+    uint32_t k = kg + PFX * KG;
+    for (; k + 7 * KG < ns; k += 8 * KG) {
+        float4 r[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) r[u] = acc[(size_t)(k + u * KG) * C4 + c];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float w = wts[k + u * KG];
+            num.x = fmaf(r[u].x, w, num.x); num.y = fmaf(r[u].y, w, num.y);
+            num.z = fmaf(r[u].z, w, num.z); num.w = fmaf(r[u].w, w, num.w);
+        }
+    }
     for (; k < ns; k += KG) {
-        const float4 v = acc[(size_t)k * C4 + c];
+        const float4 r = acc[(size_t)k * C4 + c];
         const float w = wts[k];
-        num.x = fmaf(v.x, w, num.x); num.y = fmaf(v.y, w, num.y);
-        num.z = fmaf(v.z, w, num.z); num.w = fmaf(v.w, w, num.w);
+        num.x = fmaf(r.x, w, num.x); num.y = fmaf(r.y, w, num.y);
+        num.z = fmaf(r.z, w, num.z); num.w = fmaf(r.w, w, num.w);
     }
     part[kg][c] = num;
     __syncthreads();
     if (t >= (uint32_t)C4) return;
     float4 tot = part[0][t];
     for (int g2 = 1; g2 < KG; g2++) {
-        const float4 v = part[g2][t];
-        tot.x += v.x; tot.y += v.y; tot.z += v.z; tot.w += v.w;
+        const float4 pv = part[g2][t];
+        tot.x += pv.x; tot.y += pv.y; tot.z += pv.z; tot.w += pv.w;
     }
     const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
 #pragma unroll
