@@ -1267,7 +1267,7 @@ static hipError_t gemm_rows(sg_gpu *g, const dmat *M, const float *X, uint32_t l
 }
 
 /* One chunk of n tokens at positions base..base+n-1 through every layer. */
-static hipError_t prefill_chunk(sg_gpu *g, uint32_t n) {
+static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
     const sg_cfg *c = &g->cfg;
     hipStream_t s = g->stream;
     hipError_t e;
@@ -1284,6 +1284,7 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t n) {
             A.out = g->pf_CTX; A.gate = c->attn_output_gate ? g->pf_IN + hd : NULL; A.steps = g->pf_steps;
             A.n_heads = c->n_heads; A.n_kv = c->n_kv_heads; A.hd = hd; A.rope_dim = c->rope_dim; A.q_stride = qs;
             A.q_tok = in_rows; A.out_tok = g->attn_width; A.max_splits = SGK_PREFILL_SPLITS; A.ntok = n;
+            A.seq = base + n;       /* keys of the chunk's last token: the flash pass splits deep chunks */
             A.scale = (float)(1.0 / sqrt((double)hd)); A.prefill = 1;
             A.kv_ps = hd; A.kv_hs = (uint64_t)g->max_ctx * hd;
             if ((e = sgk_attn_prep(&A, L->qn, L->kn, g->cs_table, c->rms_eps, s)) != hipSuccess) return e;
@@ -1340,7 +1341,7 @@ sg_err sg_gpu_prefill(sg_gpu *g, const sg_model *m, const int32_t *tokens, uint3
         }
         HIPCHK(hipMemcpyAsync(g->pf_steps, g->pf_hsteps, (uint64_t)n * sizeof(sgk_step), hipMemcpyHostToDevice,
                               g->stream), "chunk descriptors");
-        hipError_t he = prefill_chunk(g, n);
+        hipError_t he = prefill_chunk(g, base, n);
         if (he != hipSuccess) return errf("gpu: prefill launch failed: %s", hipGetErrorString(he));
         if (base + n >= n_tokens) {
             sgk_gemv lm = {0};

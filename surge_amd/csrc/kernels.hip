@@ -1738,6 +1738,9 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
     const uint32_t zlast = min(z0 + FA_TQ, ntok) - 1;
     const uint32_t kend = base + zlast + 1;     // keys 0 .. kend-1 (positions are consecutive)
     const uint16_t *kc = a.kc, *vc = a.vc;
+    // split sp of gridDim.z: the key tiles [sp*nt/S, (sp+1)*nt/S) of the block
+    const uint32_t S = gridDim.z, sp = blockIdx.z, ntiles = (kend + FA_TK - 1) / FA_TK;
+    const uint32_t kbeg = (sp * ntiles / S) * FA_TK, kstop = min(((sp + 1) * ntiles / S) * FA_TK, kend);
 
     // q fragments of this wave's 16 tokens (A operand: row li, dims 8*lg.. of each 32)
     f16x8 qh[NKB], ql[NKB];
@@ -1765,7 +1768,7 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
 
     const uint32_t kk = t >> 2, kd = (t & 3) * KDT;        // K staging role
     const uint32_t vkg = t / VDC, vdc = t % VDC;            // V staging role
-    for (uint32_t k0 = 0; k0 < kend; k0 += FA_TK) {
+    for (uint32_t k0 = kbeg; k0 < kstop; k0 += FA_TK) {
         // stage K [key][dim] and V^T [dim][key] (keys clamped into the range)
         {
             const uint32_t key = min(k0 + kk, kend - 1);
@@ -1863,6 +1866,21 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
         }
         __syncthreads();
     }
+    if (S > 1) {
+        // partials in the decode layout [token][head][split] for k_attn_combine:
+        // m the running max, s the running sum, acc the unnormalised output
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t z = z0 + wave * 16 + lg * 4 + e;
+            if (z >= ntok) continue;
+            const size_t ph = ((size_t)z * a.n_heads + h) * S + sp;
+            if (li == 0) { a.m[ph] = mrun[e]; a.s[ph] = srun[e]; }
+            float *acc = a.acc + ph * HD;
+#pragma unroll
+            for (int n = 0; n < NNT; n++) acc[n * 16 + li] = o[n][e];
+        }
+        return;
+    }
     // finish: o / s, sigmoid gate, store (lane: rows 4*lg+e, dims n*16+li)
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -1881,18 +1899,38 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
     }
 }
 
+extern "C" hipError_t sgk_attn_combine(const sgk_attn *a, hipStream_t s);
+
+// Launch the flash pass. A chunk has few (token block, head) pairs (192 for
+// 512 tokens x 24 heads on 256 CUs) and each walks every key up to its
+// tokens, so deep chunks split their key tiles over up to a->max_splits
+// workgroups, about one per FA_SPLIT_KEYS keys of the deepest block
+// (a->seq = the position after the chunk's last token, 0 = unknown: no
+// split), when a->m, s, acc hold ntok x n_heads x max_splits partials. The
+// splits write partials and k_attn_combine merges them in split order and
+// applies the gate.
+#define FA_SPLIT_KEYS 512u
 extern "C" hipError_t sgk_attn_flash(const sgk_attn *a, hipStream_t s) {
     if (!a->ntok || !a->n_heads) return hipSuccess;
     if (!a->steps || !a->n_kv || a->n_heads % a->n_kv || ((uintptr_t)a->q & 15) || a->q_stride % 4 || a->q_tok % 4)
         return hipErrorInvalidValue;
-    dim3 grid(a->n_heads, (a->ntok + FA_TQ - 1) / FA_TQ);
+    if (a->hd != 64 && a->hd != 128 && a->hd != 256) return hipErrorInvalidValue;
+    uint32_t S = 1;
+    if (a->m && a->s && a->acc && a->max_splits > 1 && a->seq > FA_SPLIT_KEYS)
+        S = min(a->max_splits, (a->seq + FA_SPLIT_KEYS - 1) / FA_SPLIT_KEYS);
+    sgk_attn k = kv_resolved(a);
+    k.max_splits = S;
+    dim3 grid(a->n_heads, (a->ntok + FA_TQ - 1) / FA_TQ, S);
     switch (a->hd) {
-    case 64: hipLaunchKernelGGL(k_attn_flash<64>, grid, dim3(TPB), 0, s, kv_resolved(a)); break;
-    case 128: hipLaunchKernelGGL(k_attn_flash<128>, grid, dim3(TPB), 0, s, kv_resolved(a)); break;
-    case 256: hipLaunchKernelGGL(k_attn_flash<256>, grid, dim3(TPB), 0, s, kv_resolved(a)); break;
-    default: return hipErrorInvalidValue;
+    case 64: hipLaunchKernelGGL(k_attn_flash<64>, grid, dim3(TPB), 0, s, k); break;
+    case 128: hipLaunchKernelGGL(k_attn_flash<128>, grid, dim3(TPB), 0, s, k); break;
+    case 256: hipLaunchKernelGGL(k_attn_flash<256>, grid, dim3(TPB), 0, s, k); break;
     }
-    return hipGetLastError();
+    if (S == 1) return hipGetLastError();
+    sgk_attn c = k;
+    c.steps = NULL;                 // every token has the same S splits
+    c.n_splits = S;
+    return sgk_attn_combine(&c, s);
 }
 
 extern "C" hipError_t sgk_attn_combine(const sgk_attn *a, hipStream_t s) {

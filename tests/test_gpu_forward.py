@@ -300,3 +300,29 @@ def test_prefill_gemm_round_split_matches_serial(gpu, monkeypatch):
     dflt = gpu.prefill(prompt, chunk=128)
     assert rel(last, dflt) < 1e-4
     syn.close()
+
+
+@pytest.mark.parametrize("cfg", ["HD256", "HD128"])
+def test_deep_prefill_key_split_matches_serial(gpu, cfg):
+    """Deep chunks split the flash pass's key tiles (about one workgroup per
+    512 keys) and merge the partials with the LSE combine: 1100 tokens in
+    chunks of 512 put chunk 2 at depth 1024 (2 splits, two ranges of 8 tiles)
+    and chunk 3 at 1100 (3 splits, blocks whose early splits hold fewer
+    tiles). Last logits and the next step against the serial forward
+    (2e-4, same argmax)."""
+    conf = {"HD256": HD256, "HD128": HD128}[cfg]
+    syn = S.Synth(conf, S.SG_T_Q8_0, seed=23)
+    gpu.load_model(syn.model)
+    gpu.state_new(1104)
+    rng = np.random.default_rng(24)
+    prompt = rng.integers(0, conf["vocab"], 1100).tolist()
+    serial = None
+    for p, t in enumerate(prompt):
+        serial = gpu.forward(t, p)
+    nxt_serial = gpu.forward(int(np.argmax(serial)), len(prompt))
+    last = gpu.prefill(prompt, chunk=512)
+    assert rel(last, serial) < 2e-4
+    assert int(np.argmax(last)) == int(np.argmax(serial))
+    nxt = gpu.forward(int(np.argmax(last)), len(prompt))
+    assert rel(nxt, nxt_serial) < 2e-4
+    syn.close()
