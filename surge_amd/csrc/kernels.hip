@@ -2449,17 +2449,21 @@ __global__ void __launch_bounds__(TPB) k_qk_norm_chunk(float *conv_out, uint32_t
 // key head, the block's 16 v values, beta and decay), double-buffered: the
 // next block's global loads are in flight while the current block is walked,
 // so a token step reads only LDS.
-template <int DK>
+template <int DK, int ROWS>
 struct dcg {
-    static constexpr int DCT = DK > 128 ? 16 : 32;        // tokens per staged block
+    static constexpr int DCT = 16;                        // tokens per staged block
     static constexpr int TPT = TPB / DCT;                 // threads per token (k|q)
     static constexpr int NV4 = 2 * DK / TPT / 4;          // k|q float4s per thread
+    static constexpr int VTT = ROWS / 4;                  // threads per token (v, 4 rows each)
+    static_assert(TPB / VTT >= DCT, "v staging covers a block");
 };
+template <int DK, int ROWS>
+using dcregs = f32x4[dcg<DK, ROWS>::NV4 + 1];     // one thread's staged loads of a block
 
-template <int DK>
-__device__ __forceinline__ void dc_load(f32x4 (&r)[dcg<DK>::NV4 + 1], const sgk_gdn &a, const float *conv_out,
+template <int DK, int ROWS>
+__device__ __forceinline__ void dc_load(dcregs<DK, ROWS> &r, const sgk_gdn &a, const float *conv_out,
                                         uint32_t z0, uint32_t ntok, uint32_t hk, uint32_t h, uint32_t j0) {
-    using C = dcg<DK>;
+    using C = dcg<DK, ROWS>;
     const uint32_t t = threadIdx.x, zt = t / C::TPT, part = t % C::TPT, key_dim = a.n_k * DK;
     const float *cz = conv_out + (size_t)min(z0 + zt, ntok - 1) * a.conv_dim;
 #pragma unroll
@@ -2468,22 +2472,22 @@ __device__ __forceinline__ void dc_load(f32x4 (&r)[dcg<DK>::NV4 + 1], const sgk_
         const float *src = e < DK ? cz + key_dim + (size_t)hk * DK + e : cz + (size_t)hk * DK + (e - DK);
         r[u] = *(const f32x4 *)src;
     }
-    // v: token t/4, rows j0 + 4*(t%4) .. +3
-    const uint32_t vz = t >> 2, vr = j0 + (t & 3) * 4;
+    // v: token t/VTT, rows j0 + 4*(t%VTT) .. +3
+    const uint32_t vz = t / C::VTT, vr = j0 + (t % C::VTT) * 4;
     const float *vp = conv_out + (size_t)min(z0 + vz, ntok - 1) * a.conv_dim + 2 * key_dim + (size_t)h * a.dv + vr;
     r[C::NV4] = (vz < (uint32_t)C::DCT && vr < a.dv) ? *(const f32x4 *)vp : (f32x4){0.f, 0.f, 0.f, 0.f};
 }
 
-template <int DK>
-__device__ __forceinline__ void dc_store(const f32x4 (&r)[dcg<DK>::NV4 + 1], float *kq, float *vs, float *gs,
+template <int DK, int ROWS>
+__device__ __forceinline__ void dc_store(const dcregs<DK, ROWS> &r, float *kq, float *vs, float *gs,
                                          const sgk_gdn &a, const float *gates, uint32_t in_stride, uint32_t z0,
                                          uint32_t ntok, uint32_t h) {
-    using C = dcg<DK>;
+    using C = dcg<DK, ROWS>;
     const uint32_t t = threadIdx.x, zt = t / C::TPT, part = t % C::TPT;
 #pragma unroll
     for (int u = 0; u < C::NV4; u++) *(f32x4 *)&kq[zt * 2 * DK + (part * C::NV4 + u) * 4] = r[u];
-    const uint32_t vz = t >> 2;
-    if (vz < (uint32_t)C::DCT) *(f32x4 *)&vs[vz * GDN_ROWS + (t & 3) * 4] = r[C::NV4];
+    const uint32_t vz = t / C::VTT;
+    if (vz < (uint32_t)C::DCT) *(f32x4 *)&vs[vz * ROWS + (t % C::VTT) * 4] = r[C::NV4];
     if (t < (uint32_t)C::DCT) {
         const uint32_t z = min(z0 + t, ntok - 1), cd = a.conv_dim, vd = a.n_v * a.dv;
         float beta, decay;
@@ -2499,15 +2503,15 @@ __device__ __forceinline__ void dc_store(const f32x4 (&r)[dcg<DK>::NV4 + 1], flo
     }
 }
 
-template <int DK>
+template <int DK, int ROWS>
 __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *conv_out, uint32_t in_stride,
                                                      uint32_t ntok, const float *gates) {
-    using C = dcg<DK>;
-    constexpr int EPL = drow<DK>::EPL, RPW = GDN_ROWS / (TPB / 64);
+    using C = dcg<DK, ROWS>;
+    constexpr int EPL = drow<DK>::EPL, RPW = ROWS / (TPB / 64);
     __shared__ __align__(16) float kq[2][C::DCT * 2 * DK];
-    __shared__ __align__(16) float vs[2][C::DCT * GDN_ROWS];
+    __shared__ __align__(16) float vs[2][C::DCT * ROWS];
     __shared__ float gs[2][2 * C::DCT];
-    const uint32_t h = blockIdx.x, j0 = blockIdx.y * GDN_ROWS, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t h = blockIdx.x, j0 = blockIdx.y * ROWS, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t dv = a.dv, vd = a.n_v * dv;
     const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k);
     float *Sh = a.S + (size_t)h * dv * DK;
@@ -2521,12 +2525,12 @@ __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *con
         if (j < dv) row_load<DK>(sr[u], Sh + (size_t)j * DK, lane);
     }
     f32x4 r[C::NV4 + 1];
-    dc_load<DK>(r, a, conv_out, 0, ntok, hk, h, j0);
-    dc_store<DK>(r, kq[0], vs[0], gs[0], a, gates, in_stride, 0, ntok, h);
+    dc_load<DK, ROWS>(r, a, conv_out, 0, ntok, hk, h, j0);
+    dc_store<DK, ROWS>(r, kq[0], vs[0], gs[0], a, gates, in_stride, 0, ntok, h);
     __syncthreads();
     for (uint32_t z0 = 0; z0 < ntok; z0 += C::DCT) {
         const uint32_t buf = (z0 / C::DCT) & 1;
-        dc_load<DK>(r, a, conv_out, z0 + C::DCT, ntok, hk, h, j0);    // past the end: clamped, unused
+        dc_load<DK, ROWS>(r, a, conv_out, z0 + C::DCT, ntok, hk, h, j0);    // past the end: clamped, unused
         const uint32_t zn = min((uint32_t)C::DCT, ntok - z0);
         for (uint32_t zz = 0; zz < zn; zz++) {
             // delta_update for the wave's RPW rows at once: both dot products
@@ -2548,7 +2552,7 @@ __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *con
             }
             const uint32_t myrow = rows_row<RPW>(lane), jr = wave + myrow * (TPB / 64);
             const float kvr = rows_sum<RPW>(part, lane);
-            const float dmine = (vs[buf][zz * GDN_ROWS + jr] - kvr) * beta;
+            const float dmine = (vs[buf][zz * ROWS + jr] - kvr) * beta;
 #pragma unroll
             for (int u = 0; u < RPW; u++) {
                 const float dr = lane_read(dmine, rows_lane<RPW>(u));
@@ -2560,7 +2564,7 @@ __global__ void __launch_bounds__(TPB) k_delta_chunk(sgk_gdn a, const float *con
             const float yr = rows_sum<RPW>(part, lane);
             if ((lane & (64 / RPW - 1)) == 0 && j0 + jr < dv) a.y[(size_t)(z0 + zz) * vd + (size_t)h * dv + j0 + jr] = yr;
         }
-        dc_store<DK>(r, kq[buf ^ 1], vs[buf ^ 1], gs[buf ^ 1], a, gates, in_stride, z0 + C::DCT, ntok, h);
+        dc_store<DK, ROWS>(r, kq[buf ^ 1], vs[buf ^ 1], gs[buf ^ 1], a, gates, in_stride, z0 + C::DCT, ntok, h);
         __syncthreads();
     }
 #pragma unroll
@@ -2611,14 +2615,19 @@ extern "C" hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t 
 extern "C" hipError_t sgk_delta_scan(const sgk_gdn *a, const float *qkv, uint32_t in_stride, uint32_t ntok,
                                      const float *gates, hipStream_t s) {
     if (!ntok || !a->n_v || !a->dv) return hipSuccess;
-    dim3 grid(a->n_v, (a->dv + GDN_ROWS - 1) / GDN_ROWS);
+    // 8 value rows per workgroup (16-token staged blocks: 33 KB of LDS at
+    // dk 128, so three workgroups share a CU and hide each other's serial
+    // reduction chains); 16 rows at dk 256 (its blocks take 64 KB)
+#define DSCAN(D, R) hipLaunchKernelGGL((k_delta_chunk<D, R>), dim3(a->n_v, (a->dv + (R) - 1) / (R)), dim3(TPB), 0, s, \
+                                       *a, qkv, in_stride, ntok, gates)
     switch (a->dk) {
-    case 32: hipLaunchKernelGGL(k_delta_chunk<32>, grid, dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates); break;
-    case 64: hipLaunchKernelGGL(k_delta_chunk<64>, grid, dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates); break;
-    case 128: hipLaunchKernelGGL(k_delta_chunk<128>, grid, dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates); break;
-    case 256: hipLaunchKernelGGL(k_delta_chunk<256>, grid, dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates); break;
+    case 32: DSCAN(32, 8); break;
+    case 64: DSCAN(64, 8); break;
+    case 128: DSCAN(128, 8); break;
+    case 256: DSCAN(256, 16); break;
     default: return hipErrorInvalidValue;
     }
+#undef DSCAN
     return hipGetLastError();
 }
 
