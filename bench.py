@@ -203,6 +203,8 @@ def main():
     ap.add_argument("--shape", default="27b", choices=["27b", "2b"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--chunk", type=int, default=512, help="prefill chunk (tokens)")
+    ap.add_argument("--fill", action="store_true",
+                    help="no prefill: seeded K/V and DeltaNet state up to --ctx (decode at depth)")
     ap.add_argument("--calib-mb", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (counter calibration)")
     a = ap.parse_args()
@@ -219,14 +221,25 @@ def main():
     t = time.time()
     gpu.load_model(syn.model)
     log(f"loaded to HBM in {time.time() - t:.1f} s ({gpu.alloc_bytes() / 1e9:.2f} GB allocated)")
-    gpu.state_new(a.ctx + a.warmup + a.steps + 8)
-    prompt = np.random.default_rng(0).integers(0, cfg["vocab"], a.ctx).astype(np.int32)
+    need = a.ctx + a.warmup + a.steps + 8
+    if need > S.SG_KV_CAP_MAX:
+        print(f"--ctx {a.ctx} with {a.warmup} + {a.steps} steps needs {need} positions; the cap is "
+              f"{S.SG_KV_CAP_MAX}", file=sys.stderr)
+        sys.exit(2)
+    gpu.state_new(need)
     t = time.time()
-    lg = gpu.prefill(prompt, chunk=a.chunk)
-    gpu.sync()
-    pf_s = time.time() - t
-    log(f"prefilled {a.ctx} context tokens in {pf_s:.2f} s ({a.ctx / pf_s:.0f} tok/s, chunk {a.chunk})")
-    tok = int(np.argmax(lg))
+    if a.fill:
+        gpu.fill_synthetic(a.ctx, seed=0)
+        pf_s = time.time() - t
+        log(f"filled K/V and DeltaNet state to depth {a.ctx} in {pf_s:.2f} s (no prefill)")
+        tok = 0
+    else:
+        prompt = np.random.default_rng(0).integers(0, cfg["vocab"], a.ctx).astype(np.int32)
+        lg = gpu.prefill(prompt, chunk=a.chunk)
+        gpu.sync()
+        pf_s = time.time() - t
+        log(f"prefilled {a.ctx} context tokens in {pf_s:.2f} s ({a.ctx / pf_s:.0f} tok/s, chunk {a.chunk})")
+        tok = int(np.argmax(lg))
     pos = a.ctx
     if a.warmup:
         w = gpu.decode_greedy(tok, pos, a.warmup)
@@ -256,12 +269,14 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "f32 (int8 Q8_0 weights, f16 KV)",
         "data": "synthetic (seeded random-init weights, random token ids)",
         "config": {"workload": f"{a.shape.upper()}-shape qwen35 hybrid Q8_0, greedy decode bs=1 at "
-                               f"{a.ctx}-token context (device-resident greedy loop, one HIP graph per token)",
+                               f"{a.ctx}-token context (device-resident greedy loop, one HIP graph per token"
+                               + ("; K/V and DeltaNet state filled with seeded values, no prefill)" if a.fill else ")"),
                    "ctx": a.ctx, "batch": 1, "model_bytes": syn_bytes_hint(cfg)},
         "decode_hbm": {"bytes_per_token": int(bytes_tok), "parts": parts,
                        "achieved_GBs": round(decode_gbs, 1), "frac": round(decode_gbs / HBM_PEAK_GBS, 4)},
-        "prefill": {"tokens": a.ctx, "chunk": a.chunk, "seconds": round(pf_s, 3),
-                    "tok_per_s": round(a.ctx / pf_s, 1)},
+        "prefill": ({"tokens": a.ctx, "synthetic_fill": True, "seconds": round(pf_s, 3)} if a.fill else
+                    {"tokens": a.ctx, "chunk": a.chunk, "seconds": round(pf_s, 3),
+                     "tok_per_s": round(a.ctx / pf_s, 1)}),
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -286,6 +286,14 @@ sg_err sg_gpu_sync(sg_gpu *g);
  * step i. Same tokens as calling sg_gpu_forward + sg_argmax_f32 in a loop. */
 sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
                             uint32_t n_steps, int32_t *out_tokens);
+/* Decode at depth without a prefill (no reference counterpart; for
+ * benchmarks of the KV read path at long context): fills every attention
+ * layer's K/V cache rows [0, n_tokens) with seeded f16 values in [-2, 2], the
+ * DeltaNet states and conv rings with seeded values in [-0.05, 0.05], and
+ * sets the state's position to n_tokens (< max_ctx). The next call is then
+ * sg_gpu_forward / sg_gpu_decode_greedy at pos = n_tokens. Same seed, same
+ * state. */
+sg_err sg_gpu_state_fill_synthetic(sg_gpu *g, uint32_t n_tokens, uint32_t seed);
 
 /* Measurement hooks (no reference counterpart): the library's HIP stream
  * (a hipStream_t) for event timing, and one decode-step GEMV enqueued alone

@@ -22,6 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsurge_amd.so")
 
 SG_T_F32, SG_T_F16, SG_T_Q8_0, SG_T_BF16 = 0, 1, 8, 30
+SG_KV_CAP_MAX = 262144      # the f16 KV cache's largest context (include/surge.h)
 
 
 class SurgeError(RuntimeError):
@@ -123,6 +124,7 @@ _SIGS = {
     "sg_gpu_forward_nosync": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32]),
     "sg_gpu_decode_greedy": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32,
                                      C.c_uint32, C.POINTER(C.c_int32)]),
+    "sg_gpu_state_fill_synthetic": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32]),
     "sg_gpu_prefill": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.POINTER(C.c_int32), C.c_uint32,
                                C.c_uint32, C.POINTER(C.POINTER(C.c_float))]),
     "sg_gpu_sync": (SgErr, [C.c_void_p]),
@@ -292,6 +294,10 @@ class Gpu:
         out = (C.c_int32 * n)()
         check(lib().sg_gpu_decode_greedy(self.handle, self.model, token, pos, n, out))
         return np.array(out, dtype=np.int32)
+
+    def fill_synthetic(self, n_tokens: int, seed: int = 0) -> None:
+        """Seeded K/V and DeltaNet state up to depth n_tokens (decode then starts at n_tokens)."""
+        check(lib().sg_gpu_state_fill_synthetic(self.handle, n_tokens, seed))
 
     def prefill(self, tokens, chunk: int = 0) -> np.ndarray:
         ids = np.ascontiguousarray(tokens, dtype=np.int32)

@@ -1224,6 +1224,34 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
     return SG_OK;
 }
 
+sg_err sg_gpu_state_fill_synthetic(sg_gpu *g, uint32_t n_tokens, uint32_t seed) {
+    if (!g || !g->have_state) return (sg_err){"gpu: sg_gpu_state_fill_synthetic needs a live state"};
+    if (n_tokens >= g->max_ctx) return (sg_err){"gpu: sg_gpu_state_fill_synthetic: n_tokens must be < max_ctx"};
+    const sg_cfg *c = &g->cfg;
+    hipStream_t s = g->stream;
+    HIPCHK(hipStreamSynchronize(s), "fill: previous work");
+    const uint32_t nkv = c->n_kv_heads, hd = c->head_dim;
+    for (uint32_t i = 0; i < c->n_layers; i++) {
+        glayer *L = &g->ls[i];
+        const uint32_t ls = seed * 2654435761u + 97u * i;
+        if (L->attn) {
+            /* head-major [n_kv][max_ctx][hd]: head h's first n_tokens rows are contiguous */
+            for (uint32_t h = 0; h < nkv; h++) {
+                const uint64_t off = (uint64_t)h * g->max_ctx * hd, n = (uint64_t)n_tokens * hd;
+                HIPCHK(sgk_fill_hash((uint16_t *)L->kc + off, n, 1, ls + 2 * h, 2.0f, s), "fill K");
+                HIPCHK(sgk_fill_hash((uint16_t *)L->vc + off, n, 1, ls + 2 * h + 1, 2.0f, s), "fill V");
+            }
+        } else {
+            HIPCHK(sgk_fill_hash(L->S, (uint64_t)c->n_v_heads * c->head_v_dim * c->head_k_dim, 0, ls + 7, 0.05f, s),
+                   "fill S");
+            HIPCHK(sgk_fill_hash(L->ring, (uint64_t)4 * g->conv_dim, 0, ls + 11, 0.05f, s), "fill ring");
+        }
+    }
+    HIPCHK(hipStreamSynchronize(s), "fill");
+    g->used = n_tokens;
+    return SG_OK;
+}
+
 /* ---------------------------------------------------------------------
  * prefill (surge.h:1276-1309)
  * --------------------------------------------------------------------- */

@@ -228,6 +228,8 @@ hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream_t s);
 
 /* Fills n f32 with a value (a kernel, so it may sit inside a captured graph). */
 hipError_t sgk_fill_f32(float *p, float v, uint64_t n, hipStream_t s);
+/* n seeded values in [-scale, scale], written as f16 bits (f16 != 0) or f32. */
+hipError_t sgk_fill_hash(void *p, uint64_t n, int f16, uint32_t seed, float scale, hipStream_t s);
 
 /* Prefill GEMM Y[N][M] = X[N][K] * W[M][K]^T with W in the Q8 device layout,
  * on MFMA (bf16 inputs, x split hi+lo, fp32 accumulate, per-block scale in

@@ -801,6 +801,27 @@ extern "C" hipError_t sgk_fill_f32(float *p, float v, uint64_t n, hipStream_t s)
     return hipGetLastError();
 }
 
+// Seeded fill of n values, f16 (bits of f16) or f32: a hash of (seed, index)
+// mapped to a sum of two uniforms in [-scale, scale] (a triangular spread).
+__global__ void k_fill_hash(void *p, uint64_t n, int f16, uint32_t seed, float scale) {
+    for (uint64_t i = (uint64_t)blockIdx.x * TPB + threadIdx.x; i < n; i += (uint64_t)gridDim.x * TPB) {
+        uint64_t h = (i + 1) * 0x9E3779B97F4A7C15ull ^ ((uint64_t)seed << 32 | seed);
+        h ^= h >> 31; h *= 0xBF58476D1CE4E5B9ull; h ^= h >> 29; h *= 0x94D049BB133111EBull; h ^= h >> 32;
+        const float u0 = (float)(uint32_t)(h & 0xFFFFu) / 65535.0f, u1 = (float)(uint32_t)((h >> 16) & 0xFFFFu) / 65535.0f;
+        const float v = (u0 + u1 - 1.0f) * scale;
+        if (f16) ((uint16_t *)p)[i] = f2h(v);
+        else ((float *)p)[i] = v;
+    }
+}
+
+extern "C" hipError_t sgk_fill_hash(void *p, uint64_t n, int f16, uint32_t seed, float scale, hipStream_t s) {
+    if (!n) return hipSuccess;
+    uint64_t blocks = (n + TPB - 1) / TPB;
+    hipLaunchKernelGGL(k_fill_hash, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(TPB), 0, s, p, n, f16,
+                       seed, scale);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // RMSNorm over strided slices; RoPE over strided slices; softmax.
 // ---------------------------------------------------------------------------

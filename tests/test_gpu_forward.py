@@ -326,3 +326,30 @@ def test_deep_prefill_key_split_matches_serial(gpu, cfg):
     nxt = gpu.forward(int(np.argmax(last)), len(prompt))
     assert rel(nxt, nxt_serial) < 2e-4
     syn.close()
+
+
+def test_fill_synthetic_depth_then_decode(gpu):
+    """Decode at depth without a prefill: the seeded fill sets the state's
+    position, the next forward must be at that position, the same seed gives
+    bit-identical logits, another seed different ones, and the split count
+    at depth follows the policy (1500 keys: 24 splits of about 64 keys).
+    (Its own model: the module's `small` model is replaced by later tests.)"""
+    syn = S.Synth(SMALL, S.SG_T_Q8_0, seed=5)
+    gpu.load_model(syn.model)
+    gpu.state_new(1600)
+    with pytest.raises(S.SurgeError):
+        gpu.fill_synthetic(1600)                 # must leave a position to decode
+    gpu.fill_synthetic(1500, seed=3)
+    assert gpu.used() == 1500
+    with pytest.raises(S.SurgeError):
+        gpu.forward(5, 0)                        # positions continue from the fill
+    a = gpu.forward(5, 1500)
+    assert np.isfinite(a).all()
+    gpu.fill_synthetic(1500, seed=3)
+    b = gpu.forward(5, 1500)
+    assert np.array_equal(a, b)
+    gpu.fill_synthetic(1500, seed=4)
+    c = gpu.forward(5, 1500)
+    assert not np.array_equal(a, c)
+    assert gpu.n_splits_at(1501) == 24
+    syn.close()
