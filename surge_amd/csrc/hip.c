@@ -1290,7 +1290,21 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
 static hipError_t gemm_rows(sg_gpu *g, const dmat *M, const float *X, uint32_t ldx, float *Y, uint32_t ldy,
                             uint32_t n, int epi) {
     sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi, g->pf_XS, g->pf_PART,
-                        (uint64_t)4 * g->pf_chunk * g->cfg.hidden };
+                        (uint64_t)4 * g->pf_chunk * g->cfg.hidden, NULL, 0.0f };
+    return sgk_gemm(&a, g->stream);
+}
+
+/* RMSNorm(X) (weight nw) then the GEMM: Q8 weights take the norm inside the
+ * GEMM's bf16 split (one pass over X); f32 weights normalise into pf_Xn. */
+static hipError_t gemm_rows_norm(sg_gpu *g, const dmat *M, const float *X, const float *nw, float *Y,
+                                 uint32_t ldy, uint32_t n, int epi) {
+    const uint32_t H = g->cfg.hidden;
+    if (!M->qs || !nw) {
+        hipError_t e = sgk_rmsnorm_heads(X, nw, g->pf_Xn, H, n, H, g->cfg.rms_eps, g->stream);
+        return e != hipSuccess ? e : gemm_rows(g, M, g->pf_Xn, H, Y, ldy, n, epi);
+    }
+    sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, H, ldy, epi, g->pf_XS, g->pf_PART,
+                        (uint64_t)4 * g->pf_chunk * H, nw, g->cfg.rms_eps };
     return sgk_gemm(&a, g->stream);
 }
 
@@ -1304,8 +1318,7 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
     for (uint32_t i = 0; i < c->n_layers; i++) {
         glayer *L = &g->ls[i];
         const uint32_t in_rows = L->in.rows;
-        if ((e = sgk_rmsnorm_heads(g->pf_X, L->ln1, g->pf_Xn, H, n, H, c->rms_eps, s)) != hipSuccess) return e;
-        if ((e = gemm_rows(g, &L->in, g->pf_Xn, H, g->pf_IN, in_rows, n, SGK_EPI_STORE)) != hipSuccess) return e;
+        if ((e = gemm_rows_norm(g, &L->in, g->pf_X, L->ln1, g->pf_IN, in_rows, n, SGK_EPI_STORE)) != hipSuccess) return e;
         if (L->attn) {
             sgk_attn A = {0};
             A.q = g->pf_IN; A.kc = L->kc; A.vc = L->vc; A.m = g->pf_m; A.s = g->pf_s; A.acc = g->pf_acc;
@@ -1334,8 +1347,8 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
                                             c->head_v_dim, c->n_v_heads, n, c->rms_eps, s)) != hipSuccess) return e;
             if ((e = gemm_rows(g, &L->out, g->pf_G, g->value_dim, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;
         }
-        if ((e = sgk_rmsnorm_heads(g->pf_X, L->ln2, g->pf_Xn, H, n, H, c->rms_eps, s)) != hipSuccess) return e;
-        if ((e = gemm_rows(g, &L->gu, g->pf_Xn, H, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU)) != hipSuccess) return e;
+        if ((e = gemm_rows_norm(g, &L->gu, g->pf_X, L->ln2, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU)) != hipSuccess)
+            return e;
         if ((e = gemm_rows(g, &L->down, g->pf_FF, c->ffn_hidden, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;
     }
     return hipSuccess;

@@ -245,6 +245,8 @@ typedef struct {
     uint16_t *xs;            /* Q8 W: scratch of 2*N*K bf16 (X split into hi | lo), 16-byte aligned */
     float *part;             /* optional split-K partials (NULL: never split) */
     uint64_t part_cap;       /* floats in part */
+    const float *nw;         /* Q8 W only: RMSNorm X's rows first (weight nw, eps), or NULL */
+    float eps;
 } sgk_gemm_args;
 /* Q8 W needs K % 32 == 0, ldx % 4 == 0 and X 16-byte aligned. */
 hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s);

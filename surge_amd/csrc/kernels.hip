@@ -2829,6 +2829,36 @@ __global__ void __launch_bounds__(TPB) k_split_bf16(const float *X, uint32_t ldx
     }
 }
 
+// RMSNorm fused into the split: one workgroup per row n, the row's factor
+// r = 1/sqrt(mean(x^2) + eps) with k_rmsnorm_heads' arithmetic (the same
+// per-thread order and block_sum, then (x*r)*w), so the hi | lo it writes are
+// those of the split of k_rmsnorm_heads' output.
+__global__ void __launch_bounds__(TPB) k_split_bf16_rms(const float *X, uint32_t ldx, uint32_t N, uint32_t K,
+                                                        const float *w, float eps, uint16_t *xs) {
+    __shared__ float red[4];
+    const uint32_t n = blockIdx.x, t = threadIdx.x;
+    const float *xr = X + (size_t)n * ldx;
+    float ss = 0.0f;
+    for (uint32_t i = t; i < K; i += TPB) { const float v = xr[i]; ss = fmaf(v, v, ss); }
+    ss = block_sum(ss, red);
+    const float r = 1.0f / sqrtf(ss / (float)K + eps);
+    // the split itself four columns at a time (K % 32 == 0, rows 16-byte aligned)
+    uint16_t *hi = xs + (size_t)n * K, *lo = xs + (size_t)N * K + (size_t)n * K;
+    for (uint32_t i = 4 * t; i < K; i += 4 * TPB) {
+        const float4 x4 = *(const float4 *)(xr + i);
+        float v[4] = {x4.x * r, x4.y * r, x4.z * r, x4.w * r};
+        if (w) {
+            const float4 w4 = *(const float4 *)(w + i);
+            v[0] *= w4.x; v[1] *= w4.y; v[2] *= w4.z; v[3] *= w4.w;
+        }
+        const bf16x2 h01 = {(__bf16)v[0], (__bf16)v[1]}, h23 = {(__bf16)v[2], (__bf16)v[3]};
+        const bf16x2 l01 = {(__bf16)(v[0] - (float)h01[0]), (__bf16)(v[1] - (float)h01[1])};
+        const bf16x2 l23 = {(__bf16)(v[2] - (float)h23[0]), (__bf16)(v[3] - (float)h23[1])};
+        *(uint2 *)(hi + i) = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+        *(uint2 *)(lo + i) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+    }
+}
+
 #define GM_TN 128   // tokens per workgroup tile
 #define GM_TM 128   // weight rows per workgroup tile
 #define GM_LD 40    // LDS row of one 32-wide step, padded (bf16 elements, 80 bytes)
@@ -3083,13 +3113,17 @@ __global__ void __launch_bounds__(TPB) k_gemm_f32(const float *X, const float *W
 extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
     if (!a->N || !a->M || !a->K) return hipSuccess;
     if (a->epi == SGK_EPI_SWIGLU && (a->M & 1)) return hipErrorInvalidValue;
+    if (a->nw && !a->qs) return hipErrorInvalidValue;      // the fused RMSNorm is part of the Q8 split
     if (a->qs) {
         if (a->K % 32 || !a->xs || a->ldx % 4 || ((uintptr_t)a->X & 15) || ((uintptr_t)a->xs & 15))
             return hipErrorInvalidValue;
         const uint32_t k4 = a->K / 4;
         const uint64_t total = (uint64_t)a->N * k4;
         const uint32_t sg = (uint32_t)min((total + TPB - 1) / TPB, (uint64_t)4096);
-        hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
+        if (a->nw && ((uintptr_t)a->nw & 15)) return hipErrorInvalidValue;
+        if (a->nw) hipLaunchKernelGGL(k_split_bf16_rms, dim3(a->N), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->nw,
+                                      a->eps, a->xs);
+        else hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
         const uint32_t mb = (a->M + GM_TM - 1) / GM_TM, nb = (a->N + GM_TN - 1) / GM_TN;
         const uint32_t grid = 8 * nb * ((mb + 7) / 8), nblk = a->K / 32, tiles = mb * nb;
         // Workgroups run in rounds of `slots` (two resident per CU) and every
