@@ -1357,21 +1357,8 @@ __device__ __forceinline__ float fa_sum16(float v) {
     return v + lane_xor8(v);
 }
 
-// ---------------------------------------------------------------------------
-// Decode split-K partial on MFMA (head_dim 128 or 256, fused prep): the same
-// workgroup (split, kv head), prep, position store and output partials as
-// k_attn_partial, with each 64-key tile on v_mfma_f32_16x16x32_f16:
-//  - scores: A = the group's q rows (heads in rows 0..G-1 of a 16-row tile,
-//    split into f16 hi + lo), B = the tile's K straight from the f16 cache
-//    (wave w takes keys 16w..16w+15: lane holds 8 dims of one key per 32);
-//  - softmax per head over the tile as in k_attn_partial (scores and p in LDS);
-//  - P V: A = p (f16 hi + lo), B = V^T staged in LDS (each thread transposes 8
-//    keys x 8 dims in registers); wave w owns a quarter of the head dims, so
-//    each wave writes its own slice of the partial and no fold is needed.
-// ---------------------------------------------------------------------------
-
-#define MK 64       // keys per tile
-
+// K rows for the score MFMA's A operand: lane (li, lg) takes key `key`, dims
+// 8*lg.. of each 32 (16 B per load, one per 32-dim block)
 template <int HD>
 __device__ __forceinline__ void mf_load_k(v4u (&kr)[HD / 32], const uint16_t *kh, uint32_t key, uint32_t ps,
                                           uint32_t lg) {
@@ -1379,46 +1366,56 @@ __device__ __forceinline__ void mf_load_k(v4u (&kr)[HD / 32], const uint16_t *kh
 #pragma unroll
     for (int kb = 0; kb < HD / 32; kb++) kr[kb] = p[kb * 4];
 }
+// ---------------------------------------------------------------------------
+// Decode split-K partial with one independent key stream per wave (head_dim
+// 128 or 256, fused prep). Workgroup (split, kv head), the prep and the output
+// partials are those of k_attn_partial; in each 64-key round wave w takes keys
+// 16w..16w+15 and keeps its own running max, sum and output for the group's
+// heads, so the key loop has no barrier and no LDS traffic:
+//  - scores S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys straight
+//    from the f16 cache (lane li = key, 8 dims per 32), B = the group's q
+//    (column li = head li, f16 hi + lo); lane (li, lg) gets head li's scores
+//    of keys 4lg..4lg+3;
+//  - online softmax per head over the 4 lanes that share li (two cross-row
+//    steps); the output is kept transposed (O^T), so its rescale is in-lane;
+//  - O^T += V^T P^T on v_mfma_f32_16x16x16_f16: B = p in the score layout
+//    (f16 hi + lo), A = V^T built in registers: lane (li, lg) loads keys
+//    4lg..4lg+3 at dims 8li.. (and 8(li+16).. at head_dim 256) and packs one
+//    dim of its 4 keys per operand with v_perm;
+//  - the 4 waves' (max, sum, output) merge through LDS once, at the end.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+
+// keys key0..key0+3 (clamped at klast), dims 8li..8li+7 (+128 per q)
 template <int HD>
-__device__ __forceinline__ void mf_load_v(v4u (&vr)[8], const uint16_t *vh, uint32_t key0, uint32_t klast,
-                                          uint32_t ps, uint32_t vdc) {
+__device__ __forceinline__ void wv_load_v(v4u (&vr)[4][HD / 128], const uint16_t *vh, uint32_t key0, uint32_t klast,
+                                          uint32_t ps, uint32_t li) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const uint32_t key = min(key0 + j, klast);
-        vr[j] = *(const v4u *)(vh + (size_t)key * ps + vdc * 8);
-    }
-}
-// 8 keys x 8 dims (vr[j] = key j's dims) -> rows dims 0..7 of V^T, keys in order
-__device__ __forceinline__ void mf_store_vt(const v4u (&vr)[8], uint16_t *vt, uint32_t vdc, uint32_t vkg) {
+    for (int j = 0; j < 4; j++) {
+        const uint16_t *row = vh + (size_t)min(key0 + j, klast) * ps;
 #pragma unroll
-    for (int dd = 0; dd < 8; dd++) {
-        const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-        v4u out;
-#pragma unroll
-        for (int w = 0; w < 4; w++) out[w] = __builtin_amdgcn_perm(vr[2 * w + 1][dd >> 1], vr[2 * w][dd >> 1], sel);
-        *(v4u *)&vt[(vdc * 8 + dd) * FA_PLD + vkg * 8] = out;
+        for (int q = 0; q < HD / 128; q++) vr[j][q] = *(const v4u *)(row + (li + 16 * q) * 8);
     }
 }
 
 template <int HD>
-__global__ void __launch_bounds__(TPB) k_attn_partial_mf(sgk_attn a) {
-    static_assert(HD == 128 || HD == 256, "MFMA decode partial takes head_dim 128 or 256");
-    constexpr int NKB = HD / 32, NTW = HD / 64;       // score k-blocks; output 16-dim tiles per wave
-    constexpr int VDC = HD / 8;                       // V staging: 8-dim chunks (threads t < 8*VDC)
+__global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))) k_attn_partial_wv(sgk_attn a) {
+    static_assert(HD == 128 || HD == 256, "wave-stream decode partial takes head_dim 128 or 256");
+    constexpr int NKB = HD / 32, NQ = HD / 128, NO = HD / 16;   // score k-blocks; V chunks per lane; O^T tiles
     constexpr int QPT = (GMAX * HD + TPB - 1) / TPB, KOFF = QPT * TPB;
+    constexpr int OWS = HD + 4;                                  // merge row stride (floats)
+    constexpr int BIG = (4 * GMAX * OWS > KOFF + HD) ? 4 * GMAX * OWS : KOFF + HD;
     __shared__ __align__(16) float qsh[GMAX * HD];
-    __shared__ __align__(16) float sc[GMAX][MK];
-    __shared__ float mrun[GMAX], srun[GMAX], alpha[GMAX], rn[GMAX + 1];
-    __shared__ __align__(16) uint16_t vt[HD * FA_PLD];
-    // the raw q rows and k row of the prep live in the V^T tile's space: the
-    // prep is done (and a barrier passed) before the first tile is staged
-    static_assert((KOFF + HD) * sizeof(float) <= sizeof(vt), "raw rows exceed the V^T tile");
-    float *raw = (float *)vt;
+    __shared__ __align__(16) float big[BIG];                     // prep: raw q|k rows; end: the waves' outputs
+    __shared__ float mw[4][GMAX], lw[4][GMAX], rn[GMAX + 1];
     __shared__ float cs_s[HD], qn_s[HD], kn_s[HD];
     __shared__ __align__(16) uint16_t knew[HD], vnew[HD];
+    float *raw = big;
 
     const uint32_t G = a.n_heads / a.n_kv, n_kv = a.n_kv, z = blockIdx.z;
-    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x, lane = t & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t li = lane & 15, lg = lane >> 4, h0 = hk * G;
     const float *q = a.q + (size_t)z * a.q_tok;
 
@@ -1440,16 +1437,15 @@ __global__ void __launch_bounds__(TPB) k_attn_partial_mf(sgk_attn a) {
     const uint32_t t0 = (uint32_t)((uint64_t)i * seq / ns), t1 = (uint32_t)((uint64_t)(i + 1) * seq / ns);
     const uint32_t klast = t1 ? t1 - 1 : 0;
     const size_t zoff = (size_t)z * a.n_heads * a.max_splits;
-    const uint32_t vkg = t / VDC, vdc = t % VDC;      // V staging role: keys 8*vkg.., dims 8*vdc..
-    const bool vst = vkg < MK / 8;
 
-    // 2. the position's cos|sin entry, then the first tile's K and V
+    // 2. the position's cos|sin entry, then this wave's first 16 keys of K and V
     const float cs0 = (a.cs + (size_t)pos * a.rope_dim)[min(td, a.rope_dim - 1)];
     __builtin_amdgcn_sched_barrier(0);
-    v4u kr[NKB], vr[8];
+    v4u kr[NKB], vr[4][NQ];
     const uint16_t *kch = a.kc + (size_t)hk * a.kv_hs, *vch = a.vc + (size_t)hk * a.kv_hs;
-    mf_load_k<HD>(kr, kch, min(t0 + wave * 16 + li, klast), a.kv_ps, lg);
-    mf_load_v<HD>(vr, vch, t0 + (vst ? vkg : 0) * 8, klast, a.kv_ps, vdc);
+    const uint32_t base0 = t0 + wave * 16;
+    mf_load_k<HD>(kr, kch, min(base0 + li, klast), a.kv_ps, lg);
+    wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
 
     // 3. prep: q_norm + RoPE of the group's heads into qsh; the split holding
     //    the position stores that token's K (k_norm + RoPE) and raw V as f16
@@ -1485,21 +1481,21 @@ __global__ void __launch_bounds__(TPB) k_attn_partial_mf(sgk_attn a) {
             vnew[d] = vh;
         }
     }
-    if (t < G) { mrun[t] = -INFINITY; srun[t] = 0.0f; }
     __syncthreads();
-    // the first tile was requested before the store: take the position's row from LDS
-    if (kv_writer && pos - t0 < (uint32_t)MK) {
-        if (t0 + wave * 16 + li == pos) {
+    // the first keys were requested before the store: take the position's row from LDS
+    if (kv_writer && pos - t0 < 64u) {
+        if (base0 + li == pos) {
 #pragma unroll
             for (int kb = 0; kb < NKB; kb++) kr[kb] = ((const v4u *)(knew + lg * 8))[kb * 4];
         }
-        if (vst) {
 #pragma unroll
-            for (int j = 0; j < 8; j++)
-                if (t0 + vkg * 8 + j == pos) vr[j] = *(const v4u *)(vnew + vdc * 8);
-        }
+        for (int j = 0; j < 4; j++)
+            if (base0 + 4 * lg + j == pos) {
+#pragma unroll
+                for (int qq = 0; qq < NQ; qq++) vr[j][qq] = *(const v4u *)(vnew + (li + 16 * qq) * 8);
+            }
     }
-    // q fragments: row li = head li (zero past the group), dims 8*lg.. of each 32
+    // q as the B operand: column li = head li (zero past the group), dims 8*lg.. of each 32
     f16x8 qh[NKB], ql[NKB];
 #pragma unroll
     for (int kb = 0; kb < NKB; kb++) {
@@ -1508,90 +1504,106 @@ __global__ void __launch_bounds__(TPB) k_attn_partial_mf(sgk_attn a) {
         for (int e = 0; e < 8; e++) xv[e] = li < G ? qsh[li * HD + kb * 32 + lg * 8 + e] : 0.0f;
         fa_split8(xv, qh[kb], ql[kb]);
     }
-    f32x4 o[NTW];
-#pragma unroll
-    for (int n = 0; n < NTW; n++) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    for (uint32_t ts = t0; ts < t1; ts += MK) {
-        const uint32_t nk = min((uint32_t)MK, t1 - ts);
-        if (vst) mf_store_vt(vr, vt, vdc, vkg);
-        // scores of keys 16*wave + li for the 16 rows (heads)
-        f32x4 s4 = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4 o[NO];
+#pragma unroll
+    for (int n = 0; n < NO; n++) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const uint32_t nr = (t1 - t0 + 63) / 64;
+    for (uint32_t r = 0; r < nr; r++) {
+        const uint32_t base = t0 + r * 64 + wave * 16;
+        f32x4 sh = (f32x4){0.f, 0.f, 0.f, 0.f}, sl = sh;
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
             const f16x8 bk = __builtin_bit_cast(f16x8, kr[kb]);
-            s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kb], bk, s4, 0, 0, 0);
-            s4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[kb], bk, s4, 0, 0, 0);
+            sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk, qh[kb], sh, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk, ql[kb], sl, 0, 0, 0);
         }
-        // the next tile (past the split: clamped, unused); vr was staged above
-        mf_load_k<HD>(kr, kch, min(ts + MK + wave * 16 + li, klast), a.kv_ps, lg);
-        mf_load_v<HD>(vr, vch, ts + MK + (vst ? vkg : 0) * 8, klast, a.kv_ps, vdc);
-        {
-            const uint32_t key = wave * 16 + li;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t h = lg * 4 + e;
-                if (h < G) sc[h][key] = key < nk ? s4[e] * a.scale : -INFINITY;
-            }
-        }
-        __syncthreads();
-        // softmax: one wave per head over the tile (k_attn_partial's rules)
-        for (uint32_t h = wave; h < G; h += TPB / 64) {
-            const float v = sc[h][lane];
-            const float tm = wave_max(v);
-            const float mold = mrun[h];
-            const float mnew = fmaxf(mold, tm);
-            const float p = lane < nk ? expf(v - mnew) : 0.0f;
-            sc[h][lane] = p;
-            const float ps = wave_sum(p);
-            if (lane == 0) {
-                const float al = (mold == -INFINITY) ? 0.0f : expf(mold - mnew);
-                alpha[h] = al;
-                mrun[h] = mnew;
-                srun[h] = srun[h] * al + ps;
-            }
-        }
-        __syncthreads();
-        // p fragments: row li = head, keys 8*lg.. of each 32
-        f16x8 ph[2], pl[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            float xv[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) xv[e] = li < G ? sc[li][kb * 32 + lg * 8 + e] : 0.0f;
-            fa_split8(xv, ph[kb], pl[kb]);
-        }
+        // the next round's K (past the split: clamped, unused), issued here
+        // so that it is in flight during the softmax and P V
+        mf_load_k<HD>(kr, kch, min(base + 64 + li, klast), a.kv_ps, lg);
+        __builtin_amdgcn_sched_barrier(0);
+        float p[4], tm = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const uint32_t h = lg * 4 + e;
-            const float al = h < G ? alpha[h] : 0.0f;
+            const float sv = (sh[e] + sl[e]) * a.scale;
+            p[e] = base + 4 * lg + e < t1 ? sv : -INFINITY;
+            tm = fmaxf(tm, p[e]);
+        }
+        tm = fmaxf(tm, lane_xor16(tm));
+        tm = fmaxf(tm, lane_xor32(tm));
+        const float mnew = fmaxf(m_run, tm);
+        const float al = m_run == -INFINITY ? 0.0f : expf(m_run - mnew);
+        float ps = 0.0f;
 #pragma unroll
-            for (int n = 0; n < NTW; n++) o[n][e] *= al;
+        for (int e = 0; e < 4; e++) {
+            p[e] = p[e] == -INFINITY ? 0.0f : expf(p[e] - mnew);
+            ps += p[e];
+        }
+        ps += lane_xor16(ps);
+        ps += lane_xor32(ps);
+        l_run = l_run * al + ps;
+        m_run = mnew;
+        f16x4 phi, plo;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const _Float16 hv = (_Float16)p[e];
+            phi[e] = hv;
+            plo[e] = (_Float16)(p[e] - (float)hv);
         }
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
+        for (int n = 0; n < NO; n++) o[n] *= al;
+        // O^T tile m: rows = dims 8(row + 16(m/8)) + m%8, columns = heads
 #pragma unroll
-            for (int n = 0; n < NTW; n++) {
-                const uint32_t dim = (wave * NTW + n) * 16 + li;
-                const f16x8 bv = *(const f16x8 *)&vt[dim * FA_PLD + kb * 32 + lg * 8];
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[kb], bv, o[n], 0, 0, 0);
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[kb], bv, o[n], 0, 0, 0);
+        for (int m = 0; m < NO; m++) {
+            const int qq = m / 8, w = (m % 8) / 2;
+            const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
+            const v2u pk = (v2u){__builtin_amdgcn_perm(vr[1][qq][w], vr[0][qq][w], sel),
+                                 __builtin_amdgcn_perm(vr[3][qq][w], vr[2][qq][w], sel)};
+            const f16x4 av = __builtin_bit_cast(f16x4, pk);
+            o[m] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, phi, o[m], 0, 0, 0);
+            o[m] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, plo, o[m], 0, 0, 0);
+        }
+        wv_load_v<HD>(vr, vch, base + 64 + 4 * lg, klast, a.kv_ps, li);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // merge the waves: lane (li, lg) holds head li's max / sum and O^T rows
+    // 4lg+e; each wave scales its rows by its weight exp(m_w - max) once, then
+    // the rows are summed in wave order
+    if (li < G && lg == 0) {
+        mw[wave][li] = m_run;
+        lw[wave][li] = l_run;
+    }
+    __syncthreads();
+    float *ow = big;
+    if (li < G) {
+        const float mx = fmaxf(fmaxf(mw[0][li], mw[1][li]), fmaxf(mw[2][li], mw[3][li]));
+        const float wg = m_run == -INFINITY ? 0.0f : expf(m_run - mx);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int qq = 0; qq < NQ; qq++) {
+                float *dst = ow + (wave * GMAX + li) * OWS + 8 * (4 * lg + e + 16 * qq);
+                *(f32x4 *)dst = (f32x4){o[qq * 8 + 0][e], o[qq * 8 + 1][e], o[qq * 8 + 2][e], o[qq * 8 + 3][e]} * wg;
+                *(f32x4 *)(dst + 4) = (f32x4){o[qq * 8 + 4][e], o[qq * 8 + 5][e], o[qq * 8 + 6][e], o[qq * 8 + 7][e]} * wg;
             }
-        __syncthreads();
-    }
-    // partials: lane holds heads 4*lg+e, dims (wave*NTW + n)*16 + li
+        if (wave == 0 && lg == 0) {
+            float sum = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const uint32_t h = lg * 4 + e;
-        if (h >= G) continue;
-        float *dst = a.acc + (zoff + (size_t)(h0 + h) * ns + i) * HD;
-#pragma unroll
-        for (int n = 0; n < NTW; n++) dst[(wave * NTW + n) * 16 + li] = o[n][e];
+            for (int w = 0; w < 4; w++)
+                if (mw[w][li] != -INFINITY) sum += expf(mw[w][li] - mx) * lw[w][li];
+            const size_t oi = zoff + (size_t)(h0 + li) * ns + i;
+            a.m[oi] = mx;
+            a.s[oi] = sum;
+        }
     }
-    if (t < G) {
-        const size_t oi = zoff + (size_t)(h0 + t) * ns + i;
-        a.m[oi] = mrun[t];
-        a.s[oi] = srun[t];
+    __syncthreads();
+    for (uint32_t e = t; e < G * HD / 4; e += TPB) {
+        const uint32_t h = e / (HD / 4), d = (e % (HD / 4)) * 4;
+        const float *src = ow + h * OWS + d;
+        const f32x4 acc = ((*(const f32x4 *)src + *(const f32x4 *)(src + GMAX * OWS)) +
+                           *(const f32x4 *)(src + 2 * GMAX * OWS)) + *(const f32x4 *)(src + 3 * GMAX * OWS);
+        *(f32x4 *)(a.acc + (zoff + (size_t)(h0 + h) * ns + i) * HD + d) = acc;
     }
 }
 
@@ -1610,9 +1622,10 @@ extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
     const uint32_t gx = a->steps ? a->max_splits : a->n_splits;
     if (!gx || !a->ntok) return hipSuccess;
     dim3 grid(gx, a->n_kv, a->ntok);
-    if (a->fuse_prep && (a->hd == 128 || a->hd == 256) && getenv_mf()) {
-        if (a->hd == 256) hipLaunchKernelGGL(k_attn_partial_mf<256>, grid, dim3(TPB), 0, s, kv_resolved(a));
-        else hipLaunchKernelGGL(k_attn_partial_mf<128>, grid, dim3(TPB), 0, s, kv_resolved(a));
+    // the wave-stream kernel stores its output rows as float4
+    if (a->fuse_prep && (a->hd == 128 || a->hd == 256) && ((uintptr_t)a->acc & 15) == 0 && getenv_mf()) {
+        if (a->hd == 256) hipLaunchKernelGGL(k_attn_partial_wv<256>, grid, dim3(TPB), 0, s, kv_resolved(a));
+        else hipLaunchKernelGGL(k_attn_partial_wv<128>, grid, dim3(TPB), 0, s, kv_resolved(a));
         return hipGetLastError();
     }
 #define HDCASE(H) case H: hipLaunchKernelGGL((k_attn_partial<H, 64>), grid, dim3(TPB), 0, s, kv_resolved(a)); break
