@@ -194,7 +194,10 @@ def traffic(fetch_csv, write_csv, kernel, calib_bytes, algo_bytes):
 
 def hbm(fetch_csv, write_csv, trace_csv, calib_bytes, peak_gbs=8000.0):
     def per_kernel(path, counter):
-        vals, copies = defaultdict(list), []
+        # counters of the decode steps only (from the third k_embed to the
+        # last k_step_advance, in dispatch order), so kernels that prefill also
+        # launches are not averaged with their prefill dispatches
+        vals, copies, rows = defaultdict(list), [], []
         for r in csv.DictReader(open(path)):
             if r.get("Counter_Name", counter) != counter:
                 continue
@@ -202,7 +205,14 @@ def hbm(fetch_csv, write_csv, trace_csv, calib_bytes, peak_gbs=8000.0):
             if name == "__amd_rocclr_copyBuffer":
                 copies.append(float(r["Counter_Value"]))
             else:
-                vals[name].append(float(r["Counter_Value"]))
+                rows.append((int(r.get("Dispatch_Id", len(rows))), name, float(r["Counter_Value"])))
+        rows.sort()
+        embeds = [i for i, x in enumerate(rows) if x[1] == "k_embed"]
+        ends = [i for i, x in enumerate(rows) if x[1] == "k_step_advance"]
+        if len(embeds) >= 3 and ends:
+            rows = rows[embeds[2]:ends[-1] + 1]
+        for _, name, v in rows:
+            vals[name].append(v)
         scale = calib_bytes / (max(copies) * 1024.0)
         return {k: sum(v) / len(v) * 1024.0 * scale for k, v in vals.items()}, scale
     fb, fs = per_kernel(fetch_csv, "FETCH_SIZE")
