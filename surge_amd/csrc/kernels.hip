@@ -1399,9 +1399,19 @@ __device__ __forceinline__ void wv_load_v(v4u (&vr)[4][HD / 128], const uint16_t
     }
 }
 
-template <int HD>
+// RKB = 0: q_norm + RoPE of the group's heads through LDS (any rope_dim), as in
+// k_attn_partial. RKB = 1 or 2 (rope_dim = 64*RKB): each lane preps its own
+// q fragment in registers. The 4 lanes that share li hold all of head li's
+// dims (8 per 32), so the sum of squares is two cross-row steps, and a
+// rotated dim's partner (d +- rope_dim/2) sits in the same lane, RKB k-blocks
+// away: no LDS and no barrier, except in the split that stores the new K.
+template <int HD, int RKB>
 __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))) k_attn_partial_wv(sgk_attn a) {
     static_assert(HD == 128 || HD == 256, "wave-stream decode partial takes head_dim 128 or 256");
+    static_assert(RKB >= 0 && RKB <= 2 && 2 * RKB <= HD / 32, "register prep takes rope_dim 64 or 128");
+    // the first keys' K is requested before the prep, except where the
+    // register prep's values leave no room for it (head_dim 256, rope 128)
+    constexpr bool EARLY_K = !(HD == 256 && RKB == 2);
     constexpr int NKB = HD / 32, NQ = HD / 128, NO = HD / 16;   // score k-blocks; V chunks per lane; O^T tiles
     constexpr int QPT = (GMAX * HD + TPB - 1) / TPB, KOFF = QPT * TPB;
     constexpr int OWS = HD + 4;                                  // merge row stride (floats)
@@ -1420,16 +1430,28 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
     const float *q = a.q + (size_t)z * a.q_tok;
 
     // 1. position-independent loads first (as in k_attn_partial)
-    float qv[QPT];
+    float qv[RKB ? 1 : QPT];
+    f32x4 qx[NKB][2], qw[NKB][2];     // register prep: head min(li, G-1)'s dims 32kb + 8lg.., q_norm weights
+    if constexpr (RKB == 0) {
 #pragma unroll
-    for (int k = 0; k < QPT; k++) {
-        const uint32_t e = min(t + k * TPB, G * HD - 1);
-        qv[k] = q[(size_t)(h0 + e / HD) * a.q_stride + e % HD];
+        for (int k = 0; k < QPT; k++) {
+            const uint32_t e = min(t + k * TPB, G * HD - 1);
+            qv[k] = q[(size_t)(h0 + e / HD) * a.q_stride + e % HD];
+        }
+    } else {
+        const float *qrow = q + (size_t)(h0 + min(li, G - 1)) * a.q_stride + lg * 8;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                qx[kb][c] = *(const f32x4 *)(qrow + kb * 32 + c * 4);
+                qw[kb][c] = *(const f32x4 *)(a.qn + kb * 32 + lg * 8 + c * 4);
+            }
     }
     const uint32_t td = min(t, (uint32_t)HD - 1);
     const float *krow = q + (size_t)a.n_heads * a.q_stride + (size_t)hk * HD;
     const float *vrow = krow + (size_t)n_kv * HD;
-    const float qn0 = a.qn[td], kn0 = a.kn[td], kr0 = krow[td], vr0 = vrow[td];
+    const float qn0 = RKB ? 0.0f : a.qn[td], kn0 = a.kn[td], kr0 = krow[td], vr0 = vrow[td];
 
     const uint32_t pos = a.steps[z].pos, seq = pos + 1;
     const uint32_t ns = dev_splits(seq, a.prefill, a.split_cap);
@@ -1438,71 +1460,130 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint32_t klast = t1 ? t1 - 1 : 0;
     const size_t zoff = (size_t)z * a.n_heads * a.max_splits;
 
-    // 2. the position's cos|sin entry, then this wave's first 16 keys of K and V
-    const float cs0 = (a.cs + (size_t)pos * a.rope_dim)[min(td, a.rope_dim - 1)];
+    // 2. the position's cos|sin entry (register prep: cos and sin of the
+    //    lane's rotated dims), then this wave's first 16 keys of K and V
+    const float *csp = a.cs + (size_t)pos * a.rope_dim;
+    const float cs0 = csp[min(td, a.rope_dim - 1)];
+    f32x4 rc[RKB ? RKB : 1][2], rs[RKB ? RKB : 1][2];
+    if constexpr (RKB > 0) {
+#pragma unroll
+        for (int kb = 0; kb < RKB; kb++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                rc[kb][c] = *(const f32x4 *)(csp + kb * 32 + lg * 8 + c * 4);
+                rs[kb][c] = *(const f32x4 *)(csp + RKB * 32 + kb * 32 + lg * 8 + c * 4);
+            }
+    }
     __builtin_amdgcn_sched_barrier(0);
     v4u kr[NKB], vr[4][NQ];
     const uint16_t *kch = a.kc + (size_t)hk * a.kv_hs, *vch = a.vc + (size_t)hk * a.kv_hs;
     const uint32_t base0 = t0 + wave * 16;
-    mf_load_k<HD>(kr, kch, min(base0 + li, klast), a.kv_ps, lg);
-    wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
+    if constexpr (EARLY_K) mf_load_k<HD>(kr, kch, min(base0 + li, klast), a.kv_ps, lg);
+    if constexpr (RKB == 0) wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
 
-    // 3. prep: q_norm + RoPE of the group's heads into qsh; the split holding
-    //    the position stores that token's K (k_norm + RoPE) and raw V as f16
+    // 3. prep: q_norm + RoPE of the group's heads; the split holding the
+    //    position stores that token's K (k_norm + RoPE) and raw V as f16
     const bool kv_writer = i == ns - 1;
+    if (RKB == 0 || kv_writer) {
+        if constexpr (RKB == 0) {
 #pragma unroll
-    for (int k = 0; k < QPT; k++) raw[t + k * TPB] = qv[k];
-    qn_s[td] = qn0;
-    raw[KOFF + td] = kr0;
-    kn_s[td] = kn0;
-    __syncthreads();
-    cs_s[td] = td < a.rope_dim ? cs0 : 0.0f;
-    for (uint32_t h = wave; h <= G; h += TPB / 64) {
-        if (h == G && !kv_writer) break;
-        const float *x = h < G ? raw + h * HD : raw + KOFF;
-        float ss = 0.0f;
-        for (uint32_t d = lane; d < HD; d += 64) ss = fmaf(x[d], x[d], ss);
-        ss = wave_sum(ss);
-        if (lane == 0) rn[h] = 1.0f / sqrtf(ss / (float)HD + a.eps);
-    }
-    __syncthreads();
-    for (uint32_t e = t; e < G * HD; e += TPB) {
-        const uint32_t h = e / HD, d = e % HD;
-        qsh[e] = prep_elem(raw + h * HD, rn[h], qn_s, cs_s, d, a.rope_dim);
-    }
-    if (kv_writer) {
-        const size_t at = kv_at(a, pos, hk);
-        for (uint32_t d = t; d < HD; d += TPB) {
-            const uint16_t kh = f2h(prep_elem(raw + KOFF, rn[G], kn_s, cs_s, d, a.rope_dim));
-            const uint16_t vh = f2h(vr0);
-            ((uint16_t *)a.kc)[at + d] = kh;
-            ((uint16_t *)a.vc)[at + d] = vh;
-            knew[d] = kh;
-            vnew[d] = vh;
+            for (int k = 0; k < QPT; k++) raw[t + k * TPB] = qv[k];
+            qn_s[td] = qn0;
         }
+        raw[KOFF + td] = kr0;
+        kn_s[td] = kn0;
+        cs_s[td] = td < a.rope_dim ? cs0 : 0.0f;
+        __syncthreads();
+        for (uint32_t h = RKB ? G + wave : wave; h <= G; h += TPB / 64) {
+            if (h == G && !kv_writer) break;
+            const float *x = h < G ? raw + h * HD : raw + KOFF;
+            float ss = 0.0f;
+            for (uint32_t d = lane; d < HD; d += 64) ss = fmaf(x[d], x[d], ss);
+            ss = wave_sum(ss);
+            if (lane == 0) rn[h] = 1.0f / sqrtf(ss / (float)HD + a.eps);
+        }
+        __syncthreads();
+        if constexpr (RKB == 0) {
+            for (uint32_t e = t; e < G * HD; e += TPB) {
+                const uint32_t h = e / HD, d = e % HD;
+                qsh[e] = prep_elem(raw + h * HD, rn[h], qn_s, cs_s, d, a.rope_dim);
+            }
+        }
+        if (kv_writer) {
+            const size_t at = kv_at(a, pos, hk);
+            for (uint32_t d = t; d < HD; d += TPB) {
+                const uint16_t kh = f2h(prep_elem(raw + KOFF, rn[G], kn_s, cs_s, d, a.rope_dim));
+                const uint16_t vh = f2h(vr0);
+                ((uint16_t *)a.kc)[at + d] = kh;
+                ((uint16_t *)a.vc)[at + d] = vh;
+                knew[d] = kh;
+                vnew[d] = vh;
+            }
+        }
+        __syncthreads();
     }
-    __syncthreads();
     // the first keys were requested before the store: take the position's row from LDS
     if (kv_writer && pos - t0 < 64u) {
-        if (base0 + li == pos) {
+        if (EARLY_K && base0 + li == pos) {
 #pragma unroll
             for (int kb = 0; kb < NKB; kb++) kr[kb] = ((const v4u *)(knew + lg * 8))[kb * 4];
         }
+        if constexpr (RKB == 0) {
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (base0 + 4 * lg + j == pos) {
+            for (int j = 0; j < 4; j++)
+                if (base0 + 4 * lg + j == pos) {
 #pragma unroll
-                for (int qq = 0; qq < NQ; qq++) vr[j][qq] = *(const v4u *)(vnew + (li + 16 * qq) * 8);
-            }
+                    for (int qq = 0; qq < NQ; qq++) vr[j][qq] = *(const v4u *)(vnew + (li + 16 * qq) * 8);
+                }
+        }
     }
     // q as the B operand: column li = head li (zero past the group), dims 8*lg.. of each 32
     f16x8 qh[NKB], ql[NKB];
+    if constexpr (RKB == 0) {
 #pragma unroll
-    for (int kb = 0; kb < NKB; kb++) {
-        float xv[8];
+        for (int kb = 0; kb < NKB; kb++) {
+            float xv[8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) xv[e] = li < G ? qsh[li * HD + kb * 32 + lg * 8 + e] : 0.0f;
-        fa_split8(xv, qh[kb], ql[kb]);
+            for (int e = 0; e < 8; e++) xv[e] = li < G ? qsh[li * HD + kb * 32 + lg * 8 + e] : 0.0f;
+            fa_split8(xv, qh[kb], ql[kb]);
+        }
+    } else {
+        // prep_elem's arithmetic on the lane's dims: x * r * w, then the half-split rotation
+        float ss = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) ss = fmaf(qx[kb][e / 4][e % 4], qx[kb][e / 4][e % 4], ss);
+        ss += lane_xor16(ss);
+        ss += lane_xor32(ss);
+        const float rq = 1.0f / sqrtf(ss / (float)HD + a.eps);
+        float y[NKB][8];
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) y[kb][e] = (qx[kb][e / 4][e % 4] * rq) * qw[kb][e / 4][e % 4];
+#pragma unroll
+        for (int kb = 0; kb < RKB; kb++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float c = rc[kb][e / 4][e % 4], sn = rs[kb][e / 4][e % 4];
+                const float lo = y[kb][e], hi = y[kb + RKB][e];
+                y[kb][e] = lo * c - hi * sn;
+                y[kb + RKB][e] = lo * sn + hi * c;
+            }
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            float xv[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) xv[e] = li < G ? y[kb][e] : 0.0f;
+            fa_split8(xv, qh[kb], ql[kb]);
+        }
+        // the first keys' V (and K where it waited), requested after the
+        // prep, so after the new row's store and barrier in the split that
+        // holds the position
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (!EARLY_K) mf_load_k<HD>(kr, kch, min(base0 + li, klast), a.kv_ps, lg);
+        wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
     }
 
     float m_run = -INFINITY, l_run = 0.0f;
@@ -1624,8 +1705,20 @@ extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
     dim3 grid(gx, a->n_kv, a->ntok);
     // the wave-stream kernel stores its output rows as float4
     if (a->fuse_prep && (a->hd == 128 || a->hd == 256) && ((uintptr_t)a->acc & 15) == 0 && getenv_mf()) {
-        if (a->hd == 256) hipLaunchKernelGGL(k_attn_partial_wv<256>, grid, dim3(TPB), 0, s, kv_resolved(a));
-        else hipLaunchKernelGGL(k_attn_partial_wv<128>, grid, dim3(TPB), 0, s, kv_resolved(a));
+        // register prep: rope_dim 64 or 128 and 16-byte aligned q rows, q_norm weights and cos|sin table
+        const bool al16 = ((uintptr_t)a->q & 15) == 0 && (a->q_stride & 3) == 0 && (a->q_tok & 3) == 0 &&
+                          ((uintptr_t)a->qn & 15) == 0 && ((uintptr_t)a->cs & 15) == 0;
+        const int rkb = (al16 && (a->rope_dim == 64 || a->rope_dim == 128)) ? (int)(a->rope_dim / 64) : 0;
+        const sgk_attn b = kv_resolved(a);
+        if (a->hd == 256) {
+            if (rkb == 1) hipLaunchKernelGGL((k_attn_partial_wv<256, 1>), grid, dim3(TPB), 0, s, b);
+            else if (rkb == 2) hipLaunchKernelGGL((k_attn_partial_wv<256, 2>), grid, dim3(TPB), 0, s, b);
+            else hipLaunchKernelGGL((k_attn_partial_wv<256, 0>), grid, dim3(TPB), 0, s, b);
+        } else {
+            if (rkb == 1) hipLaunchKernelGGL((k_attn_partial_wv<128, 1>), grid, dim3(TPB), 0, s, b);
+            else if (rkb == 2) hipLaunchKernelGGL((k_attn_partial_wv<128, 2>), grid, dim3(TPB), 0, s, b);
+            else hipLaunchKernelGGL((k_attn_partial_wv<128, 0>), grid, dim3(TPB), 0, s, b);
+        }
         return hipGetLastError();
     }
 #define HDCASE(H) case H: hipLaunchKernelGGL((k_attn_partial<H, 64>), grid, dim3(TPB), 0, s, kv_resolved(a)); break

@@ -269,6 +269,41 @@ def test_hd128_decode_vs_oracle_and_prefill_vs_serial(gpu):
     syn.close()
 
 
+ROPE_CASES = [(256, 128), (256, 32), (128, 64), (128, 128)]
+
+
+@pytest.mark.parametrize("hd,rope", ROPE_CASES, ids=[f"HD{h}-rope{r}" for h, r in ROPE_CASES])
+def test_decode_partial_q_prep_variants_vs_oracle(gpu, monkeypatch, hd, rope):
+    """The MFMA decode partial preps q (q_norm + RoPE) in each lane's
+    registers when rope_dim is 64 or 128 and through LDS otherwise; the
+    head_dim 256 / rope 64 and head_dim 128 / rope 32 pairs run in the tests
+    above, these are the other four. SURGE_SPLITK_GQA_CAP=4 puts about 70
+    keys in each split at 280 positions, so every split walks two 64-key
+    rounds, the second requested after the new row's store. Logits within
+    1e-3 of the oracle and the same argmax at sampled positions."""
+    cfg = dict(HD128, head_dim=hd, rope_dim=rope, n_heads=8 if hd == 256 else 12)
+    syn = S.Synth(cfg, S.SG_T_Q8_0, seed=21 + hd + rope)
+    gpu.load_model(syn.model)
+    monkeypatch.setenv("SURGE_SPLITK_GQA_CAP", "4")
+    gpu.state_new(300)
+    assert gpu.n_splits_at(279) == 4
+    rng = np.random.default_rng(hd + rope)
+    ids = rng.integers(0, cfg["vocab"], 280).tolist()
+    rm = O.RefModel(O.oracle(), syn.model, 300, kv_f16=True)
+    worst = 0.0
+    for p, t in enumerate(ids):
+        g = gpu.forward(t, p)
+        o = rm.forward(t, p)
+        if p % 19 == 0 or p >= 270:
+            worst = max(worst, rel(g, o))
+            assert np.argmax(g) == np.argmax(o), f"argmax differs at position {p}"
+    rm.close()
+    monkeypatch.delenv("SURGE_SPLITK_GQA_CAP")
+    gpu.state_new(64)
+    syn.close()
+    assert worst < 1e-3, worst
+
+
 WIDE = dict(n_layers=4, n_heads=8, n_kv_heads=2, head_dim=64, hidden=512, ffn_hidden=1024,
             vocab=700, rope_theta=1e6, rms_eps=1e-6, tied_embeddings=False, rope_dim=32,
             full_attn_interval=2, n_k_heads=4, n_v_heads=8, head_k_dim=64, head_v_dim=64,
