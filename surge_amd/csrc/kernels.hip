@@ -574,13 +574,22 @@ static int device_cus() {
 // Workgroups of the prefill GEMM resident at once: two per CU (its LDS).
 // SURGE_GEMM_SLOTS (decimal, >= 1) overrides it, for tests that exercise the
 // round split on small shapes.
-static uint32_t gemm_slots() {
+// The prefill GEMM runs warp-specialised (k_gemm_q8_ws) unless SURGE_GEMM_WS
+// is "0" (k_gemm_q8_mfma: same tiles and bits, for A/B measurement); read at
+// every launch. Two workgroups are resident per CU either way (256 threads
+// each, or 512 for the warp-specialised form).
+static bool gemm_ws() {
+    const char *e = getenv("SURGE_GEMM_WS");
+    return !(e && e[0] == '0' && !e[1]);
+}
+static uint32_t gemm_slots(bool ws) {
     const char *e = getenv("SURGE_GEMM_SLOTS");
     if (e && *e) {
         char *end = NULL;
         const unsigned long v = strtoul(e, &end, 10);
         if (end && !*end && v >= 1 && v <= 65536) return (uint32_t)v;
     }
+    (void)ws;
     return 2 * (uint32_t)device_cus();
 }
 
@@ -3136,6 +3145,178 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
             }
 }
 
+// Warp-specialised form of k_gemm_q8_mfma: one 512-thread workgroup per CU
+// and the same 128x128 tile, fragments, MFMA order and dequantisation, so the
+// same bits. Waves 0-3 (consumers) own the accumulators and, in K step s,
+// only read fragments of LDS buffer s%2 and issue MFMAs; waves 4-7
+// (producers) meanwhile dequantise block s+1's weights and stage them and its
+// X into buffer (s+1)%2. One barrier per step, so one group's MFMAs overlap
+// the other's VALU and LDS work on every SIMD. A step is short, so the
+// producers keep four register sets: block b's X and raw weights sit in set
+// (b - kb0) % 4, X requested two steps and the weights four steps before
+// they are staged.
+#define GW_TPB 512
+struct gw_set {
+    v4u x[4];        // X hi (2) and lo (2) of the staging row
+    v4u w;           // 16 raw int8 weights
+    uint32_t d;      // block scale
+};
+__device__ __forceinline__ void gw_request_x(gw_set &st, const v4u *xhr, const v4u *xlr, uint32_t blk) {
+#pragma unroll
+    for (int u = 0; u < 2; u++) { st.x[u] = xhr[blk * 4 + u]; st.x[2 + u] = xlr[blk * 4 + u]; }
+}
+__device__ __forceinline__ void gw_request_w(gw_set &st, const v4u *wrow, const uint16_t *drow, uint32_t blk) {
+    st.w = wrow[blk * 2];
+    st.d = drow[blk];
+}
+__device__ __forceinline__ void gw_stage(const gw_set &st, uint16_t (&xt)[2][GM_TN * GM_LD],
+                                         uint16_t (&wt)[2][GM_TM * GM_LD], uint32_t so) {
+    gm_dequant16(st.w, st.d, &wt[0][so], &wt[1][so]);
+    ((v4u *)&xt[0][so])[0] = st.x[0];
+    ((v4u *)&xt[0][so])[1] = st.x[1];
+    ((v4u *)&xt[1][so])[0] = st.x[2];
+    ((v4u *)&xt[1][so])[1] = st.x[3];
+}
+// Producer step s: request X of block s+2 into set rx and the weights of
+// block s+4 into set rw, stage block s+1 (set st) into buffer cb^1.
+__device__ __forceinline__ void gw_produce(gw_set &rx, gw_set &rw, const gw_set &st,
+                                           uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wt)[2][2][GM_TM * GM_LD],
+                                           uint32_t cb, const v4u *xhr, const v4u *xlr, const v4u *wrow,
+                                           const uint16_t *drow, uint32_t s, uint32_t kend, uint32_t so) {
+    gw_request_x(rx, xhr, xlr, min(s + 2, kend - 1));
+    gw_request_w(rw, wrow, drow, min(s + 4, kend - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    gw_stage(st, xt[cb ^ 1], wt[cb ^ 1], so);
+    __syncthreads();
+}
+// Consumer step s: the fragments of buffer cb and the MFMAs (none past kend).
+// The X fragments are read two token tiles at a time (register room for two
+// workgroups per CU); each accumulator still takes its three products in the
+// same order, so the result bits do not change.
+__device__ __forceinline__ void gw_consume(f32x4 (&acc)[4][4], uint16_t (&xt)[2][2][GM_TN * GM_LD],
+                                           uint16_t (&wt)[2][2][GM_TM * GM_LD], uint32_t cb, uint32_t s,
+                                           uint32_t kend, uint32_t wn, uint32_t wm, uint32_t li, uint32_t lg) {
+    if (s < kend) {
+        bf16x8 bh[4], bl[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t row = wm * 64 + c * 16 + li;
+            bh[c] = *(const bf16x8 *)&wt[cb][0][row * GM_LD + lg * 8];
+            bl[c] = *(const bf16x8 *)&wt[cb][1][row * GM_LD + lg * 8];
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            bf16x8 ah[2], al[2];
+#pragma unroll
+            for (int a = 0; a < 2; a++) {
+                const uint32_t row = wn * 64 + (2 * h + a) * 16 + li;
+                ah[a] = *(const bf16x8 *)&xt[cb][0][row * GM_LD + lg * 8];
+                al[a] = *(const bf16x8 *)&xt[cb][1][row * GM_LD + lg * 8];
+            }
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    acc[2 * h + a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[a], bh[c], acc[2 * h + a][c], 0, 0, 0);
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    acc[2 * h + a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[a], bl[c], acc[2 * h + a][c], 0, 0, 0);
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    acc[2 * h + a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[a], bh[c], acc[2 * h + a][c], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(GW_TPB) __attribute__((amdgpu_waves_per_eu(4, 4)))
+k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, uint32_t N, uint32_t M,
+             uint32_t K, uint32_t ldy, uint64_t ysplit, uint32_t boff) {
+    __shared__ __align__(16) uint16_t xt[2][2][GM_TN * GM_LD];     // [buffer][hi | lo][token][k]
+    __shared__ __align__(16) uint16_t wt[2][2][GM_TM * GM_LD];     // [buffer][hi | lo][row][k]
+    const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
+    uint32_t mt_id, nt_id;
+    if (!gm_tile(blockIdx.x + boff, mb, nb, mt_id, nt_id)) return;
+    const uint32_t n0 = nt_id * GM_TN, m0 = mt_id * GM_TM;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t nblk = K >> 5;
+    const uint32_t kb0 = (uint32_t)((uint64_t)nblk * blockIdx.y / gridDim.y);
+    const uint32_t kb1 = (uint32_t)((uint64_t)nblk * (blockIdx.y + 1) / gridDim.y);
+    // Both roles pass the same barriers: one after the prologue and one per
+    // step of the same loop (steps past kb1 only request, clamped, and stage).
+    if (wave >= 4) {
+        // producer staging role: row p/2 of both tiles, k 16*(p%2) .. +15 of each block
+        const uint32_t pt = t - 256, sr = pt >> 1, sk = (pt & 1) * 16, so = sr * GM_LD + sk;
+        const size_t xrow = (size_t)min(n0 + sr, N - 1) * K + sk;
+        const v4u *xhr = (const v4u *)(xs + xrow), *xlr = (const v4u *)(xs + (size_t)N * K + xrow);
+        const uint32_t wrow_i = min(m0 + sr, M - 1);
+        const v4u *wrow = (const v4u *)(qs + (size_t)wrow_i * K + sk);     // block s: wrow[2 s] (16 int8)
+        const uint16_t *drow = d + (size_t)wrow_i * nblk;
+        // prologue: X of blocks kb0, kb0+1 and weights of kb0..kb0+3
+        // requested, block kb0 staged into buffer 0; block b then sits in
+        // set (b - kb0) % 4
+        gw_set g0, g1, g2, g3;
+        const uint32_t kl = kb1 - 1;
+        gw_request_x(g0, xhr, xlr, kb0);
+        gw_request_w(g0, wrow, drow, kb0);
+        gw_request_x(g1, xhr, xlr, min(kb0 + 1, kl));
+        gw_request_w(g1, wrow, drow, min(kb0 + 1, kl));
+        gw_request_w(g2, wrow, drow, min(kb0 + 2, kl));
+        gw_request_w(g3, wrow, drow, min(kb0 + 3, kl));
+        __builtin_amdgcn_sched_barrier(0);
+        gw_stage(g0, xt[0], wt[0], so);
+        __syncthreads();
+        for (uint32_t s = kb0; s < kb1; s += 4) {
+            gw_produce(g2, g0, g1, xt, wt, 0, xhr, xlr, wrow, drow, s, kb1, so);
+            gw_produce(g3, g1, g2, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, kb1, so);
+            gw_produce(g0, g2, g3, xt, wt, 0, xhr, xlr, wrow, drow, s + 2, kb1, so);
+            gw_produce(g1, g3, g0, xt, wt, 1, xhr, xlr, wrow, drow, s + 3, kb1, so);
+        }
+        return;
+    }
+    const uint32_t wn = wave & 1, wm = wave >> 1;
+    const uint32_t li = lane & 15, lg = lane >> 4;
+    Y += (size_t)blockIdx.y * ysplit;
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    for (uint32_t s = kb0; s < kb1; s += 4) {
+        gw_consume(acc, xt, wt, 0, s, kb1, wn, wm, li, lg);
+        gw_consume(acc, xt, wt, 1, s + 1, kb1, wn, wm, li, lg);
+        gw_consume(acc, xt, wt, 0, s + 2, kb1, wn, wm, li, lg);
+        gw_consume(acc, xt, wt, 1, s + 3, kb1, wn, wm, li, lg);
+    }
+    // epilogue (consumers): lane holds D[i = 4*lg + e][j = li] of each tile
+    float *Yt = Y + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (GM_TN * GM_TM);
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t n = n0 + wn * 64 + a * 16 + lg * 4 + e;
+                const uint32_t m = m0 + wm * 64 + c * 16 + li;
+                const float v = acc[a][c][e];
+                if (EPI == SGK_EPI_TILE) {
+                    Yt[(n - n0) * GM_TM + (m - m0)] = v;
+                } else if (EPI == SGK_EPI_SWIGLU) {
+                    const float up = lane_xor1(v);            // column m+1 lives in lane li^1
+                    if (!(li & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(v) * up;
+                } else if (n < N && m < M) {
+                    if (EPI == SGK_EPI_ADD) Y[(size_t)n * ldy + m] += v;
+                    else Y[(size_t)n * ldy + m] = v;
+                }
+            }
+}
+
 // Split-K epilogue: the S partials P[s][N][M] summed in order, then the GEMM
 // epilogue (store, += residual, SwiGLU on (gate, up) column pairs).
 template <int EPI>
@@ -3239,15 +3420,19 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
         // the full rounds as they are and split the leftover tiles' K over a
         // whole round, partial tiles summed in order by k_tile_reduce. Splits
         // keep at least 8 Q8_0 blocks and fit the partials in a->part.
-        const uint32_t slots = gemm_slots();
+        const bool ws = gemm_ws();
+        const uint32_t slots = gemm_slots(ws);
+        const uint32_t gtpb = ws ? GW_TPB : TPB;
         uint32_t S = 1;
         if (a->part && tiles < slots) {
             S = min(4u, slots / tiles);
             while (S > 1 && (nblk / S < 8 || (uint64_t)S * a->N * a->M > a->part_cap)) S--;
         }
         if (S > 1) {
-            hipLaunchKernelGGL((k_gemm_q8_mfma<SGK_EPI_STORE>), dim3(grid, S), dim3(TPB), 0, s, a->xs, a->qs, a->d,
-                               a->part, a->N, a->M, a->K, a->M, (uint64_t)a->N * a->M, 0u);
+            if (ws) hipLaunchKernelGGL((k_gemm_q8_ws<SGK_EPI_STORE>), dim3(grid, S), dim3(gtpb), 0, s, a->xs, a->qs, a->d,
+                                       a->part, a->N, a->M, a->K, a->M, (uint64_t)a->N * a->M, 0u);
+            else hipLaunchKernelGGL((k_gemm_q8_mfma<SGK_EPI_STORE>), dim3(grid, S), dim3(gtpb), 0, s, a->xs, a->qs, a->d,
+                                    a->part, a->N, a->M, a->K, a->M, (uint64_t)a->N * a->M, 0u);
             const uint32_t rg = (uint32_t)min(((uint64_t)a->N * a->M + TPB - 1) / TPB, (uint64_t)4096);
 #define GR(E) hipLaunchKernelGGL((k_splitk_reduce<E>), dim3(rg), dim3(TPB), 0, s, a->part, S, a->N, a->M, a->Y, a->ldy)
             if (a->epi == SGK_EPI_ADD) GR(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GR(SGK_EPI_SWIGLU); else GR(SGK_EPI_STORE);
@@ -3264,13 +3449,16 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
             }
             if (S2 < 2) full = grid;
         }
-#define GQ(E) hipLaunchKernelGGL((k_gemm_q8_mfma<E>), dim3(full), dim3(TPB), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy, (uint64_t)0, 0u)
+#define GQ(E) do { if (ws) hipLaunchKernelGGL((k_gemm_q8_ws<E>), dim3(full), dim3(gtpb), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy, (uint64_t)0, 0u); \
+                 else hipLaunchKernelGGL((k_gemm_q8_mfma<E>), dim3(full), dim3(gtpb), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy, (uint64_t)0, 0u); } while (0)
         if (a->epi == SGK_EPI_ADD) GQ(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GQ(SGK_EPI_SWIGLU); else GQ(SGK_EPI_STORE);
 #undef GQ
         if (full < grid) {
             const uint32_t left = grid - full;
-            hipLaunchKernelGGL((k_gemm_q8_mfma<SGK_EPI_TILE>), dim3(left, S2), dim3(TPB), 0, s, a->xs, a->qs, a->d,
-                               a->part, a->N, a->M, a->K, 0u, (uint64_t)0, full);
+            if (ws) hipLaunchKernelGGL((k_gemm_q8_ws<SGK_EPI_TILE>), dim3(left, S2), dim3(gtpb), 0, s, a->xs, a->qs, a->d,
+                                       a->part, a->N, a->M, a->K, 0u, (uint64_t)0, full);
+            else hipLaunchKernelGGL((k_gemm_q8_mfma<SGK_EPI_TILE>), dim3(left, S2), dim3(gtpb), 0, s, a->xs, a->qs, a->d,
+                                    a->part, a->N, a->M, a->K, 0u, (uint64_t)0, full);
 #define GT(E) hipLaunchKernelGGL((k_tile_reduce<E>), dim3(left, GM_TR_PARTS), dim3(TPB), 0, s, a->part, S2, left, full, a->N, a->M, a->Y, a->ldy)
             if (a->epi == SGK_EPI_ADD) GT(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GT(SGK_EPI_SWIGLU); else GT(SGK_EPI_STORE);
 #undef GT

@@ -338,6 +338,29 @@ def test_prefill_gemm_round_split_matches_serial(gpu, monkeypatch):
     syn.close()
 
 
+@pytest.mark.parametrize("slots", [None, "12"])
+def test_prefill_gemm_warp_specialised_matches_plain(gpu, monkeypatch, slots):
+    """The warp-specialised prefill GEMM (default) and the plain one
+    (SURGE_GEMM_WS=0) share tiles, fragments, MFMA order and dequantisation:
+    a chunked prefill gives the same logits bit for bit through both, with
+    the default slots and at 12 slots (full rounds, leftover tiles split over
+    K, and the narrow weights' split-K, with every epilogue)."""
+    syn = S.Synth(WIDE, S.SG_T_Q8_0, seed=19)
+    gpu.load_model(syn.model)
+    gpu.state_new(260)
+    rng = np.random.default_rng(14)
+    prompt = rng.integers(0, WIDE["vocab"], 256).tolist()
+    if slots:
+        monkeypatch.setenv("SURGE_GEMM_SLOTS", slots)
+    ws = gpu.prefill(prompt, chunk=128)
+    monkeypatch.setenv("SURGE_GEMM_WS", "0")
+    plain = gpu.prefill(prompt, chunk=128)
+    monkeypatch.delenv("SURGE_GEMM_WS")
+    assert np.array_equal(ws, plain)
+    assert np.array_equal(gpu.prefill(prompt, chunk=128), ws)
+    syn.close()
+
+
 @pytest.mark.parametrize("cfg", ["HD256", "HD128"])
 def test_deep_prefill_key_split_matches_serial(gpu, cfg):
     """Deep chunks split the flash pass's key tiles (about one workgroup per
