@@ -2976,26 +2976,43 @@ __global__ void __launch_bounds__(TPB) k_split_bf16_rms(const float *X, uint32_t
 
 #define GM_TN 128   // tokens per workgroup tile
 #define GM_TM 128   // weight rows per workgroup tile
-#define GM_LD 40    // LDS row of one 32-wide step, padded (bf16 elements, 80 bytes)
+#define GM_LD 32    // LDS row of one 32-wide step (bf16 elements, 64 bytes, unpadded)
+
+// Element offset of 16-byte chunk c (k 8c..8c+7) of LDS tile row `row`: the
+// chunk sits at c ^ ((row >> 1) & 3), which keeps both the fragment reads
+// (lane: row li, chunk lg) and the staging writes (thread: 32 bytes of one
+// row) free of LDS bank conflicts (measured with SQ_LDS_BANK_CONFLICT).
+__device__ __forceinline__ uint32_t gm_at(uint32_t row, uint32_t c) {
+    return row * GM_LD + ((c ^ ((row >> 1) & 3)) << 3);
+}
 
 // 16 int8 weights of one row and its block scale -> 16 bf16 hi and 16 bf16 lo
-// of w = d*q, stored at h[0..15] and l[0..15].
-__device__ __forceinline__ void gm_dequant16(v4u q, uint32_t dbits, uint16_t *h, uint16_t *l) {
-    const float dd = h2f((uint16_t)dbits);
+// of w = d*q, the first 8 of each stored at element offset o0 of h and l,
+// the last 8 at o1.
+__device__ __forceinline__ void gm_dequant16(v4u q, uint32_t dbits, uint16_t *h, uint16_t *l, uint32_t o0,
+                                             uint32_t o1) {
+    // w = d*q as fma(d, q + 128, -128 d): one rounding of the exact d*q, so
+    // the bits of d*q, from an unsigned byte conversion (q ^ 0x80 = q + 128)
+    const float dd = h2f((uint16_t)dbits), off = -128.0f * dd;
     uint32_t oh[8], ol[8];
 #pragma unroll
     for (int p = 0; p < 8; p++) {
-        const uint32_t w = q[p >> 1] >> (16 * (p & 1));
-        const float w0 = dd * (float)(int8_t)w, w1 = dd * (float)(int8_t)(w >> 8);
+        const uint32_t u = (q[p >> 1] ^ 0x80808080u) >> (16 * (p & 1));
+        const float w0 = fmaf(dd, (float)(u & 0xffu), off), w1 = fmaf(dd, (float)((u >> 8) & 0xffu), off);
         const bf16x2 hh = {(__bf16)w0, (__bf16)w1};
-        const bf16x2 ll = {(__bf16)(w0 - (float)hh[0]), (__bf16)(w1 - (float)hh[1])};
-        oh[p] = __builtin_bit_cast(uint32_t, hh);
+        const uint32_t hb = __builtin_bit_cast(uint32_t, hh);
+        // hi as f32: hb << 16 (as a byte permute, so it reuses the packed
+        // conversion instead of converting w0 again) and hb with its low half cleared
+        const float h0 = __uint_as_float(__builtin_amdgcn_perm(0u, hb, 0x01000c0cu));
+        const float h1 = __uint_as_float(hb & 0xffff0000u);
+        const bf16x2 ll = {(__bf16)(w0 - h0), (__bf16)(w1 - h1)};
+        oh[p] = hb;
         ol[p] = __builtin_bit_cast(uint32_t, ll);
     }
-    ((v4u *)h)[0] = (v4u){oh[0], oh[1], oh[2], oh[3]};
-    ((v4u *)h)[1] = (v4u){oh[4], oh[5], oh[6], oh[7]};
-    ((v4u *)l)[0] = (v4u){ol[0], ol[1], ol[2], ol[3]};
-    ((v4u *)l)[1] = (v4u){ol[4], ol[5], ol[6], ol[7]};
+    *(v4u *)(h + o0) = (v4u){oh[0], oh[1], oh[2], oh[3]};
+    *(v4u *)(h + o1) = (v4u){oh[4], oh[5], oh[6], oh[7]};
+    *(v4u *)(l + o0) = (v4u){ol[0], ol[1], ol[2], ol[3]};
+    *(v4u *)(l + o1) = (v4u){ol[4], ol[5], ol[6], ol[7]};
 }
 
 // One K step (Q8_0 block s) of the prefill GEMM on LDS buffer cb: request the
@@ -3008,8 +3025,8 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
                                         const v4u &wnext, const uint32_t &dnext,
                                         uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wt)[2][2][GM_TM * GM_LD],
                                         uint32_t cb, const v4u *xhr, const v4u *xlr, const v4u *wrow,
-                                        const uint16_t *drow, uint32_t s, uint32_t kend, uint32_t so,
-                                        uint32_t wn, uint32_t wm, uint32_t li, uint32_t lg) {
+                                        const uint16_t *drow, uint32_t s, uint32_t kend, uint32_t so0,
+                                        uint32_t so1, uint32_t wn, uint32_t wm, uint32_t li, uint32_t lg) {
     const uint32_t s1 = min(s + 1, kend - 1), s2 = min(s + 2, kend - 1);
 #pragma unroll
     for (int u = 0; u < 2; u++) { xr[u] = xhr[s1 * 4 + u]; xr[2 + u] = xlr[s1 * 4 + u]; }
@@ -3023,14 +3040,14 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t row = wm * 64 + c * 16 + li;
-            bh[c] = *(const bf16x8 *)&wt[cb][0][row * GM_LD + lg * 8];
-            bl[c] = *(const bf16x8 *)&wt[cb][1][row * GM_LD + lg * 8];
+            bh[c] = *(const bf16x8 *)&wt[cb][0][gm_at(row, lg)];
+            bl[c] = *(const bf16x8 *)&wt[cb][1][gm_at(row, lg)];
         }
 #pragma unroll
         for (int a = 0; a < 4; a++) {
             const uint32_t row = wn * 64 + a * 16 + li;
-            ah[a] = *(const bf16x8 *)&xt[cb][0][row * GM_LD + lg * 8];
-            al[a] = *(const bf16x8 *)&xt[cb][1][row * GM_LD + lg * 8];
+            ah[a] = *(const bf16x8 *)&xt[cb][0][gm_at(row, lg)];
+            al[a] = *(const bf16x8 *)&xt[cb][1][gm_at(row, lg)];
         }
 #pragma unroll
         for (int a = 0; a < 4; a++)
@@ -3045,11 +3062,11 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
 #pragma unroll
             for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[a], bh[c], acc[a][c], 0, 0, 0);
     }
-    gm_dequant16(wnext, dnext, &wt[cb ^ 1][0][so], &wt[cb ^ 1][1][so]);
-    ((v4u *)&xt[cb ^ 1][0][so])[0] = xr[0];
-    ((v4u *)&xt[cb ^ 1][0][so])[1] = xr[1];
-    ((v4u *)&xt[cb ^ 1][1][so])[0] = xr[2];
-    ((v4u *)&xt[cb ^ 1][1][so])[1] = xr[3];
+    gm_dequant16(wnext, dnext, wt[cb ^ 1][0], wt[cb ^ 1][1], so0, so1);
+    *(v4u *)&xt[cb ^ 1][0][so0] = xr[0];
+    *(v4u *)&xt[cb ^ 1][0][so1] = xr[1];
+    *(v4u *)&xt[cb ^ 1][1][so0] = xr[2];
+    *(v4u *)&xt[cb ^ 1][1][so1] = xr[3];
     __syncthreads();
 }
 
@@ -3088,7 +3105,8 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     const uint32_t kb1 = (uint32_t)((uint64_t)nblk * (blockIdx.y + 1) / gridDim.y);
     Y += (size_t)blockIdx.y * ysplit;
     // staging role: row t/2 of both tiles, k 16*(t%2) .. +15 of each block
-    const uint32_t sr = t >> 1, sk = (t & 1) * 16, so = sr * GM_LD + sk;
+    // (LDS chunks 2*(t%2) and 2*(t%2)+1 of the row)
+    const uint32_t sr = t >> 1, sk = (t & 1) * 16, so0 = gm_at(sr, sk / 8), so1 = gm_at(sr, sk / 8 + 1);
     const size_t xrow = (size_t)min(n0 + sr, N - 1) * K + sk;
     const v4u *xhr = (const v4u *)(xs + xrow), *xlr = (const v4u *)(xs + (size_t)N * K + xrow);
     const uint32_t wrow_i = min(m0 + sr, M - 1);
@@ -3110,17 +3128,17 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     dA = drow[kb0];
     wB = wrow[min(kb0 + 1, kb1 - 1) * 2];
     dB = drow[min(kb0 + 1, kb1 - 1)];
-    gm_dequant16(wA, dA, &wt[0][0][so], &wt[0][1][so]);
-    ((v4u *)&xt[0][0][so])[0] = xr[0];
-    ((v4u *)&xt[0][0][so])[1] = xr[1];
-    ((v4u *)&xt[0][1][so])[0] = xr[2];
-    ((v4u *)&xt[0][1][so])[1] = xr[3];
+    gm_dequant16(wA, dA, wt[0][0], wt[0][1], so0, so1);
+    *(v4u *)&xt[0][0][so0] = xr[0];
+    *(v4u *)&xt[0][0][so1] = xr[1];
+    *(v4u *)&xt[0][1][so0] = xr[2];
+    *(v4u *)&xt[0][1][so1] = xr[3];
     __syncthreads();
     // step s uses buffer s%2; its register set (A for even s) is reloaded with
     // block s+2 while the other set (holding block s+1) is staged
     for (uint32_t s = kb0; s < kb1; s += 2) {
-        gm_step(acc, xr, wA, dA, wB, dB, xt, wt, 0, xhr, xlr, wrow, drow, s, kb1, so, wn, wm, li, lg);
-        gm_step(acc, xr, wB, dB, wA, dA, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, kb1, so, wn, wm, li, lg);
+        gm_step(acc, xr, wA, dA, wB, dB, xt, wt, 0, xhr, xlr, wrow, drow, s, kb1, so0, so1, wn, wm, li, lg);
+        gm_step(acc, xr, wB, dB, wA, dA, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, kb1, so0, so1, wn, wm, li, lg);
     }
     // epilogue: lane holds D[i = 4*lg + e][j = li] of each tile
     float *Yt = Y + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (GM_TN * GM_TM);
@@ -3153,40 +3171,46 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
 // X into buffer (s+1)%2. One barrier per step, so one group's MFMAs overlap
 // the other's VALU and LDS work on every SIMD. A step is short, so the
 // producers keep four register sets: block b's X and raw weights sit in set
-// (b - kb0) % 4, X requested two steps and the weights four steps before
-// they are staged.
+// (b - kb0) % 4, both requested three steps before they are staged.
 #define GW_TPB 512
 struct gw_set {
-    v4u x[4];        // X hi (2) and lo (2) of the staging row
+    v4u x[4];        // X hi and lo of the thread's chunk in its two token rows
     v4u w;           // 16 raw int8 weights
     uint32_t d;      // block scale
 };
-__device__ __forceinline__ void gw_request_x(gw_set &st, const v4u *xhr, const v4u *xlr, uint32_t blk) {
-#pragma unroll
-    for (int u = 0; u < 2; u++) { st.x[u] = xhr[blk * 4 + u]; st.x[2 + u] = xlr[blk * 4 + u]; }
+// X staging: thread p takes 16-byte chunk p%4 of token rows p/4 and p/4 + 64,
+// so a load instruction covers whole 64-byte rows (16 cache lines, not 32)
+__device__ __forceinline__ void gw_request_x(gw_set &st, const v4u *xhr, const v4u *xlr, uint32_t blk,
+                                             uint32_t r64) {
+    st.x[0] = xhr[blk * 4];
+    st.x[1] = xhr[blk * 4 + r64];
+    st.x[2] = xlr[blk * 4];
+    st.x[3] = xlr[blk * 4 + r64];
 }
 __device__ __forceinline__ void gw_request_w(gw_set &st, const v4u *wrow, const uint16_t *drow, uint32_t blk) {
     st.w = wrow[blk * 2];
     st.d = drow[blk];
 }
 __device__ __forceinline__ void gw_stage(const gw_set &st, uint16_t (&xt)[2][GM_TN * GM_LD],
-                                         uint16_t (&wt)[2][GM_TM * GM_LD], uint32_t so) {
-    gm_dequant16(st.w, st.d, &wt[0][so], &wt[1][so]);
-    ((v4u *)&xt[0][so])[0] = st.x[0];
-    ((v4u *)&xt[0][so])[1] = st.x[1];
-    ((v4u *)&xt[1][so])[0] = st.x[2];
-    ((v4u *)&xt[1][so])[1] = st.x[3];
+                                         uint16_t (&wt)[2][GM_TM * GM_LD], uint32_t so0, uint32_t so1,
+                                         uint32_t xo0, uint32_t xo1) {
+    gm_dequant16(st.w, st.d, wt[0], wt[1], so0, so1);
+    *(v4u *)&xt[0][xo0] = st.x[0];
+    *(v4u *)&xt[0][xo1] = st.x[1];
+    *(v4u *)&xt[1][xo0] = st.x[2];
+    *(v4u *)&xt[1][xo1] = st.x[3];
 }
-// Producer step s: request X of block s+2 into set rx and the weights of
-// block s+4 into set rw, stage block s+1 (set st) into buffer cb^1.
-__device__ __forceinline__ void gw_produce(gw_set &rx, gw_set &rw, const gw_set &st,
+// Producer step s: request X and weights of block s+3 into set rq (free:
+// block s-1 was staged in step s-2), stage block s+1 (set st) into cb^1.
+__device__ __forceinline__ void gw_produce(gw_set &rq, const gw_set &st,
                                            uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wt)[2][2][GM_TM * GM_LD],
                                            uint32_t cb, const v4u *xhr, const v4u *xlr, const v4u *wrow,
-                                           const uint16_t *drow, uint32_t s, uint32_t kend, uint32_t so) {
-    gw_request_x(rx, xhr, xlr, min(s + 2, kend - 1));
-    gw_request_w(rw, wrow, drow, min(s + 4, kend - 1));
+                                           const uint16_t *drow, uint32_t s, uint32_t kend, uint32_t so0,
+                                           uint32_t so1, uint32_t xo0, uint32_t xo1, uint32_t r64) {
+    gw_request_x(rq, xhr, xlr, min(s + 3, kend - 1), r64);
+    gw_request_w(rq, wrow, drow, min(s + 3, kend - 1));
     __builtin_amdgcn_sched_barrier(0);
-    gw_stage(st, xt[cb ^ 1], wt[cb ^ 1], so);
+    gw_stage(st, xt[cb ^ 1], wt[cb ^ 1], so0, so1, xo0, xo1);
     __syncthreads();
 }
 // Consumer step s: the fragments of buffer cb and the MFMAs (none past kend).
@@ -3201,8 +3225,8 @@ __device__ __forceinline__ void gw_consume(f32x4 (&acc)[4][4], uint16_t (&xt)[2]
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const uint32_t row = wm * 64 + c * 16 + li;
-            bh[c] = *(const bf16x8 *)&wt[cb][0][row * GM_LD + lg * 8];
-            bl[c] = *(const bf16x8 *)&wt[cb][1][row * GM_LD + lg * 8];
+            bh[c] = *(const bf16x8 *)&wt[cb][0][gm_at(row, lg)];
+            bl[c] = *(const bf16x8 *)&wt[cb][1][gm_at(row, lg)];
         }
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -3210,8 +3234,8 @@ __device__ __forceinline__ void gw_consume(f32x4 (&acc)[4][4], uint16_t (&xt)[2]
 #pragma unroll
             for (int a = 0; a < 2; a++) {
                 const uint32_t row = wn * 64 + (2 * h + a) * 16 + li;
-                ah[a] = *(const bf16x8 *)&xt[cb][0][row * GM_LD + lg * 8];
-                al[a] = *(const bf16x8 *)&xt[cb][1][row * GM_LD + lg * 8];
+                ah[a] = *(const bf16x8 *)&xt[cb][0][gm_at(row, lg)];
+                al[a] = *(const bf16x8 *)&xt[cb][1][gm_at(row, lg)];
             }
 #pragma unroll
             for (int a = 0; a < 2; a++)
@@ -3250,32 +3274,37 @@ k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, 
     // Both roles pass the same barriers: one after the prologue and one per
     // step of the same loop (steps past kb1 only request, clamped, and stage).
     if (wave >= 4) {
-        // producer staging role: row p/2 of both tiles, k 16*(p%2) .. +15 of each block
-        const uint32_t pt = t - 256, sr = pt >> 1, sk = (pt & 1) * 16, so = sr * GM_LD + sk;
-        const size_t xrow = (size_t)min(n0 + sr, N - 1) * K + sk;
+        // producer staging roles: weight row p/2, k 16*(p%2) .. +15 of each
+        // block (LDS chunks 2*(p%2), +1); X chunk p%4 of token rows p/4, p/4+64
+        const uint32_t pt = t - 256, sr = pt >> 1, sk = (pt & 1) * 16;
+        const uint32_t so0 = gm_at(sr, sk / 8), so1 = gm_at(sr, sk / 8 + 1);
+        const uint32_t xr0 = pt >> 2, xc = pt & 3;
+        const uint32_t xo0 = gm_at(xr0, xc), xo1 = gm_at(xr0 + 64, xc);
+        const uint32_t xn0 = min(n0 + xr0, N - 1), xn1 = min(n0 + xr0 + 64, N - 1);
+        const size_t xrow = (size_t)xn0 * K + xc * 8;
+        const uint32_t r64 = (uint32_t)(((size_t)(xn1 - xn0) * K) / 8);     // row p/4+64, in 16-byte units
         const v4u *xhr = (const v4u *)(xs + xrow), *xlr = (const v4u *)(xs + (size_t)N * K + xrow);
         const uint32_t wrow_i = min(m0 + sr, M - 1);
         const v4u *wrow = (const v4u *)(qs + (size_t)wrow_i * K + sk);     // block s: wrow[2 s] (16 int8)
         const uint16_t *drow = d + (size_t)wrow_i * nblk;
-        // prologue: X of blocks kb0, kb0+1 and weights of kb0..kb0+3
-        // requested, block kb0 staged into buffer 0; block b then sits in
-        // set (b - kb0) % 4
+        // prologue: blocks kb0..kb0+2 requested, block kb0 staged into
+        // buffer 0; block b then sits in set (b - kb0) % 4
         gw_set g0, g1, g2, g3;
         const uint32_t kl = kb1 - 1;
-        gw_request_x(g0, xhr, xlr, kb0);
+        gw_request_x(g0, xhr, xlr, kb0, r64);
         gw_request_w(g0, wrow, drow, kb0);
-        gw_request_x(g1, xhr, xlr, min(kb0 + 1, kl));
+        gw_request_x(g1, xhr, xlr, min(kb0 + 1, kl), r64);
         gw_request_w(g1, wrow, drow, min(kb0 + 1, kl));
+        gw_request_x(g2, xhr, xlr, min(kb0 + 2, kl), r64);
         gw_request_w(g2, wrow, drow, min(kb0 + 2, kl));
-        gw_request_w(g3, wrow, drow, min(kb0 + 3, kl));
         __builtin_amdgcn_sched_barrier(0);
-        gw_stage(g0, xt[0], wt[0], so);
+        gw_stage(g0, xt[0], wt[0], so0, so1, xo0, xo1);
         __syncthreads();
         for (uint32_t s = kb0; s < kb1; s += 4) {
-            gw_produce(g2, g0, g1, xt, wt, 0, xhr, xlr, wrow, drow, s, kb1, so);
-            gw_produce(g3, g1, g2, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, kb1, so);
-            gw_produce(g0, g2, g3, xt, wt, 0, xhr, xlr, wrow, drow, s + 2, kb1, so);
-            gw_produce(g1, g3, g0, xt, wt, 1, xhr, xlr, wrow, drow, s + 3, kb1, so);
+            gw_produce(g3, g1, xt, wt, 0, xhr, xlr, wrow, drow, s, kb1, so0, so1, xo0, xo1, r64);
+            gw_produce(g0, g2, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, kb1, so0, so1, xo0, xo1, r64);
+            gw_produce(g1, g3, xt, wt, 0, xhr, xlr, wrow, drow, s + 2, kb1, so0, so1, xo0, xo1, r64);
+            gw_produce(g2, g0, xt, wt, 1, xhr, xlr, wrow, drow, s + 3, kb1, so0, so1, xo0, xo1, r64);
         }
         return;
     }
