@@ -1354,7 +1354,11 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 #define FA_TQ 64    // tokens per workgroup (4 waves x 16)
 #define FA_TK 64    // keys per tile
-#define FA_PLD (FA_TK + 8)
+// LDS row pitches of the flash tiles: an MFMA fragment read (lane: row li,
+// 16-byte chunk lg) is free of bank conflicts when the pitch is an odd
+// multiple of 32 bytes (measured with SQ_LDS_BANK_CONFLICT: 8 LDS cycles per
+// read at 9 or 33 16-byte slots, 4 at 10 or 34), hence +16 elements
+#define FA_PLD (FA_TK + 16)
 
 // x[0..7] -> f16 hi and lo fragments
 __device__ __forceinline__ void fa_split8(const float *x, f16x8 &hi, f16x8 &lo) {
@@ -1875,7 +1879,7 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
 template <int HD>
 __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
     static_assert(HD % 64 == 0 && HD <= 256, "flash prefill takes head_dim 64, 128, 192 or 256");
-    constexpr int KLD = HD + 8, NKB = HD / 32, NNT = HD / 16;
+    constexpr int KLD = HD + 16, NKB = HD / 32, NNT = HD / 16;
     constexpr int KDT = HD / 4;                 // K staging: dims per thread (4 threads per key)
     constexpr int VDC = HD / 8, VKG = TPB / VDC; // V staging: dim chunks of 8, key groups of 8
     __shared__ __align__(16) uint16_t ks[FA_TK * KLD];
