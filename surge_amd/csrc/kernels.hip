@@ -2622,7 +2622,9 @@ __device__ __forceinline__ void dc_load(dcregs<DK, ROWS> &r, const sgk_gdn &a, c
     const float *cz = conv_out + (size_t)min(z0 + zt, ntok - 1) * a.conv_dim;
 #pragma unroll
     for (int u = 0; u < C::NV4; u++) {
-        const uint32_t e = (part * C::NV4 + u) * 4;          // 0 .. 2*DK-1: k, then q
+        // float4 u*TPT + part of the token's k|q: consecutive threads take
+        // consecutive float4s (coalesced loads, LDS stores free of bank conflicts)
+        const uint32_t e = (u * C::TPT + part) * 4;          // 0 .. 2*DK-1: k, then q
         const float *src = e < DK ? cz + key_dim + (size_t)hk * DK + e : cz + (size_t)hk * DK + (e - DK);
         r[u] = *(const f32x4 *)src;
     }
@@ -2639,7 +2641,7 @@ __device__ __forceinline__ void dc_store(const dcregs<DK, ROWS> &r, float *kq, f
     using C = dcg<DK, ROWS>;
     const uint32_t t = threadIdx.x, zt = t / C::TPT, part = t % C::TPT;
 #pragma unroll
-    for (int u = 0; u < C::NV4; u++) *(f32x4 *)&kq[zt * 2 * DK + (part * C::NV4 + u) * 4] = r[u];
+    for (int u = 0; u < C::NV4; u++) *(f32x4 *)&kq[zt * 2 * DK + (u * C::TPT + part) * 4] = r[u];
     const uint32_t vz = t / C::VTT;
     if (vz < (uint32_t)C::DCT) *(f32x4 *)&vs[vz * ROWS + (t % C::VTT) * 4] = r[C::NV4];
     if (t < (uint32_t)C::DCT) {
