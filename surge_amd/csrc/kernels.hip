@@ -174,23 +174,28 @@ __device__ __forceinline__ void stage_issue(const sgk_gemv &a, xstage<PRO, NT, K
     }
 }
 
-// Staged x layout of the Q8_0 GEMVs (CH): float4 j of 16-column chunk c (x
-// columns 16c+4j .. +3) sits at float4 index j*(nch+1) + c, so the 64 lanes of
-// a wave, reading chunks c..c+63, read 1 KB of consecutive LDS per float4
-// (no bank conflicts; the linear layout puts lanes 64 bytes apart), and the
-// staging writes of one chunk's four float4s land in different banks (the
-// one-float4 pad). It takes XS_CH_PAD floats more than the linear layout.
+// Staged x layout of the Q8_0 GEMVs (CH): chunks of 16 columns go in blocks
+// of 64; block b holds four planes of 65 float4s, float4 j of chunk c (x
+// columns 16c+4j .. +3) at (c/64)*260 + j*65 + c%64. The 64 lanes of a wave,
+// reading chunks c..c+63, then read 1 KB of consecutive LDS per float4 (no
+// bank conflicts; the linear layout puts lanes 64 bytes apart) at constant
+// offsets from one address, and the staging writes of one chunk's four
+// float4s land in different banks (the 65th float4 of a plane is padding).
 // Without CH (the f32 GEMV) x is linear.
-#define XS_CH_PAD 16
+#define XS_CH_BLK 260
+__host__ __device__ __forceinline__ uint32_t xs_ch_floats(uint32_t cols) {
+    return ((cols / 16 + 63) / 64) * XS_CH_BLK * 4;
+}
 template <bool CH>
-__device__ __forceinline__ uint32_t xs4_at(uint32_t i, uint32_t nch) {
-    return CH ? (i & 3) * (nch + 1) + (i >> 2) : i;
+__device__ __forceinline__ uint32_t xs4_at(uint32_t i) {
+    const uint32_t c = i >> 2;
+    return CH ? (c >> 6) * XS_CH_BLK + (i & 3) * 65 + (c & 63) : i;
 }
 
 template <int PRO, int NT, int K, bool CH = false>
 __device__ __forceinline__ float stage_finish(const sgk_gemv &a, xstage<PRO, NT, K> &st, float *xs) {
     __shared__ float red[NT / 64];
-    const uint32_t n = a.cols, t = threadIdx.x, n4 = n >> 2, nch = n >> 4;
+    const uint32_t n = a.cols, t = threadIdx.x, n4 = n >> 2;
     if (PRO == SGK_PRO_GATED) {
         // RMSNormGated of the DeltaNet readout (ref.c:1322-1330): head hh's
         // factor from its row blocks' sums of squares (added in block order),
@@ -213,7 +218,7 @@ __device__ __forceinline__ float stage_finish(const sgk_gemv &a, xstage<PRO, NT,
             if (i < n4) {
                 const float4 yv = st.v[k], zv = st.g[k], wv = st.w[k];
                 const float r = rh[(4 * i) / dv];
-                s4[xs4_at<CH>(i, nch)] = make_float4(zv.x * ((yv.x * r) * wv.x), zv.y * ((yv.y * r) * wv.y),
+                s4[xs4_at<CH>(i)] = make_float4(zv.x * ((yv.x * r) * wv.x), zv.y * ((yv.y * r) * wv.y),
                                                      zv.z * ((yv.z * r) * wv.z), zv.w * ((yv.w * r) * wv.w));
             }
         }
@@ -234,7 +239,7 @@ __device__ __forceinline__ float stage_finish(const sgk_gemv &a, xstage<PRO, NT,
                 ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
                 v.x *= g.x; v.y *= g.y; v.z *= g.z; v.w *= g.w;
             }
-            s4[xs4_at<CH>(i, nch)] = v;
+            s4[xs4_at<CH>(i)] = v;
         }
     }
     for (uint32_t i = t + (uint32_t)K * NT; i < n4; i += NT) {   // rows wider than K*NT*4
@@ -245,7 +250,7 @@ __device__ __forceinline__ float stage_finish(const sgk_gemv &a, xstage<PRO, NT,
             ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
             v.x *= g.x; v.y *= g.y; v.z *= g.z; v.w *= g.w;
         }
-        s4[xs4_at<CH>(i, nch)] = v;
+        s4[xs4_at<CH>(i)] = v;
     }
     for (uint32_t i = 4 * n4 + t; i < n; i += NT) {       // cols % 4 tail (f32 test models; never with CH)
         float v = a.x[i];
@@ -333,10 +338,9 @@ __device__ __forceinline__ void gemv_load(gemv_chunk<R> &ch, const int8_t *qs, c
 }
 
 template <int R>
-__device__ __forceinline__ void gemv_fma(float *acc, const gemv_chunk<R> &ch, const float *xs, uint32_t c,
-                                         uint32_t nch) {
-    const float4 *xa = (const float4 *)xs + c;         // chunked layout (xs4_at<true>)
-    const float4 a0 = xa[0], a1 = xa[nch + 1], a2 = xa[2 * (nch + 1)], a3 = xa[3 * (nch + 1)];
+__device__ __forceinline__ void gemv_fma(float *acc, const gemv_chunk<R> &ch, const float *xs, uint32_t c) {
+    const float4 *xa = (const float4 *)xs + (c >> 6) * XS_CH_BLK + (c & 63);     // xs4_at<true>
+    const float4 a0 = xa[0], a1 = xa[65], a2 = xa[130], a3 = xa[195];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = fmaf(h2f(ch.d[r]), dot16(ch.q[r], a0, a1, a2, a3), acc[r]);
 }
@@ -352,20 +356,20 @@ __device__ __forceinline__ void gemv_group(const sgk_gemv &a, const float *xs, u
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
     uint32_t c = lane;
     if (PRE) {
-        if (c < nch) gemv_fma<R>(acc, *pre, xs, c, nch);
+        if (c < nch) gemv_fma<R>(acc, *pre, xs, c);
         c += 64;
     }
     for (; c + 64 < nch; c += 128) {
         gemv_chunk<R> ca, cb;
         gemv_load<R>(ca, a.qs, a.d, r0, a.rows, cols, c);
         gemv_load<R>(cb, a.qs, a.d, r0, a.rows, cols, c + 64);
-        gemv_fma<R>(acc, ca, xs, c, nch);
-        gemv_fma<R>(acc, cb, xs, c + 64, nch);
+        gemv_fma<R>(acc, ca, xs, c);
+        gemv_fma<R>(acc, cb, xs, c + 64);
     }
     if (c < nch) {
         gemv_chunk<R> ca;
         gemv_load<R>(ca, a.qs, a.d, r0, a.rows, cols, c);
-        gemv_fma<R>(acc, ca, xs, c, nch);
+        gemv_fma<R>(acc, ca, xs, c);
     }
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]) * post;
@@ -494,13 +498,13 @@ __device__ __forceinline__ void long_load(long_batch<LU> &bt, const sgk_gemv &a,
 
 template <int LU>
 __device__ __forceinline__ float long_fma(const long_batch<LU> &bt, const float *xs, const long_task &t, uint32_t lane,
-                                          float acc, uint32_t nch) {
+                                          float acc) {
 #pragma unroll
     for (int u = 0; u < LU; u++) {
         const uint32_t c = t.c0 + lane + 64 * u;
         if (c < t.c1) {
-            const float4 *xa = (const float4 *)xs + c;     // chunked layout (xs4_at<true>)
-            acc = fmaf(h2f(bt.d[u]), dot16(bt.q[u], xa[0], xa[nch + 1], xa[2 * (nch + 1)], xa[3 * (nch + 1)]), acc);
+            const float4 *xa = (const float4 *)xs + (c >> 6) * XS_CH_BLK + (c & 63);     // xs4_at<true>
+            acc = fmaf(h2f(bt.d[u]), dot16(bt.q[u], xa[0], xa[65], xa[130], xa[195]), acc);
         }
     }
     return acc;
@@ -509,7 +513,7 @@ __device__ __forceinline__ float long_fma(const long_batch<LU> &bt, const float 
 template <int EPI, int LU>
 __global__ void __launch_bounds__(LTPB) k_gemv_q8_long(sgk_gemv a) {
     extern __shared__ float lds[];
-    float *xs = lds, *part = lds + a.cols + XS_CH_PAD;   // part[LW * LW]
+    float *xs = lds, *part = lds + xs_ch_floats(a.cols);   // part[LW * LW]
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     long_plan p;
     p.G = gridDim.x;
@@ -534,7 +538,7 @@ __global__ void __launch_bounds__(LTPB) k_gemv_q8_long(sgk_gemv a) {
         const bool hn = long_task_at<LU>(p, w, k + 1, tn);
         long_batch<LU> nxt;
         if (hn) long_load<LU>(nxt, a, tn, lane);
-        acc = long_fma<LU>(cur, xs, t, lane, acc, p.nch);
+        acc = long_fma<LU>(cur, xs, t, lane, acc);
         if (!hn || tn.row != t.row) {
             acc = wave_sum(acc);
             if (t.slot == 0xffffffffu) {
@@ -702,7 +706,7 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         return hipGetLastError();
     }
     if (PRO == SGK_PRO_NONE && EPI != SGK_EPI_SWIGLU && a->cols > 8192 && a->tune_r != 7 && a->tune_r != 8) {
-        const size_t lds = ((size_t)a->cols + XS_CH_PAD + LW * LW) * 4;
+        const size_t lds = ((size_t)xs_ch_floats(a->cols) + LW * LW) * 4;
         constexpr int LE = EPI == SGK_EPI_ADD ? SGK_EPI_ADD : SGK_EPI_STORE;
         auto kern = a->tune_r == 3 ? k_gemv_q8_long<LE, 4> : a->tune_r == 5 ? k_gemv_q8_long<LE, 6>
                   : a->tune_r == 6 ? k_gemv_q8_long<LE, 8> : k_gemv_q8_long<LE, 3>;
@@ -712,7 +716,7 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         hipLaunchKernelGGL(kern, dim3(blocks), dim3(LTPB), lds, s, *a);
         return hipGetLastError();
     }
-    const size_t lds = ((size_t)a->cols + XS_CH_PAD) * 4;
+    const size_t lds = (size_t)xs_ch_floats(a->cols) * 4;
     const int R = EPI == SGK_EPI_SWIGLU ? 2 : (a->tune_r == 1 ? 1 : (a->tune_r == 4 || a->tune_r == 8) ? 4 : 2);
     if (R == 4) return launch_q8<4, PRO, EPI>(*a, lds, s);
     if (R == 1) return launch_q8<1, PRO, (EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI)>(*a, lds, s);
