@@ -1884,8 +1884,11 @@ template <int HD>
 __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
     static_assert(HD % 64 == 0 && HD <= 256, "flash prefill takes head_dim 64, 128, 192 or 256");
     constexpr int KLD = HD + 16, NKB = HD / 32, NNT = HD / 16;
-    constexpr int KDT = HD / 4;                 // K staging: dims per thread (4 threads per key)
-    constexpr int VDC = HD / 8, VKG = TPB / VDC; // V staging: dim chunks of 8, key groups of 8
+    // K staging: a key row is KC8 16-byte chunks; consecutive threads take
+    // consecutive chunks of a row (contiguous LDS stores, coalesced loads),
+    // KPP rows per pass, KNP passes per 64-key tile
+    constexpr int KC8 = HD / 8, KPP = TPB / KC8, KNP = (FA_TK + KPP - 1) / KPP;
+    constexpr int VDC = HD / 8;                  // V staging: dim chunks of 8 (threads 8*vdc + vkg)
     __shared__ __align__(16) uint16_t ks[FA_TK * KLD];
     __shared__ __align__(16) uint16_t vt[HD * FA_PLD];
     __shared__ __align__(16) uint16_t ps[2][FA_TQ * FA_PLD];
@@ -1924,20 +1927,24 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
 #pragma unroll
     for (int n = 0; n < NNT; n++) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    const uint32_t kk = t >> 2, kd = (t & 3) * KDT;        // K staging role
-    const uint32_t vkg = t / VDC, vdc = t % VDC;            // V staging role
+    const uint32_t kk = t / KC8, kd = (t % KC8) * 8;        // K staging role: rows kk + u*KPP
+    // V staging role: consecutive threads take consecutive key groups of one
+    // dim chunk, so 8 lanes store 128 contiguous bytes of a V^T row
+    const uint32_t vkg = t % (FA_TK / 8), vdc = t / (FA_TK / 8);
     for (uint32_t k0 = kbeg; k0 < kstop; k0 += FA_TK) {
         // stage K [key][dim] and V^T [dim][key] (keys clamped into the range)
         {
-            const uint32_t key = min(k0 + kk, kend - 1);
-            const v4u *src = (const v4u *)(kc + kv_at(a, key, hk) + kd);
-            v4u r[KDT / 8];
+            v4u r[KNP];
 #pragma unroll
-            for (int u = 0; u < KDT / 8; u++) r[u] = src[u];
+            for (int u = 0; u < KNP; u++) {
+                const uint32_t key = min(k0 + min(kk + u * KPP, (uint32_t)FA_TK - 1), kend - 1);
+                r[u] = *(const v4u *)(kc + kv_at(a, key, hk) + kd);
+            }
 #pragma unroll
-            for (int u = 0; u < KDT / 8; u++) ((v4u *)&ks[kk * KLD + kd])[u] = r[u];
+            for (int u = 0; u < KNP; u++)
+                if (kk < (uint32_t)KPP && kk + u * KPP < (uint32_t)FA_TK) *(v4u *)&ks[(kk + u * KPP) * KLD + kd] = r[u];
         }
-        if (vkg < FA_TK / 8) {
+        if (vdc < (uint32_t)VDC) {
             v4u r[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
