@@ -183,6 +183,11 @@ __device__ __forceinline__ void stage_issue(const sgk_gemv &a, xstage<PRO, NT, K
 // float4s land in different banks (the 65th float4 of a plane is padding).
 // Without CH (the f32 GEMV) x is linear.
 #define XS_CH_BLK 260
+// k_gemv_q8 stages x chunked behind a prologue (RMSNorm, gated norm) and
+// linearly without one: the prologue-less GEMVs here (output and, at 2B, down
+// projections) run about one row group per wave, and were 5-8% slower chunked
+// (the conflict-free inner loop gains nothing there).
+#define GEMV_CH(PRO) ((PRO) != SGK_PRO_NONE)
 __host__ __device__ __forceinline__ uint32_t xs_ch_floats(uint32_t cols) {
     return ((cols / 16 + 63) / 64) * XS_CH_BLK * 4;
 }
@@ -337,17 +342,18 @@ __device__ __forceinline__ void gemv_load(gemv_chunk<R> &ch, const int8_t *qs, c
     }
 }
 
-template <int R>
+template <int R, bool CH>
 __device__ __forceinline__ void gemv_fma(float *acc, const gemv_chunk<R> &ch, const float *xs, uint32_t c) {
-    const float4 *xa = (const float4 *)xs + (c >> 6) * XS_CH_BLK + (c & 63);     // xs4_at<true>
-    const float4 a0 = xa[0], a1 = xa[65], a2 = xa[130], a3 = xa[195];
+    const float4 *xa = CH ? (const float4 *)xs + (c >> 6) * XS_CH_BLK + (c & 63) : (const float4 *)xs + 4 * c;
+    const float4 a0 = xa[0], a1 = xa[CH ? 65 : 1], a2 = xa[CH ? 130 : 2], a3 = xa[CH ? 195 : 3];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = fmaf(h2f(ch.d[r]), dot16(ch.q[r], a0, a1, a2, a3), acc[r]);
 }
 
 // One row group of R rows: every chunk of the rows, two chunks per step, the
-// first chunk optionally already loaded (pre). post scales each row sum.
-template <int R, int EPI, bool PRE>
+// first chunk optionally already loaded (pre). post scales each row sum. CH:
+// x staged in the chunked layout (xs4_at<true>), else linear.
+template <int R, int EPI, bool PRE, bool CH>
 __device__ __forceinline__ void gemv_group(const sgk_gemv &a, const float *xs, uint32_t g, uint32_t lane,
                                            const gemv_chunk<R> *pre, float post) {
     const uint32_t cols = a.cols, nch = cols >> 4, r0 = g * R;
@@ -356,20 +362,20 @@ __device__ __forceinline__ void gemv_group(const sgk_gemv &a, const float *xs, u
     for (int r = 0; r < R; r++) acc[r] = 0.0f;
     uint32_t c = lane;
     if (PRE) {
-        if (c < nch) gemv_fma<R>(acc, *pre, xs, c);
+        if (c < nch) gemv_fma<R, CH>(acc, *pre, xs, c);
         c += 64;
     }
     for (; c + 64 < nch; c += 128) {
         gemv_chunk<R> ca, cb;
         gemv_load<R>(ca, a.qs, a.d, r0, a.rows, cols, c);
         gemv_load<R>(cb, a.qs, a.d, r0, a.rows, cols, c + 64);
-        gemv_fma<R>(acc, ca, xs, c);
-        gemv_fma<R>(acc, cb, xs, c + 64);
+        gemv_fma<R, CH>(acc, ca, xs, c);
+        gemv_fma<R, CH>(acc, cb, xs, c + 64);
     }
     if (c < nch) {
         gemv_chunk<R> ca;
         gemv_load<R>(ca, a.qs, a.d, r0, a.rows, cols, c);
-        gemv_fma<R>(acc, ca, xs, c);
+        gemv_fma<R, CH>(acc, ca, xs, c);
     }
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]) * post;
@@ -398,10 +404,10 @@ __global__ void __launch_bounds__(TPB) k_gemv_q8(sgk_gemv a) {
     stage_issue<PRO, TPB, XK>(a, st);
     gemv_chunk<R> pre;
     if (have && lane < nch) gemv_load<R>(pre, a.qs, a.d, g * R, a.rows, a.cols, lane);
-    const float post = stage_finish<PRO, TPB, XK, true>(a, st, xs);
+    const float post = stage_finish<PRO, TPB, XK, GEMV_CH(PRO)>(a, st, xs);
     if (!have) return;
-    gemv_group<R, EPI, true>(a, xs, g, lane, &pre, post);
-    for (g += gstride; g < ngroups; g += gstride) gemv_group<R, EPI, false>(a, xs, g, lane, nullptr, post);
+    gemv_group<R, EPI, true, GEMV_CH(PRO)>(a, xs, g, lane, &pre, post);
+    for (g += gstride; g < ngroups; g += gstride) gemv_group<R, EPI, false, GEMV_CH(PRO)>(a, xs, g, lane, nullptr, post);
 }
 
 
@@ -716,7 +722,7 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         hipLaunchKernelGGL(kern, dim3(blocks), dim3(LTPB), lds, s, *a);
         return hipGetLastError();
     }
-    const size_t lds = (size_t)xs_ch_floats(a->cols) * 4;
+    const size_t lds = GEMV_CH(PRO) ? (size_t)xs_ch_floats(a->cols) * 4 : (size_t)a->cols * 4;
     const int R = EPI == SGK_EPI_SWIGLU ? 2 : (a->tune_r == 1 ? 1 : (a->tune_r == 4 || a->tune_r == 8) ? 4 : 2);
     if (R == 4) return launch_q8<4, PRO, EPI>(*a, lds, s);
     if (R == 1) return launch_q8<1, PRO, (EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI)>(*a, lds, s);
