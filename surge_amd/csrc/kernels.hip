@@ -1798,12 +1798,18 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
         const uint32_t k = kg + (uint32_t)u * KG;
         v[u] = k < ns ? acc[(size_t)k * C4 + c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+    // the output gate of this thread's four dims, last (it is needed last)
+    float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (gate && t < (uint32_t)C4) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) gv[e] = gate[4 * t + e];
+    }
     float mx = m0;
     for (uint32_t k = t + TPB; k < ns; k += TPB) mx = fmaxf(mx, mh[k]);
     mx = wave_max(mx);
     if ((t & 63) == 0) red[t >> 6] = mx;
     __syncthreads();
-    if (t == 0) bc = (ns && isnan(mh[0])) ? mh[0] : fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (t == 0) bc = (ns && isnan(m0)) ? m0 : fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));   // m0 = mh[0] here
     __syncthreads();
     const float M = bc;
     if (ns == 0 || M == -INFINITY || isnan(M)) {
@@ -1862,7 +1868,7 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
         float o;
         if (isnan(S)) o = S;
         else o = S > 0.0f ? tv[e] / S : 0.0f;
-        if (gate) o *= sigm(gate[dd]);
+        if (gate) o *= sigm(gv[e]);
         oh[dd] = o;
     }
 }
@@ -2293,6 +2299,7 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
     uint32_t ch = chan(min(t, nch - 1));
     conv_loads(ch);
     const float zraw = a.z[(size_t)h * dv + min(max(t, jlo), jhi - 1)];
+    const float nwt = NB == 1 ? a.norm_w[min(t, dv - 1)] : 0.0f;   // needed last, loaded early
     const float *bb = a.in + cd + a.n_v * dv, *aa = bb + a.n_v;
     const float gb = bb[h], ga = aa[h], gA = a.ssm_a[h], gdt = a.dt_bias[h];
     const uint32_t j0 = jlo + wave * RW;
@@ -2408,7 +2415,7 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
         const float r = 1.0f / sqrtf(tot / (float)dv + a.eps);
         if (t < dv) {
             const float yv = ysh[t];
-            a.out[(size_t)h * dv + t] = silu(zj) * ((yv * r) * a.norm_w[t]);
+            a.out[(size_t)h * dv + t] = silu(zj) * ((yv * r) * nwt);
         }
         return;
     }
