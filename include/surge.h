@@ -158,6 +158,8 @@ void sg_model_free(sg_model *m);                                     /* surge.h:
  *                     p: [0]=dv [1]=heads [2]=eps bits
  *   k_matmul_q8       X[N*K] f32            W Q8_0 M*(K/32)      Y[N*M] f32
  *                     p: [0]=N [1]=M [2]=K
+ *   k_argmax          v[n] f32              -                    u32 index (no reference
+ *                     counterpart: the greedy loop's device argmax, = sg_argmax_f32)
  * Aliasing: out must not overlap a or b, except k_conv1d_step's state tail
  * and k_delta_step's in-place S (surge.h:709-712). */
 typedef struct sg_gpu sg_gpu;
@@ -186,7 +188,6 @@ sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
  * p: [0]=n_heads [1]=n_kv [2]=hd [3]=seq [4]=q_stride [5]=scale bits. */
 sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out,
                                   const uint32_t params[8]);
-
 /* Split-K decode attention (surge.h:890-980). Split i covers
  * [i*seq/n, (i+1)*seq/n); m, s f32 [n_heads, n_splits]; acc f32
  * [n_heads, n_splits, hd]. p: [0]=n_heads [1]=n_kv [2]=hd [3]=seq
@@ -201,14 +202,13 @@ sg_err sg_gpu_run_attn_splitk_partial_gqa(sg_gpu *g, void *q, void *k, void *v,
 sg_err sg_gpu_run_attn_splitk_combine(sg_gpu *g, void *m, void *s, void *acc,
                                       void *out, const uint32_t params[8]);
 
-/* The online-softmax arm (surge.h:974-1050): the partial kernel here is the
- * online form already, so these are the same kernel and the same counts. */
+/* The online-softmax partial (surge.h:974-980): the partial kernel here is
+ * the online form already, so this one-shot is the GQA one and gives its
+ * bytes (the reference's online kernel differs from its four-pass one in the
+ * last bits). */
 sg_err sg_gpu_run_attn_splitk_partial_gqa_online(sg_gpu *g, void *q, void *k, void *v,
                                                  void *m, void *s, void *acc,
                                                  const uint32_t params[8]);
-bool sg_gpu_splitk_online_selected(const sg_gpu *g, uint32_t n_heads,
-                                   uint32_t n_kv_heads, uint32_t seq);
-uint64_t sg_gpu_splitk_online_dispatches(const sg_gpu *g);
 
 /* Causal chunk attention (surge.h:787-788): q f32 [n, n_heads, q_stride];
  * k, v f16 [base+n, n_kv, hd] already holding base+n positions; out f32
@@ -217,14 +217,35 @@ uint64_t sg_gpu_splitk_online_dispatches(const sg_gpu *g);
 sg_err sg_gpu_run_attn_prefill(sg_gpu *g, void *q, void *k, void *v, void *out,
                                const uint32_t params[8]);
 
-/* Split-count policy (surge.h:1020-1106), re-derived for 256 CUs. */
-uint32_t sg_gpu_splitk_n_splits(uint32_t seq);
-uint32_t sg_gpu_splitk_gqa_n_splits(uint32_t seq);
-uint32_t sg_gpu_splitk_gqa_n_splits_at(const sg_gpu *g, uint32_t seq);
-uint32_t sg_gpu_splitk_gqa_cap(const sg_gpu *g);
+/* Decode attention selection (surge.h:1011-1106, 1179-1254). Read at
+ * sg_gpu_state_new:
+ *   SURGE_KV_DTYPE           f16 (default); f32 is refused (no f32 cache is
+ *                            built); anything else warns and keeps f16;
+ *   SURGE_ATTN_SPLITK        1 (default) split-K; 0 one split per head (the
+ *                            single-pass form, counted in neither counter);
+ *   SURGE_ATTN_SPLITK_GQA    1 (default) the partial shared by a GQA group
+ *                            (group in [2, 8]); 0 the per-head partial (same
+ *                            bytes); unrecognised values warn, keep 1;
+ *   SURGE_ATTN_SPLITK_ONLINE exactly 0 (default) or 1, else refused; 1 counts
+ *                            the dispatches as the online arm (same kernel:
+ *                            the partial is the online form) and the GQA
+ *                            predicate then answers false;
+ *   SURGE_SPLITK_GQA_CAP     the split cap, plain digits in [4, 1024].
+ * The arm is fixed per state: the MI355X policy has no occupancy floor, so
+ * `seq` does not change the answers. The counters count what sg_gpu_forward
+ * and sg_gpu_decode_greedy encoded since the last sg_gpu_state_new, one per
+ * attention layer per step; one-shots are not counted. */
+uint32_t sg_gpu_splitk_n_splits(uint32_t seq);                     /* surge.h:1106 */
+uint32_t sg_gpu_splitk_gqa_n_splits(uint32_t seq);                 /* surge.h:1081 */
+uint32_t sg_gpu_splitk_gqa_n_splits_at(const sg_gpu *g, uint32_t seq); /* surge.h:1104 */
+uint32_t sg_gpu_splitk_gqa_cap(const sg_gpu *g);                   /* surge.h:1105 */
 bool sg_gpu_splitk_gqa_selected(const sg_gpu *g, uint32_t n_heads,
-                                uint32_t n_kv_heads, uint32_t seq);
-void sg_gpu_splitk_dispatch_counts(const sg_gpu *g, uint64_t *per_head, uint64_t *gqa);
+                                uint32_t n_kv_heads, uint32_t seq); /* surge.h:1020 */
+void sg_gpu_splitk_dispatch_counts(const sg_gpu *g, uint64_t *per_head, uint64_t *gqa); /* surge.h:1022 */
+bool sg_gpu_splitk_online_selected(const sg_gpu *g, uint32_t n_heads,
+                                   uint32_t n_kv_heads, uint32_t head_dim,
+                                   uint32_t seq);                   /* surge.h:1047 */
+uint64_t sg_gpu_splitk_online_dispatches(const sg_gpu *g);          /* surge.h:1050 */
 
 /* DeltaNet one-shots (surge.h:1133-1142). k_delta_multi: S [n_v, dv, dk]
  * in/out, qkv [conv_dim] (post conv+silu, pre norm), out [value_dim], gates
@@ -233,6 +254,17 @@ void sg_gpu_splitk_dispatch_counts(const sg_gpu *g, uint64_t *per_head, uint64_t
  * reference's k_delta_multi (kernels.metal:764-805). */
 sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *gates,
                               const uint32_t params[8]);
+/* The decode path's fused DeltaNet layer step on caller buffers (no
+ * reference counterpart: the reference's decode kernels k_conv1d_step,
+ * k_delta_gates, k_delta_multi and k_rmsnorm_gated are one kernel here).
+ *   in    [conv_dim + value_dim + 2 n_v]   qkv (before the conv) | z | b | a
+ *   w     [conv_dim ksize + 2 n_v + dv]    conv_w | ssm_a | dt_bias | ssm_norm
+ *   state [(ksize-1) conv_dim + n_v dv dk] conv tail (oldest first) | S, in/out
+ *   out   [value_dim]                      silu(z) * rmsnorm(y, ssm_norm)
+ * p: [0]=dk [1]=dv [2]=n_v [3]=n_k [4]=ksize [5]=tiled [6]=ssm_a is -exp(A_log)
+ * [7]=eps bits; conv_dim = 2 n_k dk + n_v dv; dv <= 128. */
+sg_err sg_gpu_run_gdn_step(sg_gpu *g, void *in, void *w, void *state, void *out,
+                           const uint32_t params[8]);
 /* Prefill chunk hooks (surge.h:1111-1142), reference layouts:
  *   conv1d_chunk: x [n_tok, ch], w [ch, ksize], out [n_tok, ch], state
  *     [ksize-1, ch] oldest-first in/out; no activation. p: [0]=ch [1]=ksize [2]=n_tok
@@ -311,6 +343,33 @@ uint64_t sg_kv_bytes(const sg_cfg *c, uint32_t cap, sg_tensor_type dtype); /* su
 uint64_t sg_kv_state_bytes(const sg_cfg *c);                               /* surge.h:1457 */
 uint16_t sg_f32_to_f16(float f);                                           /* surge.h:1463 */
 float    sg_f16_to_f32(uint16_t h);                                        /* surge.h:1464 */
+
+/* The KV / DeltaNet-state allocation module (surge.h:1466-1501). Buffers come
+ * from an injected backend; sg_gpu_init registers sg_gpu_alloc,
+ * sg_gpu_buf_free and sg_gpu_buf_host (reference metal.m:627-633). The alloc
+ * must zero-fill. A full-attention layer has separate K and V of
+ * [cap, n_kv_heads, head_dim] in kv_dtype (f16 or f32); a DeltaNet layer a
+ * conv tail [conv_kernel-1, conv_dim] and S [n_v_heads, head_v_dim,
+ * head_k_dim] in f32. cap 0 means SG_KV_CAP_DEFAULT; above SG_KV_CAP_MAX is
+ * refused. sg_kv_reset zeroes the conv tails and S through their host views
+ * and leaves K/V; sg_kv_advance refuses to pass cap. The getters return NULL
+ * for the other kind of layer or a layer out of range. */
+typedef struct sg_kv sg_kv;
+typedef sg_err (*sg_kv_alloc_fn)(sg_gpu *g, uint64_t nbytes, void **buf, void **host);
+typedef void   (*sg_kv_free_fn)(void *buf);
+typedef void  *(*sg_kv_host_fn)(void *buf);
+void sg_kv_set_backend(sg_kv_alloc_fn alloc, sg_kv_free_fn free_, sg_kv_host_fn host); /* surge.h:1474 */
+sg_err sg_kv_new(sg_gpu *g, const sg_cfg *c, uint32_t cap,
+                 sg_tensor_type kv_dtype, sg_kv **out);            /* surge.h:1481 */
+void sg_kv_free(sg_kv *kv);                                        /* surge.h:1483 */
+void sg_kv_reset(sg_kv *kv);                                       /* surge.h:1487 */
+sg_err sg_kv_advance(sg_kv *kv, uint32_t n);                       /* surge.h:1491 */
+uint32_t sg_kv_used(const sg_kv *kv);                              /* surge.h:1492 */
+uint32_t sg_kv_cap(const sg_kv *kv);                               /* surge.h:1493 */
+void *sg_kv_k(const sg_kv *kv, uint32_t layer);                    /* surge.h:1498 */
+void *sg_kv_v(const sg_kv *kv, uint32_t layer);                    /* surge.h:1499 */
+void *sg_kv_conv(const sg_kv *kv, uint32_t layer);                 /* surge.h:1500 */
+void *sg_kv_s(const sg_kv *kv, uint32_t layer);                    /* surge.h:1501 */
 
 /* ---------------------------------------------------------------------
  * Greedy argmax (surge.h:1503-1512): lowest index wins an exact tie.

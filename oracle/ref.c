@@ -521,6 +521,53 @@ void sg_ref_state_reset(sg_ref_state *st) {
 
 void sg_ref_state_set_kv_f16(sg_ref_state *st, bool on) { if (st) st->kv_f16 = on; }
 
+/* Test input, not part of the reference: the seeded decode state that the
+ * product's sg_gpu_state_fill_synthetic writes (K/V rows [0, n) of every
+ * attention layer, every DeltaNet S and conv tail), generated by the same
+ * integer hash and the same f32 operations, so a decode step at depth can be
+ * compared with the GPU's. Element i of a fill with seed s and scale c is
+ * ((u0 + u1) - 1) * c with u0, u1 the low two 16-bit fields of
+ * splitmix64((i + 1) * 0x9E3779B97F4A7C15 ^ (s << 32 | s)) divided by 65535;
+ * K/V values are then rounded to f16. The GPU keeps K/V head-major and the
+ * conv tail as a 4-slot ring indexed by position mod 4; this maps both onto
+ * this state's layouts (K/V [pos][n_kv][hd]; conv tail oldest first, row j
+ * taken from ring slot (n + 4 - (ksize-1) + j) mod 4). */
+static float fill_val(uint64_t i, uint32_t seed, float scale) {
+    uint64_t h = (i + 1) * 0x9E3779B97F4A7C15ull ^ ((uint64_t)seed << 32 | seed);
+    h ^= h >> 31; h *= 0xBF58476D1CE4E5B9ull; h ^= h >> 29; h *= 0x94D049BB133111EBull; h ^= h >> 32;
+    const float u0 = (float)(uint32_t)(h & 0xFFFFu) / 65535.0f, u1 = (float)(uint32_t)((h >> 16) & 0xFFFFu) / 65535.0f;
+    return (u0 + u1 - 1.0f) * scale;
+}
+
+sg_err sg_ref_state_fill_synthetic(sg_ref_state *st, uint32_t n, uint32_t seed) {
+    if (!st) return (sg_err){"ref: invalid arguments"};
+    if (n >= st->max_ctx) return (sg_err){"ref: fill: n must be < max_ctx"};
+    const sg_cfg *c = &st->c;
+    const uint32_t nkv = c->n_kv_heads, hd = c->head_dim, cd = st->conv_dim, keep = c->conv_kernel - 1;
+    for (uint32_t i = 0; i < c->n_layers; i++) {
+        ref_layer *L = &st->L[i];
+        const uint32_t ls = seed * 2654435761u + 97u * i;
+        if (L->attn) {
+            for (uint32_t h = 0; h < nkv; h++)
+                for (uint64_t e = 0; e < (uint64_t)n * hd; e++) {
+                    const size_t at = ((size_t)(e / hd) * nkv + h) * hd + e % hd;
+                    L->kc[at] = sg_ref_f16_to_f32(sg_ref_f32_to_f16(fill_val(e, ls + 2 * h, 2.0f)));
+                    L->vc[at] = sg_ref_f16_to_f32(sg_ref_f32_to_f16(fill_val(e, ls + 2 * h + 1, 2.0f)));
+                }
+        } else {
+            const uint64_t ns = (uint64_t)c->n_v_heads * c->head_v_dim * c->head_k_dim;
+            for (uint64_t e = 0; e < ns; e++) L->S[e] = fill_val(e, ls + 7, 0.05f);
+            for (uint32_t j = 0; j < keep; j++) {
+                const uint32_t slot = (n + 4 - keep + j) & 3;
+                for (uint32_t ch = 0; ch < cd; ch++)
+                    L->conv[(size_t)j * cd + ch] = fill_val((uint64_t)slot * cd + ch, ls + 11, 0.05f);
+            }
+        }
+    }
+    st->used = n;
+    return SG_OK;
+}
+
 /* Validation follows ref.c:965-1189: dims non-zero, layer kind by tensor
  * presence must agree with (L+1) % interval, rope/eps sanity, Q8_0 widths. */
 sg_err sg_ref_state_new(const sg_model *m, uint32_t max_ctx, sg_ref_state **out) {

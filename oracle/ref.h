@@ -74,6 +74,9 @@ sg_err sg_ref_forward(sg_ref_state *st, const sg_model *m, int32_t token,
  * GPU-vs-oracle comparison can separate the KV storage rounding from
  * everything else. Off by default (the reference keeps f32 K/V). */
 void sg_ref_state_set_kv_f16(sg_ref_state *st, bool on);
+/* Test input: the seeded state sg_gpu_state_fill_synthetic writes, in this
+ * state's layouts; the next forward is at position n. */
+sg_err sg_ref_state_fill_synthetic(sg_ref_state *st, uint32_t n, uint32_t seed);
 
 uint16_t sg_ref_f32_to_f16(float f);                 /* kv.c:152-190 */
 uint32_t sg_ref_argmax_f32(const float *v, uint32_t n);  /* greedy.c:17-27 */

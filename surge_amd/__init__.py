@@ -110,7 +110,12 @@ _SIGS = {
     "sg_gpu_run_rmsnorm_gated_chunk": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_run_attn_prefill": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_run_attn_splitk_partial_gqa_online": (SgErr, [C.c_void_p] * 7 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_run_gdn_step": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_splitk_online_dispatches": (C.c_uint64, [C.c_void_p]),
+    "sg_gpu_splitk_online_selected": (C.c_bool, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32,
+                                                 C.c_uint32]),
+    "sg_gpu_splitk_gqa_selected": (C.c_bool, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32]),
+    "sg_gpu_splitk_dispatch_counts": (None, [C.c_void_p, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "sg_gpu_prefill_segments": (C.c_uint64, [C.c_void_p]),
     "sg_gpu_splitk_n_splits": (C.c_uint32, [C.c_uint32]),
     "sg_gpu_splitk_gqa_n_splits": (C.c_uint32, [C.c_uint32]),
@@ -138,6 +143,16 @@ _SIGS = {
     "sg_model_free": (None, [C.POINTER(SgModel)]),
     "sg_kv_bytes": (C.c_uint64, [C.POINTER(SgCfg), C.c_uint32, C.c_int]),
     "sg_kv_state_bytes": (C.c_uint64, [C.POINTER(SgCfg)]),
+    "sg_kv_new": (SgErr, [C.c_void_p, C.POINTER(SgCfg), C.c_uint32, C.c_int, C.POINTER(C.c_void_p)]),
+    "sg_kv_free": (None, [C.c_void_p]),
+    "sg_kv_reset": (None, [C.c_void_p]),
+    "sg_kv_advance": (SgErr, [C.c_void_p, C.c_uint32]),
+    "sg_kv_used": (C.c_uint32, [C.c_void_p]),
+    "sg_kv_cap": (C.c_uint32, [C.c_void_p]),
+    "sg_kv_k": (C.c_void_p, [C.c_void_p, C.c_uint32]),
+    "sg_kv_v": (C.c_void_p, [C.c_void_p, C.c_uint32]),
+    "sg_kv_conv": (C.c_void_p, [C.c_void_p, C.c_uint32]),
+    "sg_kv_s": (C.c_void_p, [C.c_void_p, C.c_uint32]),
     "sg_f32_to_f16": (C.c_uint16, [C.c_float]),
     "sg_f16_to_f32": (C.c_float, [C.c_uint16]),
     "sg_argmax_f32": (C.c_uint32, [C.POINTER(C.c_float), C.c_uint32]),
@@ -254,6 +269,22 @@ class Gpu:
     def attn_decode_f16(self, q, k, v, out, p):
         check(lib().sg_gpu_run_attn_decode_f16(self.handle, q.handle, k.handle, v.handle,
                                                out.handle, params(p)))
+
+    def gdn_step(self, inp, w, state, out, p):
+        check(lib().sg_gpu_run_gdn_step(self.handle, inp.handle, w.handle, state.handle, out.handle,
+                                         params(p)))
+
+    def dispatch_counts(self):
+        """(per_head, gqa, online) partial dispatches encoded since sg_gpu_state_new."""
+        ph, gq = C.c_uint64(), C.c_uint64()
+        lib().sg_gpu_splitk_dispatch_counts(self.handle, C.byref(ph), C.byref(gq))
+        return ph.value, gq.value, lib().sg_gpu_splitk_online_dispatches(self.handle)
+
+    def gqa_selected(self, nh, nkv, seq) -> bool:
+        return bool(lib().sg_gpu_splitk_gqa_selected(self.handle, nh, nkv, seq))
+
+    def online_selected(self, nh, nkv, hd, seq) -> bool:
+        return bool(lib().sg_gpu_splitk_online_selected(self.handle, nh, nkv, hd, seq))
 
     def delta_multi(self, S, qkv, out, gates, p):
         check(lib().sg_gpu_run_delta_multi(self.handle, S.handle, qkv.handle, out.handle,

@@ -118,11 +118,29 @@ struct sg_gpu {
     uint16_t *pf_XS;        /* the prefill GEMMs' X split into bf16 hi | lo */
     float *pf_PART;         /* split-K partials of the narrow prefill GEMMs: 4 x chunk x hidden */
 
+    /* the pinned step descriptor's upload: the next write to h_step waits
+     * for it (event recorded after each upload) */
+    hipEvent_t step_ev;
+    bool step_pending;
+
+    /* decode attention selection, read from the environment at
+     * sg_gpu_state_new (reference surge.h:1179-1254), and what the decode
+     * path has encoded since (one per attention layer per step) */
+    bool attn_splitk, attn_gqa, attn_online;
+    int attn_arm;
+    uint64_t n_per_head, n_gqa, n_online;
+
     /* one-shot scratch */
     void *tmp;
     uint64_t tmp_bytes;
-    uint64_t splitk_gqa_dispatches;
 };
+
+/* The decode attention partial a state dispatches (fixed per state: the
+ * MI355X policy does not change the arm with depth). */
+enum { ARM_SINGLE = 0,      /* SURGE_ATTN_SPLITK=0: one split per head, no split-K */
+       ARM_PER_HEAD,        /* split-K, one workgroup per (split, query head) */
+       ARM_GQA,             /* split-K, one workgroup per (split, kv head) */
+       ARM_ONLINE };        /* SURGE_ATTN_SPLITK_ONLINE=1: the same kernel, counted apart */
 
 /* ---------------------------------------------------------------------
  * allocation bookkeeping
@@ -189,6 +207,10 @@ sg_err sg_gpu_init(sg_gpu **out) {
     }
     const char *ev = getenv("SURGE_HIP_GRAPH");
     g->use_graph = !(ev && strcmp(ev, "0") == 0);
+    g->attn_splitk = g->attn_gqa = true;       /* the defaults until a state reads the environment */
+    g->attn_online = false;
+    /* The KV module allocates through this library (reference metal.m:627-633). */
+    sg_kv_set_backend(sg_gpu_alloc, sg_gpu_buf_free, sg_gpu_buf_host);
     *out = g;
     return SG_OK;
 }
@@ -462,6 +484,15 @@ sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
         const float *zb = DEV(b);
         return finish(g, sgk_rmsnorm_gated(DEV(a), zb, zb + (uint64_t)dv * nh, DEV(out), dv, nh, fbits(p[2]), s), outs, 1);
     }
+    if (!strcmp(kernel, "k_argmax")) {
+        /* the greedy loop's device argmax: out[0] = sg_argmax_f32(a, n) */
+        if (!n) return (sg_err){"gpu: k_argmax: n is zero"};
+        if (sg_failed(e = need(a, (uint64_t)n * 4, "v")) || sg_failed(e = need(out, 4, "out"))) return e;
+        if (sg_failed(e = push(ins, 3))) return e;
+        void *t;
+        if (sg_failed(e = scratch(g, 4096, &t))) return e;
+        return finish(g, sgk_argmax(DEV(a), n, DEV(out), t, s), outs, 1);
+    }
     if (!strcmp(kernel, "k_matmul_q8")) {
         uint32_t N = p[0], M = p[1], K = p[2];
         if (!N || !M || !K || K % 32) return (sg_err){"gpu: k_matmul_q8: bad shape (K must be a nonzero multiple of 32)"};
@@ -487,20 +518,23 @@ sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
  * attention one-shots (surge.h:774-980)
  * --------------------------------------------------------------------- */
 
-static sg_err attn_check(const uint32_t p[8], bool need_splits) {
+static sg_err attn_check(const uint32_t p[8], bool need_splits, bool per_head) {
     uint32_t nh = p[0], nkv = p[1], hd = p[2], qs = p[4];
     if (!nh || !nkv || nh % nkv) return (sg_err){"gpu: n_heads must be a nonzero multiple of n_kv_heads"};
-    if (nh / nkv > 8) return (sg_err){"gpu: GQA group wider than 8 is not supported"};
+    if (!per_head && nh / nkv > 8) return (sg_err){"gpu: GQA group wider than 8 is not supported"};
     if (hd != 16 && hd != 32 && hd != 64 && hd != 128 && hd != 256) return (sg_err){"gpu: head_dim must be 16, 32, 64, 128 or 256"};
     if (qs < hd) return (sg_err){"gpu: q_stride < head_dim"};
     if (need_splits && (!p[6] || p[6] > 1024)) return (sg_err){"gpu: n_splits must be in [1, 1024]"};
     return SG_OK;
 }
 
-sg_err sg_gpu_run_attn_splitk_partial_gqa(sg_gpu *g, void *q, void *k, void *v, void *m,
-                                          void *s, void *acc, const uint32_t p[8]) {
+/* One split-K partial launch over caller buffers: the decode kernel with q
+ * taken as given (no norm, RoPE or K/V store). One-shots are not counted in
+ * the decode dispatch counters (reference surge.h:1011-1017). */
+static sg_err attn_partial_oneshot(sg_gpu *g, void *q, void *k, void *v, void *m, void *s, void *acc,
+                                   const uint32_t p[8], bool per_head) {
     if (!g || !q || !k || !v || !m || !s || !acc || !p) return (sg_err){"gpu: attention one-shot got a NULL argument"};
-    sg_err e = attn_check(p, true);
+    sg_err e = attn_check(p, true, per_head);
     if (sg_failed(e)) return e;
     uint32_t nh = p[0], nkv = p[1], hd = p[2], seq = p[3], qs = p[4], ns = p[6];
     uint64_t kvb = (uint64_t)seq * nkv * hd * 2;
@@ -514,19 +548,23 @@ sg_err sg_gpu_run_attn_splitk_partial_gqa(sg_gpu *g, void *q, void *k, void *v, 
             overlap(outs[i], outs[(i + 1) % 3])) return (sg_err){"gpu: attention outputs must not overlap"};
     void *ins[3] = {q, k, v};
     if (sg_failed(e = push(ins, 3))) return e;
-    g->splitk_gqa_dispatches++;
     sgk_attn A = {0};
     A.q = DEV(q); A.kc = DEV(k); A.vc = DEV(v); A.m = DEV(m); A.s = DEV(s); A.acc = DEV(acc);
     A.n_heads = nh; A.n_kv = nkv; A.hd = hd; A.q_stride = qs; A.seq = seq; A.n_splits = ns; A.max_splits = ns;
-    A.ntok = 1; A.scale = fbits(p[5]);
+    A.ntok = 1; A.scale = fbits(p[5]); A.per_head = per_head;
     return finish(g, sgk_attn_partial(&A, g->stream), outs, 3);
 }
 
+sg_err sg_gpu_run_attn_splitk_partial_gqa(sg_gpu *g, void *q, void *k, void *v, void *m,
+                                          void *s, void *acc, const uint32_t p[8]) {
+    return attn_partial_oneshot(g, q, k, v, m, s, acc, p, false);
+}
+
+/* The per-head partial (reference kernels_splitk.metal:156-267): one
+ * workgroup per (split, query head). Same bytes as the GQA form. */
 sg_err sg_gpu_run_attn_splitk_partial(sg_gpu *g, void *q, void *k, void *v, void *m, void *s,
                                       void *acc, const uint32_t p[8]) {
-    /* One kernel serves every GQA group size; the per-head and GQA partials
-     * of the reference produce the same bytes, and so do these. */
-    return sg_gpu_run_attn_splitk_partial_gqa(g, q, k, v, m, s, acc, p);
+    return attn_partial_oneshot(g, q, k, v, m, s, acc, p, true);
 }
 
 sg_err sg_gpu_run_attn_splitk_combine(sg_gpu *g, void *m, void *s, void *acc, void *out,
@@ -547,23 +585,25 @@ sg_err sg_gpu_run_attn_splitk_combine(sg_gpu *g, void *m, void *s, void *acc, vo
     return finish(g, sgk_attn_combine(&A, g->stream), outs, 1);
 }
 
-sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out,
-                                  const uint32_t p[8]) {
-    /* Single-pass decode attention: the split-K pair with one split per 64
-     * keys, combined, in one call. p: [0]=nh [1]=nkv [2]=hd [3]=seq [4]=q_stride [5]=scale. */
+/* Single-pass decode attention: the split-K pair with the decode policy's
+ * split count, combined, in one call. p: [0]=nh [1]=nkv [2]=hd [3]=seq
+ * [4]=q_stride [5]=scale. The partials go to the gpu's lazily grown one-shot
+ * scratch. */
+static sg_err attn_decode_oneshot(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8]) {
     if (!g || !q || !k || !v || !out || !p) return (sg_err){"gpu: attention one-shot got a NULL argument"};
     uint32_t pp[8];
     memcpy(pp, p, sizeof pp);
     pp[6] = sgk_n_splits(p[3]);
-    sg_err e = attn_check(pp, true);
+    sg_err e = attn_check(pp, true, false);
     if (sg_failed(e)) return e;
     uint32_t nh = pp[0], nkv = pp[1], hd = pp[2], seq = pp[3], qs = pp[4], ns = pp[6];
     uint64_t kvb = (uint64_t)seq * nkv * hd * 2;
     if (sg_failed(e = need(q, ((uint64_t)(nh - 1) * qs + hd) * 4, "q")) ||
         (seq && (sg_failed(e = need(k, kvb, "k")) || sg_failed(e = need(v, kvb, "v")))) ||
         sg_failed(e = need(out, (uint64_t)nh * hd * 4, "out"))) return e;
+    const uint64_t wsb = (uint64_t)nh * ns * (2 + hd) * 4;
     void *t;
-    if (sg_failed(e = scratch(g, (uint64_t)nh * ns * (2 + hd) * 4, &t))) return e;
+    if (sg_failed(e = scratch(g, wsb, &t))) return e;
     float *mm = t, *ss = mm + (uint64_t)nh * ns, *aa = ss + (uint64_t)nh * ns;
     void *ins[3] = {q, k, v}, *outs[1] = {out};
     if (sg_failed(e = push(ins, 3))) return e;
@@ -574,6 +614,10 @@ sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *ou
     hipError_t he = sgk_attn_partial(&A, g->stream);
     if (he == hipSuccess) he = sgk_attn_combine(&A, g->stream);
     return finish(g, he, outs, 1);
+}
+
+sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8]) {
+    return attn_decode_oneshot(g, q, k, v, out, p);
 }
 
 /* Split policy (surge.h:1020-1106), re-derived for 256 CUs: see kernels.h. */
@@ -587,14 +631,34 @@ uint32_t sg_gpu_splitk_gqa_cap(const sg_gpu *g) {
 uint32_t sg_gpu_splitk_gqa_n_splits_at(const sg_gpu *g, uint32_t seq) {
     return sgk_n_splits_cap(seq, sg_gpu_splitk_gqa_cap(g));
 }
-bool sg_gpu_splitk_gqa_selected(const sg_gpu *g, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq) {
+/* The selection predicates (reference surge.h:1011-1050) answer from the
+ * state's switches (SURGE_ATTN_SPLITK, _GQA, _ONLINE, read at
+ * sg_gpu_state_new; before any state, the defaults 1, 1, 0). The group must
+ * be in [2, 8]; the online arm also needs head_dim in [1, 256] and, when
+ * its switch is on, takes the dispatch from the GQA arm for the state's
+ * head_dim, so the two never both claim one. Unlike the reference, whose
+ * measured floor of 128 threadgroups leaves short contexts to the per-head
+ * partial, the MI355X policy has no floor: `seq` does not change the
+ * answer. */
+static bool gqa_band(uint32_t n_heads, uint32_t n_kv_heads) {
+    return n_kv_heads && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads >= 2 && n_heads / n_kv_heads <= 8;
+}
+bool sg_gpu_splitk_online_selected(const sg_gpu *g, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                                   uint32_t seq) {
     (void)seq;
-    return g && n_kv_heads && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8;
+    return g && g->attn_splitk && g->attn_online && gqa_band(n_heads, n_kv_heads) && head_dim >= 1 &&
+           head_dim <= 256;
+}
+bool sg_gpu_splitk_gqa_selected(const sg_gpu *g, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq) {
+    if (!g || !g->attn_splitk || !g->attn_gqa || !gqa_band(n_heads, n_kv_heads)) return false;
+    const uint32_t hd = g->model ? g->cfg.head_dim : 0;
+    return !sg_gpu_splitk_online_selected(g, n_heads, n_kv_heads, hd, seq);
 }
 void sg_gpu_splitk_dispatch_counts(const sg_gpu *g, uint64_t *per_head, uint64_t *gqa) {
-    if (per_head) *per_head = 0;
-    if (gqa) *gqa = g ? g->splitk_gqa_dispatches : 0;
+    if (per_head) *per_head = g ? g->n_per_head : 0;
+    if (gqa) *gqa = g ? g->n_gqa : 0;
 }
+uint64_t sg_gpu_splitk_online_dispatches(const sg_gpu *g) { return g ? g->n_online : 0; }
 
 sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *gates,
                               const uint32_t p[8]) {
@@ -611,6 +675,57 @@ sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *ga
     if (sg_failed(e = push(ins, 4))) return e;
     return finish(g, sgk_delta_multi(DEV(S), DEV(qkv), DEV(out), DEV(gates), dk, dv, nv, nk, kd, p[5] != 0, g->stream),
                   outs, 2);
+}
+
+/* The decode path's fused DeltaNet layer step (k_gdn_step) on caller buffers
+ * (no reference counterpart: the reference tests its decode kernels one by
+ * one, k_conv1d_step, k_delta_gates, k_delta_multi, k_rmsnorm_gated; here
+ * they are one kernel, so it is tested whole). One token:
+ *   in    [conv_dim + value_dim + 2 n_v]  the input projection's rows
+ *         qkv | z | b | a (qkv before the conv);
+ *   w     [conv_dim ksize + 2 n_v + dv]   conv_w | ssm_a | dt_bias | ssm_norm;
+ *   state [(ksize-1) conv_dim + n_v dv dk] the conv tail (oldest first) | S,
+ *         updated in place;
+ *   out   [value_dim]                     silu(z) * rmsnorm(y, ssm_norm).
+ * p: [0]=dk [1]=dv [2]=n_v [3]=n_k [4]=ksize [5]=tiled [6]=ssm_a is -exp(A_log)
+ * [7]=eps bits. conv_dim = 2 n_k dk + n_v dv. head_v_dim <= 128 (one
+ * workgroup per value head, the decode default). */
+sg_err sg_gpu_run_gdn_step(sg_gpu *g, void *in, void *w, void *state, void *out, const uint32_t p[8]) {
+    if (!g || !in || !w || !state || !out || !p) return (sg_err){"gpu: gdn_step got a NULL argument"};
+    const uint32_t dk = p[0], dv = p[1], nv = p[2], nk = p[3], ks = p[4];
+    if (dk != 32 && dk != 64 && dk != 128 && dk != 256) return (sg_err){"gpu: gdn_step: dk must be 32, 64, 128 or 256"};
+    if (!dv || dv > 128 || !nv || !nk || nv % nk || ks < 1 || ks > 4)
+        return (sg_err){"gpu: gdn_step: bad shape (dv <= 128, n_v a multiple of n_k, ksize 1..4)"};
+    const uint64_t cd = 2ull * nk * dk + (uint64_t)nv * dv, vd = (uint64_t)nv * dv, keep = ks - 1;
+    sg_err e;
+    if (sg_failed(e = need(in, (cd + vd + 2ull * nv) * 4, "in")) ||
+        sg_failed(e = need(w, (cd * ks + 2ull * nv + dv) * 4, "w")) ||
+        sg_failed(e = need(state, (keep * cd + vd * dk) * 4, "state")) || sg_failed(e = need(out, vd * 4, "out")))
+        return e;
+    if (overlap(out, in) || overlap(out, w) || overlap(out, state) || overlap(state, in) || overlap(state, w))
+        return (sg_err){"gpu: gdn_step: buffers must not overlap"};
+    void *ins[3] = {in, w, state}, *outs[2] = {state, out};
+    if (sg_failed(e = push(ins, 3))) return e;
+    /* scratch: the step descriptor, then the 4-slot ring. The step runs at
+     * position 3, so the taps read slots 3-keep .. 2, which take the conv
+     * tail's rows, and the input goes to slot 3. */
+    void *t;
+    if (sg_failed(e = scratch(g, 256 + 4 * cd * 4, &t))) return e;
+    sgk_step st = {0, 3, {0, 0}};
+    float *ring = (float *)((char *)t + 256), *dst = DEV(state), *wp = DEV(w);
+    hipStream_t s = g->stream;
+    HIPCHK(hipMemcpyAsync(t, &st, sizeof st, hipMemcpyHostToDevice, s), "gdn_step descriptor");
+    if (keep)
+        HIPCHK(hipMemcpyAsync(ring + (3 - keep) * cd, dst, keep * cd * 4, hipMemcpyDeviceToDevice, s), "conv tail in");
+    sgk_gdn d = {0};
+    d.in = DEV(in); d.z = (const float *)DEV(in) + cd; d.conv_w = wp; d.ssm_a = wp + cd * ks;
+    d.dt_bias = d.ssm_a + nv; d.norm_w = d.dt_bias + nv; d.ring = ring; d.S = dst + keep * cd;
+    d.step = t; d.n_k = nk; d.n_v = nv; d.dk = dk; d.dv = dv; d.conv_dim = (uint32_t)cd; d.ksize = ks;
+    d.tiled = p[5] != 0; d.neg_exp = p[6] != 0; d.out = DEV(out); d.eps = fbits(p[7]); d.blocks = 1;
+    hipError_t he = sgk_gdn_step(&d, s);
+    if (he == hipSuccess && keep)
+        he = hipMemcpyAsync(dst, ring + (4 - keep) * cd, keep * cd * 4, hipMemcpyDeviceToDevice, s);
+    return finish(g, he, outs, 2);
 }
 
 /* ---------------------------------------------------------------------
@@ -685,7 +800,7 @@ sg_err sg_gpu_run_rmsnorm_gated_chunk(sg_gpu *g, void *y, void *z, void *out, vo
 sg_err sg_gpu_run_attn_prefill(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8]) {
     if (!g || !q || !k || !v || !out || !p) return (sg_err){"gpu: attn_prefill got a NULL argument"};
     uint32_t pp[8] = {p[0], p[1], p[2], 0, p[5], 0, 1, 0};
-    sg_err e = attn_check(pp, false);
+    sg_err e = attn_check(pp, false, false);
     if (sg_failed(e)) return e;
     uint32_t nh = p[0], nkv = p[1], hd = p[2], base = p[3], n = p[4], qs = p[5];
     if (!n) return (sg_err){"gpu: attn_prefill: n is zero"};
@@ -709,22 +824,27 @@ sg_err sg_gpu_run_attn_prefill(sg_gpu *g, void *q, void *k, void *v, void *out, 
     A.q = DEV(q); A.kc = DEV(k); A.vc = DEV(v); A.m = mm; A.s = ss; A.acc = aa; A.out = DEV(out); A.steps = t;
     A.n_heads = nh; A.n_kv = nkv; A.hd = hd; A.q_stride = qs; A.q_tok = nh * qs; A.out_tok = nh * hd;
     A.max_splits = SGK_PREFILL_SPLITS; A.ntok = n; A.scale = fbits(p[6]); A.prefill = 1;
-    he = sgk_attn_partial(&A, g->stream);
-    if (he == hipSuccess) he = sgk_attn_combine(&A, g->stream);
+    A.seq = base + n;
+    /* The prefill path's kernel: the MFMA flash pass (deep chunks split over
+     * keys and merged by the combine) for head_dim 64/128/256 with float4 q
+     * rows; the split-K kernels per token otherwise. */
+    if ((hd == 64 || hd == 128 || hd == 256) && qs % 4 == 0) {
+        he = sgk_attn_flash(&A, g->stream);
+    } else {
+        he = sgk_attn_partial(&A, g->stream);
+        if (he == hipSuccess) he = sgk_attn_combine(&A, g->stream);
+    }
     return finish(g, he, outs, 1);
 }
 
-/* The online-softmax arm (surge.h:974-1050). The partial kernel here IS the
- * online form (running max/sum/acc rescaled across key tiles), so the
- * online entry points are the same kernel. */
+/* The online-softmax partial (surge.h:974-1050). The partial kernel here is
+ * the online form already (running max, sum and accumulator rescaled across
+ * key rounds), so this is the GQA one-shot: the same bytes, where the
+ * reference's online kernel differs from its four-pass one in the last bits. */
 sg_err sg_gpu_run_attn_splitk_partial_gqa_online(sg_gpu *g, void *q, void *k, void *v, void *m, void *s,
                                                  void *acc, const uint32_t p[8]) {
-    return sg_gpu_run_attn_splitk_partial_gqa(g, q, k, v, m, s, acc, p);
+    return attn_partial_oneshot(g, q, k, v, m, s, acc, p, false);
 }
-bool sg_gpu_splitk_online_selected(const sg_gpu *g, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq) {
-    return sg_gpu_splitk_gqa_selected(g, n_heads, n_kv_heads, seq);
-}
-uint64_t sg_gpu_splitk_online_dispatches(const sg_gpu *g) { return g ? g->splitk_gqa_dispatches : 0; }
 
 /* ---------------------------------------------------------------------
  * model load
@@ -909,6 +1029,9 @@ static void state_free(sg_gpu *g) {
     if (g->g_fwd) hipGraphExecDestroy(g->g_fwd);
     if (g->g_greedy) hipGraphExecDestroy(g->g_greedy);
     g->g_fwd = g->g_greedy = NULL;
+    if (g->step_ev) hipEventDestroy(g->step_ev);
+    g->step_ev = NULL;
+    g->step_pending = false;
     if (g->h_step) hipHostFree(g->h_step);
     if (g->h_logits) hipHostFree(g->h_logits);
     if (g->h_tok) hipHostFree(g->h_tok);
@@ -966,7 +1089,8 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             A.max_splits = g->max_splits; A.ntok = 1; A.scale = (float)(1.0 / sqrt((double)hd));
             A.kv_ps = hd; A.kv_hs = (uint64_t)g->max_ctx * hd;
             A.fuse_prep = 1; A.qn = L->qn; A.kn = L->kn; A.cs = g->cs_table; A.eps = c->rms_eps;
-            A.split_cap = g->split_cap;
+            A.split_cap = g->attn_arm == ARM_SINGLE ? 1 : g->split_cap;
+            A.per_head = g->attn_arm == ARM_PER_HEAD;
             if ((e = sgk_attn_partial(&A, s)) != hipSuccess) return e;
             if ((e = sgk_attn_combine(&A, s)) != hipSuccess) return e;
             o.x = g->ctx; o.pro = SGK_PRO_NONE;
@@ -1028,6 +1152,34 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     if (m != g->model) return (sg_err){"gpu: this gpu was loaded with a different sg_model"};
     if (!max_ctx || max_ctx > SG_KV_CAP_MAX) return (sg_err){"gpu: max_ctx must be in [1, 262144]"};
     state_free(g);
+    /* The decode-selection switches, read here as the reference reads them
+     * (surge.h:1179-1254, metal.m state_new): SURGE_KV_DTYPE f16 (default);
+     * f32 names the reference's f32 cache, which is not built here, so it is
+     * refused; anything else warns and keeps f16. SURGE_ATTN_SPLITK and
+     * SURGE_ATTN_SPLITK_GQA: "0" turns off, anything else but "1" warns and
+     * keeps the default 1. SURGE_ATTN_SPLITK_ONLINE: exactly "0" or "1", else
+     * refused. */
+    const char *dt_env = getenv("SURGE_KV_DTYPE");
+    if (dt_env && strcmp(dt_env, "f32") == 0)
+        return (sg_err){"gpu: SURGE_KV_DTYPE=f32 selects an f32 K/V cache, which this build does not have "
+                        "(f16 is the only KV dtype on MI355X)"};
+    if (dt_env && dt_env[0] && strcmp(dt_env, "f16") != 0)
+        fprintf(stderr, "gpu: SURGE_KV_DTYPE='%s' not recognized (want f16); using f16\n", dt_env);
+    bool sw[2] = {true, true};
+    const char *sw_name[2] = {"SURGE_ATTN_SPLITK", "SURGE_ATTN_SPLITK_GQA"};
+    for (int k = 0; k < 2; k++) {
+        const char *v = getenv(sw_name[k]);
+        if (v && strcmp(v, "0") == 0) sw[k] = false;
+        else if (v && v[0] && strcmp(v, "1") != 0)
+            fprintf(stderr, "gpu: %s='%s' not recognized (want 0 or 1); using 1\n", sw_name[k], v);
+    }
+    bool online = false;
+    const char *on_env = getenv("SURGE_ATTN_SPLITK_ONLINE");
+    if (on_env && on_env[0]) {
+        if (strcmp(on_env, "1") == 0) online = true;
+        else if (strcmp(on_env, "0") != 0)
+            return errf("gpu: SURGE_ATTN_SPLITK_ONLINE='%s' must be exactly 0 or 1 (default 0)", on_env);
+    }
     /* SURGE_SPLITK_GQA_CAP (reference surge.h:1239-1256): plain decimal digits
      * in [4, 1024], else the state is refused. */
     uint32_t cap = SGK_MAX_SPLITS;
@@ -1044,6 +1196,14 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     const sg_cfg *c = &g->cfg;
     g->max_ctx = max_ctx;
     g->split_cap = cap;
+    g->attn_splitk = sw[0];
+    g->attn_gqa = sw[1];
+    g->attn_online = online;
+    g->n_per_head = g->n_gqa = g->n_online = 0;
+    if (!g->attn_splitk) g->attn_arm = ARM_SINGLE;
+    else if (sg_gpu_splitk_online_selected(g, c->n_heads, c->n_kv_heads, c->head_dim, max_ctx)) g->attn_arm = ARM_ONLINE;
+    else if (sg_gpu_splitk_gqa_selected(g, c->n_heads, c->n_kv_heads, max_ctx)) g->attn_arm = ARM_GQA;
+    else g->attn_arm = ARM_PER_HEAD;
     /* One workgroup per DeltaNet value head finishes RMSNormGated itself
      * (head_v_dim <= 128); wider heads use SGK_GDN_BLOCKS row blocks and the
      * out projection's gated prologue. SURGE_GDN_BLOCKS=1|4 overrides. */
@@ -1056,7 +1216,7 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
             else return errf("gpu: SURGE_GDN_BLOCKS='%s' must be 1 (head_v_dim <= 128) or 4", gb);
         }
     }
-    g->max_splits = sgk_n_splits_cap(max_ctx, cap);
+    g->max_splits = g->attn_arm == ARM_SINGLE ? 1 : sgk_n_splits_cap(max_ctx, cap);
     sg_err e = SG_OK;
     uint32_t act_rows = 0;
     for (uint32_t i = 0; i < c->n_layers; i++) if (g->ls[i].in.rows > act_rows) act_rows = g->ls[i].in.rows;
@@ -1105,6 +1265,8 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     if (!sg_failed(e) && hipHostMalloc((void **)&g->h_step, sizeof(sgk_step), 0) != hipSuccess) e = (sg_err){"gpu: hipHostMalloc failed"};
     if (!sg_failed(e) && hipHostMalloc((void **)&g->h_logits, (uint64_t)c->vocab * 4, 0) != hipSuccess) e = (sg_err){"gpu: hipHostMalloc failed"};
     if (!sg_failed(e) && hipHostMalloc((void **)&g->h_tok, ((uint64_t)max_ctx + 2) * 4, 0) != hipSuccess) e = (sg_err){"gpu: hipHostMalloc failed"};
+    if (!sg_failed(e) && hipEventCreateWithFlags(&g->step_ev, hipEventDisableTiming) != hipSuccess)
+        e = (sg_err){"gpu: hipEventCreate failed"};
     g->have_state = true;
     if (!sg_failed(e) && g->use_graph) {
         e = capture(g, false, &g->g_fwd);
@@ -1146,11 +1308,32 @@ static uint32_t n_attn_layers(const sg_gpu *g) {
     return n;
 }
 
-static sg_err launch_step(sg_gpu *g, int32_t token, uint32_t pos, bool greedy) {
-    g->splitk_gqa_dispatches += n_attn_layers(g);
+/* Writes the pinned step descriptor and queues its upload. The previous
+ * upload of the same pinned bytes may not have run yet (forward_nosync and
+ * the greedy loop return without waiting), so the write waits for it. */
+static sg_err step_upload(sg_gpu *g, int32_t token, uint32_t pos) {
+    if (g->step_pending) HIPCHK(hipEventSynchronize(g->step_ev), "previous step upload");
     g->h_step->token = token;
     g->h_step->pos = pos;
     HIPCHK(hipMemcpyAsync(g->d_step, g->h_step, sizeof(sgk_step), hipMemcpyHostToDevice, g->stream), "step upload");
+    HIPCHK(hipEventRecord(g->step_ev, g->stream), "step upload event");
+    g->step_pending = true;
+    return SG_OK;
+}
+
+/* Counts what one decode step encodes: one partial per attention layer, in
+ * the counter of the state's arm (the single-pass arm counts in neither). */
+static void count_step(sg_gpu *g, uint64_t steps) {
+    const uint64_t n = steps * n_attn_layers(g);
+    if (g->attn_arm == ARM_PER_HEAD) g->n_per_head += n;
+    else if (g->attn_arm == ARM_GQA) g->n_gqa += n;
+    else if (g->attn_arm == ARM_ONLINE) g->n_online += n;
+}
+
+static sg_err launch_step(sg_gpu *g, int32_t token, uint32_t pos, bool greedy) {
+    sg_err se = step_upload(g, token, pos);
+    if (sg_failed(se)) return se;
+    count_step(g, 1);
     if (g->use_graph) {
         HIPCHK(hipGraphLaunch(greedy ? g->g_greedy : g->g_fwd, g->stream), "graph launch");
     } else {
@@ -1174,8 +1357,6 @@ sg_err sg_gpu_forward(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
 sg_err sg_gpu_forward_nosync(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos) {
     sg_err e = step_checks(g, m, token, pos);
     if (sg_failed(e)) return e;
-    /* The step buffer is reused: wait for the previous upload to drain. */
-    HIPCHK(hipStreamSynchronize(g->stream), "previous step");
     if (sg_failed(e = launch_step(g, token, pos, false))) return e;
     g->used = pos + 1;
     return SG_OK;
@@ -1205,10 +1386,8 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
     sg_err e = step_checks(g, m, token, pos);
     if (sg_failed(e)) return e;
     if (!n_steps || (uint64_t)pos + n_steps > g->max_ctx) return (sg_err){"gpu: greedy decode runs past max_ctx"};
-    g->h_step->token = token;
-    g->h_step->pos = pos;
-    HIPCHK(hipMemcpyAsync(g->d_step, g->h_step, sizeof(sgk_step), hipMemcpyHostToDevice, g->stream), "step upload");
-    g->splitk_gqa_dispatches += (uint64_t)n_steps * n_attn_layers(g);
+    if (sg_failed(e = step_upload(g, token, pos))) return e;
+    count_step(g, n_steps);
     for (uint32_t i = 0; i < n_steps; i++) {
         if (g->use_graph) {
             HIPCHK(hipGraphLaunch(g->g_greedy, g->stream), "graph launch");

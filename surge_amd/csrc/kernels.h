@@ -129,6 +129,11 @@ typedef struct {
      * one contiguous run. */
     uint32_t kv_ps;
     uint64_t kv_hs;
+    /* Per-head partial (the reference's k_attn_decode_splitk_partial): one
+     * workgroup per (split, query head) instead of per (split, kv head); the
+     * grid's y is n_heads. Each head's arithmetic is the same as in the
+     * group-shared form, so both give the same bytes. */
+    int per_head;
 } sgk_attn;
 
 /* q_norm/k_norm + RoPE on each head, K and V stored f16 at each token's
@@ -138,7 +143,9 @@ hipError_t sgk_attn_prep(const sgk_attn *a, const float *qn, const float *kn,
 /* Split-K GQA partials: workgroup (split, kv head, token) serves all
  * n_heads/n_kv query heads of the group (grid x = max_splits with steps).
  * With fuse_prep the prep above is done inside (q in LDS; the split holding
- * the position stores the new K/V), so a decode step needs no prep launch. */
+ * the position stores the new K/V), so a decode step needs no prep launch.
+ * Without it q is used as given (already normed and roped) and nothing is
+ * stored: the per-op one-shots run the decode kernel this way. */
 hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s);
 /* LSE combine with the optional fused sigmoid output gate. */
 hipError_t sgk_attn_combine(const sgk_attn *a, hipStream_t s);
@@ -219,7 +226,7 @@ hipError_t sgk_rmsnorm_gated(const float *y, const float *z, const float *w, flo
                              uint32_t dv, uint32_t heads, float eps, hipStream_t s);
 
 /* Argmax over n floats, lowest index wins ties; result written to *out. */
-hipError_t sgk_argmax(const float *v, uint32_t n, uint32_t *out, uint32_t *scratch,
+hipError_t sgk_argmax(const float *v, uint32_t n, uint32_t *out, uint32_t *part,
                       hipStream_t s);
 
 /* Greedy bookkeeping inside the decode graph: hist[pos + 1] = token (the

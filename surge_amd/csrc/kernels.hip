@@ -1024,6 +1024,18 @@ extern "C" hipError_t sgk_attn_prep(const sgk_attn *a, const float *qn, const fl
 
 #define GMAX 8
 
+// The query heads a partial workgroup serves: the whole GQA group of kv head
+// blockIdx.y, or (per-head form, grid y = n_heads) query head blockIdx.y
+// alone, reading its group's kv head. In the per-head form every head of the
+// split that holds the position stores the new K/V row (the same bytes), so
+// each workgroup reads back a row it has written itself.
+struct attn_group { uint32_t G, hk, h0; };
+__device__ __forceinline__ attn_group attn_group_of(const sgk_attn &a) {
+    const uint32_t gf = a.n_heads / a.n_kv;
+    if (a.per_head) return {1u, blockIdx.y / gf, blockIdx.y};
+    return {gf, blockIdx.y, blockIdx.y * gf};
+}
+
 // Query / key prep shared by k_attn_prep and the fused decode partial:
 // RMSNorm (w) then half-split RoPE over the first rope_dim dims, element d
 // of a row x whose raw values and 1/rms factor are given (ref.c:1207-1235,
@@ -1093,9 +1105,10 @@ __global__ void __launch_bounds__(TPB) k_attn_partial(sgk_attn a) {
     __shared__ float mrun[GMAX], srun[GMAX], alpha[GMAX], rn[GMAX + 1];
     __shared__ __align__(16) float red[TPB / 64][GMAX * HD];   // end fold; raw rows during prep
 
-    const uint32_t G = a.n_heads / a.n_kv, n_kv = a.n_kv, z = blockIdx.z;
-    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const uint32_t h0 = hk * G;
+    const attn_group gr = attn_group_of(a);
+    const uint32_t G = gr.G, n_kv = a.n_kv, z = blockIdx.z;
+    const uint32_t i = blockIdx.x, hk = gr.hk, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t h0 = gr.h0;
     const float *q = a.q + (size_t)z * a.q_tok;
     const bool fp = a.fuse_prep != 0;
 
@@ -1442,10 +1455,19 @@ __device__ __forceinline__ void wv_load_v(v4u (&vr)[4][HD / 128], const uint16_t
 // dims (8 per 32), so the sum of squares is two cross-row steps, and a
 // rotated dim's partner (d +- rope_dim/2) sits in the same lane, RKB k-blocks
 // away: no LDS and no barrier, except in the split that stores the new K.
+// RKB = WV_RAW: no prep and no store; q is taken as given (the per-op
+// one-shots), seq and n_splits come from the call when there are no step
+// descriptors, and an empty split writes m = -inf, s = 0, acc = 0 without
+// touching the cache.
+#define WV_RAW 3
 template <int HD, int RKB>
 __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))) k_attn_partial_wv(sgk_attn a) {
     static_assert(HD == 128 || HD == 256, "wave-stream decode partial takes head_dim 128 or 256");
-    static_assert(RKB >= 0 && RKB <= 2 && 2 * RKB <= HD / 32, "register prep takes rope_dim 64 or 128");
+    static_assert(RKB == WV_RAW || (RKB >= 0 && RKB <= 2 && 2 * RKB <= HD / 32),
+                  "register prep takes rope_dim 64 or 128");
+    constexpr bool RAW = RKB == WV_RAW;
+    constexpr int RR = RAW ? 0 : RKB;                 // rotated k-blocks of the register prep
+    constexpr bool REGQ = RAW || RKB > 0;             // q fragments straight from the rows
     // the first keys' K is requested before the prep, except where the
     // register prep's values leave no room for it (head_dim 256, rope 128)
     constexpr bool EARLY_K = !(HD == 256 && RKB == 2);
@@ -1460,16 +1482,17 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
     __shared__ __align__(16) uint16_t knew[HD], vnew[HD];
     float *raw = big;
 
-    const uint32_t G = a.n_heads / a.n_kv, n_kv = a.n_kv, z = blockIdx.z;
-    const uint32_t i = blockIdx.x, hk = blockIdx.y, t = threadIdx.x, lane = t & 63;
+    const attn_group gr = attn_group_of(a);
+    const uint32_t G = gr.G, n_kv = a.n_kv, z = blockIdx.z;
+    const uint32_t i = blockIdx.x, hk = gr.hk, t = threadIdx.x, lane = t & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t li = lane & 15, lg = lane >> 4, h0 = hk * G;
+    const uint32_t li = lane & 15, lg = lane >> 4, h0 = gr.h0;
     const float *q = a.q + (size_t)z * a.q_tok;
 
     // 1. position-independent loads first (as in k_attn_partial)
-    float qv[RKB ? 1 : QPT];
+    float qv[REGQ ? 1 : QPT];
     f32x4 qx[NKB][2], qw[NKB][2];     // register prep: head min(li, G-1)'s dims 32kb + 8lg.., q_norm weights
-    if constexpr (RKB == 0) {
+    if constexpr (!REGQ) {
 #pragma unroll
         for (int k = 0; k < QPT; k++) {
             const uint32_t e = min(t + k * TPB, G * HD - 1);
@@ -1482,33 +1505,50 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int c = 0; c < 2; c++) {
                 qx[kb][c] = *(const f32x4 *)(qrow + kb * 32 + c * 4);
-                qw[kb][c] = *(const f32x4 *)(a.qn + kb * 32 + lg * 8 + c * 4);
+                if constexpr (!RAW) qw[kb][c] = *(const f32x4 *)(a.qn + kb * 32 + lg * 8 + c * 4);
             }
     }
     const uint32_t td = min(t, (uint32_t)HD - 1);
-    const float *krow = q + (size_t)a.n_heads * a.q_stride + (size_t)hk * HD;
-    const float *vrow = krow + (size_t)n_kv * HD;
-    const float qn0 = RKB ? 0.0f : a.qn[td], kn0 = a.kn[td], kr0 = krow[td], vr0 = vrow[td];
+    float qn0 = 0.0f, kn0 = 0.0f, kr0 = 0.0f, vr0 = 0.0f;
+    if constexpr (!RAW) {
+        const float *krow = q + (size_t)a.n_heads * a.q_stride + (size_t)hk * HD;
+        const float *vrow = krow + (size_t)n_kv * HD;
+        qn0 = RKB ? 0.0f : a.qn[td];
+        kn0 = a.kn[td];
+        kr0 = krow[td];
+        vr0 = vrow[td];
+    }
 
-    const uint32_t pos = a.steps[z].pos, seq = pos + 1;
-    const uint32_t ns = dev_splits(seq, a.prefill, a.split_cap);
+    const uint32_t pos = a.steps ? a.steps[z].pos : 0;
+    const uint32_t seq = (RAW && !a.steps) ? a.seq : pos + 1;
+    const uint32_t ns = (RAW && !a.steps) ? a.n_splits : dev_splits(seq, a.prefill, a.split_cap);
     if (i >= ns) return;
     const uint32_t t0 = (uint32_t)((uint64_t)i * seq / ns), t1 = (uint32_t)((uint64_t)(i + 1) * seq / ns);
     const uint32_t klast = t1 ? t1 - 1 : 0;
     const size_t zoff = (size_t)z * a.n_heads * a.max_splits;
+    if (RAW && t1 == t0) {            // an empty split (more splits than keys, or no keys)
+        for (uint32_t e = t; e < G * HD; e += TPB)
+            a.acc[(zoff + (size_t)(h0 + e / HD) * ns + i) * HD + e % HD] = 0.0f;
+        if (t < G) {
+            a.m[zoff + (size_t)(h0 + t) * ns + i] = -INFINITY;
+            a.s[zoff + (size_t)(h0 + t) * ns + i] = 0.0f;
+        }
+        return;
+    }
 
     // 2. the position's cos|sin entry (register prep: cos and sin of the
     //    lane's rotated dims), then this wave's first 16 keys of K and V
-    const float *csp = a.cs + (size_t)pos * a.rope_dim;
-    const float cs0 = csp[min(td, a.rope_dim - 1)];
-    f32x4 rc[RKB ? RKB : 1][2], rs[RKB ? RKB : 1][2];
-    if constexpr (RKB > 0) {
+    float cs0 = 0.0f;
+    f32x4 rc[RR ? RR : 1][2], rs[RR ? RR : 1][2];
+    if constexpr (!RAW) {
+        const float *csp = a.cs + (size_t)pos * a.rope_dim;
+        cs0 = csp[min(td, a.rope_dim - 1)];
 #pragma unroll
-        for (int kb = 0; kb < RKB; kb++)
+        for (int kb = 0; kb < RR; kb++)
 #pragma unroll
             for (int c = 0; c < 2; c++) {
                 rc[kb][c] = *(const f32x4 *)(csp + kb * 32 + lg * 8 + c * 4);
-                rs[kb][c] = *(const f32x4 *)(csp + RKB * 32 + kb * 32 + lg * 8 + c * 4);
+                rs[kb][c] = *(const f32x4 *)(csp + RR * 32 + kb * 32 + lg * 8 + c * 4);
             }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1516,12 +1556,12 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
     const uint16_t *kch = a.kc + (size_t)hk * a.kv_hs, *vch = a.vc + (size_t)hk * a.kv_hs;
     const uint32_t base0 = t0 + wave * 16;
     if constexpr (EARLY_K) mf_load_k<HD>(kr, kch, min(base0 + li, klast), a.kv_ps, lg);
-    if constexpr (RKB == 0) wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
+    if constexpr (RKB == 0 || RAW) wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
 
     // 3. prep: q_norm + RoPE of the group's heads; the split holding the
     //    position stores that token's K (k_norm + RoPE) and raw V as f16
-    const bool kv_writer = i == ns - 1;
-    if (RKB == 0 || kv_writer) {
+    const bool kv_writer = !RAW && i == ns - 1;
+    if (!RAW && (RKB == 0 || kv_writer)) {
         if constexpr (RKB == 0) {
 #pragma unroll
             for (int k = 0; k < QPT; k++) raw[t + k * TPB] = qv[k];
@@ -1582,6 +1622,14 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
             float xv[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) xv[e] = li < G ? qsh[li * HD + kb * 32 + lg * 8 + e] : 0.0f;
+            fa_split8(xv, qh[kb], ql[kb]);
+        }
+    } else if constexpr (RAW) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            float xv[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) xv[e] = li < G ? qx[kb][e / 4][e % 4] : 0.0f;
             fa_split8(xv, qh[kb], ql[kb]);
         }
     } else {
@@ -1725,12 +1773,12 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
 }
 
-// SURGE_ATTN_VALU=1 keeps the decode partial on the VALU kernel (for A/B
+// SURGE_ATTN_VALU=1 keeps the partial on the VALU kernel (for A/B
 // measurement); the MFMA partial is the default for head_dim 128 and 256.
+// Read at every launch (a decode state reads it when it captures its graph).
 static bool getenv_mf() {
-    static int v = -1;
-    if (v < 0) { const char *e = getenv("SURGE_ATTN_VALU"); v = (e && e[0] == '1') ? 0 : 1; }
-    return v == 1;
+    const char *e = getenv("SURGE_ATTN_VALU");
+    return !(e && e[0] == '1');
 }
 
 extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
@@ -1739,7 +1787,16 @@ extern "C" hipError_t sgk_attn_partial(const sgk_attn *a, hipStream_t s) {
         return hipErrorInvalidValue;
     const uint32_t gx = a->steps ? a->max_splits : a->n_splits;
     if (!gx || !a->ntok) return hipSuccess;
-    dim3 grid(gx, a->n_kv, a->ntok);
+    dim3 grid(gx, a->per_head ? a->n_heads : a->n_kv, a->ntok);
+    // q taken as given (the one-shots): the wave-stream kernel's RAW form, which
+    // reads q rows as float4
+    if (!a->fuse_prep && (a->hd == 128 || a->hd == 256) && ((uintptr_t)a->acc & 15) == 0 && getenv_mf() &&
+        ((uintptr_t)a->q & 15) == 0 && (a->q_stride & 3) == 0 && (a->q_tok & 3) == 0) {
+        const sgk_attn b = kv_resolved(a);
+        if (a->hd == 256) hipLaunchKernelGGL((k_attn_partial_wv<256, WV_RAW>), grid, dim3(TPB), 0, s, b);
+        else hipLaunchKernelGGL((k_attn_partial_wv<128, WV_RAW>), grid, dim3(TPB), 0, s, b);
+        return hipGetLastError();
+    }
     // the wave-stream kernel stores its output rows as float4
     if (a->fuse_prep && (a->hd == 128 || a->hd == 256) && ((uintptr_t)a->acc & 15) == 0 && getenv_mf()) {
         // register prep: rope_dim 64 or 128 and 16-byte aligned q rows, q_norm weights and cos|sin table
@@ -2882,14 +2939,14 @@ extern "C" hipError_t sgk_embed_rows(const int8_t *qs, const uint16_t *d, const 
 
 // ---------------------------------------------------------------------------
 // Argmax (greedy.c:17-27): lowest index wins an exact tie. Two passes:
-// per-workgroup winners into scratch, then one workgroup folds them.
+// per-workgroup winners into `part`, then one workgroup folds them.
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ void better(float &bv, uint32_t &bi, float v, uint32_t i) {
     if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
 }
 
-__global__ void __launch_bounds__(TPB) k_argmax(const float *v, uint32_t n, uint32_t *scratch,
+__global__ void __launch_bounds__(TPB) k_argmax(const float *v, uint32_t n, uint32_t *part,
                                                 uint32_t *out, int final_pass) {
     __shared__ float sv[TPB];
     __shared__ uint32_t si[TPB];
@@ -2899,7 +2956,7 @@ __global__ void __launch_bounds__(TPB) k_argmax(const float *v, uint32_t n, uint
         for (uint32_t i = blockIdx.x * TPB + threadIdx.x; i < n; i += gridDim.x * TPB) better(bv, bi, v[i], i);
     } else {
         for (uint32_t k = threadIdx.x; k < n; k += TPB) {
-            const uint32_t i = scratch[k];
+            const uint32_t i = part[k];
             if (i != 0xFFFFFFFFu) better(bv, bi, v[i], i);
         }
     }
@@ -2917,16 +2974,20 @@ __global__ void __launch_bounds__(TPB) k_argmax(const float *v, uint32_t n, uint
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        if (final_pass) *out = si[0] == 0xFFFFFFFFu ? 0u : si[0];
-        else scratch[blockIdx.x] = si[0];
+        // sg_argmax_f32 scans upward from v[0] with a strict '>': a NaN at
+        // index 0 is never beaten (index 0), NaNs elsewhere never win, and an
+        // all-NaN or all -inf vector gives 0
+        const float v0 = v[0];
+        if (final_pass) *out = (si[0] == 0xFFFFFFFFu || v0 != v0) ? 0u : si[0];
+        else part[blockIdx.x] = si[0];
     }
 }
 
-extern "C" hipError_t sgk_argmax(const float *v, uint32_t n, uint32_t *out, uint32_t *scratch,
+extern "C" hipError_t sgk_argmax(const float *v, uint32_t n, uint32_t *out, uint32_t *part,
                                  hipStream_t s) {
     const uint32_t blocks = 256;
-    hipLaunchKernelGGL(k_argmax, dim3(blocks), dim3(TPB), 0, s, v, n, scratch, out, 0);
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(TPB), 0, s, v, blocks, scratch, out, 1);
+    hipLaunchKernelGGL(k_argmax, dim3(blocks), dim3(TPB), 0, s, v, n, part, out, 0);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(TPB), 0, s, v, blocks, part, out, 1);
     return hipGetLastError();
 }
 

@@ -54,6 +54,7 @@ _ORACLE_ONLY = {
     "sg_ref_attn_partials": (None, [F, F, F, u32, u32, u32, u32, u32, f32, u32, F, F, F]),
     "sg_ref_state_set_kv_f16": (None, [C.c_void_p, C.c_bool]),
     "sg_ref_set_threads": (C.c_int, [C.c_int]),
+    "sg_ref_state_fill_synthetic": (None, None),
 }
 
 
@@ -65,6 +66,8 @@ def _load(path, extra):
     sigs["sg_ref_state_new"] = (S.SgErr, [C.POINTER(S.SgModel), u32, C.POINTER(C.c_void_p)])
     sigs["sg_ref_forward"] = (S.SgErr, [C.c_void_p, C.POINTER(S.SgModel), C.c_int32, u32,
                                         C.POINTER(F)])
+    if "sg_ref_state_fill_synthetic" in sigs:
+        sigs["sg_ref_state_fill_synthetic"] = (S.SgErr, [C.c_void_p, u32, u32])
     for name, (res, args) in sigs.items():
         f = getattr(L, name)
         f.restype = res
@@ -118,6 +121,13 @@ class RefModel:
         if err.msg:
             raise S.SurgeError(err.msg.decode())
         return np.ctypeslib.as_array(lg, shape=(self.vocab,)).copy()
+
+    def fill_synthetic(self, n_tokens, seed=0):
+        """The seeded state sg_gpu_state_fill_synthetic writes (oracle only)."""
+        import surge_amd as S
+        err = self.L.sg_ref_state_fill_synthetic(self.st, n_tokens, seed)
+        if err.msg:
+            raise S.SurgeError(err.msg.decode())
 
     def close(self):
         if self.st:

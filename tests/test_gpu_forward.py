@@ -414,3 +414,116 @@ def test_fill_synthetic_depth_then_decode(gpu):
     assert not np.array_equal(a, c)
     assert gpu.n_splits_at(1501) == 24
     syn.close()
+
+
+def _per_position_vs_oracle(gpu, syn, cfg, n, max_ctx, every, seed, kv_f16=True):
+    """Decode n random ids through the GPU forward and the f16-KV oracle;
+    returns the worst scale-relative logit error at sampled positions and
+    checks the argmax there."""
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(0, cfg["vocab"], n).tolist()
+    rm = O.RefModel(O.oracle(), syn.model, max_ctx, kv_f16=kv_f16)
+    worst = 0.0
+    for p, t in enumerate(ids):
+        g = gpu.forward(t, p)
+        o = rm.forward(t, p)
+        if p % every == 0 or p >= n - 3:
+            worst = max(worst, rel(g, o))
+            assert np.argmax(g) == np.argmax(o), f"argmax differs at position {p}"
+    rm.close()
+    return worst
+
+
+WIDE_V = dict(n_layers=4, n_heads=8, n_kv_heads=2, head_dim=128, hidden=512, ffn_hidden=1024,
+              vocab=900, rope_theta=1e7, rms_eps=1e-6, tied_embeddings=False, rope_dim=64,
+              full_attn_interval=4, n_k_heads=2, n_v_heads=4, head_k_dim=128, head_v_dim=256,
+              conv_kernel=4, attn_output_gate=True)
+
+
+@pytest.mark.parametrize("cfg_name,blocks", [("HD128", "4"), ("WIDE_V", None)])
+def test_gdn_four_block_step_and_gated_prologue_vs_oracle(gpu, monkeypatch, cfg_name, blocks):
+    """The DeltaNet step split over four workgroups per value head, with
+    RMSNormGated finished in the output projection's gated prologue
+    (SGK_PRO_GATED): forced with SURGE_GDN_BLOCKS=4 on head_v_dim 64, and the
+    only path for head_v_dim 256. Logits within 1e-3 of the oracle with the
+    same argmax over 150 positions; SURGE_GDN_BLOCKS=1 is refused for
+    head_v_dim 256."""
+    cfg = {"HD128": HD128, "WIDE_V": WIDE_V}[cfg_name]
+    syn = S.Synth(cfg, S.SG_T_Q8_0, seed=31)
+    gpu.load_model(syn.model)
+    if blocks:
+        monkeypatch.setenv("SURGE_GDN_BLOCKS", blocks)
+    else:
+        monkeypatch.setenv("SURGE_GDN_BLOCKS", "1")
+        with pytest.raises(S.SurgeError):
+            gpu.state_new(160)
+        monkeypatch.delenv("SURGE_GDN_BLOCKS")
+    gpu.state_new(160)
+    worst = _per_position_vs_oracle(gpu, syn, cfg, 150, 160, 13, 41)
+    monkeypatch.delenv("SURGE_GDN_BLOCKS", raising=False)
+    gpu.state_new(8)
+    syn.close()
+    assert worst < 1e-3, worst
+
+
+@pytest.mark.parametrize("cfg_name", ["HD256", "HD128"])
+def test_valu_decode_partial_vs_oracle(gpu, monkeypatch, cfg_name):
+    """SURGE_ATTN_VALU=1 keeps the decode attention partial (with the fused
+    q/k prep and K/V store) on the VALU kernel: logits within 1e-3 of the
+    oracle with the same argmax, split cap 4 so splits walk several tiles."""
+    cfg = {"HD256": HD256, "HD128": HD128}[cfg_name]
+    syn = S.Synth(cfg, S.SG_T_Q8_0, seed=33)
+    gpu.load_model(syn.model)
+    monkeypatch.setenv("SURGE_ATTN_VALU", "1")
+    monkeypatch.setenv("SURGE_SPLITK_GQA_CAP", "4")
+    gpu.state_new(300)
+    worst = _per_position_vs_oracle(gpu, syn, cfg, 280, 300, 19, 43)
+    monkeypatch.delenv("SURGE_ATTN_VALU")
+    monkeypatch.delenv("SURGE_SPLITK_GQA_CAP")
+    gpu.state_new(8)
+    syn.close()
+    assert worst < 1e-3, worst
+
+
+def test_attention_arms_same_bytes_and_counts(gpu, monkeypatch):
+    """The decode arms the reference's switches select (surge.h:1179-1254):
+    the GQA partial (default), the per-head partial (SURGE_ATTN_SPLITK_GQA=0)
+    and the online arm (SURGE_ATTN_SPLITK_ONLINE=1, the same kernel) give the
+    same logits bit for bit; the single-pass form (SURGE_ATTN_SPLITK=0, one
+    split per head) agrees with the oracle. Each state counts one partial per
+    attention layer per step in its own arm's counter, from zero at
+    sg_gpu_state_new; one-shots are not counted."""
+    syn = S.Synth(HD256, S.SG_T_Q8_0, seed=35)
+    gpu.load_model(syn.model)
+    rng = np.random.default_rng(45)
+    ids = rng.integers(0, HD256["vocab"], 200).tolist()
+    n_attn = HD256["n_layers"] // HD256["full_attn_interval"]
+    runs = {}
+    for name, env, want in [("gqa", {}, (0, 1, 0)), ("per_head", {"SURGE_ATTN_SPLITK_GQA": "0"}, (1, 0, 0)),
+                            ("online", {"SURGE_ATTN_SPLITK_ONLINE": "1"}, (0, 0, 1)),
+                            ("single", {"SURGE_ATTN_SPLITK": "0"}, (0, 0, 0))]:
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        gpu.state_new(220)
+        assert gpu.dispatch_counts() == (0, 0, 0)
+        out = [gpu.forward(t, p) for p, t in enumerate(ids[:150])]
+        out.append(gpu.forward_nosync(ids[150], 150) or None)
+        dev = gpu.decode_greedy(ids[151], 151, 20)
+        n_steps = 150 + 1 + 20
+        assert gpu.dispatch_counts() == tuple(n_attn * n_steps * w for w in want), name
+        runs[name] = (np.stack(out[:150]), dev)
+        for k in env:
+            monkeypatch.delenv(k)
+    for name in ("per_head", "online"):
+        assert np.array_equal(runs[name][0], runs["gqa"][0]), name
+        assert np.array_equal(runs[name][1], runs["gqa"][1]), name
+    rm = O.RefModel(O.oracle(), syn.model, 220, kv_f16=True)
+    worst = 0.0
+    for p, t in enumerate(ids[:150]):
+        o = rm.forward(t, p)
+        if p % 11 == 0 or p == 149:
+            worst = max(worst, rel(runs["single"][0][p], o))
+    rm.close()
+    assert worst < 1e-3, worst
+    gpu.state_new(8)
+    syn.close()

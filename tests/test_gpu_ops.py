@@ -156,12 +156,22 @@ def oracle_attn(q, k16, v16, nh, nkv, hd, seq, qs, ns):
     return m, s, acc, out
 
 
-@pytest.mark.parametrize("seq,ns", [(512, 8), (512, 16), (4096, 32), (4096, 64), (32768, 64)])
-def test_splitk_gqa_baseline_config(gpu, seq, ns):
-    """BASELINE attention config: 16 q / 4 kv heads, head_dim 256, f16 KV
-    N(0,1), q N(0,1), scale 1/16, then the LSE combine."""
-    rng = np.random.default_rng(seq + ns)
-    nh, nkv, hd = 16, 4, 256
+ATT_CASES = [(16, 512, 8), (16, 512, 16), (16, 512, 0), (16, 4096, 32), (16, 4096, 64), (16, 4096, 0),
+             (16, 32768, 64), (16, 32768, 0), (24, 512, 0), (24, 4096, 8), (24, 4096, 0), (24, 32768, 32),
+             (24, 32768, 0), (24, 131072, 0)]
+
+
+@pytest.mark.parametrize("nh,seq,ns", ATT_CASES, ids=[f"{h}q-{s}-{n or 'policy'}" for h, s, n in ATT_CASES])
+def test_splitk_gqa_baseline_config(gpu, nh, seq, ns):
+    """BASELINE attention config: 16 q / 4 kv heads (and the 27B's 24 / 4),
+    head_dim 256, f16 KV N(0,1), q N(0,1), scale 1/16, at 512 / 4096 / 32768
+    keys with 8-64 splits and with the decode policy's own count (ns 0: about
+    64 keys per split, at most 128, so at 32768 keys every split walks four
+    64-key rounds, at 131072 sixteen), then the LSE combine. The one-shot runs the decode
+    path's MFMA partial (k_attn_partial_wv) with q taken as given."""
+    rng = np.random.default_rng(seq + ns + nh)
+    nkv, hd = 4, 256
+    ns = ns or S.lib().sg_gpu_splitk_gqa_n_splits(seq)
     q = rng.standard_normal(nh * hd).astype(np.float32)
     k16, v16 = f16(rng, seq * nkv * hd), f16(rng, seq * nkv * hd)
     gm, gs, gacc, gout = run_partial_combine(gpu, q, k16, v16, nh, nkv, hd, seq, hd, ns)
@@ -171,6 +181,46 @@ def test_splitk_gqa_baseline_config(gpu, seq, ns):
     assert_close(gacc, oacc)
     assert_close(gout, oout)
     assert rel_err(gout, oout) < 1e-5
+
+
+@pytest.mark.parametrize("hd,seq,ns", [(256, 4096, 64), (128, 1000, 7), (256, 70, 3)])
+def test_splitk_per_head_and_gqa_partials_same_bytes(gpu, hd, seq, ns):
+    """The per-head partial (one workgroup per query head) and the GQA one
+    (one per kv head, all of its group) give the same bytes, as the
+    reference contracts for its two kernels (surge.h:1170-1254)."""
+    rng = np.random.default_rng(hd + seq)
+    nh, nkv = 24, 4
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k16, v16 = f16(rng, seq * nkv * hd), f16(rng, seq * nkv * hd)
+    p = [nh, nkv, hd, seq, hd, S.fbits(1.0 / np.sqrt(hd)), ns]
+    outs = []
+    for gqa in (True, False):
+        bufs = [gpu.buf(q), gpu.buf(k16.view(np.uint16)), gpu.buf(v16.view(np.uint16)),
+                gpu.buf(np.zeros(nh * ns, np.float32)), gpu.buf(np.zeros(nh * ns, np.float32)),
+                gpu.buf(np.zeros(nh * ns * hd, np.float32))]
+        gpu.attn_partial(*bufs, p, gqa=gqa)
+        outs.append([b.array.copy() for b in bufs[3:]])
+        for b in bufs:
+            b.free()
+    for x, y in zip(*outs):
+        assert np.array_equal(x, y)
+
+
+def test_splitk_valu_partial_matches_mfma(gpu, monkeypatch):
+    """SURGE_ATTN_VALU=1 (the A/B switch) runs the VALU partial: against the
+    oracle at the 27B shape, and against the MFMA partial's output."""
+    rng = np.random.default_rng(77)
+    nh, nkv, hd, seq, ns = 24, 4, 256, 3000, 47
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k16, v16 = f16(rng, seq * nkv * hd), f16(rng, seq * nkv * hd)
+    mf = run_partial_combine(gpu, q, k16, v16, nh, nkv, hd, seq, hd, ns)
+    monkeypatch.setenv("SURGE_ATTN_VALU", "1")
+    va = run_partial_combine(gpu, q, k16, v16, nh, nkv, hd, seq, hd, ns)
+    monkeypatch.delenv("SURGE_ATTN_VALU")
+    om, os_, oacc, oout = oracle_attn(q, k16, v16, nh, nkv, hd, seq, hd, ns)
+    assert_close(va[3], oout)
+    assert_close(va[2], oacc)
+    assert rel_err(va[3], mf[3]) < 1e-5
 
 
 @pytest.mark.parametrize("nh,nkv,hd,seq,ns", [(4, 4, 64, 100, 3), (8, 1, 128, 77, 5), (6, 2, 32, 40, 64),
@@ -307,6 +357,122 @@ def test_conv1d_step_baseline_config(gpu):
         assert_close(ob.array[:ch], xo)
         assert np.array_equal(ob.array[ch:], st_o)   # the state shift is exact
         xb.free()
+
+
+def oracle_gdn_step(inp, w, state, dk, dv, nv, nk, ks, tiled, eps):
+    """ref.c's gdn_layer between its projections and its output projection
+    (ref.c:1283-1330), composed from the oracle's ops: conv + SiLU, q/k RMS
+    (eps 1e-6, no weight) then q / dk and k / sqrt(dk), beta = sigmoid(b),
+    decay from -exp(A_log) (the GGUF form), the delta rule per value head
+    (tiled or grouped k-head map), RMSNormGated. Returns (out, new state)."""
+    o = O.oracle()
+    kd, vd = nk * dk, nv * dv
+    cd = 2 * kd + vd
+    qkv = inp[:cd].copy()
+    z, bb, aa = inp[cd:cd + vd], inp[cd + vd:cd + vd + nv], inp[cd + vd + nv:]
+    conv_w, ssm_a = w[:cd * ks], w[cd * ks:cd * ks + nv]
+    dt, nw = w[cd * ks + nv:cd * ks + 2 * nv], np.ascontiguousarray(w[cd * ks + 2 * nv:])
+    keep = ks - 1
+    conv = state[:keep * cd].copy()
+    Sm = state[keep * cd:].copy()
+    o.sg_ref_conv1d_causal(fp(qkv), fp(np.ascontiguousarray(conv_w)), fp(conv), fp(conv), cd, ks)
+    o.sg_ref_silu(fp(qkv), cd)
+    inv = 1.0 / np.sqrt(np.float64(dk))
+    for h in range(nk):
+        for off in (0, kd):
+            seg = np.ascontiguousarray(qkv[off + h * dk:off + (h + 1) * dk])
+            o.sg_ref_rmsnorm(fp(seg), None, dk, 1e-6)
+            sc = inv * inv if off == 0 else inv
+            qkv[off + h * dk:off + (h + 1) * dk] = (seg.astype(np.float64) * sc).astype(np.float32)
+    y = np.zeros(vd, np.float32)
+    for h in range(nv):
+        hk = h % nk if tiled else h // (nv // nk)
+        beta = o.sg_ref_sigmoid(float(bb[h]))
+        decay = o.sg_ref_delta_decay_neg_a(float(ssm_a[h]), float(aa[h]), float(dt[h]))
+        o.sg_ref_delta_step(fp(Sm[h * dv * dk:]), fp(np.ascontiguousarray(qkv[hk * dk:(hk + 1) * dk])),
+                            fp(np.ascontiguousarray(qkv[kd + hk * dk:kd + (hk + 1) * dk])),
+                            fp(np.ascontiguousarray(qkv[2 * kd + h * dv:2 * kd + (h + 1) * dv])),
+                            beta, decay, fp(y[h * dv:]), dk, dv)
+    out = np.zeros(vd, np.float32)
+    for h in range(nv):
+        yy = y[h * dv:(h + 1) * dv].copy()
+        zz = z[h * dv:(h + 1) * dv].copy()
+        o.sg_ref_rmsnorm(fp(yy), fp(nw), dv, eps)
+        o.sg_ref_swiglu(fp(zz), fp(yy), dv)
+        out[h * dv:(h + 1) * dv] = zz
+    return out, np.concatenate([conv, Sm])
+
+
+GDN_CASES = [(16, 16, 128, 128, 4, True), (48, 16, 128, 128, 4, True), (6, 2, 64, 64, 4, False),
+             (8, 4, 128, 96, 2, True), (4, 4, 256, 128, 3, False)]
+
+
+@pytest.mark.parametrize("nv,nk,dk,dv,ks,tiled", GDN_CASES,
+                         ids=[f"{a}v{b}k-dk{c}-dv{d}-ks{e}-{'tiled' if f else 'grouped'}" for a, b, c, d, e, f in GDN_CASES])
+def test_gdn_decode_step_vs_oracle(gpu, nv, nk, dk, dv, ks, tiled):
+    """The decode path's fused DeltaNet step (k_gdn_step: conv ring + SiLU,
+    q/k norms and scales, beta/decay, rank-1 update and readout of S held in
+    registers, RMSNormGated) against ref.c's gdn_layer composed from the
+    oracle: the BASELINE config (16 heads, dk = dv = 128, S N(0, 0.1), conv
+    width 4; conv_dim 6144 of which 2048 per q/k/v), the 27B's 48 value heads
+    tiled over 16 key heads, a grouped map, other widths and conv sizes.
+    Three steps thread the state: outputs and S within 1e-3 (expect ~1e-6),
+    the conv tail bit-exact (it holds the inputs)."""
+    rng = np.random.default_rng(nv * 7 + dk + ks)
+    cd, vd = 2 * nk * dk + nv * dv, nv * dv
+    eps = 1e-6
+    w = np.concatenate([rng.standard_normal(cd * ks) * 0.5, -np.exp(rng.uniform(-1, 1, nv)),
+                        rng.uniform(-0.5, 0.5, nv), 1.0 + 0.1 * rng.standard_normal(dv)]).astype(np.float32)
+    state = np.concatenate([rng.standard_normal((ks - 1) * cd), rng.standard_normal(nv * dv * dk) * 0.1])
+    state = state.astype(np.float32)
+    wb, sb, ob = gpu.buf(w), gpu.buf(state.copy()), gpu.buf(np.zeros(vd, np.float32))
+    so = state.copy()
+    for step in range(3):
+        inp = rng.standard_normal(cd + vd + 2 * nv).astype(np.float32)
+        ib = gpu.buf(inp)
+        gpu.gdn_step(ib, wb, sb, ob, [dk, dv, nv, nk, ks, int(tiled), 1, S.fbits(eps)])
+        want, so = oracle_gdn_step(inp, w, so, dk, dv, nv, nk, ks, tiled, eps)
+        assert_close(ob.array, want)
+        assert np.array_equal(sb.array[:(ks - 1) * cd], so[:(ks - 1) * cd])
+        assert_close(sb.array[(ks - 1) * cd:], so[(ks - 1) * cd:])
+        ib.free()
+
+
+def test_gdn_step_rejects_bad_shapes(gpu):
+    b = gpu.buf(np.zeros(1 << 16, np.float32))
+    o = gpu.buf(np.zeros(1 << 12, np.float32))
+    for p in ([100, 64, 4, 4, 4, 1, 1, 0], [64, 256, 4, 4, 4, 1, 1, 0], [64, 64, 6, 4, 4, 1, 1, 0],
+              [64, 64, 4, 4, 5, 1, 1, 0]):
+        with pytest.raises(S.SurgeError):
+            gpu.gdn_step(b, b, o, o, p)
+
+
+FLASH_CASES = [(24, 4, 256, 1536, 64), (24, 4, 256, 4000, 37), (16, 4, 128, 2100, 100)]
+
+
+@pytest.mark.parametrize("nh,nkv,hd,base,n", FLASH_CASES, ids=[f"{a}q{b}kv-hd{c}-base{d}-n{e}" for a, b, c, d, e in FLASH_CASES])
+def test_attn_prefill_flash_deep_vs_oracle(gpu, nh, nkv, hd, base, n):
+    """The prefill path's MFMA flash attention, called through the
+    sg_gpu_run_attn_prefill one-shot: a chunk starting deep in the cache, so
+    its key tiles are split over several workgroups (one per 512 keys of the
+    deepest token, at most 8) and merged by the LSE combine; token t
+    (position base+t) against ref.c's decode attention over keys 0..base+t,
+    within 1e-3."""
+    rng = np.random.default_rng(base + n + hd)
+    qs = 2 * hd
+    tot = base + n
+    q = rng.standard_normal(n * nh * qs).astype(np.float32)
+    k16, v16 = f16(rng, tot * nkv * hd), f16(rng, tot * nkv * hd)
+    qb, kb, vb = gpu.buf(q), gpu.buf(k16.view(np.uint16)), gpu.buf(v16.view(np.uint16))
+    ob = gpu.buf(np.zeros(n * nh * hd, np.float32))
+    sc = 1.0 / np.sqrt(hd)
+    gpu.run4("attn_prefill", qb, kb, vb, ob, [nh, nkv, hd, base, n, qs, S.fbits(sc)])
+    kc, vc = k16.astype(np.float32), v16.astype(np.float32)
+    for t in list(range(0, n, 9)) + [n - 1]:
+        want = np.zeros(nh * hd, np.float32)
+        O.oracle().sg_ref_attn_decode(fp(np.ascontiguousarray(q[t * nh * qs:(t + 1) * nh * qs])), fp(kc), fp(vc),
+                                      nh, nkv, hd, base + t + 1, qs, np.float32(sc), fp(want))
+        assert_close(ob.array[t * nh * hd:(t + 1) * nh * hd], want)
 
 
 # ---------------------------------------------------------------- small ops

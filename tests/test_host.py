@@ -22,7 +22,7 @@ def declared_functions():
     src = open(os.path.join(ROOT, "include", "surge.h")).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     names = set()
-    for m in re.finditer(r"^(?!static)[A-Za-z_][\w \*]*?\b(sg_\w+)\s*\(", src, flags=re.M):
+    for m in re.finditer(r"^(?!static|typedef)[A-Za-z_][\w \*]*?\b(sg_\w+)\s*\(", src, flags=re.M):
         names.add(m.group(1))
     return sorted(names)
 
@@ -170,3 +170,153 @@ def test_gpu_init_fails_cleanly_without_a_device():
         S.lib().sg_gpu_free(h)
     else:
         assert b"no HIP device" in err.msg
+
+
+# ---------------------------------------------------------------- the C ABI against the reference header
+
+REF_HEADER = "/root/reference/surge.h"
+
+
+def _aux_prototypes(include_dir):
+    """gcc -aux-info over a unit that includes <include_dir>/surge.h: every
+    declared function as its prototype with parameter names dropped."""
+    import subprocess
+    with tempfile.TemporaryDirectory() as d:
+        src, aux = os.path.join(d, "u.c"), os.path.join(d, "aux.txt")
+        open(src, "w").write('#include "surge.h"\n')
+        subprocess.check_call(["gcc", "-std=c11", "-fsyntax-only", "-aux-info", aux, "-I", include_dir, src])
+        out = {}
+        for line in open(aux):
+            m = re.search(r"\*/\s*(.*?\b(sg_\w+)\s*\(.*\));", line)
+            if m:
+                out[m.group(2)] = re.sub(r"\s+", " ", m.group(1)).replace("extern ", "")
+        return out
+
+
+@pytest.mark.skipif(not os.path.exists(REF_HEADER), reason="reference sources absent")
+def test_abi_prototypes_match_reference_header():
+    """Every sg_gpu_* / sg_kv_* function the reference's surge.h declares is
+    declared here with the identical prototype (types as gcc prints them),
+    so the reference's own callers compile and link against this library."""
+    ref = _aux_prototypes(os.path.dirname(REF_HEADER))
+    ours = _aux_prototypes(os.path.join(ROOT, "include"))
+    wanted = sorted(n for n in ref if n.startswith(("sg_gpu_", "sg_kv_")))
+    assert len(wanted) >= 50
+    missing = [n for n in wanted if n not in ours]
+    assert not missing, missing
+    differ = {n: (ref[n], ours[n]) for n in wanted if ref[n] != ours[n]}
+    assert not differ, differ
+    L = C.CDLL(S.LIB_PATH)
+    assert all(hasattr(L, n) for n in wanted)
+
+
+# ---------------------------------------------------------------- sg_kv with a host backend
+
+# sg_err is one pointer, returned in a register: the callbacks return the
+# message pointer (NULL = success) as a c_void_p.
+_KV_ALLOC = C.CFUNCTYPE(C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p))
+_KV_FREE = C.CFUNCTYPE(None, C.c_void_p)
+_KV_HOST = C.CFUNCTYPE(C.c_void_p, C.c_void_p)
+
+
+class _MallocBackend:
+    """A malloc-backed sg_kv backend (the reference's test_kv.c mock): the
+    handle is the zero-filled memory itself."""
+
+    def __init__(self):
+        self.live = {}
+        libc = C.CDLL(None)
+        self.calloc, self.free_ = libc.calloc, libc.free
+        self.calloc.restype, self.calloc.argtypes = C.c_void_p, [C.c_size_t, C.c_size_t]
+        self.free_.argtypes = [C.c_void_p]
+
+        def alloc(g, n, buf, host):
+            p = self.calloc(1, n)
+            if not p:
+                return None
+            self.live[p] = n
+            buf[0] = p
+            if host:
+                host[0] = p
+            return None
+
+        def free(b):
+            if b:
+                self.live.pop(b)
+                self.free_(b)
+
+        self.cbs = (_KV_ALLOC(alloc), _KV_FREE(free), _KV_HOST(lambda b: b))
+
+    def register(self, L):
+        L.sg_kv_set_backend.argtypes = [_KV_ALLOC, _KV_FREE, _KV_HOST]
+        L.sg_kv_set_backend(*self.cbs)
+
+
+def _kv_cfg(**kw):
+    c = dict(n_layers=8, n_heads=4, n_kv_heads=2, head_dim=8, hidden=32, ffn_hidden=64, vocab=100,
+             rope_theta=1e4, rms_eps=1e-6, tied_embeddings=False, rope_dim=8, full_attn_interval=4,
+             n_k_heads=2, n_v_heads=4, head_k_dim=4, head_v_dim=4, conv_kernel=3, attn_output_gate=False)
+    c.update(kw)
+    return S.make_cfg(**c)
+
+
+def test_kv_module_object_with_host_backend():
+    """The reference's tests/test_kv.c object and rejection checks: layer-kind
+    routing, sizes, advance bounds, reset zeroing conv/S but not K/V, cap 0
+    -> default, cap above the maximum and unsupported dtypes refused, and no
+    backend -> an error."""
+    L = S.lib()
+    be = _MallocBackend()
+    be.register(L)
+    c = _kv_cfg()
+    kv = C.c_void_p()
+    S.check(L.sg_kv_new(None, C.byref(c), 16, S.SG_T_F16, C.byref(kv)))
+    try:
+        assert L.sg_kv_cap(kv) == 16 and L.sg_kv_used(kv) == 0
+        for l in range(8):
+            attn = (l + 1) % 4 == 0
+            assert bool(L.sg_kv_k(kv, l)) == attn and bool(L.sg_kv_v(kv, l)) == attn
+            assert bool(L.sg_kv_conv(kv, l)) != attn and bool(L.sg_kv_s(kv, l)) != attn
+        assert not L.sg_kv_k(kv, 8) and not L.sg_kv_conv(kv, 8)
+        # sizes: K/V [cap, n_kv, hd] f16; conv [ksize-1, conv_dim] and S [n_v, dv, dk] f32
+        assert be.live[L.sg_kv_k(kv, 3)] == 16 * 2 * 8 * 2
+        assert be.live[L.sg_kv_conv(kv, 0)] == 2 * 32 * 4 and be.live[L.sg_kv_s(kv, 0)] == 4 * 4 * 4 * 4
+        total = sum(be.live.values())
+        assert total == L.sg_kv_bytes(C.byref(c), 16, S.SG_T_F16) + L.sg_kv_state_bytes(C.byref(c))
+        S.check(L.sg_kv_advance(kv, 10))
+        S.check(L.sg_kv_advance(kv, 6))
+        assert L.sg_kv_used(kv) == 16
+        assert L.sg_kv_advance(kv, 1).msg and L.sg_kv_used(kv) == 16
+        L.sg_kv_reset(kv)
+        assert L.sg_kv_advance(kv, 0xFFFFFFFF).msg and L.sg_kv_used(kv) == 0
+        conv0, s0, k3 = L.sg_kv_conv(kv, 0), L.sg_kv_s(kv, 0), L.sg_kv_k(kv, 3)
+        C.memset(conv0, 0xAB, 64)
+        C.memset(s0, 0xCD, 64)
+        C.cast(k3, C.POINTER(C.c_uint16))[0] = 0xBEEF
+        S.check(L.sg_kv_advance(kv, 5))
+        L.sg_kv_reset(kv)
+        assert L.sg_kv_used(kv) == 0
+        assert not any((C.c_uint8 * 64).from_address(conv0)) and not any((C.c_uint8 * 64).from_address(s0))
+        assert C.cast(k3, C.POINTER(C.c_uint16))[0] == 0xBEEF
+    finally:
+        L.sg_kv_free(kv)
+    assert not be.live
+    # dense (every layer attention, no DeltaNet dims)
+    d = _kv_cfg(n_layers=6, full_attn_interval=1, n_k_heads=0, n_v_heads=0, head_k_dim=0, head_v_dim=0,
+                conv_kernel=0)
+    S.check(L.sg_kv_new(None, C.byref(d), 16, S.SG_T_F32, C.byref(kv)))
+    assert all(L.sg_kv_k(kv, l) and not L.sg_kv_s(kv, l) for l in range(6))
+    L.sg_kv_free(kv)
+    # rejections
+    for cap, dt in [(S.SG_KV_CAP_MAX + 1, S.SG_T_F16), (8, S.SG_T_Q8_0)]:
+        e = L.sg_kv_new(None, C.byref(c), cap, dt, C.byref(kv))
+        assert e.msg and not kv.value
+    assert b"cap" in L.sg_kv_new(None, C.byref(c), S.SG_KV_CAP_MAX + 1, S.SG_T_F16, C.byref(kv)).msg
+    S.check(L.sg_kv_new(None, C.byref(c), 0, S.SG_T_F16, C.byref(kv)))
+    assert L.sg_kv_cap(kv) == 131072
+    L.sg_kv_free(kv)
+    wide = _kv_cfg(head_k_dim=1 << 24)
+    assert L.sg_kv_new(None, C.byref(wide), 8, S.SG_T_F16, C.byref(kv)).msg
+    L.sg_kv_set_backend(_KV_ALLOC(), _KV_FREE(), _KV_HOST())
+    assert b"backend" in L.sg_kv_new(None, C.byref(c), 8, S.SG_T_F16, C.byref(kv)).msg
+    assert not be.live
