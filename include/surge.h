@@ -334,6 +334,25 @@ sg_err sg_gpu_state_fill_synthetic(sg_gpu *g, uint32_t n_tokens, uint32_t seed);
 void *sg_gpu_stream(const sg_gpu *g);
 sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which);
 
+/* Timing hooks for the per-kernel micro configs (no reference counterpart).
+ * Each runs one product kernel `reps` times back to back and reports the
+ * average microseconds per launch from HIP events around the launches;
+ * launch i reads input copy i mod n of n copies spanning at least
+ * rotate_bytes (0: one copy, cache resident), so timed launches do not find
+ * their inputs in the 256 MB MALL.
+ *   sg_gpu_time_matvec_q8: the decode GEMV on a Q8_0 [rows][cols/32] matrix;
+ *   sg_gpu_time_attn: the split-K partial (q as given) then the LSE combine,
+ *     p as sg_gpu_run_attn_splitk_partial_gqa (p[6] = 0: the decode policy's
+ *     split count); us[0] partial, us[1] combine;
+ *   sg_gpu_time_gdn_step: the fused DeltaNet step, in/w/p as
+ *     sg_gpu_run_gdn_step, the state S and conv ring rotated. */
+sg_err sg_gpu_time_matvec_q8(sg_gpu *g, void *w, void *x, void *y, uint32_t rows, uint32_t cols,
+                             uint64_t rotate_bytes, uint32_t reps, double *us);
+sg_err sg_gpu_time_attn(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t params[8],
+                        uint64_t rotate_bytes, uint32_t reps, double *us);
+sg_err sg_gpu_time_gdn_step(sg_gpu *g, void *in, void *w, void *out, const uint32_t params[8],
+                            uint64_t rotate_bytes, uint32_t reps, double *us);
+
 /* ---------------------------------------------------------------------
  * KV cache + DeltaNet state sizing and f16 (surge.h:1410-1501)
  * --------------------------------------------------------------------- */

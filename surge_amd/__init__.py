@@ -137,6 +137,12 @@ _SIGS = {
     "sg_gpu_used": (C.c_uint32, [C.c_void_p]),
     "sg_gpu_stream": (C.c_void_p, [C.c_void_p]),
     "sg_gpu_enqueue_gemv": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32]),
+    "sg_gpu_time_matvec_q8": (SgErr, [C.c_void_p] * 4 + [C.c_uint32, C.c_uint32, C.c_uint64, C.c_uint32,
+                                                          C.POINTER(C.c_double)]),
+    "sg_gpu_time_attn": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32), C.c_uint64, C.c_uint32,
+                                                     C.POINTER(C.c_double)]),
+    "sg_gpu_time_gdn_step": (SgErr, [C.c_void_p] * 4 + [C.POINTER(C.c_uint32), C.c_uint64, C.c_uint32,
+                                                         C.POINTER(C.c_double)]),
     "sg_gguf_open": (SgErr, [C.c_char_p, C.POINTER(C.c_void_p)]),
     "sg_gguf_close": (None, [C.c_void_p]),
     "sg_model_from_gguf": (SgErr, [C.c_void_p, C.POINTER(SgModel)]),
@@ -352,6 +358,24 @@ class Gpu:
 
     def stream(self) -> int:
         return lib().sg_gpu_stream(self.handle)
+
+    def time_matvec_q8(self, w: Buf, x: Buf, y: Buf, rows: int, cols: int, rotate: int, reps: int) -> float:
+        us = C.c_double()
+        check(lib().sg_gpu_time_matvec_q8(self.handle, w.handle, x.handle, y.handle, rows, cols, rotate, reps,
+                                          C.byref(us)))
+        return us.value
+
+    def time_attn(self, q: Buf, k: Buf, v: Buf, out: Buf, p, rotate: int, reps: int):
+        us = (C.c_double * 2)()
+        check(lib().sg_gpu_time_attn(self.handle, q.handle, k.handle, v.handle, out.handle, params(p), rotate,
+                                     reps, us))
+        return us[0], us[1]
+
+    def time_gdn_step(self, inp: Buf, w: Buf, out: Buf, p, rotate: int, reps: int) -> float:
+        us = C.c_double()
+        check(lib().sg_gpu_time_gdn_step(self.handle, inp.handle, w.handle, out.handle, params(p), rotate, reps,
+                                         C.byref(us)))
+        return us.value
 
     def enqueue_gemv(self, layer: int, which: int):
         check(lib().sg_gpu_enqueue_gemv(self.handle, layer, which))

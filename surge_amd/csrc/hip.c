@@ -850,16 +850,34 @@ sg_err sg_gpu_run_attn_splitk_partial_gqa_online(sg_gpu *g, void *q, void *k, vo
  * model load
  * --------------------------------------------------------------------- */
 
+static void mat_free(sg_gpu *g, dmat *M) {
+    dfree(g, M->qs);
+    dfree(g, M->d);
+    dfree(g, M->wf);
+    *M = (dmat){0};
+}
+
+/* Releases the loaded model's device weights and clears every handle to
+ * them, so a model loaded next (of either weight type) starts clean. */
 static void model_free(sg_gpu *g) {
-    if (!g->ls) return;
-    /* every device pointer is in the allocation table; sg_gpu_free releases
-     * them. Here we only drop the layer table so a reload starts clean. */
+    for (uint32_t i = 0; g->ls && i < g->cfg.n_layers; i++) {
+        glayer *L = &g->ls[i];
+        mat_free(g, &L->in); mat_free(g, &L->out); mat_free(g, &L->gu); mat_free(g, &L->down);
+        float *sm[] = {L->ln1, L->ln2, L->qn, L->kn, L->ssm_norm, L->conv_w, L->ssm_a, L->dt_bias};
+        for (size_t k = 0; k < sizeof sm / sizeof *sm; k++) dfree(g, sm[k]);
+    }
     free(g->ls);
     g->ls = NULL;
+    if (!g->lm_is_emb) mat_free(g, &g->lm);
+    g->lm = (dmat){0};
+    mat_free(g, &g->emb);
+    dfree(g, g->out_norm);
+    g->out_norm = NULL;
     g->model = NULL;
 }
 
 static sg_err mat_alloc(sg_gpu *g, dmat *M, uint32_t rows, uint32_t cols) {
+    *M = (dmat){0};
     M->rows = rows;
     M->cols = cols;
     sg_err e;
@@ -1630,4 +1648,180 @@ sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which) {
     a.qs = M->qs; a.d = M->d; a.wf = M->wf; a.rows = M->rows; a.cols = M->cols;
     HIPCHK(sgk_gemv_launch(&a, g->stream), "gemv launch");
     return SG_OK;
+}
+
+/* ---------------------------------------------------------------------
+ * timing hooks for the per-kernel micro configs (no reference counterpart)
+ *
+ * Each runs one product kernel `reps` times back to back on the library
+ * stream and reports the average microseconds per launch from HIP events
+ * around the launches. Launch i reads input copy i % n, the n copies laid out
+ * one after another in a scratch allocation of at least `rotate_bytes`, so a
+ * timed launch does not find its inputs in the 256 MB MALL left there by the
+ * launch before; rotate_bytes 0 keeps one copy (the cache-resident figure).
+ * Inputs come from caller buffers (uploaded from their host mirrors).
+ * --------------------------------------------------------------------- */
+
+static uint64_t n_copies(uint64_t unit, uint64_t rotate_bytes) {
+    uint64_t n = rotate_bytes ? (rotate_bytes + unit - 1) / unit : 1;
+    return n < 1 ? 1 : n;
+}
+
+static sg_err timed(sg_gpu *g, hipEvent_t a, hipEvent_t b, uint32_t reps, double *us) {
+    HIPCHK(hipEventSynchronize(b), "timing");
+    float ms = 0.0f;
+    HIPCHK(hipEventElapsedTime(&ms, a, b), "timing");
+    *us = (double)ms * 1e3 / reps;
+    (void)g;
+    return SG_OK;
+}
+
+/* The decode GEMV (k_gemv_q8, no prologue, plain store) on a Q8_0 matrix
+ * [rows][cols/32] of 34-byte blocks: y = W x. */
+sg_err sg_gpu_time_matvec_q8(sg_gpu *g, void *w, void *x, void *y, uint32_t rows, uint32_t cols,
+                             uint64_t rotate_bytes, uint32_t reps, double *us) {
+    if (!g || !w || !x || !y || !us || !reps || !rows || !cols || cols % 32)
+        return (sg_err){"gpu: sg_gpu_time_matvec_q8 got an invalid argument"};
+    sg_err e;
+    if (sg_failed(e = need(w, (uint64_t)rows * (cols / 32) * 34, "w")) || sg_failed(e = need(x, (uint64_t)cols * 4, "x")) ||
+        sg_failed(e = need(y, (uint64_t)rows * 4, "y"))) return e;
+    void *ins[2] = {w, x};
+    if (sg_failed(e = push(ins, 2))) return e;
+    const uint64_t qb = ((uint64_t)rows * cols + 255) / 256 * 256, db = ((uint64_t)rows * (cols / 32) * 2 + 255) / 256 * 256;
+    const uint64_t n = n_copies(qb + db, rotate_bytes);
+    char *base;
+    if (sg_failed(e = dalloc(g, n * (qb + db), (void **)&base))) return e;
+    hipStream_t s = g->stream;
+    hipEvent_t a = NULL, b = NULL;
+    hipError_t he = sgk_repack_q8(DEV(w), rows, cols, (int8_t *)base, (uint16_t *)(base + qb), 0, 1, s);
+    for (uint64_t i = 1; i < n && he == hipSuccess; i++)
+        he = hipMemcpyAsync(base + i * (qb + db), base, qb + db, hipMemcpyDeviceToDevice, s);
+    if (he == hipSuccess) he = hipEventCreate(&a);
+    if (he == hipSuccess) he = hipEventCreate(&b);
+    sgk_gemv ga = {0};
+    ga.rows = rows; ga.cols = cols; ga.x = DEV(x); ga.y = DEV(y); ga.pro = SGK_PRO_NONE; ga.epi = SGK_EPI_STORE;
+    for (uint32_t r = 0; r < reps + 1 && he == hipSuccess; r++) {     /* launch 0 warms up, untimed */
+        const uint64_t c = (uint64_t)(r + n - 1) % n;
+        ga.qs = (const int8_t *)(base + c * (qb + db));
+        ga.d = (const uint16_t *)(base + c * (qb + db) + qb);
+        if (r == 1) he = hipEventRecord(a, s);
+        if (he == hipSuccess) he = sgk_gemv_launch(&ga, s);
+    }
+    if (he == hipSuccess) he = hipEventRecord(b, s);
+    if (he == hipSuccess) e = timed(g, a, b, reps, us);
+    else e = errf("gpu: sg_gpu_time_matvec_q8: %s", hipGetErrorString(he));
+    hipStreamSynchronize(s);
+    if (a) hipEventDestroy(a);
+    if (b) hipEventDestroy(b);
+    dfree(g, base);
+    if (!sg_failed(e)) e = sg_gpu_buf_download(y);
+    return e;
+}
+
+/* The decode split-K attention (the partial on q as given, then the LSE
+ * combine), p as sg_gpu_run_attn_splitk_partial_gqa with p[6] = n_splits (0 =
+ * the decode policy's count). K and V [seq][n_kv][hd] f16 are rotated;
+ * us[0] = partial, us[1] = combine (each timed over its own reps launches). */
+sg_err sg_gpu_time_attn(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8],
+                        uint64_t rotate_bytes, uint32_t reps, double *us) {
+    if (!g || !q || !k || !v || !out || !p || !us || !reps) return (sg_err){"gpu: sg_gpu_time_attn got an invalid argument"};
+    uint32_t pp[8];
+    memcpy(pp, p, sizeof pp);
+    if (!pp[6]) pp[6] = sgk_n_splits(pp[3]);
+    sg_err e = attn_check(pp, true, false);
+    if (sg_failed(e)) return e;
+    const uint32_t nh = pp[0], nkv = pp[1], hd = pp[2], seq = pp[3], qs = pp[4], ns = pp[6];
+    if (!seq) return (sg_err){"gpu: sg_gpu_time_attn needs seq >= 1"};
+    const uint64_t kvb = (uint64_t)seq * nkv * hd * 2, unit = (2 * kvb + 255) / 256 * 256;
+    if (sg_failed(e = need(q, ((uint64_t)(nh - 1) * qs + hd) * 4, "q")) || sg_failed(e = need(k, kvb, "k")) ||
+        sg_failed(e = need(v, kvb, "v")) || sg_failed(e = need(out, (uint64_t)nh * hd * 4, "out"))) return e;
+    void *ins[3] = {q, k, v};
+    if (sg_failed(e = push(ins, 3))) return e;
+    const uint64_t n = n_copies(unit, rotate_bytes), part = (uint64_t)nh * ns * (2 + hd) * 4;
+    char *base;
+    if (sg_failed(e = dalloc(g, n * unit + part, (void **)&base))) return e;
+    hipStream_t s = g->stream;
+    hipEvent_t ev[4] = {0};
+    hipError_t he = hipSuccess;
+    for (uint64_t i = 0; i < n && he == hipSuccess; i++) {
+        he = hipMemcpyAsync(base + i * unit, DEV(k), kvb, hipMemcpyDeviceToDevice, s);
+        if (he == hipSuccess) he = hipMemcpyAsync(base + i * unit + kvb, DEV(v), kvb, hipMemcpyDeviceToDevice, s);
+    }
+    for (int i = 0; i < 4 && he == hipSuccess; i++) he = hipEventCreate(&ev[i]);
+    float *mm = (float *)(base + n * unit), *ss = mm + (uint64_t)nh * ns, *aa = ss + (uint64_t)nh * ns;
+    sgk_attn A = {0};
+    A.q = DEV(q); A.m = mm; A.s = ss; A.acc = aa; A.out = DEV(out);
+    A.n_heads = nh; A.n_kv = nkv; A.hd = hd; A.q_stride = qs; A.seq = seq; A.n_splits = ns; A.max_splits = ns;
+    A.ntok = 1; A.scale = fbits(pp[5]);
+    for (uint32_t r = 0; r < reps + 1 && he == hipSuccess; r++) {
+        const uint64_t c = (uint64_t)(r + n - 1) % n;
+        A.kc = (uint16_t *)(base + c * unit);
+        A.vc = (uint16_t *)(base + c * unit + kvb);
+        if (r == 1) he = hipEventRecord(ev[0], s);
+        if (he == hipSuccess) he = sgk_attn_partial(&A, s);
+    }
+    if (he == hipSuccess) he = hipEventRecord(ev[1], s);
+    for (uint32_t r = 0; r < reps + 1 && he == hipSuccess; r++) {
+        if (r == 1) he = hipEventRecord(ev[2], s);
+        if (he == hipSuccess) he = sgk_attn_combine(&A, s);
+    }
+    if (he == hipSuccess) he = hipEventRecord(ev[3], s);
+    if (he == hipSuccess) e = timed(g, ev[0], ev[1], reps, &us[0]);
+    else e = errf("gpu: sg_gpu_time_attn: %s", hipGetErrorString(he));
+    if (!sg_failed(e)) e = timed(g, ev[2], ev[3], reps, &us[1]);
+    hipStreamSynchronize(s);
+    for (int i = 0; i < 4; i++) if (ev[i]) hipEventDestroy(ev[i]);
+    dfree(g, base);
+    if (!sg_failed(e)) e = sg_gpu_buf_download(out);
+    return e;
+}
+
+/* The fused DeltaNet decode step (k_gdn_step, one workgroup per value head)
+ * with buffers and p as sg_gpu_run_gdn_step; the rotated copies are the
+ * state S and the 4-slot conv ring (the per-layer state a decode step reads
+ * and writes). */
+sg_err sg_gpu_time_gdn_step(sg_gpu *g, void *in, void *w, void *out, const uint32_t p[8], uint64_t rotate_bytes,
+                            uint32_t reps, double *us) {
+    if (!g || !in || !w || !out || !p || !us || !reps) return (sg_err){"gpu: sg_gpu_time_gdn_step got an invalid argument"};
+    const uint32_t dk = p[0], dv = p[1], nv = p[2], nk = p[3], ks = p[4];
+    if ((dk != 32 && dk != 64 && dk != 128 && dk != 256) || !dv || dv > 128 || !nv || !nk || nv % nk || ks < 1 || ks > 4)
+        return (sg_err){"gpu: sg_gpu_time_gdn_step: bad shape"};
+    const uint64_t cd = 2ull * nk * dk + (uint64_t)nv * dv, vd = (uint64_t)nv * dv;
+    sg_err e;
+    if (sg_failed(e = need(in, (cd + vd + 2ull * nv) * 4, "in")) || sg_failed(e = need(w, (cd * ks + 2ull * nv + dv) * 4, "w")) ||
+        sg_failed(e = need(out, vd * 4, "out"))) return e;
+    void *ins[2] = {in, w};
+    if (sg_failed(e = push(ins, 2))) return e;
+    const uint64_t unit = ((4 * cd + vd * dk) * 4 + 255) / 256 * 256, n = n_copies(unit, rotate_bytes);
+    char *base;
+    if (sg_failed(e = dzalloc(g, 256 + n * unit, (void **)&base))) return e;
+    hipStream_t s = g->stream;
+    sgk_step st = {0, 3, {0, 0}};
+    hipEvent_t a = NULL, b = NULL;
+    hipError_t he = hipMemcpyAsync(base, &st, sizeof st, hipMemcpyHostToDevice, s);
+    if (he == hipSuccess) he = sgk_fill_hash(base + 256, n * unit / 4, 0, 5, 0.05f, s);
+    if (he == hipSuccess) he = hipEventCreate(&a);
+    if (he == hipSuccess) he = hipEventCreate(&b);
+    const float *wp = DEV(w);
+    sgk_gdn d = {0};
+    d.in = DEV(in); d.z = (const float *)DEV(in) + cd; d.conv_w = wp; d.ssm_a = wp + cd * ks;
+    d.dt_bias = d.ssm_a + nv; d.norm_w = d.dt_bias + nv; d.step = (const sgk_step *)base;
+    d.n_k = nk; d.n_v = nv; d.dk = dk; d.dv = dv; d.conv_dim = (uint32_t)cd; d.ksize = ks;
+    d.tiled = p[5] != 0; d.neg_exp = p[6] != 0; d.out = DEV(out); d.eps = fbits(p[7]); d.blocks = 1;
+    for (uint32_t r = 0; r < reps + 1 && he == hipSuccess; r++) {
+        char *c = base + 256 + (uint64_t)((r + n - 1) % n) * unit;
+        d.ring = (float *)c;
+        d.S = (float *)c + 4 * cd;
+        if (r == 1) he = hipEventRecord(a, s);
+        if (he == hipSuccess) he = sgk_gdn_step(&d, s);
+    }
+    if (he == hipSuccess) he = hipEventRecord(b, s);
+    if (he == hipSuccess) e = timed(g, a, b, reps, us);
+    else e = errf("gpu: sg_gpu_time_gdn_step: %s", hipGetErrorString(he));
+    hipStreamSynchronize(s);
+    if (a) hipEventDestroy(a);
+    if (b) hipEventDestroy(b);
+    dfree(g, base);
+    if (!sg_failed(e)) e = sg_gpu_buf_download(out);
+    return e;
 }
