@@ -188,6 +188,16 @@ sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
  * p: [0]=n_heads [1]=n_kv [2]=hd [3]=seq [4]=q_stride [5]=scale bits. */
 sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out,
                                   const uint32_t params[8]);
+/* No reference counterpart: sg_gpu_run_attn_decode_f16 with no device
+ * allocation, for callers that cannot allocate (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). Its partials live
+ * in a static 4 MiB device workspace per GPU, so n_heads * n_splits *
+ * (head_dim + 2) * 4 bytes must fit (n_splits = sg_gpu_splitk_gqa_n_splits(seq));
+ * larger calls are refused. Calls that overlap on one GPU share the
+ * workspace and race. */
+sg_err sg_gpu_run_attn_decode_f16_noalloc(sg_gpu *g, void *q, void *k, void *v, void *out,
+                                          const uint32_t params[8]);
+
 /* Split-K decode attention (surge.h:890-980). Split i covers
  * [i*seq/n, (i+1)*seq/n); m, s f32 [n_heads, n_splits]; acc f32
  * [n_heads, n_splits, hd]. p: [0]=n_heads [1]=n_kv [2]=hd [3]=seq

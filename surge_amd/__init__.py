@@ -100,6 +100,7 @@ _SIGS = {
     "sg_gpu_run_op": (SgErr, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_void_p,
                               C.POINTER(C.c_uint32)]),
     "sg_gpu_run_attn_decode_f16": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_run_attn_decode_f16_noalloc": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_run_attn_splitk_partial": (SgErr, [C.c_void_p] * 7 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_run_attn_splitk_partial_gqa": (SgErr, [C.c_void_p] * 7 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_run_attn_splitk_combine": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),

@@ -200,6 +200,13 @@ sg_err sg_gpu_init(sg_gpu **out) {
     if (!g) return (sg_err){"gpu: out of memory"};
     g->dev = 0;
     if (hipSetDevice(0) != hipSuccess) { free(g); return (sg_err){"gpu: hipSetDevice failed"}; }
+    /* the no-allocation entry points' static workspace: its device address on
+     * this device, looked up once with the device current */
+    hipError_t se = sgk_scratch_init(g->dev);
+    if (se != hipSuccess) {
+        free(g);
+        return errf("gpu: static workspace lookup failed: %s", hipGetErrorString(se));
+    }
     /* Default priority (never a prioritised stream). */
     if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess) {
         free(g);
@@ -587,9 +594,10 @@ sg_err sg_gpu_run_attn_splitk_combine(sg_gpu *g, void *m, void *s, void *acc, vo
 
 /* Single-pass decode attention: the split-K pair with the decode policy's
  * split count, combined, in one call. p: [0]=nh [1]=nkv [2]=hd [3]=seq
- * [4]=q_stride [5]=scale. The partials go to the gpu's lazily grown one-shot
- * scratch. */
-static sg_err attn_decode_oneshot(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8]) {
+ * [4]=q_stride [5]=scale. The partials go to `ws` when given (the
+ * no-allocation variant), else to the gpu's lazily grown one-shot scratch. */
+static sg_err attn_decode_oneshot(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8],
+                                  bool no_alloc) {
     if (!g || !q || !k || !v || !out || !p) return (sg_err){"gpu: attention one-shot got a NULL argument"};
     uint32_t pp[8];
     memcpy(pp, p, sizeof pp);
@@ -603,7 +611,15 @@ static sg_err attn_decode_oneshot(sg_gpu *g, void *q, void *k, void *v, void *ou
         sg_failed(e = need(out, (uint64_t)nh * hd * 4, "out"))) return e;
     const uint64_t wsb = (uint64_t)nh * ns * (2 + hd) * 4;
     void *t;
-    if (sg_failed(e = scratch(g, wsb, &t))) return e;
+    if (no_alloc) {
+        if (wsb > SGK_SCRATCH_BYTES)
+            return errf("gpu: attn_decode_f16_noalloc: %u heads x %u splits x (head_dim %u + 2) partials need %llu "
+                        "bytes; the static workspace holds %u", nh, ns, hd, (unsigned long long)wsb,
+                        (unsigned)SGK_SCRATCH_BYTES);
+        if (!(t = sgk_scratch_ptr(g->dev))) return (sg_err){"gpu: the static workspace is not set up"};
+    } else if (sg_failed(e = scratch(g, wsb, &t))) {
+        return e;
+    }
     float *mm = t, *ss = mm + (uint64_t)nh * ns, *aa = ss + (uint64_t)nh * ns;
     void *ins[3] = {q, k, v}, *outs[1] = {out};
     if (sg_failed(e = push(ins, 3))) return e;
@@ -617,7 +633,18 @@ static sg_err attn_decode_oneshot(sg_gpu *g, void *q, void *k, void *v, void *ou
 }
 
 sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8]) {
-    return attn_decode_oneshot(g, q, k, v, out, p);
+    return attn_decode_oneshot(g, q, k, v, out, p, false);
+}
+
+/* The same call with no device allocation (no reference counterpart; for
+ * callers that cannot allocate): the partials live in the library's static
+ * device workspace (SGK_SCRATCH_BYTES = 4 MiB per GPU, found at sg_gpu_init),
+ * so n_heads * n_splits * (head_dim + 2) * 4 bytes must fit in it (24 heads
+ * at head_dim 256 and 128 splits do). Calls that overlap on one GPU share
+ * that workspace and race; this library's calls are synchronous on one
+ * stream, so its own calls never overlap. */
+sg_err sg_gpu_run_attn_decode_f16_noalloc(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8]) {
+    return attn_decode_oneshot(g, q, k, v, out, p, true);
 }
 
 /* Split policy (surge.h:1020-1106), re-derived for 256 CUs: see kernels.h. */

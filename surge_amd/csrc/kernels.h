@@ -261,6 +261,14 @@ hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, floa
                        uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, float *part,
                        uint64_t part_cap, hipStream_t s);
 
+/* The device-resident workspace of the no-allocation entry points: a
+ * file-scope device array of SGK_SCRATCH_BYTES in kernels.hip. Call
+ * sgk_scratch_init(dev) once per device with that device current; then
+ * sgk_scratch_ptr(dev) is its device address (NULL before init). */
+#define SGK_SCRATCH_BYTES (4u << 20)
+hipError_t sgk_scratch_init(int dev);
+void *sgk_scratch_ptr(int dev);
+
 #ifdef __cplusplus
 }
 #endif

@@ -3612,3 +3612,35 @@ extern "C" hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16
     sgk_gemm_args a = {X, qs, d, NULL, Y, N, M, K, K, M, SGK_EPI_STORE, xs, part, part_cap};
     return sgk_gemm(&a, s);
 }
+
+// ---------------------------------------------------------------------------
+// A device-resident workspace for callers that cannot allocate (code under
+// graph capture, serving loops): the no-allocation entry points place their
+// partials here instead of in memory from hipMalloc. Each GPU holds its own
+// copy until the process ends; its device address is looked up once per
+// device (hipGetSymbolAddress, with that device current) and kept, and only
+// that address is ever handed to kernels, fills or copies. Every call on one
+// GPU shares it, so calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[SGK_SCRATCH_BYTES];
+#define SGK_SCRATCH_DEVICES 64
+static void *scratch_at[SGK_SCRATCH_DEVICES];
+
+extern "C" hipError_t sgk_scratch_init(int dev) {
+    if (dev < 0 || dev >= SGK_SCRATCH_DEVICES) return hipErrorInvalidDevice;
+    if (scratch_at[dev]) return hipSuccess;
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != dev) return hipErrorInvalidDevice;       // the caller makes `dev` current
+    void *p = NULL;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    scratch_at[dev] = p;
+    return hipSuccess;
+}
+
+extern "C" void *sgk_scratch_ptr(int dev) {
+    return (dev >= 0 && dev < SGK_SCRATCH_DEVICES) ? scratch_at[dev] : NULL;
+}
