@@ -348,7 +348,7 @@ def main():
     t = time.time()
     gpu.load_model(syn.model)
     log(f"loaded to HBM in {time.time() - t:.1f} s ({gpu.alloc_bytes() / 1e9:.2f} GB allocated)")
-    need = a.ctx + a.warmup + a.steps + 8
+    need = a.ctx + a.warmup + 2 * a.steps + 8
     if need > S.SG_KV_CAP_MAX:
         print(f"--ctx {a.ctx} with {a.warmup} + {a.steps} steps needs {need} positions; the cap is "
               f"{S.SG_KV_CAP_MAX}", file=sys.stderr)
@@ -379,11 +379,44 @@ def main():
     log(f"decoded {a.steps} tokens in {dt * 1e3:.1f} ms: {tps:.1f} tok/s; first ids {toks[:8].tolist()}")
     bytes_tok, parts = step_bytes(cfg, a.ctx + a.warmup + a.steps // 2)
     decode_gbs = bytes_tok * tps / 1e9
+    # surge-bench's decode-by-slope over per-token times (reference cli_bench.c:627-693):
+    # K more greedy steps with a HIP event after each, fitted by sg_bench_slope
+    t_slope = time.perf_counter()
+    _, t_cum = gpu.decode_greedy_timed(int(toks[-1]), pos + a.steps, a.steps)
+    slope_wall = time.perf_counter() - t_slope
+    tc = np.ascontiguousarray(t_cum)
+    warm = S.lib().sg_bench_default_warmup(a.steps)
+    tcp = tc.ctypes.data_as(C.POINTER(C.c_double))
+    slope = S.lib().sg_bench_slope(tcp, a.steps, warm)
+    avg = S.lib().sg_bench_avg_tps(tcp, a.steps, warm)
+    log(f"decode by slope over {a.steps} timed steps (warmup {warm}): {slope:.1f} tok/s (endpoint average {avg:.1f})")
     roof = gemv_roofline(gpu, cfg)
     if a.calib_mb:
         calib_copy(a.calib_mb << 20)
     roof["traffic"] = measured_traffic("k_gemv_q8<2, 1, 2>")
     log(f"gate/up GEMV: {roof['avg_us']} us/launch, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
+    row = S.BenchRow()
+    row.model = f"qwen35-{a.shape}-shape-q8_0-random".encode()
+    row.engine = b"surge_amd (MI355X, HIP)"
+    row.prefill_tps = -1.0 if a.fill else a.ctx / pf_s
+    row.prefill_wall_s = pf_s
+    row.prefill_compute_tps = row.prefill_tps
+    row.prefill_segments = 0 if a.fill else S.lib().sg_gpu_prefill_segments(gpu.handle)
+    row.decode_tps_slope, row.decode_tps_avg = slope, avg
+    row.decode_wall_s = slope_wall
+    row.decode_compute_tps = a.steps / slope_wall
+    row.decode_rest_s = 0.0
+    row.gpu_alloc_gib = gpu.alloc_bytes() / 2 ** 30
+    row.peak_ram_gib = peak_rss_gib()
+    row.n_prompt_tok, row.n_gen = a.ctx, a.steps
+    row.wall_s = pf_s + dt + slope_wall
+    # the admission gate's GEMM reading: the prefill's projection flops over its
+    # whole wall time (a lower bound on the prefill GEMM's rate)
+    row.gemm_tflops = -1.0 if a.fill else 2.0 * a.ctx * (parts["weights"] - q8_bytes(cfg["vocab"], cfg["hidden"])) \
+        * 32 / 34 / pf_s / 1e12
+    row.ingestion_ok = gpu.used() == pos + 2 * a.steps
+    row.log_id = f"ctx{a.ctx}_{a.shape}_surge_amd".encode()
+    S.lib().sg_bench_finalize_status(C.byref(row))
     gpu.close()
     cpu = None
     if not a.no_cpu:
@@ -406,8 +439,22 @@ def main():
                      "tok_per_s": round(a.ctx / pf_s, 1)}),
         "roofline": roof,
         "cpu_baseline": cpu,
+        "decode_by_slope": {"tok_s": round(slope, 3), "endpoint_avg_tok_s": round(avg, 3), "steps": a.steps,
+                            "warmup": int(warm), "clock": "HIP events after each step"},
+        "bench_row": {"md": row.md(), "json": json.loads(row.json())},
     }
     print(json.dumps(line), flush=True)
+
+
+def peak_rss_gib():
+    """The process's peak resident set (VmHWM), GiB."""
+    try:
+        for ln in open("/proc/self/status"):
+            if ln.startswith("VmHWM:"):
+                return int(ln.split()[1]) / 2 ** 20
+    except OSError:
+        pass
+    return 0.0
 
 
 def syn_bytes_hint(cfg):

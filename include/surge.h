@@ -328,6 +328,11 @@ sg_err sg_gpu_sync(sg_gpu *g);
  * step i. Same tokens as calling sg_gpu_forward + sg_argmax_f32 in a loop. */
 sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
                             uint32_t n_steps, int32_t *out_tokens);
+/* The same with per-token timestamps (no reference counterpart): t_cum[i] is
+ * the seconds from just before the first step to the end of step i, from HIP
+ * events between the steps, the series sg_bench_slope fits. */
+sg_err sg_gpu_decode_greedy_timed(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
+                                  uint32_t n_steps, int32_t *out_tokens, double *t_cum);
 /* Decode at depth without a prefill (no reference counterpart; for
  * benchmarks of the KV read path at long context): fills every attention
  * layer's K/V cache rows [0, n_tokens) with seeded f16 values in [-2, 2], the
@@ -411,6 +416,53 @@ uint32_t sg_argmax_f32(const float *v, uint32_t n);
 double sg_bench_slope(const double *t_wall_cum, uint32_t n, uint32_t warmup);
 double sg_bench_avg_tps(const double *t_wall_cum, uint32_t n, uint32_t warmup);
 uint32_t sg_bench_default_warmup(uint32_t n_gen);
+
+/* One surge-bench leaderboard row (surge.h:1845-1914), field for field: the
+ * reference's CLI and recipes fill it and hand it to the formatters below.
+ * Every char array is NUL-terminated by whoever fills it. */
+typedef struct {
+    char model[64];
+    char engine[64];
+    double prefill_tps;          /* < 0: not measured ("-" in the md row) */
+    double decode_tps_slope;     /* sg_bench_slope */
+    double decode_tps_avg;       /* sg_bench_avg_tps */
+    double prefill_wall_s;
+    double decode_wall_s;
+    unsigned long long prefill_segments;
+    double prefill_rest_s;
+    double prefill_compute_tps;
+    double decode_rest_s;
+    double decode_compute_tps;
+    uint32_t decode_rests;
+    uint32_t decode_clamp_events;
+    double decode_baseline_ms;
+    double peak_ram_gib;
+    double gpu_alloc_gib;
+    uint32_t recall_hits;
+    uint32_t recall_total;
+    uint32_t assoc_hits;
+    uint64_t n_prompt_tok;
+    uint32_t n_gen;
+    double wall_s;
+    double gemm_tflops;
+    bool ingestion_ok;
+    char status[16];             /* "DONE" or "VOID", set by sg_bench_finalize_status */
+    char log_id[96];
+} sg_bench_row;
+
+/* | model | engine | prefill t/s | decode t/s | peak RAM | recall | wall | status |
+ * with prefill "%.0f" (or "-" below 0), decode slope "%.2f", "%.1f GiB",
+ * "hits/total", wall in whole minutes, status (surge.h:1916-1924). */
+void sg_bench_format_md_row(const sg_bench_row *row, char *buf, size_t cap); /* surge.h:1924 */
+/* A flat JSON object of every field under its field name: numbers "%.6g",
+ * ingestion_ok a JSON bool, strings JSON-escaped (quote, backslash, control
+ * bytes as \u00XX); truncated to cap like the md row (surge.h:1926-1937). */
+void sg_bench_format_json(const sg_bench_row *row, char *buf, size_t cap);   /* surge.h:1937 */
+#define SG_BENCH_GEMM_MIN_TFLOPS 20.5
+/* Admitted iff gemm_tflops > SG_BENCH_GEMM_MIN_TFLOPS and ingestion_ok;
+ * finalize sets status to "DONE" or "VOID" accordingly (surge.h:1939-1955). */
+bool sg_bench_admitted(const sg_bench_row *row);                           /* surge.h:1950 */
+void sg_bench_finalize_status(sg_bench_row *row);                          /* surge.h:1955 */
 
 /* ---------------------------------------------------------------------
  * Synthetic random-init models (no reference counterpart: the reference

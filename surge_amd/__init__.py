@@ -131,6 +131,12 @@ _SIGS = {
     "sg_gpu_decode_greedy": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32,
                                      C.c_uint32, C.POINTER(C.c_int32)]),
     "sg_gpu_state_fill_synthetic": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32]),
+    "sg_gpu_decode_greedy_timed": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32,
+                                           C.c_uint32, C.POINTER(C.c_int32), C.POINTER(C.c_double)]),
+    "sg_bench_format_md_row": (None, [C.c_void_p, C.c_char_p, C.c_size_t]),
+    "sg_bench_format_json": (None, [C.c_void_p, C.c_char_p, C.c_size_t]),
+    "sg_bench_admitted": (C.c_bool, [C.c_void_p]),
+    "sg_bench_finalize_status": (None, [C.c_void_p]),
     "sg_gpu_prefill": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.POINTER(C.c_int32), C.c_uint32,
                                C.c_uint32, C.POINTER(C.POINTER(C.c_float))]),
     "sg_gpu_sync": (SgErr, [C.c_void_p]),
@@ -333,6 +339,13 @@ class Gpu:
         check(lib().sg_gpu_decode_greedy(self.handle, self.model, token, pos, n, out))
         return np.array(out, dtype=np.int32)
 
+    def decode_greedy_timed(self, token: int, pos: int, n: int):
+        """(tokens, cumulative seconds at the end of each step)."""
+        out = (C.c_int32 * n)()
+        t = (C.c_double * n)()
+        check(lib().sg_gpu_decode_greedy_timed(self.handle, self.model, token, pos, n, out, t))
+        return np.array(out, dtype=np.int32), np.array(t, dtype=np.float64)
+
     def fill_synthetic(self, n_tokens: int, seed: int = 0) -> None:
         """Seeded K/V and DeltaNet state up to depth n_tokens (decode then starts at n_tokens)."""
         check(lib().sg_gpu_state_fill_synthetic(self.handle, n_tokens, seed))
@@ -383,6 +396,31 @@ class Gpu:
 
     def alloc_bytes(self) -> int:
         return lib().sg_gpu_current_alloc_bytes(self.handle)
+
+
+class BenchRow(C.Structure):
+    """sg_bench_row (reference surge.h:1845-1914), field for field."""
+    _fields_ = [
+        ("model", C.c_char * 64), ("engine", C.c_char * 64), ("prefill_tps", C.c_double),
+        ("decode_tps_slope", C.c_double), ("decode_tps_avg", C.c_double), ("prefill_wall_s", C.c_double),
+        ("decode_wall_s", C.c_double), ("prefill_segments", C.c_ulonglong), ("prefill_rest_s", C.c_double),
+        ("prefill_compute_tps", C.c_double), ("decode_rest_s", C.c_double), ("decode_compute_tps", C.c_double),
+        ("decode_rests", C.c_uint32), ("decode_clamp_events", C.c_uint32), ("decode_baseline_ms", C.c_double),
+        ("peak_ram_gib", C.c_double), ("gpu_alloc_gib", C.c_double), ("recall_hits", C.c_uint32),
+        ("recall_total", C.c_uint32), ("assoc_hits", C.c_uint32), ("n_prompt_tok", C.c_uint64),
+        ("n_gen", C.c_uint32), ("wall_s", C.c_double), ("gemm_tflops", C.c_double), ("ingestion_ok", C.c_bool),
+        ("status", C.c_char * 16), ("log_id", C.c_char * 96),
+    ]
+
+    def md(self) -> str:
+        buf = C.create_string_buffer(1024)
+        lib().sg_bench_format_md_row(C.byref(self), buf, len(buf))
+        return buf.value.decode()
+
+    def json(self) -> str:
+        buf = C.create_string_buffer(4096)
+        lib().sg_bench_format_json(C.byref(self), buf, len(buf))
+        return buf.value.decode()
 
 
 class Synth:

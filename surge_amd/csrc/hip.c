@@ -1448,6 +1448,45 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
     return SG_OK;
 }
 
+/* sg_gpu_decode_greedy with per-token timestamps (no reference counterpart):
+ * t_cum[i] = seconds from just before the first step to the end of step i,
+ * from HIP events recorded between the steps on the GPU's clock, the series
+ * surge-bench fits by slope (sg_bench_slope, reference cli_bench.c:627-693)
+ * without a host round trip per token. */
+sg_err sg_gpu_decode_greedy_timed(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos, uint32_t n_steps,
+                                  int32_t *out_tokens, double *t_cum) {
+    sg_err e = step_checks(g, m, token, pos);
+    if (sg_failed(e)) return e;
+    if (!t_cum || !n_steps || (uint64_t)pos + n_steps > g->max_ctx)
+        return (sg_err){"gpu: timed greedy decode needs t_cum and must stay within max_ctx"};
+    hipEvent_t *ev = calloc((size_t)n_steps + 1, sizeof *ev);
+    if (!ev) return (sg_err){"gpu: out of host memory"};
+    hipError_t he = hipSuccess;
+    for (uint32_t i = 0; i <= n_steps && he == hipSuccess; i++) he = hipEventCreate(&ev[i]);
+    if (he == hipSuccess && sg_failed(e = step_upload(g, token, pos))) he = hipErrorUnknown;
+    if (he == hipSuccess) he = hipEventRecord(ev[0], g->stream);
+    for (uint32_t i = 0; i < n_steps && he == hipSuccess; i++) {
+        he = g->use_graph ? hipGraphLaunch(g->g_greedy, g->stream) : enqueue_step(g, true);
+        if (he == hipSuccess) he = hipEventRecord(ev[i + 1], g->stream);
+    }
+    if (he == hipSuccess)
+        he = hipMemcpyAsync(g->h_tok, g->hist + pos + 1, (uint64_t)n_steps * 4, hipMemcpyDeviceToHost, g->stream);
+    if (he == hipSuccess) he = hipStreamSynchronize(g->stream);
+    for (uint32_t i = 0; i < n_steps && he == hipSuccess; i++) {
+        float ms = 0.0f;
+        he = hipEventElapsedTime(&ms, ev[0], ev[i + 1]);
+        t_cum[i] = (double)ms * 1e-3;
+    }
+    for (uint32_t i = 0; i <= n_steps; i++) if (ev[i]) hipEventDestroy(ev[i]);
+    free(ev);
+    if (sg_failed(e)) return e;
+    if (he != hipSuccess) return errf("gpu: timed greedy decode: %s", hipGetErrorString(he));
+    count_step(g, n_steps);
+    if (out_tokens) memcpy(out_tokens, g->h_tok, (uint64_t)n_steps * 4);
+    g->used = pos + n_steps;
+    return SG_OK;
+}
+
 sg_err sg_gpu_state_fill_synthetic(sg_gpu *g, uint32_t n_tokens, uint32_t seed) {
     if (!g || !g->have_state) return (sg_err){"gpu: sg_gpu_state_fill_synthetic needs a live state"};
     if (n_tokens >= g->max_ctx) return (sg_err){"gpu: sg_gpu_state_fill_synthetic: n_tokens must be < max_ctx"};

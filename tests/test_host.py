@@ -320,3 +320,51 @@ def test_kv_module_object_with_host_backend():
     L.sg_kv_set_backend(_KV_ALLOC(), _KV_FREE(), _KV_HOST())
     assert b"backend" in L.sg_kv_new(None, C.byref(c), 8, S.SG_T_F16, C.byref(kv)).msg
     assert not be.live
+
+
+# ---------------------------------------------------------------- the surge-bench row
+
+def _row(**kw):
+    r = S.BenchRow()
+    r.model, r.engine = b"qwen27b-q8", b"surge_amd mi355x"
+    r.prefill_tps, r.decode_tps_slope, r.decode_tps_avg = 5348.2, 170.794, 170.51
+    r.peak_ram_gib, r.recall_hits, r.recall_total, r.wall_s = 27.54, 7, 8, 125.0
+    r.status, r.log_id = b"DONE", b"ctx4k_27b_20261202"
+    r.n_prompt_tok, r.n_gen, r.gemm_tflops, r.ingestion_ok = 4096, 128, 301.0, True
+    for k, v in kw.items():
+        setattr(r, k, v)
+    return r
+
+
+def test_bench_row_md_json_and_admission():
+    """The leaderboard row's contract (reference surge.h:1916-1955): the
+    8-column pipe row with prefill "%.0f" or "-", decode "%.2f", "%.1f GiB",
+    hits/total and wall in whole minutes (lround); the JSON object has every
+    field under its struct name (in the reference's key order), numbers at
+    %.6g, a JSON bool,
+    escaped strings, and stays in its buffer; admission is strict on the GEMM
+    floor and needs ingestion_ok."""
+    r = _row()
+    assert r.md() == "| qwen27b-q8 | surge_amd mi355x | 5348 | 170.79 | 27.5 GiB | 7/8 | 2 min | DONE |"
+    assert _row(prefill_tps=-1.0, wall_s=150.0).md().split(" | ")[2] == "-"
+    assert _row(wall_s=150.0).md().endswith("| 3 min | DONE |")       # lround(2.5) = 3
+    import json
+    d = json.loads(r.json())
+    assert sorted(d) == sorted(f for f, _ in S.BenchRow._fields_)
+    assert list(d)[:10] == ["model", "engine", "prefill_tps", "decode_tps_slope", "decode_tps_avg", "prefill_wall_s",
+                            "decode_wall_s", "prefill_rest_s", "prefill_compute_tps", "prefill_segments"]
+    assert d["decode_tps_slope"] == float("%.6g" % 170.794) and d["n_prompt_tok"] == 4096
+    assert d["ingestion_ok"] is True and d["status"] == "DONE" and d["log_id"] == "ctx4k_27b_20261202"
+    odd = _row(model=b'a"b\\c\x01d\x1f')
+    assert json.loads(odd.json())["model"] == 'a"b\\c\x01d\x1f'
+    assert '"model":"a\\"b\\\\c\\u0001d\\u001f"' in odd.json()
+    small = C.create_string_buffer(b"\xff" * 32)
+    S.lib().sg_bench_format_json(C.byref(r), small, 10)
+    assert small.raw[:10] == b"{\"model\":\x00" and small.raw[10:32] == b"\xff" * 22
+    L = S.lib()
+    assert not L.sg_bench_admitted(None)
+    for tf, ok, want in [(20.5, True, "VOID"), (20.51, True, "DONE"), (300.0, False, "VOID")]:
+        x = _row(gemm_tflops=tf, ingestion_ok=ok, status=b"")
+        assert bool(L.sg_bench_admitted(C.byref(x))) == (want == "DONE")
+        L.sg_bench_finalize_status(C.byref(x))
+        assert x.status.decode() == want
