@@ -333,6 +333,13 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
  * events between the steps, the series sg_bench_slope fits. */
 sg_err sg_gpu_decode_greedy_timed(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
                                   uint32_t n_steps, int32_t *out_tokens, double *t_cum);
+/* Whether the live state decodes through the chain (no reference
+ * counterpart): SURGE_CHAIN=1 at sg_gpu_state_new, on a model the chain
+ * takes (Q8_0 weights, GEMV widths multiples of 1024). The chain runs each
+ * run of decode stages between attention layers as one persistent launch;
+ * outputs are the per-kernel path's within float reassociation. A chain
+ * barrier that does not resolve makes the call that waited for it fail. */
+bool sg_gpu_chain_active(const sg_gpu *g);
 /* Decode at depth without a prefill (no reference counterpart; for
  * benchmarks of the KV read path at long context): fills every attention
  * layer's K/V cache rows [0, n_tokens) with seeded f16 values in [-2, 2], the

@@ -131,6 +131,7 @@ _SIGS = {
     "sg_gpu_decode_greedy": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32,
                                      C.c_uint32, C.POINTER(C.c_int32)]),
     "sg_gpu_state_fill_synthetic": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32]),
+    "sg_gpu_chain_active": (C.c_bool, [C.c_void_p]),
     "sg_gpu_decode_greedy_timed": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32,
                                            C.c_uint32, C.POINTER(C.c_int32), C.POINTER(C.c_double)]),
     "sg_bench_format_md_row": (None, [C.c_void_p, C.c_char_p, C.c_size_t]),
@@ -318,6 +319,9 @@ class Gpu:
 
     def state_reset(self):
         lib().sg_gpu_state_reset(self.handle)
+
+    def chain_active(self) -> bool:
+        return bool(lib().sg_gpu_chain_active(self.handle))
 
     def split_cap(self) -> int:
         return int(lib().sg_gpu_splitk_gqa_cap(self.handle))

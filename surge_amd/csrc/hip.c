@@ -133,6 +133,19 @@ struct sg_gpu {
     /* one-shot scratch */
     void *tmp;
     uint64_t tmp_bytes;
+
+    /* decode chain (SURGE_CHAIN=1): the token's stage table, the runs of it
+     * one persistent launch covers (an attention layer's partial and combine
+     * run as kernels of their own between runs), the buffers its stages write
+     * once per token, the barrier counters and the token epoch */
+    bool chain;
+    sgk_cstage *ch_st;
+    uint32_t ch_n, ch_nseg;
+    struct { uint32_t s0, s1; int32_t attn; float *q; } *ch_seg;
+    float *ch_buf;
+    uint32_t *ch_cnt, *ch_err;
+    uint32_t ch_epoch;
+    uint32_t ch_spin;       /* SURGE_CHAIN_SPIN: polls per barrier wait (tests of the give-up path) */
 };
 
 /* The decode attention partial a state dispatches (fixed per state: the
@@ -1071,6 +1084,12 @@ sg_err sg_gpu_load_model(sg_gpu *g, const sg_model *m) {
 
 static void state_free(sg_gpu *g) {
     if (!g->have_state) return;
+    dfree(g, g->ch_st); dfree(g, g->ch_buf); dfree(g, g->ch_cnt); dfree(g, g->ch_err);
+    g->ch_st = NULL; g->ch_buf = NULL; g->ch_cnt = g->ch_err = NULL;
+    free(g->ch_seg);
+    g->ch_seg = NULL;
+    g->ch_n = g->ch_nseg = 0;
+    g->chain = false;
     if (g->g_fwd) hipGraphExecDestroy(g->g_fwd);
     if (g->g_greedy) hipGraphExecDestroy(g->g_greedy);
     g->g_fwd = g->g_greedy = NULL;
@@ -1108,8 +1127,47 @@ static void state_free(sg_gpu *g) {
     g->have_state = false;
 }
 
+/* The attention layer's split-K partial and combine of a decode step, q the
+ * layer's fused q|gate|k|v projection rows. */
+static hipError_t enqueue_attn(sg_gpu *g, const glayer *L, float *q) {
+    const sg_cfg *c = &g->cfg;
+    const uint32_t hd = c->head_dim, qs = c->attn_output_gate ? 2 * hd : hd;
+    sgk_attn A = {0};
+    A.q = q; A.kc = L->kc; A.vc = L->vc; A.m = g->am; A.s = g->as; A.acc = g->aacc; A.out = g->ctx;
+    A.gate = c->attn_output_gate ? q + hd : NULL; A.steps = g->d_step;
+    A.n_heads = c->n_heads; A.n_kv = c->n_kv_heads; A.hd = hd; A.rope_dim = c->rope_dim; A.q_stride = qs;
+    A.max_splits = g->max_splits; A.ntok = 1; A.scale = (float)(1.0 / sqrt((double)hd));
+    A.kv_ps = hd; A.kv_hs = (uint64_t)g->max_ctx * hd;
+    A.fuse_prep = 1; A.qn = L->qn; A.kn = L->kn; A.cs = g->cs_table; A.eps = c->rms_eps;
+    A.split_cap = g->attn_arm == ARM_SINGLE ? 1 : g->split_cap;
+    A.per_head = g->attn_arm == ARM_PER_HEAD;
+    hipError_t e = sgk_attn_partial(&A, g->stream);
+    return e != hipSuccess ? e : sgk_attn_combine(&A, g->stream);
+}
+
+/* One decode step through the chain: a persistent launch per run of stages,
+ * an attention layer's partial and combine between runs. */
+static hipError_t enqueue_chain(sg_gpu *g, bool greedy) {
+    const sg_cfg *c = &g->cfg;
+    hipError_t e;
+    g->ch_epoch++;
+    for (uint32_t k = 0; k < g->ch_nseg; k++) {
+        sgk_chain a = {g->ch_st, g->ch_seg[k].s0, g->ch_seg[k].s1, g->ch_cnt, g->ch_epoch, g->ch_err, g->ch_spin};
+        if ((e = sgk_chain_launch(&a, c->head_k_dim, c->head_v_dim, g->stream)) != hipSuccess) return e;
+        const int32_t al = g->ch_seg[k].attn;
+        if (al >= 0 && (e = enqueue_attn(g, &g->ls[al], g->ch_seg[k].q)) != hipSuccess) return e;
+    }
+    if (greedy) {
+        if ((e = sgk_argmax(g->logits, c->vocab, (uint32_t *)&g->d_step->token, g->amax_scratch, g->stream)) != hipSuccess)
+            return e;
+        if ((e = sgk_step_advance(g->d_step, g->hist, g->stream)) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 /* Enqueues one decode step (everything after the step descriptor is set). */
 static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
+    if (g->chain) return enqueue_chain(g, greedy);
     const sg_cfg *c = &g->cfg;
     hipStream_t s = g->stream;
     hipError_t e;
@@ -1178,6 +1236,123 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
     }
     return hipSuccess;
 }
+
+/* Decode through the chain needs Q8_0 weights whose GEMV widths are
+ * multiples of 1024 within the chain's limits, a residual slice per
+ * workgroup that fits its LDS, and a one-workgroup-per-head DeltaNet step of
+ * a shape the chain kernel is built for. */
+static bool chain_eligible(const sg_gpu *g) {
+    const sg_cfg *c = &g->cfg;
+    if (!g->q8 || !g->emb.qs || !g->lm.qs || g->gdn_blocks != 1) return false;
+    const uint32_t nb = sgk_chain_blocks(), H = c->hidden, rw = (c->head_v_dim + 7) / 8;
+    bool gdn = false;
+    for (uint32_t i = 0; i < c->n_layers; i++) gdn |= !g->ls[i].attn;
+    if (gdn && !((c->head_k_dim == 128 && (rw == 16 || rw == 8)) || (c->head_k_dim == 64 && (rw == 8 || rw == 4))))
+        return false;
+    if (gdn && c->n_v_heads > nb) return false;
+    const uint32_t add_rows = ((H + 1) / 2 + nb - 1) / nb * 2;
+    if (add_rows > SGK_CHAIN_MAX_RES_ROWS) return false;
+    const uint32_t rms_cols = H, none_cols[3] = {c->ffn_hidden, g->value_dim, g->attn_width};
+    if (rms_cols % 1024 || rms_cols > SGK_CHAIN_MAX_RMS_COLS) return false;
+    for (int k = 0; k < 3; k++)
+        if (none_cols[k] % 1024 || none_cols[k] > SGK_CHAIN_MAX_COLS) return false;
+    for (uint32_t i = 0; i < c->n_layers; i++) {
+        const glayer *L = &g->ls[i];
+        if (!L->in.qs || !L->out.qs || !L->gu.qs || !L->down.qs) return false;
+    }
+    return true;
+}
+
+/* The token's stage table: embedding, then per layer the input projection,
+ * (a DeltaNet step), the output projection, gate/up and down, then lm_head.
+ * A run ends after an attention layer's input projection, whose partial and
+ * combine run as kernels before the next run starts with its output
+ * projection. Every stage writes its own buffer (written once per token). */
+static sg_err chain_build(sg_gpu *g) {
+    const sg_cfg *c = &g->cfg;
+    const uint32_t NL = c->n_layers, H = c->hidden;
+#define R64(n) ((((uint64_t)(n)) + 63) & ~(uint64_t)63)
+    uint64_t tot = R64(H);
+    for (uint32_t i = 0; i < NL; i++)
+        tot += R64(g->ls[i].in.rows) + 2 * R64(H) + R64(c->ffn_hidden) + (g->ls[i].attn ? 0 : R64(g->value_dim));
+    sg_err e = dzalloc(g, tot * 4, (void **)&g->ch_buf);
+    if (sg_failed(e)) return e;
+    const uint32_t nmax = 2 + 5 * NL;
+    sgk_cstage *T = calloc(nmax, sizeof *T);
+    g->ch_seg = calloc(NL + 1, sizeof *g->ch_seg);
+    if (!T || !g->ch_seg) { free(T); return (sg_err){"gpu: out of host memory"}; }
+    float *p = g->ch_buf;
+    uint32_t n = 0, nseg = 0, seg0 = 0;
+    float *x = p; p += R64(H);
+    T[n].kind = SGK_CS_EMBED; T[n].cols = H; T[n].qs = g->emb.qs; T[n].d = g->emb.d; T[n].y = x;
+    T[n].step = g->d_step; n++;
+#define GEMV(M, PRO, EPI, X, NW, RES, Y) do { sgk_cstage *t_ = &T[n++]; t_->kind = SGK_CS_GEMV;    \
+        t_->pro = (PRO); t_->epi = (EPI); t_->rows = (M)->rows; t_->cols = (M)->cols; t_->qs = (M)->qs; \
+        t_->d = (M)->d; t_->x = (X); t_->nw = (NW); t_->res = (RES); t_->y = (Y); t_->eps = c->rms_eps; } while (0)
+    for (uint32_t i = 0; i < NL; i++) {
+        glayer *L = &g->ls[i];
+        float *act = p; p += R64(L->in.rows);
+        GEMV(&L->in, SGK_PRO_RMS, SGK_EPI_STORE, x, L->ln1, NULL, act);
+        const float *mix;
+        if (L->attn) {
+            g->ch_seg[nseg].s0 = seg0; g->ch_seg[nseg].s1 = n; g->ch_seg[nseg].attn = (int32_t)i;
+            g->ch_seg[nseg].q = act; nseg++;
+            seg0 = n;
+            mix = g->ctx;
+        } else {
+            float *go = p; p += R64(g->value_dim);
+            sgk_cstage *t = &T[n++];
+            t->kind = SGK_CS_GDN;
+            sgk_gdn *d = &t->gdn;
+            d->in = act; d->conv_w = L->conv_w; d->ring = L->ring; d->ssm_a = L->ssm_a; d->dt_bias = L->dt_bias;
+            d->S = L->S; d->y = g->ybuf; d->step = g->d_step; d->n_k = c->n_k_heads; d->n_v = c->n_v_heads;
+            d->dk = c->head_k_dim; d->dv = c->head_v_dim; d->conv_dim = g->conv_dim; d->ksize = c->conv_kernel;
+            d->tiled = g->model->v_heads_tiled; d->neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
+            d->z = act + g->conv_dim; d->norm_w = L->ssm_norm; d->out = go; d->eps = c->rms_eps;
+            d->ss = g->gss; d->blocks = 1;
+            mix = go;
+        }
+        float *xa = p; p += R64(H);
+        GEMV(&L->out, SGK_PRO_NONE, SGK_EPI_ADD, mix, NULL, x, xa);
+        float *ff = p; p += R64(c->ffn_hidden);
+        GEMV(&L->gu, SGK_PRO_RMS, SGK_EPI_SWIGLU, xa, L->ln2, NULL, ff);
+        float *xb = p; p += R64(H);
+        GEMV(&L->down, SGK_PRO_NONE, SGK_EPI_ADD, ff, NULL, xa, xb);
+        x = xb;
+    }
+    GEMV(&g->lm, SGK_PRO_RMS, SGK_EPI_STORE, x, g->out_norm, NULL, g->logits);
+#undef GEMV
+#undef R64
+    g->ch_seg[nseg].s0 = seg0; g->ch_seg[nseg].s1 = n; g->ch_seg[nseg].attn = -1; g->ch_seg[nseg].q = NULL; nseg++;
+    g->ch_n = n;
+    g->ch_nseg = nseg;
+    if (!sg_failed(e = dalloc(g, (uint64_t)n * sizeof *T, (void **)&g->ch_st)) &&
+        hipMemcpy(g->ch_st, T, (uint64_t)n * sizeof *T, hipMemcpyHostToDevice) != hipSuccess)
+        e = (sg_err){"gpu: chain stage table upload failed"};
+    free(T);
+    if (!sg_failed(e)) e = dzalloc(g, (uint64_t)n * 8 * 64 * 4, (void **)&g->ch_cnt);
+    if (!sg_failed(e)) e = dzalloc(g, 256, (void **)&g->ch_err);
+    g->ch_epoch = 0;
+    return e;
+}
+
+/* Whether a chain barrier gave up since the last check (the decode outputs
+ * of those steps are invalid); clears the flag and the counters. */
+static sg_err chain_status(sg_gpu *g) {
+    if (!g->chain) return SG_OK;
+    uint32_t v = 0;
+    HIPCHK(hipMemcpy(&v, g->ch_err, 4, hipMemcpyDeviceToHost), "chain status");
+    if (!v) return SG_OK;
+    HIPCHK(hipMemsetAsync(g->ch_cnt, 0, (uint64_t)g->ch_n * 8 * 64 * 4, g->stream), "chain reset");
+    HIPCHK(hipMemsetAsync(g->ch_err, 0, 4, g->stream), "chain reset");
+    HIPCHK(hipStreamSynchronize(g->stream), "chain reset");
+    g->ch_epoch = 0;
+    return (sg_err){"gpu: a decode chain barrier did not resolve; those decode steps' outputs are invalid"};
+}
+
+static bool graphed(const sg_gpu *g) { return g->use_graph && !g->chain; }
+
+bool sg_gpu_chain_active(const sg_gpu *g) { return g && g->have_state && g->chain; }
 
 static sg_err capture(sg_gpu *g, bool greedy, hipGraphExec_t *out) {
     hipGraph_t graph = NULL;
@@ -1313,7 +1488,20 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     if (!sg_failed(e) && hipEventCreateWithFlags(&g->step_ev, hipEventDisableTiming) != hipSuccess)
         e = (sg_err){"gpu: hipEventCreate failed"};
     g->have_state = true;
-    if (!sg_failed(e) && g->use_graph) {
+    /* SURGE_CHAIN=1: decode through the chain (one persistent launch per run
+     * of stages) when the model allows it; 0 (default): one kernel per stage. */
+    {
+        const char *ce = getenv("SURGE_CHAIN");
+        if (ce && ce[0] && strcmp(ce, "0") != 0 && strcmp(ce, "1") != 0)
+            fprintf(stderr, "gpu: SURGE_CHAIN='%s' not recognized (want 0 or 1); using 0\n", ce);
+        if (!sg_failed(e) && ce && strcmp(ce, "1") == 0 && chain_eligible(g)) {
+            e = chain_build(g);
+            g->chain = !sg_failed(e);
+        }
+        const char *sp = getenv("SURGE_CHAIN_SPIN");
+        g->ch_spin = sp && *sp ? (uint32_t)strtoul(sp, NULL, 10) : 0;
+    }
+    if (!sg_failed(e) && graphed(g)) {
         e = capture(g, false, &g->g_fwd);
         if (!sg_failed(e)) e = capture(g, true, &g->g_greedy);
     }
@@ -1330,6 +1518,11 @@ void sg_gpu_state_reset(sg_gpu *g) {
         glayer *L = &g->ls[i];
         if (L->ring) sgk_fill_f32(L->ring, 0.0f, (uint64_t)4 * g->conv_dim, g->stream);
         if (L->S) sgk_fill_f32(L->S, 0.0f, (uint64_t)c->n_v_heads * c->head_v_dim * c->head_k_dim, g->stream);
+    }
+    if (g->chain) {
+        hipMemsetAsync(g->ch_cnt, 0, (uint64_t)g->ch_n * 8 * 64 * 4, g->stream);
+        hipMemsetAsync(g->ch_err, 0, 4, g->stream);
+        g->ch_epoch = 0;
     }
     hipStreamSynchronize(g->stream);
     g->used = 0;
@@ -1379,7 +1572,7 @@ static sg_err launch_step(sg_gpu *g, int32_t token, uint32_t pos, bool greedy) {
     sg_err se = step_upload(g, token, pos);
     if (sg_failed(se)) return se;
     count_step(g, 1);
-    if (g->use_graph) {
+    if (graphed(g)) {
         HIPCHK(hipGraphLaunch(greedy ? g->g_greedy : g->g_fwd, g->stream), "graph launch");
     } else {
         hipError_t e = enqueue_step(g, greedy);
@@ -1394,6 +1587,7 @@ sg_err sg_gpu_forward(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
     if (sg_failed(e = launch_step(g, token, pos, false))) return e;
     HIPCHK(hipMemcpyAsync(g->h_logits, g->logits, (uint64_t)g->cfg.vocab * 4, hipMemcpyDeviceToHost, g->stream), "logits download");
     HIPCHK(hipStreamSynchronize(g->stream), "decode step");
+    if (sg_failed(e = chain_status(g))) return e;
     g->used = pos + 1;
     if (logits) *logits = g->h_logits;
     return SG_OK;
@@ -1410,7 +1604,7 @@ sg_err sg_gpu_forward_nosync(sg_gpu *g, const sg_model *m, int32_t token, uint32
 sg_err sg_gpu_sync(sg_gpu *g) {
     if (!g) return (sg_err){"gpu: NULL gpu"};
     HIPCHK(hipStreamSynchronize(g->stream), "stream synchronize");
-    return SG_OK;
+    return g->have_state ? chain_status(g) : SG_OK;
 }
 
 sg_err sg_gpu_argmax(sg_gpu *g, uint32_t *token_out) {
@@ -1434,7 +1628,7 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
     if (sg_failed(e = step_upload(g, token, pos))) return e;
     count_step(g, n_steps);
     for (uint32_t i = 0; i < n_steps; i++) {
-        if (g->use_graph) {
+        if (graphed(g)) {
             HIPCHK(hipGraphLaunch(g->g_greedy, g->stream), "graph launch");
         } else {
             hipError_t he = enqueue_step(g, true);
@@ -1443,6 +1637,7 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
     }
     HIPCHK(hipMemcpyAsync(g->h_tok, g->hist + pos + 1, (uint64_t)n_steps * 4, hipMemcpyDeviceToHost, g->stream), "tokens download");
     HIPCHK(hipStreamSynchronize(g->stream), "greedy decode");
+    if (sg_failed(e = chain_status(g))) return e;
     if (out_tokens) memcpy(out_tokens, g->h_tok, (uint64_t)n_steps * 4);
     g->used = pos + n_steps;
     return SG_OK;
@@ -1466,7 +1661,7 @@ sg_err sg_gpu_decode_greedy_timed(sg_gpu *g, const sg_model *m, int32_t token, u
     if (he == hipSuccess && sg_failed(e = step_upload(g, token, pos))) he = hipErrorUnknown;
     if (he == hipSuccess) he = hipEventRecord(ev[0], g->stream);
     for (uint32_t i = 0; i < n_steps && he == hipSuccess; i++) {
-        he = g->use_graph ? hipGraphLaunch(g->g_greedy, g->stream) : enqueue_step(g, true);
+        he = graphed(g) ? hipGraphLaunch(g->g_greedy, g->stream) : enqueue_step(g, true);
         if (he == hipSuccess) he = hipEventRecord(ev[i + 1], g->stream);
     }
     if (he == hipSuccess)
@@ -1481,6 +1676,7 @@ sg_err sg_gpu_decode_greedy_timed(sg_gpu *g, const sg_model *m, int32_t token, u
     free(ev);
     if (sg_failed(e)) return e;
     if (he != hipSuccess) return errf("gpu: timed greedy decode: %s", hipGetErrorString(he));
+    if (sg_failed(e = chain_status(g))) return e;
     count_step(g, n_steps);
     if (out_tokens) memcpy(out_tokens, g->h_tok, (uint64_t)n_steps * 4);
     g->used = pos + n_steps;

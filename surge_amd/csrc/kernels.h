@@ -261,6 +261,45 @@ hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, floa
                        uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, float *part,
                        uint64_t part_cap, hipStream_t s);
 
+/* Decode chain: one persistent launch (one workgroup per CU, all resident)
+ * runs stages [s0, s1) of a token's stage table in order, with a device-wide
+ * barrier between stages instead of a kernel boundary; every GEMV's first
+ * weight rows are requested before the barrier that precedes it. Stage
+ * outputs are published with device-scope (write-through) stores into
+ * buffers written once per token; `epoch` is the token's number (1, 2, ...),
+ * against which the arrival counters `cnt` (zeroed with the state, never
+ * reset between tokens) are compared. A barrier that does not resolve within
+ * a bounded number of polls sets *err and the launch runs to its end. */
+enum { SGK_CS_GEMV = 1, SGK_CS_GDN = 2, SGK_CS_EMBED = 3 };
+#define SGK_CHAIN_LDS (96u * 1024u)          /* dynamic LDS: one workgroup per CU */
+#define SGK_CHAIN_MAX_COLS 18432u            /* GEMV columns (a multiple of 1024) */
+#define SGK_CHAIN_MAX_RMS_COLS 8192u         /* ... behind the RMSNorm prologue */
+#define SGK_CHAIN_MAX_RES_ROWS 1024u         /* rows of one workgroup in an EPI_ADD stage */
+typedef struct {
+    uint32_t kind;              /* SGK_CS_* */
+    uint32_t pro, epi;          /* GEMV: SGK_PRO_NONE | RMS, SGK_EPI_STORE | ADD | SWIGLU */
+    uint32_t rows, cols;        /* GEMV; EMBED: cols = hidden */
+    const int8_t *qs;           /* GEMV / EMBED (the table) */
+    const uint16_t *d;
+    const float *x, *nw, *res;  /* input, RMS weight, EPI_ADD residual (y = res + W x) */
+    float *y;
+    float eps;
+    const sgk_step *step;       /* EMBED: the token */
+    sgk_gdn gdn;                /* GDN: one workgroup per value head (blocks == 1) */
+} sgk_cstage;
+typedef struct {
+    const sgk_cstage *st;       /* device stage table */
+    uint32_t s0, s1;
+    uint32_t *cnt;              /* [n_stages][8 XCDs][64] arrival counters */
+    uint32_t epoch;
+    uint32_t *err;
+    uint32_t spin;              /* polls a wait makes before giving up (0: the default bound) */
+} sgk_chain;
+/* DeltaNet shapes the chain's step takes: (dk, ceil(dv / 8)) in
+ * {(128, 16), (128, 8), (64, 8), (64, 4)}. */
+hipError_t sgk_chain_launch(const sgk_chain *a, uint32_t dk, uint32_t dv, hipStream_t s);
+uint32_t sgk_chain_blocks(void);
+
 /* The device-resident workspace of the no-allocation entry points: a
  * file-scope device array of SGK_SCRATCH_BYTES in kernels.hip. Call
  * sgk_scratch_init(dev) once per device with that device current; then

@@ -2311,8 +2311,17 @@ __device__ __forceinline__ uint32_t rows_lane(uint32_t r) {   // a lane holding 
 // head, so it is left to the output projection's gated prologue: each block
 // writes its readouts y, silu(z) of its rows and its rows' sum of squares,
 // with no synchronisation between blocks.
-template <int DK, int RW, int NB, int GDN_TPB>
-__global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
+// Stores that other workgroups of the same launch read after a chain barrier
+// go straight to memory (device-scope relaxed atomic stores: sc1, written
+// through the XCD's L2), so no cache-wide flush is needed to publish them.
+template <bool CO>
+__device__ __forceinline__ void st_out(float *p, float v) {
+    if (CO) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+
+template <int DK, int RW, int NB, int GDN_TPB, bool CO = false>
+__device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint32_t jb) {
     constexpr int GDN_NB = NB;
     constexpr int EPL = DK >= 64 ? DK / 64 : 1;
     constexpr int NW = GDN_TPB / 64;
@@ -2320,7 +2329,7 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
     __shared__ float vv[NW * RW];
     __shared__ float red[NW];
     __shared__ float ysh[NB == 1 ? SGK_GDN_MAX_DV : 1];
-    const uint32_t h = blockIdx.x, jb = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t dk = DK, dv = a.dv, key_dim = a.n_k * dk, cd = a.conv_dim;
     const uint32_t rpb = (dv + GDN_NB - 1) / GDN_NB, jlo = jb * rpb, jhi = min(dv, jlo + rpb);
     const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k);
@@ -2472,7 +2481,7 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
         const float r = 1.0f / sqrtf(tot / (float)dv + a.eps);
         if (t < dv) {
             const float yv = ysh[t];
-            a.out[(size_t)h * dv + t] = silu(zj) * ((yv * r) * nwt);
+            st_out<CO>(a.out + (size_t)h * dv + t, silu(zj) * ((yv * r) * nwt));
         }
         return;
     }
@@ -2485,6 +2494,11 @@ __global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
         a.ss[(size_t)h * GDN_NB + jb] = sb;
     }
     if (t >= jlo && t < jhi) a.out[(size_t)h * dv + t] = silu(zj);
+}
+
+template <int DK, int RW, int NB, int GDN_TPB>
+__global__ void __launch_bounds__(GDN_TPB) k_gdn_step(sgk_gdn a) {
+    gdn_step_body<DK, RW, NB, GDN_TPB>(a, blockIdx.x, blockIdx.y);
 }
 
 extern "C" hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s) {
@@ -3643,4 +3657,258 @@ extern "C" hipError_t sgk_scratch_init(int dev) {
 
 extern "C" void *sgk_scratch_ptr(int dev) {
     return (dev >= 0 && dev < SGK_SCRATCH_DEVICES) ? scratch_at[dev] : NULL;
+}
+
+// ---------------------------------------------------------------------------
+// Decode chain: one persistent launch runs a run of decode stages (embedding,
+// Q8_0 GEMVs, DeltaNet steps) back to back, with a barrier between stages
+// instead of a kernel boundary, and every workgroup requesting its first
+// weight rows of the next GEMV before it waits at the barrier, so HBM keeps
+// streaming while the last workgroups finish and the barrier resolves.
+//
+// Grid: one CT-thread workgroup per CU (its dynamic LDS keeps a second one
+// off the CU), all resident at once. In a GEMV stage workgroup b owns the
+// contiguous row groups [b*G/NB, (b+1)*G/NB) (G groups of CR rows); wave w
+// takes every CW-th of them from w on, every wave the same count (a wave
+// whose last group falls past the workgroup's range re-reads that range's
+// last group and stores nothing). A wave streams a row group exactly as
+// k_gemv_q8<2> does (lane l: chunks l, l+64, ... of both rows, f32 FMA per
+// chunk, one wave_sum per row), so the row sums are the same bits. Loads run
+// CP steps (one 16-byte chunk of each of the CR rows) ahead of the FMAs in a
+// register ring indexed statically.
+//
+// Coherence without cache-wide fences: a stage writes its outputs with
+// device-scope stores (st_out<true>: sc1, through the XCD's L2 to memory)
+// into buffers written once per token and never read before that write in
+// the launch, so no XCD holds a stale line of them; then waits for its
+// stores (vmcnt), and one thread per workgroup adds 1 to its XCD's arrival
+// counter of the stage. A waiter polls the 8 counters of the stage with
+// device-scope loads until each holds epoch x its workgroup count (counters
+// only grow: the host passes the token's epoch, 1, 2, ...). A wait gives up
+// after CH_SPIN_MAX polls or as soon as another workgroup has given up, and
+// sets *err, so a launch always ends.
+// ---------------------------------------------------------------------------
+#define CT 512
+#define CW (CT / 64)
+#define CR 2
+#define CP 8
+#define CH_XCDS 8u
+#define CH_CNT_STRIDE 64u            // uint32 per counter: one 256-byte line each
+#define CH_SPIN_MAX (1u << 21)
+#define CH_RES_FLOATS 1024u
+#define CH_X_FLOATS ((SGK_CHAIN_LDS - CH_RES_FLOATS * 4) / 4)
+constexpr int CXK_NONE = (SGK_CHAIN_MAX_COLS + 4 * CT - 1) / (4 * CT);   // x float4s per thread in flight
+constexpr int CXK_RMS = (SGK_CHAIN_MAX_RMS_COLS + 4 * CT - 1) / (4 * CT);
+static_assert(((SGK_CHAIN_MAX_COLS / 16 + 63) / 64) * XS_CH_BLK * 4 <= CH_X_FLOATS, "chain: staged x does not fit");
+
+__device__ __forceinline__ uint32_t ch_ld(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival at stage st: this workgroup's stores are complete, then one add.
+__device__ __forceinline__ void ch_arrive(const sgk_chain &a, uint32_t st) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(a.cnt + ((size_t)st * CH_XCDS + blockIdx.x % CH_XCDS) * CH_CNT_STRIDE, 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until every workgroup has arrived at stage st of this token.
+__device__ __forceinline__ void ch_wait(const sgk_chain &a, uint32_t st) {
+    if (threadIdx.x == 0) {
+        const uint32_t nb = gridDim.x;
+        const uint32_t *c = a.cnt + (size_t)st * CH_XCDS * CH_CNT_STRIDE;
+        for (uint32_t it = 0;; it++) {
+            bool ok = true;
+#pragma unroll
+            for (uint32_t x = 0; x < CH_XCDS; x++) {
+                const uint32_t want = a.epoch * ((nb + CH_XCDS - 1 - x) / CH_XCDS);
+                ok &= (int32_t)(ch_ld(c + x * CH_CNT_STRIDE) - want) >= 0;
+            }
+            if (ok) break;
+            if (ch_ld(a.err) != 0u) break;
+            if (it >= (a.spin ? a.spin : CH_SPIN_MAX)) { __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); break; }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+}
+
+// A wave's share of one GEMV stage.
+struct ch_gemv {
+    const int8_t *qs;
+    const uint16_t *d;
+    uint32_t rows, cols, nsteps;     // steps per row group: cols / 1024
+    uint32_t gw, gend, gb0;          // this wave's first group, the workgroup's group range end, its start
+    uint32_t nk;                     // row groups per wave (0: the workgroup has none)
+};
+
+__device__ __forceinline__ ch_gemv ch_enter(const sgk_cstage &S, uint32_t w) {
+    ch_gemv c;
+    c.qs = S.qs; c.d = S.d; c.rows = S.rows; c.cols = S.cols; c.nsteps = S.cols >> 10;
+    const uint32_t G = (S.rows + CR - 1) / CR, nb = gridDim.x, b = blockIdx.x;
+    c.gb0 = (uint32_t)((uint64_t)b * G / nb);
+    c.gend = (uint32_t)((uint64_t)(b + 1) * G / nb);
+    const uint32_t n = c.gend - c.gb0;
+    c.nk = (n + CW - 1) / CW;
+    c.gw = c.gb0 + w;
+    return c;
+}
+
+// Request step i = (group ordinal k, chunk step j) of a wave's share.
+__device__ __forceinline__ void ch_issue(gemv_chunk<CR> &ch, const ch_gemv &c, uint32_t k, uint32_t j, uint32_t lane) {
+    uint32_t g = c.gw + CW * k;
+    g = g < c.gend ? g : c.gend - 1;
+    gemv_load<CR>(ch, c.qs, c.d, g * CR, c.rows, c.cols, lane + 64 * j);
+}
+
+__device__ __forceinline__ void ch_step_next(uint32_t &k, uint32_t &j, uint32_t nsteps) {
+    if (++j == nsteps) { j = 0; k++; }
+}
+
+// The epilogue of row group g (acc already reduced and scaled).
+__device__ __forceinline__ void ch_epilogue(const sgk_cstage &S, const ch_gemv &c, uint32_t g, const float *acc,
+                                            const float *res, uint32_t lane) {
+    if (g >= c.gend) return;
+    const uint32_t r0 = g * CR;
+    if (S.epi == SGK_EPI_SWIGLU) {
+        if (lane == 0 && r0 + 1 < S.rows) st_out<true>(S.y + (r0 >> 1), silu(acc[0]) * acc[1]);
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < CR; r++) {
+        if (lane == (uint32_t)r && r0 + r < S.rows) {
+            const float v = S.epi == SGK_EPI_ADD ? res[r0 + r - c.gb0 * CR] + acc[r] : acc[r];
+            st_out<true>(S.y + r0 + r, v);
+        }
+    }
+}
+
+// Stage x (and the residual slice for EPI_ADD) into LDS; returns the RMS
+// factor (1 without a prologue).
+template <int PRO>
+__device__ __forceinline__ float ch_stage_x(const sgk_cstage &S, const ch_gemv &c, float *xs, float *res) {
+    constexpr int K = PRO == SGK_PRO_RMS ? CXK_RMS : CXK_NONE;
+    sgk_gemv ga = {};
+    ga.x = S.x; ga.nw = S.nw; ga.cols = S.cols; ga.eps = S.eps;
+    xstage<PRO, CT, K> st;
+    stage_issue<PRO, CT, K>(ga, st);
+    if (S.epi == SGK_EPI_ADD) {
+        const uint32_t n = (c.gend - c.gb0) * CR, t = threadIdx.x, r0 = c.gb0 * CR;
+        for (uint32_t i = t; i < n; i += CT) res[i] = r0 + i < S.rows ? S.res[r0 + i] : 0.0f;
+    }
+    return stage_finish<PRO, CT, K, true>(ga, st, xs);
+}
+
+__device__ __forceinline__ void ch_embed(const sgk_cstage &S) {
+    const uint32_t H = S.cols, nb = gridDim.x, b = blockIdx.x;
+    const uint32_t lo = (uint32_t)((uint64_t)b * H / nb), hi = (uint32_t)((uint64_t)(b + 1) * H / nb);
+    const uint64_t tk = (uint64_t)(uint32_t)S.step->token;
+    for (uint32_t i = lo + threadIdx.x; i < hi; i += CT)
+        st_out<true>(S.y + i, h2f(S.d[tk * (H >> 5) + (i >> 5)]) * (float)S.qs[tk * H + i]);
+}
+
+template <int DK, int RW>
+__global__ void __launch_bounds__(CT) k_chain(sgk_chain a) {
+    extern __shared__ float cl[];
+    float *xs = cl, *res = cl + CH_X_FLOATS;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    gemv_chunk<CR> ring[CP];
+    bool primed = false;
+    ch_gemv pc = {};                  // the GEMV stage the ring was primed for
+    uint32_t pst = 0;
+    // Prime the ring with the first CP steps of the next GEMV stage after
+    // st, unless this workgroup has other work (a DeltaNet step) before it:
+    // its loads would otherwise queue ahead of that work's.
+    auto prime_after = [&](uint32_t st) {
+        if (primed) return;
+        for (uint32_t t = st + 1; t < a.s1; t++) {
+            const sgk_cstage &S = a.st[t];
+            if (S.kind == SGK_CS_GEMV) {
+                pc = ch_enter(S, w);
+                pst = t;
+                if (pc.nk) {
+                    const uint32_t n = pc.nk * pc.nsteps;
+                    uint32_t k = 0, j = 0;
+#pragma unroll
+                    for (int u = 0; u < CP; u++) {
+                        if ((uint32_t)u < n) ch_issue(ring[u], pc, k, j, lane);
+                        ch_step_next(k, j, pc.nsteps);
+                    }
+                }
+                primed = true;
+                return;
+            }
+            if (S.kind == SGK_CS_GDN && blockIdx.x < S.gdn.n_v) return;
+            if (S.kind == SGK_CS_EMBED) return;
+        }
+    };
+    if (a.st[a.s0].kind == SGK_CS_GEMV) prime_after(a.s0 - 1);
+    for (uint32_t st = a.s0; st < a.s1; st++) {
+        if (st > a.s0) ch_wait(a, st - 1);
+        const sgk_cstage &S = a.st[st];
+        if (S.kind == SGK_CS_GEMV) {
+            if (!primed) prime_after(st - 1);      // workgroups that ran a DeltaNet step first
+            const ch_gemv c = pc;
+            primed = false;
+            const float post = S.pro == SGK_PRO_RMS ? ch_stage_x<SGK_PRO_RMS>(S, c, xs, res)
+                                                    : ch_stage_x<SGK_PRO_NONE>(S, c, xs, res);
+            if (c.nk) {
+                const uint32_t n = c.nk * c.nsteps;
+                float acc[CR];
+#pragma unroll
+                for (int r = 0; r < CR; r++) acc[r] = 0.0f;
+                uint32_t kc = 0, jc = 0, ki = 0, ji = 0;
+                for (uint32_t u = 0; u < CP; u++) ch_step_next(ki, ji, c.nsteps);   // the ring holds steps 0..CP-1
+                uint32_t i = 0;
+                for (;;) {
+                    const bool last = i + CP >= n;
+#pragma unroll
+                    for (int u = 0; u < CP; u++) {
+                        if (last && i + u >= n) break;
+                        gemv_fma<CR, true>(acc, ring[u], xs, lane + 64 * jc);
+                        if (jc == c.nsteps - 1) {
+#pragma unroll
+                            for (int r = 0; r < CR; r++) acc[r] = wave_sum(acc[r]) * post;
+                            ch_epilogue(S, c, c.gw + CW * kc, acc, res, lane);
+#pragma unroll
+                            for (int r = 0; r < CR; r++) acc[r] = 0.0f;
+                        }
+                        ch_step_next(kc, jc, c.nsteps);
+                        if (i + u + CP < n) {
+                            ch_issue(ring[u], c, ki, ji, lane);
+                            ch_step_next(ki, ji, c.nsteps);
+                        }
+                    }
+                    if (last) break;
+                    i += CP;
+                }
+            }
+        } else if (S.kind == SGK_CS_GDN) {
+            if (blockIdx.x < S.gdn.n_v) gdn_step_body<DK, RW, 1, CT, true>(S.gdn, blockIdx.x, 0);
+        } else if (S.kind == SGK_CS_EMBED) {
+            ch_embed(S);
+        }
+        ch_arrive(a, st);
+        prime_after(st);
+    }
+}
+
+extern "C" uint32_t sgk_chain_blocks(void) { return (uint32_t)device_cus(); }
+
+extern "C" hipError_t sgk_chain_launch(const sgk_chain *a, uint32_t dk, uint32_t dv, hipStream_t s) {
+    if (!a->st || !a->cnt || !a->err || a->s0 >= a->s1 || !a->epoch) return hipErrorInvalidValue;
+    const uint32_t rw = (dv + 7) / 8;
+    auto kern = k_chain<128, 16>;
+    if (dk == 128 && rw == 16) kern = k_chain<128, 16>;
+    else if (dk == 128 && rw == 8) kern = k_chain<128, 8>;
+    else if (dk == 64 && rw == 8) kern = k_chain<64, 8>;
+    else if (dk == 64 && rw == 4) kern = k_chain<64, 4>;
+    else return hipErrorInvalidValue;
+    hipError_t e = allow_lds((const void *)kern, SGK_CHAIN_LDS);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(device_cus()), dim3(CT), SGK_CHAIN_LDS, s, *a);
+    return hipGetLastError();
 }

@@ -85,3 +85,17 @@ def test_27b_prefill_512_chunks_matches_serial(gpu, model27):
     assert rel(last, serial) < 1e-3
     gen_prefill = gpu.decode_greedy(int(np.argmax(last)), n, n_gen)
     assert gen_prefill.tolist() == gen_serial.tolist()
+
+
+def test_27b_chain_greedy_identical_to_reference(gpu, model27, monkeypatch):
+    """The same 16 + 16 tokens through the decode chain (SURGE_CHAIN=1: one
+    persistent launch per run of stages between attention layers)."""
+    gold = json.load(open(os.path.join(fixture.GOLDEN, "greedy_27b_ref.json")))
+    prompt, want = gold["prompt_ids"], gold["gen_ids"]
+    monkeypatch.setenv("SURGE_CHAIN", "1")
+    gpu.state_new(len(prompt) + len(want) + 1)
+    assert gpu.chain_active()
+    for p, t in enumerate(prompt[:-1]):
+        gpu.forward_nosync(t, p)
+    gen = gpu.decode_greedy(prompt[-1], len(prompt) - 1, len(want))
+    assert gen.tolist() == want
