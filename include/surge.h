@@ -340,6 +340,16 @@ sg_err sg_gpu_decode_greedy_timed(sg_gpu *g, const sg_model *m, int32_t token, u
  * outputs are the per-kernel path's within float reassociation. A chain
  * barrier that does not resolve makes the call that waited for it fail. */
 bool sg_gpu_chain_active(const sg_gpu *g);
+/* Measurement hook for the chain (no reference counterpart): with
+ * SURGE_CHAIN_STAMPS=1 at sg_gpu_state_new every chain launch writes, per
+ * stage and workgroup, the device wall clock (hipDeviceAttributeWallClockRate
+ * kHz) when the stage's inputs are ready, when its x is staged and when its
+ * stores are complete; this copies the last token's [n_stages][n_blocks][3]
+ * stamps out (cap values), with each stage's kind (low byte: 1 GEMV, 2
+ * DeltaNet step, 3 embedding; GEMVs add prologue << 8, epilogue << 12 and
+ * columns / 1024 << 16). */
+sg_err sg_gpu_chain_stamps(sg_gpu *g, uint64_t *out, uint64_t cap, uint32_t *n_stages, uint32_t *n_blocks,
+                           uint32_t *kinds);
 /* Decode at depth without a prefill (no reference counterpart; for
  * benchmarks of the KV read path at long context): fills every attention
  * layer's K/V cache rows [0, n_tokens) with seeded f16 values in [-2, 2], the

@@ -146,6 +146,8 @@ struct sg_gpu {
     uint32_t *ch_cnt, *ch_err;
     uint32_t ch_epoch;
     uint32_t ch_spin;       /* SURGE_CHAIN_SPIN: polls per barrier wait (tests of the give-up path) */
+    uint64_t *ch_stamps;    /* SURGE_CHAIN_STAMPS=1: per stage and workgroup wall-clock stamps */
+    uint32_t ch_tune;       /* SURGE_CHAIN_TUNE: ring / prime depth variant (measurement) */
 };
 
 /* The decode attention partial a state dispatches (fixed per state: the
@@ -1084,8 +1086,8 @@ sg_err sg_gpu_load_model(sg_gpu *g, const sg_model *m) {
 
 static void state_free(sg_gpu *g) {
     if (!g->have_state) return;
-    dfree(g, g->ch_st); dfree(g, g->ch_buf); dfree(g, g->ch_cnt); dfree(g, g->ch_err);
-    g->ch_st = NULL; g->ch_buf = NULL; g->ch_cnt = g->ch_err = NULL;
+    dfree(g, g->ch_st); dfree(g, g->ch_buf); dfree(g, g->ch_cnt); dfree(g, g->ch_err); dfree(g, g->ch_stamps);
+    g->ch_st = NULL; g->ch_buf = NULL; g->ch_cnt = g->ch_err = NULL; g->ch_stamps = NULL;
     free(g->ch_seg);
     g->ch_seg = NULL;
     g->ch_n = g->ch_nseg = 0;
@@ -1152,7 +1154,8 @@ static hipError_t enqueue_chain(sg_gpu *g, bool greedy) {
     hipError_t e;
     g->ch_epoch++;
     for (uint32_t k = 0; k < g->ch_nseg; k++) {
-        sgk_chain a = {g->ch_st, g->ch_seg[k].s0, g->ch_seg[k].s1, g->ch_cnt, g->ch_epoch, g->ch_err, g->ch_spin};
+        sgk_chain a = {g->ch_st, g->ch_seg[k].s0, g->ch_seg[k].s1, g->ch_cnt, g->ch_epoch, g->ch_err, g->ch_spin,
+                       g->ch_stamps, g->ch_tune};
         if ((e = sgk_chain_launch(&a, c->head_k_dim, c->head_v_dim, g->stream)) != hipSuccess) return e;
         const int32_t al = g->ch_seg[k].attn;
         if (al >= 0 && (e = enqueue_attn(g, &g->ls[al], g->ch_seg[k].q)) != hipSuccess) return e;
@@ -1250,15 +1253,18 @@ static bool chain_eligible(const sg_gpu *g) {
     if (gdn && !((c->head_k_dim == 128 && (rw == 16 || rw == 8)) || (c->head_k_dim == 64 && (rw == 8 || rw == 4))))
         return false;
     if (gdn && c->n_v_heads > nb) return false;
-    const uint32_t add_rows = ((H + 1) / 2 + nb - 1) / nb * 2;
-    if (add_rows > SGK_CHAIN_MAX_RES_ROWS) return false;
     const uint32_t rms_cols = H, none_cols[3] = {c->ffn_hidden, g->value_dim, g->attn_width};
     if (rms_cols % 1024 || rms_cols > SGK_CHAIN_MAX_RMS_COLS) return false;
     for (int k = 0; k < 3; k++)
         if (none_cols[k] % 1024 || none_cols[k] > SGK_CHAIN_MAX_COLS) return false;
+    const uint32_t lds = SGK_CHAIN_LDS / 4;
+    if (sgk_chain_lds_floats(g->lm.rows, g->lm.cols, nb) > lds) return false;
     for (uint32_t i = 0; i < c->n_layers; i++) {
         const glayer *L = &g->ls[i];
         if (!L->in.qs || !L->out.qs || !L->gu.qs || !L->down.qs) return false;
+        const dmat *M[4] = {&L->in, &L->out, &L->gu, &L->down};
+        for (int k = 0; k < 4; k++)
+            if (M[k]->cols % 1024 || sgk_chain_lds_floats(M[k]->rows, M[k]->cols, nb) > lds) return false;
     }
     return true;
 }
@@ -1353,6 +1359,30 @@ static sg_err chain_status(sg_gpu *g) {
 static bool graphed(const sg_gpu *g) { return g->use_graph && !g->chain; }
 
 bool sg_gpu_chain_active(const sg_gpu *g) { return g && g->have_state && g->chain; }
+
+sg_err sg_gpu_chain_stamps(sg_gpu *g, uint64_t *out, uint64_t cap, uint32_t *n_stages, uint32_t *n_blocks,
+                           uint32_t *kinds) {
+    if (!g || !g->have_state || !g->chain || !g->ch_stamps)
+        return (sg_err){"gpu: chain stamps need a chain state made with SURGE_CHAIN_STAMPS=1"};
+    const uint32_t nb = sgk_chain_blocks();
+    const uint64_t n = (uint64_t)g->ch_n * nb * 3;
+    if (!out || cap < n) return errf("gpu: chain stamps need room for %llu values", (unsigned long long)n);
+    HIPCHK(hipStreamSynchronize(g->stream), "chain stamps");
+    HIPCHK(hipMemcpy(out, g->ch_stamps, n * 8, hipMemcpyDeviceToHost), "chain stamps");
+    if (n_stages) *n_stages = g->ch_n;
+    if (n_blocks) *n_blocks = nb;
+    if (kinds) {
+        sgk_cstage *T = malloc((uint64_t)g->ch_n * sizeof *T);
+        if (!T) return (sg_err){"gpu: out of host memory"};
+        hipError_t he = hipMemcpy(T, g->ch_st, (uint64_t)g->ch_n * sizeof *T, hipMemcpyDeviceToHost);
+        for (uint32_t i = 0; i < g->ch_n && he == hipSuccess; i++)
+            kinds[i] = T[i].kind | (T[i].kind == SGK_CS_GEMV ? (T[i].pro << 8) | (T[i].epi << 12) : 0) |
+                       (T[i].kind == SGK_CS_GEMV ? (T[i].cols >> 10) << 16 : 0);
+        free(T);
+        if (he != hipSuccess) return (sg_err){"gpu: chain stage table download failed"};
+    }
+    return SG_OK;
+}
 
 static sg_err capture(sg_gpu *g, bool greedy, hipGraphExec_t *out) {
     hipGraph_t graph = NULL;
@@ -1500,6 +1530,11 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
         }
         const char *sp = getenv("SURGE_CHAIN_SPIN");
         g->ch_spin = sp && *sp ? (uint32_t)strtoul(sp, NULL, 10) : 0;
+        const char *tu = getenv("SURGE_CHAIN_TUNE");
+        g->ch_tune = tu && *tu ? (uint32_t)strtoul(tu, NULL, 10) : 0;
+        const char *ss = getenv("SURGE_CHAIN_STAMPS");
+        if (!sg_failed(e) && g->chain && ss && !strcmp(ss, "1"))
+            e = dzalloc(g, (uint64_t)g->ch_n * sgk_chain_blocks() * 3 * 8, (void **)&g->ch_stamps);
     }
     if (!sg_failed(e) && graphed(g)) {
         e = capture(g, false, &g->g_fwd);

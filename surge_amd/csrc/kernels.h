@@ -18,6 +18,18 @@
 extern "C" {
 #endif
 
+/* Pointers that device code reads out of descriptors in memory (the chain's
+ * stage table) are typed as global-memory pointers in the device compile
+ * pass, so its loads and stores are global ones rather than flat ones (a
+ * flat access also counts against the LDS wait counter, which would make
+ * every LDS read wait for the weight stream). Same bits and layout as the
+ * host's plain pointers. */
+#if defined(__HIP_DEVICE_COMPILE__)
+#define SGK_G __attribute__((address_space(1)))
+#else
+#define SGK_G
+#endif
+
 /* Per-token step descriptor, read by every position-dependent kernel so one
  * captured HIP graph serves every decode step. */
 typedef struct {
@@ -160,22 +172,24 @@ hipError_t sgk_attn_flash(const sgk_attn *a, hipStream_t s);
  * pre-norm readout y[value_dim]. The out-projection's gated-RMS prologue
  * finishes the layer. */
 typedef struct {
-    const float *in;        /* GEMV output: qkv[conv_dim] | z[value_dim] | b[n_v] | a[n_v] */
-    const float *conv_w;    /* [conv_dim][ksize] */
-    float *ring;            /* [4][conv_dim] last inputs, slot = position % 4 */
-    const float *ssm_a, *dt_bias;  /* [n_v] */
-    float *S;               /* [n_v][dv][dk] */
-    float *y;               /* [value_dim] */
-    const sgk_step *step;
+    const float SGK_G *in;        /* GEMV output: qkv[conv_dim] | z[value_dim] | b[n_v] | a[n_v] */
+    const float SGK_G *conv_w;    /* [conv_dim][ksize] */
+    float SGK_G *ring;            /* [4][conv_dim] last inputs, slot = position % 4 */
+    const float SGK_G *ssm_a;
+    const float SGK_G *dt_bias;  /* [n_v] */
+    float SGK_G *S;               /* [n_v][dv][dk] */
+    float SGK_G *y;               /* [value_dim] */
+    const sgk_step SGK_G *step;
     uint32_t n_k, n_v, dk, dv, conv_dim, ksize;
     int tiled, neg_exp;
     /* decode step only: z [value_dim] (the projection's z rows); out receives
      * silu(z), y the pre-norm readouts and ss [n_v][SGK_GDN_BLOCKS] each row
      * block's sum of squared readouts, for the gated GEMV prologue */
-    const float *z, *norm_w;
-    float *out;
+    const float SGK_G *z;
+    const float SGK_G *norm_w;
+    float SGK_G *out;
     float eps;
-    float *ss;
+    float SGK_G *ss;
     uint32_t blocks;        /* workgroups per head: 1 (the step finishes RMSNormGated into out)
                              * or SGK_GDN_BLOCKS (out = silu(z), y and ss for the gated prologue) */
 } sgk_gdn;
@@ -274,17 +288,26 @@ enum { SGK_CS_GEMV = 1, SGK_CS_GDN = 2, SGK_CS_EMBED = 3 };
 #define SGK_CHAIN_LDS (96u * 1024u)          /* dynamic LDS: one workgroup per CU */
 #define SGK_CHAIN_MAX_COLS 18432u            /* GEMV columns (a multiple of 1024) */
 #define SGK_CHAIN_MAX_RMS_COLS 8192u         /* ... behind the RMSNorm prologue */
-#define SGK_CHAIN_MAX_RES_ROWS 1024u         /* rows of one workgroup in an EPI_ADD stage */
+/* LDS floats a GEMV stage of the chain needs with nb workgroups: the staged
+ * x (1040 floats per 1024 columns), then per row group of a workgroup CW x 2
+ * partial slots and 2 residual rows. At most SGK_CHAIN_LDS / 4. */
+static inline uint32_t sgk_chain_lds_floats(uint32_t rows, uint32_t cols, uint32_t nb) {
+    const uint32_t groups = (rows + 1) / 2, ng = (groups + nb - 1) / nb;
+    return ((cols / 16 + 63) / 64) * 1040 + ng * 18;
+}
 typedef struct {
     uint32_t kind;              /* SGK_CS_* */
     uint32_t pro, epi;          /* GEMV: SGK_PRO_NONE | RMS, SGK_EPI_STORE | ADD | SWIGLU */
     uint32_t rows, cols;        /* GEMV; EMBED: cols = hidden */
-    const int8_t *qs;           /* GEMV / EMBED (the table) */
-    const uint16_t *d;
-    const float *x, *nw, *res;  /* input, RMS weight, EPI_ADD residual (y = res + W x) */
-    float *y;
+    const int8_t SGK_G *qs;     /* GEMV / EMBED (the table) */
+    const uint16_t SGK_G *d;
+    /* input, RMS weight, EPI_ADD residual (y = res + W x) */
+    const float SGK_G *x;
+    const float SGK_G *nw;
+    const float SGK_G *res;
+    float SGK_G *y;
     float eps;
-    const sgk_step *step;       /* EMBED: the token */
+    const sgk_step SGK_G *step; /* EMBED: the token */
     sgk_gdn gdn;                /* GDN: one workgroup per value head (blocks == 1) */
 } sgk_cstage;
 typedef struct {
@@ -294,6 +317,9 @@ typedef struct {
     uint32_t epoch;
     uint32_t *err;
     uint32_t spin;              /* polls a wait makes before giving up (0: the default bound) */
+    uint64_t *stamps;           /* NULL, or [n_stages][workgroups][3] device wall-clock stamps per
+                                 * stage: inputs ready (barrier passed), x staged, stores complete */
+    uint32_t tune;              /* 0: default ring and prime depths; 1..6 measured alternatives */
 } sgk_chain;
 /* DeltaNet shapes the chain's step takes: (dk, ceil(dv / 8)) in
  * {(128, 16), (128, 8), (64, 8), (64, 4)}. */

@@ -3691,24 +3691,28 @@ extern "C" void *sgk_scratch_ptr(int dev) {
 #define CT 512
 #define CW (CT / 64)
 #define CR 2
-#define CP 8
 #define CH_XCDS 8u
 #define CH_CNT_STRIDE 64u            // uint32 per counter: one 256-byte line each
 #define CH_SPIN_MAX (1u << 21)
-#define CH_RES_FLOATS 1024u
-#define CH_X_FLOATS ((SGK_CHAIN_LDS - CH_RES_FLOATS * 4) / 4)
 constexpr int CXK_NONE = (SGK_CHAIN_MAX_COLS + 4 * CT - 1) / (4 * CT);   // x float4s per thread in flight
 constexpr int CXK_RMS = (SGK_CHAIN_MAX_RMS_COLS + 4 * CT - 1) / (4 * CT);
-static_assert(((SGK_CHAIN_MAX_COLS / 16 + 63) / 64) * XS_CH_BLK * 4 <= CH_X_FLOATS, "chain: staged x does not fit");
+static_assert(XS_CH_BLK * 4 == 1040, "chain: sgk_chain_lds_floats assumes 1040 floats per 1024 staged columns");
 
 __device__ __forceinline__ uint32_t ch_ld(const uint32_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Measurement stamps (sgk_chain.stamps): the device wall clock at point k of
+// stage st, seen by thread 0.
+__device__ __forceinline__ void ch_stamp(const sgk_chain &a, uint32_t st, uint32_t k) {
+    if (a.stamps && threadIdx.x == 0) a.stamps[((size_t)st * gridDim.x + blockIdx.x) * 3 + k] = wall_clock64();
 }
 
 // Arrival at stage st: this workgroup's stores are complete, then one add.
 __device__ __forceinline__ void ch_arrive(const sgk_chain &a, uint32_t st) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    ch_stamp(a, st, 2);
     if (threadIdx.x == 0)
         __hip_atomic_fetch_add(a.cnt + ((size_t)st * CH_XCDS + blockIdx.x % CH_XCDS) * CH_CNT_STRIDE, 1u,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -3735,70 +3739,70 @@ __device__ __forceinline__ void ch_wait(const sgk_chain &a, uint32_t st) {
     __syncthreads();
 }
 
-// A wave's share of one GEMV stage.
+// A wave's share of one GEMV stage. Workgroup b owns the row groups
+// [b*G/NB, (b+1)*G/NB) (G groups of CR rows); their steps (group, 16-column
+// step j), group-major, are dealt to the CW waves in equal contiguous
+// ranges (within one step of each other), so a stage is balanced to a step
+// per wave and a group per workgroup however few groups there are. A wave
+// streams its steps as k_gemv_q8<2> streams a row group (lane l: chunks l,
+// l+64, ... of both rows, f32 FMA per chunk), and writes one wave-reduced
+// partial per group it touched into LDS (the others' slots stay 0); after the
+// stage the workgroup adds each group's CW slots in wave order (adding the
+// zeros is exact, so a group one wave did whole keeps k_gemv_q8's bits).
 struct ch_gemv {
     const int8_t *qs;
     const uint16_t *d;
     uint32_t rows, cols, nsteps;     // steps per row group: cols / 1024
-    uint32_t gw, gend, gb0;          // this wave's first group, the workgroup's group range end, its start
-    uint32_t nk;                     // row groups per wave (0: the workgroup has none)
+    uint32_t g0, ng;                 // the workgroup's row groups
+    uint32_t s0, ns;                 // this wave's steps of them
 };
 
 __device__ __forceinline__ ch_gemv ch_enter(const sgk_cstage &S, uint32_t w) {
     ch_gemv c;
     c.qs = S.qs; c.d = S.d; c.rows = S.rows; c.cols = S.cols; c.nsteps = S.cols >> 10;
     const uint32_t G = (S.rows + CR - 1) / CR, nb = gridDim.x, b = blockIdx.x;
-    c.gb0 = (uint32_t)((uint64_t)b * G / nb);
-    c.gend = (uint32_t)((uint64_t)(b + 1) * G / nb);
-    const uint32_t n = c.gend - c.gb0;
-    c.nk = (n + CW - 1) / CW;
-    c.gw = c.gb0 + w;
+    c.g0 = (uint32_t)((uint64_t)b * G / nb);
+    c.ng = (uint32_t)((uint64_t)(b + 1) * G / nb) - c.g0;
+    const uint32_t T = c.ng * c.nsteps;
+    c.s0 = w * T / CW;
+    c.ns = (w + 1) * T / CW - c.s0;
     return c;
 }
 
-// Request step i = (group ordinal k, chunk step j) of a wave's share.
+// Request the step at (group k of the workgroup, chunk step j); groups past
+// the workgroup's re-read its last (never out of bounds).
 __device__ __forceinline__ void ch_issue(gemv_chunk<CR> &ch, const ch_gemv &c, uint32_t k, uint32_t j, uint32_t lane) {
-    uint32_t g = c.gw + CW * k;
-    g = g < c.gend ? g : c.gend - 1;
-    gemv_load<CR>(ch, c.qs, c.d, g * CR, c.rows, c.cols, lane + 64 * j);
+    const uint32_t kk = k < c.ng ? k : c.ng - 1;
+    gemv_load<CR>(ch, c.qs, c.d, (c.g0 + kk) * CR, c.rows, c.cols, lane + 64 * j);
 }
 
 __device__ __forceinline__ void ch_step_next(uint32_t &k, uint32_t &j, uint32_t nsteps) {
     if (++j == nsteps) { j = 0; k++; }
 }
 
-// The epilogue of row group g (acc already reduced and scaled).
-__device__ __forceinline__ void ch_epilogue(const sgk_cstage &S, const ch_gemv &c, uint32_t g, const float *acc,
-                                            const float *res, uint32_t lane) {
-    if (g >= c.gend) return;
-    const uint32_t r0 = g * CR;
-    if (S.epi == SGK_EPI_SWIGLU) {
-        if (lane == 0 && r0 + 1 < S.rows) st_out<true>(S.y + (r0 >> 1), silu(acc[0]) * acc[1]);
-        return;
-    }
+// LDS of a GEMV stage after the staged x: the groups' partial slots
+// [ng][CW][CR], then the residual rows [ng*CR].
+__device__ __forceinline__ uint32_t ch_part_off(uint32_t cols) { return xs_ch_floats(cols); }
+
+// The stage's outputs from the partial slots (all waves' slots written and
+// visible): thread t < ng*CR sums row t's slots in wave order.
+__device__ __forceinline__ void ch_finish(const sgk_cstage &S, const ch_gemv &c, const float *part, const float *res,
+                                          float post) {
+    const uint32_t t = threadIdx.x;
+    for (uint32_t i = t; i < c.ng * CR; i += CT) {
+        const uint32_t k = i / CR, r = i % CR, row = (c.g0 + k) * CR + r;
+        float v = 0.0f;
 #pragma unroll
-    for (int r = 0; r < CR; r++) {
-        if (lane == (uint32_t)r && r0 + r < S.rows) {
-            const float v = S.epi == SGK_EPI_ADD ? res[r0 + r - c.gb0 * CR] + acc[r] : acc[r];
-            st_out<true>(S.y + r0 + r, v);
+        for (uint32_t w = 0; w < CW; w++) v += part[(k * CW + w) * CR + r];
+        v *= post;
+        if (S.epi == SGK_EPI_SWIGLU) {
+            // (gate, up) rows: the even thread of the pair has both
+            const float u = __shfl_down(v, 1);
+            if (r == 0 && row + 1 < S.rows) st_out<true>(S.y + (row >> 1), silu(v) * u);
+        } else if (row < S.rows) {
+            st_out<true>(S.y + row, S.epi == SGK_EPI_ADD ? res[i] + v : v);
         }
     }
-}
-
-// Stage x (and the residual slice for EPI_ADD) into LDS; returns the RMS
-// factor (1 without a prologue).
-template <int PRO>
-__device__ __forceinline__ float ch_stage_x(const sgk_cstage &S, const ch_gemv &c, float *xs, float *res) {
-    constexpr int K = PRO == SGK_PRO_RMS ? CXK_RMS : CXK_NONE;
-    sgk_gemv ga = {};
-    ga.x = S.x; ga.nw = S.nw; ga.cols = S.cols; ga.eps = S.eps;
-    xstage<PRO, CT, K> st;
-    stage_issue<PRO, CT, K>(ga, st);
-    if (S.epi == SGK_EPI_ADD) {
-        const uint32_t n = (c.gend - c.gb0) * CR, t = threadIdx.x, r0 = c.gb0 * CR;
-        for (uint32_t i = t; i < n; i += CT) res[i] = r0 + i < S.rows ? S.res[r0 + i] : 0.0f;
-    }
-    return stage_finish<PRO, CT, K, true>(ga, st, xs);
 }
 
 __device__ __forceinline__ void ch_embed(const sgk_cstage &S) {
@@ -3809,35 +3813,78 @@ __device__ __forceinline__ void ch_embed(const sgk_cstage &S) {
         st_out<true>(S.y + i, h2f(S.d[tk * (H >> 5) + (i >> 5)]) * (float)S.qs[tk * H + i]);
 }
 
-template <int DK, int RW>
+// Stage x (and the residual slice for EPI_ADD), split so the ring's top-up
+// loads can go out between the x requests and the LDS stores.
+template <int PRO>
+struct ch_xs {
+    static constexpr int K = PRO == SGK_PRO_RMS ? CXK_RMS : CXK_NONE;
+    sgk_gemv ga;
+    xstage<PRO, CT, K> st;
+};
+template <int PRO>
+__device__ __forceinline__ void ch_x_issue(ch_xs<PRO> &X, const sgk_cstage &S, const ch_gemv &c, float *lds) {
+    X.ga = sgk_gemv{};
+    X.ga.x = S.x; X.ga.nw = S.nw; X.ga.cols = S.cols; X.ga.eps = S.eps;
+    stage_issue<PRO, CT, ch_xs<PRO>::K>(X.ga, X.st);
+    float *part = lds + ch_part_off(S.cols), *res = part + c.ng * CW * CR;
+    const uint32_t t = threadIdx.x;
+    for (uint32_t i = t; i < c.ng * CW * CR; i += CT) part[i] = 0.0f;
+    if (S.epi == SGK_EPI_ADD) {
+        const uint32_t r0 = c.g0 * CR;
+        for (uint32_t i = t; i < c.ng * CR; i += CT) res[i] = r0 + i < S.rows ? S.res[r0 + i] : 0.0f;
+    }
+}
+template <int PRO>
+__device__ __forceinline__ float ch_x_finish(ch_xs<PRO> &X, float *xs) {
+    return stage_finish<PRO, CT, ch_xs<PRO>::K, true>(X.ga, X.st, xs);
+}
+
+// CP: steps a wave keeps in flight while streaming (the ring); PR <= CP: how
+// many of a GEMV's first steps are requested before the barrier that
+// precedes it (the rest go out right after it, behind the x requests). Loads
+// requested before a barrier delay everything the wave requests after them
+// (returns are in order), the barrier's polls included, so PR is kept to what
+// covers the barrier.
+// The stage table is read-only for a launch: read through the constant
+// address space, its fields come in by scalar loads, which do not wait
+// behind the wave's weight requests (a vector load's wait would).
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef const __attribute__((address_space(4))) sgk_cstage ch_table;
+#else
+typedef const sgk_cstage ch_table;
+#endif
+
+template <int DK, int RW, int CP, int PR>
 __global__ void __launch_bounds__(CT) k_chain(sgk_chain a) {
+    static_assert(PR <= CP, "chain: prime at most the ring");
+    ch_table *T = (ch_table *)a.st;
     extern __shared__ float cl[];
-    float *xs = cl, *res = cl + CH_X_FLOATS;
+    float *xs = cl;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     gemv_chunk<CR> ring[CP];
     bool primed = false;
     ch_gemv pc = {};                  // the GEMV stage the ring was primed for
-    uint32_t pst = 0;
-    // Prime the ring with the first CP steps of the next GEMV stage after
-    // st, unless this workgroup has other work (a DeltaNet step) before it:
-    // its loads would otherwise queue ahead of that work's.
+    // The first PR steps of a wave's share of stage c into the ring.
+    auto prime = [&](const ch_gemv &c) {
+        if (!c.ns) return;
+        uint32_t k = c.s0 / c.nsteps, j = c.s0 % c.nsteps;
+#pragma unroll
+        for (int u = 0; u < PR; u++) {
+            ch_issue(ring[u], c, k, j, lane);
+            ch_step_next(k, j, c.nsteps);
+        }
+    };
+    // Prime the ring for the next GEMV stage after st, unless this workgroup
+    // has other work (a DeltaNet step) before it: its loads would otherwise
+    // queue ahead of that work's.
     auto prime_after = [&](uint32_t st) {
         if (primed) return;
         for (uint32_t t = st + 1; t < a.s1; t++) {
-            const sgk_cstage &S = a.st[t];
+            const sgk_cstage S = T[__builtin_amdgcn_readfirstlane(t)];
             if (S.kind == SGK_CS_GEMV) {
                 pc = ch_enter(S, w);
-                pst = t;
-                if (pc.nk) {
-                    const uint32_t n = pc.nk * pc.nsteps;
-                    uint32_t k = 0, j = 0;
-#pragma unroll
-                    for (int u = 0; u < CP; u++) {
-                        if ((uint32_t)u < n) ch_issue(ring[u], pc, k, j, lane);
-                        ch_step_next(k, j, pc.nsteps);
-                    }
-                }
+                prime(pc);
                 primed = true;
                 return;
             }
@@ -3845,47 +3892,94 @@ __global__ void __launch_bounds__(CT) k_chain(sgk_chain a) {
             if (S.kind == SGK_CS_EMBED) return;
         }
     };
-    if (a.st[a.s0].kind == SGK_CS_GEMV) prime_after(a.s0 - 1);
+    if (T[a.s0].kind == SGK_CS_GEMV) prime_after(a.s0 - 1);
     for (uint32_t st = a.s0; st < a.s1; st++) {
         if (st > a.s0) ch_wait(a, st - 1);
-        const sgk_cstage &S = a.st[st];
+        ch_stamp(a, st, 0);
+        // the descriptor by value: the stage's stores could alias the table,
+        // and a field reloaded after one would wait for every weight load
+        const sgk_cstage S = T[__builtin_amdgcn_readfirstlane(st)];
         if (S.kind == SGK_CS_GEMV) {
-            if (!primed) prime_after(st - 1);      // workgroups that ran a DeltaNet step first
+            if (!primed) {                    // workgroups that ran a DeltaNet step first
+                pc = ch_enter(S, w);
+                prime(pc);
+            }
             const ch_gemv c = pc;
             primed = false;
-            const float post = S.pro == SGK_PRO_RMS ? ch_stage_x<SGK_PRO_RMS>(S, c, xs, res)
-                                                    : ch_stage_x<SGK_PRO_NONE>(S, c, xs, res);
-            if (c.nk) {
-                const uint32_t n = c.nk * c.nsteps;
+            float *part = cl + ch_part_off(S.cols), *res = part + c.ng * CW * CR;
+            float post;
+            // x requests, then the ring's remaining first steps (CP - PR, the
+            // same count on every path, so the wait counts stay exact), then
+            // x into LDS
+#define CH_TOPUP()                                                                            \
+            if (c.ns) {                                                                       \
+                uint32_t k = (c.s0 + PR) / c.nsteps, j = (c.s0 + PR) % c.nsteps;              \
+                _Pragma("unroll")                                                             \
+                for (int u = PR; u < CP; u++) {                                               \
+                    ch_issue(ring[u], c, k, j, lane);                                         \
+                    ch_step_next(k, j, c.nsteps);                                             \
+                }                                                                             \
+            }
+            if (S.pro == SGK_PRO_RMS) {
+                ch_xs<SGK_PRO_RMS> X;
+                ch_x_issue(X, S, c, cl);
+                CH_TOPUP();
+                post = ch_x_finish(X, xs);
+            } else {
+                ch_xs<SGK_PRO_NONE> X;
+                ch_x_issue(X, S, c, cl);
+                CH_TOPUP();
+                post = ch_x_finish(X, xs);
+            }
+#undef CH_TOPUP
+            ch_stamp(a, st, 1);
+            if (c.ns) {
+                const uint32_t n = c.ns;
                 float acc[CR];
 #pragma unroll
                 for (int r = 0; r < CR; r++) acc[r] = 0.0f;
-                uint32_t kc = 0, jc = 0, ki = 0, ji = 0;
+                uint32_t kc = c.s0 / c.nsteps, jc = c.s0 % c.nsteps, ki = kc, ji = jc;
                 for (uint32_t u = 0; u < CP; u++) ch_step_next(ki, ji, c.nsteps);   // the ring holds steps 0..CP-1
+                // step i of the wave's range: FMAs of ring slot u; at a group's
+                // last step or the range's last, the group's wave partial to LDS
+                auto consume = [&](int u, uint32_t i) {
+                    gemv_fma<CR, true>(acc, ring[u], xs, lane + 64 * jc);
+                    if (jc == c.nsteps - 1 || i == n - 1) {
+#pragma unroll
+                        for (int r = 0; r < CR; r++) acc[r] = wave_sum(acc[r]);
+                        if (lane < (uint32_t)CR) part[(kc * CW + w) * CR + lane] = lane == 0 ? acc[0] : acc[CR - 1];
+#pragma unroll
+                        for (int r = 0; r < CR; r++) acc[r] = 0.0f;
+                    }
+                    ch_step_next(kc, jc, c.nsteps);
+                };
                 uint32_t i = 0;
-                for (;;) {
-                    const bool last = i + CP >= n;
+                // steady state: every consumed slot is refilled, unconditionally
+                for (; i + 2 * CP <= n; i += CP) {
 #pragma unroll
                     for (int u = 0; u < CP; u++) {
-                        if (last && i + u >= n) break;
-                        gemv_fma<CR, true>(acc, ring[u], xs, lane + 64 * jc);
-                        if (jc == c.nsteps - 1) {
+                        consume(u, i + u);
+                        ch_issue(ring[u], c, ki, ji, lane);
+                        ch_step_next(ki, ji, c.nsteps);
+                    }
+                }
+                // the last n - i (< 2 CP) steps: refill only what is still to come
 #pragma unroll
-                            for (int r = 0; r < CR; r++) acc[r] = wave_sum(acc[r]) * post;
-                            ch_epilogue(S, c, c.gw + CW * kc, acc, res, lane);
-#pragma unroll
-                            for (int r = 0; r < CR; r++) acc[r] = 0.0f;
-                        }
-                        ch_step_next(kc, jc, c.nsteps);
+                for (int u = 0; u < CP; u++) {
+                    if (i + u < n) {
+                        consume(u, i + u);
                         if (i + u + CP < n) {
                             ch_issue(ring[u], c, ki, ji, lane);
                             ch_step_next(ki, ji, c.nsteps);
                         }
                     }
-                    if (last) break;
-                    i += CP;
                 }
+#pragma unroll
+                for (int u = 0; u < CP; u++)
+                    if (i + CP + u < n) consume(u, i + CP + u);
             }
+            __syncthreads();
+            ch_finish(S, c, part, res, post);
         } else if (S.kind == SGK_CS_GDN) {
             if (blockIdx.x < S.gdn.n_v) gdn_step_body<DK, RW, 1, CT, true>(S.gdn, blockIdx.x, 0);
         } else if (S.kind == SGK_CS_EMBED) {
@@ -3898,14 +3992,27 @@ __global__ void __launch_bounds__(CT) k_chain(sgk_chain a) {
 
 extern "C" uint32_t sgk_chain_blocks(void) { return (uint32_t)device_cus(); }
 
+#define CH_CP 4
+#define CH_PR 4
 extern "C" hipError_t sgk_chain_launch(const sgk_chain *a, uint32_t dk, uint32_t dv, hipStream_t s) {
     if (!a->st || !a->cnt || !a->err || a->s0 >= a->s1 || !a->epoch) return hipErrorInvalidValue;
     const uint32_t rw = (dv + 7) / 8;
-    auto kern = k_chain<128, 16>;
-    if (dk == 128 && rw == 16) kern = k_chain<128, 16>;
-    else if (dk == 128 && rw == 8) kern = k_chain<128, 8>;
-    else if (dk == 64 && rw == 8) kern = k_chain<64, 8>;
-    else if (dk == 64 && rw == 4) kern = k_chain<64, 4>;
+    auto kern = k_chain<128, 16, CH_CP, CH_PR>;
+    if (dk == 128 && rw == 16) {
+        switch (a->tune) {           // ring / prime depth experiments (27B DeltaNet shape)
+        case 1: kern = k_chain<128, 16, 8, 8>; break;
+        case 2: kern = k_chain<128, 16, 4, 4>; break;
+        case 3: kern = k_chain<128, 16, 4, 0>; break;
+        case 4: kern = k_chain<128, 16, 3, 1>; break;
+        case 5: kern = k_chain<128, 16, 6, 2>; break;
+        case 6: kern = k_chain<128, 16, 2, 2>; break;
+        case 7: kern = k_chain<128, 16, 6, 6>; break;
+        case 8: kern = k_chain<128, 16, 5, 5>; break;
+        default: kern = k_chain<128, 16, CH_CP, CH_PR>;
+        }
+    } else if (dk == 128 && rw == 8) kern = k_chain<128, 8, CH_CP, CH_PR>;
+    else if (dk == 64 && rw == 8) kern = k_chain<64, 8, CH_CP, CH_PR>;
+    else if (dk == 64 && rw == 4) kern = k_chain<64, 4, CH_CP, CH_PR>;
     else return hipErrorInvalidValue;
     hipError_t e = allow_lds((const void *)kern, SGK_CHAIN_LDS);
     if (e != hipSuccess) return e;

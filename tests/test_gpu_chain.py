@@ -8,9 +8,10 @@ between runs.
   identical argmax, for both DeltaNet shapes the chain takes at dk 128 and
   dk 64, over enough positions that the attention partial runs several splits
   and the conv ring wraps many times.
-- The same logits as the per-kernel path within 1e-5 (the chain's GEMV row
-  sums are the per-kernel GEMV's bits; only the RMS factor's summation
-  order differs).
+- The same logits as the per-kernel path within 1e-4 (float reassociation
+  only: a chain GEMV row is summed in the per-kernel GEMV's order unless its
+  row group is split between two waves, and the RMS factor's partial sums are
+  grouped per 512 instead of 256 threads; measured about 1.3e-5).
 - The device greedy loop gives the host loop's tokens; the 2B BASELINE
   configuration gives the reference ref.c's 64 tokens.
 - A barrier that does not resolve fails the call (forced from the host with
@@ -77,7 +78,7 @@ def test_chain_matches_per_kernel_path_and_greedy_loops(gpu, monkeypatch):
     gpu.state_new(128)
     assert gpu.chain_active()
     chain = np.stack([gpu.forward(t, p) for p, t in enumerate(ids)])
-    assert rel(chain, plain) < 1e-5
+    assert rel(chain, plain) < 1e-4
     assert (chain.argmax(1) == plain.argmax(1)).all()
     # device loop == per-kernel path's device loop == host loop
     gen = gpu.decode_greedy(int(np.argmax(chain[-1])), len(ids), 24)
