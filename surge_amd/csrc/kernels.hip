@@ -695,6 +695,149 @@ static hipError_t launch_q8(const sgk_gemv &a, size_t lds, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Balanced Q8_0 GEMV (the default for Q8_0 matrices whose width is a multiple
+// of 1024). One BT-thread workgroup per CU. Workgroup b owns the row groups
+// [b*G/NB, (b+1)*G/NB) of 2 rows; their steps (group, 1024-column block j),
+// group-major, are dealt to its waves in equal contiguous ranges, so every
+// wave of the chip has the same number of 2 KB steps to within one (the
+// grid-stride kernel above gives whole row groups to waves, up to 12% apart).
+// A wave streams a step as k_gemv_q8<2> streams a chunk pair (lane l: chunk
+// l + 64 j of both rows, f32 FMA per chunk) and keeps BP steps in flight in
+// a register ring indexed statically; all BP of the first steps are
+// requested before x is staged, so HBM streams while x arrives. Each wave
+// writes one wave-reduced partial per row group it touched into LDS (the
+// other waves' slots of that group are 0); the workgroup then adds a group's
+// slots in wave order (adding zeros is exact: a group one wave did whole
+// keeps k_gemv_q8's bits) and applies the prologue's factor and the
+// epilogue. EPI_ADD may update y in place: a workgroup stages its rows of y
+// before it writes them.
+// ---------------------------------------------------------------------------
+#define BT 768
+#define BW (BT / 64)
+#define BP 4
+constexpr int BXK_NONE = (SGK_CHAIN_MAX_COLS + 4 * BT - 1) / (4 * BT);
+constexpr int BXK_RMS = (SGK_CHAIN_MAX_RMS_COLS + 4 * BT - 1) / (4 * BT);
+
+__host__ __device__ __forceinline__ uint32_t bal_lds_floats(uint32_t rows, uint32_t cols, uint32_t nb) {
+    const uint32_t G = (rows + 1) / 2, ng = (G + nb - 1) / nb;
+    return xs_ch_floats(cols) + ng * (BW * 2 + 2);
+}
+
+template <int PRO, int EPI, bool IL>
+__global__ void __launch_bounds__(BT) k_gemv_bal(sgk_gemv a) {
+    extern __shared__ float lds[];
+    const uint32_t lane = threadIdx.x & 63, t = threadIdx.x;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nsteps = a.cols >> 10, G = (a.rows + 1) / 2, nb = gridDim.x, b = blockIdx.x;
+    // IL: the workgroup's k-th group is b + k*nb (all workgroups stream one
+    // compact window at a time); else the contiguous range from g0
+    const uint32_t g0 = IL ? b : (uint32_t)((uint64_t)b * G / nb);
+    const uint32_t ng = IL ? (b < G ? (G - b + nb - 1) / nb : 0) : (uint32_t)((uint64_t)(b + 1) * G / nb) - g0;
+    const uint32_t gs = IL ? nb : 1;
+    if (!ng) return;
+    const uint32_t T = ng * nsteps, s0 = w * T / BW, ns = (w + 1) * T / BW - s0;
+    float *xs = lds, *part = lds + xs_ch_floats(a.cols), *res = part + ng * BW * 2;
+    gemv_chunk<2> ring[BP];
+    auto issue = [&](gemv_chunk<2> &ch, uint32_t k, uint32_t j) {
+        const uint32_t kk = k < ng ? k : ng - 1;
+        gemv_load<2>(ch, a.qs, a.d, (g0 + kk * gs) * 2, a.rows, a.cols, lane + 64 * j);
+    };
+    auto next = [&](uint32_t &k, uint32_t &j) { if (++j == nsteps) { j = 0; k++; } };
+    uint32_t ki = s0 / nsteps, ji = s0 % nsteps;
+#pragma unroll
+    for (int u = 0; u < BP; u++) {          // the first steps (re-reads past the range are discarded)
+        issue(ring[u], ki, ji);
+        next(ki, ji);
+    }
+    constexpr int K = PRO == SGK_PRO_RMS ? BXK_RMS : BXK_NONE;
+    xstage<PRO, BT, K> st;
+    stage_issue<PRO, BT, K>(a, st);
+    for (uint32_t i = t; i < ng * BW * 2; i += BT) part[i] = 0.0f;
+    if (EPI == SGK_EPI_ADD)
+        for (uint32_t i = t; i < ng * 2; i += BT) {
+            const uint32_t row = (g0 + (i >> 1) * gs) * 2 + (i & 1);
+            res[i] = row < a.rows ? a.y[row] : 0.0f;
+        }
+    const float post = stage_finish<PRO, BT, K, true>(a, st, xs);
+    if (ns) {
+        float acc[2] = {0.0f, 0.0f};
+        uint32_t kc = s0 / nsteps, jc = s0 % nsteps;
+        auto consume = [&](int u, uint32_t i) {
+            gemv_fma<2, true>(acc, ring[u], xs, lane + 64 * jc);
+            if (jc == nsteps - 1 || i == ns - 1) {
+                acc[0] = wave_sum(acc[0]);
+                acc[1] = wave_sum(acc[1]);
+                if (lane < 2) part[(kc * BW + w) * 2 + lane] = lane == 0 ? acc[0] : acc[1];
+                acc[0] = acc[1] = 0.0f;
+            }
+            next(kc, jc);
+        };
+        uint32_t i = 0;
+        for (; i + 2 * BP <= ns; i += BP) {
+#pragma unroll
+            for (int u = 0; u < BP; u++) {
+                consume(u, i + u);
+                issue(ring[u], ki, ji);
+                next(ki, ji);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < BP; u++) {
+            if (i + u < ns) {
+                consume(u, i + u);
+                if (i + u + BP < ns) {
+                    issue(ring[u], ki, ji);
+                    next(ki, ji);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < BP; u++)
+            if (i + BP + u < ns) consume(u, i + BP + u);
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < ng * 2; i += BT) {
+        const uint32_t k = i >> 1, r = i & 1, row = (g0 + k * gs) * 2 + r;
+        float v = 0.0f;
+#pragma unroll
+        for (uint32_t ww = 0; ww < BW; ww++) v += part[(k * BW + ww) * 2 + r];
+        v *= post;
+        if (EPI == SGK_EPI_SWIGLU) {
+            const float u = __shfl_down(v, 1);
+            if (r == 0 && row + 1 < a.rows) a.y[row >> 1] = silu(v) * u;
+        } else if (row < a.rows) {
+            a.y[row] = EPI == SGK_EPI_ADD ? res[i] + v : v;
+        }
+    }
+}
+
+// Which kernel takes a Q8_0 GEMV of `cols` columns (multiples of 1024 only):
+// 0 k_gemv_q8 / k_gemv_q8_long, 1 k_gemv_bal contiguous, 2 k_gemv_bal
+// interleaved. Measured per 27B shape (one MI355X, back-to-back launches over
+// the layers): the interleaved balanced kernel streams the 17408-column down
+// projection in 18.5 us against 20.2 for k_gemv_q8_long; at 5120 and 6144
+// columns k_gemv_q8 is as fast or faster, and contiguous ranges are slower
+// than interleaved ones everywhere. SURGE_GEMV=q8|bal|bali forces one.
+static int gemv_bal_on(uint32_t cols) {
+    const char *e = getenv("SURGE_GEMV");
+    if (e && e[0] == 'q' && e[1] == '8' && !e[2]) return 0;
+    if (e && e[0] == 'b' && e[1] == 'a' && e[2] == 'l' && e[3] == 'i' && !e[4]) return 2;
+    if (e && e[0] == 'b' && e[1] == 'a' && e[2] == 'l' && !e[3]) return 1;
+    return cols > 8192 ? 2 : 0;
+}
+
+template <int PRO, int EPI>
+static hipError_t launch_bal(const sgk_gemv &a, hipStream_t s) {
+    auto kern = gemv_bal_on(a.cols) == 2 ? k_gemv_bal<PRO, EPI, true> : k_gemv_bal<PRO, EPI, false>;
+    const uint32_t nb = (uint32_t)device_cus();
+    const size_t lds = (size_t)bal_lds_floats(a.rows, a.cols, nb) * 4;
+    hipError_t e = allow_lds((const void *)kern, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(nb), dim3(BT), lds, s, a);
+    return hipGetLastError();
+}
+
 template <int PRO, int EPI>
 static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
     if (((uintptr_t)a->x & 15) || (PRO == SGK_PRO_RMS && ((uintptr_t)a->nw & 15))) return hipErrorInvalidValue;
@@ -711,6 +854,10 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         hipLaunchKernelGGL((k_gemv_f32<PRO, EPI>), dim3(min((groups + 3) / 4, 4096u)), dim3(TPB), lds, s, *a);
         return hipGetLastError();
     }
+    if (PRO != SGK_PRO_GATED && gemv_bal_on(a->cols) && !a->tune_r && !a->tune_blocks && a->cols % 1024 == 0 &&
+        a->cols <= (PRO == SGK_PRO_RMS ? SGK_CHAIN_MAX_RMS_COLS : SGK_CHAIN_MAX_COLS) &&
+        bal_lds_floats(a->rows, a->cols, (uint32_t)device_cus()) * 4 <= 160 * 1024)
+        return launch_bal<PRO == SGK_PRO_RMS ? SGK_PRO_RMS : SGK_PRO_NONE, EPI>(*a, s);
     if (PRO == SGK_PRO_NONE && EPI != SGK_EPI_SWIGLU && a->cols > 8192 && a->tune_r != 7 && a->tune_r != 8) {
         const size_t lds = ((size_t)xs_ch_floats(a->cols) + LW * LW) * 4;
         constexpr int LE = EPI == SGK_EPI_ADD ? SGK_EPI_ADD : SGK_EPI_STORE;
@@ -3739,10 +3886,11 @@ __device__ __forceinline__ void ch_wait(const sgk_chain &a, uint32_t st) {
     __syncthreads();
 }
 
-// A wave's share of one GEMV stage. Workgroup b owns the row groups
-// [b*G/NB, (b+1)*G/NB) (G groups of CR rows); their steps (group, 16-column
-// step j), group-major, are dealt to the CW waves in equal contiguous
-// ranges (within one step of each other), so a stage is balanced to a step
+// A wave's share of one GEMV stage. Workgroup b owns the row groups b,
+// b + NB, b + 2 NB, ... (G groups of CR rows: all workgroups stream one
+// compact window of the matrix at a time, measured faster than contiguous
+// ranges); their steps (group, 1024-column step j), group-major, are dealt
+// to the CW waves in equal contiguous ranges (within one step of each other), so a stage is balanced to a step
 // per wave and a group per workgroup however few groups there are. A wave
 // streams its steps as k_gemv_q8<2> streams a row group (lane l: chunks l,
 // l+64, ... of both rows, f32 FMA per chunk), and writes one wave-reduced
@@ -3753,7 +3901,7 @@ struct ch_gemv {
     const int8_t *qs;
     const uint16_t *d;
     uint32_t rows, cols, nsteps;     // steps per row group: cols / 1024
-    uint32_t g0, ng;                 // the workgroup's row groups
+    uint32_t g0, ng;                 // the workgroup's row groups: g0 + k*NB for k < ng
     uint32_t s0, ns;                 // this wave's steps of them
 };
 
@@ -3761,8 +3909,8 @@ __device__ __forceinline__ ch_gemv ch_enter(const sgk_cstage &S, uint32_t w) {
     ch_gemv c;
     c.qs = S.qs; c.d = S.d; c.rows = S.rows; c.cols = S.cols; c.nsteps = S.cols >> 10;
     const uint32_t G = (S.rows + CR - 1) / CR, nb = gridDim.x, b = blockIdx.x;
-    c.g0 = (uint32_t)((uint64_t)b * G / nb);
-    c.ng = (uint32_t)((uint64_t)(b + 1) * G / nb) - c.g0;
+    c.g0 = b;
+    c.ng = b < G ? (G - b + nb - 1) / nb : 0;
     const uint32_t T = c.ng * c.nsteps;
     c.s0 = w * T / CW;
     c.ns = (w + 1) * T / CW - c.s0;
@@ -3773,7 +3921,7 @@ __device__ __forceinline__ ch_gemv ch_enter(const sgk_cstage &S, uint32_t w) {
 // the workgroup's re-read its last (never out of bounds).
 __device__ __forceinline__ void ch_issue(gemv_chunk<CR> &ch, const ch_gemv &c, uint32_t k, uint32_t j, uint32_t lane) {
     const uint32_t kk = k < c.ng ? k : c.ng - 1;
-    gemv_load<CR>(ch, c.qs, c.d, (c.g0 + kk) * CR, c.rows, c.cols, lane + 64 * j);
+    gemv_load<CR>(ch, c.qs, c.d, (c.g0 + kk * gridDim.x) * CR, c.rows, c.cols, lane + 64 * j);
 }
 
 __device__ __forceinline__ void ch_step_next(uint32_t &k, uint32_t &j, uint32_t nsteps) {
@@ -3790,7 +3938,7 @@ __device__ __forceinline__ void ch_finish(const sgk_cstage &S, const ch_gemv &c,
                                           float post) {
     const uint32_t t = threadIdx.x;
     for (uint32_t i = t; i < c.ng * CR; i += CT) {
-        const uint32_t k = i / CR, r = i % CR, row = (c.g0 + k) * CR + r;
+        const uint32_t k = i / CR, r = i % CR, row = (c.g0 + k * gridDim.x) * CR + r;
         float v = 0.0f;
 #pragma unroll
         for (uint32_t w = 0; w < CW; w++) v += part[(k * CW + w) * CR + r];
@@ -3830,8 +3978,10 @@ __device__ __forceinline__ void ch_x_issue(ch_xs<PRO> &X, const sgk_cstage &S, c
     const uint32_t t = threadIdx.x;
     for (uint32_t i = t; i < c.ng * CW * CR; i += CT) part[i] = 0.0f;
     if (S.epi == SGK_EPI_ADD) {
-        const uint32_t r0 = c.g0 * CR;
-        for (uint32_t i = t; i < c.ng * CR; i += CT) res[i] = r0 + i < S.rows ? S.res[r0 + i] : 0.0f;
+        for (uint32_t i = t; i < c.ng * CR; i += CT) {
+            const uint32_t row = (c.g0 + (i / CR) * gridDim.x) * CR + i % CR;
+            res[i] = row < S.rows ? S.res[row] : 0.0f;
+        }
     }
 }
 template <int PRO>
