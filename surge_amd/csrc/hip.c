@@ -117,6 +117,7 @@ struct sg_gpu {
     float *pf_X, *pf_Xn, *pf_IN, *pf_CONV, *pf_Y, *pf_G, *pf_CTX, *pf_FF, *pf_m, *pf_s, *pf_acc;
     uint16_t *pf_XS;        /* the prefill GEMMs' X split into bf16 hi | lo */
     float *pf_PART;         /* split-K partials of the narrow prefill GEMMs: 4 x chunk x hidden */
+    float *pf_WY;           /* the chunked DeltaNet scan's per-(head, sub-chunk) workspace */
 
     /* the pinned step descriptor's upload: the next write to h_step waits
      * for it (event recorded after each upload) */
@@ -819,7 +820,9 @@ sg_err sg_gpu_run_delta_chunk(sg_gpu *g, void *S, void *qkv, void *out, void *ga
     if (sg_failed(e = push(ins, 4))) return e;
     sgk_gdn d = {0};
     d.S = DEV(S); d.y = DEV(out); d.n_k = nk; d.n_v = nv; d.dk = dk; d.dv = dv; d.conv_dim = cd; d.tiled = p[5] != 0;
-    return finish(g, sgk_delta_scan(&d, DEV(qkv), cd, n_tok, DEV(gates), g->stream), outs, 2);
+    void *ws = NULL;
+    if (sg_failed(e = scratch(g, sgk_delta_wy_ws_floats(nv, n_tok) * 4, &ws))) return e;
+    return finish(g, sgk_delta_scan(&d, DEV(qkv), cd, n_tok, DEV(gates), (float *)ws, g->stream), outs, 2);
 }
 
 sg_err sg_gpu_run_rmsnorm_gated_chunk(sg_gpu *g, void *y, void *z, void *out, void *w, const uint32_t p[8]) {
@@ -1107,7 +1110,7 @@ static void state_free(sg_gpu *g) {
         void **pb[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
                         (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
                         (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc,
-                        (void **)&g->pf_XS, (void **)&g->pf_PART };
+                        (void **)&g->pf_XS, (void **)&g->pf_PART, (void **)&g->pf_WY };
         for (size_t i = 0; i < sizeof pb / sizeof *pb; i++) { dfree(g, *pb[i]); *pb[i] = NULL; }
         g->pf_chunk = 0;
     }
@@ -1756,7 +1759,7 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     void **bufs[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
                       (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
                       (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc,
-                      (void **)&g->pf_XS, (void **)&g->pf_PART };
+                      (void **)&g->pf_XS, (void **)&g->pf_PART, (void **)&g->pf_WY };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) { dfree(g, *bufs[i]); *bufs[i] = NULL; }
     if (g->pf_hsteps) { hipHostFree(g->pf_hsteps); g->pf_hsteps = NULL; }
     g->pf_chunk = 0;
@@ -1771,7 +1774,7 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     uint64_t sizes[] = { n * sizeof(sgk_step), n * c->hidden * 4, n * c->hidden * 4, n * in_rows * 4,
                          n * g->conv_dim * 4 + 4, n * g->value_dim * 4 + 4, n * g->value_dim * 4 + 4,
                          n * g->attn_width * 4 + 4, n * c->ffn_hidden * 4, ah * 4, ah * 4, ah * c->head_dim * 4,
-                         n * kmax * 4, 4 * n * c->hidden * 4 };
+                         n * kmax * 4, 4 * n * c->hidden * 4, sgk_delta_wy_ws_floats(c->n_v_heads, chunk) * 4 + 4 };
     sg_err e = SG_OK;
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs && !sg_failed(e); i++) e = dzalloc(g, sizes[i], bufs[i]);
     if (!sg_failed(e) && hipHostMalloc((void **)&g->pf_hsteps, n * sizeof(sgk_step), 0) != hipSuccess)
@@ -1836,7 +1839,7 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
             d.S = L->S; d.y = g->pf_Y; d.step = g->pf_steps; d.n_k = c->n_k_heads; d.n_v = c->n_v_heads;
             d.dk = c->head_k_dim; d.dv = c->head_v_dim; d.conv_dim = g->conv_dim; d.ksize = c->conv_kernel;
             d.tiled = g->model->v_heads_tiled; d.neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
-            if ((e = sgk_gdn_chunk(&d, g->pf_CONV, in_rows, n, s)) != hipSuccess) return e;
+            if ((e = sgk_gdn_chunk(&d, g->pf_CONV, in_rows, n, g->pf_WY, s)) != hipSuccess) return e;
             if ((e = sgk_rmsnorm_gated_rows(g->pf_Y, g->pf_IN + g->conv_dim, in_rows, L->ssm_norm, g->pf_G,
                                             c->head_v_dim, c->n_v_heads, n, c->rms_eps, s)) != hipSuccess) return e;
             if ((e = gemm_rows(g, &L->out, g->pf_G, g->value_dim, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;

@@ -206,12 +206,16 @@ hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s);
  * norms, then the delta-rule scan with S in registers. Same arithmetic as
  * sgk_gdn_step, token by token. */
 hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t in_stride, uint32_t ntok,
-                         hipStream_t s);
+                         float *ws, hipStream_t s);
 /* The delta-rule scan alone: qkv rows [ntok][in_stride] hold normalised
  * q | k | v; gates [ntok][2*n_v] = beta | decay (or NULL: computed from the
- * b/a columns of a->in as in sgk_gdn_chunk). */
+ * b/a columns of a->in as in sgk_gdn_chunk). With a workspace ws of
+ * sgk_delta_wy_ws_floats(n_v, ntok) floats, dk 64 or 128 and
+ * SURGE_DELTA_SCAN=wy it runs the chunked (WY) form over 64-token
+ * sub-chunks; otherwise the sequential scan. */
 hipError_t sgk_delta_scan(const sgk_gdn *a, const float *qkv, uint32_t in_stride, uint32_t ntok,
-                          const float *gates, hipStream_t s);
+                          const float *gates, float *ws, hipStream_t s);
+uint64_t sgk_delta_wy_ws_floats(uint32_t n_v, uint32_t ntok);
 /* Conv over a chunk with an oldest-first state [ksize-1][ch] in/out, no
  * activation (the reference's k_conv1d_chunk contract). */
 hipError_t sgk_conv1d_chunk(const float *x, const float *w, float *out, float *state, uint32_t ch,

@@ -2998,8 +2998,284 @@ __global__ void k_embed_rows(const int8_t *qs, const uint16_t *d, const float *w
     else x[i] = wf[t * hidden + i];
 }
 
+// ---------------------------------------------------------------------------
+// Chunked delta rule (the WY / UT form of the sequential scan above) over
+// sub-chunks of WY_C tokens. For one value head, with S the state at the
+// sub-chunk's start (row j: value dim j), gate products in log space
+// (LG_t = sum of log decay over the sub-chunk's tokens up to t, in double),
+//   T_ts  = beta_t exp(LG_t - LG_s) k_t.k_s   (s < t),   W = (I + T)^-1
+//   Mq_ts = exp(LG_t - LG_s) q_t.k_s          (s <= t)
+//   Delta = W [beta (V - exp(LG) K S^T)]      (rows t: the step's deltas)
+//   Y     = exp(LG) Q S^T + Mq Delta          (the readouts)
+//   S'    = exp(LG_n) S + sum_s exp(LG_n - LG_s) Delta_s k_s^T
+// which unrolls the recurrence of ref.c:708-739 (s = decay S; kv = s k;
+// delta = (v - kv) beta; S = s + delta k^T; y = S q) exactly in real
+// arithmetic; in fp32 it differs by reassociation. k_wy_prep computes the
+// state-free parts of every (sub-chunk, head) in parallel; k_wy_scan walks a
+// head's sub-chunks in order for a block of WY_RB state rows (rows are
+// independent in the rule), with only dense products per sub-chunk.
+// Workspace per (head, sub-chunk): W^T, Mq^T [WY_C][WY_C], beta, exp(LG_t),
+// exp(LG_n - LG_s) [WY_C]. Row strides: qkv (the conv output) a.conv_dim,
+// a.in (the projection rows the gates come from) in_stride.
+// ---------------------------------------------------------------------------
+#define WY_C 64
+#define WY_RB 16
+#define WY_PITCH(D) ((D) + 4)
+#define WY_WS (2 * WY_C * WY_C + 3 * WY_C)
+
+// log of the decay gate (gdn_gates' decay = exp(this)).
+__device__ __forceinline__ float gdn_log_decay(float a, float ssm_a, float dt, int neg_exp) {
+    const float sp = softplus(a + dt);
+    return neg_exp ? ssm_a * sp : -(expf(ssm_a) * sp);
+}
+
+template <int DK>
+__global__ void __launch_bounds__(TPB) k_wy_prep(sgk_gdn a, const float *qkv, uint32_t in_stride, uint32_t ntok,
+                                                 const float *gates, float *ws) {
+    __shared__ __align__(16) float KT[DK][WY_C + 4];
+    __shared__ __align__(16) float QT[DK][WY_C + 4];
+    __shared__ float Tm[WY_C][WY_C + 1];
+    __shared__ float Mq[WY_C][WY_C + 1];
+    __shared__ double L[WY_C];
+    __shared__ float bt[WY_C], red[4][WY_C];
+    const uint32_t c = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+    const uint32_t z0 = c * WY_C, n = min((uint32_t)WY_C, ntok - z0);
+    const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k), key_dim = a.n_k * DK;
+    // 1. k and q of the sub-chunk's tokens, transposed ([i][t]); zero past n
+    for (uint32_t e = t; e < WY_C * DK / 4; e += TPB) {
+        const uint32_t row = e / (DK / 4), i = (e % (DK / 4)) * 4;
+        f32x4 kv = {0.f, 0.f, 0.f, 0.f}, qv = {0.f, 0.f, 0.f, 0.f};
+        if (row < n) {
+            const float *cz = qkv + (size_t)(z0 + row) * a.conv_dim;
+            kv = *(const f32x4 *)(cz + key_dim + (size_t)hk * DK + i);
+            qv = *(const f32x4 *)(cz + (size_t)hk * DK + i);
+        }
+        KT[i][row] = kv.x; KT[i + 1][row] = kv.y; KT[i + 2][row] = kv.z; KT[i + 3][row] = kv.w;
+        QT[i][row] = qv.x; QT[i + 1][row] = qv.y; QT[i + 2][row] = qv.z; QT[i + 3][row] = qv.w;
+    }
+    // 2. beta and log decay per token (0 and 0 past n)
+    if (t < WY_C) {
+        float beta = 0.0f, lg = 0.0f;
+        if (t < n) {
+            const uint32_t z = z0 + t;
+            if (gates) {
+                beta = gates[(size_t)z * 2 * a.n_v + h];
+                const float dcy = gates[(size_t)z * 2 * a.n_v + a.n_v + h];
+                lg = dcy > 0.0f ? logf(dcy) : -1.0e30f;
+            } else {
+                const float *iz = a.in + (size_t)z * in_stride;
+                const uint32_t cd = a.conv_dim, vd = a.n_v * a.dv;
+                beta = sigm(iz[cd + vd + h]);
+                lg = gdn_log_decay(iz[cd + vd + a.n_v + h], a.ssm_a[h], a.dt_bias[h], a.neg_exp);
+            }
+        }
+        bt[t] = beta;
+        red[0][t] = lg;
+    }
+    __syncthreads();
+    if (t == 0) {
+        double acc = 0.0;
+        for (uint32_t i = 0; i < WY_C; i++) { acc += (double)red[0][i]; L[i] = acc; }
+    }
+    // 3. G = K K^T and A = Q K^T, 4x4 tiles per thread
+    const uint32_t tr = t % 16, sc = t / 16, t0 = tr * 4, s0 = sc * 4;
+    float G[4][4], A[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; x++)
+#pragma unroll
+        for (int y = 0; y < 4; y++) G[x][y] = A[x][y] = 0.0f;
+    __syncthreads();
+    for (uint32_t i = 0; i < DK; i++) {
+        const f32x4 ka = *(const f32x4 *)&KT[i][t0], kb = *(const f32x4 *)&KT[i][s0], qa = *(const f32x4 *)&QT[i][t0];
+        const float kav[4] = {ka.x, ka.y, ka.z, ka.w}, kbv[4] = {kb.x, kb.y, kb.z, kb.w}, qav[4] = {qa.x, qa.y, qa.z, qa.w};
+#pragma unroll
+        for (int x = 0; x < 4; x++)
+#pragma unroll
+            for (int y = 0; y < 4; y++) {
+                G[x][y] = fmaf(kav[x], kbv[y], G[x][y]);
+                A[x][y] = fmaf(qav[x], kbv[y], A[x][y]);
+            }
+    }
+#pragma unroll
+    for (int x = 0; x < 4; x++)
+#pragma unroll
+        for (int y = 0; y < 4; y++) {
+            const uint32_t tt = t0 + x, ss = s0 + y;
+            const float r = ss <= tt ? expf((float)(L[tt] - L[ss])) : 0.0f;
+            Tm[tt][ss] = ss < tt ? bt[tt] * r * G[x][y] : 0.0f;
+            Mq[tt][ss] = ss <= tt ? r * A[x][y] : 0.0f;
+        }
+    __syncthreads();
+    // 4. W = (I + T)^-1 in place, row by row (forward substitution):
+    //    W_t = e_t - sum_{s<t} T_ts W_s
+    {
+        const uint32_t u = t & (WY_C - 1), part = t / WY_C;
+        if (part == 0) Tm[0][u] = u == 0 ? 1.0f : 0.0f;      // W_0 = e_0 (row 0 of T is zero)
+        __syncthreads();
+        for (uint32_t row = 1; row < WY_C; row++) {
+            float acc = 0.0f;
+            for (uint32_t sidx = part; sidx < row; sidx += TPB / WY_C) acc = fmaf(Tm[row][sidx], Tm[sidx][u], acc);
+            red[part][u] = acc;
+            __syncthreads();
+            if (part == 0) {
+                const float sum = (red[0][u] + red[1][u]) + (red[2][u] + red[3][u]);
+                Tm[row][u] = (u == row ? 1.0f : 0.0f) - (u < row ? sum : 0.0f);
+            }
+            __syncthreads();
+        }
+    }
+    // 5. W^T, Mq^T, beta, exp(LG_t), exp(LG_n - LG_s)
+    float *o = ws + ((size_t)h * gridDim.x + c) * WY_WS;
+    for (uint32_t e = t; e < WY_C * WY_C; e += TPB) {
+        const uint32_t sidx = e / WY_C, tt = e % WY_C;
+        o[e] = Tm[tt][sidx];
+        o[WY_C * WY_C + e] = Mq[tt][sidx];
+    }
+    if (t < WY_C) {
+        o[2 * WY_C * WY_C + t] = bt[t];
+        o[2 * WY_C * WY_C + WY_C + t] = expf((float)L[t]);
+        o[2 * WY_C * WY_C + 2 * WY_C + t] = expf((float)(L[n - 1] - L[t]));
+    }
+}
+
+template <int DK>
+__global__ void __launch_bounds__(TPB) k_wy_scan(sgk_gdn a, const float *qkv, uint32_t in_stride, uint32_t ntok,
+                                                 const float *ws) {
+    __shared__ __align__(16) float Ks[WY_C][WY_PITCH(DK)];
+    __shared__ __align__(16) float Qs[WY_C][WY_PITCH(DK)];
+    __shared__ __align__(16) float WT[WY_C][WY_C];
+    __shared__ __align__(16) float MT[WY_C][WY_C];
+    __shared__ __align__(16) float Ss[WY_RB][WY_PITCH(DK)];
+    __shared__ float Rv[WY_C][WY_RB + 1];
+    __shared__ float Dl[WY_C][WY_RB + 1];
+    __shared__ float bt[WY_C], gg[WY_C], dd[WY_C];
+    const uint32_t h = blockIdx.x, j0 = blockIdx.y * WY_RB, t = threadIdx.x;
+    const uint32_t dv = a.dv, vd = a.n_v * dv, key_dim = a.n_k * DK;
+    const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k);
+    const uint32_t nsub = (ntok + WY_C - 1) / WY_C;
+    float *Sh = a.S + (size_t)h * dv * DK;
+    // this block's state rows (zero past dv)
+    for (uint32_t e = t; e < WY_RB * DK / 4; e += TPB) {
+        const uint32_t jj = e / (DK / 4), i = (e % (DK / 4)) * 4;
+        *(f32x4 *)&Ss[jj][i] = j0 + jj < dv ? *(const f32x4 *)(Sh + (size_t)(j0 + jj) * DK + i) : (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    const uint32_t jj = t % WY_RB, tq = t / WY_RB, tt0 = tq * 4;      // X, Z, Delta, Y: rows tt0..+3 of column jj
+    const uint32_t ij = t % WY_RB, i0 = (t / WY_RB) * (DK / (TPB / WY_RB));   // S update: row ij, DK/16 columns from i0
+    constexpr int SI = DK / (TPB / WY_RB);
+    for (uint32_t c = 0; c < nsub; c++) {
+        const uint32_t z0 = c * WY_C, n = min((uint32_t)WY_C, ntok - z0);
+        const float *o = ws + ((size_t)h * nsub + c) * WY_WS;
+        for (uint32_t e = t; e < WY_C * DK / 4; e += TPB) {
+            const uint32_t row = e / (DK / 4), i = (e % (DK / 4)) * 4;
+            f32x4 kv = {0.f, 0.f, 0.f, 0.f}, qv = {0.f, 0.f, 0.f, 0.f};
+            if (row < n) {
+                const float *cz = qkv + (size_t)(z0 + row) * a.conv_dim;
+                kv = *(const f32x4 *)(cz + key_dim + (size_t)hk * DK + i);
+                qv = *(const f32x4 *)(cz + (size_t)hk * DK + i);
+            }
+            *(f32x4 *)&Ks[row][i] = kv;
+            *(f32x4 *)&Qs[row][i] = qv;
+        }
+        for (uint32_t e = t; e < WY_C * WY_C / 4; e += TPB) {
+            *(f32x4 *)&WT[0][4 * e] = *(const f32x4 *)(o + 4 * e);
+            *(f32x4 *)&MT[0][4 * e] = *(const f32x4 *)(o + WY_C * WY_C + 4 * e);
+        }
+        if (t < WY_C) {
+            bt[t] = o[2 * WY_C * WY_C + t];
+            gg[t] = o[2 * WY_C * WY_C + WY_C + t];
+            dd[t] = o[2 * WY_C * WY_C + 2 * WY_C + t];
+        }
+        // v of this block's rows: Rv[t][jj] <- v (scaled below)
+        for (uint32_t e = t; e < WY_C * WY_RB; e += TPB) {
+            const uint32_t row = e / WY_RB, q = e % WY_RB;
+            Rv[row][q] = (row < n && j0 + q < dv) ? qkv[(size_t)(z0 + row) * a.conv_dim + 2 * key_dim + (size_t)h * dv + j0 + q]
+                                                  : 0.0f;
+        }
+        __syncthreads();
+        // X = K S^T, Z = Q S^T for rows tt0..tt0+3, column jj
+        float X[4] = {0.f, 0.f, 0.f, 0.f}, Z[4] = {0.f, 0.f, 0.f, 0.f};
+        for (uint32_t i = 0; i < DK; i += 4) {
+            const f32x4 sv = *(const f32x4 *)&Ss[jj][i];
+#pragma unroll
+            for (int x = 0; x < 4; x++) {
+                const f32x4 kv = *(const f32x4 *)&Ks[tt0 + x][i], qv = *(const f32x4 *)&Qs[tt0 + x][i];
+                X[x] = fmaf(kv.x, sv.x, fmaf(kv.y, sv.y, fmaf(kv.z, sv.z, fmaf(kv.w, sv.w, X[x]))));
+                Z[x] = fmaf(qv.x, sv.x, fmaf(qv.y, sv.y, fmaf(qv.z, sv.z, fmaf(qv.w, sv.w, Z[x]))));
+            }
+        }
+        float rv[4];
+#pragma unroll
+        for (int x = 0; x < 4; x++) rv[x] = bt[tt0 + x] * (Rv[tt0 + x][jj] - gg[tt0 + x] * X[x]);
+        __syncthreads();                     // every thread has read its v
+#pragma unroll
+        for (int x = 0; x < 4; x++) Rv[tt0 + x][jj] = rv[x];
+        __syncthreads();
+        // Delta = W Rv (W lower triangular: s <= t)
+        float dl[4] = {0.f, 0.f, 0.f, 0.f};
+        const uint32_t smax = min(tt0 + 4, n);
+        for (uint32_t sidx = 0; sidx < smax; sidx++) {
+            const f32x4 w4 = *(const f32x4 *)&WT[sidx][tt0];
+            const float r = Rv[sidx][jj];
+            dl[0] = fmaf(w4.x, r, dl[0]); dl[1] = fmaf(w4.y, r, dl[1]);
+            dl[2] = fmaf(w4.z, r, dl[2]); dl[3] = fmaf(w4.w, r, dl[3]);
+        }
+#pragma unroll
+        for (int x = 0; x < 4; x++) Dl[tt0 + x][jj] = dl[x];
+        __syncthreads();
+        // Y = exp(LG) Z + Mq Delta
+        float y[4];
+#pragma unroll
+        for (int x = 0; x < 4; x++) y[x] = gg[tt0 + x] * Z[x];
+        for (uint32_t sidx = 0; sidx < smax; sidx++) {
+            const f32x4 m4 = *(const f32x4 *)&MT[sidx][tt0];
+            const float d = Dl[sidx][jj];
+            y[0] = fmaf(m4.x, d, y[0]); y[1] = fmaf(m4.y, d, y[1]);
+            y[2] = fmaf(m4.z, d, y[2]); y[3] = fmaf(m4.w, d, y[3]);
+        }
+#pragma unroll
+        for (int x = 0; x < 4; x++)
+            if (tt0 + x < n && j0 + jj < dv) a.y[(size_t)(z0 + tt0 + x) * vd + (size_t)h * dv + j0 + jj] = y[x];
+        // S' = exp(LG_n) S + sum_s exp(LG_n - LG_s) Delta_s k_s^T (row ij, columns i0..i0+SI-1)
+        {
+            const float gn = gg[n - 1];
+            float sr[SI];
+#pragma unroll
+            for (int e = 0; e < SI; e++) sr[e] = gn * Ss[ij][i0 + e];
+            for (uint32_t sidx = 0; sidx < n; sidx++) {
+                const float coef = dd[sidx] * Dl[sidx][ij];
+#pragma unroll
+                for (int e = 0; e < SI; e += 4) {
+                    const f32x4 kv = *(const f32x4 *)&Ks[sidx][i0 + e];
+                    sr[e] = fmaf(coef, kv.x, sr[e]); sr[e + 1] = fmaf(coef, kv.y, sr[e + 1]);
+                    sr[e + 2] = fmaf(coef, kv.z, sr[e + 2]); sr[e + 3] = fmaf(coef, kv.w, sr[e + 3]);
+                }
+            }
+            __syncthreads();                 // every thread has read S (X, Z) and this row's old values
+#pragma unroll
+            for (int e = 0; e < SI; e++) Ss[ij][i0 + e] = sr[e];
+        }
+        __syncthreads();
+    }
+    for (uint32_t e = t; e < WY_RB * DK / 4; e += TPB) {
+        const uint32_t r = e / (DK / 4), i = (e % (DK / 4)) * 4;
+        if (j0 + r < dv) *(f32x4 *)(Sh + (size_t)(j0 + r) * DK + i) = *(const f32x4 *)&Ss[r][i];
+    }
+}
+
+// SURGE_DELTA_SCAN=wy selects the chunked form (read per launch); the
+// sequential scan is the default: it measured faster in the 27B prefill
+// (4096 tokens 0.78 against 0.83 s, 32768 tokens 6.94 against 7.39 s).
+static bool wy_on() {
+    const char *e = getenv("SURGE_DELTA_SCAN");
+    return e && e[0] == 'w' && e[1] == 'y' && !e[2];
+}
+
+extern "C" uint64_t sgk_delta_wy_ws_floats(uint32_t n_v, uint32_t ntok) {
+    return (uint64_t)n_v * ((ntok + WY_C - 1) / WY_C) * WY_WS;
+}
+
 extern "C" hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t in_stride, uint32_t ntok,
-                                    hipStream_t s) {
+                                    float *ws, hipStream_t s) {
     if (!ntok) return hipSuccess;
     if (a->ksize < 1 || a->ksize > 4 || !a->n_k || a->n_v % a->n_k) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_conv_chunk, dim3((a->conv_dim + TPB - 1) / TPB, (ntok + CC_TOK - 1) / CC_TOK), dim3(TPB), 0, s,
@@ -3007,12 +3283,24 @@ extern "C" hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t 
     hipLaunchKernelGGL(k_conv_ring, dim3((a->conv_dim + TPB - 1) / TPB), dim3(TPB), 0, s, a->in, in_stride, a->ring,
                        a->step, ntok, a->conv_dim);
     hipLaunchKernelGGL(k_qk_norm_chunk, dim3(2 * a->n_k, ntok), dim3(TPB), 0, s, conv_out, a->conv_dim, a->n_k, a->dk);
-    return sgk_delta_scan(a, conv_out, in_stride, ntok, NULL, s);
+    return sgk_delta_scan(a, conv_out, in_stride, ntok, NULL, ws, s);
 }
 
 extern "C" hipError_t sgk_delta_scan(const sgk_gdn *a, const float *qkv, uint32_t in_stride, uint32_t ntok,
-                                     const float *gates, hipStream_t s) {
+                                     const float *gates, float *ws, hipStream_t s) {
     if (!ntok || !a->n_v || !a->dv) return hipSuccess;
+    if (ws && wy_on() && (a->dk == 64 || a->dk == 128)) {
+        // the chunked form: state-free parts of every (sub-chunk, head), then
+        // each head's sub-chunks in order per block of WY_RB state rows
+        const uint32_t nsub = (ntok + WY_C - 1) / WY_C;
+#define WYL(D) do {                                                                                            \
+            hipLaunchKernelGGL((k_wy_prep<D>), dim3(nsub, a->n_v), dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates, ws); \
+            hipLaunchKernelGGL((k_wy_scan<D>), dim3(a->n_v, (a->dv + WY_RB - 1) / WY_RB), dim3(TPB), 0, s, *a, qkv,       \
+                               in_stride, ntok, ws); } while (0)
+        if (a->dk == 64) WYL(64); else WYL(128);
+#undef WYL
+        return hipGetLastError();
+    }
     // 8 value rows per workgroup (16-token staged blocks: 33 KB of LDS at
     // dk 128, so three workgroups share a CU and hide each other's serial
     // reduction chains); 16 rows at dk 256 (its blocks take 64 KB)

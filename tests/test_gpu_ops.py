@@ -660,6 +660,72 @@ def test_delta_chunk_scan_matches_token_loop(gpu):
     assert_close(Sg.array, So)
 
 
+def _delta_chunk_case(gpu, nv, nk, dk, dv, nt, seed, gate_lo=None):
+    """Normalised q, k (|k| = 1, |q| = 1/sqrt(dk), as the layer's q/k norm
+    leaves them), v N(0, 1), S N(0, 0.1), beta = sigmoid(N(0, 1)), decay =
+    exp(-softplus(N(0, 1))) (BASELINE's gates; gate_lo instead draws decays
+    in [gate_lo, 1e-3] to reach products far below fp32's range). Returns
+    (GPU out, GPU S, oracle out, oracle S) from sg_gpu_run_delta_chunk and
+    ref.c's delta step token by token."""
+    rng = np.random.default_rng(seed)
+    kd = nk * dk
+    cd = 2 * kd + nv * dv
+    qkv = rng.standard_normal((nt, cd)).astype(np.float32)
+    for z in range(nt):
+        for hk in range(nk):
+            q = qkv[z, hk * dk:(hk + 1) * dk]
+            k = qkv[z, kd + hk * dk:kd + (hk + 1) * dk]
+            q *= 1.0 / (np.linalg.norm(q) * np.sqrt(dk))
+            k *= 1.0 / np.linalg.norm(k)
+    qkv = qkv.reshape(-1)
+    S0 = (rng.standard_normal(nv * dv * dk) * 0.1).astype(np.float32)
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((nt, nv))))
+    if gate_lo is None:
+        x = rng.standard_normal((nt, nv))
+        decay = np.exp(-(np.maximum(x, 0) + np.log1p(np.exp(-np.abs(x)))))
+    else:
+        decay = np.exp(rng.uniform(np.log(gate_lo), np.log(1e-3), (nt, nv)))
+    gates = np.concatenate([beta, decay], axis=1).astype(np.float32)
+    Sg, qb, ob, gb = gpu.buf(S0.copy()), gpu.buf(qkv), gpu.buf(np.zeros(nt * nv * dv, np.float32)), gpu.buf(gates)
+    gpu.run4("delta_chunk", Sg, qb, ob, gb, [dk, dv, nv, nk, kd, 1, nt, cd])
+    So, want = S0.copy(), np.zeros(nt * nv * dv, np.float32)
+    for z in range(nt):
+        row = qkv[z * cd:(z + 1) * cd]
+        for h in range(nv):
+            hk = h % nk
+            O.oracle().sg_ref_delta_step(fp(So[h * dv * dk:]), fp(np.ascontiguousarray(row[hk * dk:])),
+                                         fp(np.ascontiguousarray(row[kd + hk * dk:])),
+                                         fp(np.ascontiguousarray(row[2 * kd + h * dv:])), float(gates[z, h]),
+                                         float(gates[z, nv + h]), fp(want[(z * nv + h) * dv:]), dk, dv)
+    return ob.array, Sg.array, want, So
+
+
+@pytest.mark.parametrize("scan", ["wy", "seq"])
+@pytest.mark.parametrize("nv,nk,dk,dv,nt", [(16, 16, 128, 128, 200), (48, 16, 128, 128, 130), (8, 4, 64, 64, 257)],
+                         ids=["baseline16x128", "27b-tiled48over16", "dk64"])
+def test_delta_chunk_chunked_form_vs_sequential_oracle(gpu, monkeypatch, scan, nv, nk, dk, dv, nt):
+    """The prefill scan over several 64-token sub-chunks and a partial one:
+    the chunked (WY) form (SURGE_DELTA_SCAN=wy) and the sequential scan (the
+    default) against ref.c's delta step token by token, at the BASELINE
+    DeltaNet shape (16 heads x 128^2), the 27B's 48 value heads tiled over 16
+    key heads, and dk = dv = 64; readouts and the final state within the 1e-3
+    bar."""
+    monkeypatch.setenv("SURGE_DELTA_SCAN", scan)
+    got, Sgot, want, Swant = _delta_chunk_case(gpu, nv, nk, dk, dv, nt, seed=31 + nt)
+    assert_close(got, want)
+    assert_close(Sgot, Swant)
+
+
+def test_delta_chunk_chunked_form_tiny_decays(gpu, monkeypatch):
+    """Decays down to 1e-30 per token: the chunked form's decay products
+    (in log space) underflow to exact zeros instead of NaN, as the token loop's do."""
+    monkeypatch.setenv("SURGE_DELTA_SCAN", "wy")
+    got, Sgot, want, Swant = _delta_chunk_case(gpu, 8, 4, 128, 128, 150, seed=77, gate_lo=1e-30)
+    assert np.isfinite(got).all() and np.isfinite(Sgot).all()
+    assert_close(got, want)
+    assert_close(Sgot, Swant)
+
+
 def test_rmsnorm_gated_chunk(gpu):
     rng = np.random.default_rng(24)
     dv, nh, nt = 128, 6, 3
