@@ -312,7 +312,64 @@ def micro(reps_gpu=200, rotate=1 << 30):
     line("Gated-DeltaNet step 16 heads x 128 x 128, conv 6144 channels (k_gdn_step: conv, norms, gates, "
          "rank-1 update, RMSNormGated)", algo, rot, hot, cpu_us, n,
          {"cpu_sample": "sg_ref_conv1d_causal over 6144 channels + 16 sg_ref_delta_step 128x128"})
+    # 4. the floors under every decode kernel: a plain streaming read of the decode GEMVs' sizes
+    #    (lm_head 826 MB, gate/up 190 MB, the output projection 33 MB) and an empty kernel
+    for nb in (826 << 20, 190 << 20, 33 << 20):
+        rot = gpu.time_read(nb, rotate, 50)
+        hot = gpu.time_read(nb, 0, 50)
+        print(json.dumps({"unit": f"plain streaming read of {nb >> 20} MiB (k_read, 1024 workgroups)",
+                          "algo_bytes": nb, "gpu_us": round(rot, 3), "gpu_GBs": round(nb / rot / 1e3, 1),
+                          "frac": round(nb / rot / 1e3 / HBM_PEAK_GBS, 4), "gpu_us_cache_resident": round(hot, 3),
+                          "rotate_bytes": rotate, "gpu_reps": 50}), flush=True)
+    eager, graph = gpu.time_empty(2000, False), gpu.time_empty(2000, True)
+    print(json.dumps({"unit": "empty kernel launch (k_empty)", "gpu_us_per_launch_eager": round(eager, 3),
+                      "gpu_us_per_launch_in_graph": round(graph, 3), "reps": 2000}), flush=True)
     gpu.close()
+
+
+def gemv_shapes(reps=3):
+    """Every decode GEMV shape of the 27B model timed per kernel variant:
+    average microseconds per launch over back-to-back launches across the
+    layers' distinct weight matrices (HIP events on the library stream), the
+    kernel choice forced by SURGE_GEMV and the row-group / long-row overrides.
+    One JSON line per (shape, variant)."""
+    cfg = S.CFG_27B
+    syn = S.Synth(cfg, S.SG_T_Q8_0, seed=0)
+    gpu = S.Gpu()
+    gpu.load_model(syn.model)
+    gpu.state_new(64)
+    ev = HipEvents()
+    a, b = ev.event(), ev.event()
+    L = cfg["n_layers"]
+    shapes = {0: "input projection (DeltaNet 16480x5120)", 1: "output projection 5120x6144",
+              2: "gate|up 34816x5120", 3: "down 5120x17408", 4: "lm_head 151936x5120"}
+    variants = [("default", None, 0), ("k_gemv_q8 (SURGE_GEMV=q8)", "q8", 0), ("k_gemv_bal contiguous", "bal", 0),
+                ("k_gemv_bal interleaved", "bali", 0), ("k_gemv_q8 R=1", None, 1), ("k_gemv_q8 R=4", None, 4),
+                ("k_gemv_q8_long LU=4", None, 3), ("k_gemv_q8_long LU=8", None, 6)]
+    for which, name in shapes.items():
+        layers = [0] if which == 4 else [l for l in range(L) if (l + 1) % cfg["full_attn_interval"] != 0]
+        n = 8 if which == 4 else reps
+        for vname, env, tune in variants:
+            if tune in (3, 6) and which != 3:
+                continue
+            if env:
+                os.environ["SURGE_GEMV"] = env
+            else:
+                os.environ.pop("SURGE_GEMV", None)
+            for l in layers:
+                gpu.enqueue_gemv(l, which, tune)
+            gpu.sync()
+            ev.record(a, gpu.stream())
+            for _ in range(n):
+                for l in layers:
+                    gpu.enqueue_gemv(l, which, tune)
+            ev.record(b, gpu.stream())
+            us = ev.ms(a, b) * 1e3 / (n * len(layers))
+            print(json.dumps({"shape": name, "variant": vname, "us": round(us, 2), "launches": n * len(layers)}),
+                  flush=True)
+    os.environ.pop("SURGE_GEMV", None)
+    gpu.close()
+    syn.close()
 
 
 def main():
@@ -330,7 +387,10 @@ def main():
                     help="also run one device-to-device copy of this many MiB (counter calibration)")
     ap.add_argument("--micro", action="store_true",
                     help="the per-kernel BASELINE configs instead (GEMV 4096^2, split-K attention at "
-                         "512/4096/32768 keys, the 16-head DeltaNet step): one JSON line each")
+                         "512/4096/32768 keys, the 16-head DeltaNet step, plain-read and empty-launch "
+                         "floors): one JSON line each")
+    ap.add_argument("--gemv-shapes", action="store_true",
+                    help="every 27B decode GEMV shape timed per kernel variant instead: one JSON line each")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {a.gpus}); this build has no "
@@ -338,6 +398,9 @@ def main():
         sys.exit(2)
     if a.micro:
         micro()
+        return
+    if a.gemv_shapes:
+        gemv_shapes()
         return
     cfg = S.CFG_27B if a.shape == "27b" else S.CFG_2B
     log = lambda *x: print("[bench]", *x, file=sys.stderr, flush=True)

@@ -365,6 +365,10 @@ sg_err sg_gpu_state_fill_synthetic(sg_gpu *g, uint32_t n_tokens, uint32_t seed);
  * 2 gate/up, 3 down, 4 lm_head). */
 void *sg_gpu_stream(const sg_gpu *g);
 sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which);
+/* The same with the GEMV's measurement overrides: tune_r rows per wave of
+ * the row-group kernel (1, 2 or 4; 3/5/6 the long-row kernel with 4/6/8
+ * rows per step) and tune_blocks its workgroup count (0: the launch policy). */
+sg_err sg_gpu_enqueue_gemv_tuned(sg_gpu *g, uint32_t layer, uint32_t which, uint32_t tune_r, uint32_t tune_blocks);
 
 /* Timing hooks for the per-kernel micro configs (no reference counterpart).
  * Each runs one product kernel `reps` times back to back and reports the
@@ -384,6 +388,13 @@ sg_err sg_gpu_time_attn(sg_gpu *g, void *q, void *k, void *v, void *out, const u
                         uint64_t rotate_bytes, uint32_t reps, double *us);
 sg_err sg_gpu_time_gdn_step(sg_gpu *g, void *in, void *w, void *out, const uint32_t params[8],
                             uint64_t rotate_bytes, uint32_t reps, double *us);
+/* The floors under every decode kernel (no reference counterpart): a plain
+ * streaming read of `bytes` (multiple of 16) by 1024 workgroups, with the
+ * same input rotation as above; and `reps` empty kernels launched one by one
+ * (graph = 0) or replayed from one captured HIP graph (graph != 0). Average
+ * microseconds per launch. */
+sg_err sg_gpu_time_read(sg_gpu *g, uint64_t bytes, uint64_t rotate_bytes, uint32_t reps, double *us);
+sg_err sg_gpu_time_empty(sg_gpu *g, uint32_t reps, int graph, double *us);
 
 /* ---------------------------------------------------------------------
  * KV cache + DeltaNet state sizing and f16 (surge.h:1410-1501)

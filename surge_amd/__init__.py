@@ -132,6 +132,8 @@ _SIGS = {
                                      C.c_uint32, C.POINTER(C.c_int32)]),
     "sg_gpu_state_fill_synthetic": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32]),
     "sg_gpu_chain_active": (C.c_bool, [C.c_void_p]),
+    "sg_gpu_time_read": (SgErr, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.POINTER(C.c_double)]),
+    "sg_gpu_time_empty": (SgErr, [C.c_void_p, C.c_uint32, C.c_int, C.POINTER(C.c_double)]),
     "sg_gpu_chain_stamps": (SgErr, [C.c_void_p, C.POINTER(C.c_uint64), C.c_uint64, C.POINTER(C.c_uint32),
                                     C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     "sg_gpu_decode_greedy_timed": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32,
@@ -147,6 +149,7 @@ _SIGS = {
     "sg_gpu_used": (C.c_uint32, [C.c_void_p]),
     "sg_gpu_stream": (C.c_void_p, [C.c_void_p]),
     "sg_gpu_enqueue_gemv": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32]),
+    "sg_gpu_enqueue_gemv_tuned": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
     "sg_gpu_time_matvec_q8": (SgErr, [C.c_void_p] * 4 + [C.c_uint32, C.c_uint32, C.c_uint64, C.c_uint32,
                                                           C.POINTER(C.c_double)]),
     "sg_gpu_time_attn": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32), C.c_uint64, C.c_uint32,
@@ -396,6 +399,16 @@ class Gpu:
                                           C.byref(us)))
         return us.value
 
+    def time_read(self, nbytes: int, rotate: int, reps: int) -> float:
+        us = C.c_double()
+        check(lib().sg_gpu_time_read(self.handle, nbytes, rotate, reps, C.byref(us)))
+        return us.value
+
+    def time_empty(self, reps: int, graph: bool) -> float:
+        us = C.c_double()
+        check(lib().sg_gpu_time_empty(self.handle, reps, 1 if graph else 0, C.byref(us)))
+        return us.value
+
     def time_attn(self, q: Buf, k: Buf, v: Buf, out: Buf, p, rotate: int, reps: int):
         us = (C.c_double * 2)()
         check(lib().sg_gpu_time_attn(self.handle, q.handle, k.handle, v.handle, out.handle, params(p), rotate,
@@ -408,8 +421,11 @@ class Gpu:
                                          C.byref(us)))
         return us.value
 
-    def enqueue_gemv(self, layer: int, which: int):
-        check(lib().sg_gpu_enqueue_gemv(self.handle, layer, which))
+    def enqueue_gemv(self, layer: int, which: int, tune_r: int = 0, tune_blocks: int = 0):
+        if tune_r or tune_blocks:
+            check(lib().sg_gpu_enqueue_gemv_tuned(self.handle, layer, which, tune_r, tune_blocks))
+        else:
+            check(lib().sg_gpu_enqueue_gemv(self.handle, layer, which))
 
     def alloc_bytes(self) -> int:
         return lib().sg_gpu_current_alloc_bytes(self.handle)

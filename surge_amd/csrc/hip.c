@@ -1918,6 +1918,10 @@ void *sg_gpu_stream(const sg_gpu *g) { return g ? (void *)g->stream : NULL; }
  * 3 down, 4 lm_head (layer ignored). Used to time one kernel in isolation
  * with events on sg_gpu_stream; it mutates the activation buffers. */
 sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which) {
+    return sg_gpu_enqueue_gemv_tuned(g, layer, which, 0, 0);
+}
+
+sg_err sg_gpu_enqueue_gemv_tuned(sg_gpu *g, uint32_t layer, uint32_t which, uint32_t tune_r, uint32_t tune_blocks) {
     if (!g || !g->have_state) return (sg_err){"gpu: sg_gpu_enqueue_gemv needs a live state"};
     if (which != 4 && layer >= g->cfg.n_layers) return (sg_err){"gpu: layer out of range"};
     const sg_cfg *c = &g->cfg;
@@ -1946,6 +1950,7 @@ sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which) {
         }
     }
     a.qs = M->qs; a.d = M->d; a.wf = M->wf; a.rows = M->rows; a.cols = M->cols;
+    a.tune_r = tune_r; a.tune_blocks = tune_blocks;
     HIPCHK(sgk_gemv_launch(&a, g->stream), "gemv launch");
     return SG_OK;
 }
@@ -1978,6 +1983,66 @@ static sg_err timed(sg_gpu *g, hipEvent_t a, hipEvent_t b, uint32_t reps, double
 
 /* The decode GEMV (k_gemv_q8, no prologue, plain store) on a Q8_0 matrix
  * [rows][cols/32] of 34-byte blocks: y = W x. */
+sg_err sg_gpu_time_read(sg_gpu *g, uint64_t bytes, uint64_t rotate_bytes, uint32_t reps, double *us) {
+    if (!g || !us || !reps || !bytes || bytes % 16) return (sg_err){"gpu: sg_gpu_time_read got an invalid argument"};
+    const uint64_t unit = (bytes + 255) / 256 * 256, n = n_copies(unit, rotate_bytes);
+    char *base;
+    float *out;
+    sg_err e;
+    if (sg_failed(e = dzalloc(g, n * unit, (void **)&base))) return e;
+    const uint32_t blocks = 4 * (uint32_t)sgk_chain_blocks();
+    if (sg_failed(e = dalloc(g, (uint64_t)blocks * 4, (void **)&out))) { dfree(g, base); return e; }
+    hipStream_t s = g->stream;
+    hipEvent_t a = NULL, b = NULL;
+    hipError_t he = hipEventCreate(&a);
+    if (he == hipSuccess) he = hipEventCreate(&b);
+    for (uint32_t r = 0; r < reps + 1 && he == hipSuccess; r++) {     /* launch 0 warms up, untimed */
+        if (r == 1) he = hipEventRecord(a, s);
+        if (he == hipSuccess) he = sgk_read(base + (uint64_t)((r + n - 1) % n) * unit, bytes, out, blocks, s);
+    }
+    if (he == hipSuccess) he = hipEventRecord(b, s);
+    if (he == hipSuccess) e = timed(g, a, b, reps, us);
+    else e = errf("gpu: sg_gpu_time_read: %s", hipGetErrorString(he));
+    hipStreamSynchronize(s);
+    if (a) hipEventDestroy(a);
+    if (b) hipEventDestroy(b);
+    dfree(g, out);
+    dfree(g, base);
+    return e;
+}
+
+sg_err sg_gpu_time_empty(sg_gpu *g, uint32_t reps, int graph, double *us) {
+    if (!g || !us || !reps) return (sg_err){"gpu: sg_gpu_time_empty got an invalid argument"};
+    hipStream_t s = g->stream;
+    hipEvent_t a = NULL, b = NULL;
+    hipGraph_t gr = NULL;
+    hipGraphExec_t ge = NULL;
+    hipError_t he = hipEventCreate(&a);
+    if (he == hipSuccess) he = hipEventCreate(&b);
+    if (he == hipSuccess && graph) {
+        he = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed);
+        for (uint32_t r = 0; r < reps && he == hipSuccess; r++) he = sgk_empty(s);
+        hipError_t ce = hipStreamEndCapture(s, &gr);
+        if (he == hipSuccess) he = ce;
+        if (he == hipSuccess) he = hipGraphInstantiate(&ge, gr, NULL, NULL, 0);
+        if (he == hipSuccess) he = hipGraphLaunch(ge, s);              /* warm-up */
+        if (he == hipSuccess) he = hipEventRecord(a, s);
+        if (he == hipSuccess) he = hipGraphLaunch(ge, s);
+    } else if (he == hipSuccess) {
+        he = sgk_empty(s);
+        if (he == hipSuccess) he = hipEventRecord(a, s);
+        for (uint32_t r = 0; r < reps && he == hipSuccess; r++) he = sgk_empty(s);
+    }
+    if (he == hipSuccess) he = hipEventRecord(b, s);
+    sg_err e = he == hipSuccess ? timed(g, a, b, reps, us) : errf("gpu: sg_gpu_time_empty: %s", hipGetErrorString(he));
+    hipStreamSynchronize(s);
+    if (ge) hipGraphExecDestroy(ge);
+    if (gr) hipGraphDestroy(gr);
+    if (a) hipEventDestroy(a);
+    if (b) hipEventDestroy(b);
+    return e;
+}
+
 sg_err sg_gpu_time_matvec_q8(sg_gpu *g, void *w, void *x, void *y, uint32_t rows, uint32_t cols,
                              uint64_t rotate_bytes, uint32_t reps, double *us) {
     if (!g || !w || !x || !y || !us || !reps || !rows || !cols || cols % 32)

@@ -330,6 +330,12 @@ typedef struct {
 hipError_t sgk_chain_launch(const sgk_chain *a, uint32_t dk, uint32_t dv, hipStream_t s);
 uint32_t sgk_chain_blocks(void);
 
+/* Measurement kernels: a streaming read of `bytes` (a multiple of 16) by
+ * `blocks` workgroups (one float per workgroup written to out), and an empty
+ * kernel. */
+hipError_t sgk_read(const void *p, uint64_t bytes, float *out, uint32_t blocks, hipStream_t s);
+hipError_t sgk_empty(hipStream_t s);
+
 /* The device-resident workspace of the no-allocation entry points: a
  * file-scope device array of SGK_SCRATCH_BYTES in kernels.hip. Call
  * sgk_scratch_init(dev) once per device with that device current; then

@@ -4063,6 +4063,45 @@ extern "C" hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16
 }
 
 // ---------------------------------------------------------------------------
+// Measurement kernels: a plain streaming read (16-byte non-temporal loads, a
+// grid stride over the bytes, one value per workgroup written so the loads
+// are not removed) and an empty kernel; the floor any decode kernel of the
+// same size stands on.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(TPB) k_read(const uint4 *p, uint64_t n16, float *out) {
+    // wave w of the grid reads 4 KB pieces w, w + W, ... (lane l: 16 bytes at
+    // l, l + 64, l + 128, l + 192 of the piece: four loads in flight, one
+    // contiguous stream per wave, as a GEMV wave streams its rows)
+    uint32_t acc = 0;
+    const uint64_t W = (uint64_t)gridDim.x * (TPB / 64), lane = threadIdx.x & 63;
+    const uint64_t n4k = n16 / 256;
+    for (uint64_t w = (uint64_t)blockIdx.x * (TPB / 64) + (threadIdx.x >> 6); w < n4k; w += W) {
+        const uint4 *q = p + w * 256 + lane;
+        const uint4 v0 = ldnt(q), v1 = ldnt(q + 64), v2 = ldnt(q + 128), v3 = ldnt(q + 192);
+        acc ^= (v0.x ^ v0.y ^ v0.z ^ v0.w) ^ (v1.x ^ v1.y ^ v1.z ^ v1.w) ^ (v2.x ^ v2.y ^ v2.z ^ v2.w) ^
+               (v3.x ^ v3.y ^ v3.z ^ v3.w);
+    }
+    for (uint64_t i = n4k * 256 + (uint64_t)blockIdx.x * TPB + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * TPB) {
+        const uint4 v = ldnt(p + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    __shared__ float red[TPB / 64];
+    const float s = block_sum((float)(acc & 0xffu), red);
+    if (threadIdx.x == 0) out[blockIdx.x] = s;
+}
+__global__ void k_empty() {}
+
+extern "C" hipError_t sgk_read(const void *p, uint64_t bytes, float *out, uint32_t blocks, hipStream_t s) {
+    if (!p || bytes % 16 || !blocks) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_read, dim3(blocks), dim3(TPB), 0, s, (const uint4 *)p, bytes / 16, out);
+    return hipGetLastError();
+}
+extern "C" hipError_t sgk_empty(hipStream_t s) {
+    hipLaunchKernelGGL(k_empty, dim3(1), dim3(64), 0, s);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // A device-resident workspace for callers that cannot allocate (code under
 // graph capture, serving loops): the no-allocation entry points place their
 // partials here instead of in memory from hipMalloc. Each GPU holds its own
