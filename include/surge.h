@@ -395,6 +395,14 @@ sg_err sg_gpu_time_gdn_step(sg_gpu *g, void *in, void *w, void *out, const uint3
  * microseconds per launch. */
 sg_err sg_gpu_time_read(sg_gpu *g, uint64_t bytes, uint64_t rotate_bytes, uint32_t reps, double *us);
 sg_err sg_gpu_time_empty(sg_gpu *g, uint32_t reps, int graph, double *us);
+/* The prefill GEMM (no reference counterpart) on one of the loaded model's
+ * weights (which: 0 input projection with its RMSNorm, 1 output projection
+ * += into the residual rows, 2 gate/up with RMSNorm and SwiGLU, 3 down +=)
+ * for a chunk of n tokens of synthetic activations, as the chunked prefill
+ * launches it (split, MFMA tiles, split-K reduce): `reps` back-to-back
+ * products, average microseconds per product. Needs a live state; it
+ * overwrites the state's prefill scratch. */
+sg_err sg_gpu_time_gemm(sg_gpu *g, uint32_t layer, uint32_t which, uint32_t n, uint32_t reps, double *us);
 
 /* ---------------------------------------------------------------------
  * KV cache + DeltaNet state sizing and f16 (surge.h:1410-1501)

@@ -134,6 +134,7 @@ _SIGS = {
     "sg_gpu_chain_active": (C.c_bool, [C.c_void_p]),
     "sg_gpu_time_read": (SgErr, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.POINTER(C.c_double)]),
     "sg_gpu_time_empty": (SgErr, [C.c_void_p, C.c_uint32, C.c_int, C.POINTER(C.c_double)]),
+    "sg_gpu_time_gemm": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double)]),
     "sg_gpu_chain_stamps": (SgErr, [C.c_void_p, C.POINTER(C.c_uint64), C.c_uint64, C.POINTER(C.c_uint32),
                                     C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     "sg_gpu_decode_greedy_timed": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32,
@@ -402,6 +403,13 @@ class Gpu:
     def time_read(self, nbytes: int, rotate: int, reps: int) -> float:
         us = C.c_double()
         check(lib().sg_gpu_time_read(self.handle, nbytes, rotate, reps, C.byref(us)))
+        return us.value
+
+    def time_gemm(self, layer: int, which: int, n: int, reps: int) -> float:
+        """Average microseconds of the prefill GEMM on a loaded weight
+        (which: 0 input, 1 output, 2 gate/up, 3 down) for n tokens."""
+        us = C.c_double()
+        check(lib().sg_gpu_time_gemm(self.handle, layer, which, n, reps, C.byref(us)))
         return us.value
 
     def time_empty(self, reps: int, graph: bool) -> float:

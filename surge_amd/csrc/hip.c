@@ -138,14 +138,15 @@ struct sg_gpu {
     /* decode chain (SURGE_CHAIN=1): the token's stage table, the runs of it
      * one persistent launch covers (an attention layer's partial and combine
      * run as kernels of their own between runs), the buffers its stages write
-     * once per token, the barrier counters and the token epoch */
-    bool chain;
+     * once per token and the barrier counters. SURGE_CHAIN=2 (ch_pairs): only
+     * each DeltaNet layer's step and output projection run as a two-stage
+     * launch, the rest as kernels; ch_seg[k] is the k-th DeltaNet layer's. */
+    bool chain, ch_pairs;
     sgk_cstage *ch_st;
     uint32_t ch_n, ch_nseg;
     struct { uint32_t s0, s1; int32_t attn; float *q; } *ch_seg;
     float *ch_buf;
     uint32_t *ch_cnt, *ch_err;
-    uint32_t ch_epoch;
     uint32_t ch_spin;       /* SURGE_CHAIN_SPIN: polls per barrier wait (tests of the give-up path) */
     uint64_t *ch_stamps;    /* SURGE_CHAIN_STAMPS=1: per stage and workgroup wall-clock stamps */
     uint32_t ch_tune;       /* SURGE_CHAIN_TUNE: ring / prime depth variant (measurement) */
@@ -1094,7 +1095,7 @@ static void state_free(sg_gpu *g) {
     free(g->ch_seg);
     g->ch_seg = NULL;
     g->ch_n = g->ch_nseg = 0;
-    g->chain = false;
+    g->chain = g->ch_pairs = false;
     if (g->g_fwd) hipGraphExecDestroy(g->g_fwd);
     if (g->g_greedy) hipGraphExecDestroy(g->g_greedy);
     g->g_fwd = g->g_greedy = NULL;
@@ -1155,9 +1156,8 @@ static hipError_t enqueue_attn(sg_gpu *g, const glayer *L, float *q) {
 static hipError_t enqueue_chain(sg_gpu *g, bool greedy) {
     const sg_cfg *c = &g->cfg;
     hipError_t e;
-    g->ch_epoch++;
     for (uint32_t k = 0; k < g->ch_nseg; k++) {
-        sgk_chain a = {g->ch_st, g->ch_seg[k].s0, g->ch_seg[k].s1, g->ch_cnt, g->ch_epoch, g->ch_err, g->ch_spin,
+        sgk_chain a = {g->ch_st, g->ch_seg[k].s0, g->ch_seg[k].s1, g->ch_cnt, g->ch_err, g->ch_spin,
                        g->ch_stamps, g->ch_tune};
         if ((e = sgk_chain_launch(&a, c->head_k_dim, c->head_v_dim, g->stream)) != hipSuccess) return e;
         const int32_t al = g->ch_seg[k].attn;
@@ -1180,6 +1180,7 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
     const int8_t *eq = g->emb.qs;
     if ((e = sgk_embed(eq, g->emb.d, g->emb.wf, c->hidden, g->d_step, 0, g->x, s)) != hipSuccess) return e;
     const uint32_t hd = c->head_dim, qs = c->attn_output_gate ? 2 * hd : hd;
+    uint32_t npair = 0;
     for (uint32_t i = 0; i < c->n_layers; i++) {
         glayer *L = &g->ls[i];
         sgk_gemv a = {0};
@@ -1211,6 +1212,13 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             d.tiled = g->model->v_heads_tiled; d.neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
             d.z = g->act + g->conv_dim; d.norm_w = L->ssm_norm; d.out = g->gbuf; d.eps = c->rms_eps;
             d.ss = g->gss; d.blocks = g->gdn_blocks;
+            if (g->ch_pairs) {                /* the step and the output projection in one launch */
+                sgk_chain a = {g->ch_st, g->ch_seg[npair].s0, g->ch_seg[npair].s1, g->ch_cnt, g->ch_err,
+                               g->ch_spin, g->ch_stamps, g->ch_tune ? g->ch_tune : 1};
+                npair++;
+                if ((e = sgk_chain_launch(&a, c->head_k_dim, c->head_v_dim, s)) != hipSuccess) return e;
+                goto ffn;
+            }
             if ((e = sgk_gdn_step(&d, s)) != hipSuccess) return e;
             if (g->gdn_blocks == 1) {
                 o.x = g->gbuf; o.pro = SGK_PRO_NONE;          /* the step finished RMSNormGated */
@@ -1220,6 +1228,7 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             }
         }
         if ((e = sgk_gemv_launch(&o, s)) != hipSuccess) return e;
+    ffn:;
         sgk_gemv f = {0};
         f.qs = L->gu.qs; f.d = L->gu.d; f.wf = L->gu.wf; f.rows = L->gu.rows; f.cols = L->gu.cols;
         f.x = g->x; f.nw = L->ln2; f.eps = c->rms_eps; f.y = g->ffg; f.pro = SGK_PRO_RMS; f.epi = SGK_EPI_SWIGLU;
@@ -1341,31 +1350,73 @@ static sg_err chain_build(sg_gpu *g) {
     free(T);
     if (!sg_failed(e)) e = dzalloc(g, (uint64_t)n * 8 * 64 * 4, (void **)&g->ch_cnt);
     if (!sg_failed(e)) e = dzalloc(g, 256, (void **)&g->ch_err);
-    g->ch_epoch = 0;
+    return e;
+}
+
+/* SURGE_CHAIN=2: per DeltaNet layer a two-stage table run — the step (one
+ * workgroup per value head, RMSNormGated fused, into gbuf) and the output
+ * projection (x += W gbuf, in place: a workgroup reads its residual rows
+ * before it writes them) — so the projection's workgroups request their
+ * weights while the step runs. The other stages stay kernels. */
+static sg_err chain_build_pairs(sg_gpu *g) {
+    const sg_cfg *c = &g->cfg;
+    uint32_t np = 0;
+    for (uint32_t i = 0; i < c->n_layers; i++) np += !g->ls[i].attn;
+    if (!np) return (sg_err){"gpu: SURGE_CHAIN=2 needs DeltaNet layers"};
+    sgk_cstage *T = calloc(2 * (uint64_t)np, sizeof *T);
+    g->ch_seg = calloc(np, sizeof *g->ch_seg);
+    if (!T || !g->ch_seg) { free(T); return (sg_err){"gpu: out of host memory"}; }
+    uint32_t n = 0, k = 0;
+    for (uint32_t i = 0; i < c->n_layers; i++) {
+        glayer *L = &g->ls[i];
+        if (L->attn) continue;
+        g->ch_seg[k].s0 = n; g->ch_seg[k].s1 = n + 2; g->ch_seg[k].attn = (int32_t)i; g->ch_seg[k].q = NULL; k++;
+        sgk_cstage *t = &T[n++];
+        t->kind = SGK_CS_GDN;
+        sgk_gdn *d = &t->gdn;
+        d->in = g->act; d->conv_w = L->conv_w; d->ring = L->ring; d->ssm_a = L->ssm_a; d->dt_bias = L->dt_bias;
+        d->S = L->S; d->y = g->ybuf; d->step = g->d_step; d->n_k = c->n_k_heads; d->n_v = c->n_v_heads;
+        d->dk = c->head_k_dim; d->dv = c->head_v_dim; d->conv_dim = g->conv_dim; d->ksize = c->conv_kernel;
+        d->tiled = g->model->v_heads_tiled; d->neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
+        d->z = g->act + g->conv_dim; d->norm_w = L->ssm_norm; d->out = g->gbuf; d->eps = c->rms_eps;
+        d->ss = g->gss; d->blocks = 1;
+        t = &T[n++];
+        t->kind = SGK_CS_GEMV; t->pro = SGK_PRO_NONE; t->epi = SGK_EPI_ADD; t->rows = L->out.rows;
+        t->cols = L->out.cols; t->qs = L->out.qs; t->d = L->out.d; t->x = g->gbuf; t->nw = NULL; t->res = g->x;
+        t->y = g->x; t->eps = c->rms_eps;
+    }
+    g->ch_n = n;
+    g->ch_nseg = np;
+    sg_err e = SG_OK;
+    if (!sg_failed(e = dalloc(g, (uint64_t)n * sizeof *T, (void **)&g->ch_st)) &&
+        hipMemcpy(g->ch_st, T, (uint64_t)n * sizeof *T, hipMemcpyHostToDevice) != hipSuccess)
+        e = (sg_err){"gpu: chain stage table upload failed"};
+    free(T);
+    if (!sg_failed(e)) e = dzalloc(g, (uint64_t)n * 8 * 64 * 4, (void **)&g->ch_cnt);
+    if (!sg_failed(e)) e = dzalloc(g, 256, (void **)&g->ch_err);
     return e;
 }
 
 /* Whether a chain barrier gave up since the last check (the decode outputs
  * of those steps are invalid); clears the flag and the counters. */
 static sg_err chain_status(sg_gpu *g) {
-    if (!g->chain) return SG_OK;
+    if (!g->chain && !g->ch_pairs) return SG_OK;
     uint32_t v = 0;
     HIPCHK(hipMemcpy(&v, g->ch_err, 4, hipMemcpyDeviceToHost), "chain status");
     if (!v) return SG_OK;
     HIPCHK(hipMemsetAsync(g->ch_cnt, 0, (uint64_t)g->ch_n * 8 * 64 * 4, g->stream), "chain reset");
     HIPCHK(hipMemsetAsync(g->ch_err, 0, 4, g->stream), "chain reset");
     HIPCHK(hipStreamSynchronize(g->stream), "chain reset");
-    g->ch_epoch = 0;
     return (sg_err){"gpu: a decode chain barrier did not resolve; those decode steps' outputs are invalid"};
 }
 
-static bool graphed(const sg_gpu *g) { return g->use_graph && !g->chain; }
+static bool graphed(const sg_gpu *g) { return g->use_graph; }
 
-bool sg_gpu_chain_active(const sg_gpu *g) { return g && g->have_state && g->chain; }
+bool sg_gpu_chain_active(const sg_gpu *g) { return g && g->have_state && (g->chain || g->ch_pairs); }
 
 sg_err sg_gpu_chain_stamps(sg_gpu *g, uint64_t *out, uint64_t cap, uint32_t *n_stages, uint32_t *n_blocks,
                            uint32_t *kinds) {
-    if (!g || !g->have_state || !g->chain || !g->ch_stamps)
+    if (!g || !g->have_state || !(g->chain || g->ch_pairs) || !g->ch_stamps)
         return (sg_err){"gpu: chain stamps need a chain state made with SURGE_CHAIN_STAMPS=1"};
     const uint32_t nb = sgk_chain_blocks();
     const uint64_t n = (uint64_t)g->ch_n * nb * 3;
@@ -1525,18 +1576,26 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
      * of stages) when the model allows it; 0 (default): one kernel per stage. */
     {
         const char *ce = getenv("SURGE_CHAIN");
-        if (ce && ce[0] && strcmp(ce, "0") != 0 && strcmp(ce, "1") != 0)
-            fprintf(stderr, "gpu: SURGE_CHAIN='%s' not recognized (want 0 or 1); using 0\n", ce);
+        if (ce && ce[0] && strcmp(ce, "0") != 0 && strcmp(ce, "1") != 0 && strcmp(ce, "2") != 0)
+            fprintf(stderr, "gpu: SURGE_CHAIN='%s' not recognized (want 0, 1 or 2); using 0\n", ce);
         if (!sg_failed(e) && ce && strcmp(ce, "1") == 0 && chain_eligible(g)) {
             e = chain_build(g);
             g->chain = !sg_failed(e);
+        }
+        if (!sg_failed(e) && ce && strcmp(ce, "2") == 0 && chain_eligible(g)) {
+            bool gdn = false;
+            for (uint32_t i = 0; i < c->n_layers; i++) gdn |= !g->ls[i].attn;
+            if (gdn) {
+                e = chain_build_pairs(g);
+                g->ch_pairs = !sg_failed(e);
+            }
         }
         const char *sp = getenv("SURGE_CHAIN_SPIN");
         g->ch_spin = sp && *sp ? (uint32_t)strtoul(sp, NULL, 10) : 0;
         const char *tu = getenv("SURGE_CHAIN_TUNE");
         g->ch_tune = tu && *tu ? (uint32_t)strtoul(tu, NULL, 10) : 0;
         const char *ss = getenv("SURGE_CHAIN_STAMPS");
-        if (!sg_failed(e) && g->chain && ss && !strcmp(ss, "1"))
+        if (!sg_failed(e) && (g->chain || g->ch_pairs) && ss && !strcmp(ss, "1"))
             e = dzalloc(g, (uint64_t)g->ch_n * sgk_chain_blocks() * 3 * 8, (void **)&g->ch_stamps);
     }
     if (!sg_failed(e) && graphed(g)) {
@@ -1557,10 +1616,9 @@ void sg_gpu_state_reset(sg_gpu *g) {
         if (L->ring) sgk_fill_f32(L->ring, 0.0f, (uint64_t)4 * g->conv_dim, g->stream);
         if (L->S) sgk_fill_f32(L->S, 0.0f, (uint64_t)c->n_v_heads * c->head_v_dim * c->head_k_dim, g->stream);
     }
-    if (g->chain) {
+    if (g->chain || g->ch_pairs) {
         hipMemsetAsync(g->ch_cnt, 0, (uint64_t)g->ch_n * 8 * 64 * 4, g->stream);
         hipMemsetAsync(g->ch_err, 0, 4, g->stream);
-        g->ch_epoch = 0;
     }
     hipStreamSynchronize(g->stream);
     g->used = 0;
@@ -1803,6 +1861,43 @@ static hipError_t gemm_rows_norm(sg_gpu *g, const dmat *M, const float *X, const
     sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, H, ldy, epi, g->pf_XS, g->pf_PART,
                         (uint64_t)4 * g->pf_chunk * H, nw, g->cfg.rms_eps };
     return sgk_gemm(&a, g->stream);
+}
+
+static sg_err timed(sg_gpu *g, hipEvent_t a, hipEvent_t b, uint32_t reps, double *us);
+
+sg_err sg_gpu_time_gemm(sg_gpu *g, uint32_t layer, uint32_t which, uint32_t n, uint32_t reps, double *us) {
+    if (!g || !g->have_state || !us || !reps || !n) return (sg_err){"gpu: sg_gpu_time_gemm got an invalid argument"};
+    const sg_cfg *c = &g->cfg;
+    if (layer >= c->n_layers || which > 3) return (sg_err){"gpu: sg_gpu_time_gemm: layer or which out of range"};
+    sg_err e = prefill_alloc(g, n);
+    if (sg_failed(e)) return e;
+    hipStream_t s = g->stream;
+    const glayer *L = &g->ls[layer];
+    const uint32_t H = c->hidden, ow = L->attn ? g->attn_width : g->value_dim;
+    float *ox = L->attn ? g->pf_CTX : g->pf_Y;          /* the output projection's input rows */
+    hipError_t he = sgk_fill_hash(g->pf_X, (uint64_t)n * H, 0, 11, 1.0f, s);
+    if (he == hipSuccess) he = sgk_fill_hash(g->pf_FF, (uint64_t)n * c->ffn_hidden, 0, 12, 1.0f, s);
+    if (he == hipSuccess) he = sgk_fill_hash(ox, (uint64_t)n * ow, 0, 13, 1.0f, s);
+    hipEvent_t a = NULL, b = NULL;
+    if (he == hipSuccess) he = hipEventCreate(&a);
+    if (he == hipSuccess) he = hipEventCreate(&b);
+    for (uint32_t r = 0; r < reps + 1 && he == hipSuccess; r++) {      /* product 0 warms up, untimed */
+        if (r == 1) he = hipEventRecord(a, s);
+        if (he != hipSuccess) break;
+        switch (which) {
+        case 0: he = gemm_rows_norm(g, &L->in, g->pf_X, L->ln1, g->pf_IN, L->in.rows, n, SGK_EPI_STORE); break;
+        case 1: he = gemm_rows(g, &L->out, ox, ow, g->pf_X, H, n, SGK_EPI_ADD); break;
+        case 2: he = gemm_rows_norm(g, &L->gu, g->pf_X, L->ln2, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU); break;
+        default: he = gemm_rows(g, &L->down, g->pf_FF, c->ffn_hidden, g->pf_X, H, n, SGK_EPI_ADD); break;
+        }
+    }
+    if (he == hipSuccess) he = hipEventRecord(b, s);
+    if (he == hipSuccess) e = timed(g, a, b, reps, us);
+    else e = errf("gpu: sg_gpu_time_gemm: %s", hipGetErrorString(he));
+    hipStreamSynchronize(s);
+    if (a) hipEventDestroy(a);
+    if (b) hipEventDestroy(b);
+    return e;
 }
 
 /* One chunk of n tokens at positions base..base+n-1 through every layer. */

@@ -284,10 +284,11 @@ hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, floa
  * barrier between stages instead of a kernel boundary; every GEMV's first
  * weight rows are requested before the barrier that precedes it. Stage
  * outputs are published with device-scope (write-through) stores into
- * buffers written once per token; `epoch` is the token's number (1, 2, ...),
- * against which the arrival counters `cnt` (zeroed with the state, never
- * reset between tokens) are compared. A barrier that does not resolve within
- * a bounded number of polls sets *err and the launch runs to its end. */
+ * buffers written once per token. The arrival counters `cnt` are zeroed with
+ * the state and only grow: a workgroup learns from its own arrival which
+ * launch of the stage it is in, so launches replay from a captured graph. A
+ * barrier that does not resolve within a bounded number of polls sets *err
+ * and the launch runs to its end. */
 enum { SGK_CS_GEMV = 1, SGK_CS_GDN = 2, SGK_CS_EMBED = 3 };
 #define SGK_CHAIN_LDS (96u * 1024u)          /* dynamic LDS: one workgroup per CU */
 #define SGK_CHAIN_MAX_COLS 18432u            /* GEMV columns (a multiple of 1024) */
@@ -318,7 +319,6 @@ typedef struct {
     const sgk_cstage *st;       /* device stage table */
     uint32_t s0, s1;
     uint32_t *cnt;              /* [n_stages][8 XCDs][64] arrival counters */
-    uint32_t epoch;
     uint32_t *err;
     uint32_t spin;              /* polls a wait makes before giving up (0: the default bound) */
     uint64_t *stamps;           /* NULL, or [n_stages][workgroups][3] device wall-clock stamps per

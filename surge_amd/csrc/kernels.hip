@@ -3456,16 +3456,19 @@ extern "C" hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream
 // weight), W in the Q8 device layout, on MFMA.
 //
 // Precision: x is split once per GEMM into bf16 hi + lo (k_split_bf16; x =
-// hi + lo to ~2^-18); each weight w = d*q is exact in fp32 (an f16 scale times
-// an int8 has at most 18 significant bits) and is split the same way when its
-// tile is staged. A product is xh*wh + xh*wl + xl*wh (xl*wl, ~2^-18 of it, is
-// dropped): three v_mfma_f32_16x16x32_bf16 accumulating straight into the
-// fp32 output tile, so no per-block arithmetic sits between MFMAs.
+// hi + lo to ~2^-18). An int8 weight q is exact in bf16, so a Q8_0 block
+// (32 columns: one K step of v_mfma_f32_16x16x32_bf16) of a weight row costs
+// two MFMAs, xh*q then xl*q into one fp32 partial started at zero, and the
+// row's block scale d is applied to that partial on the VALU:
+// acc = fma(d, partial, acc). Against the dequantised form (w = d*q split
+// into bf16 hi + lo, three MFMAs: xh*wh + xh*wl + xl*wh) this is a third
+// fewer MFMAs, a third less LDS per weight tile (q in bf16 instead of w's hi
+// and lo), no dequantisation, and no dropped xl*wl term.
 //
 // Tiling: workgroup 256 threads = 4 waves over a 128-token x 128-row tile
 // (waves 2 x 2, each 64 x 64 = 4 x 4 MFMA tiles of 16x16), K in steps of one
-// Q8_0 block (32). Per step the X hi|lo tile and the dequantised W hi|lo tile
-// (2 x 10 KB each) are double-buffered in LDS: X is requested one step ahead,
+// Q8_0 block (32). Per step the X hi|lo tile, the W tile (q as bf16) and the
+// tile rows' block scales are double-buffered in LDS: X is requested one step ahead,
 // the raw weights two steps ahead (two register sets), and the next step's
 // tiles are stored after the current step's MFMAs, one barrier per step.
 // XCD-aware order: workgroup b runs on XCD b % 8, which owns weight tiles
@@ -3540,47 +3543,66 @@ __device__ __forceinline__ uint32_t gm_at(uint32_t row, uint32_t c) {
     return row * GM_LD + ((c ^ ((row >> 1) & 3)) << 3);
 }
 
-// 16 int8 weights of one row and its block scale -> 16 bf16 hi and 16 bf16 lo
-// of w = d*q, the first 8 of each stored at element offset o0 of h and l,
-// the last 8 at o1.
-__device__ __forceinline__ void gm_dequant16(v4u q, uint32_t dbits, uint16_t *h, uint16_t *l, uint32_t o0,
-                                             uint32_t o1) {
-    // w = d*q as fma(d, q + 128, -128 d): one rounding of the exact d*q, so
-    // the bits of d*q, from an unsigned byte conversion (q ^ 0x80 = q + 128)
-    const float dd = h2f((uint16_t)dbits), off = -128.0f * dd;
-    uint32_t oh[8], ol[8];
+// 16 int8 weights of one row -> 16 bf16, exact (|q| <= 127 has at most 7
+// significant bits, so the f32 of q has a zero low half and its high half is
+// the bf16); the first 8 stored at element offset o0 of wq, the last 8 at o1.
+__device__ __forceinline__ void gm_stage_q16(v4u q, uint16_t *wq, uint32_t o0, uint32_t o1) {
+    uint32_t o[8];
 #pragma unroll
     for (int p = 0; p < 8; p++) {
-        const uint32_t u = (q[p >> 1] ^ 0x80808080u) >> (16 * (p & 1));
-        const float w0 = fmaf(dd, (float)(u & 0xffu), off), w1 = fmaf(dd, (float)((u >> 8) & 0xffu), off);
-        const bf16x2 hh = {(__bf16)w0, (__bf16)w1};
-        const uint32_t hb = __builtin_bit_cast(uint32_t, hh);
-        // hi as f32: hb << 16 (as a byte permute, so it reuses the packed
-        // conversion instead of converting w0 again) and hb with its low half cleared
-        const float h0 = __uint_as_float(__builtin_amdgcn_perm(0u, hb, 0x01000c0cu));
-        const float h1 = __uint_as_float(hb & 0xffff0000u);
-        const bf16x2 ll = {(__bf16)(w0 - h0), (__bf16)(w1 - h1)};
-        oh[p] = hb;
-        ol[p] = __builtin_bit_cast(uint32_t, ll);
+        const uint32_t u = q[p >> 1] >> (16 * (p & 1));
+        const float f0 = (float)(int32_t)(int8_t)(u & 0xffu), f1 = (float)(int32_t)(int8_t)((u >> 8) & 0xffu);
+        // bf16 pair (element 2p low, 2p+1 high): the high halves of f0 and f1
+        o[p] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
     }
-    *(v4u *)(h + o0) = (v4u){oh[0], oh[1], oh[2], oh[3]};
-    *(v4u *)(h + o1) = (v4u){oh[4], oh[5], oh[6], oh[7]};
-    *(v4u *)(l + o0) = (v4u){ol[0], ol[1], ol[2], ol[3]};
-    *(v4u *)(l + o1) = (v4u){ol[4], ol[5], ol[6], ol[7]};
+    *(v4u *)(wq + o0) = (v4u){o[0], o[1], o[2], o[3]};
+    *(v4u *)(wq + o1) = (v4u){o[4], o[5], o[6], o[7]};
+}
+
+// One token tile of a K step: for each of the wave's 4 weight tiles the
+// block's partial xh*q + xl*q (two MFMAs from zero), then acc += d * partial
+// with the weight row's block scale (lane j holds column j of a tile, so one
+// scale per lane and tile). Every kernel of the prefill GEMM calls this per
+// (step, token tile) in the same order, so they give the same bits.
+__device__ __forceinline__ void gm_tile_step(f32x4 (&acc)[4], const bf16x8 &ah, const bf16x8 &al,
+                                             const bf16x8 (&bq)[4], const float (&dv)[4]) {
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 p[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) p[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bq[c], z, 0, 0, 0);
+#pragma unroll
+    for (int c = 0; c < 4; c++) p[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bq[c], p[c], 0, 0, 0);
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[c][e] = fmaf(dv[c], p[c][e], acc[c][e]);
+}
+
+// The wave's weight fragments (rows wm*64 + 16c + li) and block scales of
+// LDS buffer cb.
+__device__ __forceinline__ void gm_wfrag(bf16x8 (&bq)[4], float (&dv)[4], const uint16_t *wq, const float *wd,
+                                         uint32_t wm, uint32_t li, uint32_t lg) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t row = wm * 64 + c * 16 + li;
+        bq[c] = *(const bf16x8 *)&wq[gm_at(row, lg)];
+        dv[c] = wd[row];
+    }
 }
 
 // One K step (Q8_0 block s) of the prefill GEMM on LDS buffer cb: request the
 // next block's X and, into the register set this step frees, the raw weights
-// of block s+2; the MFMAs; then stage block s+1 (X from xr, W dequantised from
-// the other register set wn) into buffer cb^1. Blocks at or past kend (the
-// end of this workgroup's K range) only request (clamped) and stage; their
-// MFMAs are skipped.
+// of block s+2; the MFMAs; then stage block s+1 (X from xr, q and the scale
+// from the other register set wn) into buffer cb^1. Blocks at or past kend
+// (the end of this workgroup's K range) only request (clamped) and stage;
+// their MFMAs are skipped.
 __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &wself, uint32_t &dself,
                                         const v4u &wnext, const uint32_t &dnext,
-                                        uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wt)[2][2][GM_TM * GM_LD],
-                                        uint32_t cb, const v4u *xhr, const v4u *xlr, const v4u *wrow,
-                                        const uint16_t *drow, uint32_t s, uint32_t kend, uint32_t so0,
-                                        uint32_t so1, uint32_t wn, uint32_t wm, uint32_t li, uint32_t lg) {
+                                        uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wq)[2][GM_TM * GM_LD],
+                                        float (&wd)[2][GM_TM], uint32_t cb, const v4u *xhr, const v4u *xlr,
+                                        const v4u *wrow, const uint16_t *drow, uint32_t s, uint32_t kend,
+                                        uint32_t so0, uint32_t so1, uint32_t sr, bool sd, uint32_t wn,
+                                        uint32_t wm, uint32_t li, uint32_t lg) {
     const uint32_t s1 = min(s + 1, kend - 1), s2 = min(s + 2, kend - 1);
 #pragma unroll
     for (int u = 0; u < 2; u++) { xr[u] = xhr[s1 * 4 + u]; xr[2 + u] = xlr[s1 * 4 + u]; }
@@ -3588,15 +3610,10 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
     wself = wrow[s2 * 2];
     dself = drow[s2];
     if (s < kend) {
-        // all fragments first, then the three products over all 16 tiles in
-        // turn, so an accumulator's next MFMA comes 16 MFMAs after its last
-        bf16x8 bh[4], bl[4], ah[4], al[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint32_t row = wm * 64 + c * 16 + li;
-            bh[c] = *(const bf16x8 *)&wt[cb][0][gm_at(row, lg)];
-            bl[c] = *(const bf16x8 *)&wt[cb][1][gm_at(row, lg)];
-        }
+        bf16x8 bq[4];
+        float dv[4];
+        gm_wfrag(bq, dv, wq[cb], wd[cb], wm, li, lg);
+        bf16x8 ah[4], al[4];
 #pragma unroll
         for (int a = 0; a < 4; a++) {
             const uint32_t row = wn * 64 + a * 16 + li;
@@ -3604,19 +3621,10 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
             al[a] = *(const bf16x8 *)&xt[cb][1][gm_at(row, lg)];
         }
 #pragma unroll
-        for (int a = 0; a < 4; a++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[a], bh[c], acc[a][c], 0, 0, 0);
-#pragma unroll
-        for (int a = 0; a < 4; a++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[a], bl[c], acc[a][c], 0, 0, 0);
-#pragma unroll
-        for (int a = 0; a < 4; a++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[a], bh[c], acc[a][c], 0, 0, 0);
+        for (int a = 0; a < 4; a++) gm_tile_step(acc[a], ah[a], al[a], bq, dv);
     }
-    gm_dequant16(wnext, dnext, wt[cb ^ 1][0], wt[cb ^ 1][1], so0, so1);
+    gm_stage_q16(wnext, wq[cb ^ 1], so0, so1);
+    if (sd) wd[cb ^ 1][sr] = h2f((uint16_t)dnext);
     *(v4u *)&xt[cb ^ 1][0][so0] = xr[0];
     *(v4u *)&xt[cb ^ 1][0][so1] = xr[1];
     *(v4u *)&xt[cb ^ 1][1][so0] = xr[2];
@@ -3646,7 +3654,8 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
 k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, uint32_t N, uint32_t M,
                uint32_t K, uint32_t ldy, uint64_t ysplit, uint32_t boff) {
     __shared__ __align__(16) uint16_t xt[2][2][GM_TN * GM_LD];     // [buffer][hi | lo][token][k]
-    __shared__ __align__(16) uint16_t wt[2][2][GM_TM * GM_LD];     // [buffer][hi | lo][row][k]
+    __shared__ __align__(16) uint16_t wq[2][GM_TM * GM_LD];        // [buffer][row][k]: q as bf16
+    __shared__ float wd[2][GM_TM];                                 // [buffer][row]: block scale
     const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
     uint32_t mt_id, nt_id;
     if (!gm_tile(blockIdx.x + boff, mb, nb, mt_id, nt_id)) return;
@@ -3659,8 +3668,10 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     const uint32_t kb1 = (uint32_t)((uint64_t)nblk * (blockIdx.y + 1) / gridDim.y);
     Y += (size_t)blockIdx.y * ysplit;
     // staging role: row t/2 of both tiles, k 16*(t%2) .. +15 of each block
-    // (LDS chunks 2*(t%2) and 2*(t%2)+1 of the row)
+    // (LDS chunks 2*(t%2) and 2*(t%2)+1 of the row); the even thread of a row
+    // stages its scale
     const uint32_t sr = t >> 1, sk = (t & 1) * 16, so0 = gm_at(sr, sk / 8), so1 = gm_at(sr, sk / 8 + 1);
+    const bool sd = !(t & 1);
     const size_t xrow = (size_t)min(n0 + sr, N - 1) * K + sk;
     const v4u *xhr = (const v4u *)(xs + xrow), *xlr = (const v4u *)(xs + (size_t)N * K + xrow);
     const uint32_t wrow_i = min(m0 + sr, M - 1);
@@ -3682,7 +3693,8 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     dA = drow[kb0];
     wB = wrow[min(kb0 + 1, kb1 - 1) * 2];
     dB = drow[min(kb0 + 1, kb1 - 1)];
-    gm_dequant16(wA, dA, wt[0][0], wt[0][1], so0, so1);
+    gm_stage_q16(wA, wq[0], so0, so1);
+    if (sd) wd[0][sr] = h2f((uint16_t)dA);
     *(v4u *)&xt[0][0][so0] = xr[0];
     *(v4u *)&xt[0][0][so1] = xr[1];
     *(v4u *)&xt[0][1][so0] = xr[2];
@@ -3691,8 +3703,9 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     // step s uses buffer s%2; its register set (A for even s) is reloaded with
     // block s+2 while the other set (holding block s+1) is staged
     for (uint32_t s = kb0; s < kb1; s += 2) {
-        gm_step(acc, xr, wA, dA, wB, dB, xt, wt, 0, xhr, xlr, wrow, drow, s, kb1, so0, so1, wn, wm, li, lg);
-        gm_step(acc, xr, wB, dB, wA, dA, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, kb1, so0, so1, wn, wm, li, lg);
+        gm_step(acc, xr, wA, dA, wB, dB, xt, wq, wd, 0, xhr, xlr, wrow, drow, s, kb1, so0, so1, sr, sd, wn, wm, li, lg);
+        gm_step(acc, xr, wB, dB, wA, dA, xt, wq, wd, 1, xhr, xlr, wrow, drow, s + 1, kb1, so0, so1, sr, sd, wn, wm, li,
+                lg);
     }
     // epilogue: lane holds D[i = 4*lg + e][j = li] of each tile
     float *Yt = Y + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (GM_TN * GM_TM);
@@ -3717,12 +3730,13 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
             }
 }
 
-// Warp-specialised form of k_gemm_q8_mfma: one 512-thread workgroup per CU
-// and the same 128x128 tile, fragments, MFMA order and dequantisation, so the
-// same bits. Waves 0-3 (consumers) own the accumulators and, in K step s,
-// only read fragments of LDS buffer s%2 and issue MFMAs; waves 4-7
-// (producers) meanwhile dequantise block s+1's weights and stage them and its
-// X into buffer (s+1)%2. One barrier per step, so one group's MFMAs overlap
+// Warp-specialised form of k_gemm_q8_mfma: 512-thread workgroups (two per
+// CU) and the same 128x128 tile, fragments and per-step arithmetic
+// (gm_tile_step), so the same bits. Waves 0-3 (consumers) own the
+// accumulators and, in K step s, only read fragments of LDS buffer s%2 and
+// issue the MFMAs and scale FMAs; waves 4-7 (producers) meanwhile convert
+// block s+1's weights to bf16 and stage them, their scales and its X into
+// buffer (s+1)%2. One barrier per step, so one group's MFMAs overlap
 // the other's VALU and LDS work on every SIMD. A step is short, so the
 // producers keep four register sets: block b's X and raw weights sit in set
 // (b - kb0) % 4, both requested three steps before they are staged.
@@ -3746,9 +3760,10 @@ __device__ __forceinline__ void gw_request_w(gw_set &st, const v4u *wrow, const 
     st.d = drow[blk];
 }
 __device__ __forceinline__ void gw_stage(const gw_set &st, uint16_t (&xt)[2][GM_TN * GM_LD],
-                                         uint16_t (&wt)[2][GM_TM * GM_LD], uint32_t so0, uint32_t so1,
-                                         uint32_t xo0, uint32_t xo1) {
-    gm_dequant16(st.w, st.d, wt[0], wt[1], so0, so1);
+                                         uint16_t (&wq)[GM_TM * GM_LD], float (&wd)[GM_TM], uint32_t so0,
+                                         uint32_t so1, uint32_t sr, bool sd, uint32_t xo0, uint32_t xo1) {
+    gm_stage_q16(st.w, wq, so0, so1);
+    if (sd) wd[sr] = h2f((uint16_t)st.d);
     *(v4u *)&xt[0][xo0] = st.x[0];
     *(v4u *)&xt[0][xo1] = st.x[1];
     *(v4u *)&xt[1][xo0] = st.x[2];
@@ -3757,55 +3772,34 @@ __device__ __forceinline__ void gw_stage(const gw_set &st, uint16_t (&xt)[2][GM_
 // Producer step s: request X and weights of block s+3 into set rq (free:
 // block s-1 was staged in step s-2), stage block s+1 (set st) into cb^1.
 __device__ __forceinline__ void gw_produce(gw_set &rq, const gw_set &st,
-                                           uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wt)[2][2][GM_TM * GM_LD],
-                                           uint32_t cb, const v4u *xhr, const v4u *xlr, const v4u *wrow,
-                                           const uint16_t *drow, uint32_t s, uint32_t kend, uint32_t so0,
-                                           uint32_t so1, uint32_t xo0, uint32_t xo1, uint32_t r64) {
+                                           uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wq)[2][GM_TM * GM_LD],
+                                           float (&wd)[2][GM_TM], uint32_t cb, const v4u *xhr, const v4u *xlr,
+                                           const v4u *wrow, const uint16_t *drow, uint32_t s, uint32_t kend,
+                                           uint32_t so0, uint32_t so1, uint32_t sr, bool sd, uint32_t xo0,
+                                           uint32_t xo1, uint32_t r64) {
     gw_request_x(rq, xhr, xlr, min(s + 3, kend - 1), r64);
     gw_request_w(rq, wrow, drow, min(s + 3, kend - 1));
     __builtin_amdgcn_sched_barrier(0);
-    gw_stage(st, xt[cb ^ 1], wt[cb ^ 1], so0, so1, xo0, xo1);
+    gw_stage(st, xt[cb ^ 1], wq[cb ^ 1], wd[cb ^ 1], so0, so1, sr, sd, xo0, xo1);
     __syncthreads();
 }
-// Consumer step s: the fragments of buffer cb and the MFMAs (none past kend).
-// The X fragments are read two token tiles at a time (register room for two
-// workgroups per CU); each accumulator still takes its three products in the
-// same order, so the result bits do not change.
+// Consumer step s: the fragments of buffer cb, the MFMAs and scale FMAs (none
+// past kend). X fragments are read one token tile at a time (register room
+// for two workgroups per CU).
 __device__ __forceinline__ void gw_consume(f32x4 (&acc)[4][4], uint16_t (&xt)[2][2][GM_TN * GM_LD],
-                                           uint16_t (&wt)[2][2][GM_TM * GM_LD], uint32_t cb, uint32_t s,
-                                           uint32_t kend, uint32_t wn, uint32_t wm, uint32_t li, uint32_t lg) {
+                                           uint16_t (&wq)[2][GM_TM * GM_LD], float (&wd)[2][GM_TM], uint32_t cb,
+                                           uint32_t s, uint32_t kend, uint32_t wn, uint32_t wm, uint32_t li,
+                                           uint32_t lg) {
     if (s < kend) {
-        bf16x8 bh[4], bl[4];
+        bf16x8 bq[4];
+        float dv[4];
+        gm_wfrag(bq, dv, wq[cb], wd[cb], wm, li, lg);
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint32_t row = wm * 64 + c * 16 + li;
-            bh[c] = *(const bf16x8 *)&wt[cb][0][gm_at(row, lg)];
-            bl[c] = *(const bf16x8 *)&wt[cb][1][gm_at(row, lg)];
-        }
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            bf16x8 ah[2], al[2];
-#pragma unroll
-            for (int a = 0; a < 2; a++) {
-                const uint32_t row = wn * 64 + (2 * h + a) * 16 + li;
-                ah[a] = *(const bf16x8 *)&xt[cb][0][gm_at(row, lg)];
-                al[a] = *(const bf16x8 *)&xt[cb][1][gm_at(row, lg)];
-            }
-#pragma unroll
-            for (int a = 0; a < 2; a++)
-#pragma unroll
-                for (int c = 0; c < 4; c++)
-                    acc[2 * h + a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[a], bh[c], acc[2 * h + a][c], 0, 0, 0);
-#pragma unroll
-            for (int a = 0; a < 2; a++)
-#pragma unroll
-                for (int c = 0; c < 4; c++)
-                    acc[2 * h + a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[a], bl[c], acc[2 * h + a][c], 0, 0, 0);
-#pragma unroll
-            for (int a = 0; a < 2; a++)
-#pragma unroll
-                for (int c = 0; c < 4; c++)
-                    acc[2 * h + a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[a], bh[c], acc[2 * h + a][c], 0, 0, 0);
+        for (int a = 0; a < 4; a++) {
+            const uint32_t row = wn * 64 + a * 16 + li;
+            const bf16x8 ah = *(const bf16x8 *)&xt[cb][0][gm_at(row, lg)];
+            const bf16x8 al = *(const bf16x8 *)&xt[cb][1][gm_at(row, lg)];
+            gm_tile_step(acc[a], ah, al, bq, dv);
         }
     }
     __syncthreads();
@@ -3816,7 +3810,8 @@ __global__ void __launch_bounds__(GW_TPB) __attribute__((amdgpu_waves_per_eu(4, 
 k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, uint32_t N, uint32_t M,
              uint32_t K, uint32_t ldy, uint64_t ysplit, uint32_t boff) {
     __shared__ __align__(16) uint16_t xt[2][2][GM_TN * GM_LD];     // [buffer][hi | lo][token][k]
-    __shared__ __align__(16) uint16_t wt[2][2][GM_TM * GM_LD];     // [buffer][hi | lo][row][k]
+    __shared__ __align__(16) uint16_t wq[2][GM_TM * GM_LD];        // [buffer][row][k]: q as bf16
+    __shared__ float wd[2][GM_TM];                                 // [buffer][row]: block scale
     const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
     uint32_t mt_id, nt_id;
     if (!gm_tile(blockIdx.x + boff, mb, nb, mt_id, nt_id)) return;
@@ -3832,6 +3827,7 @@ k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, 
         // block (LDS chunks 2*(p%2), +1); X chunk p%4 of token rows p/4, p/4+64
         const uint32_t pt = t - 256, sr = pt >> 1, sk = (pt & 1) * 16;
         const uint32_t so0 = gm_at(sr, sk / 8), so1 = gm_at(sr, sk / 8 + 1);
+        const bool sd = !(pt & 1);
         const uint32_t xr0 = pt >> 2, xc = pt & 3;
         const uint32_t xo0 = gm_at(xr0, xc), xo1 = gm_at(xr0 + 64, xc);
         const uint32_t xn0 = min(n0 + xr0, N - 1), xn1 = min(n0 + xr0 + 64, N - 1);
@@ -3852,13 +3848,13 @@ k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, 
         gw_request_x(g2, xhr, xlr, min(kb0 + 2, kl), r64);
         gw_request_w(g2, wrow, drow, min(kb0 + 2, kl));
         __builtin_amdgcn_sched_barrier(0);
-        gw_stage(g0, xt[0], wt[0], so0, so1, xo0, xo1);
+        gw_stage(g0, xt[0], wq[0], wd[0], so0, so1, sr, sd, xo0, xo1);
         __syncthreads();
         for (uint32_t s = kb0; s < kb1; s += 4) {
-            gw_produce(g3, g1, xt, wt, 0, xhr, xlr, wrow, drow, s, kb1, so0, so1, xo0, xo1, r64);
-            gw_produce(g0, g2, xt, wt, 1, xhr, xlr, wrow, drow, s + 1, kb1, so0, so1, xo0, xo1, r64);
-            gw_produce(g1, g3, xt, wt, 0, xhr, xlr, wrow, drow, s + 2, kb1, so0, so1, xo0, xo1, r64);
-            gw_produce(g2, g0, xt, wt, 1, xhr, xlr, wrow, drow, s + 3, kb1, so0, so1, xo0, xo1, r64);
+            gw_produce(g3, g1, xt, wq, wd, 0, xhr, xlr, wrow, drow, s, kb1, so0, so1, sr, sd, xo0, xo1, r64);
+            gw_produce(g0, g2, xt, wq, wd, 1, xhr, xlr, wrow, drow, s + 1, kb1, so0, so1, sr, sd, xo0, xo1, r64);
+            gw_produce(g1, g3, xt, wq, wd, 0, xhr, xlr, wrow, drow, s + 2, kb1, so0, so1, sr, sd, xo0, xo1, r64);
+            gw_produce(g2, g0, xt, wq, wd, 1, xhr, xlr, wrow, drow, s + 3, kb1, so0, so1, sr, sd, xo0, xo1, r64);
         }
         return;
     }
@@ -3872,10 +3868,10 @@ k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, 
         for (int c = 0; c < 4; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
     __syncthreads();
     for (uint32_t s = kb0; s < kb1; s += 4) {
-        gw_consume(acc, xt, wt, 0, s, kb1, wn, wm, li, lg);
-        gw_consume(acc, xt, wt, 1, s + 1, kb1, wn, wm, li, lg);
-        gw_consume(acc, xt, wt, 0, s + 2, kb1, wn, wm, li, lg);
-        gw_consume(acc, xt, wt, 1, s + 3, kb1, wn, wm, li, lg);
+        gw_consume(acc, xt, wq, wd, 0, s, kb1, wn, wm, li, lg);
+        gw_consume(acc, xt, wq, wd, 1, s + 1, kb1, wn, wm, li, lg);
+        gw_consume(acc, xt, wq, wd, 0, s + 2, kb1, wn, wm, li, lg);
+        gw_consume(acc, xt, wq, wd, 1, s + 3, kb1, wn, wm, li, lg);
     }
     // epilogue (consumers): lane holds D[i = 4*lg + e][j = li] of each tile
     float *Yt = Y + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (GM_TN * GM_TM);
@@ -4182,26 +4178,37 @@ __device__ __forceinline__ void ch_stamp(const sgk_chain &a, uint32_t st, uint32
     if (a.stamps && threadIdx.x == 0) a.stamps[((size_t)st * gridDim.x + blockIdx.x) * 3 + k] = wall_clock64();
 }
 
+// Workgroups of the grid that add to counter x of a stage.
+__device__ __forceinline__ uint32_t ch_share(uint32_t x) { return (gridDim.x + CH_XCDS - 1 - x) / CH_XCDS; }
+
 // Arrival at stage st: this workgroup's stores are complete, then one add.
-__device__ __forceinline__ void ch_arrive(const sgk_chain &a, uint32_t st) {
+// Returns, in thread 0, which launch of the stage this is (0, 1, ...): a
+// stage's counters only grow, each launch adds ch_share(x) to counter x, and
+// launches of one stage run one after another, so the value before the add
+// tells the round. No per-token number comes from the host, so the launches
+// replay unchanged from a captured graph.
+__device__ __forceinline__ uint32_t ch_arrive(const sgk_chain &a, uint32_t st) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     ch_stamp(a, st, 2);
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(a.cnt + ((size_t)st * CH_XCDS + blockIdx.x % CH_XCDS) * CH_CNT_STRIDE, 1u,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t r = 0;
+    if (threadIdx.x == 0) {
+        const uint32_t x = blockIdx.x % CH_XCDS;
+        r = __hip_atomic_fetch_add(a.cnt + ((size_t)st * CH_XCDS + x) * CH_CNT_STRIDE, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT) / ch_share(x);
+    }
+    return r;
 }
 
-// Wait until every workgroup has arrived at stage st of this token.
-__device__ __forceinline__ void ch_wait(const sgk_chain &a, uint32_t st) {
+// Wait until every workgroup has arrived at round r of stage st.
+__device__ __forceinline__ void ch_wait(const sgk_chain &a, uint32_t st, uint32_t r) {
     if (threadIdx.x == 0) {
-        const uint32_t nb = gridDim.x;
         const uint32_t *c = a.cnt + (size_t)st * CH_XCDS * CH_CNT_STRIDE;
         for (uint32_t it = 0;; it++) {
             bool ok = true;
 #pragma unroll
             for (uint32_t x = 0; x < CH_XCDS; x++) {
-                const uint32_t want = a.epoch * ((nb + CH_XCDS - 1 - x) / CH_XCDS);
+                const uint32_t want = (r + 1) * ch_share(x);
                 ok &= (int32_t)(ch_ld(c + x * CH_CNT_STRIDE) - want) >= 0;
             }
             if (ok) break;
@@ -4371,8 +4378,9 @@ __global__ void __launch_bounds__(CT) k_chain(sgk_chain a) {
         }
     };
     if (T[a.s0].kind == SGK_CS_GEMV) prime_after(a.s0 - 1);
+    uint32_t round = 0;
     for (uint32_t st = a.s0; st < a.s1; st++) {
-        if (st > a.s0) ch_wait(a, st - 1);
+        if (st > a.s0) ch_wait(a, st - 1, round);
         ch_stamp(a, st, 0);
         // the descriptor by value: the stage's stores could alias the table,
         // and a field reloaded after one would wait for every weight load
@@ -4463,7 +4471,7 @@ __global__ void __launch_bounds__(CT) k_chain(sgk_chain a) {
         } else if (S.kind == SGK_CS_EMBED) {
             ch_embed(S);
         }
-        ch_arrive(a, st);
+        round = ch_arrive(a, st);
         prime_after(st);
     }
 }
@@ -4473,7 +4481,7 @@ extern "C" uint32_t sgk_chain_blocks(void) { return (uint32_t)device_cus(); }
 #define CH_CP 4
 #define CH_PR 4
 extern "C" hipError_t sgk_chain_launch(const sgk_chain *a, uint32_t dk, uint32_t dv, hipStream_t s) {
-    if (!a->st || !a->cnt || !a->err || a->s0 >= a->s1 || !a->epoch) return hipErrorInvalidValue;
+    if (!a->st || !a->cnt || !a->err || a->s0 >= a->s1) return hipErrorInvalidValue;
     const uint32_t rw = (dv + 7) / 8;
     auto kern = k_chain<128, 16, CH_CP, CH_PR>;
     if (dk == 128 && rw == 16) {

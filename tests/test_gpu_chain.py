@@ -2,7 +2,10 @@
 between attention layers (embedding, the Q8_0 GEMVs, the DeltaNet steps,
 lm_head) is one persistent launch with device-wide barriers instead of kernel
 boundaries; an attention layer's split-K partial and combine run as kernels
-between runs.
+between runs. SURGE_CHAIN=2 runs only each DeltaNet layer's step and output
+projection as one two-stage launch (the projection's weights are requested
+while the step runs) and everything else as kernels. Both replay from
+captured HIP graphs: the barrier counters need no per-token value.
 
 - Per-position logits within 1e-3 (scale-relative) of the f16-KV oracle and
   identical argmax, for both DeltaNet shapes the chain takes at dk 128 and
@@ -42,12 +45,13 @@ def rel(got, want):
     return float(np.abs(got.astype(np.float64) - want).max() / np.abs(want).max())
 
 
+@pytest.mark.parametrize("mode", ["1", "2"])
 @pytest.mark.parametrize("name", list(CFGS))
-def test_chain_per_position_vs_oracle(gpu, monkeypatch, name):
+def test_chain_per_position_vs_oracle(gpu, monkeypatch, name, mode):
     cfg = CFGS[name]
     syn = S.Synth(cfg, S.SG_T_Q8_0, seed=21)
     gpu.load_model(syn.model)
-    monkeypatch.setenv("SURGE_CHAIN", "1")
+    monkeypatch.setenv("SURGE_CHAIN", mode)
     gpu.state_new(400)
     assert gpu.chain_active()
     rng = np.random.default_rng(8)
@@ -65,7 +69,8 @@ def test_chain_per_position_vs_oracle(gpu, monkeypatch, name):
     assert worst < 1e-3, worst
 
 
-def test_chain_matches_per_kernel_path_and_greedy_loops(gpu, monkeypatch):
+@pytest.mark.parametrize("mode", ["1", "2"])
+def test_chain_matches_per_kernel_path_and_greedy_loops(gpu, monkeypatch, mode):
     syn = S.Synth(CHAIN128, S.SG_T_Q8_0, seed=3)
     gpu.load_model(syn.model)
     ids = np.random.default_rng(2).integers(0, CHAIN128["vocab"], 40).tolist()
@@ -74,7 +79,7 @@ def test_chain_matches_per_kernel_path_and_greedy_loops(gpu, monkeypatch):
     assert not gpu.chain_active()
     plain = np.stack([gpu.forward(t, p) for p, t in enumerate(ids)])
     plain_gen = gpu.decode_greedy(int(np.argmax(plain[-1])), len(ids), 24)
-    monkeypatch.setenv("SURGE_CHAIN", "1")
+    monkeypatch.setenv("SURGE_CHAIN", mode)
     gpu.state_new(128)
     assert gpu.chain_active()
     chain = np.stack([gpu.forward(t, p) for p, t in enumerate(ids)])
@@ -99,12 +104,13 @@ def test_chain_matches_per_kernel_path_and_greedy_loops(gpu, monkeypatch):
     syn.close()
 
 
-def test_chain_2b_greedy_64_tokens_identical_to_reference(gpu, monkeypatch):
+@pytest.mark.parametrize("mode", ["1", "2"])
+def test_chain_2b_greedy_64_tokens_identical_to_reference(gpu, monkeypatch, mode):
     path = os.path.join(fixture.GOLDEN, "greedy_2b_ref.json")
     gold = json.load(open(path))
     syn = S.Synth(gold["cfg"], S.SG_T_Q8_0, seed=gold["seed"])
     gpu.load_model(syn.model)
-    monkeypatch.setenv("SURGE_CHAIN", "1")
+    monkeypatch.setenv("SURGE_CHAIN", mode)
     gpu.state_new(len(gold["prompt_ids"]) + len(gold["gen_ids"]) + 1)
     assert gpu.chain_active()
     prompt = gold["prompt_ids"]
@@ -115,10 +121,11 @@ def test_chain_2b_greedy_64_tokens_identical_to_reference(gpu, monkeypatch):
     assert gen.tolist() == gold["gen_ids"]
 
 
-def test_chain_barrier_give_up_fails_the_call(gpu, monkeypatch):
+@pytest.mark.parametrize("mode", ["1", "2"])
+def test_chain_barrier_give_up_fails_the_call(gpu, monkeypatch, mode):
     syn = S.Synth(CHAIN128, S.SG_T_Q8_0, seed=4)
     gpu.load_model(syn.model)
-    monkeypatch.setenv("SURGE_CHAIN", "1")
+    monkeypatch.setenv("SURGE_CHAIN", mode)
     monkeypatch.setenv("SURGE_CHAIN_SPIN", "1")
     gpu.state_new(64)
     assert gpu.chain_active()

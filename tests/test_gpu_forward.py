@@ -341,7 +341,8 @@ def test_prefill_gemm_round_split_matches_serial(gpu, monkeypatch):
 @pytest.mark.parametrize("slots", [None, "12"])
 def test_prefill_gemm_warp_specialised_matches_plain(gpu, monkeypatch, slots):
     """The warp-specialised prefill GEMM (default) and the plain one
-    (SURGE_GEMM_WS=0) share tiles, fragments, MFMA order and dequantisation:
+    (SURGE_GEMM_WS=0) share tiles, fragments and the per-step arithmetic
+    (two MFMAs per block from zero, then the block scale's FMA):
     a chunked prefill gives the same logits bit for bit through both, with
     the default slots and at 12 slots (full rounds, leftover tiles split over
     K, and the narrow weights' split-K, with every epilogue)."""
