@@ -63,6 +63,7 @@ typedef struct {
 typedef struct {          /* a device matrix in the GEMV layout */
     int8_t *qs;
     uint16_t *d;
+    uint16_t *dt;            /* the scales block-major [cols/32][rows], for the prefill GEMM (or NULL) */
     float *wf;
     uint32_t rows, cols;
 } dmat;
@@ -420,7 +421,7 @@ sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
             if (sg_failed(e = scratch(g, (uint64_t)rows * cols + (uint64_t)rows * (cols / 32) * 2 + 256, &t))) return e;
             ga.qs = t;
             ga.d = (uint16_t *)((char *)t + (((uint64_t)rows * cols + 255) / 256 * 256));
-            hipError_t he = sgk_repack_q8(DEV(a), rows, cols, (int8_t *)ga.qs, (uint16_t *)ga.d, 0, 1, s);
+            hipError_t he = sgk_repack_q8(DEV(a), rows, cols, (int8_t *)ga.qs, (uint16_t *)ga.d, NULL, rows, 0, 1, s);
             if (he != hipSuccess) return finish(g, he, NULL, 0);
         } else {
             ga.wf = DEV(a);
@@ -526,13 +527,13 @@ sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
         void *t;
         const uint64_t qb = ((uint64_t)M * K + 255) / 256 * 256, db = ((uint64_t)M * (K / 32) * 2 + 255) / 256 * 256;
         const uint64_t xb = ((uint64_t)N * K * 4 + 255) / 256 * 256, pc = (uint64_t)4 * N * M;   /* split-K partials */
-        if (sg_failed(e = scratch(g, qb + db + xb + pc * 4, &t))) return e;
+        if (sg_failed(e = scratch(g, qb + 2 * db + xb + pc * 4, &t))) return e;
         int8_t *qs = t;
-        uint16_t *d = (uint16_t *)((char *)t + qb);
-        uint16_t *xs = (uint16_t *)((char *)t + qb + db);
-        float *part = (float *)((char *)t + qb + db + xb);
-        hipError_t he = sgk_repack_q8(DEV(b), M, K, qs, d, 0, 1, s);
-        if (he == hipSuccess) he = sgk_gemm_q8(DEV(a), qs, d, DEV(out), N, M, K, xs, part, pc, s);
+        uint16_t *d = (uint16_t *)((char *)t + qb), *dt = (uint16_t *)((char *)t + qb + db);
+        uint16_t *xs = (uint16_t *)((char *)t + qb + 2 * db);
+        float *part = (float *)((char *)t + qb + 2 * db + xb);
+        hipError_t he = sgk_repack_q8(DEV(b), M, K, qs, d, dt, M, 0, 1, s);
+        if (he == hipSuccess) he = sgk_gemm_q8(DEV(a), qs, dt, DEV(out), N, M, K, xs, part, pc, s);
         return finish(g, he, outs, 1);
     }
     return errf("gpu: unknown kernel '%s'", kernel);
@@ -899,6 +900,7 @@ sg_err sg_gpu_run_attn_splitk_partial_gqa_online(sg_gpu *g, void *q, void *k, vo
 static void mat_free(sg_gpu *g, dmat *M) {
     dfree(g, M->qs);
     dfree(g, M->d);
+    dfree(g, M->dt);
     dfree(g, M->wf);
     *M = (dmat){0};
 }
@@ -922,13 +924,15 @@ static void model_free(sg_gpu *g) {
     g->model = NULL;
 }
 
-static sg_err mat_alloc(sg_gpu *g, dmat *M, uint32_t rows, uint32_t cols) {
+/* gemm: the prefill GEMM also multiplies by it (a block-major scale copy). */
+static sg_err mat_alloc(sg_gpu *g, dmat *M, uint32_t rows, uint32_t cols, bool gemm) {
     *M = (dmat){0};
     M->rows = rows;
     M->cols = cols;
     sg_err e;
     if (g->q8) {
         if (sg_failed(e = dalloc(g, (uint64_t)rows * cols, (void **)&M->qs))) return e;
+        if (gemm && sg_failed(e = dalloc(g, (uint64_t)rows * (cols / 32) * 2, (void **)&M->dt))) return e;
         return dalloc(g, (uint64_t)rows * (cols / 32) * 2, (void **)&M->d);
     }
     return dalloc(g, (uint64_t)rows * cols * 4, (void **)&M->wf);
@@ -942,7 +946,7 @@ static sg_err mat_put(sg_gpu *g, dmat *M, const void *host, uint32_t rows, uint3
     if (g->q8) {
         uint64_t raw = (uint64_t)rows * (cols / 32) * 34;
         HIPCHK(hipMemcpyAsync(stage, host, raw, hipMemcpyHostToDevice, g->stream), "weight upload");
-        HIPCHK(sgk_repack_q8(stage, rows, cols, M->qs, M->d, row0, step, g->stream), "repack");
+        HIPCHK(sgk_repack_q8(stage, rows, cols, M->qs, M->d, M->dt, M->rows, row0, step, g->stream), "repack");
         HIPCHK(hipStreamSynchronize(g->stream), "repack");
         return SG_OK;
     }
@@ -1036,29 +1040,29 @@ sg_err sg_gpu_load_model(sg_gpu *g, const sg_model *m) {
         L->attn = w->q_proj != NULL;
         if (sg_failed(e = small_put(g, &L->ln1, w->ln1, m->dense_type, H, sh))) break;
         if (sg_failed(e = small_put(g, &L->ln2, w->ln2, m->dense_type, H, sh))) break;
-        if (sg_failed(e = mat_alloc(g, &L->gu, 2 * c->ffn_hidden, c->hidden))) break;
+        if (sg_failed(e = mat_alloc(g, &L->gu, 2 * c->ffn_hidden, c->hidden, true))) break;
         if (sg_failed(e = mat_put(g, &L->gu, w->gate_proj, c->ffn_hidden, 0, 2, stage))) break;
         if (sg_failed(e = mat_put(g, &L->gu, w->up_proj, c->ffn_hidden, 1, 2, stage))) break;
-        if (sg_failed(e = mat_alloc(g, &L->down, c->hidden, c->ffn_hidden))) break;
+        if (sg_failed(e = mat_alloc(g, &L->down, c->hidden, c->ffn_hidden, true))) break;
         if (sg_failed(e = mat_put(g, &L->down, w->down_proj, c->hidden, 0, 1, stage))) break;
         if (L->attn) {
             uint32_t rows = g->q_width + 2 * g->kv_width;
-            if (sg_failed(e = mat_alloc(g, &L->in, rows, c->hidden))) break;
+            if (sg_failed(e = mat_alloc(g, &L->in, rows, c->hidden, true))) break;
             if (sg_failed(e = mat_put(g, &L->in, w->q_proj, g->q_width, 0, 1, stage))) break;
             if (sg_failed(e = mat_put(g, &L->in, w->k_proj, g->kv_width, g->q_width, 1, stage))) break;
             if (sg_failed(e = mat_put(g, &L->in, w->v_proj, g->kv_width, g->q_width + g->kv_width, 1, stage))) break;
-            if (sg_failed(e = mat_alloc(g, &L->out, c->hidden, g->attn_width))) break;
+            if (sg_failed(e = mat_alloc(g, &L->out, c->hidden, g->attn_width, true))) break;
             if (sg_failed(e = mat_put(g, &L->out, w->o_proj, c->hidden, 0, 1, stage))) break;
             if (sg_failed(e = small_put(g, &L->qn, w->q_norm, m->dense_type, c->head_dim, sh))) break;
             if (sg_failed(e = small_put(g, &L->kn, w->k_norm, m->dense_type, c->head_dim, sh))) break;
         } else {
             uint32_t nv = c->n_v_heads, rows = g->conv_dim + g->value_dim + 2 * nv;
-            if (sg_failed(e = mat_alloc(g, &L->in, rows, c->hidden))) break;
+            if (sg_failed(e = mat_alloc(g, &L->in, rows, c->hidden, true))) break;
             if (sg_failed(e = mat_put(g, &L->in, w->ssm_in_qkv, g->conv_dim, 0, 1, stage))) break;
             if (sg_failed(e = mat_put(g, &L->in, w->ssm_in_z, g->value_dim, g->conv_dim, 1, stage))) break;
             if (sg_failed(e = mat_put(g, &L->in, w->ssm_in_b, nv, g->conv_dim + g->value_dim, 1, stage))) break;
             if (sg_failed(e = mat_put(g, &L->in, w->ssm_in_a, nv, g->conv_dim + g->value_dim + nv, 1, stage))) break;
-            if (sg_failed(e = mat_alloc(g, &L->out, c->hidden, g->value_dim))) break;
+            if (sg_failed(e = mat_alloc(g, &L->out, c->hidden, g->value_dim, true))) break;
             if (sg_failed(e = mat_put(g, &L->out, w->ssm_out, c->hidden, 0, 1, stage))) break;
             if (sg_failed(e = small_put(g, &L->ssm_norm, w->ssm_norm, m->ssm_norm_type, c->head_v_dim, 0.0f))) break;
             if (sg_failed(e = small_put(g, &L->ssm_a, w->ssm_a, m->ssm_a_type, nv, 0.0f))) break;
@@ -1066,14 +1070,14 @@ sg_err sg_gpu_load_model(sg_gpu *g, const sg_model *m) {
             if (sg_failed(e = small_put(g, &L->conv_w, w->ssm_conv1d, m->dense_type, (uint64_t)g->conv_dim * c->conv_kernel, 0.0f))) break;
         }
     }
-    if (!sg_failed(e)) e = mat_alloc(g, &g->emb, c->vocab, c->hidden);
+    if (!sg_failed(e)) e = mat_alloc(g, &g->emb, c->vocab, c->hidden, false);
     if (!sg_failed(e)) e = mat_put(g, &g->emb, m->tok_emb, c->vocab, 0, 1, stage);
     g->lm_is_emb = m->lm_head == m->tok_emb;
     if (!sg_failed(e)) {
         if (g->lm_is_emb) {
             g->lm = g->emb;
         } else {
-            e = mat_alloc(g, &g->lm, c->vocab, c->hidden);
+            e = mat_alloc(g, &g->lm, c->vocab, c->hidden, false);
             if (!sg_failed(e)) e = mat_put(g, &g->lm, m->lm_head, c->vocab, 0, 1, stage);
         }
     }
@@ -1844,7 +1848,7 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
 
 static hipError_t gemm_rows(sg_gpu *g, const dmat *M, const float *X, uint32_t ldx, float *Y, uint32_t ldy,
                             uint32_t n, int epi) {
-    sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi, g->pf_XS, g->pf_PART,
+    sgk_gemm_args a = { X, M->qs, M->dt, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi, g->pf_XS, g->pf_PART,
                         (uint64_t)4 * g->pf_chunk * g->cfg.hidden, NULL, 0.0f };
     return sgk_gemm(&a, g->stream);
 }
@@ -1858,7 +1862,7 @@ static hipError_t gemm_rows_norm(sg_gpu *g, const dmat *M, const float *X, const
         hipError_t e = sgk_rmsnorm_heads(X, nw, g->pf_Xn, H, n, H, g->cfg.rms_eps, g->stream);
         return e != hipSuccess ? e : gemm_rows(g, M, g->pf_Xn, H, Y, ldy, n, epi);
     }
-    sgk_gemm_args a = { X, M->qs, M->d, M->wf, Y, n, M->rows, M->cols, H, ldy, epi, g->pf_XS, g->pf_PART,
+    sgk_gemm_args a = { X, M->qs, M->dt, M->wf, Y, n, M->rows, M->cols, H, ldy, epi, g->pf_XS, g->pf_PART,
                         (uint64_t)4 * g->pf_chunk * H, nw, g->cfg.rms_eps };
     return sgk_gemm(&a, g->stream);
 }
@@ -2153,7 +2157,7 @@ sg_err sg_gpu_time_matvec_q8(sg_gpu *g, void *w, void *x, void *y, uint32_t rows
     if (sg_failed(e = dalloc(g, n * (qb + db), (void **)&base))) return e;
     hipStream_t s = g->stream;
     hipEvent_t a = NULL, b = NULL;
-    hipError_t he = sgk_repack_q8(DEV(w), rows, cols, (int8_t *)base, (uint16_t *)(base + qb), 0, 1, s);
+    hipError_t he = sgk_repack_q8(DEV(w), rows, cols, (int8_t *)base, (uint16_t *)(base + qb), NULL, rows, 0, 1, s);
     for (uint64_t i = 1; i < n && he == hipSuccess; i++)
         he = hipMemcpyAsync(base + i * (qb + db), base, qb + db, hipMemcpyDeviceToDevice, s);
     if (he == hipSuccess) he = hipEventCreate(&a);

@@ -84,11 +84,14 @@ typedef struct {
 
 hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s);
 
-/* Split Q8_0 blocks (34-byte) of a [rows, cols] matrix into the device layout.
- * Destination row of source row r is row0 + r * row_step. */
+/* Split Q8_0 blocks (34-byte) of a [rows, cols] matrix into the device layout
+ * (qs [ld][cols] int8, d [ld][cols/32] f16 scales) and, when dt is not NULL,
+ * a block-major copy of the scales, dt [cols/32][ld], for the prefill GEMM.
+ * Destination row of source row r is row0 + r * row_step; ld is the
+ * destination matrix's row count. */
 hipError_t sgk_repack_q8(const uint8_t *src, uint32_t rows, uint32_t cols,
-                         int8_t *qs, uint16_t *d, uint32_t row0, uint32_t row_step,
-                         hipStream_t s);
+                         int8_t *qs, uint16_t *d, uint16_t *dt, uint32_t ld, uint32_t row0,
+                         uint32_t row_step, hipStream_t s);
 
 /* Embedding row gather: x[hidden] = row `token` of the table (token from the
  * step descriptor when `step` is non-NULL, else `token`). */
@@ -262,12 +265,13 @@ hipError_t sgk_fill_hash(void *p, uint64_t n, int f16, uint32_t seed, float scal
 typedef struct {
     const float *X;          /* [N][ldx] */
     const int8_t *qs;        /* Q8 layout W [M][K] (or NULL with wf) */
-    const uint16_t *d;
+    const uint16_t *dt;      /* its block scales, block-major [K/32][M] (sgk_repack_q8's dt) */
     const float *wf;         /* f32 W [M][K] */
     float *Y;                /* [N][ldy] */
     uint32_t N, M, K, ldx, ldy;
     int epi;                 /* SGK_EPI_*: store, += (residual), SwiGLU on (gate, up) column pairs */
-    uint16_t *xs;            /* Q8 W: scratch of 2*N*K bf16 (X split into hi | lo), 16-byte aligned */
+    uint16_t *xs;            /* Q8 W: scratch of 2*N*K bf16, 16-byte aligned: X split into hi and lo,
+                              * per Q8_0 block b and token n 32 hi then 32 lo at (b*N + n)*64 */
     float *part;             /* optional split-K partials (NULL: never split) */
     uint64_t part_cap;       /* floats in part */
     const float *nw;         /* Q8 W only: RMSNorm X's rows first (weight nw, eps), or NULL */
@@ -275,7 +279,7 @@ typedef struct {
 } sgk_gemm_args;
 /* Q8 W needs K % 32 == 0, ldx % 4 == 0 and X 16-byte aligned. */
 hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s);
-hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, float *Y,
+hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *dt, float *Y,
                        uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, float *part,
                        uint64_t part_cap, hipStream_t s);
 

@@ -595,26 +595,30 @@ static int device_cus() {
     return cus;
 }
 
-// Workgroups of the prefill GEMM resident at once: two per CU (its LDS).
-// SURGE_GEMM_SLOTS (decimal, >= 1) overrides it, for tests that exercise the
-// round split on small shapes.
-// The prefill GEMM runs warp-specialised (k_gemm_q8_ws) unless SURGE_GEMM_WS
-// is "0" (k_gemm_q8_mfma: same tiles and bits, for A/B measurement); read at
-// every launch. Two workgroups are resident per CU either way (256 threads
-// each, or 512 for the warp-specialised form).
-static bool gemm_ws() {
+// The prefill GEMM's form, read at every launch: the wide warp-specialised
+// kernel (k_gemm_q8_wide, 128 x 256 tiles, one workgroup per CU) unless
+// SURGE_GEMM_WS is "0" (k_gemm_q8_mfma: 128 x 128 tiles, 256 threads, two
+// per CU) or SURGE_GEMM_WIDE is "0" (k_gemm_q8_ws: 128 x 128 tiles, 512
+// threads, two per CU). All three give the same bits.
+enum { GEMM_PLAIN, GEMM_WS, GEMM_WIDE };
+static int gemm_kind() {
     const char *e = getenv("SURGE_GEMM_WS");
-    return !(e && e[0] == '0' && !e[1]);
+    if (e && e[0] == '0' && !e[1]) return GEMM_PLAIN;
+    e = getenv("SURGE_GEMM_WIDE");
+    if (e && e[0] == '0' && !e[1]) return GEMM_WS;
+    return GEMM_WIDE;
 }
-static uint32_t gemm_slots(bool ws) {
+// Workgroups of the prefill GEMM resident at once: one per CU for the wide
+// form, two for the others (their LDS). SURGE_GEMM_SLOTS (decimal, >= 1)
+// overrides it, for tests that exercise the round split on small shapes.
+static uint32_t gemm_slots(int kind) {
     const char *e = getenv("SURGE_GEMM_SLOTS");
     if (e && *e) {
         char *end = NULL;
         const unsigned long v = strtoul(e, &end, 10);
         if (end && !*end && v >= 1 && v <= 65536) return (uint32_t)v;
     }
-    (void)ws;
-    return 2 * (uint32_t)device_cus();
+    return (kind == GEMM_WIDE ? 1u : 2u) * (uint32_t)device_cus();
 }
 
 static hipError_t allow_lds(const void *kern, size_t lds) {
@@ -895,14 +899,16 @@ extern "C" hipError_t sgk_gemv_launch(const sgk_gemv *a, hipStream_t s) {
 // ---------------------------------------------------------------------------
 
 __global__ void k_repack_q8(const uint8_t *src, uint32_t rows, uint32_t cols, int8_t *qs,
-                            uint16_t *d, uint32_t row0, uint32_t step) {
+                            uint16_t *d, uint16_t *dt, uint32_t ld, uint32_t row0, uint32_t step) {
     const uint32_t nbl = cols >> 5;
     const uint64_t b = (uint64_t)blockIdx.x * TPB + threadIdx.x;
     if (b >= (uint64_t)rows * nbl) return;
     const uint32_t r = (uint32_t)(b / nbl), j = (uint32_t)(b % nbl);
     const uint8_t *p = src + b * 34;
     const uint64_t dr = (uint64_t)row0 + (uint64_t)r * step;
-    d[dr * nbl + j] = (uint16_t)(p[0] | (p[1] << 8));
+    const uint16_t dv = (uint16_t)(p[0] | (p[1] << 8));
+    d[dr * nbl + j] = dv;
+    if (dt) dt[(uint64_t)j * ld + dr] = dv;
     uint32_t *o = (uint32_t *)(qs + dr * cols + (uint64_t)j * 32);
 #pragma unroll
     for (int k = 0; k < 8; k++)
@@ -911,12 +917,12 @@ __global__ void k_repack_q8(const uint8_t *src, uint32_t rows, uint32_t cols, in
 }
 
 extern "C" hipError_t sgk_repack_q8(const uint8_t *src, uint32_t rows, uint32_t cols,
-                                    int8_t *qs, uint16_t *d, uint32_t row0, uint32_t row_step,
-                                    hipStream_t s) {
+                                    int8_t *qs, uint16_t *d, uint16_t *dt, uint32_t ld, uint32_t row0,
+                                    uint32_t row_step, hipStream_t s) {
     const uint64_t n = (uint64_t)rows * (cols >> 5);
     if (!n) return hipSuccess;
     hipLaunchKernelGGL(k_repack_q8, dim3((unsigned)((n + TPB - 1) / TPB)), dim3(TPB), 0, s, src,
-                       rows, cols, qs, d, row0, row_step);
+                       rows, cols, qs, d, dt, ld, row0, row_step);
     return hipGetLastError();
 }
 
@@ -3482,22 +3488,26 @@ extern "C" hipError_t sgk_step_advance(sgk_step *step, uint32_t *hist, hipStream
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// X [N][ldx] f32 -> xs[0 .. N*K) bf16 hi, xs[N*K .. 2*N*K) bf16 lo = x - hi,
-// both round-to-nearest-even, rows of K (K % 4 == 0, ldx % 4 == 0, X 16-byte
-// aligned).
+// X [N][ldx] f32 -> bf16 hi and lo = x - hi (both round-to-nearest-even),
+// laid out per Q8_0 block: the 64 bf16 of block b of token n, hi (32) then lo
+// (32), at xs + (b*N + n)*64, so a K step of the GEMM reads one contiguous
+// 128-byte line per token (K % 32 == 0, ldx % 4 == 0, X 16-byte aligned).
+__device__ __forceinline__ size_t xs_at(uint32_t N, uint32_t n, uint32_t k) {
+    return ((size_t)(k >> 5) * N + n) * 64 + (k & 31);
+}
 __global__ void __launch_bounds__(TPB) k_split_bf16(const float *X, uint32_t ldx, uint32_t N, uint32_t K,
                                                     uint16_t *xs) {
     const uint32_t k4 = K >> 2;
     const size_t total = (size_t)N * k4;
-    uint16_t *xl = xs + (size_t)N * K;
     for (size_t i = (size_t)blockIdx.x * TPB + threadIdx.x; i < total; i += (size_t)gridDim.x * TPB) {
         const uint32_t n = (uint32_t)(i / k4), c = (uint32_t)(i - (size_t)n * k4) * 4;
         const float4 v = *(const float4 *)(X + (size_t)n * ldx + c);
         const bf16x2 h01 = {(__bf16)v.x, (__bf16)v.y}, h23 = {(__bf16)v.z, (__bf16)v.w};
         const bf16x2 l01 = {(__bf16)(v.x - (float)h01[0]), (__bf16)(v.y - (float)h01[1])};
         const bf16x2 l23 = {(__bf16)(v.z - (float)h23[0]), (__bf16)(v.w - (float)h23[1])};
-        *(uint2 *)(xs + (size_t)n * K + c) = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
-        *(uint2 *)(xl + (size_t)n * K + c) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+        uint16_t *o = xs + xs_at(N, n, c);
+        *(uint2 *)o = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+        *(uint2 *)(o + 32) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
     }
 }
 
@@ -3515,7 +3525,6 @@ __global__ void __launch_bounds__(TPB) k_split_bf16_rms(const float *X, uint32_t
     ss = block_sum(ss, red);
     const float r = 1.0f / sqrtf(ss / (float)K + eps);
     // the split itself four columns at a time (K % 32 == 0, rows 16-byte aligned)
-    uint16_t *hi = xs + (size_t)n * K, *lo = xs + (size_t)N * K + (size_t)n * K;
     for (uint32_t i = 4 * t; i < K; i += 4 * TPB) {
         const float4 x4 = *(const float4 *)(xr + i);
         float v[4] = {x4.x * r, x4.y * r, x4.z * r, x4.w * r};
@@ -3526,8 +3535,9 @@ __global__ void __launch_bounds__(TPB) k_split_bf16_rms(const float *X, uint32_t
         const bf16x2 h01 = {(__bf16)v[0], (__bf16)v[1]}, h23 = {(__bf16)v[2], (__bf16)v[3]};
         const bf16x2 l01 = {(__bf16)(v[0] - (float)h01[0]), (__bf16)(v[1] - (float)h01[1])};
         const bf16x2 l23 = {(__bf16)(v[2] - (float)h23[0]), (__bf16)(v[3] - (float)h23[1])};
-        *(uint2 *)(hi + i) = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
-        *(uint2 *)(lo + i) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+        uint16_t *o = xs + xs_at(N, n, i);
+        *(uint2 *)o = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+        *(uint2 *)(o + 32) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
     }
 }
 
@@ -3599,16 +3609,16 @@ __device__ __forceinline__ void gm_wfrag(bf16x8 (&bq)[4], float (&dv)[4], const 
 __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &wself, uint32_t &dself,
                                         const v4u &wnext, const uint32_t &dnext,
                                         uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wq)[2][GM_TM * GM_LD],
-                                        float (&wd)[2][GM_TM], uint32_t cb, const v4u *xhr, const v4u *xlr,
-                                        const v4u *wrow, const uint16_t *drow, uint32_t s, uint32_t kend,
+                                        float (&wd)[2][GM_TM], uint32_t cb, const v4u *xhr, size_t xb,
+                                        const v4u *wrow, const uint16_t *dcol, uint32_t dm, uint32_t s, uint32_t kend,
                                         uint32_t so0, uint32_t so1, uint32_t sr, bool sd, uint32_t wn,
                                         uint32_t wm, uint32_t li, uint32_t lg) {
     const uint32_t s1 = min(s + 1, kend - 1), s2 = min(s + 2, kend - 1);
 #pragma unroll
-    for (int u = 0; u < 2; u++) { xr[u] = xhr[s1 * 4 + u]; xr[2 + u] = xlr[s1 * 4 + u]; }
+    for (int u = 0; u < 2; u++) { xr[u] = xhr[s1 * xb + u]; xr[2 + u] = xhr[s1 * xb + 4 + u]; }
     __builtin_amdgcn_sched_barrier(0);
     wself = wrow[s2 * 2];
-    dself = drow[s2];
+    dself = dcol[(size_t)s2 * dm];
     if (s < kend) {
         bf16x8 bq[4];
         float dv[4];
@@ -3633,11 +3643,32 @@ __device__ __forceinline__ void gm_step(f32x4 (&acc)[4][4], v4u (&xr)[4], v4u &w
 }
 
 // Tile of linear workgroup index b: consecutive indices go to the 8 XCDs in
-// turn, and each XCD walks its weight-row tiles (mt = xcd, xcd+8, ...) for one
-// token tile before the next, so its L2 holds a row tile's weights while the
-// token tiles reuse them. Indices past the last row tile of an XCD are holes.
+// turn (XCD b % 8 runs its (b / 8)-th tile). The operand every workgroup
+// re-reads is X (hi and lo, 4 bytes per element: a 128-token tile of a
+// 5120-wide X is 2.6 MB), so an XCD should work on one token tile at a time
+// and keep it in its 4 MB L2 while the weight tiles stream past. With nb
+// token tiles dividing 8 (nb = 1, 2, 4, 8), G = 8 / nb XCDs share token tile
+// xcd / G and split its row tiles (mt = xcd % G, + G, ...), so each XCD only
+// ever reads one token tile's X. Otherwise an XCD walks its row tiles
+// (mt = xcd, xcd + 8, ...) for one token tile before the next. gm_per_xcd
+// is the tiles per XCD, so the grid is 8 * gm_per_xcd; indices past an XCD's
+// last tile are holes.
+__host__ __device__ __forceinline__ uint32_t gm_per_xcd(uint32_t mb, uint32_t nb) {
+    if (nb <= 8 && 8 % nb == 0) {
+        const uint32_t G = 8 / nb;
+        return (mb + G - 1) / G;
+    }
+    return nb * ((mb + 7) / 8);
+}
 __device__ __forceinline__ bool gm_tile(uint32_t b, uint32_t mb, uint32_t nb, uint32_t &mt, uint32_t &nt) {
-    const uint32_t xcd = b & 7, qq = b >> 3, mper = (mb + 7) / 8;
+    const uint32_t xcd = b & 7, qq = b >> 3;
+    if (nb <= 8 && 8 % nb == 0) {
+        const uint32_t G = 8 / nb;
+        nt = xcd / G;
+        mt = xcd % G + G * qq;
+        return mt < mb;
+    }
+    const uint32_t mper = (mb + 7) / 8;
     mt = xcd + 8 * (qq % mper);
     nt = qq / mper;
     return mt < mb && nt < nb;
@@ -3672,11 +3703,12 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     // stages its scale
     const uint32_t sr = t >> 1, sk = (t & 1) * 16, so0 = gm_at(sr, sk / 8), so1 = gm_at(sr, sk / 8 + 1);
     const bool sd = !(t & 1);
-    const size_t xrow = (size_t)min(n0 + sr, N - 1) * K + sk;
-    const v4u *xhr = (const v4u *)(xs + xrow), *xlr = (const v4u *)(xs + (size_t)N * K + xrow);
+    // X block s of token n: hi at xhr[s * xb], lo 4 v4u later (xs_at)
+    const v4u *xhr = (const v4u *)(xs + (size_t)min(n0 + sr, N - 1) * 64 + sk);
+    const size_t xb = (size_t)N * 8;
     const uint32_t wrow_i = min(m0 + sr, M - 1);
     const v4u *wrow = (const v4u *)(qs + (size_t)wrow_i * K + sk);     // block s: wrow[2 s] (16 int8)
-    const uint16_t *drow = d + (size_t)wrow_i * nblk;
+    const uint16_t *dcol = d + wrow_i;                                   // block s: dcol[s * M]
 
     f32x4 acc[4][4];
 #pragma unroll
@@ -3687,12 +3719,12 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     uint32_t dA, dB;
     // prologue: block kb0 staged into buffer 0, block kb0+1's raw weights in B
 #pragma unroll
-    for (int u = 0; u < 2; u++) { xr[u] = xhr[kb0 * 4 + u]; xr[2 + u] = xlr[kb0 * 4 + u]; }
+    for (int u = 0; u < 2; u++) { xr[u] = xhr[kb0 * xb + u]; xr[2 + u] = xhr[kb0 * xb + 4 + u]; }
     __builtin_amdgcn_sched_barrier(0);
     wA = wrow[kb0 * 2];
-    dA = drow[kb0];
+    dA = dcol[(size_t)kb0 * M];
     wB = wrow[min(kb0 + 1, kb1 - 1) * 2];
-    dB = drow[min(kb0 + 1, kb1 - 1)];
+    dB = dcol[(size_t)min(kb0 + 1, kb1 - 1) * M];
     gm_stage_q16(wA, wq[0], so0, so1);
     if (sd) wd[0][sr] = h2f((uint16_t)dA);
     *(v4u *)&xt[0][0][so0] = xr[0];
@@ -3703,9 +3735,10 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
     // step s uses buffer s%2; its register set (A for even s) is reloaded with
     // block s+2 while the other set (holding block s+1) is staged
     for (uint32_t s = kb0; s < kb1; s += 2) {
-        gm_step(acc, xr, wA, dA, wB, dB, xt, wq, wd, 0, xhr, xlr, wrow, drow, s, kb1, so0, so1, sr, sd, wn, wm, li, lg);
-        gm_step(acc, xr, wB, dB, wA, dA, xt, wq, wd, 1, xhr, xlr, wrow, drow, s + 1, kb1, so0, so1, sr, sd, wn, wm, li,
+        gm_step(acc, xr, wA, dA, wB, dB, xt, wq, wd, 0, xhr, xb, wrow, dcol, M, s, kb1, so0, so1, sr, sd, wn, wm, li,
                 lg);
+        gm_step(acc, xr, wB, dB, wA, dA, xt, wq, wd, 1, xhr, xb, wrow, dcol, M, s + 1, kb1, so0, so1, sr, sd, wn, wm,
+                li, lg);
     }
     // epilogue: lane holds D[i = 4*lg + e][j = li] of each tile
     float *Yt = Y + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (GM_TN * GM_TM);
@@ -3741,6 +3774,9 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
 // producers keep four register sets: block b's X and raw weights sit in set
 // (b - kb0) % 4, both requested three steps before they are staged.
 #define GW_TPB 512
+#ifndef GW_NS
+#define GW_NS 4      // producer register sets: blocks requested GW_NS - 1 steps ahead
+#endif
 struct gw_set {
     v4u x[4];        // X hi and lo of the thread's chunk in its two token rows
     v4u w;           // 16 raw int8 weights
@@ -3748,16 +3784,19 @@ struct gw_set {
 };
 // X staging: thread p takes 16-byte chunk p%4 of token rows p/4 and p/4 + 64,
 // so a load instruction covers whole 64-byte rows (16 cache lines, not 32)
-__device__ __forceinline__ void gw_request_x(gw_set &st, const v4u *xhr, const v4u *xlr, uint32_t blk,
-                                             uint32_t r64) {
-    st.x[0] = xhr[blk * 4];
-    st.x[1] = xhr[blk * 4 + r64];
-    st.x[2] = xlr[blk * 4];
-    st.x[3] = xlr[blk * 4 + r64];
+// (X block blk of the thread's first token at xhr[blk * xb], its lo 4 v4u
+// later, the second token r64 v4u on; the scale of block blk at dcol[blk * dm])
+__device__ __forceinline__ void gw_request_x(gw_set &st, const v4u *xhr, size_t xb, uint32_t blk, uint32_t r64) {
+    const v4u *p = xhr + blk * xb;
+    st.x[0] = p[0];
+    st.x[1] = p[r64];
+    st.x[2] = p[4];
+    st.x[3] = p[r64 + 4];
 }
-__device__ __forceinline__ void gw_request_w(gw_set &st, const v4u *wrow, const uint16_t *drow, uint32_t blk) {
+__device__ __forceinline__ void gw_request_w(gw_set &st, const v4u *wrow, const uint16_t *dcol, uint32_t dm,
+                                             uint32_t blk) {
     st.w = wrow[blk * 2];
-    st.d = drow[blk];
+    st.d = dcol[(size_t)blk * dm];
 }
 __device__ __forceinline__ void gw_stage(const gw_set &st, uint16_t (&xt)[2][GM_TN * GM_LD],
                                          uint16_t (&wq)[GM_TM * GM_LD], float (&wd)[GM_TM], uint32_t so0,
@@ -3769,16 +3808,17 @@ __device__ __forceinline__ void gw_stage(const gw_set &st, uint16_t (&xt)[2][GM_
     *(v4u *)&xt[1][xo0] = st.x[2];
     *(v4u *)&xt[1][xo1] = st.x[3];
 }
-// Producer step s: request X and weights of block s+3 into set rq (free:
-// block s-1 was staged in step s-2), stage block s+1 (set st) into cb^1.
+// Producer step s: request X and weights of block s+NS-1 into set rq (free:
+// its last block was staged in step s-1), stage block s+1 (set st) into cb^1.
+template <int NS>
 __device__ __forceinline__ void gw_produce(gw_set &rq, const gw_set &st,
                                            uint16_t (&xt)[2][2][GM_TN * GM_LD], uint16_t (&wq)[2][GM_TM * GM_LD],
-                                           float (&wd)[2][GM_TM], uint32_t cb, const v4u *xhr, const v4u *xlr,
-                                           const v4u *wrow, const uint16_t *drow, uint32_t s, uint32_t kend,
-                                           uint32_t so0, uint32_t so1, uint32_t sr, bool sd, uint32_t xo0,
-                                           uint32_t xo1, uint32_t r64) {
-    gw_request_x(rq, xhr, xlr, min(s + 3, kend - 1), r64);
-    gw_request_w(rq, wrow, drow, min(s + 3, kend - 1));
+                                           float (&wd)[2][GM_TM], uint32_t cb, const v4u *xhr, size_t xb,
+                                           const v4u *wrow, const uint16_t *dcol, uint32_t dm, uint32_t s,
+                                           uint32_t kend, uint32_t so0, uint32_t so1, uint32_t sr, bool sd,
+                                           uint32_t xo0, uint32_t xo1, uint32_t r64) {
+    gw_request_x(rq, xhr, xb, min(s + NS - 1, kend - 1), r64);
+    gw_request_w(rq, wrow, dcol, dm, min(s + NS - 1, kend - 1));
     __builtin_amdgcn_sched_barrier(0);
     gw_stage(st, xt[cb ^ 1], wq[cb ^ 1], wd[cb ^ 1], so0, so1, sr, sd, xo0, xo1);
     __syncthreads();
@@ -3805,7 +3845,7 @@ __device__ __forceinline__ void gw_consume(f32x4 (&acc)[4][4], uint16_t (&xt)[2]
     __syncthreads();
 }
 
-template <int EPI>
+template <int EPI, int NS>
 __global__ void __launch_bounds__(GW_TPB) __attribute__((amdgpu_waves_per_eu(4, 4)))
 k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, uint32_t N, uint32_t M,
              uint32_t K, uint32_t ldy, uint64_t ysplit, uint32_t boff) {
@@ -3831,30 +3871,31 @@ k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, 
         const uint32_t xr0 = pt >> 2, xc = pt & 3;
         const uint32_t xo0 = gm_at(xr0, xc), xo1 = gm_at(xr0 + 64, xc);
         const uint32_t xn0 = min(n0 + xr0, N - 1), xn1 = min(n0 + xr0 + 64, N - 1);
-        const size_t xrow = (size_t)xn0 * K + xc * 8;
-        const uint32_t r64 = (uint32_t)(((size_t)(xn1 - xn0) * K) / 8);     // row p/4+64, in 16-byte units
-        const v4u *xhr = (const v4u *)(xs + xrow), *xlr = (const v4u *)(xs + (size_t)N * K + xrow);
+        const v4u *xhr = (const v4u *)(xs + (size_t)xn0 * 64 + xc * 8);
+        const size_t xb = (size_t)N * 8;
+        const uint32_t r64 = (xn1 - xn0) * 8;                              // token p/4+64, in 16-byte units
         const uint32_t wrow_i = min(m0 + sr, M - 1);
         const v4u *wrow = (const v4u *)(qs + (size_t)wrow_i * K + sk);     // block s: wrow[2 s] (16 int8)
-        const uint16_t *drow = d + (size_t)wrow_i * nblk;
-        // prologue: blocks kb0..kb0+2 requested, block kb0 staged into
-        // buffer 0; block b then sits in set (b - kb0) % 4
-        gw_set g0, g1, g2, g3;
+        const uint16_t *dcol = d + wrow_i;
+        // prologue: blocks kb0..kb0+NS-2 requested, block kb0 staged into
+        // buffer 0; block b then sits in set (b - kb0) % NS. The loop runs
+        // 2*NS steps per turn (set and buffer indices static), as does the
+        // consumers', so both pass the same barriers.
+        gw_set g[NS];
         const uint32_t kl = kb1 - 1;
-        gw_request_x(g0, xhr, xlr, kb0, r64);
-        gw_request_w(g0, wrow, drow, kb0);
-        gw_request_x(g1, xhr, xlr, min(kb0 + 1, kl), r64);
-        gw_request_w(g1, wrow, drow, min(kb0 + 1, kl));
-        gw_request_x(g2, xhr, xlr, min(kb0 + 2, kl), r64);
-        gw_request_w(g2, wrow, drow, min(kb0 + 2, kl));
+#pragma unroll
+        for (int u = 0; u < NS - 1; u++) {
+            gw_request_x(g[u], xhr, xb, min(kb0 + u, kl), r64);
+            gw_request_w(g[u], wrow, dcol, M, min(kb0 + u, kl));
+        }
         __builtin_amdgcn_sched_barrier(0);
-        gw_stage(g0, xt[0], wq[0], wd[0], so0, so1, sr, sd, xo0, xo1);
+        gw_stage(g[0], xt[0], wq[0], wd[0], so0, so1, sr, sd, xo0, xo1);
         __syncthreads();
-        for (uint32_t s = kb0; s < kb1; s += 4) {
-            gw_produce(g3, g1, xt, wq, wd, 0, xhr, xlr, wrow, drow, s, kb1, so0, so1, sr, sd, xo0, xo1, r64);
-            gw_produce(g0, g2, xt, wq, wd, 1, xhr, xlr, wrow, drow, s + 1, kb1, so0, so1, sr, sd, xo0, xo1, r64);
-            gw_produce(g1, g3, xt, wq, wd, 0, xhr, xlr, wrow, drow, s + 2, kb1, so0, so1, sr, sd, xo0, xo1, r64);
-            gw_produce(g2, g0, xt, wq, wd, 1, xhr, xlr, wrow, drow, s + 3, kb1, so0, so1, sr, sd, xo0, xo1, r64);
+        for (uint32_t s = kb0; s < kb1; s += 2 * NS) {
+#pragma unroll
+            for (int u = 0; u < 2 * NS; u++)
+                gw_produce<NS>(g[(u + NS - 1) % NS], g[(u + 1) % NS], xt, wq, wd, u & 1, xhr, xb, wrow, dcol, M,
+                               s + u, kb1, so0, so1, sr, sd, xo0, xo1, r64);
         }
         return;
     }
@@ -3867,11 +3908,9 @@ k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, 
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
     __syncthreads();
-    for (uint32_t s = kb0; s < kb1; s += 4) {
-        gw_consume(acc, xt, wq, wd, 0, s, kb1, wn, wm, li, lg);
-        gw_consume(acc, xt, wq, wd, 1, s + 1, kb1, wn, wm, li, lg);
-        gw_consume(acc, xt, wq, wd, 0, s + 2, kb1, wn, wm, li, lg);
-        gw_consume(acc, xt, wq, wd, 1, s + 3, kb1, wn, wm, li, lg);
+    for (uint32_t s = kb0; s < kb1; s += 2 * NS) {
+#pragma unroll
+        for (int u = 0; u < 2 * NS; u++) gw_consume(acc, xt, wq, wd, u & 1, s + u, kb1, wn, wm, li, lg);
     }
     // epilogue (consumers): lane holds D[i = 4*lg + e][j = li] of each tile
     float *Yt = Y + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (GM_TN * GM_TM);
@@ -3886,6 +3925,184 @@ k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, 
                 const float v = acc[a][c][e];
                 if (EPI == SGK_EPI_TILE) {
                     Yt[(n - n0) * GM_TM + (m - m0)] = v;
+                } else if (EPI == SGK_EPI_SWIGLU) {
+                    const float up = lane_xor1(v);            // column m+1 lives in lane li^1
+                    if (!(li & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(v) * up;
+                } else if (n < N && m < M) {
+                    if (EPI == SGK_EPI_ADD) Y[(size_t)n * ldy + m] += v;
+                    else Y[(size_t)n * ldy + m] = v;
+                }
+            }
+}
+
+// Wide form (the default): 512-thread workgroups, one per CU, over a tile of
+// 128 tokens x 256 weight rows, so each X tile staged feeds twice the MFMAs
+// of the 128-row tile (X, bf16 hi and lo, is the operand every workgroup
+// re-reads) and a step's LDS fragment reads per MFMA drop by a third. Waves
+// 0-3 (consumers, 256 registers each) own 64 tokens x 128 rows (4 x 8 MFMA
+// tiles) and run gm_tile_step's arithmetic per (step, token tile, weight
+// tile), so the bits are those of the other forms; waves 4-7 (producers)
+// stage block s+1 while the consumers work on block s, from NS register
+// sets requested NS-1 steps ahead. Producer thread p stages X as in the
+// 128-row form and all 32 weights and the scale of tile row p.
+#define GX_TM 256
+#ifndef GX_CW
+#define GX_CW 8      // consumer waves: 8 (64 x 64 each, 768 threads) or 4 (64 x 128 each, 512 threads)
+#endif
+struct gx_set {
+    v4u x[4];        // X hi and lo of the thread's chunk in its two token rows
+    uint32_t d;      // the block scale of the thread's row
+};
+__device__ __forceinline__ void gx_request(gx_set &st, const v4u *xhr, size_t xb, const uint16_t *dcol, uint32_t dm,
+                                           uint32_t blk, uint32_t r64) {
+    const v4u *p = xhr + blk * xb;
+    st.x[0] = p[0];
+    st.x[1] = p[r64];
+    st.x[2] = p[4];
+    st.x[3] = p[r64 + 4];
+    st.d = dcol[(size_t)blk * dm];
+}
+// The thread's row weights of 4 consecutive blocks (one 128-byte line when
+// aligned), requested together: a row's blocks are K bytes apart from the
+// next row's, so a request per block would touch every line four times.
+__device__ __forceinline__ void gx_request_w4(v4u (&w)[8], const v4u *wrow, uint32_t blk, uint32_t kl) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t b = min(blk + j, kl);
+        w[2 * j] = wrow[b * 2];
+        w[2 * j + 1] = wrow[b * 2 + 1];
+    }
+}
+__device__ __forceinline__ void gx_stage(const gx_set &st, const v4u &w0, const v4u &w1,
+                                         uint16_t (&xt)[2][GM_TN * GM_LD], uint16_t (&wq)[GX_TM * GM_LD],
+                                         float (&wd)[GX_TM], uint32_t row, uint32_t xo0, uint32_t xo1) {
+    gm_stage_q16(w0, wq, gm_at(row, 0), gm_at(row, 1));
+    gm_stage_q16(w1, wq, gm_at(row, 2), gm_at(row, 3));
+    wd[row] = h2f((uint16_t)st.d);
+    *(v4u *)&xt[0][xo0] = st.x[0];
+    *(v4u *)&xt[0][xo1] = st.x[1];
+    *(v4u *)&xt[1][xo0] = st.x[2];
+    *(v4u *)&xt[1][xo1] = st.x[3];
+}
+template <int WT>
+__device__ __forceinline__ void gx_consume(f32x4 (&acc)[4][WT], uint16_t (&xt)[2][2][GM_TN * GM_LD],
+                                           uint16_t (&wq)[2][GX_TM * GM_LD], float (&wd)[2][GX_TM], uint32_t cb,
+                                           uint32_t s, uint32_t kend, uint32_t wn, uint32_t wm, uint32_t li,
+                                           uint32_t lg) {
+    if (s < kend) {
+        bf16x8 bq[WT];
+        float dv[WT];
+#pragma unroll
+        for (int c = 0; c < WT; c++) {
+            const uint32_t row = wm * (16 * WT) + c * 16 + li;
+            bq[c] = *(const bf16x8 *)&wq[cb][gm_at(row, lg)];
+            dv[c] = wd[cb][row];
+        }
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const uint32_t row = wn * 64 + a * 16 + li;
+            const bf16x8 ah = *(const bf16x8 *)&xt[cb][0][gm_at(row, lg)];
+            const bf16x8 al = *(const bf16x8 *)&xt[cb][1][gm_at(row, lg)];
+#pragma unroll
+            for (int h = 0; h < WT / 4; h++) {
+                f32x4 (&ac)[4] = *reinterpret_cast<f32x4 (*)[4]>(&acc[a][4 * h]);
+                const bf16x8 (&bh)[4] = *reinterpret_cast<const bf16x8 (*)[4]>(&bq[4 * h]);
+                const float (&dh)[4] = *reinterpret_cast<const float (*)[4]>(&dv[4 * h]);
+                gm_tile_step(ac, ah, al, bh, dh);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <int EPI, int NS, int CW>
+__global__ void __launch_bounds__((CW + 4) * 64) __attribute__((amdgpu_waves_per_eu((CW + 4) / 4, (CW + 4) / 4)))
+k_gemm_q8_wide(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, uint32_t N, uint32_t M,
+               uint32_t K, uint32_t ldy, uint64_t ysplit, uint32_t boff) {
+    __shared__ __align__(16) uint16_t xt[2][2][GM_TN * GM_LD];     // [buffer][hi | lo][token][k]
+    __shared__ __align__(16) uint16_t wq[2][GX_TM * GM_LD];        // [buffer][row][k]: q as bf16
+    __shared__ float wd[2][GX_TM];                                 // [buffer][row]: block scale
+    const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GX_TM - 1) / GX_TM;
+    uint32_t mt_id, nt_id;
+    if (!gm_tile(blockIdx.x + boff, mb, nb, mt_id, nt_id)) return;
+    const uint32_t n0 = nt_id * GM_TN, m0 = mt_id * GX_TM;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t nblk = K >> 5;
+    const uint32_t kb0 = (uint32_t)((uint64_t)nblk * blockIdx.y / gridDim.y);
+    const uint32_t kb1 = (uint32_t)((uint64_t)nblk * (blockIdx.y + 1) / gridDim.y);
+    // Both roles pass the same barriers: one after the prologue and one per
+    // step, 2*NS steps per turn (steps past kb1 only request, clamped, and stage).
+    constexpr int WT = 16 / CW * 2;          // weight tiles (16 rows) per consumer wave
+    if (wave >= CW) {
+        const uint32_t pt = t - CW * 64;
+        const uint32_t xr0 = pt >> 2, xc = pt & 3;
+        const uint32_t xo0 = gm_at(xr0, xc), xo1 = gm_at(xr0 + 64, xc);
+        const uint32_t xn0 = min(n0 + xr0, N - 1), xn1 = min(n0 + xr0 + 64, N - 1);
+        const v4u *xhr = (const v4u *)(xs + (size_t)xn0 * 64 + xc * 8);
+        const size_t xb = (size_t)N * 8;
+        const uint32_t r64 = (xn1 - xn0) * 8;                              // token p/4+64, in 16-byte units
+        const uint32_t wrow_i = min(m0 + pt, M - 1);
+        const v4u *wrow = (const v4u *)(qs + (size_t)wrow_i * K);          // block s: wrow[2 s], wrow[2 s + 1]
+        const uint16_t *dcol = d + wrow_i;
+        // X and the scale per block in NS sets (block b in set (b - kb0) % NS);
+        // weights per 4 blocks in two batches (block b in batch ((b - kb0) / 4) % 2,
+        // slot (b - kb0) % 4), the next batch requested 4 steps before its first
+        // block is staged. A turn is 8 steps, so every index is static.
+        static_assert(2 * NS == 8, "wide GEMM producer: a turn of 8 steps holds two weight batches");
+        gx_set g[NS];
+        v4u wb[2][8];
+        const uint32_t kl = kb1 - 1;
+        gx_request_w4(wb[0], wrow, kb0, kl);
+        gx_request_w4(wb[1], wrow, kb0 + 4, kl);
+#pragma unroll
+        for (int u = 0; u < NS - 1; u++) gx_request(g[u], xhr, xb, dcol, M, min(kb0 + u, kl), r64);
+        __builtin_amdgcn_sched_barrier(0);
+        gx_stage(g[0], wb[0][0], wb[0][1], xt[0], wq[0], wd[0], pt, xo0, xo1);
+        __syncthreads();
+        for (uint32_t s = kb0; s < kb1; s += 2 * NS) {
+#pragma unroll
+            for (int u = 0; u < 2 * NS; u++) {
+                // request block s+u+NS-1 into the set block s+u-1 freed, and
+                // after a batch's last block is staged (steps 2 and 6) the
+                // batch 8 blocks on into it; stage block s+u+1 into the buffer
+                // step s+u does not read
+                gx_request(g[(u + NS - 1) % NS], xhr, xb, dcol, M, min(s + u + NS - 1, kl), r64);
+                if (u == 3) gx_request_w4(wb[0], wrow, s + 8, kl);
+                if (u == 7) gx_request_w4(wb[1], wrow, s + 12, kl);
+                __builtin_amdgcn_sched_barrier(0);
+                const uint32_t nbuf = (u & 1) ^ 1, b = ((u + 1) >> 2) & 1, j = (u + 1) & 3;
+                gx_stage(g[(u + 1) % NS], wb[b][2 * j], wb[b][2 * j + 1], xt[nbuf], wq[nbuf], wd[nbuf], pt, xo0, xo1);
+                __syncthreads();
+            }
+        }
+        return;
+    }
+    const uint32_t wn = wave & 1, wm = wave >> 1;
+    const uint32_t li = lane & 15, lg = lane >> 4;
+    Y += (size_t)blockIdx.y * ysplit;
+    f32x4 acc[4][WT];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int c = 0; c < WT; c++) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    for (uint32_t s = kb0; s < kb1; s += 2 * NS) {
+#pragma unroll
+        for (int u = 0; u < 2 * NS; u++) gx_consume<WT>(acc, xt, wq, wd, u & 1, s + u, kb1, wn, wm, li, lg);
+    }
+    // epilogue (consumers): lane holds D[i = 4*lg + e][j = li] of each tile
+    float *Yt = Y + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (GM_TN * GX_TM);
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int c = 0; c < WT; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t n = n0 + wn * 64 + a * 16 + lg * 4 + e;
+                const uint32_t m = m0 + wm * (16 * WT) + c * 16 + li;
+                const float v = acc[a][c][e];
+                if (EPI == SGK_EPI_TILE) {
+                    Yt[(n - n0) * GX_TM + (m - m0)] = v;
                 } else if (EPI == SGK_EPI_SWIGLU) {
                     const float up = lane_xor1(v);            // column m+1 lives in lane li^1
                     if (!(li & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(v) * up;
@@ -3918,24 +4135,26 @@ __global__ void __launch_bounds__(TPB) k_splitk_reduce(const float *P, uint32_t 
     }
 }
 
-// Split-K epilogue of the tiles a SGK_EPI_TILE launch computed: workgroup
-// (t, part) takes 1/GM_TR_PARTS of the tile of index t + boff; each thread
-// requests its 4 columns of all S partial tiles (P + (s*ntile + t)*16384) at
-// once, sums them in order, then applies the GEMM epilogue.
-#define GM_TR_PARTS 16
+// Split-K epilogue of the tiles a SGK_EPI_TILE launch computed (tiles of
+// GM_TN tokens x TM rows): workgroup (t, part) takes 1/parts of the tile of
+// index t + boff, parts = GM_TN*TM / (4*TPB); each thread requests its 4
+// columns of all S partial tiles (P + (s*ntile + t)*GM_TN*TM) at once, sums
+// them in order, then applies the GEMM epilogue.
 #define GM_TR_SMAX 16
-static_assert(GM_TR_PARTS * TPB * 4 == GM_TN * GM_TM, "k_tile_reduce covers a tile exactly");
-template <int EPI>
+template <int TM>
+constexpr uint32_t gm_tr_parts() { return GM_TN * TM / (4 * TPB); }
+template <int EPI, int TM>
 __global__ void __launch_bounds__(TPB) k_tile_reduce(const float *P, uint32_t S, uint32_t ntile, uint32_t boff,
                                                      uint32_t N, uint32_t M, float *Y, uint32_t ldy) {
-    const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + GM_TM - 1) / GM_TM;
+    static_assert(gm_tr_parts<TM>() * TPB * 4 == GM_TN * TM, "k_tile_reduce covers a tile exactly");
+    const uint32_t nb = (N + GM_TN - 1) / GM_TN, mb = (M + TM - 1) / TM;
     uint32_t mt, nt;
     if (!gm_tile(blockIdx.x + boff, mb, nb, mt, nt)) return;
     const uint32_t idx = (blockIdx.y * TPB + threadIdx.x) * 4;       // 4 columns of one token row
-    const uint32_t n = nt * GM_TN + idx / GM_TM, m = mt * GM_TM + idx % GM_TM;
+    const uint32_t n = nt * GM_TN + idx / TM, m = mt * TM + idx % TM;
     if (n >= N || m >= M) return;
-    const float4 *Pt = (const float4 *)(P + (size_t)blockIdx.x * (GM_TN * GM_TM) + idx);
-    const size_t sstride = (size_t)ntile * (GM_TN * GM_TM) / 4;
+    const float4 *Pt = (const float4 *)(P + (size_t)blockIdx.x * (GM_TN * TM) + idx);
+    const size_t sstride = (size_t)ntile * (GM_TN * TM) / 4;
     float4 part[GM_TR_SMAX];
 #pragma unroll
     for (uint32_t k = 0; k < GM_TR_SMAX; k++) part[k] = k < S ? Pt[k * sstride] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -3981,7 +4200,7 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
     if (a->epi == SGK_EPI_SWIGLU && (a->M & 1)) return hipErrorInvalidValue;
     if (a->nw && !a->qs) return hipErrorInvalidValue;      // the fused RMSNorm is part of the Q8 split
     if (a->qs) {
-        if (a->K % 32 || !a->xs || a->ldx % 4 || ((uintptr_t)a->X & 15) || ((uintptr_t)a->xs & 15))
+        if (a->K % 32 || !a->xs || !a->dt || a->ldx % 4 || ((uintptr_t)a->X & 15) || ((uintptr_t)a->xs & 15))
             return hipErrorInvalidValue;
         const uint32_t k4 = a->K / 4;
         const uint64_t total = (uint64_t)a->N * k4;
@@ -3990,28 +4209,38 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
         if (a->nw) hipLaunchKernelGGL(k_split_bf16_rms, dim3(a->N), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->nw,
                                       a->eps, a->xs);
         else hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
-        const uint32_t mb = (a->M + GM_TM - 1) / GM_TM, nb = (a->N + GM_TN - 1) / GM_TN;
-        const uint32_t grid = 8 * nb * ((mb + 7) / 8), nblk = a->K / 32, tiles = mb * nb;
-        // Workgroups run in rounds of `slots` (two resident per CU) and every
-        // tile takes the same time, so a launch costs ceil(tiles / slots)
+        const int kind = gemm_kind();
+        const uint32_t TM = kind == GEMM_WIDE ? GX_TM : GM_TM;
+        const uint32_t mb = (a->M + TM - 1) / TM, nb = (a->N + GM_TN - 1) / GM_TN;
+        const uint32_t grid = 8 * gm_per_xcd(mb, nb), nblk = a->K / 32, tiles = mb * nb;
+        // Workgroups run in rounds of `slots` (one or two resident per CU) and
+        // every tile takes the same time, so a launch costs ceil(tiles / slots)
         // rounds. Narrow weights (one partial round) split K up to 4 ways to
         // fill the round; wide ones whose last round is under half full run
         // the full rounds as they are and split the leftover tiles' K over a
         // whole round, partial tiles summed in order by k_tile_reduce. Splits
         // keep at least 8 Q8_0 blocks and fit the partials in a->part.
-        const bool ws = gemm_ws();
-        const uint32_t slots = gemm_slots(ws);
-        const uint32_t gtpb = ws ? GW_TPB : TPB;
+        const uint32_t slots = gemm_slots(kind);
+        const uint32_t gtpb = kind == GEMM_PLAIN ? TPB : kind == GEMM_WIDE ? (GX_CW + 4) * 64 : GW_TPB;
+#define GL(E, G, Yp, LDY, YS, BOFF)                                                                             \
+        do {                                                                                                   \
+            if (kind == GEMM_WIDE)                                                                              \
+                hipLaunchKernelGGL((k_gemm_q8_wide<E, GW_NS, GX_CW>), G, dim3(gtpb), 0, s, a->xs, a->qs, a->dt, Yp, a->N, \
+                                   a->M, a->K, LDY, YS, BOFF);                                                 \
+            else if (kind == GEMM_WS)                                                                           \
+                hipLaunchKernelGGL((k_gemm_q8_ws<E, GW_NS>), G, dim3(gtpb), 0, s, a->xs, a->qs, a->dt, Yp, a->N,   \
+                                   a->M, a->K, LDY, YS, BOFF);                                                 \
+            else                                                                                                \
+                hipLaunchKernelGGL((k_gemm_q8_mfma<E>), G, dim3(gtpb), 0, s, a->xs, a->qs, a->dt, Yp, a->N, a->M,  \
+                                   a->K, LDY, YS, BOFF);                                                       \
+        } while (0)
         uint32_t S = 1;
         if (a->part && tiles < slots) {
             S = min(4u, slots / tiles);
             while (S > 1 && (nblk / S < 8 || (uint64_t)S * a->N * a->M > a->part_cap)) S--;
         }
         if (S > 1) {
-            if (ws) hipLaunchKernelGGL((k_gemm_q8_ws<SGK_EPI_STORE>), dim3(grid, S), dim3(gtpb), 0, s, a->xs, a->qs, a->d,
-                                       a->part, a->N, a->M, a->K, a->M, (uint64_t)a->N * a->M, 0u);
-            else hipLaunchKernelGGL((k_gemm_q8_mfma<SGK_EPI_STORE>), dim3(grid, S), dim3(gtpb), 0, s, a->xs, a->qs, a->d,
-                                    a->part, a->N, a->M, a->K, a->M, (uint64_t)a->N * a->M, 0u);
+            GL(SGK_EPI_STORE, dim3(grid, S), a->part, a->M, (uint64_t)a->N * a->M, 0u);
             const uint32_t rg = (uint32_t)min(((uint64_t)a->N * a->M + TPB - 1) / TPB, (uint64_t)4096);
 #define GR(E) hipLaunchKernelGGL((k_splitk_reduce<E>), dim3(rg), dim3(TPB), 0, s, a->part, S, a->N, a->M, a->Y, a->ldy)
             if (a->epi == SGK_EPI_ADD) GR(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GR(SGK_EPI_SWIGLU); else GR(SGK_EPI_STORE);
@@ -4024,24 +4253,23 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
             const uint32_t left = grid - full;
             if (left && left <= slots / 2) {
                 S2 = min((uint32_t)GM_TR_SMAX, slots / left);
-                while (S2 > 1 && (nblk / S2 < 8 || (uint64_t)S2 * left * (GM_TN * GM_TM) > a->part_cap)) S2--;
+                while (S2 > 1 && (nblk / S2 < 8 || (uint64_t)S2 * left * (GM_TN * TM) > a->part_cap)) S2--;
             }
             if (S2 < 2) full = grid;
         }
-#define GQ(E) do { if (ws) hipLaunchKernelGGL((k_gemm_q8_ws<E>), dim3(full), dim3(gtpb), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy, (uint64_t)0, 0u); \
-                 else hipLaunchKernelGGL((k_gemm_q8_mfma<E>), dim3(full), dim3(gtpb), 0, s, a->xs, a->qs, a->d, a->Y, a->N, a->M, a->K, a->ldy, (uint64_t)0, 0u); } while (0)
-        if (a->epi == SGK_EPI_ADD) GQ(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GQ(SGK_EPI_SWIGLU); else GQ(SGK_EPI_STORE);
-#undef GQ
+        if (a->epi == SGK_EPI_ADD) GL(SGK_EPI_ADD, dim3(full), a->Y, a->ldy, (uint64_t)0, 0u);
+        else if (a->epi == SGK_EPI_SWIGLU) GL(SGK_EPI_SWIGLU, dim3(full), a->Y, a->ldy, (uint64_t)0, 0u);
+        else GL(SGK_EPI_STORE, dim3(full), a->Y, a->ldy, (uint64_t)0, 0u);
         if (full < grid) {
             const uint32_t left = grid - full;
-            if (ws) hipLaunchKernelGGL((k_gemm_q8_ws<SGK_EPI_TILE>), dim3(left, S2), dim3(gtpb), 0, s, a->xs, a->qs, a->d,
-                                       a->part, a->N, a->M, a->K, 0u, (uint64_t)0, full);
-            else hipLaunchKernelGGL((k_gemm_q8_mfma<SGK_EPI_TILE>), dim3(left, S2), dim3(gtpb), 0, s, a->xs, a->qs, a->d,
-                                    a->part, a->N, a->M, a->K, 0u, (uint64_t)0, full);
-#define GT(E) hipLaunchKernelGGL((k_tile_reduce<E>), dim3(left, GM_TR_PARTS), dim3(TPB), 0, s, a->part, S2, left, full, a->N, a->M, a->Y, a->ldy)
-            if (a->epi == SGK_EPI_ADD) GT(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GT(SGK_EPI_SWIGLU); else GT(SGK_EPI_STORE);
+            GL(SGK_EPI_TILE, dim3(left, S2), a->part, 0u, (uint64_t)0, full);
+#define GT(E, TMV) hipLaunchKernelGGL((k_tile_reduce<E, TMV>), dim3(left, gm_tr_parts<TMV>()), dim3(TPB), 0, s, a->part, S2, left, full, a->N, a->M, a->Y, a->ldy)
+#define GT2(E) do { if (kind == GEMM_WIDE) GT(E, GX_TM); else GT(E, GM_TM); } while (0)
+            if (a->epi == SGK_EPI_ADD) GT2(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GT2(SGK_EPI_SWIGLU); else GT2(SGK_EPI_STORE);
+#undef GT2
 #undef GT
         }
+#undef GL
     } else {
         dim3 grid((a->M + 15) / 16, (a->N + 15) / 16);
 #define GF(E) hipLaunchKernelGGL(k_gemm_f32<E>, grid, dim3(TPB), 0, s, a->X, a->wf, a->Y, a->N, a->M, a->K, a->ldx, a->ldy)
@@ -4051,10 +4279,10 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
     return hipGetLastError();
 }
 
-extern "C" hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *d, float *Y,
+extern "C" hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *dt, float *Y,
                                   uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, float *part,
                                   uint64_t part_cap, hipStream_t s) {
-    sgk_gemm_args a = {X, qs, d, NULL, Y, N, M, K, K, M, SGK_EPI_STORE, xs, part, part_cap};
+    sgk_gemm_args a = {X, qs, dt, NULL, Y, N, M, K, K, M, SGK_EPI_STORE, xs, part, part_cap};
     return sgk_gemm(&a, s);
 }
 

@@ -310,13 +310,18 @@ WIDE = dict(n_layers=4, n_heads=8, n_kv_heads=2, head_dim=64, hidden=512, ffn_hi
             conv_kernel=4, attn_output_gate=True)
 
 
-def test_prefill_gemm_round_split_matches_serial(gpu, monkeypatch):
-    """The prefill GEMMs' round split with every epilogue: at 12 workgroup
-    slots the gate|up product (16 row tiles, SwiGLU) and the DeltaNet input
-    projection (13, store) run a full round plus leftover tiles with K split
-    in two (k_tile_reduce), the output projections and down (4 tiles, +=
-    residual) split K in the narrow path. Chunked prefill against the serial
-    forward (2e-4, same argmax) and against the default-slot prefill."""
+@pytest.mark.parametrize("kind,slots", [("wide", "6"), ("ws", "12")])
+def test_prefill_gemm_round_split_matches_serial(gpu, monkeypatch, kind, slots):
+    """The prefill GEMMs' round split with every epilogue. Wide form (128 x
+    256 tiles) at 6 workgroup slots: gate|up (8 row tiles, SwiGLU) and the
+    DeltaNet input projection (7) run a full round plus leftover tiles with K
+    split in two (k_tile_reduce), the output projections and down (2 tiles,
+    += residual) split K in the narrow path. 128 x 128 tiles
+    (SURGE_GEMM_WIDE=0) at 12 slots: gate|up (16 tiles) and the input
+    projection (13) run a round plus leftovers split in two, the output
+    projections and down (4 tiles) the narrow split. Chunked prefill against
+    the serial forward (2e-4, same argmax) and against the default-slot
+    prefill."""
     syn = S.Synth(WIDE, S.SG_T_Q8_0, seed=17)
     gpu.load_model(syn.model)
     gpu.state_new(260)
@@ -325,7 +330,9 @@ def test_prefill_gemm_round_split_matches_serial(gpu, monkeypatch):
     serial = None
     for p, t in enumerate(prompt):
         serial = gpu.forward(t, p)
-    monkeypatch.setenv("SURGE_GEMM_SLOTS", "12")
+    if kind == "ws":
+        monkeypatch.setenv("SURGE_GEMM_WIDE", "0")
+    monkeypatch.setenv("SURGE_GEMM_SLOTS", slots)
     last = gpu.prefill(prompt, chunk=128)
     assert np.array_equal(gpu.prefill(prompt, chunk=128), last)     # partial tiles summed in order
     monkeypatch.delenv("SURGE_GEMM_SLOTS")
@@ -340,12 +347,17 @@ def test_prefill_gemm_round_split_matches_serial(gpu, monkeypatch):
 
 @pytest.mark.parametrize("slots", [None, "12"])
 def test_prefill_gemm_warp_specialised_matches_plain(gpu, monkeypatch, slots):
-    """The warp-specialised prefill GEMM (default) and the plain one
-    (SURGE_GEMM_WS=0) share tiles, fragments and the per-step arithmetic
-    (two MFMAs per block from zero, then the block scale's FMA):
-    a chunked prefill gives the same logits bit for bit through both, with
+    """The three prefill GEMM forms run the same per-step arithmetic (two
+    MFMAs per Q8_0 block from zero, then the block scale's FMA) per output:
+    the wide warp-specialised kernel (default, 128 x 256 tiles), the 128 x
+    128 warp-specialised one (SURGE_GEMM_WIDE=0) and the plain one
+    (SURGE_GEMM_WS=0). The two 128 x 128 forms share tiles and split plans,
+    so a chunked prefill gives the same logits bit for bit through both, with
     the default slots and at 12 slots (full rounds, leftover tiles split over
-    K, and the narrow weights' split-K, with every epilogue)."""
+    K, and the narrow weights' split-K, with every epilogue). The wide form
+    matches them bit for bit where its split plan is the same (default slots
+    on this model) and within fp32 reassociation where its wider tiles change
+    the plan (12 slots)."""
     syn = S.Synth(WIDE, S.SG_T_Q8_0, seed=19)
     gpu.load_model(syn.model)
     gpu.state_new(260)
@@ -353,12 +365,19 @@ def test_prefill_gemm_warp_specialised_matches_plain(gpu, monkeypatch, slots):
     prompt = rng.integers(0, WIDE["vocab"], 256).tolist()
     if slots:
         monkeypatch.setenv("SURGE_GEMM_SLOTS", slots)
+    wide = gpu.prefill(prompt, chunk=128)
+    monkeypatch.setenv("SURGE_GEMM_WIDE", "0")
     ws = gpu.prefill(prompt, chunk=128)
+    monkeypatch.delenv("SURGE_GEMM_WIDE")
     monkeypatch.setenv("SURGE_GEMM_WS", "0")
     plain = gpu.prefill(prompt, chunk=128)
     monkeypatch.delenv("SURGE_GEMM_WS")
     assert np.array_equal(ws, plain)
-    assert np.array_equal(gpu.prefill(prompt, chunk=128), ws)
+    if slots:
+        assert rel(wide, plain) < 1e-4
+    else:
+        assert np.array_equal(wide, plain)
+    assert np.array_equal(gpu.prefill(prompt, chunk=128), wide)
     syn.close()
 
 

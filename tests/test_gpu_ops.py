@@ -575,11 +575,13 @@ def test_matmul_q8_prefill_gemm(gpu, N, M, K):
     assert_close(yb.array.reshape(N, M), want)
 
 
-def test_matmul_q8_prefill_gemm_round_split(gpu, monkeypatch):
-    """The prefill GEMM's round split: with 28 workgroup slots, the 32 tiles
-    of a 256 x 2048 x 1792 product run as one full round plus 4 leftover
-    tiles whose K is split 7 ways (8 Q8_0 blocks each), partial tiles summed
-    in order by k_tile_reduce. Against the oracle, and against the unsplit
+@pytest.mark.parametrize("kind,slots", [("wide", "14"), ("ws", "28")])
+def test_matmul_q8_prefill_gemm_round_split(gpu, monkeypatch, kind, slots):
+    """The prefill GEMM's round split on a 256 x 2048 x 1792 product: the wide
+    form's 16 tiles (128 x 256) at 14 workgroup slots, and the 128 x 128
+    form's 32 tiles at 28 slots, run one full round plus 2 (4) leftover tiles
+    whose K is split 7 ways (8 Q8_0 blocks each), partial tiles summed in
+    order by k_tile_reduce. Against the oracle, and against the unsplit
     launch (default slots) within fp32 reassociation."""
     N, M, K = 256, 2048, 1792
     rng = np.random.default_rng(31)
@@ -587,7 +589,9 @@ def test_matmul_q8_prefill_gemm_round_split(gpu, monkeypatch):
     raw = q8_matrix(rng, M, K, sigma=1.0)
     xb, wb = gpu.buf(X), gpu.buf(raw)
     ys = gpu.buf(np.zeros(N * M, np.float32))
-    monkeypatch.setenv("SURGE_GEMM_SLOTS", "28")
+    if kind == "ws":
+        monkeypatch.setenv("SURGE_GEMM_WIDE", "0")
+    monkeypatch.setenv("SURGE_GEMM_SLOTS", slots)
     gpu.run_op("k_matmul_q8", xb, wb, ys, [N, M, K])
     monkeypatch.delenv("SURGE_GEMM_SLOTS")
     yu = gpu.buf(np.zeros(N * M, np.float32))
