@@ -268,9 +268,52 @@ def trace(path, kernel, last):
     return {"kernel": kernel, "dispatches": len(durs), "avg_us": all_avg, "last": len(tail), "last_avg_us": avg}
 
 
+def micro(micro_jsonl, shapes_jsonl):
+    """The micro-config tables from `bench.py --micro` and `bench.py
+    --gemv-shapes` output (one JSON object per line each)."""
+    rows = [json.loads(l) for l in open(micro_jsonl) if l.strip().startswith("{")]
+    print("| unit | GPU us (rotated) | GB/s | of 8 TB/s | GPU us (resident) | ref.c us (1 core) |")
+    print("|---|---|---|---|---|---|")
+    split = []
+    for r in rows:
+        if "cpu_us_median" in r:
+            print(f"| {r['unit']} | {r['gpu_us']} | {r['gpu_GBs']} | {r['frac']} | {r['gpu_us_cache_resident']} | "
+                  f"{r['cpu_us_median']} |")
+            if "gpu_us_partial" in r:
+                keys = r["unit"].split(" at ")[1].split(",")[0]
+                split.append(f"{keys}: {r['gpu_us_partial']} / {r['gpu_us_combine']}")
+    if split:
+        print("\nAttention split: partial / combine us (rotated): " + "; ".join(split) + ".")
+    print("\n| read | us (rotated) | GB/s | of 8 TB/s | us (resident) |")
+    print("|---|---|---|---|---|")
+    for r in rows:
+        if r.get("unit", "").startswith("plain streaming read"):
+            print(f"| {r['algo_bytes'] / 1e6:.1f} MB | {r['gpu_us']} | {r['gpu_GBs']} | {r['frac']} | "
+                  f"{r['gpu_us_cache_resident']} |")
+    for r in rows:
+        if r.get("unit", "").startswith("empty kernel"):
+            print(f"\nEmpty kernel: {r['gpu_us_per_launch_eager']} us per launch issued one by one, "
+                  f"{r['gpu_us_per_launch_in_graph']} us replayed from a captured HIP graph ({r['reps']} launches).")
+    if not shapes_jsonl:
+        return
+    sh = [json.loads(l) for l in open(shapes_jsonl) if l.strip().startswith("{")]
+    shapes, variants, t = [], [], {}
+    for r in sh:
+        if r["shape"] not in shapes:
+            shapes.append(r["shape"])
+        if r["variant"] not in variants:
+            variants.append(r["variant"])
+        t[(r["shape"], r["variant"])] = r["us"]
+    print("\n| shape | " + " | ".join(variants) + " |")
+    print("|---|" + "---|" * len(variants))
+    for s_ in shapes:
+        print(f"| {s_} | " + " | ".join(str(t.get((s_, v), "-")) for v in variants) + " |")
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("mode", choices=["stats", "pmc", "trace", "decode", "traffic", "prefill", "counters", "hbm"])
+    ap.add_argument("mode", choices=["stats", "pmc", "trace", "decode", "traffic", "prefill", "counters", "hbm",
+                                     "micro"])
     ap.add_argument("--trace", default=None)
     ap.add_argument("csv")
     ap.add_argument("csv2", nargs="?", default=None)
@@ -284,6 +327,8 @@ def main():
     a = ap.parse_args()
     if a.mode == "stats":
         stats(a.csv, a.tokens)
+    elif a.mode == "micro":
+        micro(a.csv, a.csv2)
     elif a.mode == "decode":
         decode(a.csv)
     elif a.mode == "prefill":
