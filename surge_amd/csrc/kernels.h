@@ -210,12 +210,13 @@ hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s);
  * sgk_gdn_step, token by token. */
 hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t in_stride, uint32_t ntok,
                          float *ws, hipStream_t s);
-/* The delta-rule scan alone: qkv rows [ntok][in_stride] hold normalised
+/* The delta-rule scan alone: qkv rows [ntok][a->conv_dim] hold normalised
  * q | k | v; gates [ntok][2*n_v] = beta | decay (or NULL: computed from the
- * b/a columns of a->in as in sgk_gdn_chunk). With a workspace ws of
- * sgk_delta_wy_ws_floats(n_v, ntok) floats, dk 64 or 128 and
- * SURGE_DELTA_SCAN=wy it runs the chunked (WY) form over 64-token
- * sub-chunks; otherwise the sequential scan. */
+ * b/a columns of a->in, rows in_stride apart, as in sgk_gdn_chunk). With a
+ * workspace ws of sgk_delta_wy_ws_floats(n_v, ntok) floats and dk 64 or 128
+ * it runs a chunked form: by default the 16-token one on the matrix cores
+ * (dv a multiple of 16), with SURGE_DELTA_SCAN=wy the 64-token one; with
+ * SURGE_DELTA_SCAN=seq, no workspace or other shapes the sequential scan. */
 hipError_t sgk_delta_scan(const sgk_gdn *a, const float *qkv, uint32_t in_stride, uint32_t ntok,
                           const float *gates, float *ws, hipStream_t s);
 uint64_t sgk_delta_wy_ws_floats(uint32_t n_v, uint32_t ntok);
