@@ -2106,7 +2106,7 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
 template <int HD>
 __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
     static_assert(HD % 64 == 0 && HD <= 256, "flash prefill takes head_dim 64, 128, 192 or 256");
-    constexpr int KLD = HD + 16, NKB = HD / 32, NNT = HD / 16;
+    constexpr int KLD = HD + 16, NKB = HD / 32, NNT = HD / 16, NSC = FA_TK / 16;
     // K staging: a key row is KC8 16-byte chunks; consecutive threads take
     // consecutive chunks of a row (contiguous LDS stores, coalesced loads),
     // KPP rows per pass, KNP passes per 64-key tile
@@ -2187,13 +2187,13 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
         }
         __syncthreads();
         // scores of this wave's 16 tokens x 64 keys
-        f32x4 sc[4];
+        f32x4 sc[NSC];
 #pragma unroll
-        for (int n = 0; n < 4; n++) sc[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int n = 0; n < NSC; n++) sc[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
 #pragma unroll
-            for (int n = 0; n < 4; n++) {
+            for (int n = 0; n < NSC; n++) {
                 const f16x8 bk = *(const f16x8 *)&ks[(n * 16 + li) * KLD + kb * 32 + lg * 8];
                 sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kb], bk, sc[n], 0, 0, 0);
                 sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[kb], bk, sc[n], 0, 0, 0);
@@ -2203,9 +2203,9 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
         float al[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            float v[4], tm = -INFINITY;
+            float v[NSC], tm = -INFINITY;
 #pragma unroll
-            for (int n = 0; n < 4; n++) {
+            for (int n = 0; n < NSC; n++) {
                 const uint32_t key = k0 + n * 16 + li;
                 v[n] = key <= rpos[e] ? sc[n][e] * a.scale : -INFINITY;
                 tm = fmaxf(tm, v[n]);
@@ -2214,7 +2214,7 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
             const float mnew = fmaxf(mrun[e], tm);
             float ps_sum = 0.0f;
 #pragma unroll
-            for (int n = 0; n < 4; n++) {
+            for (int n = 0; n < NSC; n++) {
                 const uint32_t key = k0 + n * 16 + li;
                 const float pv = key <= rpos[e] ? expf(v[n] - mnew) : 0.0f;
                 sc[n][e] = pv;
@@ -2227,7 +2227,7 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
         }
         // P (hi, lo) into LDS rows of this wave
 #pragma unroll
-        for (int n = 0; n < 4; n++)
+        for (int n = 0; n < NSC; n++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t row = wave * 16 + lg * 4 + e, col = n * 16 + li;
