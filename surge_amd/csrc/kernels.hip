@@ -2103,20 +2103,24 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
 // MFMA 16x16x32 layout as in the prefill GEMM.
 // ---------------------------------------------------------------------------
 
-template <int HD>
-__global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
+// HW query heads per workgroup (1 or 2, heads sharing one kv head): waves
+// 4 h' .. 4 h' + 3 take head HW * blockIdx.x + h', so one staged K / V^T tile
+// serves HW heads.
+template <int HD, int HW>
+__global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
     static_assert(HD % 64 == 0 && HD <= 256, "flash prefill takes head_dim 64, 128, 192 or 256");
     constexpr int KLD = HD + 16, NKB = HD / 32, NNT = HD / 16, NSC = FA_TK / 16;
     // K staging: a key row is KC8 16-byte chunks; consecutive threads take
     // consecutive chunks of a row (contiguous LDS stores, coalesced loads),
     // KPP rows per pass, KNP passes per 64-key tile
-    constexpr int KC8 = HD / 8, KPP = TPB / KC8, KNP = (FA_TK + KPP - 1) / KPP;
+    constexpr int KC8 = HD / 8, KPP = TPB * HW / KC8, KNP = (FA_TK + KPP - 1) / KPP;
     constexpr int VDC = HD / 8;                  // V staging: dim chunks of 8 (threads 8*vdc + vkg)
     __shared__ __align__(16) uint16_t ks[FA_TK * KLD];
     __shared__ __align__(16) uint16_t vt[HD * FA_PLD];
-    __shared__ __align__(16) uint16_t ps[2][FA_TQ * FA_PLD];
-    const uint32_t h = blockIdx.x, tb = blockIdx.y, G = a.n_heads / a.n_kv, hk = h / G, n_kv = a.n_kv;
-    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 15, lg = lane >> 4;
+    __shared__ __align__(16) uint16_t ps[2][HW * FA_TQ * FA_PLD];
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 15, lg = lane >> 4, tw = wave & 3;
+    const uint32_t h = blockIdx.x * HW + (wave >> 2), tb = blockIdx.y, G = a.n_heads / a.n_kv, n_kv = a.n_kv;
+    const uint32_t hk = blockIdx.x * HW / G;    // the workgroup's heads share it
     const uint32_t ntok = a.ntok, z0 = tb * FA_TQ;
     const uint32_t base = a.steps[0].pos;
     const uint32_t zlast = min(z0 + FA_TQ, ntok) - 1;
@@ -2129,7 +2133,7 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
     // q fragments of this wave's 16 tokens (A operand: row li, dims 8*lg.. of each 32)
     f16x8 qh[NKB], ql[NKB];
     {
-        const uint32_t z = min(z0 + wave * 16 + li, ntok - 1);
+        const uint32_t z = min(z0 + tw * 16 + li, ntok - 1);
         const float *qr = a.q + (size_t)z * a.q_tok + (size_t)h * a.q_stride;
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
@@ -2142,7 +2146,7 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
     // this lane's rows in the D layout: 4*lg + e of the wave's tile
     uint32_t rpos[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) rpos[e] = base + z0 + wave * 16 + lg * 4 + e;
+    for (int e = 0; e < 4; e++) rpos[e] = base + z0 + tw * 16 + lg * 4 + e;
     float mrun[4], srun[4];
     f32x4 o[NNT];
 #pragma unroll
@@ -2259,7 +2263,7 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
         // m the running max, s the running sum, acc the unnormalised output
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const uint32_t z = z0 + wave * 16 + lg * 4 + e;
+            const uint32_t z = z0 + tw * 16 + lg * 4 + e;
             if (z >= ntok) continue;
             const size_t ph = ((size_t)z * a.n_heads + h) * S + sp;
             if (li == 0) { a.m[ph] = mrun[e]; a.s[ph] = srun[e]; }
@@ -2272,7 +2276,7 @@ __global__ void __launch_bounds__(TPB) k_attn_flash(sgk_attn a) {
     // finish: o / s, sigmoid gate, store (lane: rows 4*lg+e, dims n*16+li)
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        const uint32_t z = z0 + wave * 16 + lg * 4 + e;
+        const uint32_t z = z0 + tw * 16 + lg * 4 + e;
         if (z >= ntok) continue;
         const float S = srun[e];
         float *out = a.out + (size_t)z * a.out_tok + (size_t)h * HD;
@@ -2308,12 +2312,17 @@ extern "C" hipError_t sgk_attn_flash(const sgk_attn *a, hipStream_t s) {
         S = min(a->max_splits, (a->seq + FA_SPLIT_KEYS - 1) / FA_SPLIT_KEYS);
     sgk_attn k = kv_resolved(a);
     k.max_splits = S;
-    dim3 grid(a->n_heads, (a->ntok + FA_TQ - 1) / FA_TQ, S);
+    // two query heads per workgroup when their group size allows
+    const uint32_t hw = (a->n_heads / a->n_kv) % 2 == 0 ? 2 : 1;
+    dim3 grid(a->n_heads / hw, (a->ntok + FA_TQ - 1) / FA_TQ, S);
+#define FLC(H) do { if (hw == 2) hipLaunchKernelGGL((k_attn_flash<H, 2>), grid, dim3(2 * TPB), 0, s, k);       \
+                     else hipLaunchKernelGGL((k_attn_flash<H, 1>), grid, dim3(TPB), 0, s, k); } while (0)
     switch (a->hd) {
-    case 64: hipLaunchKernelGGL(k_attn_flash<64>, grid, dim3(TPB), 0, s, k); break;
-    case 128: hipLaunchKernelGGL(k_attn_flash<128>, grid, dim3(TPB), 0, s, k); break;
-    case 256: hipLaunchKernelGGL(k_attn_flash<256>, grid, dim3(TPB), 0, s, k); break;
+    case 64: FLC(64); break;
+    case 128: FLC(128); break;
+    case 256: FLC(256); break;
     }
+#undef FLC
     if (S == 1) return hipGetLastError();
     sgk_attn c = k;
     c.steps = NULL;                 // every token has the same S splits
