@@ -1846,24 +1846,32 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     return SG_OK;
 }
 
+/* Y = X W^T with the GEMM epilogue `epi`. post_nw (SGK_EPI_ADD only): the
+ * next product over Y's rows takes RMSNorm(Y) with this weight on Q8
+ * weights; when this product splits K its reduce writes that split into
+ * pf_XS and sets *ready, and the next call passes it on (gemm_rows_norm). */
 static hipError_t gemm_rows(sg_gpu *g, const dmat *M, const float *X, uint32_t ldx, float *Y, uint32_t ldy,
-                            uint32_t n, int epi) {
+                            uint32_t n, int epi, const float *post_nw, int *ready) {
     sgk_gemm_args a = { X, M->qs, M->dt, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi, g->pf_XS, g->pf_PART,
-                        (uint64_t)4 * g->pf_chunk * g->cfg.hidden, NULL, 0.0f };
+                        (uint64_t)4 * g->pf_chunk * g->cfg.hidden, NULL, 0.0f, 0, post_nw, g->cfg.rms_eps,
+                        post_nw ? ready : NULL };
+    if (ready) *ready = 0;
     return sgk_gemm(&a, g->stream);
 }
 
 /* RMSNorm(X) (weight nw) then the GEMM: Q8 weights take the norm inside the
- * GEMM's bf16 split (one pass over X); f32 weights normalise into pf_Xn. */
+ * GEMM's bf16 split (one pass over X), or find it in pf_XS already when
+ * xs_ready (written by the previous product's reduce); f32 weights normalise
+ * into pf_Xn. */
 static hipError_t gemm_rows_norm(sg_gpu *g, const dmat *M, const float *X, const float *nw, float *Y,
-                                 uint32_t ldy, uint32_t n, int epi) {
+                                 uint32_t ldy, uint32_t n, int epi, int xs_ready) {
     const uint32_t H = g->cfg.hidden;
     if (!M->qs || !nw) {
         hipError_t e = sgk_rmsnorm_heads(X, nw, g->pf_Xn, H, n, H, g->cfg.rms_eps, g->stream);
-        return e != hipSuccess ? e : gemm_rows(g, M, g->pf_Xn, H, Y, ldy, n, epi);
+        return e != hipSuccess ? e : gemm_rows(g, M, g->pf_Xn, H, Y, ldy, n, epi, NULL, NULL);
     }
     sgk_gemm_args a = { X, M->qs, M->dt, M->wf, Y, n, M->rows, M->cols, H, ldy, epi, g->pf_XS, g->pf_PART,
-                        (uint64_t)4 * g->pf_chunk * H, nw, g->cfg.rms_eps };
+                        (uint64_t)4 * g->pf_chunk * H, nw, g->cfg.rms_eps, xs_ready, NULL, 0.0f, NULL };
     return sgk_gemm(&a, g->stream);
 }
 
@@ -1889,10 +1897,10 @@ sg_err sg_gpu_time_gemm(sg_gpu *g, uint32_t layer, uint32_t which, uint32_t n, u
         if (r == 1) he = hipEventRecord(a, s);
         if (he != hipSuccess) break;
         switch (which) {
-        case 0: he = gemm_rows_norm(g, &L->in, g->pf_X, L->ln1, g->pf_IN, L->in.rows, n, SGK_EPI_STORE); break;
-        case 1: he = gemm_rows(g, &L->out, ox, ow, g->pf_X, H, n, SGK_EPI_ADD); break;
-        case 2: he = gemm_rows_norm(g, &L->gu, g->pf_X, L->ln2, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU); break;
-        default: he = gemm_rows(g, &L->down, g->pf_FF, c->ffn_hidden, g->pf_X, H, n, SGK_EPI_ADD); break;
+        case 0: he = gemm_rows_norm(g, &L->in, g->pf_X, L->ln1, g->pf_IN, L->in.rows, n, SGK_EPI_STORE, 0); break;
+        case 1: he = gemm_rows(g, &L->out, ox, ow, g->pf_X, H, n, SGK_EPI_ADD, NULL, NULL); break;
+        case 2: he = gemm_rows_norm(g, &L->gu, g->pf_X, L->ln2, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU, 0); break;
+        default: he = gemm_rows(g, &L->down, g->pf_FF, c->ffn_hidden, g->pf_X, H, n, SGK_EPI_ADD, NULL, NULL); break;
         }
     }
     if (he == hipSuccess) he = hipEventRecord(b, s);
@@ -1911,10 +1919,13 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
     hipError_t e;
     const uint32_t H = c->hidden, hd = c->head_dim, qs = c->attn_output_gate ? 2 * hd : hd;
     if ((e = sgk_embed_rows(g->emb.qs, g->emb.d, g->emb.wf, H, g->pf_steps, n, g->pf_X, s)) != hipSuccess) return e;
+    int ready = 0;      /* pf_XS holds the next input projection's (or gate/up's) normed split */
     for (uint32_t i = 0; i < c->n_layers; i++) {
         glayer *L = &g->ls[i];
+        const glayer *Ln = i + 1 < c->n_layers ? &g->ls[i + 1] : NULL;
         const uint32_t in_rows = L->in.rows;
-        if ((e = gemm_rows_norm(g, &L->in, g->pf_X, L->ln1, g->pf_IN, in_rows, n, SGK_EPI_STORE)) != hipSuccess) return e;
+        if ((e = gemm_rows_norm(g, &L->in, g->pf_X, L->ln1, g->pf_IN, in_rows, n, SGK_EPI_STORE, ready)) != hipSuccess)
+            return e;
         if (L->attn) {
             sgk_attn A = {0};
             A.q = g->pf_IN; A.kc = L->kc; A.vc = L->vc; A.m = g->pf_m; A.s = g->pf_s; A.acc = g->pf_acc;
@@ -1931,7 +1942,9 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
                 if ((e = sgk_attn_partial(&A, s)) != hipSuccess) return e;
                 if ((e = sgk_attn_combine(&A, s)) != hipSuccess) return e;
             }
-            if ((e = gemm_rows(g, &L->out, g->pf_CTX, g->attn_width, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;
+            if ((e = gemm_rows(g, &L->out, g->pf_CTX, g->attn_width, g->pf_X, H, n, SGK_EPI_ADD, L->gu.qs ? L->ln2 : NULL,
+                               &ready)) != hipSuccess)
+                return e;
         } else {
             sgk_gdn d = {0};
             d.in = g->pf_IN; d.conv_w = L->conv_w; d.ring = L->ring; d.ssm_a = L->ssm_a; d.dt_bias = L->dt_bias;
@@ -1941,11 +1954,15 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
             if ((e = sgk_gdn_chunk(&d, g->pf_CONV, in_rows, n, g->pf_WY, s)) != hipSuccess) return e;
             if ((e = sgk_rmsnorm_gated_rows(g->pf_Y, g->pf_IN + g->conv_dim, in_rows, L->ssm_norm, g->pf_G,
                                             c->head_v_dim, c->n_v_heads, n, c->rms_eps, s)) != hipSuccess) return e;
-            if ((e = gemm_rows(g, &L->out, g->pf_G, g->value_dim, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;
+            if ((e = gemm_rows(g, &L->out, g->pf_G, g->value_dim, g->pf_X, H, n, SGK_EPI_ADD, L->gu.qs ? L->ln2 : NULL,
+                               &ready)) != hipSuccess)
+                return e;
         }
-        if ((e = gemm_rows_norm(g, &L->gu, g->pf_X, L->ln2, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU)) != hipSuccess)
+        if ((e = gemm_rows_norm(g, &L->gu, g->pf_X, L->ln2, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU, ready)) != hipSuccess)
             return e;
-        if ((e = gemm_rows(g, &L->down, g->pf_FF, c->ffn_hidden, g->pf_X, H, n, SGK_EPI_ADD)) != hipSuccess) return e;
+        if ((e = gemm_rows(g, &L->down, g->pf_FF, c->ffn_hidden, g->pf_X, H, n, SGK_EPI_ADD,
+                           Ln && Ln->in.qs ? Ln->ln1 : NULL, &ready)) != hipSuccess)
+            return e;
     }
     return hipSuccess;
 }

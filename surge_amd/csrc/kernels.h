@@ -277,6 +277,13 @@ typedef struct {
     uint64_t part_cap;       /* floats in part */
     const float *nw;         /* Q8 W only: RMSNorm X's rows first (weight nw, eps), or NULL */
     float eps;
+    int xs_ready;            /* Q8 W: xs already holds this product's split of X (with its RMSNorm) */
+    const float *post_nw;    /* SGK_EPI_ADD, Q8 W, Y rows M wide: when the product splits K, its reduce also
+                              * writes into xs the split of RMSNorm(Y rows) (weight post_nw, eps post_eps)
+                              * that the next Q8 product over Y takes (xs must hold 2*N*M bf16), and sets
+                              * *post_done (else 0) */
+    float post_eps;
+    int *post_done;
 } sgk_gemm_args;
 /* Q8 W needs K % 32 == 0, ldx % 4 == 0 and X 16-byte aligned. */
 hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s);

@@ -4473,6 +4473,57 @@ __global__ void __launch_bounds__(TPB) k_splitk_reduce(const float *P, uint32_t 
     }
 }
 
+// The split-K epilogue with += residual fused with the next product's input
+// split: workgroup n sums row n's S partials in order into Y (the arithmetic
+// of k_splitk_reduce<SGK_EPI_ADD>), then writes the bf16 hi | lo split of
+// RMSNorm(Y row n) with weight w (k_split_bf16_rms': the same per-thread order
+// of the sum of squares, block_sum, (y * r) * w), so both outputs are those
+// of the two kernels run one after the other.
+__global__ void __launch_bounds__(TPB) k_splitk_reduce_rms(const float *P, uint32_t S, uint32_t N, uint32_t M,
+                                                           float *Y, uint32_t ldy, const float *w, float eps,
+                                                           uint16_t *xs) {
+    __shared__ float red[4];
+    const uint32_t n = blockIdx.x, t = threadIdx.x;
+    const size_t nm = (size_t)N * M;
+    float *yr = Y + (size_t)n * ldy;
+    float ss = 0.0f;
+    // columns t, t + TPB, ... four at a time (all their loads in flight at
+    // once); the sum of squares still runs over them in increasing order
+    for (uint32_t i0 = t; i0 < M; i0 += 4 * TPB) {
+        float v[4], y[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t i = min(i0 + u * TPB, M - 1);
+            v[u] = P[(size_t)n * M + i];
+            y[u] = yr[i];
+        }
+        for (uint32_t k = 1; k < S; k++) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] += P[(size_t)k * nm + (size_t)n * M + min(i0 + u * TPB, M - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (i0 + u * TPB >= M) break;
+            y[u] += v[u];
+            yr[i0 + u * TPB] = y[u];
+            ss = fmaf(y[u], y[u], ss);
+        }
+    }
+    ss = block_sum(ss, red);                    // its barriers also publish the row's stores to the workgroup
+    const float r = 1.0f / sqrtf(ss / (float)M + eps);
+    for (uint32_t i = 4 * t; i < M; i += 4 * TPB) {
+        const float4 x4 = *(const float4 *)(yr + i);
+        const float4 w4 = *(const float4 *)(w + i);
+        const float v[4] = {(x4.x * r) * w4.x, (x4.y * r) * w4.y, (x4.z * r) * w4.z, (x4.w * r) * w4.w};
+        const bf16x2 h01 = {(__bf16)v[0], (__bf16)v[1]}, h23 = {(__bf16)v[2], (__bf16)v[3]};
+        const bf16x2 l01 = {(__bf16)(v[0] - (float)h01[0]), (__bf16)(v[1] - (float)h01[1])};
+        const bf16x2 l23 = {(__bf16)(v[2] - (float)h23[0]), (__bf16)(v[3] - (float)h23[1])};
+        uint16_t *o = xs + xs_at(N, n, i);
+        *(uint2 *)o = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+        *(uint2 *)(o + 32) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+    }
+}
+
 // Split-K epilogue of the tiles a SGK_EPI_TILE launch computed (tiles of
 // GM_TN tokens x TM rows): workgroup (t, part) takes 1/parts of the tile of
 // index t + boff, parts = GM_TN*TM / (4*TPB); each thread requests its 4
@@ -4544,9 +4595,14 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
         const uint64_t total = (uint64_t)a->N * k4;
         const uint32_t sg = (uint32_t)min((total + TPB - 1) / TPB, (uint64_t)4096);
         if (a->nw && ((uintptr_t)a->nw & 15)) return hipErrorInvalidValue;
-        if (a->nw) hipLaunchKernelGGL(k_split_bf16_rms, dim3(a->N), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->nw,
-                                      a->eps, a->xs);
-        else hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
+        if (a->post_done) *a->post_done = 0;
+        if (a->xs_ready) {
+            // the previous product's reduce wrote this split
+        } else if (a->nw) {
+            hipLaunchKernelGGL(k_split_bf16_rms, dim3(a->N), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->nw, a->eps, a->xs);
+        } else {
+            hipLaunchKernelGGL(k_split_bf16, dim3(sg), dim3(TPB), 0, s, a->X, a->ldx, a->N, a->K, a->xs);
+        }
         const int kind = gemm_kind();
         const uint32_t TM = kind == GEMM_WIDE ? GX_TM : GM_TM;
         const uint32_t mb = (a->M + TM - 1) / TM, nb = (a->N + GM_TN - 1) / GM_TN;
@@ -4579,6 +4635,15 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
         }
         if (S > 1) {
             GL(SGK_EPI_STORE, dim3(grid, S), a->part, a->M, (uint64_t)a->N * a->M, 0u);
+            if (a->epi == SGK_EPI_ADD && a->post_nw && a->post_done && a->ldy % 4 == 0 && a->M % 32 == 0 &&
+                !((uintptr_t)a->Y & 15) && !((uintptr_t)a->post_nw & 15)) {
+                // the residual add fused with the next product's RMSNorm and split (into this
+                // product's xs, which it has finished reading)
+                hipLaunchKernelGGL(k_splitk_reduce_rms, dim3(a->N), dim3(TPB), 0, s, a->part, S, a->N, a->M, a->Y, a->ldy,
+                                   a->post_nw, a->post_eps, a->xs);
+                *a->post_done = 1;
+                return hipGetLastError();
+            }
             const uint32_t rg = (uint32_t)min(((uint64_t)a->N * a->M + TPB - 1) / TPB, (uint64_t)4096);
 #define GR(E) hipLaunchKernelGGL((k_splitk_reduce<E>), dim3(rg), dim3(TPB), 0, s, a->part, S, a->N, a->M, a->Y, a->ldy)
             if (a->epi == SGK_EPI_ADD) GR(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GR(SGK_EPI_SWIGLU); else GR(SGK_EPI_STORE);
