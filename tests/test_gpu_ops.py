@@ -447,7 +447,9 @@ def test_gdn_step_rejects_bad_shapes(gpu):
             gpu.gdn_step(b, b, o, o, p)
 
 
-FLASH_CASES = [(24, 4, 256, 1536, 64), (24, 4, 256, 4000, 37), (16, 4, 128, 2100, 100)]
+# even GQA groups run two query heads per workgroup, odd ones (12/4, 6/6) one
+FLASH_CASES = [(24, 4, 256, 1536, 64), (24, 4, 256, 4000, 37), (16, 4, 128, 2100, 100), (12, 4, 128, 1300, 70),
+               (6, 6, 64, 900, 33)]
 
 
 @pytest.mark.parametrize("nh,nkv,hd,base,n", FLASH_CASES, ids=[f"{a}q{b}kv-hd{c}-base{d}-n{e}" for a, b, c, d, e in FLASH_CASES])
