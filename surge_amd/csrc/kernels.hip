@@ -2113,7 +2113,7 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
     // K staging: a key row is KC8 16-byte chunks; consecutive threads take
     // consecutive chunks of a row (contiguous LDS stores, coalesced loads),
     // KPP rows per pass, KNP passes per 64-key tile
-    constexpr int KC8 = HD / 8, KPP = TPB * HW / KC8, KNP = (FA_TK + KPP - 1) / KPP;
+    constexpr int KC8 = HD / 8, KPP = TPB / KC8, KNP = (FA_TK + KPP - 1) / KPP;
     constexpr int VDC = HD / 8;                  // V staging: dim chunks of 8 (threads 8*vdc + vkg)
     __shared__ __align__(16) uint16_t ks[FA_TK * KLD];
     __shared__ __align__(16) uint16_t vt[HD * FA_PLD];
@@ -2154,30 +2154,46 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
 #pragma unroll
     for (int n = 0; n < NNT; n++) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
+    // Staging roles (256 threads each): with two heads per workgroup waves
+    // 0-3 stage K and waves 4-7 V^T, with one head every thread does both.
+    // A tile's loads are requested right after the barrier that follows the
+    // previous tile's stores, so they arrive while that tile is computed.
+    const bool k_role = HW == 1 || t < TPB, v_role = HW == 1 || t >= TPB;
+    const uint32_t tv = HW == 1 ? t : t - TPB;
     const uint32_t kk = t / KC8, kd = (t % KC8) * 8;        // K staging role: rows kk + u*KPP
     // V staging role: consecutive threads take consecutive key groups of one
     // dim chunk, so 8 lanes store 128 contiguous bytes of a V^T row
-    const uint32_t vkg = t % (FA_TK / 8), vdc = t / (FA_TK / 8);
-    for (uint32_t k0 = kbeg; k0 < kstop; k0 += FA_TK) {
-        // stage K [key][dim] and V^T [dim][key] (keys clamped into the range)
-        {
-            v4u r[KNP];
+    const uint32_t vkg = tv % (FA_TK / 8), vdc = tv / (FA_TK / 8);
+    const bool v_on = v_role && vdc < (uint32_t)VDC;
+    // one register array for both roles: with two heads per workgroup a wave
+    // has one role (K in sr[0..KNP), V in sr[0..8)), with one head both
+    constexpr int VO = HW == 2 ? 0 : KNP, NSR = HW == 2 ? (KNP > 8 ? KNP : 8) : KNP + 8;
+    v4u sr[NSR];
+    auto stage_load = [&](uint32_t k0) {         // keys clamped into the range
+        if (k_role) {
 #pragma unroll
             for (int u = 0; u < KNP; u++) {
                 const uint32_t key = min(k0 + min(kk + u * KPP, (uint32_t)FA_TK - 1), kend - 1);
-                r[u] = *(const v4u *)(kc + kv_at(a, key, hk) + kd);
+                sr[u] = *(const v4u *)(kc + kv_at(a, key, hk) + kd);
             }
-#pragma unroll
-            for (int u = 0; u < KNP; u++)
-                if (kk < (uint32_t)KPP && kk + u * KPP < (uint32_t)FA_TK) *(v4u *)&ks[(kk + u * KPP) * KLD + kd] = r[u];
         }
-        if (vdc < (uint32_t)VDC) {
-            v4u r[8];
+        if (v_on) {
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const uint32_t key = min(k0 + vkg * 8 + j, kend - 1);
-                r[j] = *(const v4u *)(vc + kv_at(a, key, hk) + vdc * 8);
+                sr[VO + j] = *(const v4u *)(vc + kv_at(a, key, hk) + vdc * 8);
             }
+        }
+    };
+    if (kbeg < kstop) stage_load(kbeg);
+    for (uint32_t k0 = kbeg; k0 < kstop; k0 += FA_TK) {
+        // stage K [key][dim] and V^T [dim][key]
+        if (k_role) {
+#pragma unroll
+            for (int u = 0; u < KNP; u++)
+                if (kk + u * KPP < (uint32_t)FA_TK) *(v4u *)&ks[(kk + u * KPP) * KLD + kd] = sr[u];
+        }
+        if (v_on) {
 #pragma unroll
             for (int dd = 0; dd < 8; dd++) {
                 // half dd of keys 0..7, packed in key order
@@ -2185,11 +2201,12 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
                 v4u out;
 #pragma unroll
                 for (int w = 0; w < 4; w++)
-                    out[w] = __builtin_amdgcn_perm(r[2 * w + 1][dd >> 1], r[2 * w][dd >> 1], sel);
+                    out[w] = __builtin_amdgcn_perm(sr[VO + 2 * w + 1][dd >> 1], sr[VO + 2 * w][dd >> 1], sel);
                 *(v4u *)&vt[(vdc * 8 + dd) * FA_PLD + vkg * 8] = out;
             }
         }
         __syncthreads();
+        if (k0 + FA_TK < kstop) stage_load(k0 + FA_TK);
         // scores of this wave's 16 tokens x 64 keys
         f32x4 sc[NSC];
 #pragma unroll
