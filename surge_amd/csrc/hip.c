@@ -117,6 +117,7 @@ struct sg_gpu {
     sgk_step *pf_steps, *pf_hsteps;
     float *pf_X, *pf_Xn, *pf_IN, *pf_CONV, *pf_Y, *pf_G, *pf_CTX, *pf_FF, *pf_m, *pf_s, *pf_acc;
     uint16_t *pf_XS;        /* the prefill GEMMs' X split into bf16 hi | lo */
+    uint16_t *pf_XS2;       /* a second split: gate/up writes the down projection's into it */
     float *pf_PART;         /* split-K partials of the narrow prefill GEMMs: 4 x chunk x hidden */
     float *pf_WY;           /* the chunked DeltaNet scan's per-(head, sub-chunk) workspace */
 
@@ -1115,7 +1116,7 @@ static void state_free(sg_gpu *g) {
         void **pb[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
                         (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
                         (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc,
-                        (void **)&g->pf_XS, (void **)&g->pf_PART, (void **)&g->pf_WY };
+                        (void **)&g->pf_XS, (void **)&g->pf_PART, (void **)&g->pf_WY, (void **)&g->pf_XS2 };
         for (size_t i = 0; i < sizeof pb / sizeof *pb; i++) { dfree(g, *pb[i]); *pb[i] = NULL; }
         g->pf_chunk = 0;
     }
@@ -1821,7 +1822,7 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     void **bufs[] = { (void **)&g->pf_steps, (void **)&g->pf_X, (void **)&g->pf_Xn, (void **)&g->pf_IN,
                       (void **)&g->pf_CONV, (void **)&g->pf_Y, (void **)&g->pf_G, (void **)&g->pf_CTX,
                       (void **)&g->pf_FF, (void **)&g->pf_m, (void **)&g->pf_s, (void **)&g->pf_acc,
-                      (void **)&g->pf_XS, (void **)&g->pf_PART, (void **)&g->pf_WY };
+                      (void **)&g->pf_XS, (void **)&g->pf_PART, (void **)&g->pf_WY, (void **)&g->pf_XS2 };
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) { dfree(g, *bufs[i]); *bufs[i] = NULL; }
     if (g->pf_hsteps) { hipHostFree(g->pf_hsteps); g->pf_hsteps = NULL; }
     g->pf_chunk = 0;
@@ -1836,7 +1837,8 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     uint64_t sizes[] = { n * sizeof(sgk_step), n * c->hidden * 4, n * c->hidden * 4, n * in_rows * 4,
                          n * g->conv_dim * 4 + 4, n * g->value_dim * 4 + 4, n * g->value_dim * 4 + 4,
                          n * g->attn_width * 4 + 4, n * c->ffn_hidden * 4, ah * 4, ah * 4, ah * c->head_dim * 4,
-                         n * kmax * 4, 4 * n * c->hidden * 4, sgk_delta_wy_ws_floats(c->n_v_heads, chunk) * 4 + 4 };
+                         n * kmax * 4, 4 * n * c->hidden * 4, sgk_delta_wy_ws_floats(c->n_v_heads, chunk) * 4 + 4,
+                         n * kmax * 4 };
     sg_err e = SG_OK;
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs && !sg_failed(e); i++) e = dzalloc(g, sizes[i], bufs[i]);
     if (!sg_failed(e) && hipHostMalloc((void **)&g->pf_hsteps, n * sizeof(sgk_step), 0) != hipSuccess)
@@ -1850,29 +1852,39 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
  * next product over Y's rows takes RMSNorm(Y) with this weight on Q8
  * weights; when this product splits K its reduce writes that split into
  * pf_XS and sets *ready, and the next call passes it on (gemm_rows_norm). */
-static hipError_t gemm_rows(sg_gpu *g, const dmat *M, const float *X, uint32_t ldx, float *Y, uint32_t ldy,
-                            uint32_t n, int epi, const float *post_nw, int *ready) {
-    sgk_gemm_args a = { X, M->qs, M->dt, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi, g->pf_XS, g->pf_PART,
-                        (uint64_t)4 * g->pf_chunk * g->cfg.hidden, NULL, 0.0f, 0, post_nw, g->cfg.rms_eps,
-                        post_nw ? ready : NULL };
+static hipError_t gemm_rows_x(sg_gpu *g, const dmat *M, const float *X, uint32_t ldx, float *Y, uint32_t ldy,
+                              uint32_t n, int epi, const float *post_nw, int *ready, int xs_ready, uint16_t *xs) {
+    sgk_gemm_args a = { X, M->qs, M->dt, M->wf, Y, n, M->rows, M->cols, ldx, ldy, epi, xs, g->pf_PART,
+                        (uint64_t)4 * g->pf_chunk * g->cfg.hidden, NULL, 0.0f, xs_ready, post_nw, g->cfg.rms_eps,
+                        post_nw ? ready : NULL, NULL };
     if (ready) *ready = 0;
     return sgk_gemm(&a, g->stream);
+}
+
+static hipError_t gemm_rows(sg_gpu *g, const dmat *M, const float *X, uint32_t ldx, float *Y, uint32_t ldy,
+                            uint32_t n, int epi, const float *post_nw, int *ready) {
+    return gemm_rows_x(g, M, X, ldx, Y, ldy, n, epi, post_nw, ready, 0, g->pf_XS);
 }
 
 /* RMSNorm(X) (weight nw) then the GEMM: Q8 weights take the norm inside the
  * GEMM's bf16 split (one pass over X), or find it in pf_XS already when
  * xs_ready (written by the previous product's reduce); f32 weights normalise
  * into pf_Xn. */
-static hipError_t gemm_rows_norm(sg_gpu *g, const dmat *M, const float *X, const float *nw, float *Y,
-                                 uint32_t ldy, uint32_t n, int epi, int xs_ready) {
+static hipError_t gemm_rows_norm_x(sg_gpu *g, const dmat *M, const float *X, const float *nw, float *Y,
+                                   uint32_t ldy, uint32_t n, int epi, int xs_ready, uint16_t *xs, uint16_t *ys) {
     const uint32_t H = g->cfg.hidden;
     if (!M->qs || !nw) {
         hipError_t e = sgk_rmsnorm_heads(X, nw, g->pf_Xn, H, n, H, g->cfg.rms_eps, g->stream);
         return e != hipSuccess ? e : gemm_rows(g, M, g->pf_Xn, H, Y, ldy, n, epi, NULL, NULL);
     }
-    sgk_gemm_args a = { X, M->qs, M->dt, M->wf, Y, n, M->rows, M->cols, H, ldy, epi, g->pf_XS, g->pf_PART,
-                        (uint64_t)4 * g->pf_chunk * H, nw, g->cfg.rms_eps, xs_ready, NULL, 0.0f, NULL };
+    sgk_gemm_args a = { X, M->qs, M->dt, M->wf, Y, n, M->rows, M->cols, H, ldy, epi, xs, g->pf_PART,
+                        (uint64_t)4 * g->pf_chunk * H, nw, g->cfg.rms_eps, xs_ready, NULL, 0.0f, NULL, ys };
     return sgk_gemm(&a, g->stream);
+}
+
+static hipError_t gemm_rows_norm(sg_gpu *g, const dmat *M, const float *X, const float *nw, float *Y,
+                                 uint32_t ldy, uint32_t n, int epi, int xs_ready) {
+    return gemm_rows_norm_x(g, M, X, nw, Y, ldy, n, epi, xs_ready, g->pf_XS, NULL);
 }
 
 static sg_err timed(sg_gpu *g, hipEvent_t a, hipEvent_t b, uint32_t reps, double *us);
@@ -1919,12 +1931,18 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
     hipError_t e;
     const uint32_t H = c->hidden, hd = c->head_dim, qs = c->attn_output_gate ? 2 * hd : hd;
     if ((e = sgk_embed_rows(g->emb.qs, g->emb.d, g->emb.wf, H, g->pf_steps, n, g->pf_X, s)) != hipSuccess) return e;
-    int ready = 0;      /* pf_XS holds the next input projection's (or gate/up's) normed split */
+    /* ready: rxs holds the next product's normed split (written by the reduce
+     * of the product before). Splits go to pf_XS, except the down projection's
+     * input, which gate/up writes into pf_XS2 (it reads pf_XS meanwhile), and
+     * what the down projection's reduce writes into its own split, pf_XS2. */
+    int ready = 0;
+    uint16_t *rxs = g->pf_XS;
     for (uint32_t i = 0; i < c->n_layers; i++) {
         glayer *L = &g->ls[i];
         const glayer *Ln = i + 1 < c->n_layers ? &g->ls[i + 1] : NULL;
         const uint32_t in_rows = L->in.rows;
-        if ((e = gemm_rows_norm(g, &L->in, g->pf_X, L->ln1, g->pf_IN, in_rows, n, SGK_EPI_STORE, ready)) != hipSuccess)
+        if ((e = gemm_rows_norm_x(g, &L->in, g->pf_X, L->ln1, g->pf_IN, in_rows, n, SGK_EPI_STORE, ready,
+                                  ready ? rxs : g->pf_XS, NULL)) != hipSuccess)
             return e;
         if (L->attn) {
             sgk_attn A = {0};
@@ -1945,6 +1963,7 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
             if ((e = gemm_rows(g, &L->out, g->pf_CTX, g->attn_width, g->pf_X, H, n, SGK_EPI_ADD, L->gu.qs ? L->ln2 : NULL,
                                &ready)) != hipSuccess)
                 return e;
+            rxs = g->pf_XS;
         } else {
             sgk_gdn d = {0};
             d.in = g->pf_IN; d.conv_w = L->conv_w; d.ring = L->ring; d.ssm_a = L->ssm_a; d.dt_bias = L->dt_bias;
@@ -1952,17 +1971,27 @@ static hipError_t prefill_chunk(sg_gpu *g, uint32_t base, uint32_t n) {
             d.dk = c->head_k_dim; d.dv = c->head_v_dim; d.conv_dim = g->conv_dim; d.ksize = c->conv_kernel;
             d.tiled = g->model->v_heads_tiled; d.neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
             if ((e = sgk_gdn_chunk(&d, g->pf_CONV, in_rows, n, g->pf_WY, s)) != hipSuccess) return e;
-            if ((e = sgk_rmsnorm_gated_rows(g->pf_Y, g->pf_IN + g->conv_dim, in_rows, L->ssm_norm, g->pf_G,
-                                            c->head_v_dim, c->n_v_heads, n, c->rms_eps, s)) != hipSuccess) return e;
-            if ((e = gemm_rows(g, &L->out, g->pf_G, g->value_dim, g->pf_X, H, n, SGK_EPI_ADD, L->gu.qs ? L->ln2 : NULL,
-                               &ready)) != hipSuccess)
+            /* RMSNormGated; with Q8 output weights written straight as their GEMM's bf16 split */
+            const int gsplit = L->out.qs != NULL;
+            if (gsplit) e = sgk_rmsnorm_gated_split(g->pf_Y, g->pf_IN + g->conv_dim, in_rows, L->ssm_norm, g->pf_XS,
+                                                    c->head_v_dim, c->n_v_heads, n, c->rms_eps, s);
+            else e = sgk_rmsnorm_gated_rows(g->pf_Y, g->pf_IN + g->conv_dim, in_rows, L->ssm_norm, g->pf_G,
+                                            c->head_v_dim, c->n_v_heads, n, c->rms_eps, s);
+            if (e != hipSuccess) return e;
+            if ((e = gemm_rows_x(g, &L->out, g->pf_G, g->value_dim, g->pf_X, H, n, SGK_EPI_ADD,
+                                 L->gu.qs ? L->ln2 : NULL, &ready, gsplit, g->pf_XS)) != hipSuccess)
                 return e;
+            rxs = g->pf_XS;
         }
-        if ((e = gemm_rows_norm(g, &L->gu, g->pf_X, L->ln2, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU, ready)) != hipSuccess)
+        /* gate/up with Q8 down weights writes its SwiGLU output as the down projection's split */
+        uint16_t *ys = L->gu.qs && L->down.qs ? g->pf_XS2 : NULL;
+        if ((e = gemm_rows_norm_x(g, &L->gu, g->pf_X, L->ln2, g->pf_FF, c->ffn_hidden, n, SGK_EPI_SWIGLU, ready,
+                                  ready ? rxs : g->pf_XS, ys)) != hipSuccess)
             return e;
-        if ((e = gemm_rows(g, &L->down, g->pf_FF, c->ffn_hidden, g->pf_X, H, n, SGK_EPI_ADD,
-                           Ln && Ln->in.qs ? Ln->ln1 : NULL, &ready)) != hipSuccess)
+        if ((e = gemm_rows_x(g, &L->down, g->pf_FF, c->ffn_hidden, g->pf_X, H, n, SGK_EPI_ADD,
+                             Ln && Ln->in.qs ? Ln->ln1 : NULL, &ready, ys != NULL, ys ? ys : g->pf_XS)) != hipSuccess)
             return e;
+        rxs = ys ? ys : g->pf_XS;
     }
     return hipSuccess;
 }

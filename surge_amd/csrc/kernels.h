@@ -63,7 +63,8 @@ static inline uint32_t sgk_n_splits(uint32_t seq) { return sgk_n_splits_cap(seq,
  * each output row). */
 enum { SGK_PRO_NONE = 0, SGK_PRO_RMS = 1, SGK_PRO_GATED = 2 };
 #define SGK_GATED_MAX_HEADS 256u
-enum { SGK_EPI_STORE = 0, SGK_EPI_ADD = 1, SGK_EPI_SWIGLU = 2, SGK_EPI_TILE = 3 /* prefill GEMM internal */ };
+enum { SGK_EPI_STORE = 0, SGK_EPI_ADD = 1, SGK_EPI_SWIGLU = 2,
+       SGK_EPI_TILE = 3, SGK_EPI_SWIGLU_XS = 4 /* prefill GEMM internal */ };
 
 typedef struct {
     const int8_t *qs;       /* Q8: int8 plane [rows][cols] */
@@ -231,6 +232,11 @@ hipError_t sgk_delta_gates_chunk(const float *a, const float *b, float *gates, c
 hipError_t sgk_rmsnorm_gated_rows(const float *y, const float *z, uint32_t z_stride, const float *w,
                                   float *out, uint32_t dv, uint32_t n_v, uint32_t ntok, float eps,
                                   hipStream_t s);
+/* The same with the result written as the next prefill product's bf16 hi | lo
+ * split of its X rows (sgk_gemm_args.xs layout, N = ntok, K = n_v*dv, which
+ * must be a multiple of 32), for a product called with xs_ready. */
+hipError_t sgk_rmsnorm_gated_split(const float *y, const float *z, uint32_t z_stride, const float *w,
+                                   uint16_t *xs, uint32_t dv, uint32_t n_v, uint32_t ntok, float eps, hipStream_t s);
 /* Embedding rows for a chunk: X[z] = row steps[z].token. */
 hipError_t sgk_embed_rows(const int8_t *qs, const uint16_t *d, const float *wf, uint32_t hidden,
                           const sgk_step *steps, uint32_t ntok, float *X, hipStream_t s);
@@ -284,6 +290,9 @@ typedef struct {
                               * *post_done (else 0) */
     float post_eps;
     int *post_done;
+    uint16_t *ys;            /* SGK_EPI_SWIGLU, Q8 W: the SwiGLU outputs written as the next product's bf16
+                              * split (the xs layout, N rows of M/2, (M/2) % 32 == 0) instead of into Y;
+                              * must not alias xs */
 } sgk_gemm_args;
 /* Q8 W needs K % 32 == 0, ldx % 4 == 0 and X 16-byte aligned. */
 hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s);

@@ -3850,6 +3850,13 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ size_t xs_at(uint32_t N, uint32_t n, uint32_t k) {
     return ((size_t)(k >> 5) * N + n) * 64 + (k & 31);
 }
+// one value of X into the split: hi = bf16(v), lo = bf16(v - hi), as k_split_bf16 rounds them
+__device__ __forceinline__ void xs_put(uint16_t *xs, uint32_t N, uint32_t n, uint32_t k, float v) {
+    const __bf16 hi = (__bf16)v, lo = (__bf16)(v - (float)hi);
+    uint16_t *o = xs + xs_at(N, n, k);
+    o[0] = __builtin_bit_cast(uint16_t, hi);
+    o[32] = __builtin_bit_cast(uint16_t, lo);
+}
 __global__ void __launch_bounds__(TPB) k_split_bf16(const float *X, uint32_t ldx, uint32_t N, uint32_t K,
                                                     uint16_t *xs) {
     const uint32_t k4 = K >> 2;
@@ -3864,6 +3871,38 @@ __global__ void __launch_bounds__(TPB) k_split_bf16(const float *X, uint32_t ldx
         *(uint2 *)o = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
         *(uint2 *)(o + 32) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
     }
+}
+
+// k_rmsnorm_gated_rows' arithmetic (one wave per (value head, token)) with
+// its output written straight as the next product's bf16 hi | lo split, with
+// k_split_bf16's rounding, at xs_at(N, z, h*dv + j) ((n_v*dv) % 32 == 0).
+__global__ void k_rmsnorm_gated_split(const float *y, const float *zsrc, uint32_t z_stride, const float *w,
+                                      uint16_t *xs, uint32_t N, uint32_t dv, uint32_t n_v, float eps) {
+    const uint32_t lane = threadIdx.x & 63, h = blockIdx.x * (TPB / 64) + (threadIdx.x >> 6), z = blockIdx.y;
+    if (h >= n_v) return;
+    const float *yh = y + (size_t)z * n_v * dv + (size_t)h * dv;
+    const float *zh = zsrc + (size_t)z * z_stride + (size_t)h * dv;
+    float ss = 0.0f;
+    for (uint32_t j = lane; j < dv; j += 64) ss = fmaf(yh[j], yh[j], ss);
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)dv + eps);
+    for (uint32_t j = lane; j < dv; j += 64) {
+        const float v = silu(zh[j]) * ((yh[j] * r) * w[j]);
+        const __bf16 hi = (__bf16)v, lo = (__bf16)(v - (float)hi);
+        uint16_t *o = xs + xs_at(N, z, h * dv + j);
+        o[0] = __builtin_bit_cast(uint16_t, hi);
+        o[32] = __builtin_bit_cast(uint16_t, lo);
+    }
+}
+
+extern "C" hipError_t sgk_rmsnorm_gated_split(const float *y, const float *z, uint32_t z_stride, const float *w,
+                                              uint16_t *xs, uint32_t dv, uint32_t n_v, uint32_t ntok, float eps,
+                                              hipStream_t s) {
+    if (!ntok || !n_v) return hipSuccess;
+    if (((uint64_t)n_v * dv) % 32 || ((uintptr_t)xs & 15)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rmsnorm_gated_split, dim3((n_v + 3) / 4, ntok), dim3(TPB), 0, s, y, z, z_stride, w, xs, ntok,
+                       dv, n_v, eps);
+    return hipGetLastError();
 }
 
 // RMSNorm fused into the split: one workgroup per row n, the row's factor
@@ -4111,6 +4150,9 @@ k_gemm_q8_mfma(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
                 } else if (EPI == SGK_EPI_SWIGLU) {
                     const float up = lane_xor1(v);            // column m+1 lives in lane li^1
                     if (!(li & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(v) * up;
+                } else if (EPI == SGK_EPI_SWIGLU_XS) {        // Y is the next product's split
+                    const float up = lane_xor1(v);
+                    if (!(li & 1) && n < N && m + 1 < M) xs_put((uint16_t *)Y, N, n, m >> 1, silu(v) * up);
                 } else if (n < N && m < M) {
                     if (EPI == SGK_EPI_ADD) Y[(size_t)n * ldy + m] += v;
                     else Y[(size_t)n * ldy + m] = v;
@@ -4283,6 +4325,9 @@ k_gemm_q8_ws(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y, 
                 } else if (EPI == SGK_EPI_SWIGLU) {
                     const float up = lane_xor1(v);            // column m+1 lives in lane li^1
                     if (!(li & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(v) * up;
+                } else if (EPI == SGK_EPI_SWIGLU_XS) {        // Y is the next product's split
+                    const float up = lane_xor1(v);
+                    if (!(li & 1) && n < N && m + 1 < M) xs_put((uint16_t *)Y, N, n, m >> 1, silu(v) * up);
                 } else if (n < N && m < M) {
                     if (EPI == SGK_EPI_ADD) Y[(size_t)n * ldy + m] += v;
                     else Y[(size_t)n * ldy + m] = v;
@@ -4461,6 +4506,9 @@ k_gemm_q8_wide(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
                 } else if (EPI == SGK_EPI_SWIGLU) {
                     const float up = lane_xor1(v);            // column m+1 lives in lane li^1
                     if (!(li & 1) && n < N && m + 1 < M) Y[(size_t)n * ldy + (m >> 1)] = silu(v) * up;
+                } else if (EPI == SGK_EPI_SWIGLU_XS) {        // Y is the next product's split
+                    const float up = lane_xor1(v);
+                    if (!(li & 1) && n < N && m + 1 < M) xs_put((uint16_t *)Y, N, n, m >> 1, silu(v) * up);
                 } else if (n < N && m < M) {
                     if (EPI == SGK_EPI_ADD) Y[(size_t)n * ldy + m] += v;
                     else Y[(size_t)n * ldy + m] = v;
@@ -4473,15 +4521,16 @@ k_gemm_q8_wide(const uint16_t *xs, const int8_t *qs, const uint16_t *d, float *Y
 template <int EPI>
 __global__ void __launch_bounds__(TPB) k_splitk_reduce(const float *P, uint32_t S, uint32_t N, uint32_t M,
                                                        float *Y, uint32_t ldy) {
-    const size_t nm = (size_t)N * M, step = EPI == SGK_EPI_SWIGLU ? 2 : 1;
+    const size_t nm = (size_t)N * M, step = EPI == SGK_EPI_SWIGLU || EPI == SGK_EPI_SWIGLU_XS ? 2 : 1;
     for (size_t i = ((size_t)blockIdx.x * TPB + threadIdx.x) * step; i < nm; i += (size_t)gridDim.x * TPB * step) {
         const uint32_t n = (uint32_t)(i / M), m = (uint32_t)(i - (size_t)n * M);
         float v = P[i];
         for (uint32_t k = 1; k < S; k++) v += P[(size_t)k * nm + i];
-        if (EPI == SGK_EPI_SWIGLU) {
+        if (EPI == SGK_EPI_SWIGLU || EPI == SGK_EPI_SWIGLU_XS) {
             float u = P[i + 1];
             for (uint32_t k = 1; k < S; k++) u += P[(size_t)k * nm + i + 1];
-            Y[(size_t)n * ldy + (m >> 1)] = silu(v) * u;
+            if (EPI == SGK_EPI_SWIGLU_XS) xs_put((uint16_t *)Y, N, n, m >> 1, silu(v) * u);
+            else Y[(size_t)n * ldy + (m >> 1)] = silu(v) * u;
         } else if (EPI == SGK_EPI_ADD) {
             Y[(size_t)n * ldy + m] += v;
         } else {
@@ -4575,6 +4624,11 @@ __global__ void __launch_bounds__(TPB) k_tile_reduce(const float *P, uint32_t S,
         if (m + 3 < M) y[(m >> 1) + 1] = silu(v.z) * v.w;
         return;
     }
+    if (EPI == SGK_EPI_SWIGLU_XS) {             // Y is the next product's split
+        if (m + 1 < M) xs_put((uint16_t *)Y, N, n, m >> 1, silu(v.x) * v.y);
+        if (m + 3 < M) xs_put((uint16_t *)Y, N, n, (m >> 1) + 1, silu(v.z) * v.w);
+        return;
+    }
     const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -4604,6 +4658,10 @@ __global__ void __launch_bounds__(TPB) k_gemm_f32(const float *X, const float *W
 extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
     if (!a->N || !a->M || !a->K) return hipSuccess;
     if (a->epi == SGK_EPI_SWIGLU && (a->M & 1)) return hipErrorInvalidValue;
+    if (a->ys && (a->epi != SGK_EPI_SWIGLU || !a->qs || (a->M / 2) % 32 || a->ys == a->xs)) return hipErrorInvalidValue;
+    // the SwiGLU outputs as the next product's split: the launches below take ys for Y
+    const int epi = a->ys ? SGK_EPI_SWIGLU_XS : a->epi;
+    float *const Yo = a->ys ? (float *)a->ys : a->Y;
     if (a->nw && !a->qs) return hipErrorInvalidValue;      // the fused RMSNorm is part of the Q8 split
     if (a->qs) {
         if (a->K % 32 || !a->xs || !a->dt || a->ldx % 4 || ((uintptr_t)a->X & 15) || ((uintptr_t)a->xs & 15))
@@ -4662,8 +4720,11 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
                 return hipGetLastError();
             }
             const uint32_t rg = (uint32_t)min(((uint64_t)a->N * a->M + TPB - 1) / TPB, (uint64_t)4096);
-#define GR(E) hipLaunchKernelGGL((k_splitk_reduce<E>), dim3(rg), dim3(TPB), 0, s, a->part, S, a->N, a->M, a->Y, a->ldy)
-            if (a->epi == SGK_EPI_ADD) GR(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GR(SGK_EPI_SWIGLU); else GR(SGK_EPI_STORE);
+#define GR(E) hipLaunchKernelGGL((k_splitk_reduce<E>), dim3(rg), dim3(TPB), 0, s, a->part, S, a->N, a->M, Yo, a->ldy)
+            if (epi == SGK_EPI_ADD) GR(SGK_EPI_ADD);
+            else if (epi == SGK_EPI_SWIGLU) GR(SGK_EPI_SWIGLU);
+            else if (epi == SGK_EPI_SWIGLU_XS) GR(SGK_EPI_SWIGLU_XS);
+            else GR(SGK_EPI_STORE);
 #undef GR
             return hipGetLastError();
         }
@@ -4677,15 +4738,19 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
             }
             if (S2 < 2) full = grid;
         }
-        if (a->epi == SGK_EPI_ADD) GL(SGK_EPI_ADD, dim3(full), a->Y, a->ldy, (uint64_t)0, 0u);
-        else if (a->epi == SGK_EPI_SWIGLU) GL(SGK_EPI_SWIGLU, dim3(full), a->Y, a->ldy, (uint64_t)0, 0u);
+        if (epi == SGK_EPI_ADD) GL(SGK_EPI_ADD, dim3(full), a->Y, a->ldy, (uint64_t)0, 0u);
+        else if (epi == SGK_EPI_SWIGLU) GL(SGK_EPI_SWIGLU, dim3(full), a->Y, a->ldy, (uint64_t)0, 0u);
+        else if (epi == SGK_EPI_SWIGLU_XS) GL(SGK_EPI_SWIGLU_XS, dim3(full), Yo, a->ldy, (uint64_t)0, 0u);
         else GL(SGK_EPI_STORE, dim3(full), a->Y, a->ldy, (uint64_t)0, 0u);
         if (full < grid) {
             const uint32_t left = grid - full;
             GL(SGK_EPI_TILE, dim3(left, S2), a->part, 0u, (uint64_t)0, full);
-#define GT(E, TMV) hipLaunchKernelGGL((k_tile_reduce<E, TMV>), dim3(left, gm_tr_parts<TMV>()), dim3(TPB), 0, s, a->part, S2, left, full, a->N, a->M, a->Y, a->ldy)
+#define GT(E, TMV) hipLaunchKernelGGL((k_tile_reduce<E, TMV>), dim3(left, gm_tr_parts<TMV>()), dim3(TPB), 0, s, a->part, S2, left, full, a->N, a->M, Yo, a->ldy)
 #define GT2(E) do { if (kind == GEMM_WIDE) GT(E, GX_TM); else GT(E, GM_TM); } while (0)
-            if (a->epi == SGK_EPI_ADD) GT2(SGK_EPI_ADD); else if (a->epi == SGK_EPI_SWIGLU) GT2(SGK_EPI_SWIGLU); else GT2(SGK_EPI_STORE);
+            if (epi == SGK_EPI_ADD) GT2(SGK_EPI_ADD);
+            else if (epi == SGK_EPI_SWIGLU) GT2(SGK_EPI_SWIGLU);
+            else if (epi == SGK_EPI_SWIGLU_XS) GT2(SGK_EPI_SWIGLU_XS);
+            else GT2(SGK_EPI_STORE);
 #undef GT2
 #undef GT
         }
