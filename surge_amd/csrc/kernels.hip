@@ -2811,37 +2811,77 @@ extern "C" hipError_t sgk_rmsnorm_gated(const float *y, const float *z, const fl
 // slots; each output is the taps in order, then the current input (the
 // decode step's arithmetic). The ring is only read here: k_conv_ring writes
 // the chunk's last inputs into it afterwards.
+// With hw = 1 or 2 the q and k heads (channels below qk_end, hw waves of
+// dk = 64 hw channels each, so no head crosses a workgroup) also get k_qk_norm_chunk's
+// RMS and scale before they are written: each wave sums its squares with
+// wave_sum, and a head's waves are added in block_sum's order (the same
+// per-lane values in the same lanes, so the same bits as the separate pass).
 #define CC_TOK 16
 __global__ void __launch_bounds__(TPB) k_conv_chunk(const float *in, uint32_t in_stride, const float *conv_w,
                                                     const float *ring, float *out, const sgk_step *steps,
-                                                    uint32_t ntok, uint32_t cd, uint32_t ksize) {
+                                                    uint32_t ntok, uint32_t cd, uint32_t ksize, uint32_t qk_end,
+                                                    uint32_t hw) {
+    __shared__ float red[4][CC_TOK];
     const uint32_t ch = blockIdx.x * TPB + threadIdx.x, z0 = blockIdx.y * CC_TOK;
-    if (ch >= cd) return;
+    const bool live = ch < cd;
     const uint32_t keep = ksize - 1, pos0 = steps[0].pos;
-    float w[4], x[CC_TOK + 3];
+    float o[CC_TOK];
+    if (live) {
+        float w[4], x[CC_TOK + 3];
 #pragma unroll
-    for (uint32_t j = 0; j < 4; j++) w[j] = conv_w[(size_t)ch * ksize + min(j, keep)];
-    // x[3 + i] = input of token z0 + i; x[0..2] = the three before z0
+        for (uint32_t j = 0; j < 4; j++) w[j] = conv_w[(size_t)ch * ksize + min(j, keep)];
+        // x[3 + i] = input of token z0 + i; x[0..2] = the three before z0
 #pragma unroll
-    for (int i = 0; i < CC_TOK + 3; i++) {
-        const int z = (int)z0 + i - 3;
-        const uint32_t zc = (uint32_t)min(max(z, 0), (int)ntok - 1);
-        const float vi = in[(size_t)zc * in_stride + ch];
-        const float vr = ring[(size_t)((pos0 + 4 + (uint32_t)min(z, 0)) & 3) * cd + ch];
-        x[i] = z < 0 ? vr : vi;
+        for (int i = 0; i < CC_TOK + 3; i++) {
+            const int z = (int)z0 + i - 3;
+            const uint32_t zc = (uint32_t)min(max(z, 0), (int)ntok - 1);
+            const float vi = in[(size_t)zc * in_stride + ch];
+            const float vr = ring[(size_t)((pos0 + 4 + (uint32_t)min(z, 0)) & 3) * cd + ch];
+            x[i] = z < 0 ? vr : vi;
+        }
+#pragma unroll
+        for (int i = 0; i < CC_TOK; i++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (uint32_t jj = 0; jj < 3; jj++)
+                if (jj < keep) acc = fmaf(w[jj], x[3 + i - keep + jj], acc);
+            const float wcur = keep == 0 ? w[0] : keep == 1 ? w[1] : keep == 2 ? w[2] : w[3];
+            acc = fmaf(wcur, x[3 + i], acc);
+            o[i] = z0 + i < ntok ? silu(acc) : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < CC_TOK; i++) o[i] = 0.0f;
     }
+    if (hw && blockIdx.x * TPB < qk_end) {
+        const uint32_t w = threadIdx.x >> 6;
+        float ss[CC_TOK];
 #pragma unroll
-    for (int i = 0; i < CC_TOK; i++) {
-        const uint32_t z = z0 + i;
-        if (z >= ntok) break;
-        float acc = 0.0f;
+        for (int i = 0; i < CC_TOK; i++) ss[i] = wave_sum(fmaf(o[i], o[i], 0.0f));
+        if (hw > 1) {
+            if ((threadIdx.x & 63) == 0)
 #pragma unroll
-        for (uint32_t jj = 0; jj < 3; jj++)
-            if (jj < keep) acc = fmaf(w[jj], x[3 + i - keep + jj], acc);
-        const float wcur = keep == 0 ? w[0] : keep == 1 ? w[1] : keep == 2 ? w[2] : w[3];
-        acc = fmaf(wcur, x[3 + i], acc);
-        out[(size_t)z * cd + ch] = silu(acc);
+                for (int i = 0; i < CC_TOK; i++) red[w][i] = ss[i];
+            __syncthreads();
+            // block_sum's (r0 + r1) + (r2 + r3) with the other head's waves at zero
+            const uint32_t w0 = w & 2;
+#pragma unroll
+            for (int i = 0; i < CC_TOK; i++) ss[i] = red[w0][i] + red[w0 + 1][i];
+        }
+        if (ch < qk_end) {
+            const float dk = (float)(64 * hw);
+            const float sc = ch < qk_end / 2 ? 1.0f / dk : 1.0f / sqrtf(dk);
+#pragma unroll
+            for (int i = 0; i < CC_TOK; i++) {
+                const float r = 1.0f / sqrtf(ss[i] / dk + 1e-6f);
+                o[i] = (o[i] * r) * sc;
+            }
+        }
     }
+    if (live)
+#pragma unroll
+        for (int i = 0; i < CC_TOK; i++)
+            if (z0 + i < ntok) out[(size_t)(z0 + i) * cd + ch] = o[i];
 }
 
 // The ring after a chunk: slot p % 4 = input of position p for the chunk's
@@ -3626,11 +3666,18 @@ extern "C" hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t 
                                     float *ws, hipStream_t s) {
     if (!ntok) return hipSuccess;
     if (a->ksize < 1 || a->ksize > 4 || !a->n_k || a->n_v % a->n_k) return hipErrorInvalidValue;
+    // q/k norm inside the conv when a head is one or two whole waves; else its own pass
+    const uint32_t hw = a->dk == 64 ? 1 : a->dk == 128 ? 2 : 0;
+    const uint32_t qk_end = 2 * a->n_k * a->dk;
+    if (qk_end > a->conv_dim) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_conv_chunk, dim3((a->conv_dim + TPB - 1) / TPB, (ntok + CC_TOK - 1) / CC_TOK), dim3(TPB), 0, s,
-                       a->in, in_stride, a->conv_w, a->ring, conv_out, a->step, ntok, a->conv_dim, a->ksize);
+                       a->in, in_stride, a->conv_w, a->ring, conv_out, a->step, ntok, a->conv_dim, a->ksize,
+                       hw ? qk_end : 0u, hw);
     hipLaunchKernelGGL(k_conv_ring, dim3((a->conv_dim + TPB - 1) / TPB), dim3(TPB), 0, s, a->in, in_stride, a->ring,
                        a->step, ntok, a->conv_dim);
-    hipLaunchKernelGGL(k_qk_norm_chunk, dim3(2 * a->n_k, ntok), dim3(TPB), 0, s, conv_out, a->conv_dim, a->n_k, a->dk);
+    if (!hw)
+        hipLaunchKernelGGL(k_qk_norm_chunk, dim3(2 * a->n_k, ntok), dim3(TPB), 0, s, conv_out, a->conv_dim, a->n_k,
+                           a->dk);
     return sgk_delta_scan(a, conv_out, in_stride, ntok, NULL, ws, s);
 }
 
