@@ -275,6 +275,17 @@ sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *ga
  * [7]=eps bits; conv_dim = 2 n_k dk + n_v dv; dv <= 128. */
 sg_err sg_gpu_run_gdn_step(sg_gpu *g, void *in, void *w, void *state, void *out,
                            const uint32_t params[8]);
+/* The prefill path's DeltaNet layer core over a chunk of n tokens (the chunk
+ * conv with its q/k norm, the conv ring, the gates, the delta-rule scan in
+ * the build's default form, the RMSNormGated rows), with no reference
+ * counterpart (the reference's prefill loops its per-token kernels,
+ * kernels.metal:1111-1278). Buffers as sg_gpu_run_gdn_step with n rows: in
+ * [n][conv_dim + value_dim + 2 n_v], out [n][value_dim]; w and state the
+ * same. p: [0]=dk [1]=dv [2]=n_v [3]=n_k [4]=ksize [5]=flags (bit 0 tiled,
+ * bit 1 ssm_a is -exp(A_log), bits 2-3 the first position mod 4) [6]=n
+ * [7]=eps bits. */
+sg_err sg_gpu_run_gdn_chunk(sg_gpu *g, void *in, void *w, void *state, void *out,
+                            const uint32_t params[8]);
 /* Prefill chunk hooks (surge.h:1111-1142), reference layouts:
  *   conv1d_chunk: x [n_tok, ch], w [ch, ksize], out [n_tok, ch], state
  *     [ksize-1, ch] oldest-first in/out; no activation. p: [0]=ch [1]=ksize [2]=n_tok

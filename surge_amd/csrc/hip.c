@@ -774,6 +774,72 @@ sg_err sg_gpu_run_gdn_step(sg_gpu *g, void *in, void *w, void *state, void *out,
     return finish(g, he, outs, 2);
 }
 
+/* The prefill path's DeltaNet layer core over a chunk of n tokens, with the
+ * kernels prefill_chunk runs (sgk_gdn_chunk: the chunk conv with its q/k
+ * norm, the conv ring, the gates and the delta-rule scan in the build's
+ * default form; then the RMSNormGated rows) on caller buffers (no reference
+ * counterpart: the reference's prefill runs its per-token kernels in a loop,
+ * kernels.metal:1111-1278). Buffers as sg_gpu_run_gdn_step, with n rows:
+ *   in    [n][conv_dim + value_dim + 2 n_v]  qkv | z | b | a per token;
+ *   w     [conv_dim ksize + 2 n_v + dv]      conv_w | ssm_a | dt_bias | ssm_norm;
+ *   state [(ksize-1) conv_dim + n_v dv dk]   the conv tail (oldest first) | S,
+ *         updated in place;
+ *   out   [n][value_dim].
+ * p: [0]=dk [1]=dv [2]=n_v [3]=n_k [4]=ksize [5]=flags: bit 0 tiled, bit 1
+ * ssm_a is -exp(A_log), bits 2-3 the first position mod 4 (the ring slot the
+ * chunk starts at) [6]=n [7]=eps bits. */
+sg_err sg_gpu_run_gdn_chunk(sg_gpu *g, void *in, void *w, void *state, void *out, const uint32_t p[8]) {
+    if (!g || !in || !w || !state || !out || !p) return (sg_err){"gpu: gdn_chunk got a NULL argument"};
+    const uint32_t dk = p[0], dv = p[1], nv = p[2], nk = p[3], ks = p[4], n = p[6];
+    if (dk != 32 && dk != 64 && dk != 128 && dk != 256) return (sg_err){"gpu: gdn_chunk: dk must be 32, 64, 128 or 256"};
+    if (!dv || !nv || !nk || nv % nk || ks < 1 || ks > 4 || !n)
+        return (sg_err){"gpu: gdn_chunk: bad shape (n_v a multiple of n_k, ksize 1..4, n > 0)"};
+    const uint64_t cd = 2ull * nk * dk + (uint64_t)nv * dv, vd = (uint64_t)nv * dv, keep = ks - 1;
+    const uint64_t row = cd + vd + 2ull * nv;
+    sg_err e;
+    if (sg_failed(e = need(in, n * row * 4, "in")) || sg_failed(e = need(w, (cd * ks + 2ull * nv + dv) * 4, "w")) ||
+        sg_failed(e = need(state, (keep * cd + vd * dk) * 4, "state")) || sg_failed(e = need(out, n * vd * 4, "out")))
+        return e;
+    if (overlap(out, in) || overlap(out, w) || overlap(out, state) || overlap(state, in) || overlap(state, w))
+        return (sg_err){"gpu: gdn_chunk: buffers must not overlap"};
+    void *ins[3] = {in, w, state}, *outs[2] = {state, out};
+    if (sg_failed(e = push(ins, 3))) return e;
+    /* scratch: the chunk's step descriptors, the 4-slot ring, the conv
+     * output, the scan readouts and the scan workspace */
+    const uint64_t sb = ((uint64_t)n * sizeof(sgk_step) + 255) / 256 * 256, rb = 4 * cd * 4, cb = (uint64_t)n * cd * 4,
+                   yb = (uint64_t)n * vd * 4, wsb = (uint64_t)sgk_delta_wy_ws_floats(nv, n) * 4;
+    void *t;
+    if (sg_failed(e = scratch(g, sb + rb + cb + yb + wsb, &t))) return e;
+    const uint32_t pos0 = 4 + ((p[5] >> 2) & 3);
+    sgk_step *st = calloc(n, sizeof *st);
+    if (!st) return (sg_err){"gpu: gdn_chunk: out of host memory"};
+    for (uint32_t z = 0; z < n; z++) st[z].pos = pos0 + z;
+    hipStream_t s = g->stream;
+    hipError_t he = hipMemcpyAsync(t, st, n * sizeof *st, hipMemcpyHostToDevice, s);
+    if (he == hipSuccess) he = hipStreamSynchronize(s);
+    free(st);
+    HIPCHK(he, "gdn_chunk descriptors");
+    float *ring = (float *)((char *)t + sb), *conv = ring + 4 * cd, *y = conv + (uint64_t)n * cd, *ws = y + (uint64_t)n * vd;
+    float *dst = DEV(state), *wp = DEV(w);
+    /* the tail's row j is the input of position pos0 - keep + j */
+    for (uint64_t j = 0; j < keep; j++)
+        HIPCHK(hipMemcpyAsync(ring + ((pos0 - keep + j) & 3) * cd, dst + j * cd, cd * 4, hipMemcpyDeviceToDevice, s),
+               "conv tail in");
+    sgk_gdn d = {0};
+    d.in = DEV(in); d.conv_w = wp; d.ssm_a = wp + cd * ks; d.dt_bias = d.ssm_a + nv; d.ring = ring;
+    d.S = dst + keep * cd; d.y = y; d.step = t; d.n_k = nk; d.n_v = nv; d.dk = dk; d.dv = dv;
+    d.conv_dim = (uint32_t)cd; d.ksize = ks; d.tiled = p[5] & 1; d.neg_exp = (p[5] >> 1) & 1;
+    he = sgk_gdn_chunk(&d, conv, (uint32_t)row, n, ws, s);
+    if (he == hipSuccess)
+        he = sgk_rmsnorm_gated_rows(y, (const float *)DEV(in) + cd, (uint32_t)row, d.ssm_a + 2 * nv, DEV(out), dv, nv, n,
+                                    fbits(p[7]), s);
+    /* the new tail: the inputs of the last keep positions, which the ring
+     * holds (positions before the chunk kept their slots) */
+    for (uint64_t j = 0; he == hipSuccess && j < keep; j++)
+        he = hipMemcpyAsync(dst + j * cd, ring + ((pos0 + n - keep + j) & 3) * cd, cd * 4, hipMemcpyDeviceToDevice, s);
+    return finish(g, he, outs, 2);
+}
+
 /* ---------------------------------------------------------------------
  * prefill per-op hooks (surge.h:787-800, 1133-1142): the chunk kernels the
  * prefill path runs, one synchronous call each, with the reference's

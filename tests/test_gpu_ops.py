@@ -438,6 +438,52 @@ def test_gdn_decode_step_vs_oracle(gpu, nv, nk, dk, dv, ks, tiled):
         ib.free()
 
 
+GDN_CHUNK_CASES = [(16, 16, 128, 128, 4, True, 37, 2), (48, 16, 128, 128, 4, True, 130, 19),
+                   (6, 2, 64, 64, 4, False, 33, 50), (8, 4, 128, 96, 2, True, 20, 2),
+                   (4, 4, 256, 128, 3, False, 18, 5)]
+
+
+@pytest.mark.parametrize("nv,nk,dk,dv,ks,tiled,n1,n2", GDN_CHUNK_CASES,
+                         ids=[f"{a}v{b}k-dk{c}-dv{d}-ks{e}-{'tiled' if f else 'grouped'}-{g}+{h}"
+                              for a, b, c, d, e, f, g, h in GDN_CHUNK_CASES])
+def test_gdn_prefill_chunk_vs_oracle(gpu, nv, nk, dk, dv, ks, tiled, n1, n2):
+    """The prefill path's DeltaNet layer core (sg_gpu_run_gdn_chunk: the
+    chunk conv k_conv_chunk, with the q/k norm inside it at dk 64 and 128
+    and k_qk_norm_chunk after it at 256; the ring k_conv_ring; the scan in
+    the build's default form, k_dm_prep + k_dm_scan on the matrix cores at
+    dk 64 and 128 and the sequential k_delta_chunk at 256, with the gates
+    from the b, a columns; the RMSNormGated rows) against ref.c's gdn_layer
+    composed from the oracle, token by token: the BASELINE DeltaNet config
+    (16 heads, 128^2, conv width 4), the 27B's 48 value heads tiled over 16
+    key heads over a 130-token chunk (eight full 16-token blocks and a
+    partial one), a grouped dk 64 map, conv widths 2 and 3. Two chunks in a
+    row thread the conv tail and S, the second starting at another ring slot
+    (and shorter than the conv tail in one case); outputs and S within 1e-3,
+    the conv tail bit-exact (it holds the inputs)."""
+    rng = np.random.default_rng(nv * 11 + dk + ks + n1)
+    cd, vd = 2 * nk * dk + nv * dv, nv * dv
+    row = cd + vd + 2 * nv
+    eps = 1e-6
+    w = np.concatenate([rng.standard_normal(cd * ks) * 0.5, -np.exp(rng.uniform(-1, 1, nv)),
+                        rng.uniform(-0.5, 0.5, nv), 1.0 + 0.1 * rng.standard_normal(dv)]).astype(np.float32)
+    state = np.concatenate([rng.standard_normal((ks - 1) * cd), rng.standard_normal(nv * dv * dk) * 0.1])
+    state = state.astype(np.float32)
+    wb, sb = gpu.buf(w), gpu.buf(state.copy())
+    so = state.copy()
+    for n, slot in ((n1, 1), (n2, 2)):
+        inp = rng.standard_normal((n, row)).astype(np.float32)
+        ib, ob = gpu.buf(inp.reshape(-1)), gpu.buf(np.zeros(n * vd, np.float32))
+        gpu.gdn_chunk(ib, wb, sb, ob, [dk, dv, nv, nk, ks, int(tiled) | 2 | slot << 2, n, S.fbits(eps)])
+        want = np.zeros((n, vd), np.float32)
+        for z in range(n):
+            want[z], so = oracle_gdn_step(inp[z], w, so, dk, dv, nv, nk, ks, tiled, eps)
+        assert_close(ob.array, want.reshape(-1))
+        assert np.array_equal(sb.array[:(ks - 1) * cd], so[:(ks - 1) * cd])
+        assert_close(sb.array[(ks - 1) * cd:], so[(ks - 1) * cd:])
+        ib.free()
+        ob.free()
+
+
 def test_gdn_step_rejects_bad_shapes(gpu):
     b = gpu.buf(np.zeros(1 << 16, np.float32))
     o = gpu.buf(np.zeros(1 << 12, np.float32))
@@ -445,6 +491,20 @@ def test_gdn_step_rejects_bad_shapes(gpu):
               [64, 64, 4, 4, 5, 1, 1, 0]):
         with pytest.raises(S.SurgeError):
             gpu.gdn_step(b, b, o, o, p)
+
+
+def test_gdn_chunk_rejects_bad_shapes(gpu):
+    """dk outside 32/64/128/256, n_v not a multiple of n_k, ksize 5, an empty
+    chunk, a chunk longer than its input rows, state aliasing the input."""
+    b = gpu.buf(np.zeros(1 << 16, np.float32))
+    st = gpu.buf(np.zeros(1 << 16, np.float32))
+    o = gpu.buf(np.zeros(1 << 12, np.float32))
+    for p in ([100, 64, 4, 4, 4, 1, 4, 0], [64, 64, 6, 4, 4, 1, 4, 0], [64, 64, 4, 4, 5, 1, 4, 0],
+              [64, 64, 4, 4, 4, 1, 0, 0], [64, 64, 4, 4, 4, 1, 1000, 0]):
+        with pytest.raises(S.SurgeError):
+            gpu.gdn_chunk(b, b, st, o, p)
+    with pytest.raises(S.SurgeError):
+        gpu.gdn_chunk(b, st, b, o, [32, 16, 1, 1, 4, 1, 1, 0])
 
 
 # even GQA groups run two query heads per workgroup, odd ones (12/4, 6/6) one
