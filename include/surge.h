@@ -286,6 +286,17 @@ sg_err sg_gpu_run_gdn_step(sg_gpu *g, void *in, void *w, void *state, void *out,
  * [7]=eps bits. */
 sg_err sg_gpu_run_gdn_chunk(sg_gpu *g, void *in, void *w, void *state, void *out,
                             const uint32_t params[8]);
+/* The prefill path's attention layer core over a chunk of n tokens at
+ * positions base .. base+n-1 (q_norm / k_norm, partial RoPE, f16 K/V store,
+ * the flash pass with its key split and combine, sigmoid output gate), with
+ * no reference counterpart (the reference's prefill runs its attention
+ * kernels per token, kernels.metal:1021-1081). in [n][n_heads 2 hd + 2 n_kv
+ * hd] (per query head q | gate, then k, then v), w [2 hd] q_norm | k_norm,
+ * kv [2][base + n][n_kv][hd] f16 (K then V; positions below base given, the
+ * chunk's written), out [n][n_heads hd]. p: [0]=n_heads [1]=n_kv [2]=hd (64,
+ * 128 or 256) [3]=rope_dim [4]=base [5]=n [6]=rope_theta bits [7]=eps bits. */
+sg_err sg_gpu_run_attn_chunk(sg_gpu *g, void *in, void *w, void *kv, void *out,
+                             const uint32_t params[8]);
 /* Prefill chunk hooks (surge.h:1111-1142), reference layouts:
  *   conv1d_chunk: x [n_tok, ch], w [ch, ksize], out [n_tok, ch], state
  *     [ksize-1, ch] oldest-first in/out; no activation. p: [0]=ch [1]=ksize [2]=n_tok

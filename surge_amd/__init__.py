@@ -113,6 +113,7 @@ _SIGS = {
     "sg_gpu_run_attn_splitk_partial_gqa_online": (SgErr, [C.c_void_p] * 7 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_run_gdn_step": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_run_gdn_chunk": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
+    "sg_gpu_run_attn_chunk": (SgErr, [C.c_void_p] * 5 + [C.POINTER(C.c_uint32)]),
     "sg_gpu_splitk_online_dispatches": (C.c_uint64, [C.c_void_p]),
     "sg_gpu_splitk_online_selected": (C.c_bool, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32,
                                                  C.c_uint32]),
@@ -298,6 +299,10 @@ class Gpu:
     def gdn_chunk(self, inp, w, state, out, p):
         check(lib().sg_gpu_run_gdn_chunk(self.handle, inp.handle, w.handle, state.handle, out.handle,
                                           params(p)))
+
+    def attn_chunk(self, inp, w, kv, out, p):
+        check(lib().sg_gpu_run_attn_chunk(self.handle, inp.handle, w.handle, kv.handle, out.handle,
+                                           params(p)))
 
     def dispatch_counts(self):
         """(per_head, gqa, online) partial dispatches encoded since sg_gpu_state_new."""

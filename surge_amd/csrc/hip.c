@@ -911,6 +911,19 @@ sg_err sg_gpu_run_rmsnorm_gated_chunk(sg_gpu *g, void *y, void *z, void *out, vo
 /* Causal chunk attention (surge.h:787-788): query token t (position base+t)
  * over cache positions 0..base+t, through the split-K kernels with the
  * prefill split policy. */
+/* RoPE cos | sin per position for positions 0 .. npos-1, rd = rope_dim
+ * floats each: angle and trig in double, stored f32 (reference
+ * metal.m:4027-4037, ref.c:561-602). */
+static void rope_table(float *t, uint32_t npos, uint32_t rd, float theta) {
+    const uint32_t half = rd / 2;
+    for (uint32_t p = 0; p < npos; p++)
+        for (uint32_t i = 0; i < half; i++) {
+            const double ang = (double)p * pow((double)theta, -2.0 * (double)i / (double)rd);
+            t[(uint64_t)p * rd + i] = (float)cos(ang);
+            t[(uint64_t)p * rd + half + i] = (float)sin(ang);
+        }
+}
+
 sg_err sg_gpu_run_attn_prefill(sg_gpu *g, void *q, void *k, void *v, void *out, const uint32_t p[8]) {
     if (!g || !q || !k || !v || !out || !p) return (sg_err){"gpu: attn_prefill got a NULL argument"};
     uint32_t pp[8] = {p[0], p[1], p[2], 0, p[5], 0, 1, 0};
@@ -949,6 +962,71 @@ sg_err sg_gpu_run_attn_prefill(sg_gpu *g, void *q, void *k, void *v, void *out, 
         if (he == hipSuccess) he = sgk_attn_combine(&A, g->stream);
     }
     return finish(g, he, outs, 1);
+}
+
+/* The prefill path's attention layer core over a chunk of n tokens at
+ * positions base .. base+n-1, with the kernels prefill_chunk runs
+ * (sgk_attn_prep: q_norm / k_norm, partial RoPE, K and V stored f16 at each
+ * token's position; sgk_attn_flash: causal attention over keys 0 .. position,
+ * deep chunks split over keys and merged by the combine, sigmoid output
+ * gate), on caller buffers (no reference counterpart: the reference's
+ * prefill runs its attention kernels per token, kernels.metal:1021-1081;
+ * here they are tested whole, as one chunk):
+ *   in  [n][n_heads 2 hd + 2 n_kv hd]  the input projection's rows: per
+ *       query head q | gate, then k, then v (not modified);
+ *   w   [2 hd]                         q_norm | k_norm;
+ *   kv  [2][base + n][n_kv][hd] f16    K then V in the reference layout:
+ *       positions below base given, the chunk's written;
+ *   out [n][n_heads hd].
+ * p: [0]=n_heads [1]=n_kv [2]=hd (64, 128 or 256) [3]=rope_dim [4]=base
+ * [5]=n [6]=rope_theta bits [7]=eps bits. */
+sg_err sg_gpu_run_attn_chunk(sg_gpu *g, void *in, void *w, void *kv, void *out, const uint32_t p[8]) {
+    if (!g || !in || !w || !kv || !out || !p) return (sg_err){"gpu: attn_chunk got a NULL argument"};
+    const uint32_t nh = p[0], nkv = p[1], hd = p[2], rd = p[3], base = p[4], n = p[5];
+    if (!nh || !nkv || nh % nkv || (hd != 64 && hd != 128 && hd != 256) || rd < 2 || rd > hd || (rd & 1) || !n)
+        return (sg_err){"gpu: attn_chunk: bad shape (n_heads a multiple of n_kv, hd 64/128/256, even rope_dim <= hd, n > 0)"};
+    const uint64_t row = 2ull * nh * hd + 2ull * nkv * hd, cap = (uint64_t)base + n, kvh = cap * nkv * hd;
+    sg_err e;
+    if (sg_failed(e = need(in, n * row * 4, "in")) || sg_failed(e = need(w, 2ull * hd * 4, "w")) ||
+        sg_failed(e = need(kv, 2 * kvh * 2, "kv")) || sg_failed(e = need(out, (uint64_t)n * nh * hd * 4, "out")))
+        return e;
+    if (overlap(out, in) || overlap(out, w) || overlap(out, kv) || overlap(kv, in) || overlap(kv, w))
+        return (sg_err){"gpu: attn_chunk: buffers must not overlap"};
+    void *ins[3] = {in, w, kv}, *outs[2] = {kv, out};
+    if (sg_failed(e = push(ins, 3))) return e;
+    /* scratch: step descriptors, the RoPE table for positions 0 .. cap-1, a
+     * working copy of the rows (the prep normalises q in place) and the key
+     * splits' partials */
+    const uint64_t steps_b = ((uint64_t)n * sizeof(sgk_step) + 255) / 256 * 256, cs_b = (cap * rd * 4 + 255) / 256 * 256;
+    const uint64_t work_b = n * row * 4, ah = (uint64_t)n * nh * SGK_PREFILL_SPLITS;
+    void *t;
+    if (sg_failed(e = scratch(g, steps_b + cs_b + work_b + ah * (2 + hd) * 4, &t))) return e;
+    sgk_step *hs = calloc(n, sizeof *hs);
+    float *ht = malloc(cap * rd * 4);
+    hipError_t he = hs && ht ? hipSuccess : hipErrorOutOfMemory;
+    if (he == hipSuccess) {
+        for (uint32_t z = 0; z < n; z++) hs[z].pos = base + z;
+        rope_table(ht, (uint32_t)cap, rd, fbits(p[6]));
+        he = hipMemcpy(t, hs, (uint64_t)n * sizeof *hs, hipMemcpyHostToDevice);
+        if (he == hipSuccess) he = hipMemcpy((char *)t + steps_b, ht, cap * rd * 4, hipMemcpyHostToDevice);
+    }
+    free(hs);
+    free(ht);
+    HIPCHK(he, "attn_chunk descriptors and RoPE table");
+    hipStream_t s = g->stream;
+    float *cs = (float *)((char *)t + steps_b), *work = (float *)((char *)t + steps_b + cs_b);
+    float *mm = work + n * row, *ss = mm + ah, *aa = ss + ah;
+    HIPCHK(hipMemcpyAsync(work, DEV(in), work_b, hipMemcpyDeviceToDevice, s), "attn_chunk rows");
+    const float *wn = DEV(w);
+    uint16_t *kc = DEV(kv);
+    sgk_attn A = {0};
+    A.q = work; A.kc = kc; A.vc = kc + kvh; A.m = mm; A.s = ss; A.acc = aa; A.out = DEV(out);
+    A.gate = work + hd; A.steps = t; A.n_heads = nh; A.n_kv = nkv; A.hd = hd; A.rope_dim = rd;
+    A.q_stride = 2 * hd; A.q_tok = (uint32_t)row; A.out_tok = nh * hd; A.max_splits = SGK_PREFILL_SPLITS;
+    A.ntok = n; A.seq = (uint32_t)cap; A.scale = (float)(1.0 / sqrt((double)hd)); A.prefill = 1;
+    he = sgk_attn_prep(&A, wn, wn + hd, cs, fbits(p[7]), s);
+    if (he == hipSuccess) he = sgk_attn_flash(&A, s);
+    return finish(g, he, outs, 2);
 }
 
 /* The online-softmax partial (surge.h:974-1050). The partial kernel here is
@@ -1625,13 +1703,7 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
         float *t = malloc((uint64_t)max_ctx * rd * 4);
         if (!t) e = (sg_err){"gpu: out of host memory"};
         else {
-            uint32_t half = rd / 2;
-            for (uint32_t p = 0; p < max_ctx; p++)
-                for (uint32_t i = 0; i < half; i++) {
-                    double ang = (double)p * pow((double)c->rope_theta, -2.0 * (double)i / (double)rd);
-                    t[(uint64_t)p * rd + i] = (float)cos(ang);
-                    t[(uint64_t)p * rd + half + i] = (float)sin(ang);
-                }
+            rope_table(t, max_ctx, rd, c->rope_theta);
             if (hipMemcpy(g->cs_table, t, (uint64_t)max_ctx * rd * 4, hipMemcpyHostToDevice) != hipSuccess)
                 e = (sg_err){"gpu: RoPE table upload failed"};
             free(t);

@@ -812,6 +812,94 @@ def test_rmsnorm_gated_chunk(gpu):
     assert_close(ob.array, want)
 
 
+ATTN_CHUNK_CASES = [(24, 4, 256, 64, 1000, 150), (8, 2, 256, 64, 0, 130), (12, 4, 128, 32, 300, 70),
+                    (16, 4, 128, 128, 600, 64)]
+
+
+@pytest.mark.parametrize("nh,nkv,hd,rd,base,n", ATTN_CHUNK_CASES,
+                         ids=[f"{a}q{b}kv-hd{c}-rope{d}-base{e}-n{f}" for a, b, c, d, e, f in ATTN_CHUNK_CASES])
+def test_attn_prefill_chunk_vs_oracle(gpu, nh, nkv, hd, rd, base, n):
+    """The prefill path's attention layer core (sg_gpu_run_attn_chunk:
+    k_attn_prep's q_norm / k_norm, partial RoPE from the position table and
+    f16 K/V store, then the flash pass with its key split and combine and
+    the sigmoid output gate) against ref.c's attention mixer composed from
+    the oracle token by token (RMSNorm with weight, RoPE in double, K/V
+    rounded to f16, decode attention over keys 0..position, gate): the 27B's
+    24q/4kv/256 with rope 64 deep enough for a 3-way key split, the 2B's
+    8q/2kv/256 from position 0, an odd GQA group (12/4, one query head per
+    workgroup) at head_dim 128 / rope 32, and a full rope. Outputs within
+    1e-3; V stored bit-exact (both round the same f32); K within one f16
+    ulp of the oracle's (its f32 before rounding differs in the last bits);
+    the keys before the chunk untouched."""
+    rng = np.random.default_rng(nh + hd + base + n)
+    row = 2 * nh * hd + 2 * nkv * hd
+    theta, eps = 1e7, 1e-6
+    cap = base + n
+    inp = rng.standard_normal((n, row)).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(2 * hd)).astype(np.float32)
+    K = np.zeros((cap, nkv, hd), np.float16)
+    V = np.zeros((cap, nkv, hd), np.float16)
+    K[:base] = rng.standard_normal((base, nkv, hd))
+    V[:base] = rng.standard_normal((base, nkv, hd))
+    kvb = gpu.buf(np.concatenate([K.reshape(-1), V.reshape(-1)]).view(np.uint16))
+    ib, wb = gpu.buf(inp.reshape(-1)), gpu.buf(w)
+    ob = gpu.buf(np.zeros(n * nh * hd, np.float32))
+    gpu.attn_chunk(ib, wb, kvb, ob, [nh, nkv, hd, rd, base, n, S.fbits(theta), S.fbits(eps)])
+    got_kv = kvb.array.view(np.float16).reshape(2, cap, nkv, hd)
+    o = O.oracle()
+    Ko, Vo = K.astype(np.float32), V.astype(np.float32)
+    Kr = K.copy()
+    want = np.zeros((n, nh * hd), np.float32)
+    sc = np.float32(1.0 / np.sqrt(hd))
+    for z in range(n):
+        pos = base + z
+        r = inp[z]
+        q = r[:2 * nh * hd].copy()
+        for h in range(nh):
+            seg = np.ascontiguousarray(q[2 * h * hd:2 * h * hd + hd])
+            o.sg_ref_rmsnorm(fp(seg), fp(np.ascontiguousarray(w[:hd])), hd, eps)
+            o.sg_ref_rope_partial(fp(seg), hd, rd, pos, theta)
+            q[2 * h * hd:2 * h * hd + hd] = seg
+        for kh in range(nkv):
+            k = np.ascontiguousarray(r[2 * nh * hd + kh * hd:2 * nh * hd + (kh + 1) * hd])
+            o.sg_ref_rmsnorm(fp(k), fp(np.ascontiguousarray(w[hd:])), hd, eps)
+            o.sg_ref_rope_partial(fp(k), hd, rd, pos, theta)
+            Kr[pos, kh] = k.astype(np.float16)
+            Ko[pos, kh] = k
+            v = r[2 * nh * hd + (nkv + kh) * hd:2 * nh * hd + (nkv + kh + 1) * hd]
+            Vo[pos, kh] = v.astype(np.float16).astype(np.float32)
+        kc = Kr.astype(np.float32).reshape(-1)
+        out = np.zeros(nh * hd, np.float32)
+        o.sg_ref_attn_decode(fp(q), fp(kc), fp(np.ascontiguousarray(Vo.reshape(-1))), nh, nkv, hd, pos + 1,
+                             2 * hd, sc, fp(out))
+        for h in range(nh):
+            oh = np.ascontiguousarray(out[h * hd:(h + 1) * hd])
+            o.sg_ref_gate_sigmoid(fp(oh), fp(np.ascontiguousarray(q[2 * h * hd + hd:2 * (h + 1) * hd])), hd)
+            want[z, h * hd:(h + 1) * hd] = oh
+    assert_close(ob.array, want.reshape(-1))
+    assert np.array_equal(got_kv[1, base:].view(np.uint16), Vo[base:].astype(np.float16).view(np.uint16))
+    assert np.array_equal(got_kv[0, :base].view(np.uint16), K[:base].view(np.uint16))
+    assert np.array_equal(got_kv[1, :base].view(np.uint16), V[:base].view(np.uint16))
+    ulp = np.spacing(np.abs(Ko[base:]).astype(np.float16)).astype(np.float32)
+    assert (np.abs(got_kv[0, base:].astype(np.float32) - Ko[base:]) <= ulp).all()
+
+
+def test_attn_chunk_rejects_bad_shapes(gpu):
+    """n_heads not a multiple of n_kv, head_dim 96, odd or oversize rope, an
+    empty chunk, a chunk longer than its input rows, the cache aliasing the
+    input rows."""
+    b = gpu.buf(np.zeros(1 << 16, np.float32))
+    kv = gpu.buf(np.zeros(1 << 16, np.float32))
+    o = gpu.buf(np.zeros(1 << 14, np.float32))
+    th, ep = S.fbits(1e7), S.fbits(1e-6)
+    for p in ([6, 4, 64, 16, 0, 4], [8, 2, 96, 16, 0, 4], [8, 2, 64, 15, 0, 4], [8, 2, 64, 128, 0, 4],
+              [8, 2, 64, 16, 0, 0], [8, 2, 64, 16, 0, 1000]):
+        with pytest.raises(S.SurgeError):
+            gpu.attn_chunk(b, b, kv, o, p + [th, ep])
+    with pytest.raises(S.SurgeError):
+        gpu.attn_chunk(b, kv, b, o, [8, 2, 64, 16, 0, 4, th, ep])
+
+
 @pytest.mark.parametrize("base,n", [(0, 5), (37, 16), (2000, 9)])
 def test_attn_prefill_causal(gpu, base, n):
     """Token t of the chunk (position base+t) attends over keys 0..base+t only."""
