@@ -241,6 +241,38 @@ HD128 = dict(n_layers=4, n_heads=12, n_kv_heads=2, head_dim=128, hidden=256, ffn
              conv_kernel=4, attn_output_gate=True)
 
 
+@pytest.mark.parametrize("name,chunk,n", [("small", 64, 200), ("hd256", 128, 300), ("wide", 512, 600)])
+def test_chunked_prefill_logits_vs_oracle(gpu, name, chunk, n):
+    """The whole prefill pipeline against ref.c's forward run token by token
+    (no GPU serial path in between): sg_gpu_prefill's GEMMs with their fused
+    epilogues (the RMSNorm + bf16 split written by the previous product's
+    split-K reduce, SwiGLU written as the down projection's split, the gated
+    norm written as the output projection's split), the chunk conv with its
+    q/k norm, the matrix-core DeltaNet scan, the attention prep and flash
+    pass. Last-token logits within 1e-3 with the same argmax, then one
+    decode step on the prefilled state within 1e-3 of the oracle's next
+    position. Configs: the 8-layer small hybrid in 64-token chunks, head_dim
+    256 in 128-token chunks, and a wider model (hidden 512) over two chunks,
+    512 + 88 tokens."""
+    cfg = {"small": SMALL, "hd256": HD256, "wide": WIDE}[name]
+    syn = S.Synth(cfg, S.SG_T_Q8_0, seed=41 + n)
+    gpu.load_model(syn.model)
+    gpu.state_new(n + 8)
+    prompt = np.random.default_rng(n).integers(0, cfg["vocab"], n).tolist()
+    last = gpu.prefill(prompt, chunk=chunk)
+    rm = O.RefModel(O.oracle(), syn.model, n + 8, kv_f16=True)
+    for p, t in enumerate(prompt):
+        o = rm.forward(t, p)
+    assert rel(last, o) < 1e-3
+    assert int(np.argmax(last)) == int(np.argmax(o))
+    nxt = int(np.argmax(o))
+    g2 = gpu.forward(nxt, n)
+    o2 = rm.forward(nxt, n)
+    rm.close()
+    syn.close()
+    assert rel(g2, o2) < 1e-3
+
+
 def test_hd128_decode_vs_oracle_and_prefill_vs_serial(gpu):
     """head_dim 128 with GQA 6 (the MFMA decode partial's and the MFMA
     prefill pass's other width): decode logits within 1e-3 of the oracle
