@@ -109,6 +109,18 @@ def gemv_roofline(gpu, cfg, reps=3):
                 avg_us=round(avg_s * 1e6, 2), algo_bytes=int(algo), launches=reps * L)
 
 
+def decode_floor(gpu, ctx, reps=20):
+    """The sequential-launch floor of this decode token (sg_gpu_time_floor):
+    its launch sequence captured in one HIP graph with every kernel replaced
+    by a plain streaming read of that kernel's algorithmic bytes, and by an
+    empty kernel. What kernels run one after another cannot beat."""
+    rd_us, n, nb = gpu.time_floor(ctx, 1, reps)
+    em_us, _, _ = gpu.time_floor(ctx, 0, reps)
+    return dict(kernels=n, bytes_per_token=int(nb), plain_read_us_per_token=round(rd_us, 1),
+                plain_read_tok_s=round(1e6 / rd_us, 2), plain_read_frac=round(nb / rd_us / 1e3 / HBM_PEAK_GBS, 4),
+                empty_us_per_token=round(em_us, 1), reps=reps)
+
+
 def calib_copy(nbytes):
     """One plain device-to-device copy of known size: rocprofv3 counter runs
     scale the GEMV's FETCH_SIZE/WRITE_SIZE by what the copy kernel reads."""
@@ -458,6 +470,9 @@ def main():
         calib_copy(a.calib_mb << 20)
     roof["traffic"] = measured_traffic("k_gemv_q8<2, 1, 2>")
     log(f"gate/up GEMV: {roof['avg_us']} us/launch, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
+    floor = decode_floor(gpu, a.ctx + a.warmup + a.steps // 2)
+    log(f"sequential-launch floor: {floor['kernels']} plain reads {floor['plain_read_us_per_token']} us/token "
+        f"({floor['plain_read_tok_s']} tok/s), {floor['kernels']} empty kernels {floor['empty_us_per_token']} us")
     row = S.BenchRow()
     row.model = f"qwen35-{a.shape}-shape-q8_0-random".encode()
     row.engine = b"surge_amd (MI355X, HIP)"
@@ -501,6 +516,7 @@ def main():
                     {"tokens": a.ctx, "chunk": a.chunk, "seconds": round(pf_s, 3),
                      "tok_per_s": round(a.ctx / pf_s, 1)}),
         "roofline": roof,
+        "decode_floor": floor,
         "cpu_baseline": cpu,
         "decode_by_slope": {"tok_s": round(slope, 3), "endpoint_avg_tok_s": round(avg, 3), "steps": a.steps,
                             "warmup": int(warm), "clock": "HIP events after each step"},

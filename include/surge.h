@@ -417,6 +417,20 @@ sg_err sg_gpu_time_gdn_step(sg_gpu *g, void *in, void *w, void *out, const uint3
  * microseconds per launch. */
 sg_err sg_gpu_time_read(sg_gpu *g, uint64_t bytes, uint64_t rotate_bytes, uint32_t reps, double *us);
 sg_err sg_gpu_time_empty(sg_gpu *g, uint32_t reps, int graph, double *us);
+/* The sequential-launch floor of one greedy decode token (no reference
+ * counterpart): the loaded model's decode launch sequence at `ctx` keys, in
+ * its order (embedding; per layer the input projection, attention partial and
+ * combine or DeltaNet step, output projection, gate/up, down; lm_head, two
+ * argmax passes, step advance), captured in one HIP graph with every kernel
+ * replaced by a plain streaming read of that kernel's algorithmic bytes
+ * (mode 1, each read from its own region of a buffer of the token's total, so
+ * nothing is served from the MALL) or by an empty kernel (mode 0), and
+ * replayed `reps` times; mode 2 launches the same reads one by one without a
+ * graph (for kernel traces). Average microseconds per token; n_kernels and bytes
+ * (either may be NULL) get the launch count and the token's summed bytes.
+ * Needs a Q8_0 model and a state; mode 1 allocates the token's bytes. */
+sg_err sg_gpu_time_floor(sg_gpu *g, uint32_t ctx, uint32_t mode, uint32_t reps, double *us, uint32_t *n_kernels,
+                         uint64_t *bytes);
 /* The prefill GEMM (no reference counterpart) on one of the loaded model's
  * weights (which: 0 input projection with its RMSNorm, 1 output projection
  * += into the residual rows, 2 gate/up with RMSNorm and SwiGLU, 3 down +=)
@@ -521,6 +535,20 @@ void sg_bench_format_json(const sg_bench_row *row, char *buf, size_t cap);   /* 
  * finalize sets status to "DONE" or "VOID" accordingly (surge.h:1939-1955). */
 bool sg_bench_admitted(const sg_bench_row *row);                           /* surge.h:1950 */
 void sg_bench_finalize_status(sg_bench_row *row);                          /* surge.h:1955 */
+
+/* The peak-memory probe (surge.h:2104-2142). sg_proc_phys_footprint: the
+ * process's resident host memory in bytes, here from Linux's
+ * /proc/self/statm (resident pages x page size; the reference reads
+ * Mach's phys_footprint); 0, with a message on stderr, when it cannot be
+ * read. sg_mem_tracker: a running maximum of two signals sampled together,
+ * peak = max(peak, current_alloc, phys_footprint); reset zeroes it, a NULL
+ * tracker is a no-op and reads back 0. */
+uint64_t sg_proc_phys_footprint(void);                                     /* surge.h:2128 */
+typedef struct { uint64_t peak; } sg_mem_tracker;                          /* surge.h:2138 */
+void sg_mem_tracker_reset(sg_mem_tracker *t);                              /* surge.h:2139 */
+void sg_mem_tracker_sample(sg_mem_tracker *t, uint64_t current_alloc,      /* surge.h:2140 */
+                           uint64_t phys_footprint);
+uint64_t sg_mem_tracker_peak(const sg_mem_tracker *t);                     /* surge.h:2141 */
 
 /* ---------------------------------------------------------------------
  * Synthetic random-init models (no reference counterpart: the reference

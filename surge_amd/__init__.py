@@ -136,6 +136,8 @@ _SIGS = {
     "sg_gpu_chain_active": (C.c_bool, [C.c_void_p]),
     "sg_gpu_time_read": (SgErr, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.POINTER(C.c_double)]),
     "sg_gpu_time_empty": (SgErr, [C.c_void_p, C.c_uint32, C.c_int, C.POINTER(C.c_double)]),
+    "sg_gpu_time_floor": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double),
+                                  C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
     "sg_gpu_time_gemm": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double)]),
     "sg_gpu_chain_stamps": (SgErr, [C.c_void_p, C.POINTER(C.c_uint64), C.c_uint64, C.POINTER(C.c_uint32),
                                     C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
@@ -426,6 +428,13 @@ class Gpu:
         us = C.c_double()
         check(lib().sg_gpu_time_empty(self.handle, reps, 1 if graph else 0, C.byref(us)))
         return us.value
+
+    def time_floor(self, ctx: int, mode: int, reps: int):
+        """(us per token, kernels, bytes) of the decode token's launch sequence
+        as plain reads of each kernel's bytes (mode 1) or empty kernels (mode 0)."""
+        us, n, nb = C.c_double(), C.c_uint32(), C.c_uint64()
+        check(lib().sg_gpu_time_floor(self.handle, ctx, mode, reps, C.byref(us), C.byref(n), C.byref(nb)))
+        return us.value, n.value, nb.value
 
     def time_attn(self, q: Buf, k: Buf, v: Buf, out: Buf, p, rotate: int, reps: int):
         us = (C.c_double * 2)()

@@ -10,6 +10,7 @@
 
 #include <math.h>
 #include <stdio.h>
+#include <unistd.h>
 
 double sg_bench_slope(const double *t, uint32_t n, uint32_t warmup) {
     if (!t || n <= warmup || n - warmup < 2) return 0.0;
@@ -108,3 +109,35 @@ void sg_bench_format_json(const sg_bench_row *row, char *buf, size_t cap) {
              row->assoc_hits, (unsigned long long)row->n_prompt_tok, row->n_gen, row->wall_s, row->gemm_tflops,
              row->ingestion_ok ? "true" : "false", st, li);
 }
+
+/* The peak-memory probe (reference surge.h:2104-2142, src/bench.c:401-440).
+ * Linux has no Mach phys_footprint; the resident set from /proc/self/statm
+ * (its second field, in pages) is the nearest figure for host memory. */
+uint64_t sg_proc_phys_footprint(void) {
+    FILE *f = fopen("/proc/self/statm", "r");
+    if (!f) {
+        fprintf(stderr, "bench: proc_phys_footprint: cannot open /proc/self/statm\n");
+        return 0;
+    }
+    unsigned long long size = 0, resident = 0;
+    const int got = fscanf(f, "%llu %llu", &size, &resident);
+    fclose(f);
+    const long page = sysconf(_SC_PAGESIZE);
+    if (got != 2 || page <= 0) {
+        fprintf(stderr, "bench: proc_phys_footprint: unreadable /proc/self/statm\n");
+        return 0;
+    }
+    return (uint64_t)resident * (uint64_t)page;
+}
+
+void sg_mem_tracker_reset(sg_mem_tracker *t) {
+    if (t) t->peak = 0;
+}
+
+void sg_mem_tracker_sample(sg_mem_tracker *t, uint64_t current_alloc, uint64_t phys_footprint) {
+    if (!t) return;
+    const uint64_t hi = phys_footprint > current_alloc ? phys_footprint : current_alloc;
+    if (hi > t->peak) t->peak = hi;
+}
+
+uint64_t sg_mem_tracker_peak(const sg_mem_tracker *t) { return t ? t->peak : 0; }

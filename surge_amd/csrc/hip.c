@@ -2326,6 +2326,111 @@ sg_err sg_gpu_time_empty(sg_gpu *g, uint32_t reps, int graph, double *us) {
     return e;
 }
 
+/* Algorithmic bytes of each kernel of one greedy decode token at `ctx` keys,
+ * in the launch order of enqueue_step (greedy, per-kernel path): embedding;
+ * per layer the input projection, the attention partial and combine or the
+ * DeltaNet step, the output projection, gate/up and down; lm_head, the two
+ * argmax passes and the step advance. Returns the kernel count (b may be NULL
+ * to count). Every figure is rounded up to 16 bytes. */
+static uint32_t floor_plan(const sg_gpu *g, uint32_t ctx, uint64_t *b) {
+    const sg_cfg *c = &g->cfg;
+    const uint64_t H = c->hidden, hd = c->head_dim, nh = c->n_heads, nkv = c->n_kv_heads;
+    const uint64_t ns = sgk_n_splits_cap(ctx, g->split_cap ? g->split_cap : SGK_MAX_SPLITS);
+    uint32_t n = 0;
+#define FL_ADD(v) do { const uint64_t v_ = (v); if (b) b[n] = (v_ + 15) & ~(uint64_t)15; n++; } while (0)
+#define FL_GEMV(M, rms, orows) FL_ADD((uint64_t)(M).rows * (M).cols / 32 * 34 + (uint64_t)(M).cols * 4 * ((rms) ? 2 : 1) \
+                                      + (uint64_t)(orows) * 4)
+    FL_ADD(H + H / 16 + 4 * H);
+    for (uint32_t i = 0; i < c->n_layers; i++) {
+        const glayer *L = &g->ls[i];
+        FL_GEMV(L->in, 1, L->in.rows);
+        if (L->attn) {
+            FL_ADD(2 * (uint64_t)ctx * nkv * hd * 2 + (uint64_t)L->in.rows * 4 + nh * ns * (hd + 2) * 4);
+            FL_ADD(nh * ns * (hd + 2) * 4 + 2 * nh * hd * 4);
+        } else {
+            const uint64_t nv = c->n_v_heads, dv = c->head_v_dim, dk = c->head_k_dim, cd = g->conv_dim;
+            FL_ADD(2 * nv * dv * dk * 4 + 5 * cd * 4 + (uint64_t)L->in.rows * 4 + cd * c->conv_kernel * 4 + nv * dv * 4);
+        }
+        FL_GEMV(L->out, 0, L->out.rows);
+        FL_GEMV(L->gu, 1, L->gu.rows / 2);
+        FL_GEMV(L->down, 0, L->down.rows);
+    }
+    FL_GEMV(g->lm, 1, g->lm.rows);
+    FL_ADD((uint64_t)c->vocab * 4);
+    FL_ADD(256 * 4);
+    FL_ADD(16);
+#undef FL_GEMV
+#undef FL_ADD
+    return n;
+}
+
+sg_err sg_gpu_time_floor(sg_gpu *g, uint32_t ctx, uint32_t mode, uint32_t reps, double *us, uint32_t *n_kernels,
+                         uint64_t *bytes) {
+    if (!g || !us || !reps || mode > 2 || !ctx) return (sg_err){"gpu: sg_gpu_time_floor got an invalid argument"};
+    if (!g->have_state || !g->q8) return (sg_err){"gpu: sg_gpu_time_floor needs a Q8_0 model and a state"};
+    const uint32_t n = floor_plan(g, ctx, NULL);
+    uint64_t *b = malloc((uint64_t)n * sizeof *b);
+    if (!b) return (sg_err){"gpu: out of host memory"};
+    floor_plan(g, ctx, b);
+    uint64_t tot = 0;
+    for (uint32_t i = 0; i < n; i++) tot += (b[i] + 255) & ~(uint64_t)255;
+    char *base = NULL;
+    float *out = NULL;
+    const uint32_t maxb = 4 * (uint32_t)sgk_chain_blocks();
+    sg_err e = SG_OK;
+    if (mode != 0) e = dalloc(g, tot, (void **)&base);
+    if (!sg_failed(e)) e = dalloc(g, (uint64_t)maxb * 4, (void **)&out);
+    hipStream_t s = g->stream;
+    hipEvent_t ea = NULL, eb = NULL;
+    hipGraph_t gr = NULL;
+    hipGraphExec_t ge = NULL;
+    /* one token's launches: empty kernels, or each kernel's bytes read from
+     * its own region (about one workgroup per 16 KB, at most 4 per CU) */
+    hipError_t he;
+#define FL_TOKEN() do {                                                                        \
+        uint64_t off_ = 0;                                                                     \
+        for (uint32_t i_ = 0; i_ < n && he == hipSuccess; i_++) {                             \
+            if (mode == 0) { he = sgk_empty(s); continue; }                                    \
+            uint64_t blocks_ = b[i_] / 16384;                                                  \
+            blocks_ = blocks_ < 1 ? 1 : blocks_ > maxb ? maxb : blocks_;                       \
+            he = sgk_read(base + off_, b[i_], out, (uint32_t)blocks_, s);                      \
+            off_ += (b[i_] + 255) & ~(uint64_t)255;                                            \
+        }                                                                                      \
+    } while (0)
+    he = sg_failed(e) ? hipErrorOutOfMemory : hipEventCreate(&ea);
+    if (he == hipSuccess) he = hipEventCreate(&eb);
+    if (mode == 2) {                          /* launched one by one, as the profiler sees them */
+        if (he == hipSuccess) FL_TOKEN();
+        if (he == hipSuccess) he = hipEventRecord(ea, s);
+        for (uint32_t r = 0; r < reps && he == hipSuccess; r++) FL_TOKEN();
+    } else {
+        if (he == hipSuccess) he = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed);
+        if (he == hipSuccess) {
+            FL_TOKEN();
+            hipError_t ce = hipStreamEndCapture(s, &gr);
+            if (he == hipSuccess) he = ce;
+        }
+        if (he == hipSuccess) he = hipGraphInstantiate(&ge, gr, NULL, NULL, 0);
+        if (he == hipSuccess) he = hipGraphLaunch(ge, s);                     /* warm-up, untimed */
+        if (he == hipSuccess) he = hipEventRecord(ea, s);
+        for (uint32_t r = 0; r < reps && he == hipSuccess; r++) he = hipGraphLaunch(ge, s);
+    }
+#undef FL_TOKEN
+    if (he == hipSuccess) he = hipEventRecord(eb, s);
+    if (!sg_failed(e)) e = he == hipSuccess ? timed(g, ea, eb, reps, us) : errf("gpu: sg_gpu_time_floor: %s", hipGetErrorString(he));
+    hipStreamSynchronize(s);
+    if (ge) hipGraphExecDestroy(ge);
+    if (gr) hipGraphDestroy(gr);
+    if (ea) hipEventDestroy(ea);
+    if (eb) hipEventDestroy(eb);
+    if (n_kernels) *n_kernels = n;
+    if (bytes) { uint64_t t = 0; for (uint32_t i = 0; i < n; i++) t += b[i]; *bytes = t; }
+    free(b);
+    dfree(g, out);
+    dfree(g, base);
+    return e;
+}
+
 sg_err sg_gpu_time_matvec_q8(sg_gpu *g, void *w, void *x, void *y, uint32_t rows, uint32_t cols,
                              uint64_t rotate_bytes, uint32_t reps, double *us) {
     if (!g || !w || !x || !y || !us || !reps || !rows || !cols || cols % 32)

@@ -12,7 +12,16 @@ ingests the prompt one position at a time and greedily generates n_gen tokens
   --lib oracle  this repository's restatement, optionally with --kv-f16 (K/V
                 rounded through f16 as the GPU stores them), a diagnostic.
 
+  --fill N      instead of ingesting a prompt, start from the seeded state
+                sg_ref_state_fill_synthetic writes for N positions (the state
+                sg_gpu_state_fill_synthetic writes on the GPU: f16-exact K/V
+                rows, DeltaNet S and conv tails), then generate from the first
+                prompt id at position N. Oracle only (the reference's ref.c has
+                no such fill); its generated K/V rows stay f32 unless --kv-f16.
+
 Usage: python tests/golden/make_greedy.py --shape 2b --lib ref --out tests/golden/greedy_2b_ref.json
+       python tests/golden/make_greedy.py --shape 27b --lib oracle --fill 4096 --n-prompt 1 --n-gen 64 \
+           --out tests/golden/greedy_27b_fill4096_oracle.json
 """
 import argparse
 import json
@@ -41,6 +50,8 @@ def main():
     ap.add_argument("--lib", choices=["ref", "oracle"], default="ref")
     ap.add_argument("--kv-f16", action="store_true")
     ap.add_argument("--threads", type=int, default=8)
+    ap.add_argument("--fill", type=int, default=0)
+    ap.add_argument("--fill-seed", type=int, default=7)
     ap.add_argument("--out", required=True)
     a = ap.parse_args()
     cfg = SHAPES[a.shape]
@@ -49,20 +60,29 @@ def main():
     L = O.ref() if a.lib == "ref" else O.oracle()
     if a.lib == "oracle":
         L.sg_ref_set_threads(a.threads)
-    rm = O.RefModel(L, syn.model, a.n_prompt + a.n_gen + 1, kv_f16=a.kv_f16)
+    if a.fill and a.lib != "oracle":
+        ap.error("--fill needs --lib oracle")
+    base = a.fill
+    rm = O.RefModel(L, syn.model, base + a.n_prompt + a.n_gen + 1, kv_f16=a.kv_f16)
     t0 = time.time()
+    if a.fill:
+        rm.fill_synthetic(a.fill, a.fill_seed)
     for p, t in enumerate(prompt):
-        lg = rm.forward(t, p)
+        lg = rm.forward(t, base + p)
+        print(f"prompt position {base + p} done at {time.time() - t0:.0f} s", flush=True)
     gen, margins = [], []
     for i in range(a.n_gen):
         nxt = int(np.argmax(lg))          # numpy argmax: first (lowest) index of the max
         top2 = np.partition(lg, -2)[-2:]
         margins.append(float(top2[1] - top2[0]))
         gen.append(nxt)
-        lg = rm.forward(nxt, a.n_prompt + i)
+        lg = rm.forward(nxt, base + a.n_prompt + i)
+        print(f"token {i}: {nxt} (margin {margins[-1]:.4g}) at {time.time() - t0:.0f} s", flush=True)
     out = dict(shape=a.shape, cfg=cfg, seed=a.seed, wtype="q8_0", prompt_ids=prompt, gen_ids=gen,
                lib=("reference src/ref.c" if a.lib == "ref" else "oracle/ref.c"), kv_f16=a.kv_f16,
                min_top2_margin=min(margins), seconds=round(time.time() - t0, 1))
+    if a.fill:
+        out.update(fill=a.fill, fill_seed=a.fill_seed, margins=[round(m, 6) for m in margins])
     with open(a.out, "w") as f:
         json.dump(out, f, indent=1)
     print(a.out, "gen:", gen[:16], "... min margin", min(margins), "in", out["seconds"], "s")

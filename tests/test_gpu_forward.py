@@ -150,6 +150,33 @@ def _golden(name):
     return json.load(open(path))
 
 
+LONG_FFN = dict(SMALL, n_layers=4, ffn_hidden=9216)
+
+
+def test_long_ffn_down_projection_per_position_vs_oracle(gpu):
+    """An FFN wider than 8192 (9216): the down projection runs the balanced
+    interleaved GEMV with its residual-add epilogue (k_gemv_bal<0, 1, true>,
+    the 27B's down-projection form; gate/up stays on k_gemv_q8 at 256
+    columns). Logits within 1e-3 of the oracle at every position of a
+    48-token walk, same argmax."""
+    syn = S.Synth(LONG_FFN, S.SG_T_Q8_0, seed=17)
+    gpu.load_model(syn.model)
+    gpu.state_new(64)
+    rm = O.RefModel(O.oracle(), syn.model, 64, kv_f16=True)
+    ids = np.random.default_rng(17).integers(0, LONG_FFN["vocab"], 48).tolist()
+    worst = 0.0
+    for p, t in enumerate(ids):
+        g = gpu.forward(t, p)
+        o = rm.forward(t, p)
+        worst = max(worst, rel(g, o))
+        assert np.argmax(g) == np.argmax(o), f"argmax differs at position {p}"
+    rm.close()
+    gpu.state_new(8)
+    syn.close()
+    print(f"[long ffn] worst relative gap {worst:.3e}", flush=True)
+    assert worst < 1e-3, worst
+
+
 def test_2b_greedy_64_tokens_identical_to_reference(gpu):
     """BASELINE config: random-init 2B-shaped Q8_0 hybrid (hidden 2048, 24
     layers, 8q/2kv x 256, 16/16 DeltaNet heads x 128, FFN 6144, vocab

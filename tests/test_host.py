@@ -195,12 +195,13 @@ def _aux_prototypes(include_dir):
 
 @pytest.mark.skipif(not os.path.exists(REF_HEADER), reason="reference sources absent")
 def test_abi_prototypes_match_reference_header():
-    """Every sg_gpu_* / sg_kv_* function the reference's surge.h declares is
+    """Every sg_gpu_* / sg_kv_* function the reference's surge.h declares, and
+    the peak-memory probe's (sg_mem_tracker_*, sg_proc_phys_footprint), is
     declared here with the identical prototype (types as gcc prints them),
     so the reference's own callers compile and link against this library."""
     ref = _aux_prototypes(os.path.dirname(REF_HEADER))
     ours = _aux_prototypes(os.path.join(ROOT, "include"))
-    wanted = sorted(n for n in ref if n.startswith(("sg_gpu_", "sg_kv_")))
+    wanted = sorted(n for n in ref if n.startswith(("sg_gpu_", "sg_kv_", "sg_mem_tracker_", "sg_proc_phys_")))
     assert len(wanted) >= 50
     missing = [n for n in wanted if n not in ours]
     assert not missing, missing
@@ -370,16 +371,66 @@ def test_bench_row_md_json_and_admission():
         assert x.status.decode() == want
 
 
-def test_gemm_stamps_instrumentation_applies_to_current_kernels():
-    """The barrier-stamp harness (python -m surge_amd.gemm_stamps) edits a
-    copy of kernels.hip by exact text: it must still find every place it
-    instruments, and leave the rest of the source as it was."""
-    from surge_amd import gemm_stamps
-    path = os.path.join(os.path.dirname(S.__file__), "csrc", "kernels.hip")
-    with open(path) as f:
-        src = f.read()
-    for prio in (False, True):
-        out = gemm_stamps.instrument(src, prio)
-        assert out.count("__builtin_amdgcn_s_memtime()") == 2
-        assert ("__builtin_amdgcn_s_setprio(3)" in out) == prio
-        assert "sgk_gemm_stamps" in out and len(out) > len(src)
+# ---------------------------------------------------------------- the reference's GPU callers link unchanged
+
+REF_ROOT = "/root/reference"
+REF_CALLERS = ["test_gpu_fwd", "test_metal_ops", "test_gpu_prefill", "test_gpu_mem", "bench_splitk"]
+# what the callers take from elsewhere than the GPU layer: the reference's CPU
+# oracle (ref.c) and its safetensors reader (out of this build's scope)
+NOT_OURS = ("sg_ref_", "sg_st_", "sg_model_from_st")
+
+
+@pytest.mark.skipif(not os.path.isdir(os.path.join(REF_ROOT, "tests")) or not O.ref_available(),
+                    reason="reference sources (or oracle/_ref) absent")
+@pytest.mark.parametrize("caller", REF_CALLERS)
+def test_reference_gpu_caller_links_against_library(caller):
+    """The reference's own GPU test / bench source, compiled unchanged with the
+    reference's surge.h, links against libsurge_amd.so, and every sg_*
+    function it calls that is not the CPU oracle's or the safetensors
+    reader's resolves from this library (the oracle part from oracle/_ref,
+    the reference's ref.c compiled from its sources). Linked, not run."""
+    import subprocess
+    src = os.path.join(REF_ROOT, "tests", caller + ".c")
+    lib_dir = os.path.dirname(S.LIB_PATH)
+    with tempfile.TemporaryDirectory() as d:
+        obj, exe = os.path.join(d, caller + ".o"), os.path.join(d, caller)
+        cc = ["gcc", "-std=c11", "-D_GNU_SOURCE", "-w", "-I", REF_ROOT, "-I", os.path.join(REF_ROOT, "src"),
+              "-I", os.path.join(REF_ROOT, "tests")]
+        subprocess.check_call(cc + ["-c", src, "-o", obj])
+        und = subprocess.check_output(["nm", "-u", obj], text=True).split()
+        ours = set(subprocess.check_output(["nm", "-D", "--defined-only", S.LIB_PATH], text=True).split())
+        used = sorted({s for s in und if s.startswith("sg_")})
+        elsewhere = [s for s in used if s not in ours]
+        assert all(s.startswith(NOT_OURS) for s in elsewhere), elsewhere
+        assert any(s.startswith("sg_gpu_") for s in used)
+        subprocess.check_call(["gcc", obj, "-o", exe, "-L", lib_dir, "-lsurge_amd", "-Wl,-rpath," + lib_dir,
+                               O.REF_PATH, "-lm"])
+        assert os.path.exists(exe)
+
+
+def test_mem_tracker_and_phys_footprint():
+    """The peak-memory probe (reference tests/test_gpu_mem.c tier 1: the
+    tracker's running max, unit-exact; tier 2: the footprint is a live,
+    non-zero reading that grows with touched host memory)."""
+    L = S.lib()
+    for n, (res, args) in {"sg_mem_tracker_reset": (None, [C.c_void_p]),
+                           "sg_mem_tracker_sample": (None, [C.c_void_p, C.c_uint64, C.c_uint64]),
+                           "sg_mem_tracker_peak": (C.c_uint64, [C.c_void_p]),
+                           "sg_proc_phys_footprint": (C.c_uint64, [])}.items():
+        getattr(L, n).restype, getattr(L, n).argtypes = res, args
+    t = C.c_uint64(12345)
+    L.sg_mem_tracker_reset(C.byref(t))
+    assert L.sg_mem_tracker_peak(C.byref(t)) == 0
+    for cur, phys, want in [(10, 20, 20), (5, 5, 20), (100, 3, 100), (0, 0, 100), (2 ** 63, 1, 2 ** 63)]:
+        L.sg_mem_tracker_sample(C.byref(t), cur, phys)
+        assert L.sg_mem_tracker_peak(C.byref(t)) == want
+    L.sg_mem_tracker_reset(C.byref(t))
+    assert L.sg_mem_tracker_peak(C.byref(t)) == 0
+    L.sg_mem_tracker_sample(None, 1, 2)          # NULL tracker: no-op
+    assert L.sg_mem_tracker_peak(None) == 0
+    before = L.sg_proc_phys_footprint()
+    assert before > 0
+    block = np.ones(64 << 20, np.uint8)           # 64 MiB, touched
+    after = L.sg_proc_phys_footprint()
+    assert after >= before + (32 << 20), (before, after)
+    del block
