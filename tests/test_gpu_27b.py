@@ -31,7 +31,6 @@ FFN 17408, vocab 151936, separate lm_head), about 27.5 GB of weights.
 """
 import json
 import os
-import sys
 import time
 
 import numpy as np
@@ -115,12 +114,11 @@ def test_27b_4k_context_64_greedy_tokens_identical_to_oracle(gpu, model27):
     assert gen.tolist() == want
 
 
-def _progress(msg):
-    """Shown while the test runs (pytest captures sys.stderr, not the real one)."""
-    print(msg, file=sys.__stderr__, flush=True)
+def test_27b_32k_prefill_then_decode_matches_serial(gpu, model27, capsys):
+    def _progress(msg):          # shown while the test runs (about four minutes on one MI355X)
+        with capsys.disabled():
+            print(msg, flush=True)
 
-
-def test_27b_32k_prefill_then_decode_matches_serial(gpu, model27):
     n, n_gen = 32768, 32
     rng = np.random.default_rng(32768)
     prompt = rng.integers(0, S.CFG_27B["vocab"], n).tolist()
@@ -128,7 +126,7 @@ def test_27b_32k_prefill_then_decode_matches_serial(gpu, model27):
     t0 = time.time()
     for p, t in enumerate(prompt[:-1]):
         gpu.forward_nosync(t, p)
-        if (p + 1) % 4096 == 0:
+        if (p + 1) % 2048 == 0:
             gpu.sync()
             _progress(f"[27b-32k] serial forward at position {p + 1} of {n} ({time.time() - t0:.0f} s)")
     serial = gpu.forward(prompt[-1], n - 1)
