@@ -211,6 +211,54 @@ def cpu_baseline(syn, cfg, ctx, budget_s=15.0):
                 seconds_per_token=round(tok_s, 2), nproc=os.cpu_count())
 
 
+def secondary_2b(steps=64, ctx=128, cpu=True, cpu_positions=4):
+    """BASELINE's 2B configuration beside the headline: random-init 2B-shaped
+    Q8_0 hybrid, a 128-token random-id prompt prefilled, then greedy decode on
+    the GPU (device-resident, one HIP graph per token), tok/s over `steps`
+    steps; and the reference's own ref.c (oracle/_ref; else this repository's
+    oracle) timed on this host over the first `cpu_positions` positions of the
+    same prompt, one thread, scaled to tok/s (the whole 128 + 64 run would take
+    minutes of scalar CPU time)."""
+    cfg = S.CFG_2B
+    syn = S.Synth(cfg, S.SG_T_Q8_0, seed=0)
+    gpu = S.Gpu()
+    gpu.load_model(syn.model)
+    gpu.state_new(ctx + 8 + 2 * steps + 8)
+    prompt = np.random.default_rng(0).integers(0, cfg["vocab"], ctx).astype(np.int32)
+    lg = gpu.prefill(prompt, chunk=ctx)
+    w = gpu.decode_greedy(int(np.argmax(lg)), ctx, 8)
+    gpu.sync()
+    t0 = time.perf_counter()
+    gpu.decode_greedy(int(w[-1]), ctx + 8, steps)
+    dt = time.perf_counter() - t0
+    bytes_tok, _ = step_bytes(cfg, ctx + 8 + steps // 2)
+    fl_us, fl_n, _ = gpu.time_floor(ctx + 8 + steps // 2, 1, 20)
+    gpu.close()
+    out = dict(workload="2B-shape qwen35 hybrid Q8_0 (hidden 2048, 24 layers, 8q/2kv x 256, DeltaNet 16/16 x 128, "
+                        "FFN 6144, vocab 151936), greedy decode bs=1 after a 128-token prompt",
+               value=round(steps / dt, 2), unit="tok/s", steps=steps, ms_per_step=round(dt * 1e3 / steps, 4),
+               decode_hbm_frac=round(bytes_tok * steps / dt / 1e9 / HBM_PEAK_GBS, 4),
+               plain_read_floor_tok_s=round(1e6 / fl_us, 1), floor_kernels=fl_n, cpu_baseline=None)
+    if cpu:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_lib as O
+        kind = "reference" if O.ref_available() else "port"
+        L = O.ref() if kind == "reference" else O.oracle()
+        if kind == "port":
+            L.sg_ref_set_threads(1)
+        rm = O.RefModel(L, syn.model, cpu_positions + 1)
+        t0 = time.perf_counter()
+        for p in range(cpu_positions):
+            rm.forward(int(prompt[p]), p)
+        cs = (time.perf_counter() - t0) / cpu_positions
+        rm.close()
+        out["cpu_baseline"] = dict(value=round(1.0 / cs, 4), unit="tok/s", cores=1, kind=kind,
+                                   sample=f"sg_ref_forward of the first {cpu_positions} prompt positions of the "
+                                          f"same 2B model: {cs:.2f} s/token", nproc=os.cpu_count())
+    syn.close()
+    return out
+
+
 def micro(reps_gpu=200, rotate=1 << 30):
     """The BASELINE per-kernel configs on the product kernels, seeded as
     BASELINE.json states them: GPU microseconds per launch with every timed
@@ -392,6 +440,7 @@ def main():
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--shape", default="27b", choices=["27b", "2b"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-2b", action="store_true", help="skip the 2B-shape line beside the 27B headline")
     ap.add_argument("--chunk", type=int, default=512, help="prefill chunk (tokens)")
     ap.add_argument("--fill", action="store_true",
                     help="no prefill: seeded K/V and DeltaNet state up to --ctx (decode at depth)")
@@ -429,6 +478,13 @@ def main():
               f"{S.SG_KV_CAP_MAX}", file=sys.stderr)
         sys.exit(2)
     gpu.state_new(need)
+    # the row's GEMM gate reading, taken before the run as the reference's
+    # surge-bench takes it (cli_bench.c:346, 490): the prefill GEMM on layer
+    # 0's gate/up weight for one 512-token chunk, useful flops / time
+    gemm_us = gpu.time_gemm(0, 2, 512, 5)
+    gemm_tflops = 2.0 * 512 * 2 * cfg["ffn_hidden"] * cfg["hidden"] / (gemm_us * 1e-6) / 1e12
+    log(f"GEMM gate reading: gate/up {2 * cfg['ffn_hidden']}x{cfg['hidden']} over 512 tokens in {gemm_us:.1f} us "
+        f"({gemm_tflops:.1f} TFLOP/s)")
     t = time.time()
     if a.fill:
         gpu.fill_synthetic(a.ctx, seed=0)
@@ -488,17 +544,22 @@ def main():
     row.peak_ram_gib = peak_rss_gib()
     row.n_prompt_tok, row.n_gen = a.ctx, a.steps
     row.wall_s = pf_s + dt + slope_wall
-    # the admission gate's GEMM reading: the prefill's projection flops over its
-    # whole wall time (a lower bound on the prefill GEMM's rate)
-    row.gemm_tflops = -1.0 if a.fill else 2.0 * a.ctx * (parts["weights"] - q8_bytes(cfg["vocab"], cfg["hidden"])) \
-        * 32 / 34 / pf_s / 1e12
-    row.ingestion_ok = gpu.used() == pos + 2 * a.steps
+    row.gemm_tflops = gemm_tflops
+    ok = C.c_bool(False)
+    # the prompt's ids all went in (the fill sets the same depth without ids)
+    S.lib().sg_bench_check_ingestion(a.ctx, need, a.ctx, a.ctx, C.byref(ok))
+    row.ingestion_ok = ok.value and gpu.used() == pos + 2 * a.steps
     row.log_id = f"ctx{a.ctx}_{a.shape}_surge_amd".encode()
     S.lib().sg_bench_finalize_status(C.byref(row))
     gpu.close()
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline(syn, cfg, a.ctx)
+    sec = None
+    if a.shape == "27b" and not a.no_2b:
+        sec = secondary_2b(cpu=not a.no_cpu)
+        log(f"2B shape: {sec['value']} tok/s"
+            + (f", ref.c {sec['cpu_baseline']['value']} tok/s on one core" if sec["cpu_baseline"] else ""))
         log(f"cpu baseline: {cpu['sample']}")
     syn.close()
     line = {
@@ -518,6 +579,7 @@ def main():
         "roofline": roof,
         "decode_floor": floor,
         "cpu_baseline": cpu,
+        "secondary_2b": sec,
         "decode_by_slope": {"tok_s": round(slope, 3), "endpoint_avg_tok_s": round(avg, 3), "steps": a.steps,
                             "warmup": int(warm), "clock": "HIP events after each step"},
         "bench_row": {"md": row.md(), "json": json.loads(row.json())},

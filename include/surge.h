@@ -189,12 +189,14 @@ sg_err sg_gpu_run_op(sg_gpu *g, const char *kernel, void *a, void *b, void *out,
 sg_err sg_gpu_run_attn_decode_f16(sg_gpu *g, void *q, void *k, void *v, void *out,
                                   const uint32_t params[8]);
 /* No reference counterpart: sg_gpu_run_attn_decode_f16 with no device
- * allocation, for callers that cannot allocate (code under HIP graph
- * capture, serving loops, harnesses that forbid hipMalloc). Its partials live
- * in a static 4 MiB device workspace per GPU, so n_heads * n_splits *
- * (head_dim + 2) * 4 bytes must fit (n_splits = sg_gpu_splitk_gqa_n_splits(seq));
- * larger calls are refused. Calls that overlap on one GPU share the
- * workspace and race. */
+ * allocation, for callers that cannot allocate (serving loops, harnesses
+ * that forbid hipMalloc). Its partials live in a static 4 MiB device
+ * workspace per GPU, so n_heads * n_splits * (head_dim + 2) * 4 bytes must
+ * fit (n_splits = sg_gpu_splitk_gqa_n_splits(seq)); larger calls are refused.
+ * Like every sg_gpu_run_* call it is synchronous (it uploads and downloads
+ * the buffers' host mirrors and waits for the library's stream), so it
+ * cannot be recorded into a HIP graph capture of that stream. Calls that
+ * overlap on one GPU share the workspace and race. */
 sg_err sg_gpu_run_attn_decode_f16_noalloc(sg_gpu *g, void *q, void *k, void *v, void *out,
                                           const uint32_t params[8]);
 
@@ -294,7 +296,9 @@ sg_err sg_gpu_run_gdn_chunk(sg_gpu *g, void *in, void *w, void *state, void *out
  * hd] (per query head q | gate, then k, then v), w [2 hd] q_norm | k_norm,
  * kv [2][base + n][n_kv][hd] f16 (K then V; positions below base given, the
  * chunk's written), out [n][n_heads hd]. p: [0]=n_heads [1]=n_kv [2]=hd (64,
- * 128 or 256) [3]=rope_dim [4]=base [5]=n [6]=rope_theta bits [7]=eps bits. */
+ * 128 or 256) [3]=rope_dim [4]=base [5]=n [6]=rope_theta bits [7]=eps bits.
+ * The attention scale is fixed at 1/sqrt(hd), as the model's decode and
+ * prefill use it (ref.c:1238); params has no slot left for another. */
 sg_err sg_gpu_run_attn_chunk(sg_gpu *g, void *in, void *w, void *kv, void *out,
                              const uint32_t params[8]);
 /* Prefill chunk hooks (surge.h:1111-1142), reference layouts:
@@ -535,6 +539,11 @@ void sg_bench_format_json(const sg_bench_row *row, char *buf, size_t cap);   /* 
  * finalize sets status to "DONE" or "VOID" accordingly (surge.h:1939-1955). */
 bool sg_bench_admitted(const sg_bench_row *row);                           /* surge.h:1950 */
 void sg_bench_finalize_status(sg_bench_row *row);                          /* surge.h:1955 */
+/* The ingestion guard (surge.h:1980-1993): *ok = n_ids <= max_ctx (nothing
+ * truncated) and expect_min <= n_ids <= expect_max (the prompt's id count is
+ * the one expected); logged to stderr; a NULL ok is a no-op. */
+void sg_bench_check_ingestion(uint64_t n_ids, uint32_t max_ctx, uint64_t expect_min,
+                              uint64_t expect_max, bool *ok);                /* surge.h:1992 */
 
 /* The peak-memory probe (surge.h:2104-2142). sg_proc_phys_footprint: the
  * process's resident host memory in bytes, here from Linux's

@@ -147,6 +147,7 @@ _SIGS = {
     "sg_bench_format_json": (None, [C.c_void_p, C.c_char_p, C.c_size_t]),
     "sg_bench_admitted": (C.c_bool, [C.c_void_p]),
     "sg_bench_finalize_status": (None, [C.c_void_p]),
+    "sg_bench_check_ingestion": (None, [C.c_uint64, C.c_uint32, C.c_uint64, C.c_uint64, C.POINTER(C.c_bool)]),
     "sg_gpu_prefill": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.POINTER(C.c_int32), C.c_uint32,
                                C.c_uint32, C.POINTER(C.POINTER(C.c_float))]),
     "sg_gpu_sync": (SgErr, [C.c_void_p]),

@@ -141,3 +141,14 @@ void sg_mem_tracker_sample(sg_mem_tracker *t, uint64_t current_alloc, uint64_t p
 }
 
 uint64_t sg_mem_tracker_peak(const sg_mem_tracker *t) { return t ? t->peak : 0; }
+
+/* The row's ingestion guard (reference surge.h:1980-1993): the prompt was not
+ * cut to fit the context and its id count is in the expected range. */
+void sg_bench_check_ingestion(uint64_t n_ids, uint32_t max_ctx, uint64_t expect_min, uint64_t expect_max,
+                              bool *ok) {
+    if (!ok) return;
+    *ok = n_ids <= (uint64_t)max_ctx && n_ids >= expect_min && n_ids <= expect_max;
+    fprintf(stderr, "bench: ingestion guard: %llu ids, max_ctx %u, expected [%llu, %llu]: %s\n",
+            (unsigned long long)n_ids, max_ctx, (unsigned long long)expect_min, (unsigned long long)expect_max,
+            *ok ? "ok" : "failed");
+}

@@ -736,6 +736,14 @@ sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *ga
  * p: [0]=dk [1]=dv [2]=n_v [3]=n_k [4]=ksize [5]=tiled [6]=ssm_a is -exp(A_log)
  * [7]=eps bits. conv_dim = 2 n_k dk + n_v dv. head_v_dim <= 128 (one
  * workgroup per value head, the decode default). */
+/* SURGE_DELTA_SCAN, the prefill DeltaNet scan's form: mfma (default), wy or
+ * seq. Any other value is refused, not ignored, so an A/B of scan forms never
+ * measures one it did not name. */
+static sg_err delta_scan_env(void) {
+    if (sgk_delta_scan_env_ok()) return SG_OK;
+    return errf("gpu: SURGE_DELTA_SCAN='%s' must be mfma, wy or seq (default mfma)", getenv("SURGE_DELTA_SCAN"));
+}
+
 sg_err sg_gpu_run_gdn_step(sg_gpu *g, void *in, void *w, void *state, void *out, const uint32_t p[8]) {
     if (!g || !in || !w || !state || !out || !p) return (sg_err){"gpu: gdn_step got a NULL argument"};
     const uint32_t dk = p[0], dv = p[1], nv = p[2], nk = p[3], ks = p[4];
@@ -792,6 +800,7 @@ sg_err sg_gpu_run_gdn_chunk(sg_gpu *g, void *in, void *w, void *state, void *out
     if (!g || !in || !w || !state || !out || !p) return (sg_err){"gpu: gdn_chunk got a NULL argument"};
     const uint32_t dk = p[0], dv = p[1], nv = p[2], nk = p[3], ks = p[4], n = p[6];
     if (dk != 32 && dk != 64 && dk != 128 && dk != 256) return (sg_err){"gpu: gdn_chunk: dk must be 32, 64, 128 or 256"};
+    if (sg_failed(delta_scan_env())) return delta_scan_env();
     if (!dv || !nv || !nk || nv % nk || ks < 1 || ks > 4 || !n)
         return (sg_err){"gpu: gdn_chunk: bad shape (n_v a multiple of n_k, ksize 1..4, n > 0)"};
     const uint64_t cd = 2ull * nk * dk + (uint64_t)nv * dv, vd = (uint64_t)nv * dv, keep = ks - 1;
@@ -881,6 +890,7 @@ sg_err sg_gpu_run_delta_chunk(sg_gpu *g, void *S, void *qkv, void *out, void *ga
     if (!dk || !dv || !nv || !nk || nv % nk || kd != nk * dk || cd < 2 * kd + nv * dv || !n_tok)
         return (sg_err){"gpu: delta_chunk: bad shape"};
     if (dk != 32 && dk != 64 && dk != 128 && dk != 256) return (sg_err){"gpu: delta_chunk: dk must be 32, 64, 128 or 256"};
+    if (sg_failed(delta_scan_env())) return delta_scan_env();
     sg_err e;
     if (sg_failed(e = need(S, (uint64_t)nv * dv * dk * 4, "S")) || sg_failed(e = need(qkv, (uint64_t)n_tok * cd * 4, "qkv")) ||
         sg_failed(e = need(out, (uint64_t)n_tok * nv * dv * 4, "out")) ||
@@ -1636,6 +1646,7 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     /* SURGE_SPLITK_GQA_CAP (reference surge.h:1239-1256): plain decimal digits
      * in [4, 1024], else the state is refused. */
     uint32_t cap = SGK_MAX_SPLITS;
+    if (sg_failed(delta_scan_env())) return delta_scan_env();
     const char *cap_env = getenv("SURGE_SPLITK_GQA_CAP");
     if (cap_env && cap_env[0] != '\0') {
         uint64_t v = 0;
@@ -2146,6 +2157,7 @@ sg_err sg_gpu_prefill(sg_gpu *g, const sg_model *m, const int32_t *tokens, uint3
     if (!g->have_state) return (sg_err){"gpu: call sg_gpu_state_new first"};
     if (m != g->model) return (sg_err){"gpu: this gpu was loaded with a different sg_model"};
     if (!n_tokens || n_tokens > g->max_ctx) return (sg_err){"gpu: n_tokens must be in [1, max_ctx]"};
+    if (sg_failed(delta_scan_env())) return delta_scan_env();
     for (uint32_t i = 0; i < n_tokens; i++)
         if (tokens[i] < 0 || (uint32_t)tokens[i] >= g->cfg.vocab) return (sg_err){"gpu: token id out of range"};
     uint32_t chunk = chunk_size ? chunk_size : SG_PREFILL_CHUNK_DEFAULT;

@@ -221,6 +221,9 @@ hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t in_stride, 
 hipError_t sgk_delta_scan(const sgk_gdn *a, const float *qkv, uint32_t in_stride, uint32_t ntok,
                           const float *gates, float *ws, hipStream_t s);
 uint64_t sgk_delta_wy_ws_floats(uint32_t n_v, uint32_t ntok);
+/* Whether SURGE_DELTA_SCAN holds a form the scan knows (unset, empty, mfma,
+ * wy, seq); the host refuses to run with any other value. */
+int sgk_delta_scan_env_ok(void);
 /* Conv over a chunk with an oldest-first state [ksize-1][ch] in/out, no
  * activation (the reference's k_conv1d_chunk contract). */
 hipError_t sgk_conv1d_chunk(const float *x, const float *w, float *out, float *state, uint32_t ch,

@@ -3649,11 +3649,19 @@ __global__ void __launch_bounds__(DM_TPB) k_dm_scan(sgk_gdn a, const float *qkv,
 // run the sequential loop. Per 512-token call of the 27B layer (48 heads,
 // dk = dv = 128): mfma 51 + 11 us (scan + prep), seq 199 us.
 enum { SCAN_SEQ, SCAN_WY, SCAN_MFMA };
+// SURGE_DELTA_SCAN: unset, empty or "mfma" (default), "wy" or "seq"; any
+// other value is refused by the host before a scan launches
+// (sgk_delta_scan_env_ok), so an A/B never measures a form it did not name.
 static int scan_mode() {
     const char *e = getenv("SURGE_DELTA_SCAN");
-    if (!e || !strcmp(e, "mfma")) return SCAN_MFMA;
-    if (!strcmp(e, "wy")) return SCAN_WY;
-    return SCAN_SEQ;
+    if (e && !strcmp(e, "wy")) return SCAN_WY;
+    if (e && !strcmp(e, "seq")) return SCAN_SEQ;
+    return SCAN_MFMA;
+}
+
+extern "C" int sgk_delta_scan_env_ok(void) {
+    const char *e = getenv("SURGE_DELTA_SCAN");
+    return !e || !*e || !strcmp(e, "mfma") || !strcmp(e, "wy") || !strcmp(e, "seq");
 }
 
 extern "C" uint64_t sgk_delta_wy_ws_floats(uint32_t n_v, uint32_t ntok) {

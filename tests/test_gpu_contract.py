@@ -34,6 +34,24 @@ def tiny(gpu, monkeypatch):
     syn.close()
 
 
+def test_delta_scan_switch_rejected_not_ignored(gpu, tiny, monkeypatch):
+    """SURGE_DELTA_SCAN names the prefill DeltaNet scan's form: mfma (the
+    default), wy or seq; a misspelt value is refused at sg_gpu_state_new and
+    by the prefill and chunk entry points, not silently run as another form."""
+    for bad in ("MFMA", "wy ", "sequential", "1"):
+        monkeypatch.setenv("SURGE_DELTA_SCAN", bad)
+        with pytest.raises(S.SurgeError, match="SURGE_DELTA_SCAN"):
+            gpu.state_new(64)
+    for good in ("mfma", "wy", "seq", ""):
+        monkeypatch.setenv("SURGE_DELTA_SCAN", good)
+        gpu.state_new(64)
+    monkeypatch.setenv("SURGE_DELTA_SCAN", "Wy")
+    with pytest.raises(S.SurgeError, match="SURGE_DELTA_SCAN"):
+        gpu.prefill([1, 2, 3, 4], chunk=4)
+    monkeypatch.delenv("SURGE_DELTA_SCAN")
+    gpu.prefill([1, 2, 3, 4], chunk=4)
+
+
 def test_online_switch_rejected_not_ignored(gpu, tiny, monkeypatch):
     """SURGE_ATTN_SPLITK_ONLINE takes exactly "0" or "1"; anything else is an
     error at sg_gpu_state_new (an ignored value would make its A/B vacuous)."""

@@ -440,7 +440,7 @@ def test_gdn_decode_step_vs_oracle(gpu, nv, nk, dk, dv, ks, tiled):
 
 GDN_CHUNK_CASES = [(16, 16, 128, 128, 4, True, 37, 2), (48, 16, 128, 128, 4, True, 130, 19),
                    (6, 2, 64, 64, 4, False, 33, 50), (8, 4, 128, 96, 2, True, 20, 2),
-                   (4, 4, 256, 128, 3, False, 18, 5)]
+                   (4, 4, 256, 128, 3, False, 18, 5), (8, 4, 32, 32, 4, True, 24, 9)]
 
 
 @pytest.mark.parametrize("nv,nk,dk,dv,ks,tiled,n1,n2", GDN_CHUNK_CASES,
@@ -456,7 +456,8 @@ def test_gdn_prefill_chunk_vs_oracle(gpu, nv, nk, dk, dv, ks, tiled, n1, n2):
     composed from the oracle, token by token: the BASELINE DeltaNet config
     (16 heads, 128^2, conv width 4), the 27B's 48 value heads tiled over 16
     key heads over a 130-token chunk (eight full 16-token blocks and a
-    partial one), a grouped dk 64 map, conv widths 2 and 3. Two chunks in a
+    partial one), a grouped dk 64 map, conv widths 2 and 3, and dk 32 (the
+    sequential scan with the separate q/k norm pass). Two chunks in a
     row thread the conv tail and S, the second starting at another ring slot
     (and shorter than the conv tail in one case); outputs and S within 1e-3,
     the conv tail bit-exact (it holds the inputs)."""
@@ -813,7 +814,7 @@ def test_rmsnorm_gated_chunk(gpu):
 
 
 ATTN_CHUNK_CASES = [(24, 4, 256, 64, 1000, 150), (8, 2, 256, 64, 0, 130), (12, 4, 128, 32, 300, 70),
-                    (16, 4, 128, 128, 600, 64)]
+                    (16, 4, 128, 128, 600, 64), (8, 2, 64, 32, 200, 70)]
 
 
 @pytest.mark.parametrize("nh,nkv,hd,rd,base,n", ATTN_CHUNK_CASES,
@@ -827,7 +828,8 @@ def test_attn_prefill_chunk_vs_oracle(gpu, nh, nkv, hd, rd, base, n):
     rounded to f16, decode attention over keys 0..position, gate): the 27B's
     24q/4kv/256 with rope 64 deep enough for a 3-way key split, the 2B's
     8q/2kv/256 from position 0, an odd GQA group (12/4, one query head per
-    workgroup) at head_dim 128 / rope 32, and a full rope. Outputs within
+    workgroup) at head_dim 128 / rope 32, a full rope, and head_dim 64 with
+    rope 32 (8q/2kv). Outputs within
     1e-3; V stored bit-exact (both round the same f32); K within one f16
     ulp of the oracle's (its f32 before rounding differs in the last bits);
     the keys before the chunk untouched."""

@@ -434,3 +434,18 @@ def test_mem_tracker_and_phys_footprint():
     after = L.sg_proc_phys_footprint()
     assert after >= before + (32 << 20), (before, after)
     del block
+
+
+def test_bench_ingestion_guard():
+    """sg_bench_check_ingestion (reference surge.h:1980-1993): true iff the
+    ids fit the context and their count is in the expected range; a NULL
+    ok is a no-op."""
+    L = S.lib()
+    ok = C.c_bool(False)
+    for n, cap, lo, hi, want in [(4096, 4096, 4096, 4096, True), (4097, 4096, 0, 10 ** 6, False),
+                                 (100, 4096, 101, 200, False), (150, 4096, 101, 200, True),
+                                 (201, 4096, 101, 200, False), (0, 0, 0, 0, True)]:
+        ok.value = not want
+        L.sg_bench_check_ingestion(n, cap, lo, hi, C.byref(ok))
+        assert ok.value == want, (n, cap, lo, hi)
+    L.sg_bench_check_ingestion(1, 1, 1, 1, None)
