@@ -113,10 +113,17 @@ def decode_floor(gpu, ctx, reps=20):
     """The sequential-launch floor of this decode token (sg_gpu_time_floor):
     its launch sequence captured in one HIP graph with every kernel replaced
     by a plain streaming read of that kernel's algorithmic bytes, and by an
-    empty kernel. What kernels run one after another cannot beat."""
+    empty kernel. What kernels run one after another cannot beat. With
+    SURGE_HIP_GRAPH=0 (the decode launched kernel by kernel, as under a kernel
+    trace) the reads are launched one by one too, so a trace of the run pairs
+    each decode kernel with the read of its bytes."""
+    if os.environ.get("SURGE_HIP_GRAPH") == "0":
+        rd_us, n, nb = gpu.time_floor(ctx, 2, reps)
+        return dict(kernels=n, bytes_per_token=int(nb), launch="one by one (SURGE_HIP_GRAPH=0)",
+                    plain_read_us_per_token=round(rd_us, 1), plain_read_tok_s=round(1e6 / rd_us, 2), reps=reps)
     rd_us, n, nb = gpu.time_floor(ctx, 1, reps)
     em_us, _, _ = gpu.time_floor(ctx, 0, reps)
-    return dict(kernels=n, bytes_per_token=int(nb), plain_read_us_per_token=round(rd_us, 1),
+    return dict(kernels=n, bytes_per_token=int(nb), launch="one captured graph", plain_read_us_per_token=round(rd_us, 1),
                 plain_read_tok_s=round(1e6 / rd_us, 2), plain_read_frac=round(nb / rd_us / 1e3 / HBM_PEAK_GBS, 4),
                 empty_us_per_token=round(em_us, 1), reps=reps)
 
@@ -527,8 +534,9 @@ def main():
     roof["traffic"] = measured_traffic("k_gemv_q8<2, 1, 2>")
     log(f"gate/up GEMV: {roof['avg_us']} us/launch, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
     floor = decode_floor(gpu, a.ctx + a.warmup + a.steps // 2)
-    log(f"sequential-launch floor: {floor['kernels']} plain reads {floor['plain_read_us_per_token']} us/token "
-        f"({floor['plain_read_tok_s']} tok/s), {floor['kernels']} empty kernels {floor['empty_us_per_token']} us")
+    log(f"sequential-launch floor ({floor['launch']}): {floor['kernels']} plain reads "
+        f"{floor['plain_read_us_per_token']} us/token ({floor['plain_read_tok_s']} tok/s)"
+        + (f", {floor['kernels']} empty kernels {floor['empty_us_per_token']} us" if "empty_us_per_token" in floor else ""))
     row = S.BenchRow()
     row.model = f"qwen35-{a.shape}-shape-q8_0-random".encode()
     row.engine = b"surge_amd (MI355X, HIP)"

@@ -1381,8 +1381,8 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             if ((e = sgk_gdn_step(&d, s)) != hipSuccess) return e;
             if (g->gdn_blocks == 1) {
                 o.x = g->gbuf; o.pro = SGK_PRO_NONE;          /* the step finished RMSNormGated */
-            } else {                                          /* RMSNormGated in the out projection's prologue */
-                o.x = g->ybuf; o.x2 = g->gbuf; o.gss = g->gss; o.nw = L->ssm_norm; o.gdv = c->head_v_dim;
+            } else {                  /* each head's RMS factor applied in the out projection's prologue */
+                o.x = g->gbuf; o.gss = g->gss; o.gdv = c->head_v_dim;
                 o.pro = SGK_PRO_GATED;
             }
         }
@@ -1668,10 +1668,16 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     else if (sg_gpu_splitk_online_selected(g, c->n_heads, c->n_kv_heads, c->head_dim, max_ctx)) g->attn_arm = ARM_ONLINE;
     else if (sg_gpu_splitk_gqa_selected(g, c->n_heads, c->n_kv_heads, max_ctx)) g->attn_arm = ARM_GQA;
     else g->attn_arm = ARM_PER_HEAD;
-    /* One workgroup per DeltaNet value head finishes RMSNormGated itself
-     * (head_v_dim <= 128); wider heads use SGK_GDN_BLOCKS row blocks and the
-     * out projection's gated prologue. SURGE_GDN_BLOCKS=1|4 overrides. */
-    g->gdn_blocks = c->head_v_dim <= 128 ? 1 : SGK_GDN_BLOCKS;
+    /* The DeltaNet step runs SGK_GDN_BLOCKS row-block workgroups per value
+     * head, the out projection's gated prologue finishing RMSNormGated
+     * (measured faster than one workgroup per head finishing it itself);
+     * a decode chain (SURGE_CHAIN=1|2) takes one workgroup per head.
+     * SURGE_GDN_BLOCKS=1 (head_v_dim <= 128) | 4 overrides. */
+    g->gdn_blocks = SGK_GDN_BLOCKS;
+    {
+        const char *cr = getenv("SURGE_CHAIN");
+        if (c->head_v_dim <= 128 && cr && (!strcmp(cr, "1") || !strcmp(cr, "2"))) g->gdn_blocks = 1;
+    }
     {
         const char *gb = getenv("SURGE_GDN_BLOCKS");
         if (gb && gb[0]) {
@@ -2234,10 +2240,7 @@ sg_err sg_gpu_enqueue_gemv_tuned(sg_gpu *g, uint32_t layer, uint32_t which, uint
             M = &L->out; a.y = g->x; a.epi = SGK_EPI_ADD;
             if (L->attn) { a.x = g->ctx; a.pro = SGK_PRO_NONE; }
             else if (g->gdn_blocks == 1) { a.x = g->gbuf; a.pro = SGK_PRO_NONE; }
-            else {
-                a.x = g->ybuf; a.x2 = g->gbuf; a.gss = g->gss; a.nw = L->ssm_norm; a.gdv = c->head_v_dim;
-                a.pro = SGK_PRO_GATED;
-            }
+            else { a.x = g->gbuf; a.gss = g->gss; a.gdv = c->head_v_dim; a.pro = SGK_PRO_GATED; }
             break;
         case 2: M = &L->gu; a.x = g->x; a.nw = L->ln2; a.y = g->ffg; a.pro = SGK_PRO_RMS; a.epi = SGK_EPI_SWIGLU; break;
         case 3: M = &L->down; a.x = g->ffg; a.y = g->x; a.pro = SGK_PRO_NONE; a.epi = SGK_EPI_ADD; break;

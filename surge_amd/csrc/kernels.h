@@ -62,7 +62,7 @@ static inline uint32_t sgk_n_splits(uint32_t seq) { return sgk_n_splits_cap(seq,
  * the RMS factor applied to each row sum) and epilogues (what is done with
  * each output row). */
 enum { SGK_PRO_NONE = 0, SGK_PRO_RMS = 1, SGK_PRO_GATED = 2 };
-#define SGK_GATED_MAX_HEADS 256u
+#define SGK_GATED_MAX_HEADS 256u    /* value heads the gated prologue takes */
 enum { SGK_EPI_STORE = 0, SGK_EPI_ADD = 1, SGK_EPI_SWIGLU = 2,
        SGK_EPI_TILE = 3, SGK_EPI_SWIGLU_XS = 4 /* prefill GEMM internal */ };
 
@@ -77,9 +77,11 @@ typedef struct {
     float *y;               /* output [rows] (or [rows/2] for SWIGLU) */
     int pro, epi;
     uint32_t tune_r, tune_blocks;   /* 0 = default; rows per wave (1/2/4), workgroups */
-    /* PRO_GATED (the DeltaNet out projection): x = readout y, x2 = silu(z),
-     * nw = ssm_norm [gdv], gss = row-block sums of squares [heads][SGK_GDN_BLOCKS] */
-    const float *x2, *gss;
+    /* PRO_GATED (the DeltaNet out projection after a step of SGK_GDN_BLOCKS
+     * workgroups per head): x = silu(z) * (y * ssm_norm), gss = each head's
+     * row-block sums of y^2 [heads][SGK_GDN_BLOCKS], gdv = head_v_dim; the
+     * prologue stages x * rsqrt(mean y^2 + eps) per head */
+    const float *gss;
     uint32_t gdv;
 } sgk_gemv;
 
@@ -186,9 +188,11 @@ typedef struct {
     const sgk_step SGK_G *step;
     uint32_t n_k, n_v, dk, dv, conv_dim, ksize;
     int tiled, neg_exp;
-    /* decode step only: z [value_dim] (the projection's z rows); out receives
-     * silu(z), y the pre-norm readouts and ss [n_v][SGK_GDN_BLOCKS] each row
-     * block's sum of squared readouts, for the gated GEMV prologue */
+    /* decode step only: z [value_dim] (the projection's z rows), norm_w the
+     * ssm_norm weight [dv]; with blocks == 1 out receives RMSNormGated's
+     * output, with SGK_GDN_BLOCKS out receives silu(z) * (y * norm_w) and ss
+     * [n_v][SGK_GDN_BLOCKS] each row block's sum of squared readouts y, for
+     * the gated GEMV prologue (y is not written) */
     const float SGK_G *z;
     const float SGK_G *norm_w;
     float SGK_G *out;
@@ -199,9 +203,9 @@ typedef struct {
 } sgk_gdn;
 #define SGK_GDN_MAX_DV 256u
 #define SGK_GDN_BLOCKS 4u
-/* The decode step (SGK_GDN_BLOCKS workgroups per value head; needs dv <=
- * SGK_GDN_MAX_DV); RMSNormGated is finished by the out projection's
- * SGK_PRO_GATED prologue. */
+/* The decode step (blocks == 1: one workgroup per value head, dv <= 128;
+ * else SGK_GDN_BLOCKS per head, dv <= SGK_GDN_MAX_DV, RMSNormGated's per-head
+ * factor applied by the out projection's SGK_PRO_GATED prologue). */
 hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s);
 
 /* The DeltaNet layer over a prefill chunk of ntok tokens (a->step holds the

@@ -140,11 +140,11 @@ __device__ __forceinline__ uint32_t dev_n_splits(uint32_t seq, uint32_t cap) {
 // the epilogue to apply to each row sum: W(x*r*w) = r * W(x*w). Other
 // prologues return 1. Needs x and w 16-byte aligned (every buffer of this
 // library is).
-// PRO_GATED keeps y in v, silu(z) in g, the norm weight in w and this
-// thread's head's per-block sums of squares in gs.
+// PRO_GATED keeps the step's gated product silu(z) * (y * w) in v and the
+// per-block sums of y^2 of head t (thread t < heads) in gs.
 template <int PRO, int NT, int K>
 struct xstage {
-    float4 v[K], g[PRO != SGK_PRO_NONE ? K : 1], w[PRO == SGK_PRO_GATED ? K : 1];
+    float4 v[K], g[PRO == SGK_PRO_RMS ? K : 1];
     float gs[PRO == SGK_PRO_GATED ? SGK_GDN_BLOCKS : 1];
 };
 
@@ -154,17 +154,11 @@ __device__ __forceinline__ void stage_issue(const sgk_gemv &a, xstage<PRO, NT, K
     if (!n4) return;
     const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.nw;
     if (PRO == SGK_PRO_GATED) {
-        const float4 *z4 = (const float4 *)a.x2;
         const uint32_t nh = a.cols / a.gdv, hh = min(t, nh - 1);
 #pragma unroll
         for (uint32_t b = 0; b < SGK_GDN_BLOCKS; b++) st.gs[b] = a.gss[hh * SGK_GDN_BLOCKS + b];
 #pragma unroll
-        for (int k = 0; k < K; k++) {
-            const uint32_t i = min(t + (uint32_t)k * NT, n4 - 1), j = 4 * i;
-            st.v[k] = x4[i];
-            st.g[k] = z4[i];
-            st.w[k] = *(const float4 *)(a.nw + (j - (j / a.gdv) * a.gdv));
-        }
+        for (int k = 0; k < K; k++) st.v[k] = x4[min(t + (uint32_t)k * NT, n4 - 1)];
         return;
     }
 #pragma unroll
@@ -184,11 +178,12 @@ __device__ __forceinline__ void stage_issue(const sgk_gemv &a, xstage<PRO, NT, K
 // float4s land in different banks (the 65th float4 of a plane is padding).
 // Without CH (the f32 GEMV) x is linear.
 #define XS_CH_BLK 260
-// k_gemv_q8 stages x chunked behind a prologue (RMSNorm, gated norm) and
-// linearly without one: the prologue-less GEMVs here (output and, at 2B, down
-// projections) run about one row group per wave, and were 5-8% slower chunked
-// (the conflict-free inner loop gains nothing there).
-#define GEMV_CH(PRO) ((PRO) != SGK_PRO_NONE)
+// k_gemv_q8 stages x chunked behind the RMSNorm prologue and linearly
+// otherwise: the output projections (prologue-less, or the gated one after a
+// multi-block DeltaNet step) and, at 2B, the down projections run about one
+// row group per wave, and were 5-8% slower chunked (the conflict-free inner
+// loop gains nothing there).
+#define GEMV_CH(PRO) ((PRO) == SGK_PRO_RMS)
 __host__ __device__ __forceinline__ uint32_t xs_ch_floats(uint32_t cols) {
     return ((cols / 16 + 63) / 64) * XS_CH_BLK * 4;
 }
@@ -203,18 +198,20 @@ __device__ __forceinline__ float stage_finish(const sgk_gemv &a, xstage<PRO, NT,
     __shared__ float red[NT / 64];
     const uint32_t n = a.cols, t = threadIdx.x, n4 = n >> 2;
     if (PRO == SGK_PRO_GATED) {
-        // RMSNormGated of the DeltaNet readout (ref.c:1322-1330): head hh's
-        // factor from its row blocks' sums of squares (added in block order),
-        // then x = silu(z) * ((y * r) * w) with silu(z) precomputed.
+        // RMSNormGated of the DeltaNet readout (ref.c:1322-1330) finished:
+        // head hh's factor r = rsqrt(mean y^2 + eps) from its row blocks' sums
+        // of squares (added in block order), then x = (silu(z) * (y * w)) * r,
+        // the step having written the product in parentheses.
         // The loads were issued by stage_issue (K float4s per thread cover
-        // every column: the launcher holds cols <= K*NT*4 and heads <= NT).
+        // every column: the launcher holds cols <= K*NT*4 and heads <=
+        // SGK_GATED_MAX_HEADS <= NT).
         __shared__ float rh[SGK_GATED_MAX_HEADS];
-        const uint32_t dv = a.gdv, nh = n / dv;
+        const uint32_t nh = n / a.gdv;
         if (t < nh) {
             float tot = 0.0f;
 #pragma unroll
             for (uint32_t b = 0; b < SGK_GDN_BLOCKS; b++) tot += st.gs[b];
-            rh[t] = 1.0f / sqrtf(tot / (float)dv + a.eps);
+            rh[t] = 1.0f / sqrtf(tot / (float)a.gdv + a.eps);
         }
         __syncthreads();
         float4 *s4 = (float4 *)xs;
@@ -222,10 +219,9 @@ __device__ __forceinline__ float stage_finish(const sgk_gemv &a, xstage<PRO, NT,
         for (int k = 0; k < K; k++) {
             const uint32_t i = t + (uint32_t)k * NT;
             if (i < n4) {
-                const float4 yv = st.v[k], zv = st.g[k], wv = st.w[k];
-                const float r = rh[(4 * i) / dv];
-                s4[xs4_at<CH>(i)] = make_float4(zv.x * ((yv.x * r) * wv.x), zv.y * ((yv.y * r) * wv.y),
-                                                     zv.z * ((yv.z * r) * wv.z), zv.w * ((yv.w * r) * wv.w));
+                const float4 xv = st.v[k];
+                const float r = rh[(4 * i) / a.gdv];
+                s4[xs4_at<CH>(i)] = make_float4(xv.x * r, xv.y * r, xv.z * r, xv.w * r);
             }
         }
         __syncthreads();
@@ -278,6 +274,7 @@ __device__ __forceinline__ float stage_finish(const sgk_gemv &a, xstage<PRO, NT,
 // float4s per thread a TPB-thread workgroup's stage_issue keeps in flight:
 // enough for rows of 8192 columns, the widest the row-group GEMV takes.
 constexpr int XK = 8192 / 4 / TPB;
+static_assert(SGK_GATED_MAX_HEADS <= TPB, "gated prologue: one thread per head's factor");
 
 template <int PRO>
 __device__ __forceinline__ float stage_x(const sgk_gemv &a, float *xs) {
@@ -846,10 +843,8 @@ static hipError_t launch_bal(const sgk_gemv &a, hipStream_t s) {
 template <int PRO, int EPI>
 static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
     if (((uintptr_t)a->x & 15) || (PRO == SGK_PRO_RMS && ((uintptr_t)a->nw & 15))) return hipErrorInvalidValue;
-    if (PRO == SGK_PRO_GATED && (!a->x2 || !a->gss || !a->nw || !a->gdv || a->gdv % 4 || a->cols % a->gdv ||
-                                 a->cols / a->gdv > SGK_GATED_MAX_HEADS || a->cols > (uint32_t)XK * TPB * 4 ||
-                                 ((uintptr_t)a->x2 & 15) ||
-                                 ((uintptr_t)a->nw & 15)))
+    if (PRO == SGK_PRO_GATED && (!a->gss || !a->gdv || a->gdv % 4 || a->cols % a->gdv ||
+                                 a->cols / a->gdv > SGK_GATED_MAX_HEADS || a->cols > (uint32_t)XK * TPB * 4))
         return hipErrorInvalidValue;
     if (!a->qs) {
         const size_t lds = (size_t)a->cols * 4;
@@ -2487,10 +2482,11 @@ __device__ __forceinline__ uint32_t rows_lane(uint32_t r) {   // a lane holding 
 // (eps 1e-6, no weight) then q/dk and k/sqrt(dk), beta/decay, the rank-1
 // delta update of its dv/GDN_NB state rows with their readout, all requested
 // before any arithmetic. Wave w updates RW rows; each row's two dot products
-// are reduced for all of them at once (rows_sum). RMSNormGated needs the whole
-// head, so it is left to the output projection's gated prologue: each block
-// writes its readouts y, silu(z) of its rows and its rows' sum of squares,
-// with no synchronisation between blocks.
+// are reduced for all of them at once (rows_sum). With one block per head the
+// block finishes RMSNormGated itself; with several, the head's factor needs
+// every block's readouts, so it is left to the output projection's gated
+// prologue: each block writes silu(z) * (y * w) of its rows and the sum of its
+// rows' squared readouts, with no synchronisation between blocks.
 // Stores that other workgroups of the same launch read after a chain barrier
 // go straight to memory (device-scope relaxed atomic stores: sc1, written
 // through the XCD's L2), so no cache-wide flush is needed to publish them.
@@ -2508,7 +2504,7 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
     __shared__ float qk[2 * DK];
     __shared__ float vv[NW * RW];
     __shared__ float red[NW];
-    __shared__ float ysh[NB == 1 ? SGK_GDN_MAX_DV : 1];
+    __shared__ float ysh[SGK_GDN_MAX_DV];
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t dk = DK, dv = a.dv, key_dim = a.n_k * dk, cd = a.conv_dim;
     const uint32_t rpb = (dv + GDN_NB - 1) / GDN_NB, jlo = jb * rpb, jhi = min(dv, jlo + rpb);
@@ -2545,7 +2541,7 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
     uint32_t ch = chan(min(t, nch - 1));
     conv_loads(ch);
     const float zraw = a.z[(size_t)h * dv + min(max(t, jlo), jhi - 1)];
-    const float nwt = NB == 1 ? a.norm_w[min(t, dv - 1)] : 0.0f;   // needed last, loaded early
+    const float nwt = a.norm_w[min(t, dv - 1)];   // needed last, loaded early
     const float *bb = a.in + cd + a.n_v * dv, *aa = bb + a.n_v;
     const float gb = bb[h], ga = aa[h], gA = a.ssm_a[h], gdt = a.dt_bias[h];
     const uint32_t j0 = jlo + wave * RW;
@@ -2628,10 +2624,7 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
         }
         const float yr = rows_sum<RW>(part, lane);
         const bool owner = (lane & (64 / RW - 1)) == 0 && j0 + myrow < jhi;
-        if (owner) {
-            if (NB == 1) ysh[j0 + myrow] = yr;
-            else a.y[(size_t)h * dv + j0 + myrow] = yr;
-        }
+        if (owner) ysh[j0 + myrow] = yr;
         // sum of squares of this wave's readouts, in row order
         float yy[RW];
 #pragma unroll
@@ -2665,15 +2658,16 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
         }
         return;
     }
-    // 5. this block's sum of squares and silu(z) of its rows: the output
-    //    projection's gated prologue finishes RMSNormGated from them.
+    // 5. this block's sum of squared readouts, and silu(z) * (y * w) of its
+    //    rows: the output projection's gated prologue finishes RMSNormGated
+    //    with the head's factor from the blocks' sums.
     if (t == 0) {
         float sb = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; w++) sb += red[w];
         a.ss[(size_t)h * GDN_NB + jb] = sb;
     }
-    if (t >= jlo && t < jhi) a.out[(size_t)h * dv + t] = silu(zj);
+    if (t >= jlo && t < jhi) a.out[(size_t)h * dv + t] = silu(zj) * (ysh[t] * nwt);
 }
 
 template <int DK, int RW, int NB, int GDN_TPB>
@@ -2704,7 +2698,7 @@ extern "C" hipError_t sgk_gdn_step(const sgk_gdn *a, hipStream_t s) {
 #undef DKCASE1
         return hipGetLastError();
     }
-    if (!a->y || !a->ss || a->dv > 256) return hipErrorInvalidValue;
+    if (!a->norm_w || !a->ss || a->dv > SGK_GDN_MAX_DV) return hipErrorInvalidValue;
     const uint32_t rpb = (a->dv + SGK_GDN_BLOCKS - 1) / SGK_GDN_BLOCKS;    // rows per block, at most 64
     dim3 grid(a->n_v, SGK_GDN_BLOCKS);
 #define DKCASE(D) case D:                                                                                  \

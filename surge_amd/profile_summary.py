@@ -35,6 +35,13 @@
       calibrated by the plain copy of B bytes in its run), the average duration
       over the decode region of the trace, and the achieved HBM GB/s and its
       fraction of the 8 TB/s peak;
+  python -m surge_amd.profile_summary floor KERNEL_TRACE_CSV
+      per decode kernel of one token: its average duration against that of
+      the plain read of its algorithmic bytes at the same place of the
+      token's launch sequence, from a `rocprofv3 --kernel-trace` run of
+      `SURGE_HIP_GRAPH=0 bench.py --fill` (decode tokens k_embed ..
+      k_step_advance after the first two; the floor's k_read dispatches in
+      tokens of the same length after the first), and the time lost per token;
   python -m surge_amd.profile_summary trace KERNEL_TRACE_CSV --kernel NAME --last N
       average duration of the last N dispatches of kernel NAME (prefix match)
       from a `rocprofv3 --kernel-trace` run, next to the average over all of
@@ -251,6 +258,67 @@ def hbm(fetch_csv, write_csv, trace_csv, calib_bytes, peak_gbs=8000.0):
     return out
 
 
+def floor(path):
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    dur = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    # decode tokens: k_embed .. k_step_advance, in launch order
+    toks, cur = [], None
+    for r in rows:
+        n = short(r["Kernel_Name"])
+        if n == "k_embed":
+            cur = [r]
+        elif cur is not None:
+            cur.append(r)
+            if n == "k_step_advance":
+                toks.append(cur)
+                cur = None
+    toks = toks[2:]
+    if not toks:
+        print("no decode tokens in the trace")
+        return None
+    n = len(toks[0])
+    toks = [t for t in toks if len(t) == n]
+
+    def kind(i):
+        nm = short(toks[0][i]["Kernel_Name"])
+        if nm.startswith("k_gemv_q8<2, 1, 0>"):
+            return "lm_head" if i + 1 < n and short(toks[0][i + 1]["Kernel_Name"]) == "k_argmax" else "input projection"
+        for pre, k in (("k_embed", "embedding"), ("k_attn_partial", "attention partial"),
+                       ("k_attn_combine", "attention combine"), ("k_gdn_step", "DeltaNet step"),
+                       ("k_gemv_q8<2, 0, 1>", "output projection"), ("k_gemv_q8<2, 1, 2>", "gate/up"),
+                       ("k_gemv_bal", "down projection"), ("k_argmax", "argmax"), ("k_step_advance", "step advance")):
+            if nm.startswith(pre):
+                return k
+        return nm
+    reads = [r for r in rows if short(r["Kernel_Name"]).startswith("k_read")]
+    nfl = len(reads) // n
+    fl = [reads[t * n:(t + 1) * n] for t in range(1, nfl)]
+    if not fl:
+        print("no floor reads in the trace")
+        return None
+    kinds = [kind(i) for i in range(n)]
+    order = list(dict.fromkeys(kinds))
+    agg = {k: [0, 0.0, 0.0] for k in order}
+    for i, k in enumerate(kinds):
+        agg[k][0] += 1
+        agg[k][1] += sum(dur(t[i]) for t in toks) / len(toks)
+        agg[k][2] += sum(dur(t[i]) for t in fl) / len(fl)
+    print(f"{len(toks)} decode tokens and {len(fl)} floor tokens of {n} kernels each (eager launches)")
+    print()
+    print("| kernel | launches/token | plain read of its bytes us | decode kernel us | lost per token us |")
+    print("|---|---|---|---|---|")
+    tot_d = tot_f = 0.0
+    for k in order:
+        c, d, f = agg[k]
+        tot_d += d
+        tot_f += f
+        print(f"| {k} | {c} | {f / c:.2f} | {d / c:.2f} | {d - f:.1f} |")
+    print(f"| all | {n} | | | {tot_d - tot_f:.1f} |")
+    print()
+    print(f"busy per token: decode {tot_d:.1f} us, plain reads {tot_f:.1f} us")
+    return agg
+
+
 def trace(path, kernel, last):
     durs = []
     for r in csv.DictReader(open(path)):
@@ -313,7 +381,7 @@ def micro(micro_jsonl, shapes_jsonl):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("mode", choices=["stats", "pmc", "trace", "decode", "traffic", "prefill", "counters", "hbm",
-                                     "micro"])
+                                     "micro", "floor"])
     ap.add_argument("--trace", default=None)
     ap.add_argument("csv")
     ap.add_argument("csv2", nargs="?", default=None)
@@ -331,6 +399,8 @@ def main():
         micro(a.csv, a.csv2)
     elif a.mode == "decode":
         decode(a.csv)
+    elif a.mode == "floor":
+        floor(a.csv)
     elif a.mode == "prefill":
         prefill(a.csv)
     elif a.mode == "hbm":

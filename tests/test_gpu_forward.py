@@ -519,20 +519,22 @@ WIDE_V = dict(n_layers=4, n_heads=8, n_kv_heads=2, head_dim=128, hidden=512, ffn
               conv_kernel=4, attn_output_gate=True)
 
 
-@pytest.mark.parametrize("cfg_name,blocks", [("HD128", "4"), ("WIDE_V", None)])
-def test_gdn_four_block_step_and_gated_prologue_vs_oracle(gpu, monkeypatch, cfg_name, blocks):
-    """The DeltaNet step split over four workgroups per value head, with
-    RMSNormGated finished in the output projection's gated prologue
-    (SGK_PRO_GATED): forced with SURGE_GDN_BLOCKS=4 on head_v_dim 64, and the
-    only path for head_v_dim 256. Logits within 1e-3 of the oracle with the
-    same argmax over 150 positions; SURGE_GDN_BLOCKS=1 is refused for
-    head_v_dim 256."""
+@pytest.mark.parametrize("cfg_name,blocks", [("HD128", None), ("HD128", "1"), ("WIDE_V", None)])
+def test_gdn_step_block_forms_vs_oracle(gpu, monkeypatch, cfg_name, blocks):
+    """Both forms of the DeltaNet decode step: four workgroups per value head
+    with RMSNormGated finished by the output projection's gated prologue
+    (SGK_PRO_GATED: the step writes silu(z) * (y * w) and each block's sum
+    of y^2, the prologue applies the head's factor), the default, here at
+    head_v_dim 64 and 256; and one workgroup per head finishing it itself
+    (SURGE_GDN_BLOCKS=1, which the decode chain uses). Logits within 1e-3 of
+    the oracle with the same argmax over 150 positions; SURGE_GDN_BLOCKS=1 is
+    refused for head_v_dim 256."""
     cfg = {"HD128": HD128, "WIDE_V": WIDE_V}[cfg_name]
     syn = S.Synth(cfg, S.SG_T_Q8_0, seed=31)
     gpu.load_model(syn.model)
     if blocks:
         monkeypatch.setenv("SURGE_GDN_BLOCKS", blocks)
-    else:
+    elif cfg_name == "WIDE_V":
         monkeypatch.setenv("SURGE_GDN_BLOCKS", "1")
         with pytest.raises(S.SurgeError):
             gpu.state_new(160)
