@@ -411,14 +411,11 @@ def gemv_shapes(reps=3):
     shapes = {0: "input projection (DeltaNet 16480x5120)", 1: "output projection 5120x6144",
               2: "gate|up 34816x5120", 3: "down 5120x17408", 4: "lm_head 151936x5120"}
     variants = [("default", None, 0), ("k_gemv_q8 (SURGE_GEMV=q8)", "q8", 0), ("k_gemv_bal contiguous", "bal", 0),
-                ("k_gemv_bal interleaved", "bali", 0), ("k_gemv_q8 R=1", None, 1), ("k_gemv_q8 R=4", None, 4),
-                ("k_gemv_q8_long LU=4", None, 3), ("k_gemv_q8_long LU=8", None, 6)]
+                ("k_gemv_bal interleaved", "bali", 0), ("k_gemv_q8 R=1", None, 1), ("k_gemv_q8 R=4", None, 4)]
     for which, name in shapes.items():
         layers = [0] if which == 4 else [l for l in range(L) if (l + 1) % cfg["full_attn_interval"] != 0]
         n = 8 if which == 4 else reps
         for vname, env, tune in variants:
-            if tune in (3, 6) and which != 3:
-                continue
             if env:
                 os.environ["SURGE_GEMV"] = env
             else:

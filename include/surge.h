@@ -359,23 +359,6 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
  * events between the steps, the series sg_bench_slope fits. */
 sg_err sg_gpu_decode_greedy_timed(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
                                   uint32_t n_steps, int32_t *out_tokens, double *t_cum);
-/* Whether the live state decodes through the chain (no reference
- * counterpart): SURGE_CHAIN=1 at sg_gpu_state_new, on a model the chain
- * takes (Q8_0 weights, GEMV widths multiples of 1024). The chain runs each
- * run of decode stages between attention layers as one persistent launch;
- * outputs are the per-kernel path's within float reassociation. A chain
- * barrier that does not resolve makes the call that waited for it fail. */
-bool sg_gpu_chain_active(const sg_gpu *g);
-/* Measurement hook for the chain (no reference counterpart): with
- * SURGE_CHAIN_STAMPS=1 at sg_gpu_state_new every chain launch writes, per
- * stage and workgroup, the device wall clock (hipDeviceAttributeWallClockRate
- * kHz) when the stage's inputs are ready, when its x is staged and when its
- * stores are complete; this copies the last token's [n_stages][n_blocks][3]
- * stamps out (cap values), with each stage's kind (low byte: 1 GEMV, 2
- * DeltaNet step, 3 embedding; GEMVs add prologue << 8, epilogue << 12 and
- * columns / 1024 << 16). */
-sg_err sg_gpu_chain_stamps(sg_gpu *g, uint64_t *out, uint64_t cap, uint32_t *n_stages, uint32_t *n_blocks,
-                           uint32_t *kinds);
 /* Decode at depth without a prefill (no reference counterpart; for
  * benchmarks of the KV read path at long context): fills every attention
  * layer's K/V cache rows [0, n_tokens) with seeded f16 values in [-2, 2], the
@@ -392,8 +375,8 @@ sg_err sg_gpu_state_fill_synthetic(sg_gpu *g, uint32_t n_tokens, uint32_t seed);
 void *sg_gpu_stream(const sg_gpu *g);
 sg_err sg_gpu_enqueue_gemv(sg_gpu *g, uint32_t layer, uint32_t which);
 /* The same with the GEMV's measurement overrides: tune_r rows per wave of
- * the row-group kernel (1, 2 or 4; 3/5/6 the long-row kernel with 4/6/8
- * rows per step) and tune_blocks its workgroup count (0: the launch policy). */
+ * the row-group kernel (1, 2 or 4) and tune_blocks its workgroup count (0:
+ * the launch policy). */
 sg_err sg_gpu_enqueue_gemv_tuned(sg_gpu *g, uint32_t layer, uint32_t which, uint32_t tune_r, uint32_t tune_blocks);
 
 /* Timing hooks for the per-kernel micro configs (no reference counterpart).

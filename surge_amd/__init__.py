@@ -133,14 +133,11 @@ _SIGS = {
     "sg_gpu_decode_greedy": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32,
                                      C.c_uint32, C.POINTER(C.c_int32)]),
     "sg_gpu_state_fill_synthetic": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32]),
-    "sg_gpu_chain_active": (C.c_bool, [C.c_void_p]),
     "sg_gpu_time_read": (SgErr, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.POINTER(C.c_double)]),
     "sg_gpu_time_empty": (SgErr, [C.c_void_p, C.c_uint32, C.c_int, C.POINTER(C.c_double)]),
     "sg_gpu_time_floor": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double),
                                   C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
     "sg_gpu_time_gemm": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double)]),
-    "sg_gpu_chain_stamps": (SgErr, [C.c_void_p, C.POINTER(C.c_uint64), C.c_uint64, C.POINTER(C.c_uint32),
-                                    C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     "sg_gpu_decode_greedy_timed": (SgErr, [C.c_void_p, C.POINTER(SgModel), C.c_int32, C.c_uint32,
                                            C.c_uint32, C.POINTER(C.c_int32), C.POINTER(C.c_double)]),
     "sg_bench_format_md_row": (None, [C.c_void_p, C.c_char_p, C.c_size_t]),
@@ -338,20 +335,6 @@ class Gpu:
 
     def state_reset(self):
         lib().sg_gpu_state_reset(self.handle)
-
-    def chain_active(self) -> bool:
-        return bool(lib().sg_gpu_chain_active(self.handle))
-
-    def chain_stamps(self, max_stages: int = 1024):
-        """(stamps [n_stages][n_blocks][3] uint64 device wall clock, stage kinds) of the
-        last chain token (state made with SURGE_CHAIN_STAMPS=1)."""
-        cap = max_stages * 1024 * 3
-        buf = (C.c_uint64 * cap)()
-        kinds = (C.c_uint32 * max_stages)()
-        ns, nbk = C.c_uint32(), C.c_uint32()
-        check(lib().sg_gpu_chain_stamps(self.handle, buf, cap, C.byref(ns), C.byref(nbk), kinds))
-        a = np.ctypeslib.as_array(buf)[: ns.value * nbk.value * 3].reshape(ns.value, nbk.value, 3).copy()
-        return a, np.array(kinds[: ns.value], dtype=np.uint32)
 
     def split_cap(self) -> int:
         return int(lib().sg_gpu_splitk_gqa_cap(self.handle))

@@ -137,21 +137,6 @@ struct sg_gpu {
     void *tmp;
     uint64_t tmp_bytes;
 
-    /* decode chain (SURGE_CHAIN=1): the token's stage table, the runs of it
-     * one persistent launch covers (an attention layer's partial and combine
-     * run as kernels of their own between runs), the buffers its stages write
-     * once per token and the barrier counters. SURGE_CHAIN=2 (ch_pairs): only
-     * each DeltaNet layer's step and output projection run as a two-stage
-     * launch, the rest as kernels; ch_seg[k] is the k-th DeltaNet layer's. */
-    bool chain, ch_pairs;
-    sgk_cstage *ch_st;
-    uint32_t ch_n, ch_nseg;
-    struct { uint32_t s0, s1; int32_t attn; float *q; } *ch_seg;
-    float *ch_buf;
-    uint32_t *ch_cnt, *ch_err;
-    uint32_t ch_spin;       /* SURGE_CHAIN_SPIN: polls per barrier wait (tests of the give-up path) */
-    uint64_t *ch_stamps;    /* SURGE_CHAIN_STAMPS=1: per stage and workgroup wall-clock stamps */
-    uint32_t ch_tune;       /* SURGE_CHAIN_TUNE: ring / prime depth variant (measurement) */
 };
 
 /* The decode attention partial a state dispatches (fixed per state: the
@@ -736,12 +721,12 @@ sg_err sg_gpu_run_delta_multi(sg_gpu *g, void *S, void *qkv, void *out, void *ga
  * p: [0]=dk [1]=dv [2]=n_v [3]=n_k [4]=ksize [5]=tiled [6]=ssm_a is -exp(A_log)
  * [7]=eps bits. conv_dim = 2 n_k dk + n_v dv. head_v_dim <= 128 (one
  * workgroup per value head, the decode default). */
-/* SURGE_DELTA_SCAN, the prefill DeltaNet scan's form: mfma (default), wy or
- * seq. Any other value is refused, not ignored, so an A/B of scan forms never
+/* SURGE_DELTA_SCAN, the prefill DeltaNet scan's form: mfma (default) or seq.
+ * Any other value is refused, not ignored, so an A/B of scan forms never
  * measures one it did not name. */
 static sg_err delta_scan_env(void) {
     if (sgk_delta_scan_env_ok()) return SG_OK;
-    return errf("gpu: SURGE_DELTA_SCAN='%s' must be mfma, wy or seq (default mfma)", getenv("SURGE_DELTA_SCAN"));
+    return errf("gpu: SURGE_DELTA_SCAN='%s' must be mfma or seq (default mfma)", getenv("SURGE_DELTA_SCAN"));
 }
 
 sg_err sg_gpu_run_gdn_step(sg_gpu *g, void *in, void *w, void *state, void *out, const uint32_t p[8]) {
@@ -816,7 +801,7 @@ sg_err sg_gpu_run_gdn_chunk(sg_gpu *g, void *in, void *w, void *state, void *out
     /* scratch: the chunk's step descriptors, the 4-slot ring, the conv
      * output, the scan readouts and the scan workspace */
     const uint64_t sb = ((uint64_t)n * sizeof(sgk_step) + 255) / 256 * 256, rb = 4 * cd * 4, cb = (uint64_t)n * cd * 4,
-                   yb = (uint64_t)n * vd * 4, wsb = (uint64_t)sgk_delta_wy_ws_floats(nv, n) * 4;
+                   yb = (uint64_t)n * vd * 4, wsb = (uint64_t)sgk_delta_ws_floats(nv, n) * 4;
     void *t;
     if (sg_failed(e = scratch(g, sb + rb + cb + yb + wsb, &t))) return e;
     const uint32_t pos0 = 4 + ((p[5] >> 2) & 3);
@@ -900,7 +885,7 @@ sg_err sg_gpu_run_delta_chunk(sg_gpu *g, void *S, void *qkv, void *out, void *ga
     sgk_gdn d = {0};
     d.S = DEV(S); d.y = DEV(out); d.n_k = nk; d.n_v = nv; d.dk = dk; d.dv = dv; d.conv_dim = cd; d.tiled = p[5] != 0;
     void *ws = NULL;
-    if (sg_failed(e = scratch(g, sgk_delta_wy_ws_floats(nv, n_tok) * 4, &ws))) return e;
+    if (sg_failed(e = scratch(g, sgk_delta_ws_floats(nv, n_tok) * 4, &ws))) return e;
     return finish(g, sgk_delta_scan(&d, DEV(qkv), cd, n_tok, DEV(gates), (float *)ws, g->stream), outs, 2);
 }
 
@@ -1249,12 +1234,6 @@ sg_err sg_gpu_load_model(sg_gpu *g, const sg_model *m) {
 
 static void state_free(sg_gpu *g) {
     if (!g->have_state) return;
-    dfree(g, g->ch_st); dfree(g, g->ch_buf); dfree(g, g->ch_cnt); dfree(g, g->ch_err); dfree(g, g->ch_stamps);
-    g->ch_st = NULL; g->ch_buf = NULL; g->ch_cnt = g->ch_err = NULL; g->ch_stamps = NULL;
-    free(g->ch_seg);
-    g->ch_seg = NULL;
-    g->ch_n = g->ch_nseg = 0;
-    g->chain = g->ch_pairs = false;
     if (g->g_fwd) hipGraphExecDestroy(g->g_fwd);
     if (g->g_greedy) hipGraphExecDestroy(g->g_greedy);
     g->g_fwd = g->g_greedy = NULL;
@@ -1310,36 +1289,13 @@ static hipError_t enqueue_attn(sg_gpu *g, const glayer *L, float *q) {
     return e != hipSuccess ? e : sgk_attn_combine(&A, g->stream);
 }
 
-/* One decode step through the chain: a persistent launch per run of stages,
- * an attention layer's partial and combine between runs. */
-static hipError_t enqueue_chain(sg_gpu *g, bool greedy) {
-    const sg_cfg *c = &g->cfg;
-    hipError_t e;
-    for (uint32_t k = 0; k < g->ch_nseg; k++) {
-        sgk_chain a = {g->ch_st, g->ch_seg[k].s0, g->ch_seg[k].s1, g->ch_cnt, g->ch_err, g->ch_spin,
-                       g->ch_stamps, g->ch_tune};
-        if ((e = sgk_chain_launch(&a, c->head_k_dim, c->head_v_dim, g->stream)) != hipSuccess) return e;
-        const int32_t al = g->ch_seg[k].attn;
-        if (al >= 0 && (e = enqueue_attn(g, &g->ls[al], g->ch_seg[k].q)) != hipSuccess) return e;
-    }
-    if (greedy) {
-        if ((e = sgk_argmax(g->logits, c->vocab, (uint32_t *)&g->d_step->token, g->amax_scratch, g->stream)) != hipSuccess)
-            return e;
-        if ((e = sgk_step_advance(g->d_step, g->hist, g->stream)) != hipSuccess) return e;
-    }
-    return hipSuccess;
-}
-
 /* Enqueues one decode step (everything after the step descriptor is set). */
 static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
-    if (g->chain) return enqueue_chain(g, greedy);
     const sg_cfg *c = &g->cfg;
     hipStream_t s = g->stream;
     hipError_t e;
     const int8_t *eq = g->emb.qs;
     if ((e = sgk_embed(eq, g->emb.d, g->emb.wf, c->hidden, g->d_step, 0, g->x, s)) != hipSuccess) return e;
-    const uint32_t hd = c->head_dim, qs = c->attn_output_gate ? 2 * hd : hd;
-    uint32_t npair = 0;
     for (uint32_t i = 0; i < c->n_layers; i++) {
         glayer *L = &g->ls[i];
         sgk_gemv a = {0};
@@ -1351,17 +1307,7 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
         o.qs = L->out.qs; o.d = L->out.d; o.wf = L->out.wf; o.rows = L->out.rows; o.cols = L->out.cols;
         o.y = g->x; o.epi = SGK_EPI_ADD; o.eps = c->rms_eps;
         if (L->attn) {
-            sgk_attn A = {0};
-            A.q = g->act; A.kc = L->kc; A.vc = L->vc; A.m = g->am; A.s = g->as; A.acc = g->aacc; A.out = g->ctx;
-            A.gate = c->attn_output_gate ? g->act + hd : NULL; A.steps = g->d_step;
-            A.n_heads = c->n_heads; A.n_kv = c->n_kv_heads; A.hd = hd; A.rope_dim = c->rope_dim; A.q_stride = qs;
-            A.max_splits = g->max_splits; A.ntok = 1; A.scale = (float)(1.0 / sqrt((double)hd));
-            A.kv_ps = hd; A.kv_hs = (uint64_t)g->max_ctx * hd;
-            A.fuse_prep = 1; A.qn = L->qn; A.kn = L->kn; A.cs = g->cs_table; A.eps = c->rms_eps;
-            A.split_cap = g->attn_arm == ARM_SINGLE ? 1 : g->split_cap;
-            A.per_head = g->attn_arm == ARM_PER_HEAD;
-            if ((e = sgk_attn_partial(&A, s)) != hipSuccess) return e;
-            if ((e = sgk_attn_combine(&A, s)) != hipSuccess) return e;
+            if ((e = enqueue_attn(g, L, g->act)) != hipSuccess) return e;
             o.x = g->ctx; o.pro = SGK_PRO_NONE;
         } else {
             sgk_gdn d = {0};
@@ -1371,13 +1317,6 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             d.tiled = g->model->v_heads_tiled; d.neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
             d.z = g->act + g->conv_dim; d.norm_w = L->ssm_norm; d.out = g->gbuf; d.eps = c->rms_eps;
             d.ss = g->gss; d.blocks = g->gdn_blocks;
-            if (g->ch_pairs) {                /* the step and the output projection in one launch */
-                sgk_chain a = {g->ch_st, g->ch_seg[npair].s0, g->ch_seg[npair].s1, g->ch_cnt, g->ch_err,
-                               g->ch_spin, g->ch_stamps, g->ch_tune ? g->ch_tune : 1};
-                npair++;
-                if ((e = sgk_chain_launch(&a, c->head_k_dim, c->head_v_dim, s)) != hipSuccess) return e;
-                goto ffn;
-            }
             if ((e = sgk_gdn_step(&d, s)) != hipSuccess) return e;
             if (g->gdn_blocks == 1) {
                 o.x = g->gbuf; o.pro = SGK_PRO_NONE;          /* the step finished RMSNormGated */
@@ -1387,7 +1326,6 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
             }
         }
         if ((e = sgk_gemv_launch(&o, s)) != hipSuccess) return e;
-    ffn:;
         sgk_gemv f = {0};
         f.qs = L->gu.qs; f.d = L->gu.d; f.wf = L->gu.wf; f.rows = L->gu.rows; f.cols = L->gu.cols;
         f.x = g->x; f.nw = L->ln2; f.eps = c->rms_eps; f.y = g->ffg; f.pro = SGK_PRO_RMS; f.epi = SGK_EPI_SWIGLU;
@@ -1411,191 +1349,7 @@ static hipError_t enqueue_step(sg_gpu *g, bool greedy) {
     return hipSuccess;
 }
 
-/* Decode through the chain needs Q8_0 weights whose GEMV widths are
- * multiples of 1024 within the chain's limits, a residual slice per
- * workgroup that fits its LDS, and a one-workgroup-per-head DeltaNet step of
- * a shape the chain kernel is built for. */
-static bool chain_eligible(const sg_gpu *g) {
-    const sg_cfg *c = &g->cfg;
-    if (!g->q8 || !g->emb.qs || !g->lm.qs || g->gdn_blocks != 1) return false;
-    const uint32_t nb = sgk_chain_blocks(), H = c->hidden, rw = (c->head_v_dim + 7) / 8;
-    bool gdn = false;
-    for (uint32_t i = 0; i < c->n_layers; i++) gdn |= !g->ls[i].attn;
-    if (gdn && !((c->head_k_dim == 128 && (rw == 16 || rw == 8)) || (c->head_k_dim == 64 && (rw == 8 || rw == 4))))
-        return false;
-    if (gdn && c->n_v_heads > nb) return false;
-    const uint32_t rms_cols = H, none_cols[3] = {c->ffn_hidden, g->value_dim, g->attn_width};
-    if (rms_cols % 1024 || rms_cols > SGK_CHAIN_MAX_RMS_COLS) return false;
-    for (int k = 0; k < 3; k++)
-        if (none_cols[k] % 1024 || none_cols[k] > SGK_CHAIN_MAX_COLS) return false;
-    const uint32_t lds = SGK_CHAIN_LDS / 4;
-    if (sgk_chain_lds_floats(g->lm.rows, g->lm.cols, nb) > lds) return false;
-    for (uint32_t i = 0; i < c->n_layers; i++) {
-        const glayer *L = &g->ls[i];
-        if (!L->in.qs || !L->out.qs || !L->gu.qs || !L->down.qs) return false;
-        const dmat *M[4] = {&L->in, &L->out, &L->gu, &L->down};
-        for (int k = 0; k < 4; k++)
-            if (M[k]->cols % 1024 || sgk_chain_lds_floats(M[k]->rows, M[k]->cols, nb) > lds) return false;
-    }
-    return true;
-}
-
-/* The token's stage table: embedding, then per layer the input projection,
- * (a DeltaNet step), the output projection, gate/up and down, then lm_head.
- * A run ends after an attention layer's input projection, whose partial and
- * combine run as kernels before the next run starts with its output
- * projection. Every stage writes its own buffer (written once per token). */
-static sg_err chain_build(sg_gpu *g) {
-    const sg_cfg *c = &g->cfg;
-    const uint32_t NL = c->n_layers, H = c->hidden;
-#define R64(n) ((((uint64_t)(n)) + 63) & ~(uint64_t)63)
-    uint64_t tot = R64(H);
-    for (uint32_t i = 0; i < NL; i++)
-        tot += R64(g->ls[i].in.rows) + 2 * R64(H) + R64(c->ffn_hidden) + (g->ls[i].attn ? 0 : R64(g->value_dim));
-    sg_err e = dzalloc(g, tot * 4, (void **)&g->ch_buf);
-    if (sg_failed(e)) return e;
-    const uint32_t nmax = 2 + 5 * NL;
-    sgk_cstage *T = calloc(nmax, sizeof *T);
-    g->ch_seg = calloc(NL + 1, sizeof *g->ch_seg);
-    if (!T || !g->ch_seg) { free(T); return (sg_err){"gpu: out of host memory"}; }
-    float *p = g->ch_buf;
-    uint32_t n = 0, nseg = 0, seg0 = 0;
-    float *x = p; p += R64(H);
-    T[n].kind = SGK_CS_EMBED; T[n].cols = H; T[n].qs = g->emb.qs; T[n].d = g->emb.d; T[n].y = x;
-    T[n].step = g->d_step; n++;
-#define GEMV(M, PRO, EPI, X, NW, RES, Y) do { sgk_cstage *t_ = &T[n++]; t_->kind = SGK_CS_GEMV;    \
-        t_->pro = (PRO); t_->epi = (EPI); t_->rows = (M)->rows; t_->cols = (M)->cols; t_->qs = (M)->qs; \
-        t_->d = (M)->d; t_->x = (X); t_->nw = (NW); t_->res = (RES); t_->y = (Y); t_->eps = c->rms_eps; } while (0)
-    for (uint32_t i = 0; i < NL; i++) {
-        glayer *L = &g->ls[i];
-        float *act = p; p += R64(L->in.rows);
-        GEMV(&L->in, SGK_PRO_RMS, SGK_EPI_STORE, x, L->ln1, NULL, act);
-        const float *mix;
-        if (L->attn) {
-            g->ch_seg[nseg].s0 = seg0; g->ch_seg[nseg].s1 = n; g->ch_seg[nseg].attn = (int32_t)i;
-            g->ch_seg[nseg].q = act; nseg++;
-            seg0 = n;
-            mix = g->ctx;
-        } else {
-            float *go = p; p += R64(g->value_dim);
-            sgk_cstage *t = &T[n++];
-            t->kind = SGK_CS_GDN;
-            sgk_gdn *d = &t->gdn;
-            d->in = act; d->conv_w = L->conv_w; d->ring = L->ring; d->ssm_a = L->ssm_a; d->dt_bias = L->dt_bias;
-            d->S = L->S; d->y = g->ybuf; d->step = g->d_step; d->n_k = c->n_k_heads; d->n_v = c->n_v_heads;
-            d->dk = c->head_k_dim; d->dv = c->head_v_dim; d->conv_dim = g->conv_dim; d->ksize = c->conv_kernel;
-            d->tiled = g->model->v_heads_tiled; d->neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
-            d->z = act + g->conv_dim; d->norm_w = L->ssm_norm; d->out = go; d->eps = c->rms_eps;
-            d->ss = g->gss; d->blocks = 1;
-            mix = go;
-        }
-        float *xa = p; p += R64(H);
-        GEMV(&L->out, SGK_PRO_NONE, SGK_EPI_ADD, mix, NULL, x, xa);
-        float *ff = p; p += R64(c->ffn_hidden);
-        GEMV(&L->gu, SGK_PRO_RMS, SGK_EPI_SWIGLU, xa, L->ln2, NULL, ff);
-        float *xb = p; p += R64(H);
-        GEMV(&L->down, SGK_PRO_NONE, SGK_EPI_ADD, ff, NULL, xa, xb);
-        x = xb;
-    }
-    GEMV(&g->lm, SGK_PRO_RMS, SGK_EPI_STORE, x, g->out_norm, NULL, g->logits);
-#undef GEMV
-#undef R64
-    g->ch_seg[nseg].s0 = seg0; g->ch_seg[nseg].s1 = n; g->ch_seg[nseg].attn = -1; g->ch_seg[nseg].q = NULL; nseg++;
-    g->ch_n = n;
-    g->ch_nseg = nseg;
-    if (!sg_failed(e = dalloc(g, (uint64_t)n * sizeof *T, (void **)&g->ch_st)) &&
-        hipMemcpy(g->ch_st, T, (uint64_t)n * sizeof *T, hipMemcpyHostToDevice) != hipSuccess)
-        e = (sg_err){"gpu: chain stage table upload failed"};
-    free(T);
-    if (!sg_failed(e)) e = dzalloc(g, (uint64_t)n * 8 * 64 * 4, (void **)&g->ch_cnt);
-    if (!sg_failed(e)) e = dzalloc(g, 256, (void **)&g->ch_err);
-    return e;
-}
-
-/* SURGE_CHAIN=2: per DeltaNet layer a two-stage table run — the step (one
- * workgroup per value head, RMSNormGated fused, into gbuf) and the output
- * projection (x += W gbuf, in place: a workgroup reads its residual rows
- * before it writes them) — so the projection's workgroups request their
- * weights while the step runs. The other stages stay kernels. */
-static sg_err chain_build_pairs(sg_gpu *g) {
-    const sg_cfg *c = &g->cfg;
-    uint32_t np = 0;
-    for (uint32_t i = 0; i < c->n_layers; i++) np += !g->ls[i].attn;
-    if (!np) return (sg_err){"gpu: SURGE_CHAIN=2 needs DeltaNet layers"};
-    sgk_cstage *T = calloc(2 * (uint64_t)np, sizeof *T);
-    g->ch_seg = calloc(np, sizeof *g->ch_seg);
-    if (!T || !g->ch_seg) { free(T); return (sg_err){"gpu: out of host memory"}; }
-    uint32_t n = 0, k = 0;
-    for (uint32_t i = 0; i < c->n_layers; i++) {
-        glayer *L = &g->ls[i];
-        if (L->attn) continue;
-        g->ch_seg[k].s0 = n; g->ch_seg[k].s1 = n + 2; g->ch_seg[k].attn = (int32_t)i; g->ch_seg[k].q = NULL; k++;
-        sgk_cstage *t = &T[n++];
-        t->kind = SGK_CS_GDN;
-        sgk_gdn *d = &t->gdn;
-        d->in = g->act; d->conv_w = L->conv_w; d->ring = L->ring; d->ssm_a = L->ssm_a; d->dt_bias = L->dt_bias;
-        d->S = L->S; d->y = g->ybuf; d->step = g->d_step; d->n_k = c->n_k_heads; d->n_v = c->n_v_heads;
-        d->dk = c->head_k_dim; d->dv = c->head_v_dim; d->conv_dim = g->conv_dim; d->ksize = c->conv_kernel;
-        d->tiled = g->model->v_heads_tiled; d->neg_exp = g->model->ssm_a_form == SG_SSM_A_NEG_EXP;
-        d->z = g->act + g->conv_dim; d->norm_w = L->ssm_norm; d->out = g->gbuf; d->eps = c->rms_eps;
-        d->ss = g->gss; d->blocks = 1;
-        t = &T[n++];
-        t->kind = SGK_CS_GEMV; t->pro = SGK_PRO_NONE; t->epi = SGK_EPI_ADD; t->rows = L->out.rows;
-        t->cols = L->out.cols; t->qs = L->out.qs; t->d = L->out.d; t->x = g->gbuf; t->nw = NULL; t->res = g->x;
-        t->y = g->x; t->eps = c->rms_eps;
-    }
-    g->ch_n = n;
-    g->ch_nseg = np;
-    sg_err e = SG_OK;
-    if (!sg_failed(e = dalloc(g, (uint64_t)n * sizeof *T, (void **)&g->ch_st)) &&
-        hipMemcpy(g->ch_st, T, (uint64_t)n * sizeof *T, hipMemcpyHostToDevice) != hipSuccess)
-        e = (sg_err){"gpu: chain stage table upload failed"};
-    free(T);
-    if (!sg_failed(e)) e = dzalloc(g, (uint64_t)n * 8 * 64 * 4, (void **)&g->ch_cnt);
-    if (!sg_failed(e)) e = dzalloc(g, 256, (void **)&g->ch_err);
-    return e;
-}
-
-/* Whether a chain barrier gave up since the last check (the decode outputs
- * of those steps are invalid); clears the flag and the counters. */
-static sg_err chain_status(sg_gpu *g) {
-    if (!g->chain && !g->ch_pairs) return SG_OK;
-    uint32_t v = 0;
-    HIPCHK(hipMemcpy(&v, g->ch_err, 4, hipMemcpyDeviceToHost), "chain status");
-    if (!v) return SG_OK;
-    HIPCHK(hipMemsetAsync(g->ch_cnt, 0, (uint64_t)g->ch_n * 8 * 64 * 4, g->stream), "chain reset");
-    HIPCHK(hipMemsetAsync(g->ch_err, 0, 4, g->stream), "chain reset");
-    HIPCHK(hipStreamSynchronize(g->stream), "chain reset");
-    return (sg_err){"gpu: a decode chain barrier did not resolve; those decode steps' outputs are invalid"};
-}
-
 static bool graphed(const sg_gpu *g) { return g->use_graph; }
-
-bool sg_gpu_chain_active(const sg_gpu *g) { return g && g->have_state && (g->chain || g->ch_pairs); }
-
-sg_err sg_gpu_chain_stamps(sg_gpu *g, uint64_t *out, uint64_t cap, uint32_t *n_stages, uint32_t *n_blocks,
-                           uint32_t *kinds) {
-    if (!g || !g->have_state || !(g->chain || g->ch_pairs) || !g->ch_stamps)
-        return (sg_err){"gpu: chain stamps need a chain state made with SURGE_CHAIN_STAMPS=1"};
-    const uint32_t nb = sgk_chain_blocks();
-    const uint64_t n = (uint64_t)g->ch_n * nb * 3;
-    if (!out || cap < n) return errf("gpu: chain stamps need room for %llu values", (unsigned long long)n);
-    HIPCHK(hipStreamSynchronize(g->stream), "chain stamps");
-    HIPCHK(hipMemcpy(out, g->ch_stamps, n * 8, hipMemcpyDeviceToHost), "chain stamps");
-    if (n_stages) *n_stages = g->ch_n;
-    if (n_blocks) *n_blocks = nb;
-    if (kinds) {
-        sgk_cstage *T = malloc((uint64_t)g->ch_n * sizeof *T);
-        if (!T) return (sg_err){"gpu: out of host memory"};
-        hipError_t he = hipMemcpy(T, g->ch_st, (uint64_t)g->ch_n * sizeof *T, hipMemcpyDeviceToHost);
-        for (uint32_t i = 0; i < g->ch_n && he == hipSuccess; i++)
-            kinds[i] = T[i].kind | (T[i].kind == SGK_CS_GEMV ? (T[i].pro << 8) | (T[i].epi << 12) : 0) |
-                       (T[i].kind == SGK_CS_GEMV ? (T[i].cols >> 10) << 16 : 0);
-        free(T);
-        if (he != hipSuccess) return (sg_err){"gpu: chain stage table download failed"};
-    }
-    return SG_OK;
-}
 
 static sg_err capture(sg_gpu *g, bool greedy, hipGraphExec_t *out) {
     hipGraph_t graph = NULL;
@@ -1670,14 +1424,9 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     else g->attn_arm = ARM_PER_HEAD;
     /* The DeltaNet step runs SGK_GDN_BLOCKS row-block workgroups per value
      * head, the out projection's gated prologue finishing RMSNormGated
-     * (measured faster than one workgroup per head finishing it itself);
-     * a decode chain (SURGE_CHAIN=1|2) takes one workgroup per head.
+     * (measured faster than one workgroup per head finishing it itself).
      * SURGE_GDN_BLOCKS=1 (head_v_dim <= 128) | 4 overrides. */
     g->gdn_blocks = SGK_GDN_BLOCKS;
-    {
-        const char *cr = getenv("SURGE_CHAIN");
-        if (c->head_v_dim <= 128 && cr && (!strcmp(cr, "1") || !strcmp(cr, "2"))) g->gdn_blocks = 1;
-    }
     {
         const char *gb = getenv("SURGE_GDN_BLOCKS");
         if (gb && gb[0]) {
@@ -1732,32 +1481,6 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
     if (!sg_failed(e) && hipEventCreateWithFlags(&g->step_ev, hipEventDisableTiming) != hipSuccess)
         e = (sg_err){"gpu: hipEventCreate failed"};
     g->have_state = true;
-    /* SURGE_CHAIN=1: decode through the chain (one persistent launch per run
-     * of stages) when the model allows it; 0 (default): one kernel per stage. */
-    {
-        const char *ce = getenv("SURGE_CHAIN");
-        if (ce && ce[0] && strcmp(ce, "0") != 0 && strcmp(ce, "1") != 0 && strcmp(ce, "2") != 0)
-            fprintf(stderr, "gpu: SURGE_CHAIN='%s' not recognized (want 0, 1 or 2); using 0\n", ce);
-        if (!sg_failed(e) && ce && strcmp(ce, "1") == 0 && chain_eligible(g)) {
-            e = chain_build(g);
-            g->chain = !sg_failed(e);
-        }
-        if (!sg_failed(e) && ce && strcmp(ce, "2") == 0 && chain_eligible(g)) {
-            bool gdn = false;
-            for (uint32_t i = 0; i < c->n_layers; i++) gdn |= !g->ls[i].attn;
-            if (gdn) {
-                e = chain_build_pairs(g);
-                g->ch_pairs = !sg_failed(e);
-            }
-        }
-        const char *sp = getenv("SURGE_CHAIN_SPIN");
-        g->ch_spin = sp && *sp ? (uint32_t)strtoul(sp, NULL, 10) : 0;
-        const char *tu = getenv("SURGE_CHAIN_TUNE");
-        g->ch_tune = tu && *tu ? (uint32_t)strtoul(tu, NULL, 10) : 0;
-        const char *ss = getenv("SURGE_CHAIN_STAMPS");
-        if (!sg_failed(e) && (g->chain || g->ch_pairs) && ss && !strcmp(ss, "1"))
-            e = dzalloc(g, (uint64_t)g->ch_n * sgk_chain_blocks() * 3 * 8, (void **)&g->ch_stamps);
-    }
     if (!sg_failed(e) && graphed(g)) {
         e = capture(g, false, &g->g_fwd);
         if (!sg_failed(e)) e = capture(g, true, &g->g_greedy);
@@ -1775,10 +1498,6 @@ void sg_gpu_state_reset(sg_gpu *g) {
         glayer *L = &g->ls[i];
         if (L->ring) sgk_fill_f32(L->ring, 0.0f, (uint64_t)4 * g->conv_dim, g->stream);
         if (L->S) sgk_fill_f32(L->S, 0.0f, (uint64_t)c->n_v_heads * c->head_v_dim * c->head_k_dim, g->stream);
-    }
-    if (g->chain || g->ch_pairs) {
-        hipMemsetAsync(g->ch_cnt, 0, (uint64_t)g->ch_n * 8 * 64 * 4, g->stream);
-        hipMemsetAsync(g->ch_err, 0, 4, g->stream);
     }
     hipStreamSynchronize(g->stream);
     g->used = 0;
@@ -1843,7 +1562,6 @@ sg_err sg_gpu_forward(sg_gpu *g, const sg_model *m, int32_t token, uint32_t pos,
     if (sg_failed(e = launch_step(g, token, pos, false))) return e;
     HIPCHK(hipMemcpyAsync(g->h_logits, g->logits, (uint64_t)g->cfg.vocab * 4, hipMemcpyDeviceToHost, g->stream), "logits download");
     HIPCHK(hipStreamSynchronize(g->stream), "decode step");
-    if (sg_failed(e = chain_status(g))) return e;
     g->used = pos + 1;
     if (logits) *logits = g->h_logits;
     return SG_OK;
@@ -1860,7 +1578,7 @@ sg_err sg_gpu_forward_nosync(sg_gpu *g, const sg_model *m, int32_t token, uint32
 sg_err sg_gpu_sync(sg_gpu *g) {
     if (!g) return (sg_err){"gpu: NULL gpu"};
     HIPCHK(hipStreamSynchronize(g->stream), "stream synchronize");
-    return g->have_state ? chain_status(g) : SG_OK;
+    return SG_OK;
 }
 
 sg_err sg_gpu_argmax(sg_gpu *g, uint32_t *token_out) {
@@ -1893,7 +1611,6 @@ sg_err sg_gpu_decode_greedy(sg_gpu *g, const sg_model *m, int32_t token, uint32_
     }
     HIPCHK(hipMemcpyAsync(g->h_tok, g->hist + pos + 1, (uint64_t)n_steps * 4, hipMemcpyDeviceToHost, g->stream), "tokens download");
     HIPCHK(hipStreamSynchronize(g->stream), "greedy decode");
-    if (sg_failed(e = chain_status(g))) return e;
     if (out_tokens) memcpy(out_tokens, g->h_tok, (uint64_t)n_steps * 4);
     g->used = pos + n_steps;
     return SG_OK;
@@ -1932,7 +1649,6 @@ sg_err sg_gpu_decode_greedy_timed(sg_gpu *g, const sg_model *m, int32_t token, u
     free(ev);
     if (sg_failed(e)) return e;
     if (he != hipSuccess) return errf("gpu: timed greedy decode: %s", hipGetErrorString(he));
-    if (sg_failed(e = chain_status(g))) return e;
     count_step(g, n_steps);
     if (out_tokens) memcpy(out_tokens, g->h_tok, (uint64_t)n_steps * 4);
     g->used = pos + n_steps;
@@ -1992,7 +1708,7 @@ static sg_err prefill_alloc(sg_gpu *g, uint32_t chunk) {
     uint64_t sizes[] = { n * sizeof(sgk_step), n * c->hidden * 4, n * c->hidden * 4, n * in_rows * 4,
                          n * g->conv_dim * 4 + 4, n * g->value_dim * 4 + 4, n * g->value_dim * 4 + 4,
                          n * g->attn_width * 4 + 4, n * c->ffn_hidden * 4, ah * 4, ah * 4, ah * c->head_dim * 4,
-                         n * kmax * 4, 4 * n * c->hidden * 4, sgk_delta_wy_ws_floats(c->n_v_heads, chunk) * 4 + 4,
+                         n * kmax * 4, 4 * n * c->hidden * 4, sgk_delta_ws_floats(c->n_v_heads, chunk) * 4 + 4,
                          n * kmax * 4 };
     sg_err e = SG_OK;
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs && !sg_failed(e); i++) e = dzalloc(g, sizes[i], bufs[i]);
@@ -2288,7 +2004,7 @@ sg_err sg_gpu_time_read(sg_gpu *g, uint64_t bytes, uint64_t rotate_bytes, uint32
     float *out;
     sg_err e;
     if (sg_failed(e = dzalloc(g, n * unit, (void **)&base))) return e;
-    const uint32_t blocks = 4 * (uint32_t)sgk_chain_blocks();
+    const uint32_t blocks = 4 * (uint32_t)sgk_device_cus();
     if (sg_failed(e = dalloc(g, (uint64_t)blocks * 4, (void **)&out))) { dfree(g, base); return e; }
     hipStream_t s = g->stream;
     hipEvent_t a = NULL, b = NULL;
@@ -2391,7 +2107,7 @@ sg_err sg_gpu_time_floor(sg_gpu *g, uint32_t ctx, uint32_t mode, uint32_t reps, 
     for (uint32_t i = 0; i < n; i++) tot += (b[i] + 255) & ~(uint64_t)255;
     char *base = NULL;
     float *out = NULL;
-    const uint32_t maxb = 4 * (uint32_t)sgk_chain_blocks();
+    const uint32_t maxb = 4 * (uint32_t)sgk_device_cus();
     sg_err e = SG_OK;
     if (mode != 0) e = dalloc(g, tot, (void **)&base);
     if (!sg_failed(e)) e = dalloc(g, (uint64_t)maxb * 4, (void **)&out);

@@ -18,11 +18,10 @@
 extern "C" {
 #endif
 
-/* Pointers that device code reads out of descriptors in memory (the chain's
- * stage table) are typed as global-memory pointers in the device compile
- * pass, so its loads and stores are global ones rather than flat ones (a
- * flat access also counts against the LDS wait counter, which would make
- * every LDS read wait for the weight stream). Same bits and layout as the
+/* The DeltaNet descriptor's pointers are typed as global-memory pointers in
+ * the device compile pass, so their loads and stores are global ones rather
+ * than flat ones (a flat access also counts against the LDS wait counter,
+ * which would make LDS reads wait for memory). Same bits and layout as the
  * host's plain pointers. */
 #if defined(__HIP_DEVICE_COMPILE__)
 #define SGK_G __attribute__((address_space(1)))
@@ -218,15 +217,15 @@ hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t in_stride, 
 /* The delta-rule scan alone: qkv rows [ntok][a->conv_dim] hold normalised
  * q | k | v; gates [ntok][2*n_v] = beta | decay (or NULL: computed from the
  * b/a columns of a->in, rows in_stride apart, as in sgk_gdn_chunk). With a
- * workspace ws of sgk_delta_wy_ws_floats(n_v, ntok) floats and dk 64 or 128
- * it runs a chunked form: by default the 16-token one on the matrix cores
- * (dv a multiple of 16), with SURGE_DELTA_SCAN=wy the 64-token one; with
- * SURGE_DELTA_SCAN=seq, no workspace or other shapes the sequential scan. */
+ * workspace ws of sgk_delta_ws_floats(n_v, ntok) floats, dk 64 or 128 and
+ * dv a multiple of 16 it runs the 16-token chunked form on the matrix cores;
+ * with SURGE_DELTA_SCAN=seq, no workspace or other shapes the sequential
+ * scan. */
 hipError_t sgk_delta_scan(const sgk_gdn *a, const float *qkv, uint32_t in_stride, uint32_t ntok,
                           const float *gates, float *ws, hipStream_t s);
-uint64_t sgk_delta_wy_ws_floats(uint32_t n_v, uint32_t ntok);
+uint64_t sgk_delta_ws_floats(uint32_t n_v, uint32_t ntok);
 /* Whether SURGE_DELTA_SCAN holds a form the scan knows (unset, empty, mfma,
- * wy, seq); the host refuses to run with any other value. */
+ * seq); the host refuses to run with any other value. */
 int sgk_delta_scan_env_ok(void);
 /* Conv over a chunk with an oldest-first state [ksize-1][ch] in/out, no
  * activation (the reference's k_conv1d_chunk contract). */
@@ -307,56 +306,12 @@ hipError_t sgk_gemm_q8(const float *X, const int8_t *qs, const uint16_t *dt, flo
                        uint32_t N, uint32_t M, uint32_t K, uint16_t *xs, float *part,
                        uint64_t part_cap, hipStream_t s);
 
-/* Decode chain: one persistent launch (one workgroup per CU, all resident)
- * runs stages [s0, s1) of a token's stage table in order, with a device-wide
- * barrier between stages instead of a kernel boundary; every GEMV's first
- * weight rows are requested before the barrier that precedes it. Stage
- * outputs are published with device-scope (write-through) stores into
- * buffers written once per token. The arrival counters `cnt` are zeroed with
- * the state and only grow: a workgroup learns from its own arrival which
- * launch of the stage it is in, so launches replay from a captured graph. A
- * barrier that does not resolve within a bounded number of polls sets *err
- * and the launch runs to its end. */
-enum { SGK_CS_GEMV = 1, SGK_CS_GDN = 2, SGK_CS_EMBED = 3 };
-#define SGK_CHAIN_LDS (96u * 1024u)          /* dynamic LDS: one workgroup per CU */
-#define SGK_CHAIN_MAX_COLS 18432u            /* GEMV columns (a multiple of 1024) */
-#define SGK_CHAIN_MAX_RMS_COLS 8192u         /* ... behind the RMSNorm prologue */
-/* LDS floats a GEMV stage of the chain needs with nb workgroups: the staged
- * x (1040 floats per 1024 columns), then per row group of a workgroup CW x 2
- * partial slots and 2 residual rows. At most SGK_CHAIN_LDS / 4. */
-static inline uint32_t sgk_chain_lds_floats(uint32_t rows, uint32_t cols, uint32_t nb) {
-    const uint32_t groups = (rows + 1) / 2, ng = (groups + nb - 1) / nb;
-    return ((cols / 16 + 63) / 64) * 1040 + ng * 18;
-}
-typedef struct {
-    uint32_t kind;              /* SGK_CS_* */
-    uint32_t pro, epi;          /* GEMV: SGK_PRO_NONE | RMS, SGK_EPI_STORE | ADD | SWIGLU */
-    uint32_t rows, cols;        /* GEMV; EMBED: cols = hidden */
-    const int8_t SGK_G *qs;     /* GEMV / EMBED (the table) */
-    const uint16_t SGK_G *d;
-    /* input, RMS weight, EPI_ADD residual (y = res + W x) */
-    const float SGK_G *x;
-    const float SGK_G *nw;
-    const float SGK_G *res;
-    float SGK_G *y;
-    float eps;
-    const sgk_step SGK_G *step; /* EMBED: the token */
-    sgk_gdn gdn;                /* GDN: one workgroup per value head (blocks == 1) */
-} sgk_cstage;
-typedef struct {
-    const sgk_cstage *st;       /* device stage table */
-    uint32_t s0, s1;
-    uint32_t *cnt;              /* [n_stages][8 XCDs][64] arrival counters */
-    uint32_t *err;
-    uint32_t spin;              /* polls a wait makes before giving up (0: the default bound) */
-    uint64_t *stamps;           /* NULL, or [n_stages][workgroups][3] device wall-clock stamps per
-                                 * stage: inputs ready (barrier passed), x staged, stores complete */
-    uint32_t tune;              /* 0: default ring and prime depths; 1..6 measured alternatives */
-} sgk_chain;
-/* DeltaNet shapes the chain's step takes: (dk, ceil(dv / 8)) in
- * {(128, 16), (128, 8), (64, 8), (64, 4)}. */
-hipError_t sgk_chain_launch(const sgk_chain *a, uint32_t dk, uint32_t dv, hipStream_t s);
-uint32_t sgk_chain_blocks(void);
+/* Widest rows the balanced GEMV (k_gemv_bal: one workgroup per CU, x staged
+ * once) takes: columns a multiple of 1024, up to these. */
+#define SGK_BAL_MAX_COLS 18432u
+#define SGK_BAL_MAX_RMS_COLS 8192u         /* ... behind the RMSNorm prologue */
+/* The device's compute units (the grid of one workgroup per CU). */
+uint32_t sgk_device_cus(void);
 
 /* Measurement kernels: a streaming read of `bytes` (a multiple of 16) by
  * `blocks` workgroups (one float per workgroup written to out), and an empty

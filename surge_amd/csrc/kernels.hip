@@ -439,131 +439,6 @@ __global__ void __launch_bounds__(TPB) k_gemv_f32(sgk_gemv a) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// Q8_0 GEMV for long rows (more than 8192 columns: the 27B down-projection,
-// 17408). One 1024-thread workgroup per CU stages x once in LDS (68 KB for
-// 17408 columns). Rows are dealt as a chip-wide contiguous front: in round t,
-// wave w of workgroup b takes row (t*16 + w)*G + b, so at any moment the chip
-// reads neighbouring rows. The rows left after the full rounds (fewer than
-// 16*G) go to workgroup b as base + i*G + b and each is split by chunk range
-// over S = 16/n of its waves; the S partial sums meet in LDS and are added in
-// part order, so results do not depend on timing. Each wave requests its next
-// batch of chunks before multiplying the current one.
-// ---------------------------------------------------------------------------
-
-#define LTPB 1024
-#define LW (LTPB / 64)
-// float4s of x per thread in flight when the long kernel stages rows of up to 20480 columns.
-constexpr int LXK = 5;
-
-struct long_task { uint32_t row, c0, c1, slot; };
-struct long_plan { uint32_t nch, F, nb, S, nbr, G, b, base; };
-
-// The k-th batch of wave w; false past the end. slot: LW*LW+ for a whole row,
-// else the LDS partial slot (i*LW + part).
-template <int LU>
-__device__ __forceinline__ bool long_task_at(const long_plan &p, uint32_t w, uint32_t k, long_task &t) {
-    const uint32_t nfull = p.F * p.nbr;
-    if (k < nfull) {
-        const uint32_t i = k / p.nbr, bb = k - i * p.nbr;
-        t.row = (i * LW + w) * p.G + p.b;
-        t.c0 = bb * 64 * LU;
-        t.c1 = min(t.c0 + 64 * LU, p.nch);
-        t.slot = 0xffffffffu;
-        return true;
-    }
-    k -= nfull;
-    if (p.nb == 0 || w >= p.nb * p.S) return false;
-    const uint32_t i = w / p.S, part = w - i * p.S;
-    const uint32_t pc0 = (uint32_t)((uint64_t)part * p.nch / p.S);
-    const uint32_t pc1 = (uint32_t)((uint64_t)(part + 1) * p.nch / p.S);
-    const uint32_t c0 = pc0 + k * 64 * LU;
-    if (c0 >= pc1) return false;
-    t.row = p.base + i * p.G + p.b;
-    t.c0 = c0;
-    t.c1 = min(c0 + 64 * LU, pc1);
-    t.slot = i * LW + part;
-    return true;
-}
-
-template <int LU>
-struct long_batch { uint4 q[LU]; uint16_t d[LU]; };
-
-template <int LU>
-__device__ __forceinline__ void long_load(long_batch<LU> &bt, const sgk_gemv &a, const long_task &t, uint32_t lane) {
-    const uint4 *q = (const uint4 *)(a.qs + (size_t)t.row * a.cols);
-    const uint16_t *dr = a.d + (size_t)t.row * (a.cols >> 5);
-#pragma unroll
-    for (int u = 0; u < LU; u++) {
-        const uint32_t c = t.c0 + lane + 64 * u;
-        if (c < t.c1) { bt.q[u] = ldnt(q + c); bt.d[u] = dr[c >> 1]; }
-    }
-}
-
-template <int LU>
-__device__ __forceinline__ float long_fma(const long_batch<LU> &bt, const float *xs, const long_task &t, uint32_t lane,
-                                          float acc) {
-#pragma unroll
-    for (int u = 0; u < LU; u++) {
-        const uint32_t c = t.c0 + lane + 64 * u;
-        if (c < t.c1) {
-            const float4 *xa = (const float4 *)xs + (c >> 6) * XS_CH_BLK + (c & 63);     // xs4_at<true>
-            acc = fmaf(h2f(bt.d[u]), dot16(bt.q[u], xa[0], xa[65], xa[130], xa[195]), acc);
-        }
-    }
-    return acc;
-}
-
-template <int EPI, int LU>
-__global__ void __launch_bounds__(LTPB) k_gemv_q8_long(sgk_gemv a) {
-    extern __shared__ float lds[];
-    float *xs = lds, *part = lds + xs_ch_floats(a.cols);   // part[LW * LW]
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    long_plan p;
-    p.G = gridDim.x;
-    p.b = blockIdx.x;
-    p.nch = a.cols >> 4;
-    p.F = a.rows / (LW * p.G);
-    p.base = p.F * LW * p.G;
-    const uint32_t urem = a.rows - p.base;
-    p.nb = urem > p.b ? (urem - p.b + p.G - 1) / p.G : 0;
-    p.S = p.nb ? LW / p.nb : 1;
-    p.nbr = (p.nch + 64 * LU - 1) / (64 * LU);
-    long_task t;
-    bool have = long_task_at<LU>(p, w, 0, t);
-    xstage<SGK_PRO_NONE, LTPB, LXK> st;                 // x first, then the first weights
-    stage_issue<SGK_PRO_NONE, LTPB, LXK>(a, st);
-    long_batch<LU> cur;
-    if (have) long_load<LU>(cur, a, t, lane);
-    stage_finish<SGK_PRO_NONE, LTPB, LXK, true>(a, st, xs);
-    float acc = 0.0f;
-    for (uint32_t k = 0; have; k++) {
-        long_task tn;
-        const bool hn = long_task_at<LU>(p, w, k + 1, tn);
-        long_batch<LU> nxt;
-        if (hn) long_load<LU>(nxt, a, tn, lane);
-        acc = long_fma<LU>(cur, xs, t, lane, acc);
-        if (!hn || tn.row != t.row) {
-            acc = wave_sum(acc);
-            if (t.slot == 0xffffffffu) {
-                if (lane == 0) gemv_store<EPI>(a, t.row, acc);
-            } else if (lane == 0) {
-                part[t.slot] = acc;
-            }
-            acc = 0.0f;
-        }
-        if (!hn) break;
-        t = tn;
-        cur = nxt;
-    }
-    if (p.nb == 0) return;
-    __syncthreads();
-    if (threadIdx.x < p.nb) {
-        float s = 0.0f;
-        for (uint32_t q = 0; q < p.S; q++) s += part[threadIdx.x * LW + q];
-        gemv_store<EPI>(a, p.base + threadIdx.x * p.G + p.b, s);
-    }
-}
 
 // Workgroups of `kern` (tpb threads, lds bytes of dynamic LDS) that fit on one
 // CU at once: the wave slots its VGPR count leaves per SIMD, and the LDS.
@@ -718,8 +593,8 @@ static hipError_t launch_q8(const sgk_gemv &a, size_t lds, hipStream_t s) {
 #define BT 768
 #define BW (BT / 64)
 #define BP 4
-constexpr int BXK_NONE = (SGK_CHAIN_MAX_COLS + 4 * BT - 1) / (4 * BT);
-constexpr int BXK_RMS = (SGK_CHAIN_MAX_RMS_COLS + 4 * BT - 1) / (4 * BT);
+constexpr int BXK_NONE = (SGK_BAL_MAX_COLS + 4 * BT - 1) / (4 * BT);
+constexpr int BXK_RMS = (SGK_BAL_MAX_RMS_COLS + 4 * BT - 1) / (4 * BT);
 
 __host__ __device__ __forceinline__ uint32_t bal_lds_floats(uint32_t rows, uint32_t cols, uint32_t nb) {
     const uint32_t G = (rows + 1) / 2, ng = (G + nb - 1) / nb;
@@ -815,10 +690,10 @@ __global__ void __launch_bounds__(BT) k_gemv_bal(sgk_gemv a) {
 }
 
 // Which kernel takes a Q8_0 GEMV of `cols` columns (multiples of 1024 only):
-// 0 k_gemv_q8 / k_gemv_q8_long, 1 k_gemv_bal contiguous, 2 k_gemv_bal
+// 0 k_gemv_q8, 1 k_gemv_bal contiguous, 2 k_gemv_bal
 // interleaved. Measured per 27B shape (one MI355X, back-to-back launches over
 // the layers): the interleaved balanced kernel streams the 17408-column down
-// projection in 18.5 us against 20.2 for k_gemv_q8_long; at 5120 and 6144
+// projection in 18.5 us against 20.2 for the row-front kernel it replaced; at 5120 and 6144
 // columns k_gemv_q8 is as fast or faster, and contiguous ranges are slower
 // than interleaved ones everywhere. SURGE_GEMV=q8|bal|bali forces one.
 static int gemv_bal_on(uint32_t cols) {
@@ -855,22 +730,11 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         return hipGetLastError();
     }
     if (PRO != SGK_PRO_GATED && gemv_bal_on(a->cols) && !a->tune_r && !a->tune_blocks && a->cols % 1024 == 0 &&
-        a->cols <= (PRO == SGK_PRO_RMS ? SGK_CHAIN_MAX_RMS_COLS : SGK_CHAIN_MAX_COLS) &&
+        a->cols <= (PRO == SGK_PRO_RMS ? SGK_BAL_MAX_RMS_COLS : SGK_BAL_MAX_COLS) &&
         bal_lds_floats(a->rows, a->cols, (uint32_t)device_cus()) * 4 <= 160 * 1024)
         return launch_bal<PRO == SGK_PRO_RMS ? SGK_PRO_RMS : SGK_PRO_NONE, EPI>(*a, s);
-    if (PRO == SGK_PRO_NONE && EPI != SGK_EPI_SWIGLU && a->cols > 8192 && a->tune_r != 7 && a->tune_r != 8) {
-        const size_t lds = ((size_t)xs_ch_floats(a->cols) + LW * LW) * 4;
-        constexpr int LE = EPI == SGK_EPI_ADD ? SGK_EPI_ADD : SGK_EPI_STORE;
-        auto kern = a->tune_r == 3 ? k_gemv_q8_long<LE, 4> : a->tune_r == 5 ? k_gemv_q8_long<LE, 6>
-                  : a->tune_r == 6 ? k_gemv_q8_long<LE, 8> : k_gemv_q8_long<LE, 3>;
-        hipError_t e = allow_lds((const void *)kern, lds);
-        if (e != hipSuccess) return e;
-        const uint32_t blocks = a->tune_blocks ? a->tune_blocks : (uint32_t)device_cus();
-        hipLaunchKernelGGL(kern, dim3(blocks), dim3(LTPB), lds, s, *a);
-        return hipGetLastError();
-    }
     const size_t lds = GEMV_CH(PRO) ? (size_t)xs_ch_floats(a->cols) * 4 : (size_t)a->cols * 4;
-    const int R = EPI == SGK_EPI_SWIGLU ? 2 : (a->tune_r == 1 ? 1 : (a->tune_r == 4 || a->tune_r == 8) ? 4 : 2);
+    const int R = EPI == SGK_EPI_SWIGLU ? 2 : (a->tune_r == 1 ? 1 : a->tune_r == 4 ? 4 : 2);
     if (R == 4) return launch_q8<4, PRO, EPI>(*a, lds, s);
     if (R == 1) return launch_q8<1, PRO, (EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI)>(*a, lds, s);
     return launch_q8<2, PRO, EPI>(*a, lds, s);
@@ -2487,16 +2351,7 @@ __device__ __forceinline__ uint32_t rows_lane(uint32_t r) {   // a lane holding 
 // every block's readouts, so it is left to the output projection's gated
 // prologue: each block writes silu(z) * (y * w) of its rows and the sum of its
 // rows' squared readouts, with no synchronisation between blocks.
-// Stores that other workgroups of the same launch read after a chain barrier
-// go straight to memory (device-scope relaxed atomic stores: sc1, written
-// through the XCD's L2), so no cache-wide flush is needed to publish them.
-template <bool CO>
-__device__ __forceinline__ void st_out(float *p, float v) {
-    if (CO) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *p = v;
-}
-
-template <int DK, int RW, int NB, int GDN_TPB, bool CO = false>
+template <int DK, int RW, int NB, int GDN_TPB>
 __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint32_t jb) {
     constexpr int GDN_NB = NB;
     constexpr int EPL = DK >= 64 ? DK / 64 : 1;
@@ -2654,7 +2509,7 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
         const float r = 1.0f / sqrtf(tot / (float)dv + a.eps);
         if (t < dv) {
             const float yv = ysh[t];
-            st_out<CO>(a.out + (size_t)h * dv + t, silu(zj) * ((yv * r) * nwt));
+            a.out[(size_t)h * dv + t] = silu(zj) * ((yv * r) * nwt);
         }
         return;
     }
@@ -3066,270 +2921,6 @@ __global__ void k_embed_rows(const int8_t *qs, const uint16_t *d, const float *w
 }
 
 // ---------------------------------------------------------------------------
-// Chunked delta rule (the WY / UT form of the sequential scan above) over
-// sub-chunks of WY_C tokens. For one value head, with S the state at the
-// sub-chunk's start (row j: value dim j), gate products in log space
-// (LG_t = sum of log decay over the sub-chunk's tokens up to t, in double),
-//   T_ts  = beta_t exp(LG_t - LG_s) k_t.k_s   (s < t),   W = (I + T)^-1
-//   Mq_ts = exp(LG_t - LG_s) q_t.k_s          (s <= t)
-//   Delta = W [beta (V - exp(LG) K S^T)]      (rows t: the step's deltas)
-//   Y     = exp(LG) Q S^T + Mq Delta          (the readouts)
-//   S'    = exp(LG_n) S + sum_s exp(LG_n - LG_s) Delta_s k_s^T
-// which unrolls the recurrence of ref.c:708-739 (s = decay S; kv = s k;
-// delta = (v - kv) beta; S = s + delta k^T; y = S q) exactly in real
-// arithmetic; in fp32 it differs by reassociation. k_wy_prep computes the
-// state-free parts of every (sub-chunk, head) in parallel; k_wy_scan walks a
-// head's sub-chunks in order for a block of WY_RB state rows (rows are
-// independent in the rule), with only dense products per sub-chunk.
-// Workspace per (head, sub-chunk): W^T, Mq^T [WY_C][WY_C], beta, exp(LG_t),
-// exp(LG_n - LG_s) [WY_C]. Row strides: qkv (the conv output) a.conv_dim,
-// a.in (the projection rows the gates come from) in_stride.
-// ---------------------------------------------------------------------------
-#define WY_C 64
-#define WY_RB 16
-#define WY_PITCH(D) ((D) + 4)
-#define WY_WS (2 * WY_C * WY_C + 3 * WY_C)
-
-// log of the decay gate (gdn_gates' decay = exp(this)).
-__device__ __forceinline__ float gdn_log_decay(float a, float ssm_a, float dt, int neg_exp) {
-    const float sp = softplus(a + dt);
-    return neg_exp ? ssm_a * sp : -(expf(ssm_a) * sp);
-}
-
-template <int DK>
-__global__ void __launch_bounds__(TPB) k_wy_prep(sgk_gdn a, const float *qkv, uint32_t in_stride, uint32_t ntok,
-                                                 const float *gates, float *ws) {
-    __shared__ __align__(16) float KT[DK][WY_C + 4];
-    __shared__ __align__(16) float QT[DK][WY_C + 4];
-    __shared__ float Tm[WY_C][WY_C + 1];
-    __shared__ float Mq[WY_C][WY_C + 1];
-    __shared__ double L[WY_C];
-    __shared__ float bt[WY_C], red[4][WY_C];
-    const uint32_t c = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
-    const uint32_t z0 = c * WY_C, n = min((uint32_t)WY_C, ntok - z0);
-    const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k), key_dim = a.n_k * DK;
-    // 1. k and q of the sub-chunk's tokens, transposed ([i][t]); zero past n
-    for (uint32_t e = t; e < WY_C * DK / 4; e += TPB) {
-        const uint32_t row = e / (DK / 4), i = (e % (DK / 4)) * 4;
-        f32x4 kv = {0.f, 0.f, 0.f, 0.f}, qv = {0.f, 0.f, 0.f, 0.f};
-        if (row < n) {
-            const float *cz = qkv + (size_t)(z0 + row) * a.conv_dim;
-            kv = *(const f32x4 *)(cz + key_dim + (size_t)hk * DK + i);
-            qv = *(const f32x4 *)(cz + (size_t)hk * DK + i);
-        }
-        KT[i][row] = kv.x; KT[i + 1][row] = kv.y; KT[i + 2][row] = kv.z; KT[i + 3][row] = kv.w;
-        QT[i][row] = qv.x; QT[i + 1][row] = qv.y; QT[i + 2][row] = qv.z; QT[i + 3][row] = qv.w;
-    }
-    // 2. beta and log decay per token (0 and 0 past n)
-    if (t < WY_C) {
-        float beta = 0.0f, lg = 0.0f;
-        if (t < n) {
-            const uint32_t z = z0 + t;
-            if (gates) {
-                beta = gates[(size_t)z * 2 * a.n_v + h];
-                const float dcy = gates[(size_t)z * 2 * a.n_v + a.n_v + h];
-                lg = dcy > 0.0f ? logf(dcy) : -1.0e30f;
-            } else {
-                const float *iz = a.in + (size_t)z * in_stride;
-                const uint32_t cd = a.conv_dim, vd = a.n_v * a.dv;
-                beta = sigm(iz[cd + vd + h]);
-                lg = gdn_log_decay(iz[cd + vd + a.n_v + h], a.ssm_a[h], a.dt_bias[h], a.neg_exp);
-            }
-        }
-        bt[t] = beta;
-        red[0][t] = lg;
-    }
-    __syncthreads();
-    if (t == 0) {
-        double acc = 0.0;
-        for (uint32_t i = 0; i < WY_C; i++) { acc += (double)red[0][i]; L[i] = acc; }
-    }
-    // 3. G = K K^T and A = Q K^T, 4x4 tiles per thread
-    const uint32_t tr = t % 16, sc = t / 16, t0 = tr * 4, s0 = sc * 4;
-    float G[4][4], A[4][4];
-#pragma unroll
-    for (int x = 0; x < 4; x++)
-#pragma unroll
-        for (int y = 0; y < 4; y++) G[x][y] = A[x][y] = 0.0f;
-    __syncthreads();
-    for (uint32_t i = 0; i < DK; i++) {
-        const f32x4 ka = *(const f32x4 *)&KT[i][t0], kb = *(const f32x4 *)&KT[i][s0], qa = *(const f32x4 *)&QT[i][t0];
-        const float kav[4] = {ka.x, ka.y, ka.z, ka.w}, kbv[4] = {kb.x, kb.y, kb.z, kb.w}, qav[4] = {qa.x, qa.y, qa.z, qa.w};
-#pragma unroll
-        for (int x = 0; x < 4; x++)
-#pragma unroll
-            for (int y = 0; y < 4; y++) {
-                G[x][y] = fmaf(kav[x], kbv[y], G[x][y]);
-                A[x][y] = fmaf(qav[x], kbv[y], A[x][y]);
-            }
-    }
-#pragma unroll
-    for (int x = 0; x < 4; x++)
-#pragma unroll
-        for (int y = 0; y < 4; y++) {
-            const uint32_t tt = t0 + x, ss = s0 + y;
-            const float r = ss <= tt ? expf((float)(L[tt] - L[ss])) : 0.0f;
-            Tm[tt][ss] = ss < tt ? bt[tt] * r * G[x][y] : 0.0f;
-            Mq[tt][ss] = ss <= tt ? r * A[x][y] : 0.0f;
-        }
-    __syncthreads();
-    // 4. W = (I + T)^-1 in place, row by row (forward substitution):
-    //    W_t = e_t - sum_{s<t} T_ts W_s
-    {
-        const uint32_t u = t & (WY_C - 1), part = t / WY_C;
-        if (part == 0) Tm[0][u] = u == 0 ? 1.0f : 0.0f;      // W_0 = e_0 (row 0 of T is zero)
-        __syncthreads();
-        for (uint32_t row = 1; row < WY_C; row++) {
-            float acc = 0.0f;
-            for (uint32_t sidx = part; sidx < row; sidx += TPB / WY_C) acc = fmaf(Tm[row][sidx], Tm[sidx][u], acc);
-            red[part][u] = acc;
-            __syncthreads();
-            if (part == 0) {
-                const float sum = (red[0][u] + red[1][u]) + (red[2][u] + red[3][u]);
-                Tm[row][u] = (u == row ? 1.0f : 0.0f) - (u < row ? sum : 0.0f);
-            }
-            __syncthreads();
-        }
-    }
-    // 5. W^T, Mq^T, beta, exp(LG_t), exp(LG_n - LG_s)
-    float *o = ws + ((size_t)h * gridDim.x + c) * WY_WS;
-    for (uint32_t e = t; e < WY_C * WY_C; e += TPB) {
-        const uint32_t sidx = e / WY_C, tt = e % WY_C;
-        o[e] = Tm[tt][sidx];
-        o[WY_C * WY_C + e] = Mq[tt][sidx];
-    }
-    if (t < WY_C) {
-        o[2 * WY_C * WY_C + t] = bt[t];
-        o[2 * WY_C * WY_C + WY_C + t] = expf((float)L[t]);
-        o[2 * WY_C * WY_C + 2 * WY_C + t] = expf((float)(L[n - 1] - L[t]));
-    }
-}
-
-template <int DK>
-__global__ void __launch_bounds__(TPB) k_wy_scan(sgk_gdn a, const float *qkv, uint32_t in_stride, uint32_t ntok,
-                                                 const float *ws) {
-    __shared__ __align__(16) float Ks[WY_C][WY_PITCH(DK)];
-    __shared__ __align__(16) float Qs[WY_C][WY_PITCH(DK)];
-    __shared__ __align__(16) float WT[WY_C][WY_C];
-    __shared__ __align__(16) float MT[WY_C][WY_C];
-    __shared__ __align__(16) float Ss[WY_RB][WY_PITCH(DK)];
-    __shared__ float Rv[WY_C][WY_RB + 1];
-    __shared__ float Dl[WY_C][WY_RB + 1];
-    __shared__ float bt[WY_C], gg[WY_C], dd[WY_C];
-    const uint32_t h = blockIdx.x, j0 = blockIdx.y * WY_RB, t = threadIdx.x;
-    const uint32_t dv = a.dv, vd = a.n_v * dv, key_dim = a.n_k * DK;
-    const uint32_t hk = a.tiled ? h % a.n_k : h / (a.n_v / a.n_k);
-    const uint32_t nsub = (ntok + WY_C - 1) / WY_C;
-    float *Sh = a.S + (size_t)h * dv * DK;
-    // this block's state rows (zero past dv)
-    for (uint32_t e = t; e < WY_RB * DK / 4; e += TPB) {
-        const uint32_t jj = e / (DK / 4), i = (e % (DK / 4)) * 4;
-        *(f32x4 *)&Ss[jj][i] = j0 + jj < dv ? *(const f32x4 *)(Sh + (size_t)(j0 + jj) * DK + i) : (f32x4){0.f, 0.f, 0.f, 0.f};
-    }
-    const uint32_t jj = t % WY_RB, tq = t / WY_RB, tt0 = tq * 4;      // X, Z, Delta, Y: rows tt0..+3 of column jj
-    const uint32_t ij = t % WY_RB, i0 = (t / WY_RB) * (DK / (TPB / WY_RB));   // S update: row ij, DK/16 columns from i0
-    constexpr int SI = DK / (TPB / WY_RB);
-    for (uint32_t c = 0; c < nsub; c++) {
-        const uint32_t z0 = c * WY_C, n = min((uint32_t)WY_C, ntok - z0);
-        const float *o = ws + ((size_t)h * nsub + c) * WY_WS;
-        for (uint32_t e = t; e < WY_C * DK / 4; e += TPB) {
-            const uint32_t row = e / (DK / 4), i = (e % (DK / 4)) * 4;
-            f32x4 kv = {0.f, 0.f, 0.f, 0.f}, qv = {0.f, 0.f, 0.f, 0.f};
-            if (row < n) {
-                const float *cz = qkv + (size_t)(z0 + row) * a.conv_dim;
-                kv = *(const f32x4 *)(cz + key_dim + (size_t)hk * DK + i);
-                qv = *(const f32x4 *)(cz + (size_t)hk * DK + i);
-            }
-            *(f32x4 *)&Ks[row][i] = kv;
-            *(f32x4 *)&Qs[row][i] = qv;
-        }
-        for (uint32_t e = t; e < WY_C * WY_C / 4; e += TPB) {
-            *(f32x4 *)&WT[0][4 * e] = *(const f32x4 *)(o + 4 * e);
-            *(f32x4 *)&MT[0][4 * e] = *(const f32x4 *)(o + WY_C * WY_C + 4 * e);
-        }
-        if (t < WY_C) {
-            bt[t] = o[2 * WY_C * WY_C + t];
-            gg[t] = o[2 * WY_C * WY_C + WY_C + t];
-            dd[t] = o[2 * WY_C * WY_C + 2 * WY_C + t];
-        }
-        // v of this block's rows: Rv[t][jj] <- v (scaled below)
-        for (uint32_t e = t; e < WY_C * WY_RB; e += TPB) {
-            const uint32_t row = e / WY_RB, q = e % WY_RB;
-            Rv[row][q] = (row < n && j0 + q < dv) ? qkv[(size_t)(z0 + row) * a.conv_dim + 2 * key_dim + (size_t)h * dv + j0 + q]
-                                                  : 0.0f;
-        }
-        __syncthreads();
-        // X = K S^T, Z = Q S^T for rows tt0..tt0+3, column jj
-        float X[4] = {0.f, 0.f, 0.f, 0.f}, Z[4] = {0.f, 0.f, 0.f, 0.f};
-        for (uint32_t i = 0; i < DK; i += 4) {
-            const f32x4 sv = *(const f32x4 *)&Ss[jj][i];
-#pragma unroll
-            for (int x = 0; x < 4; x++) {
-                const f32x4 kv = *(const f32x4 *)&Ks[tt0 + x][i], qv = *(const f32x4 *)&Qs[tt0 + x][i];
-                X[x] = fmaf(kv.x, sv.x, fmaf(kv.y, sv.y, fmaf(kv.z, sv.z, fmaf(kv.w, sv.w, X[x]))));
-                Z[x] = fmaf(qv.x, sv.x, fmaf(qv.y, sv.y, fmaf(qv.z, sv.z, fmaf(qv.w, sv.w, Z[x]))));
-            }
-        }
-        float rv[4];
-#pragma unroll
-        for (int x = 0; x < 4; x++) rv[x] = bt[tt0 + x] * (Rv[tt0 + x][jj] - gg[tt0 + x] * X[x]);
-        __syncthreads();                     // every thread has read its v
-#pragma unroll
-        for (int x = 0; x < 4; x++) Rv[tt0 + x][jj] = rv[x];
-        __syncthreads();
-        // Delta = W Rv (W lower triangular: s <= t)
-        float dl[4] = {0.f, 0.f, 0.f, 0.f};
-        const uint32_t smax = min(tt0 + 4, n);
-        for (uint32_t sidx = 0; sidx < smax; sidx++) {
-            const f32x4 w4 = *(const f32x4 *)&WT[sidx][tt0];
-            const float r = Rv[sidx][jj];
-            dl[0] = fmaf(w4.x, r, dl[0]); dl[1] = fmaf(w4.y, r, dl[1]);
-            dl[2] = fmaf(w4.z, r, dl[2]); dl[3] = fmaf(w4.w, r, dl[3]);
-        }
-#pragma unroll
-        for (int x = 0; x < 4; x++) Dl[tt0 + x][jj] = dl[x];
-        __syncthreads();
-        // Y = exp(LG) Z + Mq Delta
-        float y[4];
-#pragma unroll
-        for (int x = 0; x < 4; x++) y[x] = gg[tt0 + x] * Z[x];
-        for (uint32_t sidx = 0; sidx < smax; sidx++) {
-            const f32x4 m4 = *(const f32x4 *)&MT[sidx][tt0];
-            const float d = Dl[sidx][jj];
-            y[0] = fmaf(m4.x, d, y[0]); y[1] = fmaf(m4.y, d, y[1]);
-            y[2] = fmaf(m4.z, d, y[2]); y[3] = fmaf(m4.w, d, y[3]);
-        }
-#pragma unroll
-        for (int x = 0; x < 4; x++)
-            if (tt0 + x < n && j0 + jj < dv) a.y[(size_t)(z0 + tt0 + x) * vd + (size_t)h * dv + j0 + jj] = y[x];
-        // S' = exp(LG_n) S + sum_s exp(LG_n - LG_s) Delta_s k_s^T (row ij, columns i0..i0+SI-1)
-        {
-            const float gn = gg[n - 1];
-            float sr[SI];
-#pragma unroll
-            for (int e = 0; e < SI; e++) sr[e] = gn * Ss[ij][i0 + e];
-            for (uint32_t sidx = 0; sidx < n; sidx++) {
-                const float coef = dd[sidx] * Dl[sidx][ij];
-#pragma unroll
-                for (int e = 0; e < SI; e += 4) {
-                    const f32x4 kv = *(const f32x4 *)&Ks[sidx][i0 + e];
-                    sr[e] = fmaf(coef, kv.x, sr[e]); sr[e + 1] = fmaf(coef, kv.y, sr[e + 1]);
-                    sr[e + 2] = fmaf(coef, kv.z, sr[e + 2]); sr[e + 3] = fmaf(coef, kv.w, sr[e + 3]);
-                }
-            }
-            __syncthreads();                 // every thread has read S (X, Z) and this row's old values
-#pragma unroll
-            for (int e = 0; e < SI; e++) Ss[ij][i0 + e] = sr[e];
-        }
-        __syncthreads();
-    }
-    for (uint32_t e = t; e < WY_RB * DK / 4; e += TPB) {
-        const uint32_t r = e / (DK / 4), i = (e % (DK / 4)) * 4;
-        if (j0 + r < dv) *(f32x4 *)(Sh + (size_t)(j0 + r) * DK + i) = *(const f32x4 *)&Ss[r][i];
-    }
-}
-
-// ---------------------------------------------------------------------------
 // Chunked delta rule on the matrix cores: blocks of DM_T = 16 tokens in fp32
 // MFMA (v_mfma_f32_16x16x4_f32). With d_t the decay, R_tw = d_{w+1}...d_t
 // (R_tt = 1), g_t = d_0...d_t, G = K K^T and H = Q K^T over the block's tokens:
@@ -3338,8 +2929,10 @@ __global__ void __launch_bounds__(TPB) k_wy_scan(sgk_gdn a, const float *qkv, ui
 //   Delta = W' (V - g * (K S^T))      (rows: tokens t, columns: value rows j)
 //   Y     = g * (Q S^T) + M Delta
 //   S'    = g_15 S + (rho * Delta)^T K
-// which is the token loop of ref.c:708-739 unrolled over the block, as in the
-// 64-token form above, with the decay products taken as plain products.
+// which is the token loop of ref.c:708-739 (s = decay S; kv = s k; delta =
+// (v - kv) beta; S = s + delta k^T; y = S q) unrolled over the block exactly
+// in real arithmetic (in fp32 it differs by reassociation), with the decay
+// products taken as plain products.
 // k_dm_prep computes W', M, g and rho of every (head, block) in parallel, one
 // wave each; k_dm_scan walks a head's blocks in order for 16 value rows, with
 // the state held in MFMA accumulator layout across the workgroup's 4 waves
@@ -3637,31 +3230,27 @@ __global__ void __launch_bounds__(DM_TPB) k_dm_scan(sgk_gdn a, const float *qkv,
 }
 
 // SURGE_DELTA_SCAN (read per launch) selects the prefill scan: "mfma" (the
-// default) the 16-token chunked form on the matrix cores, "wy" the 64-token
-// chunked form, "seq" the sequential token loop. The chunked forms need the
-// workspace and dk 64 or 128 (mfma also dv a multiple of 16); other shapes
-// run the sequential loop. Per 512-token call of the 27B layer (48 heads,
-// dk = dv = 128): mfma 51 + 11 us (scan + prep), seq 199 us.
-enum { SCAN_SEQ, SCAN_WY, SCAN_MFMA };
-// SURGE_DELTA_SCAN: unset, empty or "mfma" (default), "wy" or "seq"; any
-// other value is refused by the host before a scan launches
+// default) the 16-token chunked form on the matrix cores, "seq" the
+// sequential token loop. The chunked form needs the workspace, dk 64 or 128
+// and dv a multiple of 16; other shapes run the sequential loop. Per
+// 512-token call of the 27B layer (48 heads, dk = dv = 128): mfma 51 + 11 us
+// (scan + prep), seq 199 us.
+enum { SCAN_SEQ, SCAN_MFMA };
+// SURGE_DELTA_SCAN: unset, empty or "mfma" (default), or "seq"; any other
+// value is refused by the host before a scan launches
 // (sgk_delta_scan_env_ok), so an A/B never measures a form it did not name.
 static int scan_mode() {
     const char *e = getenv("SURGE_DELTA_SCAN");
-    if (e && !strcmp(e, "wy")) return SCAN_WY;
-    if (e && !strcmp(e, "seq")) return SCAN_SEQ;
-    return SCAN_MFMA;
+    return e && !strcmp(e, "seq") ? SCAN_SEQ : SCAN_MFMA;
 }
 
 extern "C" int sgk_delta_scan_env_ok(void) {
     const char *e = getenv("SURGE_DELTA_SCAN");
-    return !e || !*e || !strcmp(e, "mfma") || !strcmp(e, "wy") || !strcmp(e, "seq");
+    return !e || !*e || !strcmp(e, "mfma") || !strcmp(e, "seq");
 }
 
-extern "C" uint64_t sgk_delta_wy_ws_floats(uint32_t n_v, uint32_t ntok) {
-    const uint64_t wy = (uint64_t)n_v * ((ntok + WY_C - 1) / WY_C) * WY_WS;
-    const uint64_t dm = (uint64_t)n_v * ((ntok + DM_T - 1) / DM_T) * DM_WS;
-    return wy > dm ? wy : dm;
+extern "C" uint64_t sgk_delta_ws_floats(uint32_t n_v, uint32_t ntok) {
+    return (uint64_t)n_v * ((ntok + DM_T - 1) / DM_T) * DM_WS;
 }
 
 extern "C" hipError_t sgk_gdn_chunk(const sgk_gdn *a, float *conv_out, uint32_t in_stride, uint32_t ntok,
@@ -3697,18 +3286,6 @@ extern "C" hipError_t sgk_delta_scan(const sgk_gdn *a, const float *qkv, uint32_
             hipLaunchKernelGGL((k_dm_scan<D>), dim3(a->n_v, a->dv / DM_T), dim3(DM_TPB), 0, s, *a, qkv, ntok, ws); } while (0)
         if (a->dk == 64) DML(64); else DML(128);
 #undef DML
-        return hipGetLastError();
-    }
-    if (mode == SCAN_WY) {
-        // the chunked form: state-free parts of every (sub-chunk, head), then
-        // each head's sub-chunks in order per block of WY_RB state rows
-        const uint32_t nsub = (ntok + WY_C - 1) / WY_C;
-#define WYL(D) do {                                                                                            \
-            hipLaunchKernelGGL((k_wy_prep<D>), dim3(nsub, a->n_v), dim3(TPB), 0, s, *a, qkv, in_stride, ntok, gates, ws); \
-            hipLaunchKernelGGL((k_wy_scan<D>), dim3(a->n_v, (a->dv + WY_RB - 1) / WY_RB), dim3(TPB), 0, s, *a, qkv,       \
-                               in_stride, ntok, ws); } while (0)
-        if (a->dk == 64) WYL(64); else WYL(128);
-#undef WYL
         return hipGetLastError();
     }
     // 8 value rows per workgroup (16-token staged blocks: 33 KB of LDS at
@@ -4891,379 +4468,4 @@ extern "C" void *sgk_scratch_ptr(int dev) {
     return (dev >= 0 && dev < SGK_SCRATCH_DEVICES) ? scratch_at[dev] : NULL;
 }
 
-// ---------------------------------------------------------------------------
-// Decode chain: one persistent launch runs a run of decode stages (embedding,
-// Q8_0 GEMVs, DeltaNet steps) back to back, with a barrier between stages
-// instead of a kernel boundary, and every workgroup requesting its first
-// weight rows of the next GEMV before it waits at the barrier, so HBM keeps
-// streaming while the last workgroups finish and the barrier resolves.
-//
-// Grid: one CT-thread workgroup per CU (its dynamic LDS keeps a second one
-// off the CU), all resident at once. In a GEMV stage workgroup b owns the
-// contiguous row groups [b*G/NB, (b+1)*G/NB) (G groups of CR rows); wave w
-// takes every CW-th of them from w on, every wave the same count (a wave
-// whose last group falls past the workgroup's range re-reads that range's
-// last group and stores nothing). A wave streams a row group exactly as
-// k_gemv_q8<2> does (lane l: chunks l, l+64, ... of both rows, f32 FMA per
-// chunk, one wave_sum per row), so the row sums are the same bits. Loads run
-// CP steps (one 16-byte chunk of each of the CR rows) ahead of the FMAs in a
-// register ring indexed statically.
-//
-// Coherence without cache-wide fences: a stage writes its outputs with
-// device-scope stores (st_out<true>: sc1, through the XCD's L2 to memory)
-// into buffers written once per token and never read before that write in
-// the launch, so no XCD holds a stale line of them; then waits for its
-// stores (vmcnt), and one thread per workgroup adds 1 to its XCD's arrival
-// counter of the stage. A waiter polls the 8 counters of the stage with
-// device-scope loads until each holds epoch x its workgroup count (counters
-// only grow: the host passes the token's epoch, 1, 2, ...). A wait gives up
-// after CH_SPIN_MAX polls or as soon as another workgroup has given up, and
-// sets *err, so a launch always ends.
-// ---------------------------------------------------------------------------
-#define CT 512
-#define CW (CT / 64)
-#define CR 2
-#define CH_XCDS 8u
-#define CH_CNT_STRIDE 64u            // uint32 per counter: one 256-byte line each
-#define CH_SPIN_MAX (1u << 21)
-constexpr int CXK_NONE = (SGK_CHAIN_MAX_COLS + 4 * CT - 1) / (4 * CT);   // x float4s per thread in flight
-constexpr int CXK_RMS = (SGK_CHAIN_MAX_RMS_COLS + 4 * CT - 1) / (4 * CT);
-static_assert(XS_CH_BLK * 4 == 1040, "chain: sgk_chain_lds_floats assumes 1040 floats per 1024 staged columns");
-
-__device__ __forceinline__ uint32_t ch_ld(const uint32_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Measurement stamps (sgk_chain.stamps): the device wall clock at point k of
-// stage st, seen by thread 0.
-__device__ __forceinline__ void ch_stamp(const sgk_chain &a, uint32_t st, uint32_t k) {
-    if (a.stamps && threadIdx.x == 0) a.stamps[((size_t)st * gridDim.x + blockIdx.x) * 3 + k] = wall_clock64();
-}
-
-// Workgroups of the grid that add to counter x of a stage.
-__device__ __forceinline__ uint32_t ch_share(uint32_t x) { return (gridDim.x + CH_XCDS - 1 - x) / CH_XCDS; }
-
-// Arrival at stage st: this workgroup's stores are complete, then one add.
-// Returns, in thread 0, which launch of the stage this is (0, 1, ...): a
-// stage's counters only grow, each launch adds ch_share(x) to counter x, and
-// launches of one stage run one after another, so the value before the add
-// tells the round. No per-token number comes from the host, so the launches
-// replay unchanged from a captured graph.
-__device__ __forceinline__ uint32_t ch_arrive(const sgk_chain &a, uint32_t st) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    ch_stamp(a, st, 2);
-    uint32_t r = 0;
-    if (threadIdx.x == 0) {
-        const uint32_t x = blockIdx.x % CH_XCDS;
-        r = __hip_atomic_fetch_add(a.cnt + ((size_t)st * CH_XCDS + x) * CH_CNT_STRIDE, 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT) / ch_share(x);
-    }
-    return r;
-}
-
-// Wait until every workgroup has arrived at round r of stage st.
-__device__ __forceinline__ void ch_wait(const sgk_chain &a, uint32_t st, uint32_t r) {
-    if (threadIdx.x == 0) {
-        const uint32_t *c = a.cnt + (size_t)st * CH_XCDS * CH_CNT_STRIDE;
-        for (uint32_t it = 0;; it++) {
-            bool ok = true;
-#pragma unroll
-            for (uint32_t x = 0; x < CH_XCDS; x++) {
-                const uint32_t want = (r + 1) * ch_share(x);
-                ok &= (int32_t)(ch_ld(c + x * CH_CNT_STRIDE) - want) >= 0;
-            }
-            if (ok) break;
-            if (ch_ld(a.err) != 0u) break;
-            if (it >= (a.spin ? a.spin : CH_SPIN_MAX)) { __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); break; }
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
-    __syncthreads();
-}
-
-// A wave's share of one GEMV stage. Workgroup b owns the row groups
-// [b*G/NB, (b+1)*G/NB) (G groups of CR rows; interleaving them across
-// workgroups measured 2% slower in the chain, though faster in the
-// standalone balanced GEMV); their steps (group, 1024-column step j),
-// group-major, are dealt to the CW waves in equal contiguous ranges (within
-// one step of each other), so a stage is balanced to a step
-// per wave and a group per workgroup however few groups there are. A wave
-// streams its steps as k_gemv_q8<2> streams a row group (lane l: chunks l,
-// l+64, ... of both rows, f32 FMA per chunk), and writes one wave-reduced
-// partial per group it touched into LDS (the others' slots stay 0); after the
-// stage the workgroup adds each group's CW slots in wave order (adding the
-// zeros is exact, so a group one wave did whole keeps k_gemv_q8's bits).
-struct ch_gemv {
-    const int8_t *qs;
-    const uint16_t *d;
-    uint32_t rows, cols, nsteps;     // steps per row group: cols / 1024
-    uint32_t g0, ng;                 // the workgroup's row groups [g0, g0 + ng)
-    uint32_t s0, ns;                 // this wave's steps of them
-};
-
-__device__ __forceinline__ ch_gemv ch_enter(const sgk_cstage &S, uint32_t w) {
-    ch_gemv c;
-    c.qs = S.qs; c.d = S.d; c.rows = S.rows; c.cols = S.cols; c.nsteps = S.cols >> 10;
-    const uint32_t G = (S.rows + CR - 1) / CR, nb = gridDim.x, b = blockIdx.x;
-    c.g0 = (uint32_t)((uint64_t)b * G / nb);
-    c.ng = (uint32_t)((uint64_t)(b + 1) * G / nb) - c.g0;
-    const uint32_t T = c.ng * c.nsteps;
-    c.s0 = w * T / CW;
-    c.ns = (w + 1) * T / CW - c.s0;
-    return c;
-}
-
-// Request the step at (group k of the workgroup, chunk step j); groups past
-// the workgroup's re-read its last (never out of bounds).
-__device__ __forceinline__ void ch_issue(gemv_chunk<CR> &ch, const ch_gemv &c, uint32_t k, uint32_t j, uint32_t lane) {
-    const uint32_t kk = k < c.ng ? k : c.ng - 1;
-    gemv_load<CR>(ch, c.qs, c.d, (c.g0 + kk) * CR, c.rows, c.cols, lane + 64 * j);
-}
-
-__device__ __forceinline__ void ch_step_next(uint32_t &k, uint32_t &j, uint32_t nsteps) {
-    if (++j == nsteps) { j = 0; k++; }
-}
-
-// LDS of a GEMV stage after the staged x: the groups' partial slots
-// [ng][CW][CR], then the residual rows [ng*CR].
-__device__ __forceinline__ uint32_t ch_part_off(uint32_t cols) { return xs_ch_floats(cols); }
-
-// The stage's outputs from the partial slots (all waves' slots written and
-// visible): thread t < ng*CR sums row t's slots in wave order.
-__device__ __forceinline__ void ch_finish(const sgk_cstage &S, const ch_gemv &c, const float *part, const float *res,
-                                          float post) {
-    const uint32_t t = threadIdx.x;
-    for (uint32_t i = t; i < c.ng * CR; i += CT) {
-        const uint32_t k = i / CR, r = i % CR, row = (c.g0 + k) * CR + r;
-        float v = 0.0f;
-#pragma unroll
-        for (uint32_t w = 0; w < CW; w++) v += part[(k * CW + w) * CR + r];
-        v *= post;
-        if (S.epi == SGK_EPI_SWIGLU) {
-            // (gate, up) rows: the even thread of the pair has both
-            const float u = __shfl_down(v, 1);
-            if (r == 0 && row + 1 < S.rows) st_out<true>(S.y + (row >> 1), silu(v) * u);
-        } else if (row < S.rows) {
-            st_out<true>(S.y + row, S.epi == SGK_EPI_ADD ? res[i] + v : v);
-        }
-    }
-}
-
-__device__ __forceinline__ void ch_embed(const sgk_cstage &S) {
-    const uint32_t H = S.cols, nb = gridDim.x, b = blockIdx.x;
-    const uint32_t lo = (uint32_t)((uint64_t)b * H / nb), hi = (uint32_t)((uint64_t)(b + 1) * H / nb);
-    const uint64_t tk = (uint64_t)(uint32_t)S.step->token;
-    for (uint32_t i = lo + threadIdx.x; i < hi; i += CT)
-        st_out<true>(S.y + i, h2f(S.d[tk * (H >> 5) + (i >> 5)]) * (float)S.qs[tk * H + i]);
-}
-
-// Stage x (and the residual slice for EPI_ADD), split so the ring's top-up
-// loads can go out between the x requests and the LDS stores.
-template <int PRO>
-struct ch_xs {
-    static constexpr int K = PRO == SGK_PRO_RMS ? CXK_RMS : CXK_NONE;
-    sgk_gemv ga;
-    xstage<PRO, CT, K> st;
-};
-template <int PRO>
-__device__ __forceinline__ void ch_x_issue(ch_xs<PRO> &X, const sgk_cstage &S, const ch_gemv &c, float *lds) {
-    X.ga = sgk_gemv{};
-    X.ga.x = S.x; X.ga.nw = S.nw; X.ga.cols = S.cols; X.ga.eps = S.eps;
-    stage_issue<PRO, CT, ch_xs<PRO>::K>(X.ga, X.st);
-    float *part = lds + ch_part_off(S.cols), *res = part + c.ng * CW * CR;
-    const uint32_t t = threadIdx.x;
-    for (uint32_t i = t; i < c.ng * CW * CR; i += CT) part[i] = 0.0f;
-    if (S.epi == SGK_EPI_ADD) {
-        for (uint32_t i = t; i < c.ng * CR; i += CT) {
-            const uint32_t row = c.g0 * CR + i;
-            res[i] = row < S.rows ? S.res[row] : 0.0f;
-        }
-    }
-}
-template <int PRO>
-__device__ __forceinline__ float ch_x_finish(ch_xs<PRO> &X, float *xs) {
-    return stage_finish<PRO, CT, ch_xs<PRO>::K, true>(X.ga, X.st, xs);
-}
-
-// CP: steps a wave keeps in flight while streaming (the ring); PR <= CP: how
-// many of a GEMV's first steps are requested before the barrier that
-// precedes it (the rest go out right after it, behind the x requests). Loads
-// requested before a barrier delay everything the wave requests after them
-// (returns are in order), the barrier's polls included, so PR is kept to what
-// covers the barrier.
-// The stage table is read-only for a launch: read through the constant
-// address space, its fields come in by scalar loads, which do not wait
-// behind the wave's weight requests (a vector load's wait would).
-#if defined(__HIP_DEVICE_COMPILE__)
-typedef const __attribute__((address_space(4))) sgk_cstage ch_table;
-#else
-typedef const sgk_cstage ch_table;
-#endif
-
-template <int DK, int RW, int CP, int PR>
-__global__ void __launch_bounds__(CT) k_chain(sgk_chain a) {
-    static_assert(PR <= CP, "chain: prime at most the ring");
-    ch_table *T = (ch_table *)a.st;
-    extern __shared__ float cl[];
-    float *xs = cl;
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    gemv_chunk<CR> ring[CP];
-    bool primed = false;
-    ch_gemv pc = {};                  // the GEMV stage the ring was primed for
-    // The first PR steps of a wave's share of stage c into the ring.
-    auto prime = [&](const ch_gemv &c) {
-        if (!c.ns) return;
-        uint32_t k = c.s0 / c.nsteps, j = c.s0 % c.nsteps;
-#pragma unroll
-        for (int u = 0; u < PR; u++) {
-            ch_issue(ring[u], c, k, j, lane);
-            ch_step_next(k, j, c.nsteps);
-        }
-    };
-    // Prime the ring for the next GEMV stage after st, unless this workgroup
-    // has other work (a DeltaNet step) before it: its loads would otherwise
-    // queue ahead of that work's.
-    auto prime_after = [&](uint32_t st) {
-        if (primed) return;
-        for (uint32_t t = st + 1; t < a.s1; t++) {
-            const sgk_cstage S = T[__builtin_amdgcn_readfirstlane(t)];
-            if (S.kind == SGK_CS_GEMV) {
-                pc = ch_enter(S, w);
-                prime(pc);
-                primed = true;
-                return;
-            }
-            if (S.kind == SGK_CS_GDN && blockIdx.x < S.gdn.n_v) return;
-            if (S.kind == SGK_CS_EMBED) return;
-        }
-    };
-    if (T[a.s0].kind == SGK_CS_GEMV) prime_after(a.s0 - 1);
-    uint32_t round = 0;
-    for (uint32_t st = a.s0; st < a.s1; st++) {
-        if (st > a.s0) ch_wait(a, st - 1, round);
-        ch_stamp(a, st, 0);
-        // the descriptor by value: the stage's stores could alias the table,
-        // and a field reloaded after one would wait for every weight load
-        const sgk_cstage S = T[__builtin_amdgcn_readfirstlane(st)];
-        if (S.kind == SGK_CS_GEMV) {
-            if (!primed) {                    // workgroups that ran a DeltaNet step first
-                pc = ch_enter(S, w);
-                prime(pc);
-            }
-            const ch_gemv c = pc;
-            primed = false;
-            float *part = cl + ch_part_off(S.cols), *res = part + c.ng * CW * CR;
-            float post;
-            // x requests, then the ring's remaining first steps (CP - PR, the
-            // same count on every path, so the wait counts stay exact), then
-            // x into LDS
-#define CH_TOPUP()                                                                            \
-            if (c.ns) {                                                                       \
-                uint32_t k = (c.s0 + PR) / c.nsteps, j = (c.s0 + PR) % c.nsteps;              \
-                _Pragma("unroll")                                                             \
-                for (int u = PR; u < CP; u++) {                                               \
-                    ch_issue(ring[u], c, k, j, lane);                                         \
-                    ch_step_next(k, j, c.nsteps);                                             \
-                }                                                                             \
-            }
-            if (S.pro == SGK_PRO_RMS) {
-                ch_xs<SGK_PRO_RMS> X;
-                ch_x_issue(X, S, c, cl);
-                CH_TOPUP();
-                post = ch_x_finish(X, xs);
-            } else {
-                ch_xs<SGK_PRO_NONE> X;
-                ch_x_issue(X, S, c, cl);
-                CH_TOPUP();
-                post = ch_x_finish(X, xs);
-            }
-#undef CH_TOPUP
-            ch_stamp(a, st, 1);
-            if (c.ns) {
-                const uint32_t n = c.ns;
-                float acc[CR];
-#pragma unroll
-                for (int r = 0; r < CR; r++) acc[r] = 0.0f;
-                uint32_t kc = c.s0 / c.nsteps, jc = c.s0 % c.nsteps, ki = kc, ji = jc;
-                for (uint32_t u = 0; u < CP; u++) ch_step_next(ki, ji, c.nsteps);   // the ring holds steps 0..CP-1
-                // step i of the wave's range: FMAs of ring slot u; at a group's
-                // last step or the range's last, the group's wave partial to LDS
-                auto consume = [&](int u, uint32_t i) {
-                    gemv_fma<CR, true>(acc, ring[u], xs, lane + 64 * jc);
-                    if (jc == c.nsteps - 1 || i == n - 1) {
-#pragma unroll
-                        for (int r = 0; r < CR; r++) acc[r] = wave_sum(acc[r]);
-                        if (lane < (uint32_t)CR) part[(kc * CW + w) * CR + lane] = lane == 0 ? acc[0] : acc[CR - 1];
-#pragma unroll
-                        for (int r = 0; r < CR; r++) acc[r] = 0.0f;
-                    }
-                    ch_step_next(kc, jc, c.nsteps);
-                };
-                uint32_t i = 0;
-                // steady state: every consumed slot is refilled, unconditionally
-                for (; i + 2 * CP <= n; i += CP) {
-#pragma unroll
-                    for (int u = 0; u < CP; u++) {
-                        consume(u, i + u);
-                        ch_issue(ring[u], c, ki, ji, lane);
-                        ch_step_next(ki, ji, c.nsteps);
-                    }
-                }
-                // the last n - i (< 2 CP) steps: refill only what is still to come
-#pragma unroll
-                for (int u = 0; u < CP; u++) {
-                    if (i + u < n) {
-                        consume(u, i + u);
-                        if (i + u + CP < n) {
-                            ch_issue(ring[u], c, ki, ji, lane);
-                            ch_step_next(ki, ji, c.nsteps);
-                        }
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < CP; u++)
-                    if (i + CP + u < n) consume(u, i + CP + u);
-            }
-            __syncthreads();
-            ch_finish(S, c, part, res, post);
-        } else if (S.kind == SGK_CS_GDN) {
-            if (blockIdx.x < S.gdn.n_v) gdn_step_body<DK, RW, 1, CT, true>(S.gdn, blockIdx.x, 0);
-        } else if (S.kind == SGK_CS_EMBED) {
-            ch_embed(S);
-        }
-        round = ch_arrive(a, st);
-        prime_after(st);
-    }
-}
-
-extern "C" uint32_t sgk_chain_blocks(void) { return (uint32_t)device_cus(); }
-
-#define CH_CP 4
-#define CH_PR 4
-extern "C" hipError_t sgk_chain_launch(const sgk_chain *a, uint32_t dk, uint32_t dv, hipStream_t s) {
-    if (!a->st || !a->cnt || !a->err || a->s0 >= a->s1) return hipErrorInvalidValue;
-    const uint32_t rw = (dv + 7) / 8;
-    auto kern = k_chain<128, 16, CH_CP, CH_PR>;
-    if (dk == 128 && rw == 16) {
-        switch (a->tune) {           // ring / prime depth experiments (27B DeltaNet shape)
-        case 1: kern = k_chain<128, 16, 8, 8>; break;
-        case 2: kern = k_chain<128, 16, 4, 4>; break;
-        case 3: kern = k_chain<128, 16, 4, 0>; break;
-        case 4: kern = k_chain<128, 16, 3, 1>; break;
-        case 5: kern = k_chain<128, 16, 6, 2>; break;
-        case 6: kern = k_chain<128, 16, 2, 2>; break;
-        case 7: kern = k_chain<128, 16, 6, 6>; break;
-        case 8: kern = k_chain<128, 16, 5, 5>; break;
-        default: kern = k_chain<128, 16, CH_CP, CH_PR>;
-        }
-    } else if (dk == 128 && rw == 8) kern = k_chain<128, 8, CH_CP, CH_PR>;
-    else if (dk == 64 && rw == 8) kern = k_chain<64, 8, CH_CP, CH_PR>;
-    else if (dk == 64 && rw == 4) kern = k_chain<64, 4, CH_CP, CH_PR>;
-    else return hipErrorInvalidValue;
-    hipError_t e = allow_lds((const void *)kern, SGK_CHAIN_LDS);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3(device_cus()), dim3(CT), SGK_CHAIN_LDS, s, *a);
-    return hipGetLastError();
-}
+extern "C" uint32_t sgk_device_cus(void) { return (uint32_t)device_cus(); }

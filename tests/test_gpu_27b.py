@@ -138,19 +138,3 @@ def test_27b_32k_prefill_then_decode_matches_serial(gpu, model27, capsys):
     print(f"[27b-32k] prefill vs serial last-logit relative gap {rel(last, serial):.3e}", flush=True)
     assert int(np.argmax(last)) == int(np.argmax(serial))
     assert gen_prefill.tolist() == gen_serial.tolist()
-
-
-@pytest.mark.parametrize("mode", ["1", "2"])
-def test_27b_chain_greedy_identical_to_reference(gpu, model27, monkeypatch, mode):
-    """The same 16 + 16 tokens through the decode chain (SURGE_CHAIN=1: one
-    persistent launch per run of stages between attention layers; 2: each
-    DeltaNet layer's step and output projection in one launch)."""
-    gold = json.load(open(os.path.join(fixture.GOLDEN, "greedy_27b_ref.json")))
-    prompt, want = gold["prompt_ids"], gold["gen_ids"]
-    monkeypatch.setenv("SURGE_CHAIN", mode)
-    gpu.state_new(len(prompt) + len(want) + 1)
-    assert gpu.chain_active()
-    for p, t in enumerate(prompt[:-1]):
-        gpu.forward_nosync(t, p)
-    gen = gpu.decode_greedy(prompt[-1], len(prompt) - 1, len(want))
-    assert gen.tolist() == want

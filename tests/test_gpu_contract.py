@@ -36,13 +36,13 @@ def tiny(gpu, monkeypatch):
 
 def test_delta_scan_switch_rejected_not_ignored(gpu, tiny, monkeypatch):
     """SURGE_DELTA_SCAN names the prefill DeltaNet scan's form: mfma (the
-    default), wy or seq; a misspelt value is refused at sg_gpu_state_new and
+    default) or seq; a misspelt value is refused at sg_gpu_state_new and
     by the prefill and chunk entry points, not silently run as another form."""
-    for bad in ("MFMA", "wy ", "sequential", "1"):
+    for bad in ("MFMA", "wy", "seq ", "sequential", "1"):
         monkeypatch.setenv("SURGE_DELTA_SCAN", bad)
         with pytest.raises(S.SurgeError, match="SURGE_DELTA_SCAN"):
             gpu.state_new(64)
-    for good in ("mfma", "wy", "seq", ""):
+    for good in ("mfma", "seq", ""):
         monkeypatch.setenv("SURGE_DELTA_SCAN", good)
         gpu.state_new(64)
     monkeypatch.setenv("SURGE_DELTA_SCAN", "Wy")

@@ -526,7 +526,7 @@ def test_gdn_step_block_forms_vs_oracle(gpu, monkeypatch, cfg_name, blocks):
     (SGK_PRO_GATED: the step writes silu(z) * (y * w) and each block's sum
     of y^2, the prologue applies the head's factor), the default, here at
     head_v_dim 64 and 256; and one workgroup per head finishing it itself
-    (SURGE_GDN_BLOCKS=1, which the decode chain uses). Logits within 1e-3 of
+    (SURGE_GDN_BLOCKS=1). Logits within 1e-3 of
     the oracle with the same argmax over 150 positions; SURGE_GDN_BLOCKS=1 is
     refused for head_v_dim 256."""
     cfg = {"HD128": HD128, "WIDE_V": WIDE_V}[cfg_name]
