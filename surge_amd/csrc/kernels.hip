@@ -1491,7 +1491,7 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
     __shared__ __align__(16) float qsh[GMAX * HD];
     __shared__ __align__(16) float big[BIG];                     // prep: raw q|k rows; end: the waves' outputs
     __shared__ float mw[4][GMAX], lw[4][GMAX], rn[GMAX + 1];
-    __shared__ float cs_s[HD], qn_s[HD], kn_s[HD];
+    __shared__ __align__(16) float cs_s[HD], qn_s[HD], kn_s[HD];
     __shared__ __align__(16) uint16_t knew[HD], vnew[HD];
     float *raw = big;
 
@@ -1504,7 +1504,7 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
 
     // 1. position-independent loads first (as in k_attn_partial)
     float qv[REGQ ? 1 : QPT];
-    f32x4 qx[NKB][2], qw[NKB][2];     // register prep: head min(li, G-1)'s dims 32kb + 8lg.., q_norm weights
+    f32x4 qx[NKB][2];                 // register prep: head min(li, G-1)'s dims 32kb + 8lg..
     if constexpr (!REGQ) {
 #pragma unroll
         for (int k = 0; k < QPT; k++) {
@@ -1516,17 +1516,14 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
-            for (int c = 0; c < 2; c++) {
-                qx[kb][c] = *(const f32x4 *)(qrow + kb * 32 + c * 4);
-                if constexpr (!RAW) qw[kb][c] = *(const f32x4 *)(a.qn + kb * 32 + lg * 8 + c * 4);
-            }
+            for (int c = 0; c < 2; c++) qx[kb][c] = *(const f32x4 *)(qrow + kb * 32 + c * 4);
     }
     const uint32_t td = min(t, (uint32_t)HD - 1);
     float qn0 = 0.0f, kn0 = 0.0f, kr0 = 0.0f, vr0 = 0.0f;
     if constexpr (!RAW) {
         const float *krow = q + (size_t)a.n_heads * a.q_stride + (size_t)hk * HD;
         const float *vrow = krow + (size_t)n_kv * HD;
-        qn0 = RKB ? 0.0f : a.qn[td];
+        qn0 = a.qn[td];
         kn0 = a.kn[td];
         kr0 = krow[td];
         vr0 = vrow[td];
@@ -1549,27 +1546,24 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
         return;
     }
 
-    // 2. the position's cos|sin entry (register prep: cos and sin of the
-    //    lane's rotated dims), then this wave's first 16 keys of K and V
+    // 2. the position's cos|sin entry, then this wave's first 16 keys of K
+    //    and V
     float cs0 = 0.0f;
-    f32x4 rc[RR ? RR : 1][2], rs[RR ? RR : 1][2];
-    if constexpr (!RAW) {
-        const float *csp = a.cs + (size_t)pos * a.rope_dim;
-        cs0 = csp[min(td, a.rope_dim - 1)];
-#pragma unroll
-        for (int kb = 0; kb < RR; kb++)
-#pragma unroll
-            for (int c = 0; c < 2; c++) {
-                rc[kb][c] = *(const f32x4 *)(csp + kb * 32 + lg * 8 + c * 4);
-                rs[kb][c] = *(const f32x4 *)(csp + RR * 32 + kb * 32 + lg * 8 + c * 4);
-            }
-    }
+    if constexpr (!RAW) cs0 = a.cs[(size_t)pos * a.rope_dim + min(td, a.rope_dim - 1)];
     __builtin_amdgcn_sched_barrier(0);
     v4u kr[NKB], vr[4][NQ];
     const uint16_t *kch = a.kc + (size_t)hk * a.kv_hs, *vch = a.vc + (size_t)hk * a.kv_hs;
     const uint32_t base0 = t0 + wave * 16;
     if constexpr (EARLY_K) mf_load_k<HD>(kr, kch, min(base0 + li, klast), a.kv_ps, lg);
-    if constexpr (RKB == 0 || RAW) wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
+    if constexpr (EARLY_K) wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
+    // register prep: the q_norm weights and the cos|sin entry go to LDS (the
+    // lanes read their dims' values there, which keeps them out of registers
+    // while K and V are in flight)
+    if constexpr (!RAW && RKB > 0) {
+        qn_s[td] = qn0;
+        cs_s[td] = td < a.rope_dim ? cs0 : 0.0f;
+        __syncthreads();
+    }
 
     // 3. prep: q_norm + RoPE of the group's heads; the split holding the
     //    position stores that token's K (k_norm + RoPE) and raw V as f16
@@ -1579,10 +1573,10 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int k = 0; k < QPT; k++) raw[t + k * TPB] = qv[k];
             qn_s[td] = qn0;
+            cs_s[td] = td < a.rope_dim ? cs0 : 0.0f;
         }
         raw[KOFF + td] = kr0;
         kn_s[td] = kn0;
-        cs_s[td] = td < a.rope_dim ? cs0 : 0.0f;
         __syncthreads();
         for (uint32_t h = RKB ? G + wave : wave; h <= G; h += TPB / 64) {
             if (h == G && !kv_writer) break;
@@ -1618,7 +1612,7 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int kb = 0; kb < NKB; kb++) kr[kb] = ((const v4u *)(knew + lg * 8))[kb * 4];
         }
-        if constexpr (RKB == 0) {
+        if constexpr (EARLY_K) {
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 if (base0 + 4 * lg + j == pos) {
@@ -1659,12 +1653,12 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) y[kb][e] = (qx[kb][e / 4][e % 4] * rq) * qw[kb][e / 4][e % 4];
+            for (int e = 0; e < 8; e++) y[kb][e] = (qx[kb][e / 4][e % 4] * rq) * qn_s[kb * 32 + lg * 8 + e];
 #pragma unroll
         for (int kb = 0; kb < RKB; kb++)
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float c = rc[kb][e / 4][e % 4], sn = rs[kb][e / 4][e % 4];
+                const float c = cs_s[kb * 32 + lg * 8 + e], sn = cs_s[RR * 32 + kb * 32 + lg * 8 + e];
                 const float lo = y[kb][e], hi = y[kb + RKB][e];
                 y[kb][e] = lo * c - hi * sn;
                 y[kb + RKB][e] = lo * sn + hi * c;
@@ -1679,9 +1673,11 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
         // the first keys' V (and K where it waited), requested after the
         // prep, so after the new row's store and barrier in the split that
         // holds the position
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (!EARLY_K) mf_load_k<HD>(kr, kch, min(base0 + li, klast), a.kv_ps, lg);
-        wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
+        if constexpr (!EARLY_K) {
+            __builtin_amdgcn_sched_barrier(0);
+            mf_load_k<HD>(kr, kch, min(base0 + li, klast), a.kv_ps, lg);
+            wv_load_v<HD>(vr, vch, base0 + 4 * lg, klast, a.kv_ps, li);
+        }
     }
 
     float m_run = -INFINITY, l_run = 0.0f;
