@@ -1406,20 +1406,6 @@ __device__ __forceinline__ void fa_split8(const float *x, f16x8 &hi, f16x8 &lo) 
     }
 }
 
-// max / sum over the 16 lanes of a row group (lanes sharing lane / 16)
-__device__ __forceinline__ float fa_max16(float v) {
-    v = fmaxf(v, lane_xor1(v));
-    v = fmaxf(v, lane_xor2(v));
-    v = fmaxf(v, lane_xor<4>(v));
-    return fmaxf(v, lane_xor8(v));
-}
-__device__ __forceinline__ float fa_sum16(float v) {
-    v += lane_xor1(v);
-    v += lane_xor2(v);
-    v += lane_xor<4>(v);
-    return v + lane_xor8(v);
-}
-
 // K rows for the score MFMA's A operand: lane (li, lg) takes key `key`, dims
 // 8*lg.. of each 32 (16 B per load, one per 32-dim block)
 template <int HD>
@@ -1946,16 +1932,23 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
 // block, query head) with an online softmax, finished in place (divide by the
 // row sum, sigmoid output gate), so no partials or combine pass.
 //
-// Scores S = Q K^T on v_mfma_f32_16x16x32_f16: K is the f16 cache itself, q is
-// split into f16 hi + lo (q = hi + lo to ~2^-22), two MFMAs per tile. P V on
-// the same MFMA with p split into f16 hi + lo against V, which is staged
-// transposed in LDS (an 8 x 8 transpose in registers per thread) so its
-// B fragments are contiguous. Per 64-key tile: K and V^T staged, one wave per
-// 16-token row tile: scores (scaled, masked above the row's position), tile
-// maximum and sum by 16-lane butterflies, the running max/sum/accumulator
+// Scores are computed transposed, S^T = K Q^T, on v_mfma_f32_16x16x32_f16:
+// A = 16 keys straight from the staged f16 K tile, B = 16 tokens' q split
+// into f16 hi + lo (q = hi + lo to ~2^-22), two MFMAs per 32 dims. Lane
+// (li, lg) then holds token li's scores of keys 4lg..4lg+3 of each 16-key
+// block, so a token's tile maximum and sum are in-lane plus two cross-row
+// steps, and its probabilities are already the B operand of O^T += V^T P^T
+// (p split into f16 hi + lo): the 8 keys of MFMA k-slots 8lg..8lg+7 are keys
+// 4lg..4lg+3 of two consecutive 16-key blocks, and V is staged transposed in
+// LDS with its keys in that order (an 8 x 8 transpose in registers per
+// thread), so an A fragment is one 16-byte read. P never goes through LDS.
+// Per 64-key tile: K and V^T staged, one wave per 16-token tile: scores
+// (scaled, masked above the token's position), the running max/sum/output
 // rescaled as the decode partial does per tile (ref.c:416-555 semantics; a
-// fully masked tile leaves a row unchanged), P through LDS into the A layout.
-// MFMA 16x16x32 layout as in the prefill GEMM.
+// fully masked tile leaves a token unchanged), then P V. MFMA 16x16x32 layout
+// as in the prefill GEMM. The output is kept transposed (O^T: lane (li, lg)
+// holds dims 4lg..4lg+3 of each 16-dim tile of token li), so it is stored as
+// float4s.
 // ---------------------------------------------------------------------------
 
 // HW query heads per workgroup (1 or 2, heads sharing one kv head): waves
@@ -1964,6 +1957,7 @@ __global__ void __launch_bounds__(TPB) k_attn_combine(sgk_attn a) {
 template <int HD, int HW>
 __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
     static_assert(HD % 64 == 0 && HD <= 256, "flash prefill takes head_dim 64, 128, 192 or 256");
+    static_assert(FA_TK == 64, "the V^T key order pairs 16-key blocks within 32-key steps");
     constexpr int KLD = HD + 16, NKB = HD / 32, NNT = HD / 16, NSC = FA_TK / 16;
     // K staging: a key row is KC8 16-byte chunks; consecutive threads take
     // consecutive chunks of a row (contiguous LDS stores, coalesced loads),
@@ -1972,7 +1966,6 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
     constexpr int VDC = HD / 8;                  // V staging: dim chunks of 8 (threads 8*vdc + vkg)
     __shared__ __align__(16) uint16_t ks[FA_TK * KLD];
     __shared__ __align__(16) uint16_t vt[HD * FA_PLD];
-    __shared__ __align__(16) uint16_t ps[2][HW * FA_TQ * FA_PLD];
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 15, lg = lane >> 4, tw = wave & 3;
     const uint32_t h = blockIdx.x * HW + (wave >> 2), tb = blockIdx.y, G = a.n_heads / a.n_kv, n_kv = a.n_kv;
     const uint32_t hk = blockIdx.x * HW / G;    // the workgroup's heads share it
@@ -1985,11 +1978,12 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
     const uint32_t S = gridDim.z, sp = blockIdx.z, ntiles = (kend + FA_TK - 1) / FA_TK;
     const uint32_t kbeg = (sp * ntiles / S) * FA_TK, kstop = min(((sp + 1) * ntiles / S) * FA_TK, kend);
 
-    // q fragments of this wave's 16 tokens (A operand: row li, dims 8*lg.. of each 32)
+    // q fragments of this wave's 16 tokens (B operand: column li = token li,
+    // dims 8*lg.. of each 32)
+    const uint32_t zq = z0 + tw * 16 + li;      // this lane's token
     f16x8 qh[NKB], ql[NKB];
     {
-        const uint32_t z = min(z0 + tw * 16 + li, ntok - 1);
-        const float *qr = a.q + (size_t)z * a.q_tok + (size_t)h * a.q_stride;
+        const float *qr = a.q + (size_t)min(zq, ntok - 1) * a.q_tok + (size_t)h * a.q_stride;
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
             const float4 x0 = *(const float4 *)(qr + kb * 32 + lg * 8);
@@ -1998,14 +1992,9 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
             fa_split8(xv, qh[kb], ql[kb]);
         }
     }
-    // this lane's rows in the D layout: 4*lg + e of the wave's tile
-    uint32_t rpos[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) rpos[e] = base + z0 + tw * 16 + lg * 4 + e;
-    float mrun[4], srun[4];
-    f32x4 o[NNT];
-#pragma unroll
-    for (int e = 0; e < 4; e++) { mrun[e] = -INFINITY; srun[e] = 0.0f; }
+    const uint32_t rpos = base + zq;            // keys 0..rpos are visible to token zq
+    float mrun = -INFINITY, srun = 0.0f;
+    f32x4 o[NNT];                               // O^T tile n: dims 16n + 4lg + e of token li
 #pragma unroll
     for (int n = 0; n < NNT; n++) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
@@ -2016,10 +2005,13 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
     const bool k_role = HW == 1 || t < TPB, v_role = HW == 1 || t >= TPB;
     const uint32_t tv = HW == 1 ? t : t - TPB;
     const uint32_t kk = t / KC8, kd = (t % KC8) * 8;        // K staging role: rows kk + u*KPP
-    // V staging role: consecutive threads take consecutive key groups of one
-    // dim chunk, so 8 lanes store 128 contiguous bytes of a V^T row
+    // V staging role: thread (vdc, vkg) transposes keys 8vkg..8vkg+7 of dims
+    // 8vdc..8vdc+7. In a V^T row, key 32m + 16hh + 4q + e sits at column
+    // 32m + 8q + 4hh + e (the P^T fragment's k-slot order), so a thread's
+    // 8 keys land as two 4-key runs, 8 columns apart.
     const uint32_t vkg = tv % (FA_TK / 8), vdc = tv / (FA_TK / 8);
     const bool v_on = v_role && vdc < (uint32_t)VDC;
+    const uint32_t vcol = 32 * (vkg >> 2) + 16 * (vkg & 1) + 4 * ((vkg >> 1) & 1);
     // one register array for both roles: with two heads per workgroup a wave
     // has one role (K in sr[0..KNP), V in sr[0..8)), with one head both
     constexpr int VO = HW == 2 ? 0 : KNP, NSR = HW == 2 ? (KNP > 8 ? KNP : 8) : KNP + 8;
@@ -2042,7 +2034,7 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
     };
     if (kbeg < kstop) stage_load(kbeg);
     for (uint32_t k0 = kbeg; k0 < kstop; k0 += FA_TK) {
-        // stage K [key][dim] and V^T [dim][key]
+        // stage K [key][dim] and V^T [dim][key, in k-slot order]
         if (k_role) {
 #pragma unroll
             for (int u = 0; u < KNP; u++)
@@ -2051,18 +2043,22 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
         if (v_on) {
 #pragma unroll
             for (int dd = 0; dd < 8; dd++) {
-                // half dd of keys 0..7, packed in key order
+                // half dd of keys 0..7, packed in key order: keys 0-3, then 4-7
                 const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-                v4u out;
+                v2u lo2, hi2;
 #pragma unroll
-                for (int w = 0; w < 4; w++)
-                    out[w] = __builtin_amdgcn_perm(sr[VO + 2 * w + 1][dd >> 1], sr[VO + 2 * w][dd >> 1], sel);
-                *(v4u *)&vt[(vdc * 8 + dd) * FA_PLD + vkg * 8] = out;
+                for (int w = 0; w < 2; w++) {
+                    lo2[w] = __builtin_amdgcn_perm(sr[VO + 2 * w + 1][dd >> 1], sr[VO + 2 * w][dd >> 1], sel);
+                    hi2[w] = __builtin_amdgcn_perm(sr[VO + 2 * w + 5][dd >> 1], sr[VO + 2 * w + 4][dd >> 1], sel);
+                }
+                uint16_t *row = &vt[(vdc * 8 + dd) * FA_PLD + vcol];
+                *(v2u *)row = lo2;
+                *(v2u *)(row + 8) = hi2;
             }
         }
         __syncthreads();
         if (k0 + FA_TK < kstop) stage_load(k0 + FA_TK);
-        // scores of this wave's 16 tokens x 64 keys
+        // scores S^T: lane (li, lg) gets token li's scores of keys 16n + 4lg + e
         f32x4 sc[NSC];
 #pragma unroll
         for (int n = 0; n < NSC; n++) sc[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -2071,95 +2067,86 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
 #pragma unroll
             for (int n = 0; n < NSC; n++) {
                 const f16x8 bk = *(const f16x8 *)&ks[(n * 16 + li) * KLD + kb * 32 + lg * 8];
-                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kb], bk, sc[n], 0, 0, 0);
-                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[kb], bk, sc[n], 0, 0, 0);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk, qh[kb], sc[n], 0, 0, 0);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk, ql[kb], sc[n], 0, 0, 0);
             }
         }
-        // online softmax per row (lane holds rows 4*lg+e, key n*16+li)
-        float al[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            float v[NSC], tm = -INFINITY;
-#pragma unroll
-            for (int n = 0; n < NSC; n++) {
-                const uint32_t key = k0 + n * 16 + li;
-                v[n] = key <= rpos[e] ? sc[n][e] * a.scale : -INFINITY;
-                tm = fmaxf(tm, v[n]);
-            }
-            tm = fa_max16(tm);
-            const float mnew = fmaxf(mrun[e], tm);
-            float ps_sum = 0.0f;
-#pragma unroll
-            for (int n = 0; n < NSC; n++) {
-                const uint32_t key = k0 + n * 16 + li;
-                const float pv = key <= rpos[e] ? expf(v[n] - mnew) : 0.0f;
-                sc[n][e] = pv;
-                ps_sum += pv;
-            }
-            ps_sum = fa_sum16(ps_sum);
-            al[e] = (mrun[e] == -INFINITY) ? 0.0f : expf(mrun[e] - mnew);
-            mrun[e] = mnew;
-            srun[e] = srun[e] * al[e] + ps_sum;
-        }
-        // P (hi, lo) into LDS rows of this wave
+        // online softmax of token li over this tile's keys
+        float tm = -INFINITY;
 #pragma unroll
         for (int n = 0; n < NSC; n++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const uint32_t row = wave * 16 + lg * 4 + e, col = n * 16 + li;
-                const _Float16 hp = (_Float16)sc[n][e];
-                ps[0][row * FA_PLD + col] = __builtin_bit_cast(uint16_t, hp);
-                ps[1][row * FA_PLD + col] = __builtin_bit_cast(uint16_t, (_Float16)(sc[n][e] - (float)hp));
+                const uint32_t key = k0 + n * 16 + lg * 4 + e;
+                sc[n][e] = key <= rpos ? sc[n][e] * a.scale : -INFINITY;
+                tm = fmaxf(tm, sc[n][e]);
+            }
+        tm = fmaxf(tm, lane_xor16(tm));
+        tm = fmaxf(tm, lane_xor32(tm));
+        const float mnew = fmaxf(mrun, tm);
+        float ps_sum = 0.0f;
+#pragma unroll
+        for (int n = 0; n < NSC; n++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t key = k0 + n * 16 + lg * 4 + e;
+                const float pv = key <= rpos ? expf(sc[n][e] - mnew) : 0.0f;
+                sc[n][e] = pv;
+                ps_sum += pv;
+            }
+        ps_sum += lane_xor16(ps_sum);
+        ps_sum += lane_xor32(ps_sum);
+        const float al = (mrun == -INFINITY) ? 0.0f : expf(mrun - mnew);
+        mrun = mnew;
+        srun = srun * al + ps_sum;
+#pragma unroll
+        for (int n = 0; n < NNT; n++) o[n] *= al;
+        // O^T += V^T P^T per 32-key step m: k-slots 8lg+e and 8lg+4+e are
+        // keys 32m + 4lg + e and 32m + 16 + 4lg + e
+#pragma unroll
+        for (int m = 0; m < FA_TK / 32; m++) {
+            f16x8 ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float pv = sc[2 * m + (e >> 2)][e & 3];
+                const _Float16 hv = (_Float16)pv;
+                ph[e] = hv;
+                pl[e] = (_Float16)(pv - (float)hv);
             }
 #pragma unroll
-        for (int n = 0; n < NNT; n++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) o[n][e] *= al[e];
-        __syncthreads();
-        // O += P V
-#pragma unroll
-        for (int kb = 0; kb < FA_TK / 32; kb++) {
-            const f16x8 ph = *(const f16x8 *)&ps[0][(wave * 16 + li) * FA_PLD + kb * 32 + lg * 8];
-            const f16x8 pl = *(const f16x8 *)&ps[1][(wave * 16 + li) * FA_PLD + kb * 32 + lg * 8];
-#pragma unroll
             for (int n = 0; n < NNT; n++) {
-                const f16x8 bv = *(const f16x8 *)&vt[(n * 16 + li) * FA_PLD + kb * 32 + lg * 8];
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bv, o[n], 0, 0, 0);
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, bv, o[n], 0, 0, 0);
+                const f16x8 av = *(const f16x8 *)&vt[(n * 16 + li) * FA_PLD + m * 32 + lg * 8];
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, ph, o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pl, o[n], 0, 0, 0);
             }
         }
         __syncthreads();
     }
+    if (zq >= ntok) return;
     if (S > 1) {
         // partials in the decode layout [token][head][split] for k_attn_combine:
         // m the running max, s the running sum, acc the unnormalised output
+        const size_t ph = ((size_t)zq * a.n_heads + h) * S + sp;
+        if (lg == 0) { a.m[ph] = mrun; a.s[ph] = srun; }
+        float *acc = a.acc + ph * HD;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const uint32_t z = z0 + tw * 16 + lg * 4 + e;
-            if (z >= ntok) continue;
-            const size_t ph = ((size_t)z * a.n_heads + h) * S + sp;
-            if (li == 0) { a.m[ph] = mrun[e]; a.s[ph] = srun[e]; }
-            float *acc = a.acc + ph * HD;
-#pragma unroll
-            for (int n = 0; n < NNT; n++) acc[n * 16 + li] = o[n][e];
-        }
+        for (int n = 0; n < NNT; n++) *(f32x4 *)(acc + n * 16 + lg * 4) = o[n];
         return;
     }
-    // finish: o / s, sigmoid gate, store (lane: rows 4*lg+e, dims n*16+li)
+    // finish: o / s, sigmoid gate, store (lane: token li, dims 16n + 4lg + e)
+    float *out = a.out + (size_t)zq * a.out_tok + (size_t)h * HD;
+    const float *gate = a.gate ? a.gate + (size_t)zq * a.q_tok + (size_t)h * a.q_stride : NULL;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const uint32_t z = z0 + tw * 16 + lg * 4 + e;
-        if (z >= ntok) continue;
-        const float S = srun[e];
-        float *out = a.out + (size_t)z * a.out_tok + (size_t)h * HD;
-        const float *gate = a.gate ? a.gate + (size_t)z * a.q_tok + (size_t)h * a.q_stride : NULL;
+    for (int n = 0; n < NNT; n++) {
+        const uint32_t d0 = n * 16 + lg * 4;
+        f32x4 v;
 #pragma unroll
-        for (int n = 0; n < NNT; n++) {
-            const uint32_t dd = n * 16 + li;
-            float v = isnan(S) ? S : (S > 0.0f ? o[n][e] / S : 0.0f);
-            if (gate) v *= sigm(gate[dd]);
-            out[dd] = v;
+        for (int e = 0; e < 4; e++) {
+            float x = isnan(srun) ? srun : (srun > 0.0f ? o[n][e] / srun : 0.0f);
+            if (gate) x *= sigm(gate[d0 + e]);
+            v[e] = x;
         }
+        *(f32x4 *)(out + d0) = v;
     }
 }
 
@@ -2179,6 +2166,8 @@ extern "C" hipError_t sgk_attn_flash(const sgk_attn *a, hipStream_t s) {
     if (!a->steps || !a->n_kv || a->n_heads % a->n_kv || ((uintptr_t)a->q & 15) || a->q_stride % 4 || a->q_tok % 4)
         return hipErrorInvalidValue;
     if (a->hd != 64 && a->hd != 128 && a->hd != 256) return hipErrorInvalidValue;
+    // the output rows (and the split partials) are stored as float4s
+    if (((uintptr_t)a->out & 15) || a->out_tok % 4 || (a->acc && ((uintptr_t)a->acc & 15))) return hipErrorInvalidValue;
     uint32_t S = 1;
     if (a->m && a->s && a->acc && a->max_splits > 1 && a->seq > FA_SPLIT_KEYS)
         S = min(a->max_splits, (a->seq + FA_SPLIT_KEYS - 1) / FA_SPLIT_KEYS);
