@@ -1993,6 +1993,7 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
         }
     }
     const uint32_t rpos = base + zq;            // keys 0..rpos are visible to token zq
+    const float sl2 = a.scale * 1.44269504088896340736f;   // scale * log2(e)
     float mrun = -INFINITY, srun = 0.0f;
     f32x4 o[NNT];                               // O^T tile n: dims 16n + 4lg + e of token li
 #pragma unroll
@@ -2071,14 +2072,16 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
                 sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk, ql[kb], sc[n], 0, 0, 0);
             }
         }
-        // online softmax of token li over this tile's keys
+        // online softmax of token li over this tile's keys, in base 2: the
+        // scores are scaled by scale * log2(e), so p = 2^(s - m) on the
+        // hardware exp2 (the running max m is kept in that domain)
         float tm = -INFINITY;
 #pragma unroll
         for (int n = 0; n < NSC; n++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t key = k0 + n * 16 + lg * 4 + e;
-                sc[n][e] = key <= rpos ? sc[n][e] * a.scale : -INFINITY;
+                sc[n][e] = key <= rpos ? sc[n][e] * sl2 : -INFINITY;
                 tm = fmaxf(tm, sc[n][e]);
             }
         tm = fmaxf(tm, lane_xor16(tm));
@@ -2090,17 +2093,20 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t key = k0 + n * 16 + lg * 4 + e;
-                const float pv = key <= rpos ? expf(sc[n][e] - mnew) : 0.0f;
+                const float pv = key <= rpos ? __builtin_amdgcn_exp2f(sc[n][e] - mnew) : 0.0f;
                 sc[n][e] = pv;
                 ps_sum += pv;
             }
         ps_sum += lane_xor16(ps_sum);
         ps_sum += lane_xor32(ps_sum);
-        const float al = (mrun == -INFINITY) ? 0.0f : expf(mrun - mnew);
+        const float al = (mrun == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mrun - mnew);
         mrun = mnew;
         srun = srun * al + ps_sum;
+        // most tiles at depth leave every running max of the wave unchanged
+        if (__builtin_amdgcn_ballot_w64(al != 1.0f)) {
 #pragma unroll
-        for (int n = 0; n < NNT; n++) o[n] *= al;
+            for (int n = 0; n < NNT; n++) o[n] *= al;
+        }
         // O^T += V^T P^T per 32-key step m: k-slots 8lg+e and 8lg+4+e are
         // keys 32m + 4lg + e and 32m + 16 + 4lg + e
 #pragma unroll
@@ -2127,7 +2133,7 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
         // partials in the decode layout [token][head][split] for k_attn_combine:
         // m the running max, s the running sum, acc the unnormalised output
         const size_t ph = ((size_t)zq * a.n_heads + h) * S + sp;
-        if (lg == 0) { a.m[ph] = mrun; a.s[ph] = srun; }
+        if (lg == 0) { a.m[ph] = mrun * 0.69314718055994530942f; a.s[ph] = srun; }   // the max back in base e
         float *acc = a.acc + ph * HD;
 #pragma unroll
         for (int n = 0; n < NNT; n++) *(f32x4 *)(acc + n * 16 + lg * 4) = o[n];
