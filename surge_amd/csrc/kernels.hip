@@ -2063,13 +2063,21 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
         f32x4 sc[NSC];
 #pragma unroll
         for (int n = 0; n < NSC; n++) sc[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        // K fragments (kb, n) in order i = kb * NSC + n, each requested two
+        // fragments before its MFMAs (a ring of three)
+        {
+            auto kfrag = [&](int i) {
+                return *(const f16x8 *)&ks[((i % NSC) * 16 + li) * KLD + (i / NSC) * 32 + lg * 8];
+            };
+            f16x8 bk[3];
+            bk[0] = kfrag(0);
+            bk[1] = kfrag(1);
 #pragma unroll
-        for (int kb = 0; kb < NKB; kb++) {
-#pragma unroll
-            for (int n = 0; n < NSC; n++) {
-                const f16x8 bk = *(const f16x8 *)&ks[(n * 16 + li) * KLD + kb * 32 + lg * 8];
-                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk, qh[kb], sc[n], 0, 0, 0);
-                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk, ql[kb], sc[n], 0, 0, 0);
+            for (int i = 0; i < NKB * NSC; i++) {
+                if (i + 2 < NKB * NSC) bk[(i + 2) % 3] = kfrag(i + 2);
+                const int kb = i / NSC, n = i % NSC;
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk[i % 3], qh[kb], sc[n], 0, 0, 0);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk[i % 3], ql[kb], sc[n], 0, 0, 0);
             }
         }
         // online softmax of token li over this tile's keys, in base 2: the
@@ -2109,21 +2117,31 @@ __global__ void __launch_bounds__(TPB * HW) k_attn_flash(sgk_attn a) {
         }
         // O^T += V^T P^T per 32-key step m: k-slots 8lg+e and 8lg+4+e are
         // keys 32m + 4lg + e and 32m + 16 + 4lg + e
+        f16x8 ph[FA_TK / 32], pl[FA_TK / 32];
 #pragma unroll
-        for (int m = 0; m < FA_TK / 32; m++) {
-            f16x8 ph, pl;
+        for (int m = 0; m < FA_TK / 32; m++)
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const float pv = sc[2 * m + (e >> 2)][e & 3];
                 const _Float16 hv = (_Float16)pv;
-                ph[e] = hv;
-                pl[e] = (_Float16)(pv - (float)hv);
+                ph[m][e] = hv;
+                pl[m][e] = (_Float16)(pv - (float)hv);
             }
+        // V^T fragments (m, n) in order i = m * NNT + n, each requested two
+        // fragments ahead, as the K fragments
+        {
+            auto vfrag = [&](int i) {
+                return *(const f16x8 *)&vt[((i % NNT) * 16 + li) * FA_PLD + (i / NNT) * 32 + lg * 8];
+            };
+            f16x8 av[3];
+            av[0] = vfrag(0);
+            av[1] = vfrag(1);
 #pragma unroll
-            for (int n = 0; n < NNT; n++) {
-                const f16x8 av = *(const f16x8 *)&vt[(n * 16 + li) * FA_PLD + m * 32 + lg * 8];
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, ph, o[n], 0, 0, 0);
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pl, o[n], 0, 0, 0);
+            for (int i = 0; i < (FA_TK / 32) * NNT; i++) {
+                if (i + 2 < (FA_TK / 32) * NNT) av[(i + 2) % 3] = vfrag(i + 2);
+                const int m = i / NNT, n = i % NNT;
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i % 3], ph[m], o[n], 0, 0, 0);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i % 3], pl[m], o[n], 0, 0, 0);
             }
         }
         __syncthreads();
