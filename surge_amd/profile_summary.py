@@ -285,7 +285,9 @@ def floor(path):
             return "lm_head" if i + 1 < n and short(toks[0][i + 1]["Kernel_Name"]) == "k_argmax" else "input projection"
         for pre, k in (("k_embed", "embedding"), ("k_attn_partial", "attention partial"),
                        ("k_attn_combine", "attention combine"), ("k_gdn_step", "DeltaNet step"),
-                       ("k_gemv_q8<2, 0, 1>", "output projection"), ("k_gemv_q8<2, 1, 2>", "gate/up"),
+                       ("k_gemv_q8<2, 0, 1>", "output projection (attention)"),
+                       ("k_gemv_q8<2, 2, 1>", "output projection (DeltaNet, gated prologue)"),
+                       ("k_gemv_bal<0, 0", "output projection (attention)"), ("k_gemv_q8<2, 1, 2>", "gate/up"),
                        ("k_gemv_bal", "down projection"), ("k_argmax", "argmax"), ("k_step_advance", "step advance")):
             if nm.startswith(pre):
                 return k
