@@ -21,6 +21,7 @@
 //     fast-math); f16 denormal scales decode exactly;
 //   - the GEMV streams 16-byte loads of int8 weights, coalesced along a row,
 //     with the input vector staged once per workgroup in LDS.
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
@@ -1670,8 +1671,13 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
     f32x4 o[NO];
 #pragma unroll
     for (int n = 0; n < NO; n++) o[n] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    // One 64-key round (16 keys per wave). PREF: request the next round's K
+    // and V during this one; the last round requests nothing (nothing would
+    // use it, and the merge below would wait for it), and it is a separate
+    // instance so the loop's wait counts stay exact.
     const uint32_t nr = (t1 - t0 + 63) / 64;
-    for (uint32_t r = 0; r < nr; r++) {
+    auto round = [&](uint32_t r, auto pref) {
+        constexpr bool PREF = decltype(pref)::value;
         const uint32_t base = t0 + r * 64 + wave * 16;
         f32x4 sh = (f32x4){0.f, 0.f, 0.f, 0.f}, sl = sh;
 #pragma unroll
@@ -1680,9 +1686,9 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
             sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk, qh[kb], sh, 0, 0, 0);
             sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(bk, ql[kb], sl, 0, 0, 0);
         }
-        // the next round's K (past the split: clamped, unused), issued here
-        // so that it is in flight during the softmax and P V
-        mf_load_k<HD>(kr, kch, min(base + 64 + li, klast), a.kv_ps, lg);
+        // the next round's K, issued here so that it is in flight during the
+        // softmax and P V
+        if constexpr (PREF) mf_load_k<HD>(kr, kch, min(base + 64 + li, klast), a.kv_ps, lg);
         __builtin_amdgcn_sched_barrier(0);
         float p[4], tm = -INFINITY;
 #pragma unroll
@@ -1725,9 +1731,11 @@ __global__ void __launch_bounds__(TPB) __attribute__((amdgpu_waves_per_eu(2, 2))
             o[m] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, phi, o[m], 0, 0, 0);
             o[m] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, plo, o[m], 0, 0, 0);
         }
-        wv_load_v<HD>(vr, vch, base + 64 + 4 * lg, klast, a.kv_ps, li);
+        if constexpr (PREF) wv_load_v<HD>(vr, vch, base + 64 + 4 * lg, klast, a.kv_ps, li);
         __builtin_amdgcn_sched_barrier(0);
-    }
+    };
+    for (uint32_t r = 0; r + 1 < nr; r++) round(r, std::true_type{});
+    if (nr) round(nr - 1, std::false_type{});
     // merge the waves: lane (li, lg) holds head li's max / sum and O^T rows
     // 4lg+e; each wave scales its rows by its weight exp(m_w - max) once, then
     // the rows are summed in wave order
