@@ -398,7 +398,7 @@ def gemv_shapes(reps=3):
     """Every decode GEMV shape of the 27B model timed per kernel variant:
     average microseconds per launch over back-to-back launches across the
     layers' distinct weight matrices (HIP events on the library stream), the
-    kernel choice forced by SURGE_GEMV and the row-group / long-row overrides.
+    kernel choice forced by SURGE_GEMV and the row-group override.
     One JSON line per (shape, variant)."""
     cfg = S.CFG_27B
     syn = S.Synth(cfg, S.SG_T_Q8_0, seed=0)
