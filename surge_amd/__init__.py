@@ -135,6 +135,7 @@ _SIGS = {
     "sg_gpu_state_fill_synthetic": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32]),
     "sg_gpu_time_read": (SgErr, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.POINTER(C.c_double)]),
     "sg_gpu_time_empty": (SgErr, [C.c_void_p, C.c_uint32, C.c_int, C.POINTER(C.c_double)]),
+    "sgk_device_cus": (C.c_uint32, []),     # kernel-library helper: the current device's CU count
     "sg_gpu_time_floor": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double),
                                   C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
     "sg_gpu_time_gemm": (SgErr, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double)]),

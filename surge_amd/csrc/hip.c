@@ -1398,8 +1398,12 @@ sg_err sg_gpu_state_new(sg_gpu *g, const sg_model *m, uint32_t max_ctx) {
             return errf("gpu: SURGE_ATTN_SPLITK_ONLINE='%s' must be exactly 0 or 1 (default 0)", on_env);
     }
     /* SURGE_SPLITK_GQA_CAP (reference surge.h:1239-1256): plain decimal digits
-     * in [4, 1024], else the state is refused. */
-    uint32_t cap = SGK_MAX_SPLITS;
+     * in [4, 1024], else the state is refused. Unset, the cap is the split
+     * count that gives one partial workgroup per CU (CUs / n_kv_heads, within
+     * [SGK_SPLIT_CAP_MIN, SGK_MAX_SPLITS]). */
+    const uint32_t nkv = g->cfg.n_kv_heads ? g->cfg.n_kv_heads : 1;
+    uint32_t cap = sgk_device_cus() / nkv;
+    cap = cap < SGK_SPLIT_CAP_MIN ? SGK_SPLIT_CAP_MIN : cap > SGK_MAX_SPLITS ? SGK_MAX_SPLITS : cap;
     if (sg_failed(delta_scan_env())) return delta_scan_env();
     const char *cap_env = getenv("SURGE_SPLITK_GQA_CAP");
     if (cap_env && cap_env[0] != '\0') {

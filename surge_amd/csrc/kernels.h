@@ -39,11 +39,12 @@ typedef struct {
 
 /* The split-K decode-attention split count (also evaluated on the device).
  * MI355X policy: about 64 keys per split (one key tile of the partial kernel
- * at head_dim 256) so that n_splits * n_kv_heads reaches a workgroup per CU
- * at 4k context with 4 kv heads, capped at SGK_MAX_SPLITS; never more
- * splits than keys. Past 8k keys a split walks several tiles: 512
- * workgroups (two per CU, which is what the partial's registers allow)
- * with a 128-way combine beat 1024 workgroups with a 256-way one. */
+ * at head_dim 256), capped; never more splits than keys. A decode state's
+ * cap defaults to one partial workgroup per CU (n_splits * n_kv_heads <=
+ * CUs, at most SGK_MAX_SPLITS): on the 27B shape (4 kv heads) 64 splits
+ * beat 128 (two workgroups per CU) at every depth measured from 8k to 262k
+ * keys, and a count just past one per CU (65 at 4097 keys) cost a second
+ * pass. The state-free count (sgk_n_splits) keeps the SGK_MAX_SPLITS cap. */
 #define SGK_MAX_SPLITS 128u
 #define SGK_KEYS_PER_SPLIT 64u
 /* A state may lower or raise the cap (SURGE_SPLITK_GQA_CAP) within [4, 1024]. */

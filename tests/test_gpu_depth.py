@@ -31,12 +31,19 @@ def rel(got, want):
     return float(np.abs(got.astype(np.float64) - want).max() / np.abs(want).max())
 
 
-@pytest.mark.parametrize("depth", [32768, 131072])
-def test_decode_at_depth_vs_oracle(gpu, depth):
+# the default cap (one partial workgroup per CU: 256 CUs / 4 kv heads = 64
+# splits on an MI355X) at 32768 keys, and the cap raised to 128 splits (two
+# workgroups per CU) at 131072
+@pytest.mark.parametrize("depth,cap", [(32768, None), (131072, "128")])
+def test_decode_at_depth_vs_oracle(gpu, depth, cap, monkeypatch):
     syn = S.Synth(DEEP, S.SG_T_Q8_0, seed=51)
     gpu.load_model(syn.model)
+    if cap:
+        monkeypatch.setenv("SURGE_SPLITK_GQA_CAP", cap)
+    else:
+        monkeypatch.delenv("SURGE_SPLITK_GQA_CAP", raising=False)
     gpu.state_new(depth + 8)
-    assert gpu.n_splits_at(depth + 1) == 128
+    assert gpu.n_splits_at(depth + 1) == (int(cap) if cap else min(128, S.lib().sgk_device_cus() // DEEP["n_kv_heads"]))
     gpu.fill_synthetic(depth, seed=7)
     rm = O.RefModel(O.oracle(), syn.model, depth + 8, kv_f16=True)
     rm.fill_synthetic(depth, seed=7)
