@@ -242,7 +242,9 @@ sg_err sg_gpu_run_attn_prefill(sg_gpu *g, void *q, void *k, void *v, void *out,
  *                            the dispatches as the online arm (same kernel:
  *                            the partial is the online form) and the GQA
  *                            predicate then answers false;
- *   SURGE_SPLITK_GQA_CAP     the split cap, plain digits in [4, 1024].
+ *   SURGE_SPLITK_GQA_CAP     the split cap, plain digits in [4, 1024]
+ *                            (unset: one partial workgroup per CU,
+ *                            CUs / n_kv_heads within [4, 128]).
  * The arm is fixed per state: the MI355X policy has no occupancy floor, so
  * `seq` does not change the answers. The counters count what sg_gpu_forward
  * and sg_gpu_decode_greedy encoded since the last sg_gpu_state_new, one per
