@@ -812,7 +812,8 @@ def test_rmsnorm_gated_chunk(gpu):
 
 
 ATTN_CHUNK_CASES = [(24, 4, 256, 64, 1000, 150), (8, 2, 256, 64, 0, 130), (12, 4, 128, 32, 300, 70),
-                    (16, 4, 128, 128, 600, 64), (8, 2, 64, 32, 200, 70)]
+                    (16, 4, 128, 128, 600, 64), (8, 2, 64, 32, 200, 70),
+                    (12, 4, 128, 32, 1100, 70), (8, 2, 64, 32, 1100, 40)]
 
 
 @pytest.mark.parametrize("nh,nkv,hd,rd,base,n", ATTN_CHUNK_CASES,
@@ -827,7 +828,8 @@ def test_attn_prefill_chunk_vs_oracle(gpu, nh, nkv, hd, rd, base, n):
     24q/4kv/256 with rope 64 deep enough for a 3-way key split, the 2B's
     8q/2kv/256 from position 0, an odd GQA group (12/4, one query head per
     workgroup) at head_dim 128 / rope 32, a full rope, and head_dim 64 with
-    rope 32 (8q/2kv). Outputs within
+    rope 32 (8q/2kv); the odd group and head_dim 64 again deep enough for a
+    3-way key split. Outputs within
     1e-3; V stored bit-exact (both round the same f32); K within one f16
     ulp of the oracle's (its f32 before rounding differs in the last bits);
     the keys before the chunk untouched."""
