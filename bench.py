@@ -569,6 +569,7 @@ def main():
         sec = secondary_2b(cpu=not a.no_cpu)
         log(f"2B shape: {sec['value']} tok/s"
             + (f", ref.c {sec['cpu_baseline']['value']} tok/s on one core" if sec["cpu_baseline"] else ""))
+    if cpu:
         log(f"cpu baseline: {cpu['sample']}")
     syn.close()
     line = {

@@ -349,6 +349,25 @@ __device__ __forceinline__ void gemv_fma(float *acc, const gemv_chunk<R> &ch, co
     for (int r = 0; r < R; r++) acc[r] = fmaf(h2f(ch.d[r]), dot16(ch.q[r], a0, a1, a2, a3), acc[r]);
 }
 
+// The end of a row group: each lane's partial sums of the R rows summed over
+// the wave, scaled by post, and stored by the epilogue.
+template <int R, int EPI>
+__device__ __forceinline__ void gemv_finish(const sgk_gemv &a, float *acc, uint32_t r0, uint32_t lane, float post) {
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]) * post;
+    if (EPI == SGK_EPI_SWIGLU) {
+        // rows come in (gate, up) pairs: y[i] = silu(gate_i) * up_i
+#pragma unroll
+        for (int p = 0; p < R / 2; p++)
+            if (lane == (uint32_t)p && r0 + 2 * p + 1 < a.rows)
+                a.y[(r0 >> 1) + p] = silu(acc[2 * p]) * acc[2 * p + 1];
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (lane == (uint32_t)r && r0 + r < a.rows) gemv_store<EPI>(a, r0 + r, acc[r]);
+    }
+}
+
 // One row group of R rows: every chunk of the rows, two chunks per step, the
 // first chunk optionally already loaded (pre). post scales each row sum. CH:
 // x staged in the chunked layout (xs4_at<true>), else linear.
@@ -376,19 +395,7 @@ __device__ __forceinline__ void gemv_group(const sgk_gemv &a, const float *xs, u
         gemv_load<R>(ca, a.qs, a.d, r0, a.rows, cols, c);
         gemv_fma<R, CH>(acc, ca, xs, c);
     }
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]) * post;
-    if (EPI == SGK_EPI_SWIGLU) {
-        // rows come in (gate, up) pairs: y[i] = silu(gate_i) * up_i
-#pragma unroll
-        for (int p = 0; p < R / 2; p++)
-            if (lane == (uint32_t)p && r0 + 2 * p + 1 < a.rows)
-                a.y[(r0 >> 1) + p] = silu(acc[2 * p]) * acc[2 * p + 1];
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; r++)
-            if (lane == (uint32_t)r && r0 + r < a.rows) gemv_store<EPI>(a, r0 + r, acc[r]);
-    }
+    gemv_finish<R, EPI>(a, acc, r0, lane, post);
 }
 
 template <int R, int PRO, int EPI>
@@ -409,8 +416,129 @@ __global__ void __launch_bounds__(TPB) k_gemv_q8(sgk_gemv a) {
     for (g += gstride; g < ngroups; g += gstride) gemv_group<R, EPI, false, GEMV_CH(PRO)>(a, xs, g, lane, nullptr, post);
 }
 
+// ---------------------------------------------------------------------------
+// Q8_0 GEMV with a two-step load ring (the default behind the RMSNorm and
+// gated prologues). The same row groups, lanes, chunks and summation order as
+// k_gemv_q8 (so the same bits), but a wave walks its whole sequence of steps
+// (row group g, chunks 128s + lane and 128s + 64 + lane) with two step
+// buffers: while one step's FMAs run, the next step's chunks are already in
+// flight, and a buffer is refilled two steps ahead as soon as its FMAs are
+// done. k_gemv_q8 requests a step and waits for all of it, so its FMAs and
+// the row-group ends ran with nothing of the wave in flight. Both buffers
+// are requested before the input vector is staged.
+// The wave index is read as a uniform value, so the step walk is scalar
+// control flow with one exit; the compiler then tracks which loads are in
+// flight exactly (a per-lane loop, or a second exit, made it wait for the
+// other buffer too). The loads are unconditional buffer loads: a step past
+// the wave's last one, a chunk past the row's end and a row past the matrix
+// take an offset past the descriptor's range, which reads zeros without a
+// memory request (clamped addresses instead re-read up to two steps per
+// wave, 17 MB per gate/up launch).
+// ---------------------------------------------------------------------------
+#define RING_OOB 0x80000000u
+struct ring_src {
+    __amdgpu_buffer_rsrc_t q, d;
+};
 
+// A step's two chunks of the group's R rows; for the residual-add epilogue
+// also y[r0 + lane] (lanes < R), read with the step's chunks so that the
+// group's end does not wait on a load of its own (a read there would wait
+// for every request in flight, the other buffer's too).
+template <int R>
+struct gemv_step {
+    gemv_chunk<R> x, y;
+    float yr;
+};
 
+template <int R>
+__device__ __forceinline__ void ring_chunk(const sgk_gemv &a, const ring_src &rs, gemv_chunk<R> &ch, uint32_t r0,
+                                           bool live, uint32_t c) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const bool ok = live && r0 + r < a.rows && c < (a.cols >> 4);
+        const uint32_t qo = ok ? (r0 + r) * a.cols + 16 * c : RING_OOB;
+        const uint32_t dof = ok ? ((r0 + r) * (a.cols >> 5) + (c >> 1)) * 2 : RING_OOB;
+        const v4u v = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs.q, (int)qo, 0, 2));   // nt
+        ch.q[r] = make_uint4(v.x, v.y, v.z, v.w);
+        ch.d[r] = __builtin_amdgcn_raw_buffer_load_b16(rs.d, (int)dof, 0, 0);
+    }
+}
+
+template <int R, int EPI>
+__device__ __forceinline__ void ring_load(const sgk_gemv &a, const ring_src &rs, gemv_step<R> &b, uint32_t g,
+                                          uint32_t s, uint32_t ngroups, uint32_t lane) {
+    const bool live = g < ngroups;
+    const uint32_t r0 = g * R;
+    ring_chunk<R>(a, rs, b.x, r0, live, 128 * s + lane);
+    ring_chunk<R>(a, rs, b.y, r0, live, 128 * s + 64 + lane);
+    if (EPI == SGK_EPI_ADD) b.yr = a.y[min(r0 + min(lane, (uint32_t)R - 1), a.rows - 1)];
+}
+
+template <int R, int EPI, bool CH>
+__device__ __forceinline__ void ring_fma(const sgk_gemv &a, const float *xs, const gemv_step<R> &b, float *acc,
+                                         uint32_t g, uint32_t s, uint32_t spg, uint32_t lane, float post) {
+    const uint32_t nch = a.cols >> 4, c = 128 * s + lane;
+    if (c < nch) gemv_fma<R, CH>(acc, b.x, xs, c);
+    if (c + 64 < nch) gemv_fma<R, CH>(acc, b.y, xs, c + 64);
+    if (s == spg - 1) {
+        if (EPI == SGK_EPI_ADD) {                   // y += row sum, y as read with this step
+            const uint32_t r0 = g * R;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                acc[r] = wave_sum(acc[r]) * post;
+                if (lane == (uint32_t)r && r0 + r < a.rows) a.y[r0 + r] = b.yr + acc[r];
+            }
+        } else {
+            gemv_finish<R, EPI>(a, acc, g * R, lane, post);
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    }
+}
+
+template <int R, int PRO, int EPI>
+__global__ void __launch_bounds__(TPB) k_gemv_ring(sgk_gemv a) {
+    extern __shared__ float xs[];
+    constexpr bool CH = GEMV_CH(PRO);
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nch = a.cols >> 4, spg = (nch + 127) / 128;
+    // Rounds of one row group per wave over consecutive groups, a
+    // workgroup's waves on adjacent groups: all waves stream one compact
+    // window of rows at a time. Measured over a 27B token against this
+    // order: contiguous ranges per wave 6% slower, and a round's groups
+    // dealt wave-major (wave j of workgroup b at j * blocks + b, which spreads
+    // a partial last round over the CUs) 3% slower.
+    const uint32_t ngroups = (a.rows + R - 1) / R, gstride = gridDim.x * (TPB / 64);
+    uint32_t g = blockIdx.x * (TPB / 64) + wave, s = 0;
+    uint32_t gb = g, sb = s;                        // buffer b's step: one after buffer a's
+    if (++sb == spg) { sb = 0; gb += gstride; }
+    ring_src rs;
+    rs.q = __builtin_amdgcn_make_buffer_rsrc((void *)a.qs, (short)0, (int)(a.rows * a.cols), 0x00020000);
+    rs.d = __builtin_amdgcn_make_buffer_rsrc((void *)a.d, (short)0, (int)(a.rows * (a.cols >> 5) * 2), 0x00020000);
+    xstage<PRO, TPB, XK> st;
+    stage_issue<PRO, TPB, XK>(a, st);
+    gemv_step<R> ba, bb;
+    ring_load<R, EPI>(a, rs, ba, g, s, ngroups, lane);
+    __builtin_amdgcn_sched_barrier(0);              // keep a's requests ahead of b's
+    ring_load<R, EPI>(a, rs, bb, gb, sb, ngroups, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    const float post = stage_finish<PRO, TPB, XK, CH>(a, st, xs);
+    if (g >= ngroups) return;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    while (true) {
+        ring_fma<R, EPI, CH>(a, xs, ba, acc, g, s, spg, lane, post);
+        g = gb; s = sb;                             // a's next step: one after b's
+        if (++s == spg) { s = 0; g += gstride; }
+        ring_load<R, EPI>(a, rs, ba, g, s, ngroups, lane);
+        if (gb < ngroups) ring_fma<R, EPI, CH>(a, xs, bb, acc, gb, sb, spg, lane, post);
+        gb = g; sb = s;                             // b's next step: one after a's
+        if (++sb == spg) { sb = 0; gb += gstride; }
+        ring_load<R, EPI>(a, rs, bb, gb, sb, ngroups, lane);
+        if (g >= ngroups) break;
+    }
+}
 
 // f32-weight GEMV (small test models only): one wave per row pair.
 template <int PRO, int EPI>
@@ -573,6 +701,33 @@ static hipError_t launch_q8(const sgk_gemv &a, size_t lds, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Launch k_gemv_ring<2,...>: two workgroups per CU (8 waves, each with two
+// steps in flight), fewer if there are fewer row groups than waves. Measured
+// on MI355X over the 27B shapes (one workgroup per CU, 1.5, 2, 2.5 and 3):
+// two per CU was fastest for every shape it takes; three, with the ring, put
+// more in flight than the memory system serves faster.
+template <int PRO, int EPI>
+static hipError_t launch_ring(const sgk_gemv &a, size_t lds, hipStream_t s) {
+    auto kern = k_gemv_ring<2, PRO, EPI>;
+    hipError_t e = allow_lds((const void *)kern, lds);
+    if (e != hipSuccess) return e;
+    static size_t seen_lds[8];
+    static uint32_t seen_per[8];
+    static int nseen = 0;
+    uint32_t per = 0;
+    for (int i = 0; i < nseen; i++)
+        if (seen_lds[i] == lds) per = seen_per[i];
+    if (!per) {
+        per = resident_per_cu(kern, TPB, lds);
+        if (nseen < 8) { seen_lds[nseen] = lds; seen_per[nseen] = per; nseen++; }
+    }
+    const uint32_t groups = (a.rows + 1) / 2, wpb = TPB / 64;
+    uint32_t blocks = (uint32_t)device_cus() * (per < 2 ? per : 2u);
+    if ((groups + wpb - 1) / wpb < blocks) blocks = (groups + wpb - 1) / wpb;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(TPB), lds, s, a);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Balanced Q8_0 GEMV (the default for Q8_0 matrices whose width is a multiple
 // of 1024). One BT-thread workgroup per CU. Workgroup b owns the row groups
@@ -704,6 +859,20 @@ static int gemv_bal_on(uint32_t cols) {
     if (e && e[0] == 'b' && e[1] == 'a' && e[2] == 'l' && !e[3]) return 1;
     return cols > 8192 ? 2 : 0;
 }
+// Whether a Q8_0 GEMV with a prologue (RMSNorm or gated) that k_gemv_bal
+// does not take runs the ring form k_gemv_ring (the default) or the
+// row-group form k_gemv_q8 (SURGE_GEMV=q8, or the tune_r / tune_blocks
+// measurement overrides). Without a prologue k_gemv_q8 stays. The ring there
+// ran the 2B shape's output and down projections (4-13 MB) 4% faster over a
+// token, but it is not built: with those instantiations in the code object
+// the 27B decode ran 0.5% slower on the same kernels (also with them
+// present and never launched), a code-layout effect on the headline shape.
+// The ring also loses to k_gemv_bal on the 17408-column down projection
+// (20.3-21.7 against 18.7-19.4 us).
+static int gemv_ring_on() {
+    const char *e = getenv("SURGE_GEMV");
+    return !(e && e[0] == 'q' && e[1] == '8' && !e[2]);
+}
 
 template <int PRO, int EPI>
 static hipError_t launch_bal(const sgk_gemv &a, hipStream_t s) {
@@ -735,6 +904,9 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         bal_lds_floats(a->rows, a->cols, (uint32_t)device_cus()) * 4 <= 160 * 1024)
         return launch_bal<PRO == SGK_PRO_RMS ? SGK_PRO_RMS : SGK_PRO_NONE, EPI>(*a, s);
     const size_t lds = GEMV_CH(PRO) ? (size_t)xs_ch_floats(a->cols) * 4 : (size_t)a->cols * 4;
+    if constexpr (PRO != SGK_PRO_NONE)
+        if (!a->tune_r && !a->tune_blocks && gemv_ring_on() && (uint64_t)a->rows * a->cols < RING_OOB)
+            return launch_ring<PRO, EPI>(*a, lds, s);
     const int R = EPI == SGK_EPI_SWIGLU ? 2 : (a->tune_r == 1 ? 1 : a->tune_r == 4 ? 4 : 2);
     if (R == 4) return launch_q8<4, PRO, EPI>(*a, lds, s);
     if (R == 1) return launch_q8<1, PRO, (EPI == SGK_EPI_SWIGLU ? SGK_EPI_STORE : EPI)>(*a, lds, s);

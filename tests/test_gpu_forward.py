@@ -156,7 +156,7 @@ LONG_FFN = dict(SMALL, n_layers=4, ffn_hidden=9216)
 def test_long_ffn_down_projection_per_position_vs_oracle(gpu):
     """An FFN wider than 8192 (9216): the down projection runs the balanced
     interleaved GEMV with its residual-add epilogue (k_gemv_bal<0, 1, true>,
-    the 27B's down-projection form; gate/up stays on k_gemv_q8 at 256
+    the 27B's down-projection form; gate/up stays on the ring GEMV at 256
     columns). Logits within 1e-3 of the oracle at every position of a
     48-token walk, same argmax."""
     syn = S.Synth(LONG_FFN, S.SG_T_Q8_0, seed=17)
@@ -174,6 +174,40 @@ def test_long_ffn_down_projection_per_position_vs_oracle(gpu):
     gpu.state_new(8)
     syn.close()
     print(f"[long ffn] worst relative gap {worst:.3e}", flush=True)
+    assert worst < 1e-3, worst
+
+
+RAGGED = dict(SMALL, n_layers=4, hidden=2080, ffn_hidden=1056, vocab=1001)
+
+
+def test_ring_gemv_same_bits_as_row_group_gemv(gpu, monkeypatch):
+    """The ring GEMV (k_gemv_ring: the default behind the RMSNorm and gated
+    prologues) sums the same chunks in the same order as the row-group GEMV
+    (k_gemv_q8, forced by SURGE_GEMV=q8), so the logits agree bit for bit.
+    Hidden 2080 is 130 chunks per row: each row group takes a second step of
+    two chunks, the rest of that step reading past the row (zeros, no
+    request). The odd vocab leaves the lm_head a last row group of one row;
+    the DeltaNet output projection (gated prologue, residual add) has 384
+    columns, 24 chunks, so most lanes of its one step read past the row.
+    12 positions; the default also stays within 1e-3 of the oracle."""
+    syn = S.Synth(RAGGED, S.SG_T_Q8_0, seed=23)
+    ids = np.random.default_rng(23).integers(0, RAGGED["vocab"], 12).tolist()
+    out = {}
+    for mode in ("q8", "default"):
+        if mode == "q8":
+            monkeypatch.setenv("SURGE_GEMV", "q8")
+        else:
+            monkeypatch.delenv("SURGE_GEMV", raising=False)
+        gpu.load_model(syn.model)
+        gpu.state_new(16)
+        out[mode] = np.stack([gpu.forward(t, p) for p, t in enumerate(ids)])
+    gpu.state_new(8)
+    rm = O.RefModel(O.oracle(), syn.model, 16, kv_f16=True)
+    worst = max(rel(out["default"][p], rm.forward(t, p)) for p, t in enumerate(ids))
+    rm.close()
+    syn.close()
+    print(f"[ring gemv] worst relative gap to the oracle {worst:.3e}", flush=True)
+    assert np.array_equal(out["q8"], out["default"])
     assert worst < 1e-3, worst
 
 
