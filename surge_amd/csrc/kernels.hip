@@ -743,8 +743,8 @@ static hipError_t launch_ring(const sgk_gemv &a, size_t lds, hipStream_t s) {
 // other waves' slots of that group are 0); the workgroup then adds a group's
 // slots in wave order (adding zeros is exact: a group one wave did whole
 // keeps k_gemv_q8's bits) and applies the prologue's factor and the
-// epilogue. EPI_ADD may update y in place: a workgroup stages its rows of y
-// before it writes them.
+// epilogue. EPI_ADD may update y in place: a workgroup reads its rows of y
+// (into registers, one row per thread) before it writes them.
 // ---------------------------------------------------------------------------
 #define BT 768
 #define BW (BT / 64)
@@ -777,21 +777,26 @@ __global__ void __launch_bounds__(BT) k_gemv_bal(sgk_gemv a) {
         gemv_load<2>(ch, a.qs, a.d, (g0 + kk * gs) * 2, a.rows, a.cols, lane + 64 * j);
     };
     auto next = [&](uint32_t &k, uint32_t &j) { if (++j == nsteps) { j = 0; k++; } };
+    // x is requested first and the ring after it: the loads return in order,
+    // so x requested behind the ring's BP steps (96 KB per CU) waited for all
+    // of them. For EPI_ADD thread t < 2 * ng holds y of the workgroup's row t
+    // in a register, requested with x (the launcher keeps 2 * ng <= BT): a
+    // read into LDS here made the staging wait for every request in flight.
+    constexpr int K = PRO == SGK_PRO_RMS ? BXK_RMS : BXK_NONE;
+    xstage<PRO, BT, K> st;
+    stage_issue<PRO, BT, K>(a, st);
     uint32_t ki = s0 / nsteps, ji = s0 % nsteps;
 #pragma unroll
     for (int u = 0; u < BP; u++) {          // the first steps (re-reads past the range are discarded)
         issue(ring[u], ki, ji);
         next(ki, ji);
     }
-    constexpr int K = PRO == SGK_PRO_RMS ? BXK_RMS : BXK_NONE;
-    xstage<PRO, BT, K> st;
-    stage_issue<PRO, BT, K>(a, st);
+    float yv = 0.0f;
+    if (EPI == SGK_EPI_ADD) {
+        const uint32_t i = min(t, 2 * ng - 1), row = (g0 + (i >> 1) * gs) * 2 + (i & 1);
+        yv = a.y[min(row, a.rows - 1)];
+    }
     for (uint32_t i = t; i < ng * BW * 2; i += BT) part[i] = 0.0f;
-    if (EPI == SGK_EPI_ADD)
-        for (uint32_t i = t; i < ng * 2; i += BT) {
-            const uint32_t row = (g0 + (i >> 1) * gs) * 2 + (i & 1);
-            res[i] = row < a.rows ? a.y[row] : 0.0f;
-        }
     const float post = stage_finish<PRO, BT, K, true>(a, st, xs);
     if (ns) {
         float acc[2] = {0.0f, 0.0f};
@@ -829,6 +834,7 @@ __global__ void __launch_bounds__(BT) k_gemv_bal(sgk_gemv a) {
         for (int u = 0; u < BP; u++)
             if (i + BP + u < ns) consume(u, i + BP + u);
     }
+    if (EPI == SGK_EPI_ADD && t < ng * 2) res[t] = yv;
     __syncthreads();
     for (uint32_t i = t; i < ng * 2; i += BT) {
         const uint32_t k = i >> 1, r = i & 1, row = (g0 + k * gs) * 2 + r;
@@ -900,6 +906,7 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         return hipGetLastError();
     }
     if (PRO != SGK_PRO_GATED && gemv_bal_on(a->cols) && !a->tune_r && !a->tune_blocks && a->cols % 1024 == 0 &&
+        2 * (((a->rows + 1) / 2 + (uint32_t)device_cus() - 1) / (uint32_t)device_cus()) <= BT &&
         a->cols <= (PRO == SGK_PRO_RMS ? SGK_BAL_MAX_RMS_COLS : SGK_BAL_MAX_COLS) &&
         bal_lds_floats(a->rows, a->cols, (uint32_t)device_cus()) * 4 <= 160 * 1024)
         return launch_bal<PRO == SGK_PRO_RMS ? SGK_PRO_RMS : SGK_PRO_NONE, EPI>(*a, s);
