@@ -738,7 +738,7 @@ static hipError_t launch_ring(const sgk_gemv &a, size_t lds, hipStream_t s) {
 // A wave streams a step as k_gemv_q8<2> streams a chunk pair (lane l: chunk
 // l + 64 j of both rows, f32 FMA per chunk) and keeps BP steps in flight in
 // a register ring indexed statically; all BP of the first steps are
-// requested before x is staged, so HBM streams while x arrives. Each wave
+// requested (after x) before x is staged, so HBM streams while x arrives. Each wave
 // writes one wave-reduced partial per row group it touched into LDS (the
 // other waves' slots of that group are 0); the workgroup then adds a group's
 // slots in wave order (adding zeros is exact: a group one wave did whole
@@ -771,25 +771,35 @@ __global__ void __launch_bounds__(BT) k_gemv_bal(sgk_gemv a) {
     if (!ng) return;
     const uint32_t T = ng * nsteps, s0 = w * T / BW, ns = (w + 1) * T / BW - s0;
     float *xs = lds, *part = lds + xs_ch_floats(a.cols), *res = part + ng * BW * 2;
+    // The ring's loads are range-checked buffer loads (as k_gemv_ring's): a
+    // step past the wave's range reads zeros without a memory request, so
+    // every slot is refilled unconditionally and the walk below is one loop
+    // with one exit, whose waits the compiler counts exactly (a steady loop
+    // plus peeled tails made it copy the ring into other registers at the
+    // loop's entry, which waited for all BP steps).
+    ring_src rs;
+    rs.q = __builtin_amdgcn_make_buffer_rsrc((void *)a.qs, (short)0, (int)(a.rows * a.cols), 0x00020000);
+    rs.d = __builtin_amdgcn_make_buffer_rsrc((void *)a.d, (short)0, (int)(a.rows * (a.cols >> 5) * 2), 0x00020000);
     gemv_chunk<2> ring[BP];
-    auto issue = [&](gemv_chunk<2> &ch, uint32_t k, uint32_t j) {
-        const uint32_t kk = k < ng ? k : ng - 1;
-        gemv_load<2>(ch, a.qs, a.d, (g0 + kk * gs) * 2, a.rows, a.cols, lane + 64 * j);
+    auto issue = [&](gemv_chunk<2> &ch, uint32_t k, uint32_t j, bool live) {
+        ring_chunk<2>(a, rs, ch, (g0 + k * gs) * 2, live, lane + 64 * j);
     };
     auto next = [&](uint32_t &k, uint32_t &j) { if (++j == nsteps) { j = 0; k++; } };
     // x is requested first and the ring after it: the loads return in order,
     // so x requested behind the ring's BP steps (96 KB per CU) waited for all
     // of them. For EPI_ADD thread t < 2 * ng holds y of the workgroup's row t
-    // in a register, requested with x (the launcher keeps 2 * ng <= BT): a
-    // read into LDS here made the staging wait for every request in flight.
+    // in a register, requested with the ring (the launcher keeps 2 * ng <=
+    // BT): a read into LDS here made the staging wait for every request in
+    // flight.
     constexpr int K = PRO == SGK_PRO_RMS ? BXK_RMS : BXK_NONE;
     xstage<PRO, BT, K> st;
     stage_issue<PRO, BT, K>(a, st);
     uint32_t ki = s0 / nsteps, ji = s0 % nsteps;
 #pragma unroll
-    for (int u = 0; u < BP; u++) {          // the first steps (re-reads past the range are discarded)
-        issue(ring[u], ki, ji);
+    for (int u = 0; u < BP; u++) {          // the first steps, in slot order
+        issue(ring[u], ki, ji, (uint32_t)u < ns);
         next(ki, ji);
+        __builtin_amdgcn_sched_barrier(0);
     }
     float yv = 0.0f;
     if (EPI == SGK_EPI_ADD) {
@@ -798,41 +808,25 @@ __global__ void __launch_bounds__(BT) k_gemv_bal(sgk_gemv a) {
     }
     for (uint32_t i = t; i < ng * BW * 2; i += BT) part[i] = 0.0f;
     const float post = stage_finish<PRO, BT, K, true>(a, st, xs);
-    if (ns) {
-        float acc[2] = {0.0f, 0.0f};
-        uint32_t kc = s0 / nsteps, jc = s0 % nsteps;
-        auto consume = [&](int u, uint32_t i) {
-            gemv_fma<2, true>(acc, ring[u], xs, lane + 64 * jc);
-            if (jc == nsteps - 1 || i == ns - 1) {
-                acc[0] = wave_sum(acc[0]);
-                acc[1] = wave_sum(acc[1]);
-                if (lane < 2) part[(kc * BW + w) * 2 + lane] = lane == 0 ? acc[0] : acc[1];
-                acc[0] = acc[1] = 0.0f;
-            }
-            next(kc, jc);
-        };
-        uint32_t i = 0;
-        for (; i + 2 * BP <= ns; i += BP) {
-#pragma unroll
-            for (int u = 0; u < BP; u++) {
-                consume(u, i + u);
-                issue(ring[u], ki, ji);
-                next(ki, ji);
-            }
+    float acc[2] = {0.0f, 0.0f};
+    uint32_t kc = s0 / nsteps, jc = s0 % nsteps;
+    auto consume = [&](int u, uint32_t i) {
+        gemv_fma<2, true>(acc, ring[u], xs, lane + 64 * jc);
+        if (jc == nsteps - 1 || i == ns - 1) {
+            acc[0] = wave_sum(acc[0]);
+            acc[1] = wave_sum(acc[1]);
+            if (lane < 2) part[(kc * BW + w) * 2 + lane] = lane == 0 ? acc[0] : acc[1];
+            acc[0] = acc[1] = 0.0f;
         }
+        next(kc, jc);
+    };
+    for (uint32_t i = 0; i < ns; i += BP) {
 #pragma unroll
         for (int u = 0; u < BP; u++) {
-            if (i + u < ns) {
-                consume(u, i + u);
-                if (i + u + BP < ns) {
-                    issue(ring[u], ki, ji);
-                    next(ki, ji);
-                }
-            }
+            if (i + u < ns) consume(u, i + u);
+            issue(ring[u], ki, ji, i + u + BP < ns);
+            next(ki, ji);
         }
-#pragma unroll
-        for (int u = 0; u < BP; u++)
-            if (i + BP + u < ns) consume(u, i + BP + u);
     }
     if (EPI == SGK_EPI_ADD && t < ng * 2) res[t] = yv;
     __syncthreads();
@@ -907,6 +901,7 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
     }
     if (PRO != SGK_PRO_GATED && gemv_bal_on(a->cols) && !a->tune_r && !a->tune_blocks && a->cols % 1024 == 0 &&
         2 * (((a->rows + 1) / 2 + (uint32_t)device_cus() - 1) / (uint32_t)device_cus()) <= BT &&
+        (uint64_t)a->rows * a->cols < RING_OOB &&
         a->cols <= (PRO == SGK_PRO_RMS ? SGK_BAL_MAX_RMS_COLS : SGK_BAL_MAX_COLS) &&
         bal_lds_floats(a->rows, a->cols, (uint32_t)device_cus()) * 4 <= 160 * 1024)
         return launch_bal<PRO == SGK_PRO_RMS ? SGK_PRO_RMS : SGK_PRO_NONE, EPI>(*a, s);
