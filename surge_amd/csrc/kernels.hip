@@ -2575,17 +2575,27 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
         return 2 * key_dim + h * dv + jlo + (e - 2 * dk);
     };
     // All four ring slots are loaded (their addresses need no position), the
-    // taps' slots picked once the position is in.
-    float cx, cw[4], rs[4];
-    auto conv_loads = [&](uint32_t c) {
+    // taps' slots picked once the position is in. A thread's first two
+    // channels (t and t + GDN_TPB) are both requested here: the 27B's 288
+    // channels per block gave 32 threads a second channel whose loads, issued
+    // after the first one's arithmetic, were a memory round trip of their own
+    // in front of the barrier.
+    float4 cw0, rs0, cw1, rs1;
+    float cx0, cx1;
+    auto conv_loads = [&](float &cx, float4 &cw, float4 &rs, uint32_t c) {
         cx = a.in[c];
-#pragma unroll
-        for (uint32_t jj = 0; jj < 4; jj++) cw[jj] = a.conv_w[(size_t)c * a.ksize + min(jj, keep)];
-#pragma unroll
-        for (uint32_t sl = 0; sl < 4; sl++) rs[sl] = a.ring[(size_t)sl * cd + c];
+        cw.x = a.conv_w[(size_t)c * a.ksize];
+        cw.y = a.conv_w[(size_t)c * a.ksize + min(1u, keep)];
+        cw.z = a.conv_w[(size_t)c * a.ksize + min(2u, keep)];
+        cw.w = a.conv_w[(size_t)c * a.ksize + min(3u, keep)];
+        rs.x = a.ring[c];
+        rs.y = a.ring[(size_t)cd + c];
+        rs.z = a.ring[(size_t)2 * cd + c];
+        rs.w = a.ring[(size_t)3 * cd + c];
     };
-    uint32_t ch = chan(min(t, nch - 1));
-    conv_loads(ch);
+    const uint32_t ch0 = chan(min(t, nch - 1)), ch1 = chan(min(t + GDN_TPB, nch - 1));
+    conv_loads(cx0, cw0, rs0, ch0);
+    conv_loads(cx1, cw1, rs1, ch1);
     const float zraw = a.z[(size_t)h * dv + min(max(t, jlo), jhi - 1)];
     const float nwt = a.norm_w[min(t, dv - 1)];   // needed last, loaded early
     const float *bb = a.in + cd + a.n_v * dv, *aa = bb + a.n_v;
@@ -2606,23 +2616,31 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
 
     // 2. conv + SiLU (the taps in order, then the current input; ref.c
     //    conv1d step); this step's input into the ring slot pos % 4.
-    for (uint32_t e = t; e < nch; e += GDN_TPB) {
-        if (e != t) {
-            ch = chan(e);
-            conv_loads(ch);
-        }
+    auto conv_out = [&](uint32_t e, uint32_t c, float cx, float4 cw, float4 rs) {
         float acc = 0.0f;
 #pragma unroll
         for (uint32_t jj = 0; jj < 3; jj++) {
             const uint32_t sl = (pos + 4 - keep + jj) & 3;
-            const float cr = sl == 0 ? rs[0] : sl == 1 ? rs[1] : sl == 2 ? rs[2] : rs[3];
-            if (jj < keep) acc = fmaf(cw[jj], cr, acc);
+            const float cr = sl == 0 ? rs.x : sl == 1 ? rs.y : sl == 2 ? rs.z : rs.w;
+            const float wj = jj == 0 ? cw.x : jj == 1 ? cw.y : cw.z;
+            if (jj < keep) acc = fmaf(wj, cr, acc);
         }
-        const float wcur = keep == 0 ? cw[0] : keep == 1 ? cw[1] : keep == 2 ? cw[2] : cw[3];
+        const float wcur = keep == 0 ? cw.x : keep == 1 ? cw.y : keep == 2 ? cw.z : cw.w;
         acc = fmaf(wcur, cx, acc);
         const float o = silu(acc);
-        if (e < 2 * dk) qk[e] = o; else vv[e - 2 * dk] = o;
-        if (e >= 2 * dk || qk_writer) a.ring[(size_t)(pos & 3) * cd + ch] = cx;
+        if (e < nch) {
+            if (e < 2 * dk) qk[e] = o; else vv[e - 2 * dk] = o;
+            if (e >= 2 * dk || qk_writer) a.ring[(size_t)(pos & 3) * cd + c] = cx;
+        }
+    };
+    // computed unconditionally (only the stores are guarded), so the second
+    // channel's loads stay up front instead of sinking into a branch
+    conv_out(t, ch0, cx0, cw0, rs0);
+    conv_out(t + GDN_TPB, ch1, cx1, cw1, rs1);
+    for (uint32_t e = t + 2 * GDN_TPB; e < nch; e += GDN_TPB) {     // wider blocks than the shapes in use
+        const uint32_t c = chan(e);
+        conv_loads(cx0, cw0, rs0, c);
+        conv_out(e, c, cx0, cw0, rs0);
     }
     __syncthreads();
     // 3. q, k: RMS (eps 1e-6, no weight), then q / dk and k / sqrt(dk).
