@@ -105,7 +105,7 @@ def gemv_roofline(gpu, cfg, reps=3):
     gbs = algo / avg_s / 1e9
     return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
-                kernel="k_gemv_q8 gate|up %dx%d (RMSNorm prologue, SwiGLU epilogue)" % (rows, cols),
+                kernel="k_gemv_ring gate|up %dx%d (RMSNorm prologue, SwiGLU epilogue)" % (rows, cols),
                 avg_us=round(avg_s * 1e6, 2), algo_bytes=int(algo), launches=reps * L)
 
 
@@ -530,7 +530,7 @@ def main():
     roof = gemv_roofline(gpu, cfg)
     if a.calib_mb:
         calib_copy(a.calib_mb << 20)
-    roof["traffic"] = measured_traffic("k_gemv_q8<2, 1, 2>")
+    roof["traffic"] = measured_traffic("k_gemv_ring<2, 1, 2>")
     log(f"gate/up GEMV: {roof['avg_us']} us/launch, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
     floor = None
     if not a.no_floor:

@@ -281,13 +281,15 @@ def floor(path):
 
     def kind(i):
         nm = short(toks[0][i]["Kernel_Name"])
-        if nm.startswith("k_gemv_q8<2, 1, 0>"):
+        if nm.startswith(("k_gemv_ring<2, 1, 0>", "k_gemv_q8<2, 1, 0>")):
             return "lm_head" if i + 1 < n and short(toks[0][i + 1]["Kernel_Name"]) == "k_argmax" else "input projection"
         for pre, k in (("k_embed", "embedding"), ("k_attn_partial", "attention partial"),
                        ("k_attn_combine", "attention combine"), ("k_gdn_step", "DeltaNet step"),
                        ("k_gemv_q8<2, 0, 1>", "output projection (attention)"),
+                       ("k_gemv_ring<2, 2, 1>", "output projection (DeltaNet, gated prologue)"),
                        ("k_gemv_q8<2, 2, 1>", "output projection (DeltaNet, gated prologue)"),
-                       ("k_gemv_bal<0, 0", "output projection (attention)"), ("k_gemv_q8<2, 1, 2>", "gate/up"),
+                       ("k_gemv_bal<0, 0", "output projection (attention)"), ("k_gemv_ring<2, 1, 2>", "gate/up"),
+                       ("k_gemv_q8<2, 1, 2>", "gate/up"),
                        ("k_gemv_bal", "down projection"), ("k_argmax", "argmax"), ("k_step_advance", "step advance")):
             if nm.startswith(pre):
                 return k
@@ -392,7 +394,7 @@ def main():
     ap.add_argument("--counter", default="FETCH_SIZE")
     ap.add_argument("--calib-bytes", type=float, default=0)
     ap.add_argument("--json", default=None)
-    ap.add_argument("--kernel", default="k_gemv_q8<2, 1, 2>")
+    ap.add_argument("--kernel", default="k_gemv_ring<2, 1, 2>")
     ap.add_argument("--last", type=int, default=0)
     a = ap.parse_args()
     if a.mode == "stats":
