@@ -748,7 +748,9 @@ static hipError_t launch_ring(const sgk_gemv &a, size_t lds, hipStream_t s) {
 // ---------------------------------------------------------------------------
 #define BT 768
 #define BW (BT / 64)
-#define BP 4
+// Steps in flight per wave: 3 (72 KB per CU). Over a 27B decode token, 2 and
+// 3 ran alike and 0.4-0.7% faster than 4; 6 was 2% slower.
+#define BP 3
 constexpr int BXK_NONE = (SGK_BAL_MAX_COLS + 4 * BT - 1) / (4 * BT);
 constexpr int BXK_RMS = (SGK_BAL_MAX_RMS_COLS + 4 * BT - 1) / (4 * BT);
 
@@ -786,7 +788,7 @@ __global__ void __launch_bounds__(BT) k_gemv_bal(sgk_gemv a) {
     };
     auto next = [&](uint32_t &k, uint32_t &j) { if (++j == nsteps) { j = 0; k++; } };
     // x is requested first and the ring after it: the loads return in order,
-    // so x requested behind the ring's BP steps (96 KB per CU) waited for all
+    // so x requested behind the ring's BP steps (72 KB per CU) waited for all
     // of them. For EPI_ADD thread t < 2 * ng holds y of the workgroup's row t
     // in a register, requested with the ring (the launcher keeps 2 * ng <=
     // BT): a read into LDS here made the staging wait for every request in
