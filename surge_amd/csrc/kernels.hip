@@ -4382,7 +4382,8 @@ __global__ void __launch_bounds__(TPB) k_splitk_reduce(const float *P, uint32_t 
 // RMSNorm(Y row n) with weight w (k_split_bf16_rms': the same per-thread order
 // of the sum of squares, block_sum, (y * r) * w), so both outputs are those
 // of the two kernels run one after the other.
-__global__ void __launch_bounds__(TPB) k_splitk_reduce_rms(const float *P, uint32_t S, uint32_t N, uint32_t M,
+template <int S>
+__global__ void __launch_bounds__(TPB) k_splitk_reduce_rms(const float *P, uint32_t N, uint32_t M,
                                                            float *Y, uint32_t ldy, const float *w, float eps,
                                                            uint16_t *xs) {
     __shared__ float red[4];
@@ -4390,26 +4391,32 @@ __global__ void __launch_bounds__(TPB) k_splitk_reduce_rms(const float *P, uint3
     const size_t nm = (size_t)N * M;
     float *yr = Y + (size_t)n * ldy;
     float ss = 0.0f;
-    // columns t, t + TPB, ... four at a time (all their loads in flight at
-    // once); the sum of squares still runs over them in increasing order
-    for (uint32_t i0 = t; i0 < M; i0 += 4 * TPB) {
-        float v[4], y[4];
+    // columns t, t + TPB, ... eight at a time, each with its S partials and
+    // residual requested together before any is added (a runtime loop over the
+    // splits waited for each split's loads in turn: 15 memory round trips per
+    // 5120-column row at S = 3, now 3); the partials are added in split order
+    // and the sum of squares runs over the columns in increasing order
+    constexpr int U = 8;
+    for (uint32_t i0 = t; i0 < M; i0 += U * TPB) {
+        float v[S][U], y[U];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < U; u++) {
             const uint32_t i = min(i0 + u * TPB, M - 1);
-            v[u] = P[(size_t)n * M + i];
             y[u] = yr[i];
-        }
-        for (uint32_t k = 1; k < S; k++) {
 #pragma unroll
-            for (int u = 0; u < 4; u++) v[u] += P[(size_t)k * nm + (size_t)n * M + min(i0 + u * TPB, M - 1)];
+            for (int k = 0; k < S; k++) v[k][u] = P[(size_t)k * nm + (size_t)n * M + i];
         }
+        __builtin_amdgcn_sched_barrier(0);          // all of them before the first add
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            if (i0 + u * TPB >= M) break;
-            y[u] += v[u];
-            yr[i0 + u * TPB] = y[u];
-            ss = fmaf(y[u], y[u], ss);
+        for (int u = 0; u < U; u++) {
+            float acc = v[0][u];
+#pragma unroll
+            for (int k = 1; k < S; k++) acc += v[k][u];
+            if (i0 + u * TPB < M) {
+                y[u] += acc;
+                yr[i0 + u * TPB] = y[u];
+                ss = fmaf(y[u], y[u], ss);
+            }
         }
     }
     ss = block_sum(ss, red);                    // its barriers also publish the row's stores to the workgroup
@@ -4551,7 +4558,8 @@ extern "C" hipError_t sgk_gemm(const sgk_gemm_args *a, hipStream_t s) {
                 !((uintptr_t)a->Y & 15) && !((uintptr_t)a->post_nw & 15)) {
                 // the residual add fused with the next product's RMSNorm and split (into this
                 // product's xs, which it has finished reading)
-                hipLaunchKernelGGL(k_splitk_reduce_rms, dim3(a->N), dim3(TPB), 0, s, a->part, S, a->N, a->M, a->Y, a->ldy,
+                auto red = S == 2 ? k_splitk_reduce_rms<2> : S == 3 ? k_splitk_reduce_rms<3> : k_splitk_reduce_rms<4>;
+                hipLaunchKernelGGL(red, dim3(a->N), dim3(TPB), 0, s, a->part, a->N, a->M, a->Y, a->ldy,
                                    a->post_nw, a->post_eps, a->xs);
                 *a->post_done = 1;
                 return hipGetLastError();
