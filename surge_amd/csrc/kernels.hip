@@ -1584,13 +1584,15 @@ __device__ __forceinline__ void fa_split8(const float *x, f16x8 &hi, f16x8 &lo) 
 }
 
 // K rows for the score MFMA's A operand: lane (li, lg) takes key `key`, dims
-// 8*lg.. of each 32 (16 B per load, one per 32-dim block)
+// 8*lg.. of each 32 (16 B per load, one per 32-dim block). K and V are read
+// once per token, so their loads are non-temporal, as the weights' are: at
+// 262000 keys, 122.2 -> 127.4 tok/s; at 4k no change.
 template <int HD>
 __device__ __forceinline__ void mf_load_k(v4u (&kr)[HD / 32], const uint16_t *kh, uint32_t key, uint32_t ps,
                                           uint32_t lg) {
     const v4u *p = (const v4u *)(kh + (size_t)key * ps + lg * 8);
 #pragma unroll
-    for (int kb = 0; kb < HD / 32; kb++) kr[kb] = p[kb * 4];
+    for (int kb = 0; kb < HD / 32; kb++) kr[kb] = __builtin_nontemporal_load(p + kb * 4);
 }
 // ---------------------------------------------------------------------------
 // Decode split-K partial with one independent key stream per wave (head_dim
@@ -1621,7 +1623,7 @@ __device__ __forceinline__ void wv_load_v(v4u (&vr)[4][HD / 128], const uint16_t
     for (int j = 0; j < 4; j++) {
         const uint16_t *row = vh + (size_t)min(key0 + j, klast) * ps;
 #pragma unroll
-        for (int q = 0; q < HD / 128; q++) vr[j][q] = *(const v4u *)(row + (li + 16 * q) * 8);
+        for (int q = 0; q < HD / 128; q++) vr[j][q] = __builtin_nontemporal_load((const v4u *)(row + (li + 16 * q) * 8));
     }
 }
 
@@ -2569,7 +2571,9 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
     //    the gate inputs, the ring (its slots need the position), then this
     //    wave's state rows. Every load is unconditional at a clamped index and
     //    the tap loops have a fixed trip count, so nothing waits until all of
-    //    them are in flight.
+    //    them are in flight. The state rows are read and written back
+    //    non-temporally (each is touched once per token): 4k decode
+    //    182.6 -> 185.8 tok/s, 262000 keys 127.3 -> 128.9.
     const uint32_t nch = 2 * dk + (jhi - jlo);
     auto chan = [&](uint32_t e) -> uint32_t {
         if (e < dk) return hk * dk + e;
@@ -2608,7 +2612,7 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
     for (int r = 0; r < RW; r++) {
         const uint32_t j = min(j0 + r, jhi - 1);
 #pragma unroll
-        for (int e = 0; e < EPL; e++) sr[r][e] = Sh[(size_t)j * dk + (on ? lane * EPL + e : 0)];
+        for (int e = 0; e < EPL; e++) sr[r][e] = __builtin_nontemporal_load(Sh + (size_t)j * dk + (on ? lane * EPL + e : 0));
     }
     const float zj = (t >= jlo && t < jhi) ? zraw : 0.0f;
 #pragma unroll
@@ -2705,7 +2709,7 @@ __device__ __forceinline__ void gdn_step_body(const sgk_gdn &a, uint32_t h, uint
             const uint32_t j = j0 + r;
             if (j < jhi && on) {
 #pragma unroll
-                for (int e = 0; e < EPL; e++) Sh[(size_t)j * dk + lane * EPL + e] = sr[r][e];
+                for (int e = 0; e < EPL; e++) __builtin_nontemporal_store(sr[r][e], Sh + (size_t)j * dk + lane * EPL + e);
             }
         }
     }
