@@ -337,7 +337,7 @@ __device__ __forceinline__ void gemv_load(gemv_chunk<R> &ch, const int8_t *qs, c
     for (int r = 0; r < R; r++) {
         const uint32_t rr = min(r0 + r, rows - 1);
         ch.q[r] = ldnt((const uint4 *)(qs + (size_t)rr * cols) + c);
-        ch.d[r] = d[(size_t)rr * (cols >> 5) + (c >> 1)];
+        ch.d[r] = __builtin_nontemporal_load(d + (size_t)rr * (cols >> 5) + (c >> 1));   // read once per token, as the weights
     }
 }
 
@@ -460,7 +460,7 @@ __device__ __forceinline__ void ring_chunk(const sgk_gemv &a, const ring_src &rs
         const uint32_t dof = ok ? ((r0 + r) * (a.cols >> 5) + (c >> 1)) * 2 : RING_OOB;
         const v4u v = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs.q, (int)qo, 0, 2));   // nt
         ch.q[r] = make_uint4(v.x, v.y, v.z, v.w);
-        ch.d[r] = __builtin_amdgcn_raw_buffer_load_b16(rs.d, (int)dof, 0, 0);
+        ch.d[r] = __builtin_amdgcn_raw_buffer_load_b16(rs.d, (int)dof, 0, 2);   // nt (as the scales of k_gemv_q8)
     }
 }
 
