@@ -847,19 +847,22 @@ __global__ void __launch_bounds__(BT) k_gemv_bal(sgk_gemv a) {
     }
 }
 
-// Which kernel takes a Q8_0 GEMV of `cols` columns (multiples of 1024 only):
-// 0 k_gemv_q8, 1 k_gemv_bal contiguous, 2 k_gemv_bal
-// interleaved. Measured per 27B shape (one MI355X, back-to-back launches over
-// the layers): the interleaved balanced kernel streams the 17408-column down
-// projection in 18.5 us against 20.2 for the row-front kernel it replaced; at 5120 and 6144
-// columns k_gemv_q8 is as fast or faster, and contiguous ranges are slower
-// than interleaved ones everywhere. SURGE_GEMV=q8|bal|bali forces one.
-static int gemv_bal_on(uint32_t cols) {
+// Which kernel takes a Q8_0 GEMV of `cols` columns (multiples of 1024 only)
+// and prologue `pro`: 0 k_gemv_q8 or k_gemv_ring, 1 k_gemv_bal contiguous,
+// 2 k_gemv_bal interleaved. By default the interleaved balanced kernel takes
+// the GEMVs without a prologue longer than 4096 columns: the 27B down
+// projection (17408 columns, 18.5 us against 20.2 for the row-front kernel
+// it replaced, back-to-back over the layers) and the attention output
+// projections of 6144 columns (27B decode 187.2-187.8 -> 187.6-187.9 tok/s,
+// 2B 1251 -> 1263 tok/s with its 6144-column down projection, same boxes,
+// alternating, same tokens). Contiguous ranges are slower than interleaved
+// ones everywhere. SURGE_GEMV=q8|bal|bali forces one.
+static int gemv_bal_on(uint32_t cols, int pro) {
     const char *e = getenv("SURGE_GEMV");
     if (e && e[0] == 'q' && e[1] == '8' && !e[2]) return 0;
     if (e && e[0] == 'b' && e[1] == 'a' && e[2] == 'l' && e[3] == 'i' && !e[4]) return 2;
     if (e && e[0] == 'b' && e[1] == 'a' && e[2] == 'l' && !e[3]) return 1;
-    return cols > 8192 ? 2 : 0;
+    return pro == SGK_PRO_NONE && cols > 4096 ? 2 : 0;
 }
 // Whether a Q8_0 GEMV with a prologue (RMSNorm or gated) that k_gemv_bal
 // does not take runs the ring form k_gemv_ring (the default) or the
@@ -878,7 +881,7 @@ static int gemv_ring_on() {
 
 template <int PRO, int EPI>
 static hipError_t launch_bal(const sgk_gemv &a, hipStream_t s) {
-    auto kern = gemv_bal_on(a.cols) == 2 ? k_gemv_bal<PRO, EPI, true> : k_gemv_bal<PRO, EPI, false>;
+    auto kern = gemv_bal_on(a.cols, PRO) == 2 ? k_gemv_bal<PRO, EPI, true> : k_gemv_bal<PRO, EPI, false>;
     const uint32_t nb = (uint32_t)device_cus();
     const size_t lds = (size_t)bal_lds_floats(a.rows, a.cols, nb) * 4;
     hipError_t e = allow_lds((const void *)kern, lds);
@@ -901,7 +904,7 @@ static hipError_t gemv_dispatch(const sgk_gemv *a, hipStream_t s) {
         hipLaunchKernelGGL((k_gemv_f32<PRO, EPI>), dim3(min((groups + 3) / 4, 4096u)), dim3(TPB), lds, s, *a);
         return hipGetLastError();
     }
-    if (PRO != SGK_PRO_GATED && gemv_bal_on(a->cols) && !a->tune_r && !a->tune_blocks && a->cols % 1024 == 0 &&
+    if (PRO != SGK_PRO_GATED && gemv_bal_on(a->cols, PRO) && !a->tune_r && !a->tune_blocks && a->cols % 1024 == 0 &&
         2 * (((a->rows + 1) / 2 + (uint32_t)device_cus() - 1) / (uint32_t)device_cus()) <= BT &&
         (uint64_t)a->rows * a->cols < RING_OOB &&
         a->cols <= (PRO == SGK_PRO_RMS ? SGK_BAL_MAX_RMS_COLS : SGK_BAL_MAX_COLS) &&
