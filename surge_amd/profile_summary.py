@@ -283,6 +283,8 @@ def floor(path):
         nm = short(toks[0][i]["Kernel_Name"])
         if nm.startswith(("k_gemv_ring<2, 1, 0>", "k_gemv_q8<2, 1, 0>")):
             return "lm_head" if i + 1 < n and short(toks[0][i + 1]["Kernel_Name"]) == "k_argmax" else "input projection"
+        if nm.startswith("k_gemv_bal") and i and short(toks[0][i - 1]["Kernel_Name"]).startswith("k_attn_combine"):
+            return "output projection (attention)"     # the attention output projection on the balanced GEMV
         for pre, k in (("k_embed", "embedding"), ("k_attn_partial", "attention partial"),
                        ("k_attn_combine", "attention combine"), ("k_gdn_step", "DeltaNet step"),
                        ("k_gemv_q8<2, 0, 1>", "output projection (attention)"),
